@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Decode hot-path benchmark on one MI355X.
+
+Headline workload: one token's routed MoE FFN in FP4 - 6 of 256 experts
+(top-6 of sigmoid scores over N(0,1) router logits, renormalised), each
+w1/w3 2048x4096 and w2 4096x2048 E2M1 with a UE8M0 scale per 32 columns,
+x ~ N(0,1) in bf16, SwiGLU then down then the ordered weighted sum.  A step
+is one token; each step routes a fresh token on one of `--layers` resident
+layers of 256 experts (round robin), so no step reuses weights that the
+previous ones left in the 256 MB Infinity Cache.  Inputs are resident in
+HBM before the timed region; value = algorithmic bytes / wall time.
+
+Also reported: per-kernel mean durations (HIP events on the library stream),
+the FP8 dense GEMV (4096x4096, fp32 128x128 block scales) over 40 rotating
+copies, and the reference's AVX2 algorithm (the CPU oracle) timed on the
+host cores with the reference's thread count.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+EXPERT_BYTES = 13_369_344             # 3 x (4 MiB packed + 256 KiB UE8M0)
+TOKEN_BYTES = 6 * EXPERT_BYTES + 4096 * 2 + 4096 * 4   # + bf16 x + f32 y = 80,240,640
+# gate/up kernel: 6 x (w1 + w3) + x codes/scales in + hidden (f32 + codes) out
+GATEUP_BYTES = 6 * 2 * (4_194_304 + 262_144) + 4096 + 64 * 4 + 6 * 2048 * 5 + 6 * 32 * 4
+DOWN_BYTES = 6 * (4_194_304 + 262_144) + 6 * (2048 + 32 * 4) + 6 * 4096 * 4 * 2 + 4096 * 4
+FP8_BYTES = 4096 * 4096 + 32 * 32 * 4 + 4096 * 4 + 4096 * 4
+
+
+def log(msg: str):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(lib, seed: int, budget_s: float):
+    """The oracle's AVX2 restatement of the reference expert path on this host."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    from wohper_amd import workloads as wl
+
+    oracle.build()
+    threads = max(1, (os.cpu_count() or 3) - 2)  # reference default: available_parallelism - 2
+    # a container's CPU quota can be below os.cpu_count(); respect the affinity mask
+    try:
+        threads = max(1, min(threads, len(os.sched_getaffinity(0)) - 2))
+    except AttributeError:
+        pass
+    oracle.set_threads(threads)
+    idx, w, x = wl.moe_token_case(seed)
+    experts = [wl.synth_expert_host(lib, seed, 0, int(e)) for e in idx]
+    tokens = 0
+    t0 = time.perf_counter()
+    while True:
+        outs = np.stack([oracle.fp4_expert_forward(*ex, x) for ex in experts])
+        oracle.routed_combine(outs, w)
+        tokens += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or tokens >= 200:
+            break
+    gbs = tokens * TOKEN_BYTES / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{tokens} tokens x 6 routed FP4 experts (4096/2048 shapes), oracle AVX2 restatement "
+                      f"of the reference kernel, {threads} threads, {el:.1f} s; {el / tokens * 1e3:.1f} ms/token"}
+
+
+def fp8_dense(ctx, steps: int, warmup: int):
+    """4096x4096 FP8 GEMV (fp32 block scales) over 40 rotating copies (672 MB)."""
+    import wohper_amd
+    from wohper_amd import workloads as wl
+
+    case = wl.fp8_gemv_case(4096, 4096, seed=0)
+    copies = 40
+    handles = [ctx.store_fp8(case.w, 4096, 4096, case.scales, 32, 32, wohper_amd.SCALE_F32) for _ in range(copies)]
+    xd = ctx.device_alloc(4096 * 4)
+    yd = ctx.device_alloc(4096 * 4)
+    ctx.to_device(xd, case.x)
+    for i in range(warmup):
+        ctx.fp8_gemv_async(handles[i % copies], 0, 4096, xd, yd)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ctx.fp8_gemv_async(handles[i % copies], 0, 4096, xd, yd)
+    ctx.synchronize()
+    el = time.perf_counter() - t0
+    us = el / steps * 1e6
+    gbs = FP8_BYTES / (us * 1e-6) / 1e9
+    ctx.device_free(xd)
+    ctx.device_free(yd)
+    return {"workload": "fp8 e4m3 GEMV 4096x4096, fp32 128x128 block scales, bf16 x, batch 1",
+            "us_per_gemv": round(us, 3), "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "note": "wall time of back-to-back launches, 40 rotating weight copies"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--layers", type=int, default=8, help="resident layers of 256 experts")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-fp8", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (every box here has one MI355X); --gpus {args.gpus} is not supported",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import wohper_amd
+    from wohper_amd import workloads as wl
+
+    seed = 2
+    ctx = wohper_amd.Context(0)
+    t0 = time.perf_counter()
+    for layer in range(args.layers):
+        for e in range(wl.N_ROUTED):
+            ctx.store_expert_synthetic(layer, e, wl.HIDDEN, wl.INTER, seed)
+    dev_bytes, _, n_exp = ctx.usage()
+    log(f"resident: {n_exp} experts, {dev_bytes / 1e9:.1f} GB in {time.perf_counter() - t0:.1f} s")
+
+    total = args.warmup + args.steps
+    rng = np.random.default_rng(seed)
+    routes = []
+    for i in range(total):
+        logits = rng.standard_normal(wl.N_ROUTED).astype(np.float32)
+        idx, w = wl.route_topk_sigmoid(logits)
+        routes.append([(i % args.layers, int(e), float(wt)) for e, wt in zip(idx, w)])
+    xs = wl.bf16_bits(rng.standard_normal((total, wl.HIDDEN)).astype(np.float32))
+    x_dev = ctx.device_alloc(xs.nbytes)
+    out_dev = ctx.device_alloc(total * wl.HIDDEN * 4)
+    ctx.to_device(x_dev, xs)
+
+    def step(i):
+        ctx.routed_experts_async(routes[i], x_dev + i * wl.HIDDEN * 2, True, 1, out_dev + i * wl.HIDDEN * 4)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.warmup, total):
+        step(i)
+    ctx.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / args.steps * 1e3
+    value = args.steps * TOKEN_BYTES / elapsed / 1e9
+    log(f"routed FP4 MoE: {ms_per_step * 1e3:.2f} us/token, {value:.1f} GB/s")
+
+    # per-kernel durations, HIP events on the library stream around each kernel
+    prof_steps = min(args.steps, 200)
+    ctx.profile_enable(prof_steps)
+    for i in range(prof_steps):
+        step(args.warmup + i)
+    ctx.synchronize()
+    (t_aq, t_gu, t_dn), n = ctx.profile_read()
+    ctx.profile_enable(0)
+    gu_gbs = GATEUP_BYTES / (t_gu * 1e-6) / 1e9
+    dn_gbs = DOWN_BYTES / (t_dn * 1e-6) / 1e9
+    log(f"kernels (mean of {n}): act-quant {t_aq:.2f} us, gate/up {t_gu:.2f} us ({gu_gbs:.0f} GB/s), "
+        f"down {t_dn:.2f} us ({dn_gbs:.0f} GB/s)")
+
+    extra = {}
+    if not args.no_fp8:
+        extra["fp8_dense_gemv"] = fp8_dense(ctx, max(200, args.steps), 40)
+        log(f"fp8 dense: {extra['fp8_dense_gemv']}")
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(ctx.lib, seed, args.cpu_seconds)
+        log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": "HBM GB/s (% of peak) for FP4 expert + FP8 dense matvec; batch-1 decode step us",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp4-e2m1/fp8-e4m3 weights, f32 accumulate",
+        "data": "synthetic (seeded random weights and activations; no checkpoint offline)",
+        "config": {"workload": "routed MoE FFN, 1 token, top-6 of 256 FP4 experts (w1/w3 2048x4096, "
+                               "w2 4096x2048, UE8M0 per 32), bf16 x",
+                   "global_batch": 1, "experts_resident": n_exp, "resident_GB": round(dev_bytes / 1e9, 2),
+                   "bytes_per_step": TOKEN_BYTES, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_moe_gateup", "bytes_per_launch": GATEUP_BYTES,
+                     "avg_launch_us": round(t_gu, 3)},
+        "kernels_us": {"k_act_quant_codes": round(t_aq, 3), "k_moe_gateup": round(t_gu, 3),
+                       "k_moe_down": round(t_dn, 3), "k_moe_down_GBps": round(dn_gbs, 1)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.device_free(x_dev)
+    ctx.device_free(out_dev)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,196 @@
+/*
+ * wohper_hip.h - C ABI of the MI355X (gfx950) decode hot path.
+ *
+ * Drop-in boundary for the reference engine's DeepSeek-V4 kernel entry points
+ * (Twenytwo/wohper, engine/zc_infer_core/src = E/).  Every hot-path function
+ * below names the reference function it replaces.  The reference is Rust; its
+ * binding is an `extern "C"` block behind a `rocm` cargo feature (see
+ * INTEGRATION.md).  Plain pointers and sizes only.
+ *
+ * Ownership: the caller owns every host buffer; the library never frees
+ * caller memory.  Device weights are owned by the context's weight store for
+ * the context's lifetime (or until wh_store_release).  All functions are
+ * thread-compatible: one context (one HIP stream) per engine thread.
+ *
+ * Synchronous entry points take host slices and return after the result is
+ * in the caller's buffer (the reference's semantics).  *_async entry points
+ * take device pointers, are ordered on the context stream, and report
+ * failures through wh_stream_status().
+ */
+#ifndef WOHPER_HIP_H
+#define WOHPER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  1..8 mirror DeepSeekV4KernelError (E/deepseek_v4.rs:398-408)
+ * in order; the rest cover ComputeError cases of the FP8 path
+ * (E/compute.rs:6180-6215), the weight store and the HIP runtime. */
+enum wh_status {
+    WH_OK = 0,
+    WH_EMPTY_SHAPE = 1,
+    WH_INVALID_SHAPE = 2,
+    WH_PACKED_WEIGHT_TOO_SMALL = 3,
+    WH_SCALE_TOO_SMALL = 4,
+    WH_INPUT_TOO_SMALL = 5,
+    WH_OUTPUT_TOO_SMALL = 6,
+    WH_SCRATCH_TOO_SMALL = 7,
+    WH_NON_FINITE_OUTPUT = 8,
+    WH_INVALID_QUANT_FORMAT = 9,   /* e.g. "DeepSeek FP8 scale is not UE8M0" */
+    WH_NOT_RESIDENT = 10,          /* unknown tensor handle or (layer, expert) key */
+    WH_OUT_OF_MEMORY = 11,
+    WH_HIP_ERROR = 12,
+    WH_INVALID_ARGUMENT = 13,
+    WH_NON_FINITE_INPUT = 14,      /* an activation block held inf/NaN */
+    WH_UNSUPPORTED = 15
+};
+
+/* Scale formats of an FP8 block-scaled tensor. */
+enum wh_scale_format {
+    WH_SCALE_UE8M0 = 0, /* one byte per block: 2^(b-127), 0 -> 0.0, 255 -> inf */
+    WH_SCALE_F32 = 1    /* one float per block */
+};
+
+typedef struct wh_ctx wh_ctx;
+typedef uint64_t wh_tensor; /* handle into the weight store, 0 = none */
+
+/* One routed expert of a token: IoBlockPtr{layer_id, expert_id, route_weight}
+ * (E/compute.rs:896-904) without the host pointer - experts are resident. */
+typedef struct {
+    uint32_t layer_id;
+    uint32_t expert_id;
+    float route_weight;
+} wh_expert_route;
+
+/* ----------------------------------------------------------- lifecycle */
+int wh_init(int device, wh_ctx** out);
+int wh_shutdown(wh_ctx* ctx);
+const char* wh_status_string(int status);
+/* Blocks until the stream drains; returns the first deferred kernel status
+ * (WH_NON_FINITE_OUTPUT / WH_NON_FINITE_INPUT) raised since the last call. */
+int wh_synchronize(wh_ctx* ctx);
+/* The context's hipStream_t, for callers that interleave their own work. */
+void* wh_stream(wh_ctx* ctx);
+/* Library build description (architecture, libm table sizes). */
+const char* wh_build_info(void);
+
+/* --------------------------------------------------------- weight store
+ * Replaces the SSD/page-cache streaming path of the reference
+ * (E/direct_io.rs:575-681, E/scheduler.rs:148-194, E/server/generation.rs:196-306):
+ * tensors are re-laid out once for the GPU kernels and stay in HBM. */
+
+/* FP8 E4M3 weight [rows x cols] with block scales [scale_rows x scale_cols]
+ * (E/compute.rs:6174-6215 shape rules: rows % scale_rows == cols % scale_cols == 0). */
+int wh_store_fp8(wh_ctx* ctx, const uint8_t* weight, size_t weight_len, size_t rows, size_t cols,
+                 const void* scales, size_t scales_len, int scale_format, size_t scale_rows,
+                 size_t scale_cols, wh_tensor* out);
+
+/* FP4 E2M1 packed weight [rows x ceil(cols/2)] (low nibble = even column) with
+ * UE8M0 scales [rows x scale_cols]: the Fp4Matvec of E/deepseek_v4.rs:410-417,
+ * validated as validate_fp4_matvec (E/deepseek_v4.rs:434-462). */
+int wh_store_fp4(wh_ctx* ctx, const uint8_t* packed, size_t packed_len, const uint8_t* scales,
+                 size_t scales_len, size_t rows, size_t cols, size_t scale_cols, wh_tensor* out);
+
+/* Registers an FP4 SwiGLU expert (DeepSeekV4Fp4Expert, E/deepseek_v4.rs:419-424)
+ * under the (layer_id, expert_id) key the engine routes by.  Shapes are checked
+ * as in deepseek_v4_fp4_expert_from_quant_block (E/compute.rs:1249-1268). */
+int wh_store_expert(wh_ctx* ctx, uint32_t layer_id, uint32_t expert_id, wh_tensor w1, wh_tensor w3,
+                    wh_tensor w2);
+
+/* Device-side synthetic fill of an FP4 expert with the counter-based RNG of
+ * the benchmark (uniform packed bytes, UE8M0 bytes in [scale_lo, scale_hi]),
+ * written directly in the resident layout - for stacks too large to stage
+ * through the host.  Identical bytes to wh_synth_fp4_host. */
+int wh_store_expert_synthetic(wh_ctx* ctx, uint32_t layer_id, uint32_t expert_id, size_t hidden,
+                              size_t inter, uint64_t seed, uint32_t scale_lo, uint32_t scale_hi);
+
+/* Host generator of the same bytes (original reference layout). */
+void wh_synth_fp4_host(uint64_t seed, uint64_t stream, uint8_t* packed, size_t packed_len,
+                       uint8_t* scales, size_t scales_len, uint32_t scale_lo, uint32_t scale_hi);
+
+int wh_store_release(wh_ctx* ctx, wh_tensor t);
+int wh_store_usage(wh_ctx* ctx, size_t* device_bytes, size_t* tensors, size_t* experts);
+
+/* Bit-exact dequantisation of a resident tensor back to reference values, in
+ * the original column order: FP4 -> decode_fp4_e2m1(nibble, scale)
+ * (E/deepseek_v4.rs:358-372); FP8 -> decode_fp8_e4m3(byte, 1.0)
+ * (E/deepseek_v4.rs:151-164, scales not applied).  out: rows*cols floats. */
+int wh_tensor_dequant(wh_ctx* ctx, wh_tensor t, float* out, size_t out_len);
+
+/* ------------------------------------------------------------- hot path */
+
+/* gemv_fp8_e4m3_ue8m0_tensorwise (E/compute.rs:6174) when row_start == 0 and
+ * row_end == rows, else gemv_fp8_e4m3_ue8m0_rows (E/compute.rs:6244): output
+ * gets row_end - row_start values; *values_out = weight values consumed, as
+ * the reference's Ok(usize). */
+int wh_fp8_gemv(wh_ctx* ctx, wh_tensor w, size_t row_start, size_t row_end, const float* input,
+                size_t input_len, float* output, size_t output_len, size_t* values_out);
+
+/* gemv_fp8_e4m3_ue8m0_rows_multi (E/compute.rs:6384): n inputs of length
+ * cols at stride input_stride, n outputs at stride output_stride. */
+int wh_fp8_gemv_multi(wh_ctx* ctx, wh_tensor w, size_t row_start, size_t row_end,
+                      const float* inputs, size_t n, size_t input_stride, float* outputs,
+                      size_t output_stride, size_t* values_out);
+
+/* fp4_e2m1_ue8m0_matvec_scalar (E/deepseek_v4.rs:464). */
+int wh_fp4_matvec(wh_ctx* ctx, wh_tensor w, const float* input, size_t input_len, float* output,
+                  size_t output_len);
+
+/* deepseek_v4_fp4_expert_forward_scalar (E/deepseek_v4.rs:561): scratch_len is
+ * the caller's scratch size in floats (checked like the reference, >= 2*inter;
+ * the device keeps its own scratch). */
+int wh_fp4_expert_forward(wh_ctx* ctx, uint32_t layer_id, uint32_t expert_id, const float* input,
+                          size_t input_len, float* output, size_t output_len, size_t scratch_len);
+
+/* fp8_act_quant_dequant_in_place (E/compute.rs:2504). */
+int wh_act_quant_dequant(wh_ctx* ctx, float* values, size_t n, size_t block_size);
+
+/* compute_active_experts (E/compute.rs:1948): hidden (len >= hidden size) is
+ * replaced by the route-weighted sum of the experts' outputs, in route order. */
+int wh_routed_experts(wh_ctx* ctx, const wh_expert_route* routes, size_t n_routes, float* hidden,
+                      size_t hidden_len);
+
+/* Device-pointer variant for the resident decode path: x_dev holds n_tokens
+ * rows of `hidden` values (f32, or bf16 when x_is_bf16), all routed to the same
+ * expert list; out_dev gets n_tokens rows of f32.  Stream-ordered. */
+int wh_routed_experts_async(wh_ctx* ctx, const wh_expert_route* routes, size_t n_routes,
+                            const void* x_dev, int x_is_bf16, size_t n_tokens, float* out_dev);
+
+/* Device-pointer FP8 GEMV (rows [row_start,row_end) of w, x_dev f32 or bf16). */
+int wh_fp8_gemv_async(wh_ctx* ctx, wh_tensor w, size_t row_start, size_t row_end,
+                      const float* x_dev, float* y_dev);
+
+/* Deferred status of *_async calls (same as wh_synchronize). */
+int wh_stream_status(wh_ctx* ctx);
+
+/* Device buffers for the *_async entry points (the engine's resident
+ * hidden-state buffers).  kind: 0 host->device, 1 device->host,
+ * 2 device->device; wh_memcpy is ordered on the context stream and returns
+ * when the copy is done. */
+int wh_device_alloc(wh_ctx* ctx, size_t bytes, void** out);
+int wh_device_free(wh_ctx* ctx, void* ptr);
+int wh_memcpy(wh_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
+
+/* Per-kernel timing of the routed-expert pipeline, the device counterpart
+ * of the reference's ZC_PROF pass timers (E/server/generation.rs:2344-2351):
+ * after wh_profile_enable(ctx, n), the next n routed calls record HIP events
+ * on the context stream around each kernel; wh_profile_read returns the mean
+ * microseconds of [act-quant of x, gate/up + SwiGLU, down + routed sum] in
+ * avg_us[0..2].  n = 0 disables it. */
+int wh_profile_enable(wh_ctx* ctx, size_t max_steps);
+int wh_profile_read(wh_ctx* ctx, double* avg_us, size_t* steps);
+
+/* Test support, no counterpart in the reference: evaluates the device libm
+ * emulation on n values.  fn 0: silu(x) = x / (1 + expf(-x)) for x <= 10;
+ * fn 1: expf(x) for x >= -10; fn 2: the act-quant block scale
+ * exp2f(ceilf(log2f(max(x, 1e-4) / 448))) for finite x >= 0. */
+int wh_debug_eval(wh_ctx* ctx, int fn, const float* in, float* out, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WOHPER_HIP_H */

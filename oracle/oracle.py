@@ -1,0 +1,235 @@
+"""ctypes front-end of the CPU oracle (oracle/oracle.c) - test infrastructure.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use
+this module, as the checker.  Build with `make -C oracle`.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "_build" / "liboracle.so"
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+class Fp4Spec(ctypes.Structure):
+    _fields_ = [
+        ("packed", ctypes.POINTER(ctypes.c_uint8)),
+        ("packed_len", ctypes.c_size_t),
+        ("scales", ctypes.POINTER(ctypes.c_uint8)),
+        ("scales_len", ctypes.c_size_t),
+        ("rows", ctypes.c_size_t),
+        ("cols", ctypes.c_size_t),
+        ("scale_cols", ctypes.c_size_t),
+    ]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = ctypes.CDLL(str(LIB))
+        c = ctypes
+        f32p, u8p, sz = c.POINTER(c.c_float), c.POINTER(c.c_uint8), c.c_size_t
+        sigs = {
+            "or_decode_fp8_e4m3": (c.c_float, [c.c_uint8, c.c_float]),
+            "or_decode_ue8m0_scale": (c.c_float, [c.c_uint8]),
+            "or_decode_fp4_e2m1": (c.c_float, [c.c_uint8, c.c_float]),
+            "or_luts": (None, [f32p, f32p, f32p, f32p]),
+            "or_set_threads": (None, [c.c_int]),
+            "or_thread_count": (c.c_int, []),
+            "or_fp8_dot_row_avx2": (c.c_float, [u8p, f32p, sz, sz, f32p]),
+            "or_fp8_dot_row_scalar": (c.c_float, [u8p, f32p, sz, sz, f32p]),
+            "or_fp8_gemv": (c.c_int, [u8p, sz, sz, f32p, sz, sz, sz, sz, f32p, f32p, c.c_int]),
+            "or_fp4_dot_row_avx2": (c.c_float, [u8p, u8p, sz, sz, sz, f32p]),
+            "or_fp4_matvec": (c.c_int, [u8p, sz, u8p, sz, sz, sz, sz, f32p, sz, f32p, sz, c.c_int]),
+            "or_nearest_e4m3": (c.c_float, [c.c_float]),
+            "or_act_quant_dequant": (None, [f32p, sz, sz]),
+            "or_act_quant_scale": (c.c_float, [c.c_float]),
+            "or_silu": (c.c_float, [c.c_float]),
+            "or_swiglu": (c.c_float, [c.c_float, c.c_float]),
+            "or_fp4_expert_forward": (c.c_int, [c.POINTER(Fp4Spec)] * 3 + [f32p, sz, f32p, sz, f32p, sz, c.c_int]),
+            "or_route_weight_sum": (c.c_int, [f32p, sz, f32p]),
+            "or_routed_combine": (None, [f32p, f32p, sz, sz, f32p]),
+            "or_accumulate_expert": (None, [f32p, c.POINTER(c.c_size_t), f32p, sz, sz, f32p]),
+            "or_silu_array": (None, [f32p, f32p, sz]),
+            "or_expf_array": (None, [f32p, f32p, sz]),
+            "or_act_quant_scale_array": (None, [f32p, f32p, sz]),
+            "or_fp8_shared_expert": (c.c_int, [u8p, f32p, u8p, f32p, u8p, f32p, sz, sz, sz, sz, sz, sz, f32p, f32p]),
+        }
+        for name, (res, args) in sigs.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _f(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def _u(a):
+    return np.ascontiguousarray(a, np.uint8)
+
+
+def _pf(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _pu(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8))
+
+
+class OracleError(RuntimeError):
+    def __init__(self, code):
+        self.code = code
+        super().__init__(f"oracle status {code}")
+
+
+def luts():
+    fp8, ue, fp4, srt = (np.zeros(256, np.float32), np.zeros(256, np.float32),
+                         np.zeros(16, np.float32), np.zeros(256, np.float32))
+    lib().or_luts(_pf(fp8), _pf(ue), _pf(fp4), _pf(srt))
+    return fp8, ue, fp4, srt
+
+
+def set_threads(n: int):
+    lib().or_set_threads(int(n))
+
+
+def thread_count() -> int:
+    return lib().or_thread_count()
+
+
+def decode_ue8m0(scales_u8) -> np.ndarray:
+    _, ue, _, _ = luts()
+    return ue[_u(scales_u8)]
+
+
+def fp8_gemv(w, rows, cols, scales_f32, scale_rows, scale_cols, x, row_start=0, row_end=None, avx2=True):
+    w, s, x = _u(w), _f(scales_f32), _f(x)
+    row_end = rows if row_end is None else row_end
+    y = np.zeros(row_end - row_start, np.float32)
+    st = lib().or_fp8_gemv(_pu(w), rows, cols, _pf(s), scale_rows, scale_cols, row_start, row_end, _pf(x),
+                           _pf(y), 1 if avx2 else 0)
+    if st:
+        raise OracleError(st)
+    return y
+
+
+def fp8_dot_row(w_row, scales_f32, col_group, x, avx2=True):
+    w, s, x = _u(w_row), _f(scales_f32), _f(x)
+    fn = lib().or_fp8_dot_row_avx2 if avx2 else lib().or_fp8_dot_row_scalar
+    return fn(_pu(w), _pf(s), s.size, col_group, _pf(x))
+
+
+def fp4_matvec(packed, scales, rows, cols, scale_cols, x, force_path=-1):
+    p, s, x = _u(packed), _u(scales), _f(x)
+    y = np.zeros(rows, np.float32)
+    st = lib().or_fp4_matvec(_pu(p), p.size, _pu(s), s.size, rows, cols, scale_cols, _pf(x), x.size, _pf(y),
+                             y.size, force_path)
+    if st:
+        raise OracleError(st)
+    return y
+
+
+def act_quant(values, block=64):
+    v = _f(values).copy()
+    lib().or_act_quant_dequant(_pf(v), v.size, block)
+    return v
+
+
+def act_quant_scale(amax: float) -> float:
+    return lib().or_act_quant_scale(amax)
+
+
+def nearest_e4m3(t: float) -> float:
+    return lib().or_nearest_e4m3(t)
+
+
+def silu(x: float) -> float:
+    return lib().or_silu(x)
+
+
+def swiglu(g: float, u: float) -> float:
+    return lib().or_swiglu(g, u)
+
+
+def _spec(m):
+    packed, scales, rows, cols, scale_cols = m
+    p, s = _u(packed), _u(scales)
+    spec = Fp4Spec(_pu(p), p.size, _pu(s), s.size, rows, cols, scale_cols)
+    return spec, (p, s)
+
+
+def fp4_expert_forward(w1, w3, w2, x, force_path=-1, scratch_len=None):
+    """w1/w3/w2 = (packed, scales, rows, cols, scale_cols)."""
+    s1, k1 = _spec(w1)
+    s3, k3 = _spec(w3)
+    s2, k2 = _spec(w2)
+    x = _f(x)
+    y = np.zeros(w2[2], np.float32)
+    n_scratch = 2 * w1[2] if scratch_len is None else scratch_len
+    scratch = np.zeros(max(1, n_scratch), np.float32)
+    st = lib().or_fp4_expert_forward(ctypes.byref(s1), ctypes.byref(s3), ctypes.byref(s2), _pf(x), x.size,
+                                     _pf(y), y.size, _pf(scratch), n_scratch, force_path)
+    if st:
+        raise OracleError(st)
+    return y
+
+
+def routed_combine(outs, weights):
+    outs, w = _f(outs), _f(weights)
+    n, hidden = outs.shape
+    out = np.zeros(hidden, np.float32)
+    lib().or_routed_combine(_pf(outs), _pf(w), n, hidden, _pf(out))
+    return out
+
+
+def route_weight_sum(weights):
+    w = _f(weights)
+    s = ctypes.c_float()
+    ok = lib().or_route_weight_sum(_pf(w), w.size, ctypes.byref(s))
+    return s.value if ok else None
+
+
+def accumulate_expert(y_per_target, positions, weights, routed_acc):
+    y, w = _f(y_per_target), _f(weights)
+    pos = np.ascontiguousarray(positions, np.uintp)
+    acc = _f(routed_acc).copy()
+    hidden = acc.shape[-1]
+    lib().or_accumulate_expert(_pf(y), pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)), _pf(w), w.size,
+                               hidden, _pf(acc))
+    return acc
+
+
+def silu_array(x):
+    x = _f(x)
+    y = np.empty_like(x)
+    lib().or_silu_array(_pf(x), _pf(y), x.size)
+    return y
+
+
+def expf_array(x):
+    x = _f(x)
+    y = np.empty_like(x)
+    lib().or_expf_array(_pf(x), _pf(y), x.size)
+    return y
+
+
+def act_quant_scale_array(amax):
+    a = _f(amax)
+    y = np.empty_like(a)
+    lib().or_act_quant_scale_array(_pf(a), _pf(y), a.size)
+    return y

@@ -1,0 +1,429 @@
+"""wohper_amd - MI355X (gfx950) decode hot path of wohper's DeepSeek-V4 engine.
+
+Host mirror of the reference's kernel interface over the C ABI in
+include/wohper_hip.h (libwohper_hip.so, built from wohper_amd/csrc):
+
+  reference (engine/zc_infer_core/src)                this module
+  -------------------------------------------------   ---------------------------------
+  Fp4Matvec / DeepSeekV4Fp4Expert  deepseek_v4.rs:410-424      Fp4Matvec / DeepSeekV4Fp4Expert
+  fp4_e2m1_ue8m0_matvec_scalar     deepseek_v4.rs:464          fp4_e2m1_ue8m0_matvec_scalar
+  deepseek_v4_fp4_expert_forward_scalar deepseek_v4.rs:561     deepseek_v4_fp4_expert_forward_scalar
+  gemv_fp8_e4m3_ue8m0_tensorwise   compute.rs:6174             gemv_fp8_e4m3_ue8m0_tensorwise
+  gemv_fp8_e4m3_ue8m0_rows         compute.rs:6244             gemv_fp8_e4m3_ue8m0_rows
+  gemv_fp8_e4m3_ue8m0_rows_multi   compute.rs:6384             gemv_fp8_e4m3_ue8m0_rows_multi
+  fp8_act_quant_dequant_in_place   compute.rs:2504             fp8_act_quant_dequant_in_place
+  compute_active_experts           compute.rs:1948             Context.routed_experts
+  DeepSeekV4KernelError            deepseek_v4.rs:398-408      DeepSeekV4KernelError
+
+The slice-based functions upload the weights for the call, as the reference
+reads them from its I/O buffers; the resident path (Context.store_* plus the
+handle-based methods) keeps them in HBM.  There is no CPU fallback: without
+the HIP library or a GPU every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = _PKG / "libwohper_hip.so"
+
+STATUS_NAMES = {
+    0: "Ok",
+    1: "EmptyShape",
+    2: "InvalidShape",
+    3: "PackedWeightTooSmall",
+    4: "ScaleTooSmall",
+    5: "InputTooSmall",
+    6: "OutputTooSmall",
+    7: "ScratchTooSmall",
+    8: "NonFiniteOutput",
+    9: "InvalidQuantFormat",
+    10: "NotResident",
+    11: "OutOfMemory",
+    12: "HipError",
+    13: "InvalidArgument",
+    14: "NonFiniteInput",
+    15: "Unsupported",
+}
+
+SCALE_UE8M0 = 0
+SCALE_F32 = 1
+
+# every symbol include/wohper_hip.h declares
+EXPORTED = (
+    "wh_init", "wh_shutdown", "wh_status_string", "wh_synchronize", "wh_stream", "wh_build_info",
+    "wh_store_fp8", "wh_store_fp4", "wh_store_expert", "wh_store_expert_synthetic",
+    "wh_synth_fp4_host", "wh_store_release", "wh_store_usage", "wh_tensor_dequant",
+    "wh_fp8_gemv", "wh_fp8_gemv_multi", "wh_fp4_matvec", "wh_fp4_expert_forward",
+    "wh_act_quant_dequant", "wh_routed_experts", "wh_routed_experts_async", "wh_fp8_gemv_async",
+    "wh_stream_status", "wh_debug_eval", "wh_profile_enable", "wh_profile_read",
+    "wh_device_alloc", "wh_device_free", "wh_memcpy",
+)
+
+
+class DeepSeekV4KernelError(RuntimeError):
+    """Mirror of the reference's error enum (E/deepseek_v4.rs:398-408) plus
+    the store/runtime codes of the C ABI."""
+
+    def __init__(self, code: int, where: str = ""):
+        self.code = int(code)
+        self.name = STATUS_NAMES.get(self.code, f"status {code}")
+        super().__init__(f"{self.name}" + (f" ({where})" if where else ""))
+
+
+class WhExpertRoute(ctypes.Structure):
+    _fields_ = [("layer_id", ctypes.c_uint32), ("expert_id", ctypes.c_uint32),
+                ("route_weight", ctypes.c_float)]
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
+    """Loads libwohper_hip.so.  Raises if it was not built - there is no
+    fallback implementation."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(f"{p} is missing: run `python -m wohper_amd.build` (no CPU fallback exists)")
+    lib = ctypes.CDLL(str(p))
+    c = ctypes
+    vp, sz, u8p, f32p = c.c_void_p, c.c_size_t, c.POINTER(c.c_uint8), c.POINTER(c.c_float)
+    sig = {
+        "wh_init": (c.c_int, [c.c_int, c.POINTER(vp)]),
+        "wh_shutdown": (c.c_int, [vp]),
+        "wh_status_string": (c.c_char_p, [c.c_int]),
+        "wh_synchronize": (c.c_int, [vp]),
+        "wh_stream": (vp, [vp]),
+        "wh_build_info": (c.c_char_p, []),
+        "wh_store_fp8": (c.c_int, [vp, u8p, sz, sz, sz, vp, sz, c.c_int, sz, sz, c.POINTER(c.c_uint64)]),
+        "wh_store_fp4": (c.c_int, [vp, u8p, sz, u8p, sz, sz, sz, sz, c.POINTER(c.c_uint64)]),
+        "wh_store_expert": (c.c_int, [vp, c.c_uint32, c.c_uint32, c.c_uint64, c.c_uint64, c.c_uint64]),
+        "wh_store_expert_synthetic": (c.c_int, [vp, c.c_uint32, c.c_uint32, sz, sz, c.c_uint64,
+                                                c.c_uint32, c.c_uint32]),
+        "wh_synth_fp4_host": (None, [c.c_uint64, c.c_uint64, u8p, sz, u8p, sz, c.c_uint32, c.c_uint32]),
+        "wh_store_release": (c.c_int, [vp, c.c_uint64]),
+        "wh_store_usage": (c.c_int, [vp, c.POINTER(sz), c.POINTER(sz), c.POINTER(sz)]),
+        "wh_tensor_dequant": (c.c_int, [vp, c.c_uint64, f32p, sz]),
+        "wh_fp8_gemv": (c.c_int, [vp, c.c_uint64, sz, sz, f32p, sz, f32p, sz, c.POINTER(sz)]),
+        "wh_fp8_gemv_multi": (c.c_int, [vp, c.c_uint64, sz, sz, f32p, sz, sz, f32p, sz, c.POINTER(sz)]),
+        "wh_fp4_matvec": (c.c_int, [vp, c.c_uint64, f32p, sz, f32p, sz]),
+        "wh_fp4_expert_forward": (c.c_int, [vp, c.c_uint32, c.c_uint32, f32p, sz, f32p, sz, sz]),
+        "wh_act_quant_dequant": (c.c_int, [vp, f32p, sz, sz]),
+        "wh_routed_experts": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, f32p, sz]),
+        "wh_routed_experts_async": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, vp, c.c_int, sz, vp]),
+        "wh_fp8_gemv_async": (c.c_int, [vp, c.c_uint64, sz, sz, vp, vp]),
+        "wh_stream_status": (c.c_int, [vp]),
+        "wh_debug_eval": (c.c_int, [vp, c.c_int, f32p, f32p, sz]),
+        "wh_device_alloc": (c.c_int, [vp, sz, c.POINTER(vp)]),
+        "wh_device_free": (c.c_int, [vp, vp]),
+        "wh_memcpy": (c.c_int, [vp, vp, vp, sz, c.c_int]),
+        "wh_profile_enable": (c.c_int, [vp, sz]),
+        "wh_profile_read": (c.c_int, [vp, c.POINTER(c.c_double), c.POINTER(sz)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _u8(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a: np.ndarray, ct):
+    return a.ctypes.data_as(ctypes.POINTER(ct))
+
+
+def _check(code: int, where: str = ""):
+    if code != 0:
+        raise DeepSeekV4KernelError(code, where)
+
+
+class Context:
+    """One device context: a HIP stream plus the HBM weight store."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        _check(self.lib.wh_init(device, ctypes.byref(h)), "wh_init")
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self.lib.wh_shutdown(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self) -> int:
+        return self.lib.wh_stream(self._h)
+
+    def synchronize(self):
+        _check(self.lib.wh_synchronize(self._h), "deferred kernel status")
+
+    # ------------------------------------------------------------- store
+    def store_fp8(self, weight, rows: int, cols: int, scales, scale_rows: int, scale_cols: int,
+                  scale_format: int = SCALE_UE8M0) -> int:
+        w = _u8(weight).reshape(-1)
+        s = np.ascontiguousarray(scales, dtype=np.float32 if scale_format == SCALE_F32 else np.uint8).reshape(-1)
+        out = ctypes.c_uint64()
+        _check(self.lib.wh_store_fp8(self._h, _p(w, ctypes.c_uint8), w.size, rows, cols,
+                                     s.ctypes.data_as(ctypes.c_void_p), s.nbytes, scale_format,
+                                     scale_rows, scale_cols, ctypes.byref(out)), "store_fp8")
+        return out.value
+
+    def store_fp4(self, packed, scales, rows: int, cols: int, scale_cols: int) -> int:
+        w, s = _u8(packed).reshape(-1), _u8(scales).reshape(-1)
+        out = ctypes.c_uint64()
+        _check(self.lib.wh_store_fp4(self._h, _p(w, ctypes.c_uint8), w.size, _p(s, ctypes.c_uint8), s.size,
+                                     rows, cols, scale_cols, ctypes.byref(out)), "store_fp4")
+        return out.value
+
+    def store_expert(self, layer_id: int, expert_id: int, w1: int, w3: int, w2: int):
+        _check(self.lib.wh_store_expert(self._h, layer_id, expert_id, w1, w3, w2), "store_expert")
+
+    def store_fp4_expert(self, layer_id: int, expert_id: int, expert: "DeepSeekV4Fp4Expert"):
+        hs = [self.store_fp4(m.packed_weight, m.ue8m0_scales, m.rows, m.cols, m.scale_cols)
+              for m in (expert.w1, expert.w3, expert.w2)]
+        self.store_expert(layer_id, expert_id, *hs)
+        return hs
+
+    def store_expert_synthetic(self, layer_id: int, expert_id: int, hidden: int, inter: int,
+                               seed: int, scale_lo: int = 119, scale_hi: int = 127):
+        _check(self.lib.wh_store_expert_synthetic(self._h, layer_id, expert_id, hidden, inter, seed,
+                                                  scale_lo, scale_hi), "store_expert_synthetic")
+
+    def release(self, t: int):
+        _check(self.lib.wh_store_release(self._h, t), "release")
+
+    def usage(self):
+        b, t, e = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        _check(self.lib.wh_store_usage(self._h, ctypes.byref(b), ctypes.byref(t), ctypes.byref(e)))
+        return b.value, t.value, e.value
+
+    def dequant(self, t: int, rows: int, cols: int) -> np.ndarray:
+        out = np.empty(rows * cols, np.float32)
+        _check(self.lib.wh_tensor_dequant(self._h, t, _p(out, ctypes.c_float), out.size), "dequant")
+        return out.reshape(rows, cols)
+
+    # ---------------------------------------------------------- hot path
+    def fp8_gemv(self, t: int, x, out_rows: int, row_start: int = 0, row_end: Optional[int] = None):
+        x = _f32(x)
+        if row_end is None:
+            row_end = row_start + out_rows
+        y = np.empty(out_rows, np.float32)
+        vals = ctypes.c_size_t()
+        _check(self.lib.wh_fp8_gemv(self._h, t, row_start, row_end, _p(x, ctypes.c_float), x.size,
+                                    _p(y, ctypes.c_float), y.size, ctypes.byref(vals)), "fp8_gemv")
+        return y, vals.value
+
+    def fp8_gemv_multi(self, t: int, xs, row_start: int, row_end: int):
+        xs = _f32(xs)
+        n, k = xs.shape
+        y = np.empty((n, row_end - row_start), np.float32)
+        vals = ctypes.c_size_t()
+        _check(self.lib.wh_fp8_gemv_multi(self._h, t, row_start, row_end, _p(xs, ctypes.c_float), n, k,
+                                          _p(y, ctypes.c_float), y.shape[1], ctypes.byref(vals)),
+               "fp8_gemv_multi")
+        return y, vals.value
+
+    def fp4_matvec(self, t: int, x, rows: int):
+        x = _f32(x)
+        y = np.empty(rows, np.float32)
+        _check(self.lib.wh_fp4_matvec(self._h, t, _p(x, ctypes.c_float), x.size, _p(y, ctypes.c_float), y.size),
+               "fp4_matvec")
+        return y
+
+    def fp4_expert_forward(self, layer_id: int, expert_id: int, x, out_len: int, scratch_len: int):
+        x = _f32(x)
+        y = np.empty(out_len, np.float32)
+        _check(self.lib.wh_fp4_expert_forward(self._h, layer_id, expert_id, _p(x, ctypes.c_float), x.size,
+                                              _p(y, ctypes.c_float), y.size, scratch_len), "fp4_expert_forward")
+        return y
+
+    def act_quant_dequant(self, values, block_size: int = 64) -> np.ndarray:
+        v = _f32(values).copy()
+        _check(self.lib.wh_act_quant_dequant(self._h, _p(v, ctypes.c_float), v.size, block_size), "act_quant")
+        return v
+
+    def routed_experts(self, routes: Sequence[tuple], hidden) -> np.ndarray:
+        """compute_active_experts: routes = [(layer_id, expert_id, weight), ...]."""
+        h = _f32(hidden).copy()
+        arr = (WhExpertRoute * max(1, len(routes)))(*[WhExpertRoute(int(a), int(b), float(w)) for a, b, w in routes])
+        _check(self.lib.wh_routed_experts(self._h, arr, len(routes), _p(h, ctypes.c_float), h.size),
+               "routed_experts")
+        return h
+
+    def routed_experts_async(self, routes: Sequence[tuple], x_ptr: int, x_is_bf16: bool, n_tokens: int,
+                             out_ptr: int):
+        arr = (WhExpertRoute * len(routes))(*[WhExpertRoute(int(a), int(b), float(w)) for a, b, w in routes])
+        _check(self.lib.wh_routed_experts_async(self._h, arr, len(routes), ctypes.c_void_p(x_ptr),
+                                                int(x_is_bf16), n_tokens, ctypes.c_void_p(out_ptr)),
+               "routed_experts_async")
+
+    def fp8_gemv_async(self, t: int, row_start: int, row_end: int, x_ptr: int, y_ptr: int):
+        _check(self.lib.wh_fp8_gemv_async(self._h, t, row_start, row_end, ctypes.c_void_p(x_ptr),
+                                          ctypes.c_void_p(y_ptr)), "fp8_gemv_async")
+
+    def device_alloc(self, nbytes: int) -> int:
+        p = ctypes.c_void_p()
+        _check(self.lib.wh_device_alloc(self._h, nbytes, ctypes.byref(p)), "device_alloc")
+        return p.value or 0
+
+    def device_free(self, ptr: int):
+        _check(self.lib.wh_device_free(self._h, ctypes.c_void_p(ptr)), "device_free")
+
+    def to_device(self, ptr: int, arr: np.ndarray):
+        a = np.ascontiguousarray(arr)
+        _check(self.lib.wh_memcpy(self._h, ctypes.c_void_p(ptr), a.ctypes.data_as(ctypes.c_void_p), a.nbytes, 0),
+               "memcpy h2d")
+
+    def from_device(self, arr: np.ndarray, ptr: int):
+        assert arr.flags.c_contiguous
+        _check(self.lib.wh_memcpy(self._h, arr.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(ptr), arr.nbytes, 1),
+               "memcpy d2h")
+
+    def profile_enable(self, max_steps: int):
+        _check(self.lib.wh_profile_enable(self._h, max_steps), "profile_enable")
+
+    def profile_read(self):
+        """Mean microseconds of (act-quant, gate/up, down) over the recorded steps."""
+        avg = (ctypes.c_double * 3)()
+        n = ctypes.c_size_t()
+        _check(self.lib.wh_profile_read(self._h, avg, ctypes.byref(n)), "profile_read")
+        return list(avg), n.value
+
+    def debug_eval(self, fn: int, x) -> np.ndarray:
+        x = _f32(x)
+        y = np.empty_like(x)
+        _check(self.lib.wh_debug_eval(self._h, fn, _p(x, ctypes.c_float), _p(y, ctypes.c_float), x.size),
+               "debug_eval")
+        return y
+
+
+# ------------------------------------------- reference-shaped slice API
+@dataclass
+class Fp4Matvec:
+    """E/deepseek_v4.rs:410-417"""
+    packed_weight: np.ndarray
+    ue8m0_scales: np.ndarray
+    rows: int
+    cols: int
+    scale_cols: int
+
+
+@dataclass
+class DeepSeekV4Fp4Expert:
+    """E/deepseek_v4.rs:419-424"""
+    w1: Fp4Matvec
+    w3: Fp4Matvec
+    w2: Fp4Matvec
+
+
+_default_ctx: Optional[Context] = None
+
+
+def default_context() -> Context:
+    global _default_ctx
+    if _default_ctx is None:
+        _default_ctx = Context(0)
+    return _default_ctx
+
+
+def fp4_e2m1_ue8m0_matvec_scalar(spec: Fp4Matvec, input, output: np.ndarray, ctx: Optional[Context] = None):
+    """E/deepseek_v4.rs:464 on the GPU; output[:rows] is written."""
+    ctx = ctx or default_context()
+    x = _f32(input)
+    # validate_fp4_matvec order (E/deepseek_v4.rs:434-462)
+    if spec.rows == 0 or spec.cols == 0 or spec.scale_cols == 0:
+        raise DeepSeekV4KernelError(1)
+    if x.size < spec.cols:
+        raise DeepSeekV4KernelError(5)
+    if output.size < spec.rows:
+        raise DeepSeekV4KernelError(6)
+    t = ctx.store_fp4(spec.packed_weight, spec.ue8m0_scales, spec.rows, spec.cols, spec.scale_cols)
+    try:
+        output[: spec.rows] = ctx.fp4_matvec(t, x[: spec.cols], spec.rows)
+    finally:
+        ctx.release(t)
+
+
+def deepseek_v4_fp4_expert_forward_scalar(expert: DeepSeekV4Fp4Expert, input, output: np.ndarray,
+                                          scratch_len: int, ctx: Optional[Context] = None,
+                                          key=(0xFFFFFFFF, 0xFFFFFFFF)):
+    """E/deepseek_v4.rs:561 on the GPU."""
+    ctx = ctx or default_context()
+    x = _f32(input)
+    hs = ctx.store_fp4_expert(key[0], key[1], expert)
+    try:
+        output[: expert.w2.rows] = ctx.fp4_expert_forward(key[0], key[1], x, output.size, scratch_len)[: expert.w2.rows]
+    finally:
+        for h in hs:
+            ctx.release(h)
+
+
+def fp8_act_quant_dequant_in_place(values: np.ndarray, block_size: int, ctx: Optional[Context] = None):
+    """E/compute.rs:2504 on the GPU (values: float32 array, modified in place)."""
+    ctx = ctx or default_context()
+    values[...] = ctx.act_quant_dequant(values, block_size).reshape(values.shape)
+
+
+def gemv_fp8_e4m3_ue8m0_rows(weight, rows: int, cols: int, scales, scale_rows: int, scale_cols: int,
+                             row_start: int, row_end: int, input, output: np.ndarray,
+                             scale_format: int = SCALE_UE8M0, ctx: Optional[Context] = None) -> int:
+    """E/compute.rs:6244 on the GPU; returns the consumed value count."""
+    ctx = ctx or default_context()
+    t = ctx.store_fp8(weight, rows, cols, scales, scale_rows, scale_cols, scale_format)
+    try:
+        y, vals = ctx.fp8_gemv(t, input, row_end - row_start, row_start, row_end)
+        output[: row_end - row_start] = y
+        return vals
+    finally:
+        ctx.release(t)
+
+
+def gemv_fp8_e4m3_ue8m0_tensorwise(weight, rows: int, cols: int, scales, scale_rows: int, scale_cols: int,
+                                   input, output: np.ndarray, scale_format: int = SCALE_UE8M0,
+                                   ctx: Optional[Context] = None) -> int:
+    """E/compute.rs:6174 on the GPU."""
+    return gemv_fp8_e4m3_ue8m0_rows(weight, rows, cols, scales, scale_rows, scale_cols, 0, rows, input,
+                                    output, scale_format, ctx)
+
+
+def gemv_fp8_e4m3_ue8m0_rows_multi(weight, rows: int, cols: int, scales, scale_rows: int, scale_cols: int,
+                                   row_start: int, row_end: int, inputs, scale_format: int = SCALE_UE8M0,
+                                   ctx: Optional[Context] = None):
+    """E/compute.rs:6384 on the GPU: returns (outputs [n x rows], values)."""
+    ctx = ctx or default_context()
+    t = ctx.store_fp8(weight, rows, cols, scales, scale_rows, scale_cols, scale_format)
+    try:
+        return ctx.fp8_gemv_multi(t, inputs, row_start, row_end)
+    finally:
+        ctx.release(t)

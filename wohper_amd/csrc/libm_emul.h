@@ -1,0 +1,148 @@
+// glibc-exact float libm pieces used on the decode path, shared by the HIP
+// device code and by the host-side table generator (gen_libm_tables.c).
+//
+// The reference engine calls the platform libm through Rust's f32 methods:
+//   silu(x) = x / (1 + expf(-x))                 E/deepseek_v4.rs:551-554
+//   act-quant block scale exp2f(ceilf(log2f(r)))  E/compute.rs:2514
+// glibc's expf is not correctly rounded (it misrounds roughly 7e-5 of the
+// inputs in [-10, 89]), so matching it bit for bit needs more than an
+// accurate exp.  The scheme here:
+//   1. wh_exp_double(y): exp(y) in double, relative error below 1e-15
+//      (Cody-Waite reduction by ln2/32, 32-entry 2^(j/32) table, degree-6
+//      Taylor polynomial), built only from IEEE add/mul/fma/rint, so host
+//      and device evaluate it to the same bits.
+//   2. Round to float.  If the double result lies within
+//      WH_EXPF_WINDOW ulp of a float rounding midpoint, look the input up in
+//      a sorted table of inputs where glibc's result is the other neighbour
+//      of that midpoint, and flip.  The generator builds that table by
+//      comparing this exact code with the host glibc expf over every float
+//      input of the silu domain [-10, +inf), and then re-verifies the whole
+//      domain.
+//   3. ceil(log2f(r)) for normal r is e + (mantissa > T[e]), where the
+//      per-binade thresholds T[] are found by scanning the host log2f and
+//      verified over every mantissa of every binade.
+#pragma once
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define WH_HD __host__ __device__ inline
+#else
+#define WH_HD static inline
+#endif
+
+#define WH_EXPF_WINDOW 0.003  // in float ulps; must exceed glibc's error beyond 0.5 ulp
+
+WH_HD double wh_bits_to_double(uint64_t b) {
+    union { uint64_t u; double d; } v;
+    v.u = b;
+    return v.d;
+}
+WH_HD uint64_t wh_double_to_bits(double d) {
+    union { uint64_t u; double d; } v;
+    v.d = d;
+    return v.u;
+}
+WH_HD float wh_bits_to_float(uint32_t b) {
+    union { uint32_t u; float f; } v;
+    v.u = b;
+    return v.f;
+}
+WH_HD uint32_t wh_float_to_bits(float f) {
+    union { uint32_t u; float f; } v;
+    v.f = f;
+    return v.u;
+}
+
+// exp(y) for finite y with |y| < 104 (callers clamp).  exp2_tab holds, as
+// double bit patterns, 2^(j/32) for j = 0..31, then 32/ln2, then ln2/32 split
+// into a 32-significant-bit head (so n*head is exact) and a tail; the
+// generator derives them from long double arithmetic.
+WH_HD double wh_exp_double(float yf, const uint64_t* exp2_tab) {
+    const double inv_l = wh_bits_to_double(exp2_tab[32]);
+    const double l_hi = wh_bits_to_double(exp2_tab[33]);
+    const double l_lo = wh_bits_to_double(exp2_tab[34]);
+    double x = (double)yf;
+    double nd = __builtin_rint(x * inv_l);
+    double r = __builtin_fma(-nd, l_hi, x);
+    r = __builtin_fma(-nd, l_lo, r);
+    // Taylor polynomial of exp(r) on |r| <= ln2/64, Horner with fma
+    double p = 1.0 / 720.0;
+    p = __builtin_fma(p, r, 1.0 / 120.0);
+    p = __builtin_fma(p, r, 1.0 / 24.0);
+    p = __builtin_fma(p, r, 1.0 / 6.0);
+    p = __builtin_fma(p, r, 0.5);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
+    int64_t n = (int64_t)nd;
+    int64_t j = n & 31;
+    int64_t k = (n - j) / 32;  // exact floor division
+    double t = wh_bits_to_double(exp2_tab[j]);
+    double s = wh_bits_to_double((uint64_t)(k + 1023) << 52);  // 2^k, |k| < 160 here
+    return (t * p) * s;
+}
+
+// Returns 1 if the double result `d` (positive, finite) is within the window
+// of the rounding midpoint between float(d) and its neighbour on d's side.
+WH_HD int wh_expf_near_midpoint(double d, float f) {
+    double fd = (double)f;
+    double diff = d - fd;
+    uint32_t fb = wh_float_to_bits(f);
+    int ex = (int)((fb >> 23) & 0xff);
+    if (ex == 0 || ex == 0xff) return 1;  // subnormal / inf: always consult the table
+    double ulp = wh_bits_to_double((uint64_t)(ex - 127 - 23 + 1023) << 52);
+    // below a power of two the neighbour spacing halves
+    double ulp_side = (diff < 0.0 && (fb & 0x7fffff) == 0) ? ulp * 0.5 : ulp;
+    double dist = 0.5 * ulp_side - (diff < 0.0 ? -diff : diff);
+    return dist < WH_EXPF_WINDOW * ulp_side;
+}
+
+WH_HD int wh_table_contains(const uint32_t* tab, uint32_t n, uint32_t key) {
+    uint32_t lo = 0, hi = n;
+    while (lo < hi) {
+        uint32_t mid = (lo + hi) >> 1;
+        uint32_t v = tab[mid];
+        if (v == key) return 1;
+        if (v < key) lo = mid + 1;
+        else hi = mid;
+    }
+    return 0;
+}
+
+// glibc-exact expf(y) for y in [-10, +inf) (the silu domain); y is never NaN
+// there.  `flip` lists (sorted) the inputs whose glibc result is the other
+// neighbour of the nearby rounding midpoint.
+WH_HD float wh_expf_glibc(float y, const uint64_t* exp2_tab, const uint32_t* flip, uint32_t nflip) {
+    if (y > 89.0f) return wh_bits_to_float(0x7f800000u);
+    double d = wh_exp_double(y, exp2_tab);
+    float f = (float)d;
+    if (wh_expf_near_midpoint(d, f) && wh_table_contains(flip, nflip, wh_float_to_bits(y))) {
+        uint32_t fb = wh_float_to_bits(f);
+        double diff = d - (double)f;
+        if ((fb & 0x7fffffffu) == 0x7f800000u) {
+            f = wh_bits_to_float(0x7f7fffffu);  // inf -> FLT_MAX
+        } else {
+            f = wh_bits_to_float(diff > 0.0 ? fb + 1 : fb - 1);  // positive f: +1 bit = next up
+        }
+    }
+    return f;
+}
+
+// silu exactly as the reference computes it in f32: x / (1 + expf(-x)).
+WH_HD float wh_silu(float x, const uint64_t* exp2_tab, const uint32_t* flip, uint32_t nflip) {
+    float e = wh_expf_glibc(-x, exp2_tab, flip, nflip);
+    float den = 1.0f + e;
+    return x / den;
+}
+
+// ceil(log2f(r)) for a positive normal float r, glibc-exact given the
+// per-binade thresholds thr[e + 126] (e = unbiased exponent, -126..127).
+WH_HD int wh_ceil_log2f(float r, const uint32_t* thr) {
+    uint32_t b = wh_float_to_bits(r);
+    int e = (int)((b >> 23) & 0xff) - 127;
+    uint32_t m = b & 0x7fffff;
+    if (m == 0) return e;
+    return m > thr[e + 126] ? e + 1 : e;
+}
+
+// 2^k as float for -126 <= k <= 127 (exp2f of an integral float is exact there).
+WH_HD float wh_pow2f(int k) { return wh_bits_to_float((uint32_t)(k + 127) << 23); }

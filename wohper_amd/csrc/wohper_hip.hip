@@ -1,0 +1,1029 @@
+// Host side of the MI355X decode hot path: context, HBM weight store,
+// resident layouts, and the C ABI declared in include/wohper_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "libm_tables.inc"
+#define WH_LIBM_TABLES_INCLUDED 1
+#include "kernels.h"
+#include "wohper_hip.h"
+
+namespace {
+
+constexpr int kFp8 = 1, kFp4 = 2;
+
+struct Tensor {
+    int kind = 0;
+    uint8_t* w = nullptr;  // device
+    void* s = nullptr;     // device scales
+    size_t rows = 0, cols = 0, scale_rows = 0, scale_cols = 0;
+    int scale_fmt = WH_SCALE_UE8M0;
+    bool fast = false;     // resident lane layout (else original row-major)
+    bool special = false;  // FP8 codes 0x7F/0xFF present
+    size_t bytes = 0;
+};
+
+struct Expert {
+    wh_tensor w1 = 0, w3 = 0, w2 = 0;
+};
+
+// Bump allocator over large hipMalloc chunks: tensors of a weight store are
+// never freed individually in the hot path, and a 150 GB stack would
+// otherwise need ~10^5 separate allocations.
+struct Arena {
+    std::vector<void*> chunks;
+    uint8_t* cur = nullptr;
+    size_t left = 0;
+    size_t total = 0;
+    static constexpr size_t kChunk = size_t(4) << 30;
+
+    hipError_t alloc(size_t n, void** out) {
+        n = (n + 255) & ~size_t(255);
+        if (n > left) {
+            size_t sz = std::max(n, kChunk);
+            void* p = nullptr;
+            hipError_t e = hipMalloc(&p, sz);
+            if (e != hipSuccess) {
+                // retry with an exact-size chunk before giving up
+                if (sz != n && hipMalloc(&p, n) == hipSuccess) {
+                    (void)hipGetLastError();
+                    chunks.push_back(p);
+                    total += n;
+                    *out = p;
+                    return hipSuccess;
+                }
+                return e;
+            }
+            chunks.push_back(p);
+            cur = (uint8_t*)p;
+            left = sz;
+            total += sz;
+        }
+        *out = cur;
+        cur += n;
+        left -= n;
+        return hipSuccess;
+    }
+    void release_all() {
+        for (void* p : chunks) (void)hipFree(p);
+        chunks.clear();
+        cur = nullptr;
+        left = total = 0;
+    }
+};
+
+// Device scratch that grows on demand (allocation happens outside the
+// steady state: the first call at a given size allocates, later calls reuse).
+struct Scratch {
+    void* p = nullptr;
+    size_t n = 0;
+    hipError_t ensure(size_t bytes, bool zero) {
+        if (bytes <= n) return hipSuccess;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+        hipError_t e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return e;
+        if (zero) {
+            e = hipMemset(p, 0, bytes);
+            if (e != hipSuccess) return e;
+        }
+        n = bytes;
+        return hipSuccess;
+    }
+    template <class T>
+    T* as() const { return (T*)p; }
+};
+
+struct HostBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    hipError_t ensure(size_t bytes) {
+        if (bytes <= n) return hipSuccess;
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        n = 0;
+        hipError_t e = hipHostMalloc(&p, bytes, hipHostMallocDefault);
+        if (e != hipSuccess) return e;
+        n = bytes;
+        return hipSuccess;
+    }
+};
+
+}  // namespace
+
+struct wh_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    Arena arena;
+    std::unordered_map<wh_tensor, Tensor> tensors;
+    std::map<std::pair<uint32_t, uint32_t>, Expert> experts;
+    wh_tensor next_id = 1;
+    size_t device_bytes = 0;
+    uint32_t* status = nullptr;  // device status word
+    uint32_t* status_host = nullptr;
+    Scratch x_in, y_out, xq_codes, xq_scales, h, hq_codes, hq_scales, ybuf, cnt_h, cnt_y, tmp;
+    HostBuf stage_in, stage_out;
+    std::mutex mu;
+    // optional per-kernel timing of the routed-expert pipeline (off by default)
+    bool prof = false;
+    std::vector<hipEvent_t> prof_ev;   // 4 events per recorded step
+    size_t prof_steps = 0, prof_cap = 0;
+};
+
+namespace {
+
+int hip_status(hipError_t e) {
+    if (e == hipSuccess) return WH_OK;
+    if (e == hipErrorOutOfMemory) return WH_OUT_OF_MEMORY;
+    return WH_HIP_ERROR;
+}
+
+#define WH_HIP(expr)                                  \
+    do {                                              \
+        hipError_t _e = (expr);                       \
+        if (_e != hipSuccess) return hip_status(_e);  \
+    } while (0)
+
+#define WH_TRY(expr)               \
+    do {                           \
+        int _s = (expr);           \
+        if (_s != WH_OK) return _s; \
+    } while (0)
+
+int read_status(wh_ctx* c) {
+    WH_HIP(hipMemcpyAsync(c->status_host, c->status, sizeof(uint32_t), hipMemcpyDeviceToHost,
+                          c->stream));
+    WH_HIP(hipStreamSynchronize(c->stream));
+    uint32_t st = *c->status_host;
+    if (st) {
+        WH_HIP(hipMemsetAsync(c->status, 0, sizeof(uint32_t), c->stream));
+        WH_HIP(hipStreamSynchronize(c->stream));
+    }
+    if (st & WH_ST_NONFINITE_INPUT) return WH_NON_FINITE_INPUT;
+    if (st & WH_ST_NONFINITE_OUTPUT) return WH_NON_FINITE_OUTPUT;
+    return WH_OK;
+}
+
+Tensor* find_tensor(wh_ctx* c, wh_tensor t) {
+    auto it = c->tensors.find(t);
+    return it == c->tensors.end() ? nullptr : &it->second;
+}
+
+int alloc_device(wh_ctx* c, size_t n, void** out) {
+    hipError_t e = c->arena.alloc(n, out);
+    if (e != hipSuccess) return hip_status(e);
+    c->device_bytes += n;
+    return WH_OK;
+}
+
+int upload(wh_ctx* c, void* dst, const void* src, size_t n) {
+    if (n == 0) return WH_OK;
+    WH_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream));
+    WH_HIP(hipStreamSynchronize(c->stream));
+    return WH_OK;
+}
+
+// FP8 resident permutation within each 128-col group (see kernels.h).
+void fp8_permute_row(const uint8_t* src, uint8_t* dst, size_t cols) {
+    for (size_t g = 0; g < cols / 128; ++g) {
+        const uint8_t* s = src + g * 128;
+        uint8_t* d = dst + g * 128;
+        for (int l = 0; l < 8; ++l)
+            for (int i = 0; i < 16; ++i) d[l * 16 + i] = s[(i & 7) * 16 + (i >> 3) * 8 + l];
+    }
+}
+
+// FP4 resident encoding of one row (see wh_fp4_decode8).
+void fp4_encode_row(const uint8_t* src, uint8_t* dst, size_t cols) {
+    auto nib = [src](size_t col) -> uint32_t {
+        uint8_t b = src[col >> 1];
+        return (col & 1) ? (b >> 4) : (b & 15);
+    };
+    for (size_t sp = 0; sp < cols / 256; ++sp) {
+        for (uint32_t l = 0; l < 8; ++l) {
+            for (uint32_t d = 0; d < 4; ++d) {
+                size_t ga = sp * 8 + d * 2, gb = ga + 1;
+                uint32_t word = 0;
+                for (uint32_t k = 0; k < 4; ++k) {
+                    uint32_t a = nib(32 * ga + l + 8 * k);
+                    uint32_t aprev = nib(32 * ga + l + 8 * ((k + 3) & 3));
+                    uint32_t b = nib(32 * gb + l + 8 * k);
+                    uint32_t byte = (a & 7) | ((aprev >> 3) << 3) | ((b & 7) << 4) | ((b >> 3) << 7);
+                    word |= byte << (8 * k);
+                }
+                std::memcpy(dst + sp * 128 + l * 16 + d * 4, &word, 4);
+            }
+        }
+    }
+}
+
+hipError_t kernel_setup_once() {
+    static std::once_flag once;
+    static hipError_t err = hipSuccess;
+    std::call_once(once, [] {
+        const int lds = 160 * 1024;
+        hipError_t e = hipSuccess;
+        auto set = [&](const void* f) {
+            hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+            if (r != hipSuccess && e == hipSuccess) e = r;
+        };
+        set((const void*)k_fp8_gemv<false, false>);
+        set((const void*)k_fp8_gemv<false, true>);
+        set((const void*)k_fp8_gemv<true, false>);
+        set((const void*)k_fp8_gemv<true, true>);
+        set((const void*)k_fp4_matvec);
+        set((const void*)k_moe_gateup);
+        set((const void*)k_moe_down);
+        err = e;
+    });
+    return err;
+}
+
+// ------------------------------------------------------------ FP8 launch
+int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x, float* y,
+               size_t n_batch, size_t x_stride, size_t y_stride) {
+    wh_fp8_args a;
+    a.w = t.w;
+    a.scales = t.s;
+    a.x = x;
+    a.y = y;
+    a.status = c->status;
+    a.cols = (uint32_t)t.cols;
+    a.scale_cols = (uint32_t)t.scale_cols;
+    a.row_group = (uint32_t)(t.rows / t.scale_rows);
+    a.row_start = (uint32_t)r0;
+    a.row_end = (uint32_t)r1;
+    a.x_stride = (uint32_t)x_stride;
+    a.y_stride = (uint32_t)y_stride;
+    bool u8 = t.scale_fmt == WH_SCALE_UE8M0;
+    if (t.fast) {
+        dim3 grid((unsigned)((r1 - r0 + 31) / 32), (unsigned)n_batch);
+        size_t lds = t.cols * sizeof(float);
+        if (t.special) {
+            if (u8) k_fp8_gemv<true, true><<<grid, 256, lds, c->stream>>>(a);
+            else k_fp8_gemv<true, false><<<grid, 256, lds, c->stream>>>(a);
+        } else {
+            if (u8) k_fp8_gemv<false, true><<<grid, 256, lds, c->stream>>>(a);
+            else k_fp8_gemv<false, false><<<grid, 256, lds, c->stream>>>(a);
+        }
+    } else {
+        dim3 grid((unsigned)((r1 - r0 + 63) / 64), (unsigned)n_batch);
+        uint32_t col_group = (uint32_t)(t.cols / t.scale_cols);
+        if (u8) k_fp8_gemv_generic<true><<<grid, 64, 0, c->stream>>>(a, col_group);
+        else k_fp8_gemv_generic<false><<<grid, 64, 0, c->stream>>>(a, col_group);
+    }
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+int launch_fp4(wh_ctx* c, const Tensor& t, const float* x, float* y) {
+    wh_fp4_args a;
+    a.w = t.w;
+    a.s = (const uint8_t*)t.s;
+    a.x = x;
+    a.y = y;
+    a.status = c->status;
+    a.rows = (uint32_t)t.rows;
+    a.cols = (uint32_t)t.cols;
+    if (t.fast) {
+        k_fp4_matvec<<<(unsigned)((t.rows + 31) / 32), 256, t.cols * sizeof(float), c->stream>>>(a);
+    } else {
+        k_fp4_matvec_generic<<<(unsigned)((t.rows + 63) / 64), 64, 0, c->stream>>>(a, (uint32_t)t.scale_cols);
+    }
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+__global__ void k_swiglu_generic(const float* g, const float* u, float* h, uint32_t n,
+                                 uint32_t* status) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) h[i] = wh_swiglu(g[i], u[i], kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
+}
+
+__global__ void k_combine_generic(const float* y, const float* w, uint32_t n_experts,
+                                  uint32_t hidden, float* out) {
+    uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= hidden) return;
+    if (n_experts == 1) {
+        out[r] = y[r];
+        return;
+    }
+    float sum = 0.0f;
+    bool valid = true;
+    for (uint32_t i = 0; i < n_experts; ++i) {
+        float wi = w[i];
+        if (!(fabsf(wi) <= 3.4028235e38f && wi >= 0.0f)) valid = false;
+        sum = sum + wi;
+    }
+    if (sum <= 1.1920929e-07f) valid = false;
+    float uniform = 1.0f / (float)n_experts;
+    float o = 0.0f;
+    for (uint32_t i = 0; i < n_experts; ++i) {
+        float wi = valid ? w[i] / sum : uniform;
+        float p = y[(size_t)i * hidden + r] * wi;
+        o = o + p;
+    }
+    out[r] = o;
+}
+
+struct ExpertView {
+    const Tensor *w1, *w3, *w2;
+};
+
+int resolve_expert(wh_ctx* c, uint32_t layer, uint32_t expert, ExpertView* v) {
+    auto it = c->experts.find({layer, expert});
+    if (it == c->experts.end()) return WH_NOT_RESIDENT;
+    v->w1 = find_tensor(c, it->second.w1);
+    v->w3 = find_tensor(c, it->second.w3);
+    v->w2 = find_tensor(c, it->second.w2);
+    if (!v->w1 || !v->w3 || !v->w2) return WH_NOT_RESIDENT;
+    return WH_OK;
+}
+
+bool expert_fast(const ExpertView& v) {
+    return v.w1->fast && v.w3->fast && v.w2->fast && v.w1->cols % 256 == 0 &&
+           v.w1->rows % 256 == 0 && v.w1->rows * 4 <= 160 * 1024 && v.w1->cols * 4 <= 160 * 1024;
+}
+
+// Routed experts for n_tokens rows of x (all with the same route list).
+// x_dev: device input (f32 or bf16).  out_dev: n_tokens x hidden f32.
+int moe_forward(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n, const void* x_dev,
+                int x_bf16, size_t n_tokens, float* out_dev) {
+    const size_t hidden = ev[0].w1->cols, inter = ev[0].w1->rows, osz = ev[0].w2->rows;
+    bool fast = osz == hidden;
+    for (size_t i = 0; i < n; ++i) {
+        if (ev[i].w1->cols != hidden || ev[i].w1->rows != inter || ev[i].w2->rows != osz)
+            return WH_INVALID_SHAPE;
+        fast = fast && expert_fast(ev[i]);
+    }
+    if (fast && n <= WH_MAX_EXPERTS) {
+        WH_HIP(c->xq_codes.ensure(n_tokens * hidden, false));
+        WH_HIP(c->xq_scales.ensure(n_tokens * (hidden / 64) * sizeof(float), false));
+        WH_HIP(c->h.ensure(n_tokens * n * inter * sizeof(float), false));
+        WH_HIP(c->hq_codes.ensure(n_tokens * n * inter, false));
+        WH_HIP(c->hq_scales.ensure(n_tokens * n * (inter / 64) * sizeof(float), false));
+        WH_HIP(c->ybuf.ensure(n_tokens * n * hidden * sizeof(float), false));
+        WH_HIP(c->cnt_h.ensure(n_tokens * n * (inter / 64) * sizeof(uint32_t), true));
+        WH_HIP(c->cnt_y.ensure(n_tokens * (hidden / 32) * sizeof(uint32_t), true));
+        wh_moe_args a;
+        std::memset(&a, 0, sizeof a);
+        for (size_t i = 0; i < n; ++i) {
+            a.ex[i].w1 = ev[i].w1->w;
+            a.ex[i].s1 = (const uint8_t*)ev[i].w1->s;
+            a.ex[i].w3 = ev[i].w3->w;
+            a.ex[i].s3 = (const uint8_t*)ev[i].w3->s;
+            a.ex[i].w2 = ev[i].w2->w;
+            a.ex[i].s2 = (const uint8_t*)ev[i].w2->s;
+            a.route_w[i] = route_w[i];
+        }
+        a.n_experts = (uint32_t)n;
+        a.hidden = (uint32_t)hidden;
+        a.inter = (uint32_t)inter;
+        a.n_tokens = (uint32_t)n_tokens;
+        a.xq_codes = c->xq_codes.as<uint8_t>();
+        a.xq_scales = c->xq_scales.as<float>();
+        a.h = c->h.as<float>();
+        a.hq_codes = c->hq_codes.as<uint8_t>();
+        a.hq_scales = c->hq_scales.as<float>();
+        a.y = c->ybuf.as<float>();
+        a.out = out_dev;
+        a.cnt_h = c->cnt_h.as<uint32_t>();
+        a.cnt_y = c->cnt_y.as<uint32_t>();
+        a.status = c->status;
+        unsigned aq_blocks = (unsigned)((n_tokens * hidden + 63) / 64);
+        hipEvent_t* ev = nullptr;
+        if (c->prof && c->prof_steps < c->prof_cap) ev = &c->prof_ev[4 * c->prof_steps++];
+        if (ev) WH_HIP(hipEventRecord(ev[0], c->stream));
+        k_act_quant_codes<<<aq_blocks, 64, 0, c->stream>>>(x_dev, x_bf16, (uint32_t)(n_tokens * hidden),
+                                                           c->xq_codes.as<uint8_t>(),
+                                                           c->xq_scales.as<float>(), c->status);
+        if (ev) WH_HIP(hipEventRecord(ev[1], c->stream));
+        k_moe_gateup<<<dim3((unsigned)(inter / 16), (unsigned)n, (unsigned)n_tokens), 128,
+                       hidden * sizeof(float), c->stream>>>(a);
+        if (ev) WH_HIP(hipEventRecord(ev[2], c->stream));
+        k_moe_down<<<dim3((unsigned)(hidden / 32), (unsigned)n, (unsigned)n_tokens), 256,
+                     inter * sizeof(float), c->stream>>>(a);
+        if (ev) WH_HIP(hipEventRecord(ev[3], c->stream));
+        WH_HIP(hipGetLastError());
+        return WH_OK;
+    }
+    // Generic composition (any shape the reference accepts), one token at a time.
+    if (x_bf16) return WH_UNSUPPORTED;
+    const size_t per = hidden + 3 * inter + n * osz + n;
+    WH_HIP(c->tmp.ensure(per * sizeof(float), false));
+    float* xq = c->tmp.as<float>();
+    float* g = xq + hidden;
+    float* u = g + inter;
+    float* hh = u + inter;
+    float* ys = hh + inter;
+    float* wdev = ys + n * osz;
+    WH_HIP(hipMemcpyAsync(wdev, route_w, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    for (size_t tok = 0; tok < n_tokens; ++tok) {
+        const float* xt = (const float*)x_dev + tok * hidden;
+        for (size_t i = 0; i < n; ++i) {
+            WH_HIP(hipMemcpyAsync(xq, xt, hidden * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
+            k_act_quant_inplace<<<(unsigned)((hidden + 63) / 64), 256, 0, c->stream>>>(xq, (uint32_t)hidden, 64);
+            WH_TRY(launch_fp4(c, *ev[i].w1, xq, g));
+            WH_TRY(launch_fp4(c, *ev[i].w3, xq, u));
+            k_swiglu_generic<<<(unsigned)((inter + 255) / 256), 256, 0, c->stream>>>(g, u, hh, (uint32_t)inter, c->status);
+            k_act_quant_inplace<<<(unsigned)((inter + 63) / 64), 256, 0, c->stream>>>(hh, (uint32_t)inter, 64);
+            WH_TRY(launch_fp4(c, *ev[i].w2, hh, ys + i * osz));
+        }
+        k_combine_generic<<<(unsigned)((osz + 255) / 256), 256, 0, c->stream>>>(
+            ys, wdev, (uint32_t)n, (uint32_t)osz, out_dev + tok * osz);
+        WH_HIP(hipGetLastError());
+    }
+    return WH_OK;
+}
+
+// splitmix64 finaliser, the counter-based generator of the synthetic weights
+__host__ __device__ inline uint64_t wh_mix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+__host__ __device__ inline uint8_t wh_synth_byte(uint64_t seed, uint64_t stream, uint64_t i) {
+    uint64_t v = wh_mix64(seed ^ wh_mix64(stream * 0x100000001b3ull + (i >> 3)));
+    return (uint8_t)(v >> (8 * (i & 7)));
+}
+
+// Device synthetic FP4 tensor straight into the resident layout: each
+// thread builds one lane dword from the generated original nibbles.
+__global__ void k_synth_fp4(uint8_t* w, uint8_t* s, uint32_t rows, uint32_t cols, uint64_t seed,
+                            uint64_t stream, uint32_t slo, uint32_t shi) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t spans = cols / 256;
+    const size_t words = (size_t)rows * spans * 32;
+    if (t < words) {
+        uint32_t d = t & 3, l = (t >> 2) & 7;
+        size_t rs = t >> 5;
+        uint32_t sp = rs % spans;
+        size_t row = rs / spans;
+        size_t rowbase = row * (cols / 2);
+        auto nib = [&](size_t col) -> uint32_t {
+            uint8_t b = wh_synth_byte(seed, stream, rowbase + (col >> 1));
+            return (col & 1) ? (b >> 4) : (b & 15);
+        };
+        size_t ga = (size_t)sp * 8 + d * 2, gb = ga + 1;
+        uint32_t word = 0;
+        for (uint32_t k = 0; k < 4; ++k) {
+            uint32_t a = nib(32 * ga + l + 8 * k);
+            uint32_t ap = nib(32 * ga + l + 8 * ((k + 3) & 3));
+            uint32_t b = nib(32 * gb + l + 8 * k);
+            word |= ((a & 7) | ((ap >> 3) << 3) | ((b & 7) << 4) | ((b >> 3) << 7)) << (8 * k);
+        }
+        ((uint32_t*)(w + rowbase + (size_t)sp * 128 + l * 16))[d] = word;
+    }
+    const size_t nscale = (size_t)rows * (cols / 32);
+    if (t < nscale) {
+        uint32_t span = shi - slo + 1;
+        s[t] = (uint8_t)(slo + wh_synth_byte(seed, stream ^ 0x5ca1e5ull, t) % span);
+    }
+}
+
+int store_tensor_common(wh_ctx* c, Tensor&& t, wh_tensor* out) {
+    wh_tensor id = c->next_id++;
+    c->tensors.emplace(id, std::move(t));
+    *out = id;
+    return WH_OK;
+}
+
+}  // namespace
+
+// ===================================================================== ABI
+extern "C" {
+
+const char* wh_status_string(int s) {
+    switch (s) {
+        case WH_OK: return "ok";
+        case WH_EMPTY_SHAPE: return "EmptyShape";
+        case WH_INVALID_SHAPE: return "InvalidShape";
+        case WH_PACKED_WEIGHT_TOO_SMALL: return "PackedWeightTooSmall";
+        case WH_SCALE_TOO_SMALL: return "ScaleTooSmall";
+        case WH_INPUT_TOO_SMALL: return "InputTooSmall";
+        case WH_OUTPUT_TOO_SMALL: return "OutputTooSmall";
+        case WH_SCRATCH_TOO_SMALL: return "ScratchTooSmall";
+        case WH_NON_FINITE_OUTPUT: return "NonFiniteOutput";
+        case WH_INVALID_QUANT_FORMAT: return "InvalidQuantFormat";
+        case WH_NOT_RESIDENT: return "NotResident";
+        case WH_OUT_OF_MEMORY: return "OutOfMemory";
+        case WH_HIP_ERROR: return "HipError";
+        case WH_INVALID_ARGUMENT: return "InvalidArgument";
+        case WH_NON_FINITE_INPUT: return "NonFiniteInput";
+        case WH_UNSUPPORTED: return "Unsupported";
+        default: return "unknown";
+    }
+}
+
+const char* wh_build_info(void) {
+    static char buf[160];
+    std::snprintf(buf, sizeof buf, "wohper_hip gfx950; expf flip table %u entries; max experts %d",
+                  (unsigned)WH_EXPF_FLIP_COUNT, WH_MAX_EXPERTS);
+    return buf;
+}
+
+int wh_init(int device, wh_ctx** out) {
+    if (!out) return WH_INVALID_ARGUMENT;
+    *out = nullptr;
+    int n = 0;
+    WH_HIP(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return WH_INVALID_ARGUMENT;
+    WH_HIP(hipSetDevice(device));
+    WH_HIP(kernel_setup_once());
+    wh_ctx* c = new wh_ctx();
+    c->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMalloc(&c->status, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(c->status, 0, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipHostMalloc((void**)&c->status_host, sizeof(uint32_t), hipHostMallocDefault);
+    if (e != hipSuccess) {
+        delete c;
+        return hip_status(e);
+    }
+    *out = c;
+    return WH_OK;
+}
+
+int wh_shutdown(wh_ctx* c) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    c->arena.release_all();
+    for (Scratch* s : {&c->x_in, &c->y_out, &c->xq_codes, &c->xq_scales, &c->h, &c->hq_codes,
+                       &c->hq_scales, &c->ybuf, &c->cnt_h, &c->cnt_y, &c->tmp})
+        if (s->p) (void)hipFree(s->p);
+    for (HostBuf* h : {&c->stage_in, &c->stage_out})
+        if (h->p) (void)hipHostFree(h->p);
+    for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
+    (void)hipFree(c->status);
+    (void)hipHostFree(c->status_host);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return WH_OK;
+}
+
+int wh_synchronize(wh_ctx* c) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    return read_status(c);
+}
+
+int wh_stream_status(wh_ctx* c) { return wh_synchronize(c); }
+
+void* wh_stream(wh_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+int wh_store_fp8(wh_ctx* c, const uint8_t* weight, size_t weight_len, size_t rows, size_t cols,
+                 const void* scales, size_t scales_len, int scale_format, size_t scale_rows,
+                 size_t scale_cols, wh_tensor* out) {
+    if (!c || !out || !weight || !scales) return WH_INVALID_ARGUMENT;
+    if (scale_format != WH_SCALE_UE8M0 && scale_format != WH_SCALE_F32) return WH_INVALID_QUANT_FORMAT;
+    // E/compute.rs:6184-6215
+    if (rows == 0 || cols == 0 || scale_rows == 0 || scale_cols == 0 || rows % scale_rows ||
+        cols % scale_cols)
+        return WH_INVALID_SHAPE;
+    if (weight_len < rows * cols) return WH_PACKED_WEIGHT_TOO_SMALL;
+    size_t sbytes = scale_rows * scale_cols * (scale_format == WH_SCALE_F32 ? 4 : 1);
+    if (scales_len < sbytes) return WH_SCALE_TOO_SMALL;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    Tensor t;
+    t.kind = kFp8;
+    t.rows = rows;
+    t.cols = cols;
+    t.scale_rows = scale_rows;
+    t.scale_cols = scale_cols;
+    t.scale_fmt = scale_format;
+    t.fast = (cols / scale_cols == 128) && cols * 4 <= 160 * 1024;
+    for (size_t i = 0; i < rows * cols && !t.special; ++i) t.special = (weight[i] & 0x7f) == 0x7f;
+    t.bytes = rows * cols + sbytes;
+    void* wd = nullptr;
+    void* sd = nullptr;
+    WH_TRY(alloc_device(c, rows * cols, &wd));
+    WH_TRY(alloc_device(c, sbytes, &sd));
+    t.w = (uint8_t*)wd;
+    t.s = sd;
+    const size_t chunk_rows = std::max<size_t>(1, (size_t(64) << 20) / cols);
+    WH_HIP(c->stage_in.ensure(std::min(rows, chunk_rows) * cols));
+    for (size_t r = 0; r < rows; r += chunk_rows) {
+        size_t nr = std::min(chunk_rows, rows - r);
+        uint8_t* st = (uint8_t*)c->stage_in.p;
+        if (t.fast)
+            for (size_t i = 0; i < nr; ++i) fp8_permute_row(weight + (r + i) * cols, st + i * cols, cols);
+        else
+            std::memcpy(st, weight + r * cols, nr * cols);
+        WH_TRY(upload(c, t.w + r * cols, st, nr * cols));
+    }
+    WH_TRY(upload(c, t.s, scales, sbytes));
+    return store_tensor_common(c, std::move(t), out);
+}
+
+int wh_store_fp4(wh_ctx* c, const uint8_t* packed, size_t packed_len, const uint8_t* scales,
+                 size_t scales_len, size_t rows, size_t cols, size_t scale_cols, wh_tensor* out) {
+    if (!c || !out || !packed || !scales) return WH_INVALID_ARGUMENT;
+    // validate_fp4_matvec, E/deepseek_v4.rs:434-462 (input/output lengths are
+    // checked per call)
+    if (rows == 0 || cols == 0 || scale_cols == 0) return WH_EMPTY_SHAPE;
+    if (cols % scale_cols != 0) return WH_INVALID_SHAPE;
+    const size_t row_bytes = (cols + 1) / 2;
+    if (packed_len < rows * row_bytes) return WH_PACKED_WEIGHT_TOO_SMALL;
+    if (scales_len < rows * scale_cols) return WH_SCALE_TOO_SMALL;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    Tensor t;
+    t.kind = kFp4;
+    t.rows = rows;
+    t.cols = cols;
+    t.scale_rows = rows;
+    t.scale_cols = scale_cols;
+    t.fast = (cols / scale_cols == 32) && cols % 256 == 0 && cols * 4 <= 160 * 1024;
+    t.bytes = rows * row_bytes + rows * scale_cols;
+    void* wd = nullptr;
+    void* sd = nullptr;
+    WH_TRY(alloc_device(c, rows * row_bytes, &wd));
+    WH_TRY(alloc_device(c, rows * scale_cols, &sd));
+    t.w = (uint8_t*)wd;
+    t.s = sd;
+    const size_t chunk_rows = std::max<size_t>(1, (size_t(64) << 20) / row_bytes);
+    WH_HIP(c->stage_in.ensure(std::min(rows, chunk_rows) * row_bytes));
+    for (size_t r = 0; r < rows; r += chunk_rows) {
+        size_t nr = std::min(chunk_rows, rows - r);
+        uint8_t* st = (uint8_t*)c->stage_in.p;
+        if (t.fast)
+            for (size_t i = 0; i < nr; ++i)
+                fp4_encode_row(packed + (r + i) * row_bytes, st + i * row_bytes, cols);
+        else
+            std::memcpy(st, packed + r * row_bytes, nr * row_bytes);
+        WH_TRY(upload(c, t.w + r * row_bytes, st, nr * row_bytes));
+    }
+    WH_TRY(upload(c, t.s, scales, rows * scale_cols));
+    return store_tensor_common(c, std::move(t), out);
+}
+
+int wh_store_expert(wh_ctx* c, uint32_t layer, uint32_t expert, wh_tensor w1, wh_tensor w3,
+                    wh_tensor w2) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    Tensor *t1 = find_tensor(c, w1), *t3 = find_tensor(c, w3), *t2 = find_tensor(c, w2);
+    if (!t1 || !t3 || !t2) return WH_NOT_RESIDENT;
+    if (t1->kind != kFp4 || t3->kind != kFp4 || t2->kind != kFp4) return WH_INVALID_QUANT_FORMAT;
+    // E/compute.rs:1263-1265
+    if (t1->cols != t3->cols || t1->rows != t3->rows || t2->cols != t1->rows) return WH_INVALID_SHAPE;
+    c->experts[{layer, expert}] = Expert{w1, w3, w2};
+    return WH_OK;
+}
+
+void wh_synth_fp4_host(uint64_t seed, uint64_t stream, uint8_t* packed, size_t packed_len,
+                       uint8_t* scales, size_t scales_len, uint32_t slo, uint32_t shi) {
+    for (size_t i = 0; i < packed_len; ++i) packed[i] = wh_synth_byte(seed, stream, i);
+    uint32_t span = shi - slo + 1;
+    for (size_t i = 0; i < scales_len; ++i)
+        scales[i] = (uint8_t)(slo + wh_synth_byte(seed, stream ^ 0x5ca1e5ull, i) % span);
+}
+
+int wh_store_expert_synthetic(wh_ctx* c, uint32_t layer, uint32_t expert, size_t hidden,
+                              size_t inter, uint64_t seed, uint32_t slo, uint32_t shi) {
+    if (!c || slo > shi || shi > 255) return WH_INVALID_ARGUMENT;
+    if (hidden % 256 || inter % 256 || hidden == 0 || inter == 0) return WH_INVALID_SHAPE;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    wh_tensor ids[3];
+    const size_t shapes[3][2] = {{inter, hidden}, {inter, hidden}, {hidden, inter}};
+    for (int m = 0; m < 3; ++m) {
+        Tensor t;
+        t.kind = kFp4;
+        t.rows = shapes[m][0];
+        t.cols = shapes[m][1];
+        t.scale_rows = t.rows;
+        t.scale_cols = t.cols / 32;
+        t.fast = true;
+        t.bytes = t.rows * t.cols / 2 + t.rows * t.scale_cols;
+        void* wd = nullptr;
+        void* sd = nullptr;
+        WH_TRY(alloc_device(c, t.rows * t.cols / 2, &wd));
+        WH_TRY(alloc_device(c, t.rows * t.scale_cols, &sd));
+        t.w = (uint8_t*)wd;
+        t.s = sd;
+        uint64_t stream = ((uint64_t)layer << 40) ^ ((uint64_t)expert << 8) ^ (uint64_t)m;
+        size_t words = t.rows * (t.cols / 256) * 32;
+        size_t work = std::max(words, t.rows * t.scale_cols);
+        k_synth_fp4<<<(unsigned)((work + 255) / 256), 256, 0, c->stream>>>(
+            t.w, (uint8_t*)t.s, (uint32_t)t.rows, (uint32_t)t.cols, seed, stream, slo, shi);
+        WH_HIP(hipGetLastError());
+        WH_TRY(store_tensor_common(c, std::move(t), &ids[m]));
+    }
+    WH_HIP(hipStreamSynchronize(c->stream));
+    c->experts[{layer, expert}] = Expert{ids[0], ids[1], ids[2]};
+    return WH_OK;
+}
+
+int wh_store_release(wh_ctx* c, wh_tensor t) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    auto it = c->tensors.find(t);
+    if (it == c->tensors.end()) return WH_NOT_RESIDENT;
+    // arena memory is reclaimed at shutdown; the handle stops resolving now
+    c->tensors.erase(it);
+    return WH_OK;
+}
+
+int wh_store_usage(wh_ctx* c, size_t* bytes, size_t* tensors, size_t* experts) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (bytes) *bytes = c->device_bytes;
+    if (tensors) *tensors = c->tensors.size();
+    if (experts) *experts = c->experts.size();
+    return WH_OK;
+}
+
+int wh_tensor_dequant(wh_ctx* c, wh_tensor th, float* out, size_t out_len) {
+    if (!c || !out) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    Tensor* t = find_tensor(c, th);
+    if (!t) return WH_NOT_RESIDENT;
+    if (!t->fast) return WH_UNSUPPORTED;
+    size_t n = t->rows * t->cols;
+    if (out_len < n) return WH_OUTPUT_TOO_SMALL;
+    WH_HIP(c->y_out.ensure(n * sizeof(float), false));
+    float* d = c->y_out.as<float>();
+    if (t->kind == kFp4) {
+        size_t th_n = t->rows * (t->cols / 256) * 8;
+        k_fp4_dequant<<<(unsigned)((th_n + 255) / 256), 256, 0, c->stream>>>(
+            t->w, (const uint8_t*)t->s, (uint32_t)t->rows, (uint32_t)t->cols, d);
+    } else {
+        size_t th_n = t->rows * (t->cols / 128) * 8;
+        if (t->special)
+            k_fp8_dequant<true><<<(unsigned)((th_n + 255) / 256), 256, 0, c->stream>>>(t->w, (uint32_t)t->rows, (uint32_t)t->cols, d);
+        else
+            k_fp8_dequant<false><<<(unsigned)((th_n + 255) / 256), 256, 0, c->stream>>>(t->w, (uint32_t)t->rows, (uint32_t)t->cols, d);
+    }
+    WH_HIP(hipGetLastError());
+    WH_HIP(hipMemcpyAsync(out, d, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    WH_HIP(hipStreamSynchronize(c->stream));
+    return WH_OK;
+}
+
+int wh_fp8_gemv_multi(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end,
+                      const float* inputs, size_t n, size_t input_stride, float* outputs,
+                      size_t output_stride, size_t* values_out) {
+    if (!c || !inputs || !outputs) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    Tensor* t = find_tensor(c, w);
+    if (!t) return WH_NOT_RESIDENT;
+    if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
+    if (n == 0) return WH_INVALID_SHAPE;
+    // E/compute.rs:6400-6430
+    if (row_start >= row_end || row_end > t->rows) return WH_INVALID_SHAPE;
+    if (input_stride < t->cols) return WH_INPUT_TOO_SMALL;
+    const size_t rows = row_end - row_start;
+    if (output_stride < rows) return WH_OUTPUT_TOO_SMALL;
+    WH_HIP(c->x_in.ensure(n * t->cols * sizeof(float), false));
+    WH_HIP(c->y_out.ensure(n * rows * sizeof(float), false));
+    WH_HIP(c->stage_in.ensure(n * t->cols * sizeof(float)));
+    WH_HIP(c->stage_out.ensure(n * rows * sizeof(float)));
+    float* si = (float*)c->stage_in.p;
+    for (size_t b = 0; b < n; ++b) std::memcpy(si + b * t->cols, inputs + b * input_stride, t->cols * sizeof(float));
+    WH_HIP(hipMemcpyAsync(c->x_in.p, si, n * t->cols * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    WH_TRY(launch_fp8(c, *t, row_start, row_end, c->x_in.as<float>(), c->y_out.as<float>(), n, t->cols, rows));
+    WH_HIP(hipMemcpyAsync(c->stage_out.p, c->y_out.p, n * rows * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    int st = read_status(c);
+    if (st != WH_OK) return st;
+    float* so = (float*)c->stage_out.p;
+    for (size_t b = 0; b < n; ++b) std::memcpy(outputs + b * output_stride, so + b * rows, rows * sizeof(float));
+    if (values_out) *values_out = rows * t->cols;
+    return WH_OK;
+}
+
+int wh_fp8_gemv(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end, const float* input,
+                size_t input_len, float* output, size_t output_len, size_t* values_out) {
+    if (!c || !input || !output) return WH_INVALID_ARGUMENT;
+    {
+        std::lock_guard<std::mutex> lk(c->mu);
+        Tensor* t = find_tensor(c, w);
+        if (!t) return WH_NOT_RESIDENT;
+        if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
+        if (row_start >= row_end || row_end > t->rows) return WH_INVALID_SHAPE;
+        if (input_len < t->cols) return WH_INPUT_TOO_SMALL;
+        if (output_len < row_end - row_start) return WH_OUTPUT_TOO_SMALL;
+    }
+    return wh_fp8_gemv_multi(c, w, row_start, row_end, input, 1, input_len, output, output_len,
+                             values_out);
+}
+
+int wh_fp8_gemv_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end,
+                      const float* x_dev, float* y_dev) {
+    if (!c || !x_dev || !y_dev) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    Tensor* t = find_tensor(c, w);
+    if (!t) return WH_NOT_RESIDENT;
+    if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
+    if (row_start >= row_end || row_end > t->rows) return WH_INVALID_SHAPE;
+    return launch_fp8(c, *t, row_start, row_end, x_dev, y_dev, 1, t->cols, row_end - row_start);
+}
+
+int wh_fp4_matvec(wh_ctx* c, wh_tensor w, const float* input, size_t input_len, float* output,
+                  size_t output_len) {
+    if (!c || !input || !output) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    Tensor* t = find_tensor(c, w);
+    if (!t) return WH_NOT_RESIDENT;
+    if (t->kind != kFp4) return WH_INVALID_QUANT_FORMAT;
+    if (input_len < t->cols) return WH_INPUT_TOO_SMALL;
+    if (output_len < t->rows) return WH_OUTPUT_TOO_SMALL;
+    WH_HIP(c->x_in.ensure(t->cols * sizeof(float), false));
+    WH_HIP(c->y_out.ensure(t->rows * sizeof(float), false));
+    WH_HIP(c->stage_out.ensure(t->rows * sizeof(float)));
+    WH_HIP(hipMemcpyAsync(c->x_in.p, input, t->cols * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    WH_TRY(launch_fp4(c, *t, c->x_in.as<float>(), c->y_out.as<float>()));
+    WH_HIP(hipMemcpyAsync(c->stage_out.p, c->y_out.p, t->rows * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    int st = read_status(c);
+    if (st != WH_OK) return st;
+    std::memcpy(output, c->stage_out.p, t->rows * sizeof(float));
+    return WH_OK;
+}
+
+int wh_act_quant_dequant(wh_ctx* c, float* values, size_t n, size_t block) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    if (block == 0 || n == 0) return WH_OK;  // E/compute.rs:2505-2507
+    if (!values) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    WH_HIP(c->x_in.ensure(n * sizeof(float), false));
+    WH_HIP(hipMemcpyAsync(c->x_in.p, values, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    k_act_quant_inplace<<<(unsigned)((n + block - 1) / block), 256, 0, c->stream>>>(
+        c->x_in.as<float>(), (uint32_t)n, (uint32_t)block);
+    WH_HIP(hipGetLastError());
+    WH_HIP(hipMemcpyAsync(values, c->x_in.p, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    WH_HIP(hipStreamSynchronize(c->stream));
+    return WH_OK;
+}
+
+static int routed_common(wh_ctx* c, const wh_expert_route* routes, size_t n, ExpertView* ev,
+                         float* wts) {
+    if (n > WH_MAX_EXPERTS) return WH_UNSUPPORTED;
+    for (size_t i = 0; i < n; ++i) {
+        WH_TRY(resolve_expert(c, routes[i].layer_id, routes[i].expert_id, &ev[i]));
+        wts[i] = routes[i].route_weight;
+    }
+    return WH_OK;
+}
+
+int wh_routed_experts(wh_ctx* c, const wh_expert_route* routes, size_t n, float* hidden,
+                      size_t hidden_len) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    if (n == 0) return WH_OK;  // E/compute.rs:1956-1958
+    if (!routes || !hidden) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    ExpertView ev[WH_MAX_EXPERTS];
+    float wts[WH_MAX_EXPERTS];
+    WH_TRY(routed_common(c, routes, n, ev, wts));
+    const size_t hsz = ev[0].w1->cols, osz = ev[0].w2->rows;
+    if (hidden_len < hsz) return WH_INVALID_SHAPE;  // "DeepSeek FP4 expert input dim"
+    if (osz > hidden_len) return WH_OUTPUT_TOO_SMALL;
+    WH_HIP(c->x_in.ensure(hsz * sizeof(float), false));
+    WH_HIP(c->y_out.ensure(osz * sizeof(float), false));
+    WH_HIP(c->stage_out.ensure(osz * sizeof(float)));
+    WH_HIP(hipMemcpyAsync(c->x_in.p, hidden, hsz * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    WH_TRY(moe_forward(c, ev, wts, n, c->x_in.p, 0, 1, c->y_out.as<float>()));
+    WH_HIP(hipMemcpyAsync(c->stage_out.p, c->y_out.p, osz * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    int st = read_status(c);
+    if (st != WH_OK) return st;
+    std::memcpy(hidden, c->stage_out.p, osz * sizeof(float));
+    return WH_OK;
+}
+
+int wh_routed_experts_async(wh_ctx* c, const wh_expert_route* routes, size_t n, const void* x_dev,
+                            int x_bf16, size_t n_tokens, float* out_dev) {
+    if (!c || !routes || !x_dev || !out_dev || n == 0 || n_tokens == 0) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    ExpertView ev[WH_MAX_EXPERTS];
+    float wts[WH_MAX_EXPERTS];
+    WH_TRY(routed_common(c, routes, n, ev, wts));
+    return moe_forward(c, ev, wts, n, x_dev, x_bf16, n_tokens, out_dev);
+}
+
+int wh_fp4_expert_forward(wh_ctx* c, uint32_t layer, uint32_t expert, const float* input,
+                          size_t input_len, float* output, size_t output_len, size_t scratch_len) {
+    if (!c || !input || !output) return WH_INVALID_ARGUMENT;
+    ExpertView ev;
+    {
+        std::lock_guard<std::mutex> lk(c->mu);
+        WH_TRY(resolve_expert(c, layer, expert, &ev));
+    }
+    // E/deepseek_v4.rs:567-580
+    if (ev.w1->cols != input_len || ev.w3->cols != input_len || ev.w1->rows != ev.w3->rows ||
+        ev.w2->cols != ev.w1->rows)
+        return WH_INVALID_SHAPE;
+    if (output_len < ev.w2->rows) return WH_OUTPUT_TOO_SMALL;
+    if (scratch_len < ev.w1->rows * 2) return WH_SCRATCH_TOO_SMALL;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    const size_t hsz = ev.w1->cols, osz = ev.w2->rows;
+    WH_HIP(c->x_in.ensure(hsz * sizeof(float), false));
+    WH_HIP(c->y_out.ensure(osz * sizeof(float), false));
+    WH_HIP(c->stage_out.ensure(osz * sizeof(float)));
+    WH_HIP(hipMemcpyAsync(c->x_in.p, input, hsz * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    float one = 1.0f;
+    WH_TRY(moe_forward(c, &ev, &one, 1, c->x_in.p, 0, 1, c->y_out.as<float>()));
+    WH_HIP(hipMemcpyAsync(c->stage_out.p, c->y_out.p, osz * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    int st = read_status(c);
+    if (st != WH_OK) return st;
+    std::memcpy(output, c->stage_out.p, osz * sizeof(float));
+    return WH_OK;
+}
+
+int wh_device_alloc(wh_ctx* c, size_t bytes, void** out) {
+    if (!c || !out) return WH_INVALID_ARGUMENT;
+    *out = nullptr;
+    if (bytes == 0) return WH_OK;
+    WH_HIP(hipSetDevice(c->device));
+    WH_HIP(hipMalloc(out, bytes));
+    return WH_OK;
+}
+
+int wh_device_free(wh_ctx* c, void* p) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    if (!p) return WH_OK;
+    WH_HIP(hipSetDevice(c->device));
+    WH_HIP(hipStreamSynchronize(c->stream));
+    WH_HIP(hipFree(p));
+    return WH_OK;
+}
+
+int wh_memcpy(wh_ctx* c, void* dst, const void* src, size_t bytes, int kind) {
+    if (!c || (bytes && (!dst || !src)) || kind < 0 || kind > 2) return WH_INVALID_ARGUMENT;
+    if (bytes == 0) return WH_OK;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    const hipMemcpyKind kinds[3] = {hipMemcpyHostToDevice, hipMemcpyDeviceToHost, hipMemcpyDeviceToDevice};
+    WH_HIP(hipMemcpyAsync(dst, src, bytes, kinds[kind], c->stream));
+    WH_HIP(hipStreamSynchronize(c->stream));
+    return WH_OK;
+}
+
+int wh_profile_enable(wh_ctx* c, size_t max_steps) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    WH_HIP(hipStreamSynchronize(c->stream));
+    for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
+    c->prof_ev.clear();
+    c->prof_steps = 0;
+    c->prof_cap = max_steps;
+    c->prof = max_steps > 0;
+    for (size_t i = 0; i < 4 * max_steps; ++i) {
+        hipEvent_t e;
+        WH_HIP(hipEventCreate(&e));
+        c->prof_ev.push_back(e);
+    }
+    return WH_OK;
+}
+
+int wh_profile_read(wh_ctx* c, double* avg_us, size_t* steps) {
+    if (!c || !avg_us) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipStreamSynchronize(c->stream));
+    double acc[3] = {0, 0, 0};
+    for (size_t s = 0; s < c->prof_steps; ++s) {
+        for (int k = 0; k < 3; ++k) {
+            float ms = 0.f;
+            WH_HIP(hipEventElapsedTime(&ms, c->prof_ev[4 * s + k], c->prof_ev[4 * s + k + 1]));
+            acc[k] += ms * 1000.0;
+        }
+    }
+    for (int k = 0; k < 3; ++k) avg_us[k] = c->prof_steps ? acc[k] / (double)c->prof_steps : 0.0;
+    if (steps) *steps = c->prof_steps;
+    return WH_OK;
+}
+
+int wh_debug_eval(wh_ctx* c, int fn, const float* in, float* out, size_t n) {
+    if (!c || !in || !out || fn < 0 || fn > 2) return WH_INVALID_ARGUMENT;
+    if (n == 0) return WH_OK;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    WH_HIP(c->x_in.ensure(n * sizeof(float), false));
+    WH_HIP(c->y_out.ensure(n * sizeof(float), false));
+    WH_HIP(hipMemcpyAsync(c->x_in.p, in, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    k_debug_eval<<<(unsigned)((n + 255) / 256), 256, 0, c->stream>>>(fn, c->x_in.as<float>(), c->y_out.as<float>(), (uint32_t)n);
+    WH_HIP(hipGetLastError());
+    WH_HIP(hipMemcpyAsync(out, c->y_out.p, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    WH_HIP(hipStreamSynchronize(c->stream));
+    return WH_OK;
+}
+
+}  // extern "C"
