@@ -75,6 +75,8 @@ const char* wh_status_string(int status);
 int wh_synchronize(wh_ctx* ctx);
 /* The context's hipStream_t, for callers that interleave their own work. */
 void* wh_stream(wh_ctx* ctx);
+/* Text of the last HIP runtime failure on this thread (empty if none). */
+const char* wh_last_error(void);
 /* Library build description (architecture, libm table sizes). */
 const char* wh_build_info(void);
 

@@ -63,7 +63,7 @@ EXPORTED = (
     "wh_fp8_gemv", "wh_fp8_gemv_multi", "wh_fp4_matvec", "wh_fp4_expert_forward",
     "wh_act_quant_dequant", "wh_routed_experts", "wh_routed_experts_async", "wh_fp8_gemv_async",
     "wh_stream_status", "wh_debug_eval", "wh_profile_enable", "wh_profile_read",
-    "wh_device_alloc", "wh_device_free", "wh_memcpy",
+    "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
 )
 
 
@@ -104,6 +104,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_synchronize": (c.c_int, [vp]),
         "wh_stream": (vp, [vp]),
         "wh_build_info": (c.c_char_p, []),
+        "wh_last_error": (c.c_char_p, []),
         "wh_store_fp8": (c.c_int, [vp, u8p, sz, sz, sz, vp, sz, c.c_int, sz, sz, c.POINTER(c.c_uint64)]),
         "wh_store_fp4": (c.c_int, [vp, u8p, sz, u8p, sz, sz, sz, sz, c.POINTER(c.c_uint64)]),
         "wh_store_expert": (c.c_int, [vp, c.c_uint32, c.c_uint32, c.c_uint64, c.c_uint64, c.c_uint64]),
@@ -152,6 +153,8 @@ def _p(a: np.ndarray, ct):
 
 def _check(code: int, where: str = ""):
     if code != 0:
+        if code in (11, 12) and _lib is not None:
+            where = f"{where}: {_lib.wh_last_error().decode(errors='replace')}"
         raise DeepSeekV4KernelError(code, where)
 
 

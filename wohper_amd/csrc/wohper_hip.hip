@@ -141,16 +141,22 @@ struct wh_ctx {
 
 namespace {
 
-int hip_status(hipError_t e) {
+thread_local char g_last_error[256] = "";
+
+int hip_status_at(hipError_t e, const char* what, int line) {
     if (e == hipSuccess) return WH_OK;
+    std::snprintf(g_last_error, sizeof g_last_error, "%s (%d) at wohper_hip.hip:%d: %s",
+                  hipGetErrorName(e), (int)e, line, what);
     if (e == hipErrorOutOfMemory) return WH_OUT_OF_MEMORY;
     return WH_HIP_ERROR;
 }
 
-#define WH_HIP(expr)                                  \
-    do {                                              \
-        hipError_t _e = (expr);                       \
-        if (_e != hipSuccess) return hip_status(_e);  \
+#define hip_status(e) hip_status_at((e), "", __LINE__)
+
+#define WH_HIP(expr)                                                   \
+    do {                                                               \
+        hipError_t _e = (expr);                                        \
+        if (_e != hipSuccess) return hip_status_at(_e, #expr, __LINE__); \
     } while (0)
 
 #define WH_TRY(expr)               \
@@ -202,35 +208,44 @@ void fp8_permute_row(const uint8_t* src, uint8_t* dst, size_t cols) {
     }
 }
 
-// FP4 resident encoding of one row (see wh_fp4_decode8).
-void fp4_encode_row(const uint8_t* src, uint8_t* dst, size_t cols) {
+// FP4 resident encoding of one row (layout described in kernels.h): the
+// weights of each 4-group chunk re-ordered per quad thread, and the row's
+// UE8M0 bytes grouped by owning quad thread.
+void fp4_encode_row(const uint8_t* src, const uint8_t* ssrc, uint8_t* dst, uint8_t* sdst, size_t cols) {
     auto nib = [src](size_t col) -> uint32_t {
         uint8_t b = src[col >> 1];
         return (col & 1) ? (b >> 4) : (b & 15);
     };
-    for (size_t sp = 0; sp < cols / 256; ++sp) {
-        for (uint32_t l = 0; l < 8; ++l) {
-            for (uint32_t d = 0; d < 4; ++d) {
-                size_t ga = sp * 8 + d * 2, gb = ga + 1;
-                uint32_t word = 0;
+    const size_t chunks = cols / 128, G = cols / 32;
+    for (size_t j = 0; j < chunks; ++j) {
+        for (uint32_t t = 0; t < 4; ++t) {
+            for (uint32_t i = 0; i < 4; ++i) {
+                size_t g = 4 * j + i;
+                uint32_t a[4], b[4];
                 for (uint32_t k = 0; k < 4; ++k) {
-                    uint32_t a = nib(32 * ga + l + 8 * k);
-                    uint32_t aprev = nib(32 * ga + l + 8 * ((k + 3) & 3));
-                    uint32_t b = nib(32 * gb + l + 8 * k);
-                    uint32_t byte = (a & 7) | ((aprev >> 3) << 3) | ((b & 7) << 4) | ((b >> 3) << 7);
-                    word |= byte << (8 * k);
+                    a[k] = nib(32 * g + t + 8 * k);
+                    b[k] = nib(32 * g + t + 4 + 8 * k);
                 }
-                std::memcpy(dst + sp * 128 + l * 16 + d * 4, &word, 4);
+                uint32_t word = wh_fp4_encode_word(a, b);
+                std::memcpy(dst + (4 * j + t) * 16 + 4 * i, &word, 4);
             }
         }
     }
+    for (size_t g = 0; g < G; ++g) sdst[(g & 3) * (G / 4) + (g >> 2)] = ssrc[g];
 }
 
-hipError_t kernel_setup_once() {
+// Dynamic LDS a workgroup may use: the device's per-block limit (160 KB on
+// gfx950) when the runtime accepts raising the kernels' attribute, else 64 KB.
+size_t g_max_lds = 64 * 1024;
+
+hipError_t kernel_setup_once(int device) {
     static std::once_flag once;
     static hipError_t err = hipSuccess;
-    std::call_once(once, [] {
-        const int lds = 160 * 1024;
+    std::call_once(once, [device] {
+        int lds = 64 * 1024;
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > lds)
+            lds = v;
         hipError_t e = hipSuccess;
         auto set = [&](const void* f) {
             hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -240,10 +255,19 @@ hipError_t kernel_setup_once() {
         set((const void*)k_fp8_gemv<false, true>);
         set((const void*)k_fp8_gemv<true, false>);
         set((const void*)k_fp8_gemv<true, true>);
-        set((const void*)k_fp4_matvec);
-        set((const void*)k_moe_gateup);
-        set((const void*)k_moe_down);
-        err = e;
+        set((const void*)k_fp4_matvec<0>);
+        set((const void*)k_fp4_matvec<16>);
+        set((const void*)k_fp4_matvec<32>);
+        set((const void*)k_moe_gateup<0>);
+        set((const void*)k_moe_gateup<32>);
+        set((const void*)k_moe_down<0>);
+        set((const void*)k_moe_down<16>);
+        if (e == hipSuccess) {
+            g_max_lds = (size_t)lds;
+        } else {
+            (void)hipGetLastError();  // keep the 64 KB default
+        }
+        err = hipSuccess;
     });
     return err;
 }
@@ -295,7 +319,11 @@ int launch_fp4(wh_ctx* c, const Tensor& t, const float* x, float* y) {
     a.rows = (uint32_t)t.rows;
     a.cols = (uint32_t)t.cols;
     if (t.fast) {
-        k_fp4_matvec<<<(unsigned)((t.rows + 31) / 32), 256, t.cols * sizeof(float), c->stream>>>(a);
+        dim3 grid((unsigned)((t.rows + 63) / 64));
+        size_t lds = t.cols * sizeof(float);
+        if (t.cols == 4096) k_fp4_matvec<32><<<grid, 256, lds, c->stream>>>(a);
+        else if (t.cols == 2048) k_fp4_matvec<16><<<grid, 256, lds, c->stream>>>(a);
+        else k_fp4_matvec<0><<<grid, 256, lds, c->stream>>>(a);
     } else {
         k_fp4_matvec_generic<<<(unsigned)((t.rows + 63) / 64), 64, 0, c->stream>>>(a, (uint32_t)t.scale_cols);
     }
@@ -350,8 +378,8 @@ int resolve_expert(wh_ctx* c, uint32_t layer, uint32_t expert, ExpertView* v) {
 }
 
 bool expert_fast(const ExpertView& v) {
-    return v.w1->fast && v.w3->fast && v.w2->fast && v.w1->cols % 256 == 0 &&
-           v.w1->rows % 256 == 0 && v.w1->rows * 4 <= 160 * 1024 && v.w1->cols * 4 <= 160 * 1024;
+    return v.w1->fast && v.w3->fast && v.w2->fast && v.w1->cols % 512 == 0 &&
+           v.w1->rows % 512 == 0 && v.w1->rows * 4 <= g_max_lds && v.w1->cols * 4 <= g_max_lds;
 }
 
 // Routed experts for n_tokens rows of x (all with the same route list).
@@ -407,11 +435,13 @@ int moe_forward(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n,
                                                            c->xq_codes.as<uint8_t>(),
                                                            c->xq_scales.as<float>(), c->status);
         if (ev) WH_HIP(hipEventRecord(ev[1], c->stream));
-        k_moe_gateup<<<dim3((unsigned)(inter / 16), (unsigned)n, (unsigned)n_tokens), 128,
-                       hidden * sizeof(float), c->stream>>>(a);
+        dim3 ggrid((unsigned)(inter / 16), (unsigned)n, (unsigned)n_tokens);
+        if (hidden == 4096) k_moe_gateup<32><<<ggrid, 128, hidden * sizeof(float), c->stream>>>(a);
+        else k_moe_gateup<0><<<ggrid, 128, hidden * sizeof(float), c->stream>>>(a);
         if (ev) WH_HIP(hipEventRecord(ev[2], c->stream));
-        k_moe_down<<<dim3((unsigned)(hidden / 32), (unsigned)n, (unsigned)n_tokens), 256,
-                     inter * sizeof(float), c->stream>>>(a);
+        dim3 dgrid((unsigned)(hidden / 32), (unsigned)n, (unsigned)n_tokens);
+        if (inter == 2048) k_moe_down<16><<<dgrid, 128, inter * sizeof(float), c->stream>>>(a);
+        else k_moe_down<0><<<dgrid, 128, inter * sizeof(float), c->stream>>>(a);
         if (ev) WH_HIP(hipEventRecord(ev[3], c->stream));
         WH_HIP(hipGetLastError());
         return WH_OK;
@@ -459,36 +489,37 @@ __host__ __device__ inline uint8_t wh_synth_byte(uint64_t seed, uint64_t stream,
 }
 
 // Device synthetic FP4 tensor straight into the resident layout: each
-// thread builds one lane dword from the generated original nibbles.
+// thread builds one weight dword (or one scale byte) from the generated
+// original bytes.
 __global__ void k_synth_fp4(uint8_t* w, uint8_t* s, uint32_t rows, uint32_t cols, uint64_t seed,
                             uint64_t stream, uint32_t slo, uint32_t shi) {
-    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const uint32_t spans = cols / 256;
-    const size_t words = (size_t)rows * spans * 32;
-    if (t < words) {
-        uint32_t d = t & 3, l = (t >> 2) & 7;
-        size_t rs = t >> 5;
-        uint32_t sp = rs % spans;
-        size_t row = rs / spans;
-        size_t rowbase = row * (cols / 2);
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t chunks = cols / 128, G = cols / 32;
+    const size_t words = (size_t)rows * chunks * 16;
+    if (id < words) {
+        const uint32_t i = id & 3, t = (id >> 2) & 3;
+        const size_t rj = id >> 4;
+        const uint32_t j = rj % chunks;
+        const size_t row = rj / chunks;
+        const size_t rowbase = row * (cols / 2);
         auto nib = [&](size_t col) -> uint32_t {
             uint8_t b = wh_synth_byte(seed, stream, rowbase + (col >> 1));
             return (col & 1) ? (b >> 4) : (b & 15);
         };
-        size_t ga = (size_t)sp * 8 + d * 2, gb = ga + 1;
-        uint32_t word = 0;
+        const size_t g = (size_t)4 * j + i;
+        uint32_t a[4], b[4];
         for (uint32_t k = 0; k < 4; ++k) {
-            uint32_t a = nib(32 * ga + l + 8 * k);
-            uint32_t ap = nib(32 * ga + l + 8 * ((k + 3) & 3));
-            uint32_t b = nib(32 * gb + l + 8 * k);
-            word |= ((a & 7) | ((ap >> 3) << 3) | ((b & 7) << 4) | ((b >> 3) << 7)) << (8 * k);
+            a[k] = nib(32 * g + t + 8 * k);
+            b[k] = nib(32 * g + t + 4 + 8 * k);
         }
-        ((uint32_t*)(w + rowbase + (size_t)sp * 128 + l * 16))[d] = word;
+        ((uint32_t*)(w + rowbase + ((size_t)4 * j + t) * 16))[i] = wh_fp4_encode_word(a, b);
     }
-    const size_t nscale = (size_t)rows * (cols / 32);
-    if (t < nscale) {
+    const size_t nscale = (size_t)rows * G;
+    if (id < nscale) {
+        const size_t row = id / G;
+        const uint32_t g = id % G;
         uint32_t span = shi - slo + 1;
-        s[t] = (uint8_t)(slo + wh_synth_byte(seed, stream ^ 0x5ca1e5ull, t) % span);
+        s[row * G + (g & 3) * (G / 4) + (g >> 2)] = (uint8_t)(slo + wh_synth_byte(seed, stream ^ 0x5ca1e5ull, id) % span);
     }
 }
 
@@ -526,10 +557,12 @@ const char* wh_status_string(int s) {
     }
 }
 
+const char* wh_last_error(void) { return g_last_error; }
+
 const char* wh_build_info(void) {
     static char buf[160];
-    std::snprintf(buf, sizeof buf, "wohper_hip gfx950; expf flip table %u entries; max experts %d",
-                  (unsigned)WH_EXPF_FLIP_COUNT, WH_MAX_EXPERTS);
+    std::snprintf(buf, sizeof buf, "wohper_hip gfx950; expf flip table %u entries; max experts %d; lds %zu",
+                  (unsigned)WH_EXPF_FLIP_COUNT, WH_MAX_EXPERTS, g_max_lds);
     return buf;
 }
 
@@ -540,7 +573,7 @@ int wh_init(int device, wh_ctx** out) {
     WH_HIP(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) return WH_INVALID_ARGUMENT;
     WH_HIP(hipSetDevice(device));
-    WH_HIP(kernel_setup_once());
+    WH_HIP(kernel_setup_once(device));
     wh_ctx* c = new wh_ctx();
     c->device = device;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
@@ -605,7 +638,7 @@ int wh_store_fp8(wh_ctx* c, const uint8_t* weight, size_t weight_len, size_t row
     t.scale_rows = scale_rows;
     t.scale_cols = scale_cols;
     t.scale_fmt = scale_format;
-    t.fast = (cols / scale_cols == 128) && cols * 4 <= 160 * 1024;
+    t.fast = (cols / scale_cols == 128) && cols * 4 <= g_max_lds;
     for (size_t i = 0; i < rows * cols && !t.special; ++i) t.special = (weight[i] & 0x7f) == 0x7f;
     t.bytes = rows * cols + sbytes;
     void* wd = nullptr;
@@ -647,7 +680,7 @@ int wh_store_fp4(wh_ctx* c, const uint8_t* packed, size_t packed_len, const uint
     t.cols = cols;
     t.scale_rows = rows;
     t.scale_cols = scale_cols;
-    t.fast = (cols / scale_cols == 32) && cols % 256 == 0 && cols * 4 <= 160 * 1024;
+    t.fast = (cols / scale_cols == 32) && cols % 512 == 0 && cols * 4 <= g_max_lds;
     t.bytes = rows * row_bytes + rows * scale_cols;
     void* wd = nullptr;
     void* sd = nullptr;
@@ -656,18 +689,23 @@ int wh_store_fp4(wh_ctx* c, const uint8_t* packed, size_t packed_len, const uint
     t.w = (uint8_t*)wd;
     t.s = sd;
     const size_t chunk_rows = std::max<size_t>(1, (size_t(64) << 20) / row_bytes);
-    WH_HIP(c->stage_in.ensure(std::min(rows, chunk_rows) * row_bytes));
+    const size_t nr0 = std::min(rows, chunk_rows);
+    WH_HIP(c->stage_in.ensure(nr0 * (row_bytes + scale_cols)));
     for (size_t r = 0; r < rows; r += chunk_rows) {
         size_t nr = std::min(chunk_rows, rows - r);
         uint8_t* st = (uint8_t*)c->stage_in.p;
-        if (t.fast)
+        uint8_t* ss = st + nr0 * row_bytes;
+        if (t.fast) {
             for (size_t i = 0; i < nr; ++i)
-                fp4_encode_row(packed + (r + i) * row_bytes, st + i * row_bytes, cols);
-        else
+                fp4_encode_row(packed + (r + i) * row_bytes, scales + (r + i) * scale_cols, st + i * row_bytes,
+                               ss + i * scale_cols, cols);
+        } else {
             std::memcpy(st, packed + r * row_bytes, nr * row_bytes);
+            std::memcpy(ss, scales + r * scale_cols, nr * scale_cols);
+        }
         WH_TRY(upload(c, t.w + r * row_bytes, st, nr * row_bytes));
+        WH_TRY(upload(c, (uint8_t*)t.s + r * scale_cols, ss, nr * scale_cols));
     }
-    WH_TRY(upload(c, t.s, scales, rows * scale_cols));
     return store_tensor_common(c, std::move(t), out);
 }
 
@@ -695,7 +733,7 @@ void wh_synth_fp4_host(uint64_t seed, uint64_t stream, uint8_t* packed, size_t p
 int wh_store_expert_synthetic(wh_ctx* c, uint32_t layer, uint32_t expert, size_t hidden,
                               size_t inter, uint64_t seed, uint32_t slo, uint32_t shi) {
     if (!c || slo > shi || shi > 255) return WH_INVALID_ARGUMENT;
-    if (hidden % 256 || inter % 256 || hidden == 0 || inter == 0) return WH_INVALID_SHAPE;
+    if (hidden % 512 || inter % 512 || hidden == 0 || inter == 0) return WH_INVALID_SHAPE;
     std::lock_guard<std::mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     wh_tensor ids[3];
@@ -716,7 +754,7 @@ int wh_store_expert_synthetic(wh_ctx* c, uint32_t layer, uint32_t expert, size_t
         t.w = (uint8_t*)wd;
         t.s = sd;
         uint64_t stream = ((uint64_t)layer << 40) ^ ((uint64_t)expert << 8) ^ (uint64_t)m;
-        size_t words = t.rows * (t.cols / 256) * 32;
+        size_t words = t.rows * (t.cols / 128) * 16;
         size_t work = std::max(words, t.rows * t.scale_cols);
         k_synth_fp4<<<(unsigned)((work + 255) / 256), 256, 0, c->stream>>>(
             t.w, (uint8_t*)t.s, (uint32_t)t.rows, (uint32_t)t.cols, seed, stream, slo, shi);
@@ -759,7 +797,7 @@ int wh_tensor_dequant(wh_ctx* c, wh_tensor th, float* out, size_t out_len) {
     WH_HIP(c->y_out.ensure(n * sizeof(float), false));
     float* d = c->y_out.as<float>();
     if (t->kind == kFp4) {
-        size_t th_n = t->rows * (t->cols / 256) * 8;
+        size_t th_n = t->rows * (t->cols / 128) * 4;
         k_fp4_dequant<<<(unsigned)((th_n + 255) / 256), 256, 0, c->stream>>>(
             t->w, (const uint8_t*)t->s, (uint32_t)t->rows, (uint32_t)t->cols, d);
     } else {
