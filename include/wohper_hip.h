@@ -189,7 +189,8 @@ int wh_profile_read(wh_ctx* ctx, double* avg_us, size_t* steps);
 /* Test support, no counterpart in the reference: evaluates the device libm
  * emulation on n values.  fn 0: silu(x) = x / (1 + expf(-x)) for x <= 10;
  * fn 1: expf(x) for x >= -10; fn 2: the act-quant block scale
- * exp2f(ceilf(log2f(max(x, 1e-4) / 448))) for finite x >= 0. */
+ * exp2f(ceilf(log2f(max(x, 1e-4) / 448))) for finite x >= 0; fn 3: a plain
+ * device copy out = in (n a multiple of 4) that calibrates HBM byte counters. */
 int wh_debug_eval(wh_ctx* ctx, int fn, const float* in, float* out, size_t n);
 
 #ifdef __cplusplus

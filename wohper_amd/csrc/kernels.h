@@ -30,9 +30,9 @@ __device__ __forceinline__ uint32_t wh_fp8_lds_index(uint32_t col) {
     return ((g * 8 + l) << 4) + i;
 }
 
-// FP4 resident layout: per row, per 256-col span (8 groups), lane l owns 16
-// bytes = 4 dwords, dword d = groups 2d, 2d+1 of the span (see wh_fp4_decode8).
-// x staged in LDS as xs[(g*8 + l)*4 + k] = x[32g + l + 8k].
+// FP4 matvec input order in LDS (the weight layout is described with the FP4
+// kernels below): xs[(g*8 + l)*4 + k] = x[32g + l + 8k], so AVX lane l's four
+// columns of group g are one float4.
 __device__ __forceinline__ uint32_t wh_fp4_lds_index(uint32_t col) {
     uint32_t g = col >> 5, w = col & 31, k = w >> 3, l = w & 7;
     return ((g * 8 + l) << 2) + k;
@@ -861,4 +861,10 @@ __global__ void k_debug_eval(int fn, const float* __restrict__ in, float* __rest
     else if (fn == 1) r = wh_expf_glibc(x, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
     else r = wh_pow2f(wh_aq_scale_exp(x, kLog2Thr));
     out[i] = r;
+}
+
+// Plain streaming copy (fn 3 of the debug entry): the known-size kernel that
+// calibrates the HBM byte counters against the hot kernels' algorithmic bytes.
+__global__ void __launch_bounds__(256) k_copy_f32x4(const float4* __restrict__ in, float4* __restrict__ out, uint32_t n4) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) out[i] = in[i];
 }

@@ -1050,14 +1050,19 @@ int wh_profile_read(wh_ctx* c, double* avg_us, size_t* steps) {
 }
 
 int wh_debug_eval(wh_ctx* c, int fn, const float* in, float* out, size_t n) {
-    if (!c || !in || !out || fn < 0 || fn > 2) return WH_INVALID_ARGUMENT;
+    if (!c || !in || !out || fn < 0 || fn > 3) return WH_INVALID_ARGUMENT;
+    if (fn == 3 && n % 4) return WH_INVALID_ARGUMENT;
     if (n == 0) return WH_OK;
     std::lock_guard<std::mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     WH_HIP(c->x_in.ensure(n * sizeof(float), false));
     WH_HIP(c->y_out.ensure(n * sizeof(float), false));
     WH_HIP(hipMemcpyAsync(c->x_in.p, in, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
-    k_debug_eval<<<(unsigned)((n + 255) / 256), 256, 0, c->stream>>>(fn, c->x_in.as<float>(), c->y_out.as<float>(), (uint32_t)n);
+    if (fn == 3)
+        k_copy_f32x4<<<(unsigned)std::min<size_t>((n / 4 + 255) / 256, 8192), 256, 0, c->stream>>>(
+            reinterpret_cast<const float4*>(c->x_in.p), reinterpret_cast<float4*>(c->y_out.p), (uint32_t)(n / 4));
+    else
+        k_debug_eval<<<(unsigned)((n + 255) / 256), 256, 0, c->stream>>>(fn, c->x_in.as<float>(), c->y_out.as<float>(), (uint32_t)n);
     WH_HIP(hipGetLastError());
     WH_HIP(hipMemcpyAsync(out, c->y_out.p, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     WH_HIP(hipStreamSynchronize(c->stream));
