@@ -177,14 +177,13 @@ int wh_device_alloc(wh_ctx* ctx, size_t bytes, void** out);
 int wh_device_free(wh_ctx* ctx, void* ptr);
 int wh_memcpy(wh_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
 
-/* Per-kernel timing of the routed-expert pipeline, the device counterpart
- * of the reference's ZC_PROF pass timers (E/server/generation.rs:2344-2351):
- * after wh_profile_enable(ctx, n), the next n routed calls record HIP events
- * on the context stream around each kernel; wh_profile_read returns the mean
- * microseconds of [act-quant of x, gate/up + SwiGLU, down + routed sum] in
- * avg_us[0..2].  n = 0 disables it. */
-int wh_profile_enable(wh_ctx* ctx, size_t max_steps);
-int wh_profile_read(wh_ctx* ctx, double* avg_us, size_t* steps);
+/* Device timer on the context stream, the device counterpart of the
+ * reference's ZC_PROF pass timers (E/server/generation.rs:2344-2351):
+ * wh_timer_start records a HIP event on the stream; wh_timer_stop records a
+ * second one, waits for it and returns the microseconds between the two -
+ * the device time of everything enqueued in between. */
+int wh_timer_start(wh_ctx* ctx);
+int wh_timer_stop(wh_ctx* ctx, double* elapsed_us);
 
 /* Test support, no counterpart in the reference: evaluates the device libm
  * emulation on n values.  fn 0: silu(x) = x / (1 + expf(-x)) for x <= 10;

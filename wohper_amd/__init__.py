@@ -62,7 +62,7 @@ EXPORTED = (
     "wh_synth_fp4_host", "wh_store_release", "wh_store_usage", "wh_tensor_dequant",
     "wh_fp8_gemv", "wh_fp8_gemv_multi", "wh_fp4_matvec", "wh_fp4_expert_forward",
     "wh_act_quant_dequant", "wh_routed_experts", "wh_routed_experts_async", "wh_fp8_gemv_async",
-    "wh_stream_status", "wh_debug_eval", "wh_profile_enable", "wh_profile_read",
+    "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
 )
 
@@ -127,8 +127,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_device_alloc": (c.c_int, [vp, sz, c.POINTER(vp)]),
         "wh_device_free": (c.c_int, [vp, vp]),
         "wh_memcpy": (c.c_int, [vp, vp, vp, sz, c.c_int]),
-        "wh_profile_enable": (c.c_int, [vp, sz]),
-        "wh_profile_read": (c.c_int, [vp, c.POINTER(c.c_double), c.POINTER(sz)]),
+        "wh_timer_start": (c.c_int, [vp]),
+        "wh_timer_stop": (c.c_int, [vp, c.POINTER(c.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -313,15 +313,15 @@ class Context:
         _check(self.lib.wh_memcpy(self._h, arr.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(ptr), arr.nbytes, 1),
                "memcpy d2h")
 
-    def profile_enable(self, max_steps: int):
-        _check(self.lib.wh_profile_enable(self._h, max_steps), "profile_enable")
+    def timer_start(self):
+        """Records the start event on the library stream."""
+        _check(self.lib.wh_timer_start(self._h), "timer_start")
 
-    def profile_read(self):
-        """Mean microseconds of (act-quant, gate/up, down) over the recorded steps."""
-        avg = (ctypes.c_double * 3)()
-        n = ctypes.c_size_t()
-        _check(self.lib.wh_profile_read(self._h, avg, ctypes.byref(n)), "profile_read")
-        return list(avg), n.value
+    def timer_stop(self) -> float:
+        """Device microseconds since timer_start (waits for the stream)."""
+        us = ctypes.c_double()
+        _check(self.lib.wh_timer_stop(self._h, ctypes.byref(us)), "timer_stop")
+        return us.value
 
     def debug_eval(self, fn: int, x) -> np.ndarray:
         x = _f32(x)

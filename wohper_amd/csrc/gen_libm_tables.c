@@ -100,6 +100,36 @@ static void* log_verify(void* p) {
     return NULL;
 }
 
+// Every float t in [-448, 448] against the brute-force nearest E4M3 value
+// (ties to the lower value, +0 for zero), walking the positive grid upward.
+static int check_e4m3_round(void) {
+    float grid[127];
+    int n = 0;
+    for (int code = 0; code < 0x7f; ++code) {  // +0 .. 448, ascending
+        int e = (code >> 3) & 15, m = code & 7;
+        grid[n++] = e == 0 ? (float)m * 0.001953125f : ldexpf(1.0f + (float)m / 8.0f, e - 7);
+    }
+    long bad = 0;
+    int i = 0;
+    for (uint32_t b = 0; b <= 0x43e00000u; ++b) {  // +0 .. 448
+        float a = wh_bits_to_float(b);
+        while (i + 1 < n && grid[i + 1] <= a) ++i;
+        float lo = grid[i], hi = i + 1 < n ? grid[i + 1] : grid[i];
+        float dlo = a - lo, dhi = hi - a;
+        float pos = dhi < dlo ? hi : lo;   // positive t: ties to lo
+        float neg = dlo < dhi ? lo : hi;   // negative t: ties to the larger magnitude
+        float want_p = pos, want_n = neg == 0.0f ? 0.0f : -neg;
+        float got_p = wh_e4m3_round(a), got_n = wh_e4m3_round(-a);
+        if (wh_float_to_bits(got_p) != wh_float_to_bits(want_p) ||
+            wh_float_to_bits(got_n) != wh_float_to_bits(want_n)) {
+            if (bad++ < 5) fprintf(stderr, "e4m3 round mismatch at %a: %a/%a want %a/%a\n", a, got_p, got_n, want_p, want_n);
+        }
+    }
+    if (bad) fprintf(stderr, "e4m3 round: %ld mismatches\n", bad);
+    else fprintf(stderr, "e4m3 round: every float in [-448, 448] matches the brute-force nearest\n");
+    return bad != 0;
+}
+
 int main(int argc, char** argv) {
     if (argc != 2) {
         fprintf(stderr, "usage: %s out.inc\n", argv[0]);
@@ -193,6 +223,8 @@ int main(int argc, char** argv) {
             return 1;
         }
     }
+
+    if (check_e4m3_round()) return 1;
 
     FILE* out = fopen(argv[1], "w");
     if (!out) {

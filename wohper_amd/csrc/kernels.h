@@ -31,12 +31,13 @@ __device__ __forceinline__ uint32_t wh_fp8_lds_index(uint32_t col) {
 }
 
 // FP4 matvec input order in LDS (the weight layout is described with the FP4
-// kernels below): xs[(g*8 + l)*4 + k] = x[32g + l + 8k], so AVX lane l's four
-// columns of group g are one float4.
-__device__ __forceinline__ uint32_t wh_fp4_lds_index(uint32_t col) {
-    uint32_t g = col >> 5, w = col & 31, k = w >> 3, l = w & 7;
-    return ((g * 8 + l) << 2) + k;
-}
+// kernels below): AVX lane l's four columns 32g + l + 8k (k = 0..3) of group
+// g are one float4, at float4 index g*8 + l plus one float4 of padding per
+// two groups, which spreads the staging stores of neighbouring threads over
+// all LDS banks (the matvec reads use compile-time offsets either way).
+__host__ __device__ constexpr uint32_t wh_xs_f4(uint32_t g, uint32_t l) { return g * 8 + l + (g >> 1); }
+// Floats of the staged x for `cols` columns.
+__host__ __device__ constexpr uint32_t wh_xs_floats(uint32_t cols) { return cols + (cols >> 4); }
 
 // Cross-workgroup hand-off inside one launch.  The 8 XCDs of an MI355X have
 // separate L2s, so an agent-scope fence writes back and invalidates the whole
@@ -81,7 +82,7 @@ __device__ __forceinline__ float wh_f4_get(const float4& v, int c) {
 __device__ __forceinline__ void wh_stage_fp4_store_group(float* xs, uint32_t g, const float* v32) {
 #pragma unroll
     for (int l = 0; l < 8; ++l)
-        ((float4*)xs)[g * 8 + l] = make_float4(v32[l], v32[8 + l], v32[16 + l], v32[24 + l]);
+        ((float4*)xs)[wh_xs_f4(g, l)] = make_float4(v32[l], v32[8 + l], v32[16 + l], v32[24 + l]);
 }
 __device__ __forceinline__ void wh_stage_f32_fp4_store(const wh_stage_f32_fp4& st, float* xs) {
     if (!st.on) return;
@@ -89,47 +90,6 @@ __device__ __forceinline__ void wh_stage_f32_fp4_store(const wh_stage_f32_fp4& s
 #pragma unroll
     for (int m = 0; m < 32; ++m) v[m] = wh_f4_get(st.v[m >> 2], m & 3);
     wh_stage_fp4_store_group(xs, st.g, v);
-}
-
-// FP4 lane order from act-quant codes (E4M3 bytes + one scale per 64).
-struct wh_stage_codes {
-    uint4 c0, c1;
-    float sc;
-    uint32_t g;
-    bool on;
-};
-__device__ __forceinline__ void wh_stage_codes_load(wh_stage_codes& st, const uint8_t* codes, const float* scales,
-                                                    uint32_t n, uint32_t g) {
-    st.g = g;
-    st.on = g < n / 32;
-    if (st.on) {
-        st.c0 = ((const uint4*)codes)[2 * g];
-        st.c1 = ((const uint4*)codes)[2 * g + 1];
-        st.sc = scales[g >> 1];
-    }
-}
-__device__ __forceinline__ void wh_stage_codes_store(const wh_stage_codes& st, float* xs) {
-    if (!st.on) return;
-    const uint32_t words[8] = {st.c0.x, st.c0.y, st.c0.z, st.c0.w, st.c1.x, st.c1.y, st.c1.z, st.c1.w};
-    float v[32];
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-        wh_f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[d], false);
-        wh_f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[d], true);
-        v[4 * d + 0] = lo.x * st.sc;
-        v[4 * d + 1] = lo.y * st.sc;
-        v[4 * d + 2] = hi.x * st.sc;
-        v[4 * d + 3] = hi.y * st.sc;
-    }
-    wh_stage_fp4_store_group(xs, st.g, v);
-}
-// Whole-vector variants (any n, looping over groups).
-__device__ __forceinline__ void wh_stage_codes_all(float* xs, const uint8_t* codes, const float* scales, uint32_t n) {
-    for (uint32_t g = threadIdx.x; g < n / 32; g += blockDim.x) {
-        wh_stage_codes st;
-        wh_stage_codes_load(st, codes, scales, n, g);
-        wh_stage_codes_store(st, xs);
-    }
 }
 
 // FP8 lane order from f32 x: one 16-col chunk per thread.
@@ -183,36 +143,10 @@ __global__ void __launch_bounds__(256) k_act_quant_inplace(float* __restrict__ v
         if (t != t) {
             q = -480.0f;  // partition_point over NaN -> lut[0]
         } else {
-            wh_e4m3_nearest(wh_clamp448(t), &q);
+            q = wh_e4m3_round(wh_clamp448(t));
         }
         v[i] = q * scale;
     }
-}
-
-// Act-quant of a vector into E4M3 codes plus one f32 scale per 64-block
-// (block size 64, as every call site of the expert path uses, E/deepseek_v4.rs:587,595).
-// code * scale reproduces the reference's dequantized value exactly.
-// One wave per block; x is f32 or bf16 (is_bf16).
-__global__ void __launch_bounds__(64) k_act_quant_codes(const void* __restrict__ x, int is_bf16,
-                                                        uint32_t n, uint8_t* __restrict__ codes,
-                                                        float* __restrict__ scales,
-                                                        uint32_t* __restrict__ status) {
-    uint32_t i = blockIdx.x * 64 + threadIdx.x;
-    float v = 0.0f;
-    if (i < n) {
-        if (is_bf16) v = __uint_as_float((uint32_t)((const uint16_t*)x)[i] << 16);
-        else v = ((const float*)x)[i];
-    }
-    float amax = wh_wave_max(fabsf(v));
-    if (!(amax <= 3.4028235e38f)) {  // inf or NaN input: reported, not quantized
-        if (threadIdx.x == 0) atomicOr(status, WH_ST_NONFINITE_INPUT);
-        amax = 1.0f;
-    }
-    int k = wh_aq_scale_exp(amax, kLog2Thr);
-    float q;
-    uint32_t code = wh_e4m3_nearest(wh_clamp448(v * wh_pow2f(-k)), &q);
-    if (i < n) codes[i] = (uint8_t)code;
-    if (threadIdx.x == 0) scales[blockIdx.x] = wh_pow2f(k);
 }
 
 // ------------------------------------------------------------- FP8 GEMV
@@ -234,8 +168,10 @@ __device__ __forceinline__ float wh_fp8_scale(const void* s, uint32_t idx) {
 
 // One 128-col group of one AVX lane: two 8-FMA chains (g0 over cols
 // 16c + l, g1 over 16c + 8 + l), then acc = fma(g0 + g1, scale, acc).
+// g0 + g1 of one 128-col group of one AVX lane: two 8-FMA chains, g0 over
+// cols 16c + l and g1 over cols 16c + 8 + l (E/compute.rs:5990-6005).
 template <bool kSpecial>
-__device__ __forceinline__ float wh_fp8_lane_group(uint4 wv, const float4* xg, float s, float acc) {
+__device__ __forceinline__ float wh_fp8_lane_gsum(uint4 wv, const float4* xg) {
     float4 x0 = xg[0], x1 = xg[1], x2 = xg[2], x3 = xg[3];
     wh_f2 w0 = wh_fp8x2<kSpecial, false>(wv.x), w1 = wh_fp8x2<kSpecial, true>(wv.x);
     wh_f2 w2 = wh_fp8x2<kSpecial, false>(wv.y), w3 = wh_fp8x2<kSpecial, true>(wv.y);
@@ -257,7 +193,11 @@ __device__ __forceinline__ float wh_fp8_lane_group(uint4 wv, const float4* xg, f
     g1 = __builtin_fmaf(w6.y, x3.y, g1);
     g1 = __builtin_fmaf(w7.x, x3.z, g1);
     g1 = __builtin_fmaf(w7.y, x3.w, g1);
-    return __builtin_fmaf(g0 + g1, s, acc);
+    return g0 + g1;
+}
+template <bool kSpecial>
+__device__ __forceinline__ float wh_fp8_lane_group(uint4 wv, const float4* xg, float s, float acc) {
+    return __builtin_fmaf(wh_fp8_lane_gsum<kSpecial>(wv, xg), s, acc);
 }
 
 // Fast path: col_group == 128.  One thread = one (row, AVX lane); 256
@@ -326,6 +266,89 @@ __global__ void __launch_bounds__(256) k_fp8_gemv(wh_fp8_args a) {
     }
 }
 
+// Split-K path (col_group == 128, groups % 8 == 0): 256 threads = 4 rows x 8
+// column segments x 8 AVX lanes; wave w runs row w.  Each thread forms
+// g0 + g1 for its segment's groups into LDS, then the 8 lane threads of
+// each row run the reference's sequential acc = fma(g0 + g1, scale, acc)
+// over all groups - the same operations in the same order as the one-thread
+// row, with 8x the threads in flight.  kGps = groups per segment when the
+// segment's weights fit in registers (4 for 4096 columns), else 0.
+template <bool kSpecial, bool kScaleU8, int kGps>
+__global__ void __launch_bounds__(256) k_fp8_gemv_sk(wh_fp8_args a) {
+    extern __shared__ __align__(16) float lds[];
+    const uint32_t batch = blockIdx.y;
+    const float* x = a.x + (size_t)batch * a.x_stride;
+    const uint32_t lane = threadIdx.x & 7, seg = (threadIdx.x >> 3) & 7, rr = threadIdx.x >> 6;
+    const uint32_t row = a.row_start + blockIdx.x * 4 + rr;
+    const bool active = row < a.row_end;
+    const uint32_t srow_idx = active ? row : a.row_start;
+    const uint32_t G = a.cols >> 7, gps = G >> 3, gbeg = seg * gps;
+    const uint4* wp = (const uint4*)(a.w + (size_t)srow_idx * a.cols) + lane;  // group g at wp[8 g]
+    const uint32_t sbase = (srow_idx / a.row_group) * a.scale_cols;
+    float* xs = lds;
+    float* gsum = lds + a.cols + (rr * 8 + lane) * G;  // per (row, lane): g0 + g1 of every group
+    float* scl = lds + a.cols + 32 * G + rr * G;        // per row: the group scales
+    const float4* xp = (const float4*)xs + lane * 4;   // group g at xp[32 g]
+    // staging loads (x chunk, this lane's share of the row's scales) go out
+    // before the weight loads, so waiting for them never waits for weights
+    wh_stage_f32_fp8 st;
+    wh_stage_f32_fp8_load(st, x, a.cols, threadIdx.x);
+    const uint32_t sg = seg * 8 + lane;  // scales g = sg, sg + 64, ...
+    float sv = sg < G ? wh_fp8_scale<kSpecial, kScaleU8>(a.scales, sbase + sg) : 0.0f;
+    if constexpr (kGps > 0) {
+        uint4 w[kGps];
+#pragma unroll
+        for (int i = 0; i < kGps; ++i) w[i] = wp[8 * (gbeg + i)];
+        __builtin_amdgcn_sched_barrier(0);
+        wh_stage_f32_fp8_store(st, xs);
+        if (sg < G) scl[sg] = sv;
+        for (uint32_t q = threadIdx.x + 256; q < a.cols / 16; q += 256) {
+            wh_stage_f32_fp8 s2;
+            wh_stage_f32_fp8_load(s2, x, a.cols, q);
+            wh_stage_f32_fp8_store(s2, xs);
+        }
+        for (uint32_t g = sg + 64; g < G; g += 64) scl[g] = wh_fp8_scale<kSpecial, kScaleU8>(a.scales, sbase + g);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kGps; ++i) gsum[gbeg + i] = wh_fp8_lane_gsum<kSpecial>(w[i], xp + 32 * (gbeg + i));
+    } else {
+        wh_stage_f32_fp8_store(st, xs);
+        for (uint32_t q = threadIdx.x + 256; q < a.cols / 16; q += 256) {
+            wh_stage_f32_fp8 s2;
+            wh_stage_f32_fp8_load(s2, x, a.cols, q);
+            wh_stage_f32_fp8_store(s2, xs);
+        }
+        for (uint32_t g = sg; g < G; g += 64) scl[g] = wh_fp8_scale<kSpecial, kScaleU8>(a.scales, sbase + g);
+        __syncthreads();
+        for (uint32_t g = gbeg; g < gbeg + gps; ++g) gsum[g] = wh_fp8_lane_gsum<kSpecial>(wp[8 * g], xp + 32 * g);
+    }
+    __syncthreads();
+    if (seg != 0) return;
+    float acc = 0.0f;
+    if constexpr (kGps > 0) {  // G = 8 kGps known: all operands read as vectors first
+        float4 gv[2 * kGps], sv4[2 * kGps];
+#pragma unroll
+        for (int i = 0; i < 2 * kGps; ++i) {
+            gv[i] = ((const float4*)gsum)[i];
+            sv4[i] = ((const float4*)scl)[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * kGps; ++i) {
+            acc = __builtin_fmaf(gv[i].x, sv4[i].x, acc);
+            acc = __builtin_fmaf(gv[i].y, sv4[i].y, acc);
+            acc = __builtin_fmaf(gv[i].z, sv4[i].z, acc);
+            acc = __builtin_fmaf(gv[i].w, sv4[i].w, acc);
+        }
+    } else {
+        for (uint32_t g = 0; g < G; ++g) acc = __builtin_fmaf(gsum[g], scl[g], acc);
+    }
+    const float sum = wh_hsum8(acc) + 0.0f;  // + tail (0 for col_group % 16 == 0)
+    if (active && lane == 0) {
+        a.y[(size_t)batch * a.y_stride + (row - a.row_start)] = sum;
+        if (!(fabsf(sum) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
+    }
+}
+
 // Generic path for any col_group: one thread per row emulating the 8 AVX2
 // lanes, the scalar tail and `hsum256 + tail` exactly (E/compute.rs:5978-6018).
 // Weights are in the original row-major order.
@@ -369,15 +392,17 @@ __global__ void __launch_bounds__(64) k_fp8_gemv_generic(wh_fp8_args a, uint32_t
 }
 
 // ------------------------------------------------------------- FP4 matvec
-// Resident FP4 layout (fast path: group_cols == 32, cols % 512 == 0).  A row
-// is run by a quad of 4 threads; thread t owns AVX lanes t and t + 4.
-//   weights: chunk j = groups 4j..4j+3 (64 bytes of the row); thread t's 16
-//            bytes sit at (4j + t) * 16, dword i = group 4j + i, encoded by
-//            wh_fp4_encode_word with A = lane t, B = lane t + 4;
-//   scales:  thread t owns the UE8M0 bytes of groups t, t+4, t+8, ... stored
-//            contiguously: byte t * (G/4) + j is the scale of group 4j + t.
-// Each thread decodes one scale per chunk and the quad shares it through a
-// DPP broadcast fused into the accumulate FMA.
+// Resident FP4 layout (fast path: group_cols == 32, cols % 256 == 0).  A row
+// is run by 8 threads, one per AVX lane of E/deepseek_v4.rs:294-347: lane l
+// owns columns l, 8+l, 16+l, 24+l of every 32-col group.
+//   weights: per block of 8 groups (256 columns = 128 bytes of the row),
+//            lane l's 16 bytes sit at block*128 + l*16; dword d holds the
+//            lane's 4 values of group 8b+2d (A) and of group 8b+2d+1 (B),
+//            packed by wh_fp4_encode_word;
+//   scales:  unchanged, [row][cols/32] UE8M0 bytes.
+// A workgroup stages x in LDS in lane order (wh_fp4_lds_index) next to a
+// table of its rows' group scales, each already multiplied by 1/8 as the
+// reference does (`scale * 0.125`, E/deepseek_v4.rs:329).
 __host__ __device__ inline uint32_t wh_fp4_encode_word(const uint32_t* a, const uint32_t* b) {
     uint32_t word = 0;
     for (uint32_t k = 0; k < 4; ++k) {
@@ -388,192 +413,199 @@ __host__ __device__ inline uint32_t wh_fp4_encode_word(const uint32_t* a, const 
     return word;
 }
 
-template <int kI>
-__device__ __forceinline__ float wh_quad_bcast(float v) {  // quad_perm [kI,kI,kI,kI]
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kI * 0x55, 0xf, 0xf, false));
+// Row stride (floats) of the LDS scale table; the 4 extra floats put
+// consecutive rows on different banks.
+__host__ __device__ constexpr uint32_t wh_s8_stride(uint32_t groups) { return groups + 4; }
+
+// LDS bytes of a 32-row FP4 workgroup: staged x + the scale table.
+__host__ __device__ constexpr size_t wh_fp4_wg_lds(size_t cols) {
+    return sizeof(float) * (wh_xs_floats((uint32_t)cols) + 32 * (size_t)wh_s8_stride((uint32_t)(cols / 32)));
 }
 
-// Group 4j + kI of one quad thread: two 4-FMA chains (lanes t and t+4) on the
-// x8 values, then acc = fma(gacc, scale / 8, acc) per lane.
-template <int kI>
-__device__ __forceinline__ void wh_fp4_quad_group_x(uint32_t word, float4 xa, float4 xb, float smine,
-                                                    float& acc_a, float& acc_b) {
+// One dword of one lane = two groups: a 4-FMA chain from zero per group over
+// the x8 integer values, folded in with acc = fma(gacc, scale/8, acc).
+__device__ __forceinline__ float wh_fp4_lane_pair(uint32_t word, const float4& xa, const float4& xb, float sa,
+                                                  float sb, float acc) {
     wh_fp4x8 e = wh_fp4_decode8(word);
     float ga = __builtin_fmaf(e.a01.x, xa.x, 0.0f);
     ga = __builtin_fmaf(e.a01.y, xa.y, ga);
     ga = __builtin_fmaf(e.a23.x, xa.z, ga);
     ga = __builtin_fmaf(e.a23.y, xa.w, ga);
+    acc = __builtin_fmaf(ga, sa, acc);
     float gb = __builtin_fmaf(e.b01.x, xb.x, 0.0f);
     gb = __builtin_fmaf(e.b01.y, xb.y, gb);
     gb = __builtin_fmaf(e.b23.x, xb.z, gb);
     gb = __builtin_fmaf(e.b23.y, xb.w, gb);
-    float s8 = wh_quad_bcast<kI>(smine);
-    acc_a = __builtin_fmaf(ga, s8, acc_a);
-    acc_b = __builtin_fmaf(gb, s8, acc_b);
+    return __builtin_fmaf(gb, sb, acc);
 }
 
-template <int kI>
-__device__ __forceinline__ void wh_fp4_quad_group(uint32_t word, const float4* xg, uint32_t t,
-                                                  float smine, float& acc_a, float& acc_b) {
-    wh_fp4x8 e = wh_fp4_decode8(word);
-    float4 xa = xg[t], xb = xg[t + 4];
-    float ga = __builtin_fmaf(e.a01.x, xa.x, 0.0f);
-    ga = __builtin_fmaf(e.a01.y, xa.y, ga);
-    ga = __builtin_fmaf(e.a23.x, xa.z, ga);
-    ga = __builtin_fmaf(e.a23.y, xa.w, ga);
-    float gb = __builtin_fmaf(e.b01.x, xb.x, 0.0f);
-    gb = __builtin_fmaf(e.b01.y, xb.y, gb);
-    gb = __builtin_fmaf(e.b23.x, xb.z, gb);
-    gb = __builtin_fmaf(e.b23.y, xb.w, gb);
-    float s8 = wh_quad_bcast<kI>(smine);
-    acc_a = __builtin_fmaf(ga, s8, acc_a);
-    acc_b = __builtin_fmaf(gb, s8, acc_b);
+// One block (8 groups) of one lane.  xp = (float4*)xs + lane; s8row = the
+// row's scale table.
+__device__ __forceinline__ float wh_fp4_lane_block(uint4 w, const float4* xp, const float* s8row, uint32_t b,
+                                                   float acc) {
+    const float4 s0 = ((const float4*)s8row)[2 * b], s1 = ((const float4*)s8row)[2 * b + 1];
+    const float4* xg = xp + 68 * b;  // group 8b + j -> xg[wh_xs_f4(j, 0)]
+    acc = wh_fp4_lane_pair(w.x, xg[wh_xs_f4(0, 0)], xg[wh_xs_f4(1, 0)], s0.x, s0.y, acc);
+    acc = wh_fp4_lane_pair(w.y, xg[wh_xs_f4(2, 0)], xg[wh_xs_f4(3, 0)], s0.z, s0.w, acc);
+    acc = wh_fp4_lane_pair(w.z, xg[wh_xs_f4(4, 0)], xg[wh_xs_f4(5, 0)], s1.x, s1.y, acc);
+    acc = wh_fp4_lane_pair(w.w, xg[wh_xs_f4(6, 0)], xg[wh_xs_f4(7, 0)], s1.z, s1.w, acc);
+    return acc;
 }
 
-__device__ __forceinline__ void wh_fp4_quad_chunk(uint4 w, uint32_t sbyte, uint32_t j, const float4* xp,
-                                                  uint32_t t, float& acc_a, float& acc_b) {
-    float smine = wh_ue8m0(sbyte) * 0.125f;
-    const float4* xg = xp + j * 32;  // group 4j at float4 index (4j * 8)
-    wh_fp4_quad_group<0>(w.x, xg, t, smine, acc_a, acc_b);
-    wh_fp4_quad_group<1>(w.y, xg + 8, t, smine, acc_a, acc_b);
-    wh_fp4_quad_group<2>(w.z, xg + 16, t, smine, acc_a, acc_b);
-    wh_fp4_quad_group<3>(w.w, xg + 24, t, smine, acc_a, acc_b);
-}
-
-// A quad thread's whole row in registers (kChunks known at compile time:
-// 32 for K = 4096, 16 for K = 2048): every load is issued before any math,
-// since one token's matvec is a single latency-bound sweep.
-template <int kChunks>
-struct wh_fp4_rowbuf {
-    uint4 w[kChunks];
-    uint32_t sw[kChunks / 4];
+// A lane's whole row in registers (kBlk = cols / 256 known at compile time),
+// loaded before anything waits so the row's bytes are all in flight at once.
+template <int kBlk>
+struct wh_fp4_lane_row {
+    uint4 w[kBlk];
 };
-
-template <int kChunks>
-__device__ __forceinline__ void wh_fp4_rowbuf_load(wh_fp4_rowbuf<kChunks>& b, const uint8_t* __restrict__ wrow,
-                                                   const uint8_t* __restrict__ srow, uint32_t t) {
-    const uint4* wp = (const uint4*)wrow + t;
-    const uint32_t* sp = (const uint32_t*)(srow + t * kChunks);
+template <int kBlk>
+__device__ __forceinline__ void wh_fp4_lane_row_load(wh_fp4_lane_row<kBlk>& r, const uint8_t* __restrict__ wrow,
+                                                     uint32_t lane) {
+    const uint4* p = (const uint4*)wrow + lane;
 #pragma unroll
-    for (int q = 0; q < kChunks / 4; ++q) b.sw[q] = sp[q];
+    for (int b = 0; b < kBlk; ++b) r.w[b] = p[8 * b];
+}
+// LDS operands of one block of one lane: x of its 8 groups and their scales.
+struct wh_fp4_blk_lds {
+    float4 x[8];
+    float4 s0, s1;
+};
+// `dep` is an opaque zero tied to the running sum: block reads indexed with
+// it cannot be hoisted above the blocks before them, which would keep every
+// block's operands live at once.
+__device__ __forceinline__ void wh_fp4_blk_lds_read(wh_fp4_blk_lds& o, const float4* xp, const float* s8row,
+                                                    uint32_t b, uint32_t dep) {
+    const float4* xg = xp + 68 * b + dep;  // group 8b + j -> xg[wh_xs_f4(j, 0)]
 #pragma unroll
-    for (int j = 0; j < kChunks; ++j) b.w[j] = wp[4 * j];
+    for (int j = 0; j < 8; ++j) o.x[j] = xg[wh_xs_f4(j, 0)];
+    const float4* sp = (const float4*)s8row + 2 * b + dep;
+    o.s0 = sp[0];
+    o.s1 = sp[1];
+}
+__device__ __forceinline__ uint32_t wh_opaque_zero(float after) {
+    uint32_t z = 0;
+    asm volatile("" : "+v"(z) : "v"(after));
+    return z;
+}
+__device__ __forceinline__ float wh_fp4_blk_compute(uint4 w, const wh_fp4_blk_lds& o, float acc) {
+    acc = wh_fp4_lane_pair(w.x, o.x[0], o.x[1], o.s0.x, o.s0.y, acc);
+    acc = wh_fp4_lane_pair(w.y, o.x[2], o.x[3], o.s0.z, o.s0.w, acc);
+    acc = wh_fp4_lane_pair(w.z, o.x[4], o.x[5], o.s1.x, o.s1.y, acc);
+    acc = wh_fp4_lane_pair(w.w, o.x[6], o.x[7], o.s1.z, o.s1.w, acc);
+    return acc;
 }
 
-// The x values of chunk j + 1 are read from LDS while chunk j computes, so
-// the LDS latency is hidden even at one wave per SIMD.
-template <int kChunks>
-__device__ __forceinline__ void wh_fp4_rowbuf_dot(const wh_fp4_rowbuf<kChunks>& b, const float* xs, uint32_t t,
-                                                  float& acc_a, float& acc_b) {
-    const float4* xp = (const float4*)xs + t;
-    acc_a = 0.0f;
-    acc_b = 0.0f;
-    float4 xc[8], xn[8];
+// The LDS reads of block b + 1 are issued before block b computes, so their
+// latency hides behind that block's arithmetic (kBlk even; two named
+// buffers, alternated by hand, stay in registers).
+template <int kBlk>
+__device__ __forceinline__ float wh_fp4_lane_row_dot(const wh_fp4_lane_row<kBlk>& r, const float* xs,
+                                                     const float* s8row, uint32_t lane) {
+    static_assert(kBlk % 2 == 0, "blocks are processed in pairs");
+    const float4* xp = (const float4*)xs + lane;
+    wh_fp4_blk_lds ba, bb;
+    float acc = 0.0f;
+    wh_fp4_blk_lds_read(ba, xp, s8row, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        xc[2 * i] = xp[i * 8];
-        xc[2 * i + 1] = xp[i * 8 + 4];
-    }
-#pragma unroll
-    for (int j = 0; j < kChunks; ++j) {
-        if (j + 1 < kChunks) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                xn[2 * i] = xp[((j + 1) * 4 + i) * 8];
-                xn[2 * i + 1] = xp[((j + 1) * 4 + i) * 8 + 4];
-            }
-        }
+    for (int b = 0; b < kBlk; b += 2) {
+        wh_fp4_blk_lds_read(bb, xp, s8row, b + 1, wh_opaque_zero(acc));
         __builtin_amdgcn_sched_barrier(0);
-        const float smine = wh_ue8m0((b.sw[j >> 2] >> (8 * (j & 3))) & 0xffu) * 0.125f;
-        wh_fp4_quad_group_x<0>(b.w[j].x, xc[0], xc[1], smine, acc_a, acc_b);
-        wh_fp4_quad_group_x<1>(b.w[j].y, xc[2], xc[3], smine, acc_a, acc_b);
-        wh_fp4_quad_group_x<2>(b.w[j].z, xc[4], xc[5], smine, acc_a, acc_b);
-        wh_fp4_quad_group_x<3>(b.w[j].w, xc[6], xc[7], smine, acc_a, acc_b);
+        acc = wh_fp4_blk_compute(r.w[b], ba, acc);
+        if (b + 2 < kBlk) wh_fp4_blk_lds_read(ba, xp, s8row, b + 2, wh_opaque_zero(acc));
         __builtin_amdgcn_sched_barrier(0);
+        acc = wh_fp4_blk_compute(r.w[b + 1], bb, acc);
+    }
+    return acc;
+}
+// Runtime block count: weights streamed one block ahead.
+__device__ __forceinline__ float wh_fp4_lane_dot_rt(const uint8_t* __restrict__ wrow, uint32_t blocks,
+                                                    const float* xs, const float* s8row, uint32_t lane) {
+    const uint4* p = (const uint4*)wrow + lane;
+    const float4* xp = (const float4*)xs + lane;
+    float acc = 0.0f;
+    uint4 nxt = p[0];
+    for (uint32_t b = 0; b < blocks; ++b) {
+        uint4 cur = nxt;
+        if (b + 1 < blocks) nxt = p[8 * (b + 1)];
+        acc = wh_fp4_lane_block(cur, xp, s8row, b, acc);
+    }
+    return acc;
+}
+
+// A row's UE8M0 bytes staged as scale/8 floats: lane l takes the kBlk bytes
+// [l*kBlk, (l+1)*kBlk) of the row (kBlk = groups / 8, a multiple of 4).
+template <int kBlk>
+struct wh_s8_stage {
+    uint32_t v[kBlk / 4];
+};
+template <int kBlk>
+__device__ __forceinline__ void wh_s8_stage_load(wh_s8_stage<kBlk>& st, const uint8_t* srow, uint32_t lane) {
+    const uint32_t* p = (const uint32_t*)(srow + lane * kBlk);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xc[i] = xn[i];
+    for (int i = 0; i < kBlk / 4; ++i) st.v[i] = p[i];
+}
+template <int kBlk>
+__device__ __forceinline__ void wh_s8_stage_store(const wh_s8_stage<kBlk>& st, float* s8row, uint32_t lane) {
+    float4* d = (float4*)(s8row + lane * kBlk);
+#pragma unroll
+    for (int i = 0; i < kBlk / 4; ++i) {
+        const uint32_t v = st.v[i];
+        d[i] = make_float4(wh_ue8m0(v) * 0.125f, wh_ue8m0(v >> 8) * 0.125f, wh_ue8m0(v >> 16) * 0.125f,
+                           wh_ue8m0(v >> 24) * 0.125f);
     }
 }
-
-// Runtime chunk count (multiple of 4), blocks of 4 chunks double-buffered.
-__device__ __forceinline__ void wh_fp4_quad_dot_rt(const uint8_t* __restrict__ wrow, const uint8_t* __restrict__ srow,
-                                                   uint32_t chunks, uint32_t t, const float* xs, float& acc_a,
-                                                   float& acc_b) {
-    const uint4* wp = (const uint4*)wrow + t;
-    const uint32_t* sp = (const uint32_t*)(srow + t * chunks);
-    const float4* xp = (const float4*)xs;
-    acc_a = 0.0f;
-    acc_b = 0.0f;
-    uint4 n0 = wp[0], n1 = wp[4], n2 = wp[8], n3 = wp[12];
-    uint32_t ns = sp[0];
-    for (uint32_t j = 0; j < chunks; j += 4) {
-        uint4 c0 = n0, c1 = n1, c2 = n2, c3 = n3;
-        uint32_t cs = ns;
-        if (j + 4 < chunks) {
-            n0 = wp[4 * (j + 4)];
-            n1 = wp[4 * (j + 5)];
-            n2 = wp[4 * (j + 6)];
-            n3 = wp[4 * (j + 7)];
-            ns = sp[(j + 4) >> 2];
-        }
-        wh_fp4_quad_chunk(c0, cs & 0xffu, j, xp, t, acc_a, acc_b);
-        wh_fp4_quad_chunk(c1, (cs >> 8) & 0xffu, j + 1, xp, t, acc_a, acc_b);
-        wh_fp4_quad_chunk(c2, (cs >> 16) & 0xffu, j + 2, xp, t, acc_a, acc_b);
-        wh_fp4_quad_chunk(c3, cs >> 24, j + 3, xp, t, acc_a, acc_b);
-    }
-}
-
-// The AVX2 horizontal sum ((l0+l1)+(l2+l3)) + ((l4+l5)+(l6+l7)) over the
-// quad's (lane t, lane t+4) accumulators; valid in quad thread 0.
-__device__ __forceinline__ float wh_quad_hsum(float acc_a, float acc_b) {
-    float p = acc_a + wh_dpp_quad_swap1(acc_a);
-    p = p + wh_dpp_quad_swap2(p);
-    float q = acc_b + wh_dpp_quad_swap1(acc_b);
-    q = q + wh_dpp_quad_swap2(q);
-    return p + q;
+__device__ __forceinline__ void wh_s8_stage_rt(const uint8_t* srow, uint32_t groups, float* s8row, uint32_t lane) {
+    for (uint32_t g = lane; g < groups; g += 8) s8row[g] = wh_ue8m0(srow[g]) * 0.125f;
 }
 
 struct wh_fp4_args {
     const uint8_t* w;  // resident
-    const uint8_t* s;  // resident scales
+    const uint8_t* s;  // scales
     const float* x;
     float* y;
     uint32_t* status;
     uint32_t rows, cols;
 };
 
-// Fast path: 256 threads = 64 rows (one quad per row).  kChunks = cols/128
-// when it is 16 or 32 (row fully in registers), else 0 (runtime loop).
-template <int kChunks>
+// Fast path: 256 threads = 32 rows (8 lanes each).  kBlk = cols/256 when
+// it is 8 or 16 (row fully in registers), else 0 (runtime loop).
+template <int kBlk>
 __global__ void __launch_bounds__(256) k_fp4_matvec(wh_fp4_args a) {
-    extern __shared__ __align__(16) float xs[];
-    const uint32_t t = threadIdx.x & 3;
-    const uint32_t row = blockIdx.x * 64 + (threadIdx.x >> 2);
+    extern __shared__ __align__(16) float lds[];
+    const uint32_t G = a.cols >> 5;
+    const uint32_t lane = threadIdx.x & 7, oct = threadIdx.x >> 3;
+    const uint32_t row = blockIdx.x * 32 + oct;
     const bool active = row < a.rows;
     const uint32_t rr = active ? row : 0;
     const uint8_t* wrow = a.w + (size_t)rr * (a.cols / 2);
-    const uint8_t* srow = a.s + (size_t)rr * (a.cols / 32);
-    float acc_a = 0.0f, acc_b = 0.0f;
-    if constexpr (kChunks > 0) {
+    const uint8_t* srow = a.s + (size_t)rr * G;
+    float* xs = lds;
+    float* s8row = lds + wh_xs_floats(a.cols) + oct * wh_s8_stride(G);
+    float acc;
+    if constexpr (kBlk > 0) {
         wh_stage_f32_fp4 st;
         wh_stage_f32_fp4_load(st, a.x, a.cols, threadIdx.x);
-        wh_fp4_rowbuf<kChunks> b;
-        wh_fp4_rowbuf_load<kChunks>(b, wrow, srow, t);
+        wh_s8_stage<kBlk> ss;
+        wh_s8_stage_load<kBlk>(ss, srow, lane);
+        wh_fp4_lane_row<kBlk> r;
+        wh_fp4_lane_row_load<kBlk>(r, wrow, lane);
         __builtin_amdgcn_sched_barrier(0);
         wh_stage_f32_fp4_store(st, xs);
+        wh_s8_stage_store<kBlk>(ss, s8row, lane);
         __syncthreads();
-        wh_fp4_rowbuf_dot<kChunks>(b, xs, t, acc_a, acc_b);
+        acc = wh_fp4_lane_row_dot<kBlk>(r, xs, s8row, lane);
     } else {
-        for (uint32_t g = threadIdx.x; g < a.cols / 32; g += 256) {
+        for (uint32_t g = threadIdx.x; g < G; g += 256) {
             wh_stage_f32_fp4 st;
             wh_stage_f32_fp4_load(st, a.x, a.cols, g);
             wh_stage_f32_fp4_store(st, xs);
         }
+        wh_s8_stage_rt(srow, G, s8row, lane);
         __syncthreads();
-        wh_fp4_quad_dot_rt(wrow, srow, a.cols >> 7, t, xs, acc_a, acc_b);
+        acc = wh_fp4_lane_dot_rt(wrow, G >> 3, xs, s8row, lane);
     }
-    float sum = wh_quad_hsum(acc_a, acc_b) + 0.0f;  // + tail (0 here)
-    if (active && t == 0) {
+    float sum = wh_hsum8(acc) + 0.0f;  // + tail (0 here)
+    if (active && lane == 0) {
         a.y[row] = sum;
         if (!(fabsf(sum) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
     }
@@ -642,6 +674,16 @@ __global__ void __launch_bounds__(64) k_fp4_matvec_generic(wh_fp4_args a, uint32
 }
 
 // --------------------------------------------------- routed expert pipeline
+// Two launches per decode step run the routed-expert FFN of
+// E/compute.rs:1948-2012 for every token of the step:
+//   k_moe_gateup: gate/up matvecs + SwiGLU (E/deepseek_v4.rs:586-594), with
+//                 the act-quant of x recomputed by every workgroup from the
+//                 input (a 4096-vector, cheaper than another launch);
+//   k_moe_down:   act-quant of the hidden (E/deepseek_v4.rs:595) recomputed
+//                 per workgroup while staging it, the down matvec
+//                 (E/deepseek_v4.rs:596-599) and the ordered weighted sum.
+// The launch boundary is the only hand-off between the two; the routed sum
+// is the one value that crosses workgroups inside a launch.
 struct wh_expert_ptrs {
     const uint8_t* w1;
     const uint8_t* s1;
@@ -656,128 +698,275 @@ struct wh_moe_args {
     float route_w[WH_MAX_EXPERTS];
     uint32_t n_experts;
     uint32_t hidden, inter;        // w1/w3: inter x hidden, w2: hidden x inter
-    uint32_t n_tokens;             // tokens sharing the same expert list (1 for decode)
-    const uint8_t* xq_codes;       // [n_tokens][hidden] act-quant codes of x
-    const float* xq_scales;        // [n_tokens][hidden/64]
-    float* h;                      // [n_tokens][n_experts][inter] swiglu hidden (pre-quant)
-    uint8_t* hq_codes;             // [n_tokens][n_experts][inter]
-    float* hq_scales;              // [n_tokens][n_experts][inter/64]
+    uint32_t n_tokens;             // tokens sharing the same expert list
+    const void* x;                 // [n_tokens][hidden], f32 or bf16
+    uint32_t x_is_bf16;
+    float* h;                      // [n_tokens][n_experts][inter] SwiGLU output
     float* y;                      // [n_tokens][n_experts][hidden] per-expert outputs
     float* out;                    // [n_tokens][hidden] routed sum
-    uint32_t* cnt_h;               // [n_tokens][n_experts][inter/64] arrival counters
-    uint32_t* cnt_y;               // [n_tokens][hidden/32] arrival counters
+    uint32_t* cnt_y;               // [n_tokens][hidden/32] arrivals per 32-row slice
     uint32_t* status;
 };
 
-// Gate/up + SwiGLU + act-quant of the hidden.  Grid: (inter/16, n_experts,
-// n_tokens); 128 threads = 32 quads = 16 rows x {w1, w3}: quad 2r runs w1
-// row r and quad 2r+1 the w3 row r (E/deepseek_v4.rs:588-594).  The last of
-// the 4 workgroups that complete a 64-row block quantizes it
-// (E/deepseek_v4.rs:595).
-template <int kChunks>
-__global__ void __launch_bounds__(128) k_moe_gateup(wh_moe_args a) {
-    extern __shared__ __align__(16) float xs[];
-    __shared__ uint32_t last;
-    const uint32_t e = blockIdx.y, tok = blockIdx.z;
-    const wh_expert_ptrs ep = a.ex[e];
-    const uint32_t t = threadIdx.x & 3, quad = threadIdx.x >> 2;
-    const uint32_t row = blockIdx.x * 16 + (quad >> 1);
-    const bool up = quad & 1;
-    const size_t rb = (size_t)row * (a.hidden / 2), sb = (size_t)row * (a.hidden / 32);
-    const uint8_t* wrow = (up ? ep.w3 : ep.w1) + rb;
-    const uint8_t* srow = (up ? ep.s3 : ep.s1) + sb;
-    const uint8_t* codes = a.xq_codes + (size_t)tok * a.hidden;
-    const float* cscales = a.xq_scales + (size_t)tok * (a.hidden / 64);
-    float acc_a, acc_b;
-    if constexpr (kChunks > 0) {
-        wh_stage_codes st;
-        wh_stage_codes_load(st, codes, cscales, a.hidden, threadIdx.x);
-        wh_fp4_rowbuf<kChunks> b;
-        wh_fp4_rowbuf_load<kChunks>(b, wrow, srow, t);
-        __builtin_amdgcn_sched_barrier(0);
-        wh_stage_codes_store(st, xs);
-        __syncthreads();
-        wh_fp4_rowbuf_dot<kChunks>(b, xs, t, acc_a, acc_b);
+// The per-binade log2f thresholds of the act-quant scale, staged in LDS: a
+// table lookup in global memory after the weight loads would make the wave
+// wait for all of them (memory loads complete in issue order).
+struct wh_thr_stage {
+    uint32_t v;
+};
+__device__ __forceinline__ void wh_thr_stage_load(wh_thr_stage& st) {
+    st.v = threadIdx.x < 254 ? kLog2Thr[threadIdx.x] : 0u;
+}
+__device__ __forceinline__ void wh_thr_stage_store(const wh_thr_stage& st, uint32_t* thr) {
+    if (threadIdx.x < 254) thr[threadIdx.x] = st.v;
+}
+// LDS bytes of a routed-expert workgroup over `cols` input columns.
+__host__ __device__ constexpr size_t wh_moe_wg_lds(size_t cols) { return wh_fp4_wg_lds(cols) + 256 * sizeof(uint32_t); }
+
+// 16 consecutive x values of one thread (bf16 or f32), loaded early.
+struct wh_xq_stage {
+    uint4 raw[4];
+    uint32_t c0;
+    bool on;
+};
+__device__ __forceinline__ void wh_xq_stage_load(wh_xq_stage& st, const void* x, bool bf16, uint32_t n,
+                                                 uint32_t idx) {
+    st.c0 = 16 * idx;
+    st.on = st.c0 < n;
+    if (!st.on) {
+        for (int i = 0; i < 4; ++i) st.raw[i] = make_uint4(0, 0, 0, 0);
+        return;
+    }
+    if (bf16) {
+        const uint4* p = (const uint4*)((const uint16_t*)x + st.c0);
+        st.raw[0] = p[0];
+        st.raw[1] = p[1];
     } else {
-        wh_stage_codes_all(xs, codes, cscales, a.hidden);
-        __syncthreads();
-        wh_fp4_quad_dot_rt(wrow, srow, a.hidden >> 7, t, xs, acc_a, acc_b);
+        const uint4* p = (const uint4*)((const float*)x + st.c0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st.raw[i] = p[i];
     }
-    float v = wh_quad_hsum(acc_a, acc_b) + 0.0f;
-    float u = wh_dpp_row_shl4(v);  // lane 8r <- lane 8r + 4 (the w3 quad)
-    const size_t hbase = ((size_t)tok * a.n_experts + e) * a.inter;
-    if ((threadIdx.x & 7) == 0) {
-        if (!(fabsf(v) <= 3.4028235e38f) || !(fabsf(u) <= 3.4028235e38f)) {
-            atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
+}
+// Act-quant of the 64-block the thread's quad covers (E/compute.rs:2504-2521,
+// block 64), result written to LDS in FP4 lane order.  Non-finite input is
+// reported through the status word.
+__device__ __forceinline__ void wh_xq_stage_store(const wh_xq_stage& st, bool bf16, float* xs,
+                                                  const uint32_t* log2_thr, uint32_t* status) {
+    float v[16];
+    if (bf16) {
+        const uint32_t w[8] = {st.raw[0].x, st.raw[0].y, st.raw[0].z, st.raw[0].w,
+                               st.raw[1].x, st.raw[1].y, st.raw[1].z, st.raw[1].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
         }
-        wh_store_coherent(a.h + hbase + row, wh_swiglu(v, u, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[4 * i] = __uint_as_float(st.raw[i].x);
+            v[4 * i + 1] = __uint_as_float(st.raw[i].y);
+            v[4 * i + 2] = __uint_as_float(st.raw[i].z);
+            v[4 * i + 3] = __uint_as_float(st.raw[i].w);
+        }
     }
-    wh_stores_done();
-    __syncthreads();
-    const uint32_t blk = row >> 6;
-    uint32_t* cnt = a.cnt_h + ((size_t)tok * a.n_experts + e) * (a.inter / 64) + blk;
-    if (threadIdx.x == 0) last = wh_arrive(cnt) == 3u;
-    __syncthreads();
-    if (!last || threadIdx.x >= 64) return;
-    float hv = wh_load_coherent(a.h + hbase + blk * 64 + threadIdx.x);
-    float amax = wh_wave_max(fabsf(hv));
-    if (!(amax <= 3.4028235e38f)) amax = 1.0f;  // non-finite rows already reported
-    int k = wh_aq_scale_exp(amax, kLog2Thr);
-    float q;
-    uint32_t code = wh_e4m3_nearest(wh_clamp448(hv * wh_pow2f(-k)), &q);
-    a.hq_codes[hbase + blk * 64 + threadIdx.x] = (uint8_t)code;
-    if (threadIdx.x == 0) {
-        a.hq_scales[hbase / 64 + blk] = wh_pow2f(k);
-        *cnt = 0u;  // ready for the next launch
+    float amax = 0.0f;
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float m = fabsf(v[i]);
+        bad |= !(m <= 3.4028235e38f);
+        amax = fmaxf(amax, m);
+    }
+    amax = fmaxf(amax, wh_dpp_quad_swap1(amax));  // the quad holds one 64-block
+    amax = fmaxf(amax, wh_dpp_quad_swap2(amax));
+    if (!st.on) return;
+    if (bad) atomicOr(status, WH_ST_NONFINITE_INPUT);
+    if (!(amax <= 3.4028235e38f)) amax = 1.0f;
+    const int k = wh_aq_scale_exp(amax, log2_thr);
+    const float inv = wh_pow2f(-k), sc = wh_pow2f(k);
+    float q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        q[i] = wh_e4m3_round(wh_clamp448(v[i] * inv)) * sc;
+    }
+    // columns c0 + j: group c0/32, lane j % 8, k = 2*((c0/16) & 1) + j/8
+    const uint32_t g = st.c0 >> 5, h = (st.c0 >> 4) & 1;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) ((float2*)xs)[wh_xs_f4(g, l) * 2 + h] = make_float2(q[l], q[8 + l]);
+}
+
+__device__ __forceinline__ float wh_dpp_row_shl8(float v) {  // lane i <- lane i+8 (within 16)
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x108, 0xf, 0xf, false));
+}
+
+// Gate/up: grid (n_experts * inter / 16, n_tokens), 256 threads = 32 rows =
+// 16 hidden rows x {w1, w3}; octet 2r runs w1 row r, octet 2r+1 the w3 row r.
+// kBlk = hidden / 256 when the rows fit in registers, else 0.
+template <int kBlk>
+__global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
+    extern __shared__ __align__(16) float lds[];
+    const uint32_t tok = blockIdx.y;
+    const uint32_t per_e = a.inter >> 4;
+    const uint32_t e = blockIdx.x / per_e;
+    const uint32_t rb = blockIdx.x - e * per_e;  // 16-row block of the hidden
+    const uint32_t lane = threadIdx.x & 7, oct = threadIdx.x >> 3;
+    const uint32_t row = rb * 16 + (oct >> 1);
+    const bool up = oct & 1;
+    const uint32_t G = a.hidden >> 5;
+    const wh_expert_ptrs ep = a.ex[e];
+    const uint8_t* wrow = (up ? ep.w3 : ep.w1) + (size_t)row * (a.hidden >> 1);
+    const uint8_t* srow = (up ? ep.s3 : ep.s1) + (size_t)row * G;
+    float* xs = lds;
+    float* s8row = lds + wh_xs_floats(a.hidden) + oct * wh_s8_stride(G);
+    uint32_t* thr = (uint32_t*)(lds + wh_fp4_wg_lds(a.hidden) / sizeof(float));
+    const bool bf16 = a.x_is_bf16 != 0;
+    const void* xt = bf16 ? (const void*)((const uint16_t*)a.x + (size_t)tok * a.hidden)
+                          : (const void*)((const float*)a.x + (size_t)tok * a.hidden);
+    wh_thr_stage ts;
+    wh_thr_stage_load(ts);
+    float acc;
+    if constexpr (kBlk > 0) {
+        // staging loads first, then the weight row; the staging waits below
+        // therefore never wait for weight bytes
+        wh_xq_stage xst;
+        wh_xq_stage_load(xst, xt, bf16, a.hidden, threadIdx.x);
+        wh_s8_stage<kBlk> ss;
+        wh_s8_stage_load<kBlk>(ss, srow, lane);
+        wh_fp4_lane_row<kBlk> r;
+        wh_fp4_lane_row_load<kBlk>(r, wrow, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        wh_thr_stage_store(ts, thr);
+        __syncthreads();
+        wh_xq_stage_store(xst, bf16, xs, thr, a.status);
+        wh_s8_stage_store<kBlk>(ss, s8row, lane);
+        __syncthreads();
+        acc = wh_fp4_lane_row_dot<kBlk>(r, xs, s8row, lane);
+    } else {
+        wh_thr_stage_store(ts, thr);
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < (a.hidden >> 4); i += 256) {
+            wh_xq_stage xst;
+            wh_xq_stage_load(xst, xt, bf16, a.hidden, i);
+            wh_xq_stage_store(xst, bf16, xs, thr, a.status);
+        }
+        wh_s8_stage_rt(srow, G, s8row, lane);
+        __syncthreads();
+        acc = wh_fp4_lane_dot_rt(wrow, G >> 3, xs, s8row, lane);
+    }
+    const float v = wh_hsum8(acc) + 0.0f;
+    const float u = wh_dpp_row_shl8(v);  // lane 16k <- lane 16k + 8: the w3 row
+    if ((threadIdx.x & 15) == 0) {
+        if (!(fabsf(v) <= 3.4028235e38f) || !(fabsf(u) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
+        a.h[((size_t)tok * a.n_experts + e) * a.inter + row] = wh_swiglu(v, u, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
     }
 }
 
-// Down projection + ordered routed sum.  Grid: (hidden/32, n_experts,
-// n_tokens); 128 threads = 32 quads = 32 rows.  The last expert to finish a
-// 32-row block combines all experts in route order (E/compute.rs:1948-2012).
-template <int kChunks>
-__global__ void __launch_bounds__(128) k_moe_down(wh_moe_args a) {
-    extern __shared__ __align__(16) float xs[];
-    __shared__ uint32_t last;
-    const uint32_t e = blockIdx.y, tok = blockIdx.z;
-    const wh_expert_ptrs ep = a.ex[e];
-    const size_t hbase = ((size_t)tok * a.n_experts + e) * a.inter;
-    const uint32_t t = threadIdx.x & 3;
-    const uint32_t row = blockIdx.x * 32 + (threadIdx.x >> 2);
-    const uint8_t* wrow = ep.w2 + (size_t)row * (a.inter / 2);
-    const uint8_t* srow = ep.s2 + (size_t)row * (a.inter / 32);
-    float acc_a, acc_b;
-    if constexpr (kChunks > 0) {
-        wh_stage_codes st;
-        wh_stage_codes_load(st, a.hq_codes + hbase, a.hq_scales + hbase / 64, a.inter, threadIdx.x);
-        wh_fp4_rowbuf<kChunks> b;
-        wh_fp4_rowbuf_load<kChunks>(b, wrow, srow, t);
-        __builtin_amdgcn_sched_barrier(0);
-        wh_stage_codes_store(st, xs);
-        __syncthreads();
-        wh_fp4_rowbuf_dot<kChunks>(b, xs, t, acc_a, acc_b);
+// Act-quant (block 64) of the hidden while staging it: thread t takes the 8
+// values [8t, 8t+8), so 8 consecutive threads hold one 64-block; the result
+// goes to LDS in FP4 lane order.  Loaded early, stored after the weight
+// loads are issued.
+struct wh_h_stage {
+    float4 p, q;
+    uint32_t t;
+    bool on;
+};
+__device__ __forceinline__ void wh_h_stage_load(wh_h_stage& st, const float* __restrict__ h, uint32_t n, uint32_t t) {
+    st.t = t;
+    st.on = t < n / 8;
+    if (st.on) {
+        st.p = ((const float4*)h)[2 * t];
+        st.q = ((const float4*)h)[2 * t + 1];
     } else {
-        wh_stage_codes_all(xs, a.hq_codes + hbase, a.hq_scales + hbase / 64, a.inter);
-        __syncthreads();
-        wh_fp4_quad_dot_rt(wrow, srow, a.inter >> 7, t, xs, acc_a, acc_b);
+        st.p = st.q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    float yv = wh_quad_hsum(acc_a, acc_b) + 0.0f;
-    const size_t ybase = ((size_t)tok * a.n_experts + e) * a.hidden;
-    if (t == 0) {
+}
+__device__ __forceinline__ void wh_h_stage_store(const wh_h_stage& st, float* xs, const uint32_t* log2_thr) {
+    const float v[8] = {st.p.x, st.p.y, st.p.z, st.p.w, st.q.x, st.q.y, st.q.z, st.q.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, wh_dpp_quad_swap1(amax));
+    amax = fmaxf(amax, wh_dpp_quad_swap2(amax));
+    const float lo = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x104, 0xf, 0xf, false));
+    const float hi = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x114, 0xf, 0xf, false));
+    amax = fmaxf(amax, (threadIdx.x & 4) ? hi : lo);  // the other quad of the 64-block
+    if (!st.on) return;
+    if (!(amax <= 3.4028235e38f)) amax = 1.0f;        // non-finite rows already reported
+    const int k = wh_aq_scale_exp(amax, log2_thr);
+    const float inv = wh_pow2f(-k), sc = wh_pow2f(k);
+    const uint32_t g = st.t >> 2, kk = st.t & 3;  // columns 32g + 8kk + j: lane j, slot kk
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xs[wh_xs_f4(g, j) * 4 + kk] = wh_e4m3_round(wh_clamp448(v[j] * inv)) * sc;
+}
+
+// Down + ordered routed sum: grid (n_experts * hidden / 32, n_tokens), 256
+// threads = 32 output rows of one expert.  The last expert to finish a
+// 32-row slice sums all experts in route order (E/compute.rs:1948-2012).
+template <int kBlk>
+__global__ void __launch_bounds__(256) k_moe_down(wh_moe_args a) {
+    extern __shared__ __align__(16) float lds[];
+    __shared__ uint32_t last;
+    const uint32_t tok = blockIdx.y;
+    const uint32_t per_e = a.hidden >> 5;
+    const uint32_t e = blockIdx.x / per_e;
+    const uint32_t rb = blockIdx.x - e * per_e;  // 32-row slice of the output
+    const uint32_t lane = threadIdx.x & 7, oct = threadIdx.x >> 3;
+    const uint32_t row = rb * 32 + oct;
+    const uint32_t G = a.inter >> 5;
+    const wh_expert_ptrs ep = a.ex[e];
+    const uint8_t* wrow = ep.w2 + (size_t)row * (a.inter >> 1);
+    const uint8_t* srow = ep.s2 + (size_t)row * G;
+    float* xs = lds;
+    float* s8row = lds + wh_xs_floats(a.inter) + oct * wh_s8_stride(G);
+    uint32_t* thr = (uint32_t*)(lds + wh_fp4_wg_lds(a.inter) / sizeof(float));
+    const float* hrow = a.h + ((size_t)tok * a.n_experts + e) * a.inter;
+    wh_thr_stage ts;
+    wh_thr_stage_load(ts);
+    float acc;
+    if constexpr (kBlk > 0) {
+        wh_h_stage hst;
+        wh_h_stage_load(hst, hrow, a.inter, threadIdx.x);  // inter == 2048: one pass
+        wh_s8_stage<kBlk> ss;
+        wh_s8_stage_load<kBlk>(ss, srow, lane);
+        wh_fp4_lane_row<kBlk> r;
+        wh_fp4_lane_row_load<kBlk>(r, wrow, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        wh_thr_stage_store(ts, thr);
+        __syncthreads();
+        wh_h_stage_store(hst, xs, thr);
+        wh_s8_stage_store<kBlk>(ss, s8row, lane);
+        __syncthreads();
+        acc = wh_fp4_lane_row_dot<kBlk>(r, xs, s8row, lane);
+    } else {
+        wh_thr_stage_store(ts, thr);
+        __syncthreads();
+        for (uint32_t t = threadIdx.x; t < a.inter / 8; t += 256) {
+            wh_h_stage hst;
+            wh_h_stage_load(hst, hrow, a.inter, t);
+            wh_h_stage_store(hst, xs, thr);
+        }
+        wh_s8_stage_rt(srow, G, s8row, lane);
+        __syncthreads();
+        acc = wh_fp4_lane_dot_rt(wrow, G >> 3, xs, s8row, lane);
+    }
+    const float yv = wh_hsum8(acc) + 0.0f;
+    const size_t yb = ((size_t)tok * a.n_experts + e) * a.hidden;
+    if (lane == 0) {
         if (!(fabsf(yv) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
-        wh_store_coherent(a.y + ybase + row, yv);
+        wh_store_coherent(a.y + yb + row, yv);
     }
     wh_stores_done();
     __syncthreads();
-    uint32_t* cnt = a.cnt_y + (size_t)tok * (a.hidden / 32) + blockIdx.x;
+    uint32_t* cnt = a.cnt_y + (size_t)tok * (a.hidden >> 5) + rb;
     if (threadIdx.x == 0) last = wh_arrive(cnt) == a.n_experts - 1;
     __syncthreads();
     if (!last || threadIdx.x >= 32) return;
-    const uint32_t r = blockIdx.x * 32 + threadIdx.x;
+    const uint32_t r_out = rb * 32 + threadIdx.x;
     const size_t t0 = (size_t)tok * a.n_experts * a.hidden;
     float o;
     if (a.n_experts == 1) {
-        o = wh_load_coherent(a.y + t0 + r);
+        o = wh_load_coherent(a.y + t0 + r_out);
     } else {
         // valid_route_weight_sum (E/compute.rs:2014-2030)
         float sum = 0.0f;
@@ -788,16 +977,16 @@ __global__ void __launch_bounds__(128) k_moe_down(wh_moe_args a) {
             sum = sum + w;
         }
         if (sum <= 1.1920929e-07f) valid = false;
-        float uniform = 1.0f / (float)a.n_experts;
+        const float uniform = 1.0f / (float)a.n_experts;
         o = 0.0f;
         for (uint32_t i = 0; i < a.n_experts; ++i) {
             float w = valid ? a.route_w[i] / sum : uniform;
-            float p = wh_load_coherent(a.y + t0 + (size_t)i * a.hidden + r) * w;
+            float p = wh_load_coherent(a.y + t0 + (size_t)i * a.hidden + r_out) * w;
             o = o + p;
         }
     }
-    a.out[(size_t)tok * a.hidden + r] = o;
-    if (threadIdx.x == 0) *cnt = 0u;
+    a.out[(size_t)tok * a.hidden + r_out] = o;
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Bit-exact dequant of a resident FP4 tensor back to reference values
@@ -806,24 +995,24 @@ __global__ void __launch_bounds__(128) k_moe_down(wh_moe_args a) {
 __global__ void __launch_bounds__(256) k_fp4_dequant(const uint8_t* __restrict__ w,
                                                      const uint8_t* __restrict__ s, uint32_t rows,
                                                      uint32_t cols, float* __restrict__ out) {
-    // one thread per (row, chunk, quad thread): 4 groups x 8 values
+    // one thread per (row, block, lane): 8 groups x 4 values
     const size_t id = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const uint32_t chunks = cols >> 7, G = cols >> 5;
-    if (id >= (size_t)rows * chunks * 4) return;
-    const uint32_t t = id & 3, j = (id >> 2) % chunks;
-    const size_t row = (id >> 2) / chunks;
-    uint4 wv = ((const uint4*)(w + row * (cols / 2)))[4 * j + t];
-    uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-    for (uint32_t i = 0; i < 4; ++i) {
-        const uint32_t g = 4 * j + i;
-        wh_fp4x8 v = wh_fp4_decode8(words[i]);
-        float va[4] = {v.a01.x, v.a01.y, v.a23.x, v.a23.y};
-        float vb[4] = {v.b01.x, v.b01.y, v.b23.x, v.b23.y};
-        float sc = wh_ue8m0(s[row * G + (g & 3) * (G / 4) + (g >> 2)]);
+    const uint32_t blocks = cols >> 8, G = cols >> 5;
+    if (id >= (size_t)rows * blocks * 8) return;
+    const uint32_t lane = id & 7, b = (id >> 3) % blocks;
+    const size_t row = (id >> 3) / blocks;
+    const uint4 wv = ((const uint4*)(w + row * (cols / 2)))[8 * b + lane];
+    const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+    for (uint32_t d = 0; d < 4; ++d) {
+        const wh_fp4x8 v = wh_fp4_decode8(words[d]);
+        const float va[4] = {v.a01.x, v.a01.y, v.a23.x, v.a23.y};
+        const float vb[4] = {v.b01.x, v.b01.y, v.b23.x, v.b23.y};
+        const uint32_t ga = 8 * b + 2 * d;
+        const float sa = wh_ue8m0(s[row * G + ga]), sb = wh_ue8m0(s[row * G + ga + 1]);
         for (uint32_t k = 0; k < 4; ++k) {
-            float a8 = va[k] * 0.125f, b8 = vb[k] * 0.125f;
-            out[row * cols + g * 32 + t + 8 * k] = a8 == 0.0f ? 0.0f : a8 * sc;
-            out[row * cols + g * 32 + t + 4 + 8 * k] = b8 == 0.0f ? 0.0f : b8 * sc;
+            const float a8 = va[k] * 0.125f, b8 = vb[k] * 0.125f;
+            out[row * cols + ga * 32 + lane + 8 * k] = a8 == 0.0f ? 0.0f : a8 * sa;
+            out[row * cols + (ga + 1) * 32 + lane + 8 * k] = b8 == 0.0f ? 0.0f : b8 * sb;
         }
     }
 }

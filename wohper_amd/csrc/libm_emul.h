@@ -146,3 +146,23 @@ WH_HD int wh_ceil_log2f(float r, const uint32_t* thr) {
 
 // 2^k as float for -126 <= k <= 127 (exp2f of an integral float is exact there).
 WH_HD float wh_pow2f(int k) { return wh_bits_to_float((uint32_t)(k + 127) << 23); }
+
+// Nearest E4M3 value to t in [-448, 448] (the act-quant grid, E/compute.rs:
+// 2537-2545): ties go to the lower value (toward -inf) and a zero result is
+// +0.  For |t| >= 2^-6 the grid has 3 mantissa bits at t's own exponent, so
+// rounding is an integer add on the f32 bits: 0x7ffff below the dropped
+// half for positive t (ties stay low), 0x80000 for negative t (ties move the
+// magnitude up, i.e. toward -inf).  Below 2^-6 the grid is m * 2^-9.  The
+// generator checks this against a brute-force nearest over every float in
+// [-448, 448].
+WH_HD float wh_e4m3_round(float t) {
+    const uint32_t b = wh_float_to_bits(t);
+    const uint32_t s = b & 0x80000000u, a = b & 0x7fffffffu;
+    if (a >= 0x3c800000u) return wh_bits_to_float(((a + 0x7ffffu + (s >> 31)) & 0xfff00000u) | s);
+    const float r = wh_bits_to_float(a) * 512.0f;  // exact
+    const float n = floorf(r);
+    const float f = r - n;  // exact
+    const float m = (f > 0.5f || (f == 0.5f && s)) ? n + 1.0f : n;
+    if (m == 0.0f) return 0.0f;
+    return wh_bits_to_float(wh_float_to_bits(m * 0.001953125f) | s);
+}

@@ -43,7 +43,7 @@ __device__ __forceinline__ float wh_fp8_exact(uint32_t b) {
 }
 
 // ---------------------------------------------------------------- FP4 codes
-// Resident FP4 encoding (written by the store, see store.cpp): one dword
+// Resident FP4 encoding (written by fp4_encode_row and k_synth_fp4): one dword
 // holds the 8 elements that one lane consumes from two consecutive 32-col
 // groups, byte k = [sB_k | mB_k(3) | sA_(k-1 mod 4) | mA_k(3)], where A_k / B_k
 // are column l + 8k of the first / second group and m/s are the E2M1
@@ -116,38 +116,6 @@ __device__ __forceinline__ float wh_wave_max(float v) {
 }
 
 // ------------------------------------------------------------ act-quant
-// Nearest E4M3 value of t in [-448, 448], ties toward the lower value, +0
-// for a zero result (E/compute.rs:2537-2545 over the sorted LUT of
-// E/compute.rs:2524-2535).  Returns the E4M3 code; *val gets the value.
-__device__ __forceinline__ uint32_t wh_e4m3_nearest(float t, float* val) {
-    uint32_t tb = __float_as_uint(t);
-    uint32_t neg = tb >> 31;
-    float a = __uint_as_float(tb & 0x7fffffffu);
-    // spacing: 2^-9 below 2^-6, else 2^(e-3)
-    int e = (int)((__float_as_uint(a) >> 23) & 0xff) - 127;
-    int se = e < -6 ? -9 : e - 3;
-    float q = a * wh_pow2f(-se);  // exact
-    float n = floorf(q);
-    float frac = q - n;           // exact
-    if (frac > 0.5f || (frac == 0.5f && neg)) n += 1.0f;
-    float mag = n * wh_pow2f(se);
-    uint32_t code;
-    if (n == 0.0f) {
-        *val = 0.0f;
-        return 0u;
-    }
-    // encode magnitude: value = n * 2^se, n in [1, 16]
-    uint32_t mb = __float_as_uint(mag);
-    int me = (int)((mb >> 23) & 0xff) - 127;
-    if (me < -6) {
-        code = (uint32_t)n;  // subnormal: n * 2^-9 with n in 1..7
-    } else {
-        code = ((uint32_t)(me + 7) << 3) | ((mb >> 20) & 7u);
-    }
-    *val = neg ? -mag : mag;
-    return code | (neg << 7);
-}
-
 // Block scale of act-quant: exp2f(ceilf(log2f(max(amax,1e-4)/448)))
 __device__ __forceinline__ int wh_aq_scale_exp(float amax, const uint32_t* log2_thr) {
     amax = fmaxf(amax, 1.0e-4f);

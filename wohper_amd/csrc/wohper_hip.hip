@@ -130,13 +130,10 @@ struct wh_ctx {
     size_t device_bytes = 0;
     uint32_t* status = nullptr;  // device status word
     uint32_t* status_host = nullptr;
-    Scratch x_in, y_out, xq_codes, xq_scales, h, hq_codes, hq_scales, ybuf, cnt_h, cnt_y, tmp;
+    Scratch x_in, y_out, h, ybuf, cnt_y, tmp;
     HostBuf stage_in, stage_out;
     std::mutex mu;
-    // optional per-kernel timing of the routed-expert pipeline (off by default)
-    bool prof = false;
-    std::vector<hipEvent_t> prof_ev;   // 4 events per recorded step
-    size_t prof_steps = 0, prof_cap = 0;
+    hipEvent_t timer[2] = {nullptr, nullptr};  // wh_timer_start / wh_timer_stop
 };
 
 namespace {
@@ -208,30 +205,30 @@ void fp8_permute_row(const uint8_t* src, uint8_t* dst, size_t cols) {
     }
 }
 
-// FP4 resident encoding of one row (layout described in kernels.h): the
-// weights of each 4-group chunk re-ordered per quad thread, and the row's
-// UE8M0 bytes grouped by owning quad thread.
+// FP4 resident encoding of one row (layout described with the FP4 kernels
+// in kernels.h): per 256-column block, lane l's 16 bytes hold its values of
+// the block's 8 groups, two groups per dword.  Scales keep their order.
 void fp4_encode_row(const uint8_t* src, const uint8_t* ssrc, uint8_t* dst, uint8_t* sdst, size_t cols) {
     auto nib = [src](size_t col) -> uint32_t {
         uint8_t b = src[col >> 1];
         return (col & 1) ? (b >> 4) : (b & 15);
     };
-    const size_t chunks = cols / 128, G = cols / 32;
-    for (size_t j = 0; j < chunks; ++j) {
-        for (uint32_t t = 0; t < 4; ++t) {
-            for (uint32_t i = 0; i < 4; ++i) {
-                size_t g = 4 * j + i;
+    const size_t blocks = cols / 256;
+    for (size_t blk = 0; blk < blocks; ++blk) {
+        for (uint32_t l = 0; l < 8; ++l) {
+            for (uint32_t d = 0; d < 4; ++d) {
+                const size_t g = 8 * blk + 2 * d;
                 uint32_t a[4], b[4];
                 for (uint32_t k = 0; k < 4; ++k) {
-                    a[k] = nib(32 * g + t + 8 * k);
-                    b[k] = nib(32 * g + t + 4 + 8 * k);
+                    a[k] = nib(32 * g + l + 8 * k);
+                    b[k] = nib(32 * (g + 1) + l + 8 * k);
                 }
                 uint32_t word = wh_fp4_encode_word(a, b);
-                std::memcpy(dst + (4 * j + t) * 16 + 4 * i, &word, 4);
+                std::memcpy(dst + blk * 128 + l * 16 + 4 * d, &word, 4);
             }
         }
     }
-    for (size_t g = 0; g < G; ++g) sdst[(g & 3) * (G / 4) + (g >> 2)] = ssrc[g];
+    std::memcpy(sdst, ssrc, cols / 32);
 }
 
 // Dynamic LDS a workgroup may use: the device's per-block limit (160 KB on
@@ -251,17 +248,22 @@ hipError_t kernel_setup_once(int device) {
             hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
             if (r != hipSuccess && e == hipSuccess) e = r;
         };
+        for (const void* f : {(const void*)k_fp8_gemv_sk<false, false, 4>, (const void*)k_fp8_gemv_sk<false, true, 4>,
+                              (const void*)k_fp8_gemv_sk<true, false, 4>, (const void*)k_fp8_gemv_sk<true, true, 4>,
+                              (const void*)k_fp8_gemv_sk<false, false, 0>, (const void*)k_fp8_gemv_sk<false, true, 0>,
+                              (const void*)k_fp8_gemv_sk<true, false, 0>, (const void*)k_fp8_gemv_sk<true, true, 0>})
+            set(f);
         set((const void*)k_fp8_gemv<false, false>);
         set((const void*)k_fp8_gemv<false, true>);
         set((const void*)k_fp8_gemv<true, false>);
         set((const void*)k_fp8_gemv<true, true>);
         set((const void*)k_fp4_matvec<0>);
+        set((const void*)k_fp4_matvec<8>);
         set((const void*)k_fp4_matvec<16>);
-        set((const void*)k_fp4_matvec<32>);
         set((const void*)k_moe_gateup<0>);
-        set((const void*)k_moe_gateup<32>);
+        set((const void*)k_moe_gateup<16>);
         set((const void*)k_moe_down<0>);
-        set((const void*)k_moe_down<16>);
+        set((const void*)k_moe_down<8>);
         if (e == hipSuccess) {
             g_max_lds = (size_t)lds;
         } else {
@@ -273,6 +275,10 @@ hipError_t kernel_setup_once(int device) {
 }
 
 // ------------------------------------------------------------ FP8 launch
+// LDS of a split-K FP8 workgroup: staged x, the 4 x 8 x groups partial sums
+// and the 4 rows' group scales.
+size_t fp8_sk_lds(size_t cols) { return sizeof(float) * (cols + 36 * (cols / 128)); }
+
 int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x, float* y,
                size_t n_batch, size_t x_stride, size_t y_stride) {
     wh_fp8_args a;
@@ -289,7 +295,24 @@ int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x,
     a.x_stride = (uint32_t)x_stride;
     a.y_stride = (uint32_t)y_stride;
     bool u8 = t.scale_fmt == WH_SCALE_UE8M0;
-    if (t.fast) {
+    if (t.fast && (t.cols / 128) % 8 == 0 && fp8_sk_lds(t.cols) <= g_max_lds) {
+        dim3 grid((unsigned)((r1 - r0 + 3) / 4), (unsigned)n_batch);
+        const size_t lds = fp8_sk_lds(t.cols);
+        const bool g4 = t.cols == 4096;
+#define WH_SK(SP, U8)                                                                             \
+    do {                                                                                          \
+        if (g4) k_fp8_gemv_sk<SP, U8, 4><<<grid, 256, lds, c->stream>>>(a);                      \
+        else k_fp8_gemv_sk<SP, U8, 0><<<grid, 256, lds, c->stream>>>(a);                         \
+    } while (0)
+        if (t.special) {
+            if (u8) WH_SK(true, true);
+            else WH_SK(true, false);
+        } else {
+            if (u8) WH_SK(false, true);
+            else WH_SK(false, false);
+        }
+#undef WH_SK
+    } else if (t.fast) {
         dim3 grid((unsigned)((r1 - r0 + 31) / 32), (unsigned)n_batch);
         size_t lds = t.cols * sizeof(float);
         if (t.special) {
@@ -319,10 +342,10 @@ int launch_fp4(wh_ctx* c, const Tensor& t, const float* x, float* y) {
     a.rows = (uint32_t)t.rows;
     a.cols = (uint32_t)t.cols;
     if (t.fast) {
-        dim3 grid((unsigned)((t.rows + 63) / 64));
-        size_t lds = t.cols * sizeof(float);
-        if (t.cols == 4096) k_fp4_matvec<32><<<grid, 256, lds, c->stream>>>(a);
-        else if (t.cols == 2048) k_fp4_matvec<16><<<grid, 256, lds, c->stream>>>(a);
+        dim3 grid((unsigned)((t.rows + 31) / 32));
+        size_t lds = wh_fp4_wg_lds(t.cols);
+        if (t.cols == 4096) k_fp4_matvec<16><<<grid, 256, lds, c->stream>>>(a);
+        else if (t.cols == 2048) k_fp4_matvec<8><<<grid, 256, lds, c->stream>>>(a);
         else k_fp4_matvec<0><<<grid, 256, lds, c->stream>>>(a);
     } else {
         k_fp4_matvec_generic<<<(unsigned)((t.rows + 63) / 64), 64, 0, c->stream>>>(a, (uint32_t)t.scale_cols);
@@ -378,8 +401,8 @@ int resolve_expert(wh_ctx* c, uint32_t layer, uint32_t expert, ExpertView* v) {
 }
 
 bool expert_fast(const ExpertView& v) {
-    return v.w1->fast && v.w3->fast && v.w2->fast && v.w1->cols % 512 == 0 &&
-           v.w1->rows % 512 == 0 && v.w1->rows * 4 <= g_max_lds && v.w1->cols * 4 <= g_max_lds;
+    return v.w1->fast && v.w3->fast && v.w2->fast && v.w1->cols % 256 == 0 && v.w1->rows % 256 == 0 &&
+           wh_moe_wg_lds(v.w1->cols) <= g_max_lds && wh_moe_wg_lds(v.w1->rows) <= g_max_lds;
 }
 
 // Routed experts for n_tokens rows of x (all with the same route list).
@@ -394,13 +417,9 @@ int moe_forward(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n,
         fast = fast && expert_fast(ev[i]);
     }
     if (fast && n <= WH_MAX_EXPERTS) {
-        WH_HIP(c->xq_codes.ensure(n_tokens * hidden, false));
-        WH_HIP(c->xq_scales.ensure(n_tokens * (hidden / 64) * sizeof(float), false));
+        if (((uintptr_t)x_dev & 15) || ((uintptr_t)out_dev & 3)) return WH_INVALID_ARGUMENT;
         WH_HIP(c->h.ensure(n_tokens * n * inter * sizeof(float), false));
-        WH_HIP(c->hq_codes.ensure(n_tokens * n * inter, false));
-        WH_HIP(c->hq_scales.ensure(n_tokens * n * (inter / 64) * sizeof(float), false));
         WH_HIP(c->ybuf.ensure(n_tokens * n * hidden * sizeof(float), false));
-        WH_HIP(c->cnt_h.ensure(n_tokens * n * (inter / 64) * sizeof(uint32_t), true));
         WH_HIP(c->cnt_y.ensure(n_tokens * (hidden / 32) * sizeof(uint32_t), true));
         wh_moe_args a;
         std::memset(&a, 0, sizeof a);
@@ -417,32 +436,19 @@ int moe_forward(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n,
         a.hidden = (uint32_t)hidden;
         a.inter = (uint32_t)inter;
         a.n_tokens = (uint32_t)n_tokens;
-        a.xq_codes = c->xq_codes.as<uint8_t>();
-        a.xq_scales = c->xq_scales.as<float>();
+        a.x = x_dev;
+        a.x_is_bf16 = x_bf16 ? 1u : 0u;
         a.h = c->h.as<float>();
-        a.hq_codes = c->hq_codes.as<uint8_t>();
-        a.hq_scales = c->hq_scales.as<float>();
         a.y = c->ybuf.as<float>();
         a.out = out_dev;
-        a.cnt_h = c->cnt_h.as<uint32_t>();
         a.cnt_y = c->cnt_y.as<uint32_t>();
         a.status = c->status;
-        unsigned aq_blocks = (unsigned)((n_tokens * hidden + 63) / 64);
-        hipEvent_t* ev = nullptr;
-        if (c->prof && c->prof_steps < c->prof_cap) ev = &c->prof_ev[4 * c->prof_steps++];
-        if (ev) WH_HIP(hipEventRecord(ev[0], c->stream));
-        k_act_quant_codes<<<aq_blocks, 64, 0, c->stream>>>(x_dev, x_bf16, (uint32_t)(n_tokens * hidden),
-                                                           c->xq_codes.as<uint8_t>(),
-                                                           c->xq_scales.as<float>(), c->status);
-        if (ev) WH_HIP(hipEventRecord(ev[1], c->stream));
-        dim3 ggrid((unsigned)(inter / 16), (unsigned)n, (unsigned)n_tokens);
-        if (hidden == 4096) k_moe_gateup<32><<<ggrid, 128, hidden * sizeof(float), c->stream>>>(a);
-        else k_moe_gateup<0><<<ggrid, 128, hidden * sizeof(float), c->stream>>>(a);
-        if (ev) WH_HIP(hipEventRecord(ev[2], c->stream));
-        dim3 dgrid((unsigned)(hidden / 32), (unsigned)n, (unsigned)n_tokens);
-        if (inter == 2048) k_moe_down<16><<<dgrid, 128, inter * sizeof(float), c->stream>>>(a);
-        else k_moe_down<0><<<dgrid, 128, inter * sizeof(float), c->stream>>>(a);
-        if (ev) WH_HIP(hipEventRecord(ev[3], c->stream));
+        dim3 ggrid((unsigned)(n * inter / 16), (unsigned)n_tokens);
+        if (hidden == 4096) k_moe_gateup<16><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
+        else k_moe_gateup<0><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
+        dim3 dgrid((unsigned)(n * hidden / 32), (unsigned)n_tokens);
+        if (inter == 2048) k_moe_down<8><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
+        else k_moe_down<0><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
         WH_HIP(hipGetLastError());
         return WH_OK;
     }
@@ -494,32 +500,30 @@ __host__ __device__ inline uint8_t wh_synth_byte(uint64_t seed, uint64_t stream,
 __global__ void k_synth_fp4(uint8_t* w, uint8_t* s, uint32_t rows, uint32_t cols, uint64_t seed,
                             uint64_t stream, uint32_t slo, uint32_t shi) {
     const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const uint32_t chunks = cols / 128, G = cols / 32;
-    const size_t words = (size_t)rows * chunks * 16;
+    const uint32_t blocks = cols / 256, G = cols / 32;
+    const size_t words = (size_t)rows * blocks * 32;
     if (id < words) {
-        const uint32_t i = id & 3, t = (id >> 2) & 3;
-        const size_t rj = id >> 4;
-        const uint32_t j = rj % chunks;
-        const size_t row = rj / chunks;
+        const uint32_t d = id & 3, l = (id >> 2) & 7;
+        const size_t rb = id >> 5;
+        const uint32_t blk = rb % blocks;
+        const size_t row = rb / blocks;
         const size_t rowbase = row * (cols / 2);
         auto nib = [&](size_t col) -> uint32_t {
             uint8_t b = wh_synth_byte(seed, stream, rowbase + (col >> 1));
             return (col & 1) ? (b >> 4) : (b & 15);
         };
-        const size_t g = (size_t)4 * j + i;
+        const size_t g = (size_t)8 * blk + 2 * d;
         uint32_t a[4], b[4];
         for (uint32_t k = 0; k < 4; ++k) {
-            a[k] = nib(32 * g + t + 8 * k);
-            b[k] = nib(32 * g + t + 4 + 8 * k);
+            a[k] = nib(32 * g + l + 8 * k);
+            b[k] = nib(32 * (g + 1) + l + 8 * k);
         }
-        ((uint32_t*)(w + rowbase + ((size_t)4 * j + t) * 16))[i] = wh_fp4_encode_word(a, b);
+        ((uint32_t*)(w + rowbase + (size_t)blk * 128 + l * 16))[d] = wh_fp4_encode_word(a, b);
     }
     const size_t nscale = (size_t)rows * G;
     if (id < nscale) {
-        const size_t row = id / G;
-        const uint32_t g = id % G;
         uint32_t span = shi - slo + 1;
-        s[row * G + (g & 3) * (G / 4) + (g >> 2)] = (uint8_t)(slo + wh_synth_byte(seed, stream ^ 0x5ca1e5ull, id) % span);
+        s[id] = (uint8_t)(slo + wh_synth_byte(seed, stream ^ 0x5ca1e5ull, id) % span);
     }
 }
 
@@ -580,6 +584,8 @@ int wh_init(int device, wh_ctx** out) {
     if (e == hipSuccess) e = hipMalloc(&c->status, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c->status, 0, sizeof(uint32_t));
     if (e == hipSuccess) e = hipHostMalloc((void**)&c->status_host, sizeof(uint32_t), hipHostMallocDefault);
+    if (e == hipSuccess) e = hipEventCreate(&c->timer[0]);
+    if (e == hipSuccess) e = hipEventCreate(&c->timer[1]);
     if (e != hipSuccess) {
         delete c;
         return hip_status(e);
@@ -593,12 +599,12 @@ int wh_shutdown(wh_ctx* c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     c->arena.release_all();
-    for (Scratch* s : {&c->x_in, &c->y_out, &c->xq_codes, &c->xq_scales, &c->h, &c->hq_codes,
-                       &c->hq_scales, &c->ybuf, &c->cnt_h, &c->cnt_y, &c->tmp})
+    for (Scratch* s : {&c->x_in, &c->y_out, &c->h, &c->ybuf, &c->cnt_y, &c->tmp})
         if (s->p) (void)hipFree(s->p);
     for (HostBuf* h : {&c->stage_in, &c->stage_out})
         if (h->p) (void)hipHostFree(h->p);
-    for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
+    for (hipEvent_t e : c->timer)
+        if (e) (void)hipEventDestroy(e);
     (void)hipFree(c->status);
     (void)hipHostFree(c->status_host);
     (void)hipStreamDestroy(c->stream);
@@ -680,7 +686,7 @@ int wh_store_fp4(wh_ctx* c, const uint8_t* packed, size_t packed_len, const uint
     t.cols = cols;
     t.scale_rows = rows;
     t.scale_cols = scale_cols;
-    t.fast = (cols / scale_cols == 32) && cols % 512 == 0 && cols * 4 <= g_max_lds;
+    t.fast = (cols / scale_cols == 32) && cols % 256 == 0 && wh_fp4_wg_lds(cols) <= g_max_lds;
     t.bytes = rows * row_bytes + rows * scale_cols;
     void* wd = nullptr;
     void* sd = nullptr;
@@ -733,7 +739,7 @@ void wh_synth_fp4_host(uint64_t seed, uint64_t stream, uint8_t* packed, size_t p
 int wh_store_expert_synthetic(wh_ctx* c, uint32_t layer, uint32_t expert, size_t hidden,
                               size_t inter, uint64_t seed, uint32_t slo, uint32_t shi) {
     if (!c || slo > shi || shi > 255) return WH_INVALID_ARGUMENT;
-    if (hidden % 512 || inter % 512 || hidden == 0 || inter == 0) return WH_INVALID_SHAPE;
+    if (hidden % 256 || inter % 256 || hidden == 0 || inter == 0) return WH_INVALID_SHAPE;
     std::lock_guard<std::mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     wh_tensor ids[3];
@@ -754,7 +760,7 @@ int wh_store_expert_synthetic(wh_ctx* c, uint32_t layer, uint32_t expert, size_t
         t.w = (uint8_t*)wd;
         t.s = sd;
         uint64_t stream = ((uint64_t)layer << 40) ^ ((uint64_t)expert << 8) ^ (uint64_t)m;
-        size_t words = t.rows * (t.cols / 128) * 16;
+        size_t words = t.rows * (t.cols / 256) * 32;
         size_t work = std::max(words, t.rows * t.scale_cols);
         k_synth_fp4<<<(unsigned)((work + 255) / 256), 256, 0, c->stream>>>(
             t.w, (uint8_t*)t.s, (uint32_t)t.rows, (uint32_t)t.cols, seed, stream, slo, shi);
@@ -797,7 +803,7 @@ int wh_tensor_dequant(wh_ctx* c, wh_tensor th, float* out, size_t out_len) {
     WH_HIP(c->y_out.ensure(n * sizeof(float), false));
     float* d = c->y_out.as<float>();
     if (t->kind == kFp4) {
-        size_t th_n = t->rows * (t->cols / 128) * 4;
+        size_t th_n = t->rows * (t->cols / 256) * 8;
         k_fp4_dequant<<<(unsigned)((th_n + 255) / 256), 256, 0, c->stream>>>(
             t->w, (const uint8_t*)t->s, (uint32_t)t->rows, (uint32_t)t->cols, d);
     } else {
@@ -949,6 +955,7 @@ int wh_routed_experts_async(wh_ctx* c, const wh_expert_route* routes, size_t n, 
                             int x_bf16, size_t n_tokens, float* out_dev) {
     if (!c || !routes || !x_dev || !out_dev || n == 0 || n_tokens == 0) return WH_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
     ExpertView ev[WH_MAX_EXPERTS];
     float wts[WH_MAX_EXPERTS];
     WH_TRY(routed_common(c, routes, n, ev, wts));
@@ -1014,38 +1021,23 @@ int wh_memcpy(wh_ctx* c, void* dst, const void* src, size_t bytes, int kind) {
     return WH_OK;
 }
 
-int wh_profile_enable(wh_ctx* c, size_t max_steps) {
+int wh_timer_start(wh_ctx* c) {
     if (!c) return WH_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
-    WH_HIP(hipStreamSynchronize(c->stream));
-    for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
-    c->prof_ev.clear();
-    c->prof_steps = 0;
-    c->prof_cap = max_steps;
-    c->prof = max_steps > 0;
-    for (size_t i = 0; i < 4 * max_steps; ++i) {
-        hipEvent_t e;
-        WH_HIP(hipEventCreate(&e));
-        c->prof_ev.push_back(e);
-    }
+    WH_HIP(hipEventRecord(c->timer[0], c->stream));
     return WH_OK;
 }
 
-int wh_profile_read(wh_ctx* c, double* avg_us, size_t* steps) {
-    if (!c || !avg_us) return WH_INVALID_ARGUMENT;
+int wh_timer_stop(wh_ctx* c, double* elapsed_us) {
+    if (!c || !elapsed_us) return WH_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lk(c->mu);
-    WH_HIP(hipStreamSynchronize(c->stream));
-    double acc[3] = {0, 0, 0};
-    for (size_t s = 0; s < c->prof_steps; ++s) {
-        for (int k = 0; k < 3; ++k) {
-            float ms = 0.f;
-            WH_HIP(hipEventElapsedTime(&ms, c->prof_ev[4 * s + k], c->prof_ev[4 * s + k + 1]));
-            acc[k] += ms * 1000.0;
-        }
-    }
-    for (int k = 0; k < 3; ++k) avg_us[k] = c->prof_steps ? acc[k] / (double)c->prof_steps : 0.0;
-    if (steps) *steps = c->prof_steps;
+    WH_HIP(hipSetDevice(c->device));
+    WH_HIP(hipEventRecord(c->timer[1], c->stream));
+    WH_HIP(hipEventSynchronize(c->timer[1]));
+    float ms = 0.0f;
+    WH_HIP(hipEventElapsedTime(&ms, c->timer[0], c->timer[1]));
+    *elapsed_us = (double)ms * 1000.0;
     return WH_OK;
 }
 
