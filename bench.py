@@ -32,9 +32,14 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 EXPERT_BYTES = 13_369_344             # 3 x (4 MiB packed + 256 KiB UE8M0)
 TOKEN_BYTES = 6 * EXPERT_BYTES + 4096 * 2 + 4096 * 4   # + bf16 x + f32 y = 80,240,640
-# HBM bytes per k_moe_token launch from rocprofv3 FETCH_SIZE/WRITE_SIZE, scaled
-# by the same counters on a plain copy kernel (None until measured)
-TRAFFIC_BYTES = None
+# algorithmic bytes per launch of the two routed-expert kernels: weights and
+# scales once, plus the vectors each kernel must read and write
+GATEUP_BYTES = 6 * 2 * (4_194_304 + 262_144) + 4096 * 2 + 6 * 2048 * 4     # 53,534,720
+DOWN_BYTES = 6 * (4_194_304 + 262_144) + 6 * 2048 * 4 + 4096 * 4           # 26,804,224
+# HBM bytes per k_moe_gateup<16> launch: rocprofv3 FETCH_SIZE 26,319 KiB and
+# WRITE_SIZE 48 KiB per dispatch, scaled by what the same counters read for a
+# 268,435,456-byte copy (FETCH x2.00, WRITE x1.00); see profiles/
+GATEUP_TRAFFIC_BYTES = (26_319 * 2 + 48) * 1024
 FP8_BYTES = 4096 * 4096 + 32 * 32 * 4 + 4096 * 4 + 4096 * 4
 
 
@@ -169,12 +174,23 @@ def main():
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed / args.steps * 1e3
     value = args.steps * TOKEN_BYTES / elapsed / 1e9
-    launch_us = dev_us / args.steps  # one k_moe_token launch per step
-    kern_gbs = TOKEN_BYTES / (launch_us * 1e-6) / 1e9
+    launch_us = dev_us / args.steps  # k_moe_gateup + k_moe_down per step
     log(f"routed FP4 MoE: {ms_per_step * 1e3:.2f} us/token wall, {value:.1f} GB/s; "
-        f"device {launch_us:.2f} us/launch, {kern_gbs:.1f} GB/s")
+        f"device {launch_us:.2f} us/token, {TOKEN_BYTES / (launch_us * 1e-6) / 1e9:.1f} GB/s")
 
-    extra = {}
+    # per-kernel launch durations: each stage launched back to back over the
+    # timed steps' route lists, between HIP events on the library stream
+    gu_us, dn_us = ctx.profile_routed(routes[args.warmup:args.warmup + min(args.steps, 64)], x_dev, True, out_dev,
+                                      max(200, args.steps))
+    gu_gbs = GATEUP_BYTES / (gu_us * 1e-6) / 1e9
+    dn_gbs = DOWN_BYTES / (dn_us * 1e-6) / 1e9
+    log(f"kernels: k_moe_gateup {gu_us:.2f} us ({gu_gbs:.0f} GB/s), k_moe_down {dn_us:.2f} us ({dn_gbs:.0f} GB/s)")
+
+    extra = {"kernels": {"k_moe_gateup<16>": {"us": round(gu_us, 3), "GBps": round(gu_gbs, 1),
+                                              "bytes_per_launch": GATEUP_BYTES},
+                         "k_moe_down<8>": {"us": round(dn_us, 3), "GBps": round(dn_gbs, 1),
+                                           "bytes_per_launch": DOWN_BYTES},
+                         "token_device_us": round(launch_us, 3)}}
     if not args.no_fp8:
         extra["fp8_dense_gemv"] = fp8_dense(ctx, max(200, args.steps), 40)
         log(f"fp8 dense: {extra['fp8_dense_gemv']}")
@@ -201,10 +217,10 @@ def main():
                    "global_batch": 1, "experts_resident": n_exp, "resident_GB": round(dev_bytes / 1e9, 2),
                    "bytes_per_step": TOKEN_BYTES, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_BYTES,
-                     "kernel": "k_moe_token<16,8>", "bytes_per_launch": TOKEN_BYTES,
-                     "avg_launch_us": round(launch_us, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
+                     "kernel": "k_moe_gateup<16>", "bytes_per_launch": GATEUP_BYTES,
+                     "avg_launch_us": round(gu_us, 3)},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -185,6 +185,19 @@ int wh_memcpy(wh_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
 int wh_timer_start(wh_ctx* ctx);
 int wh_timer_stop(wh_ctx* ctx, double* elapsed_us);
 
+/* Per-kernel timing of the routed-expert path, no counterpart in the
+ * reference (the engine's ZC_PROF timers, E/server/generation.rs:2344-2351,
+ * time whole passes on the CPU).  routes holds n_sets route lists of n_routes
+ * entries each; every list must resolve to experts on the fast path.  Each
+ * kernel stage (gate/up + SwiGLU, then down + routed sum) is launched iters
+ * times back to back, cycling through the lists so that the weights come
+ * from HBM, between two HIP events on the context stream.  us_per_launch[0]
+ * and [1] receive the mean microseconds per launch of the two stages.  The
+ * down stage reads whatever hidden vector the last gate/up launch left. */
+int wh_profile_routed(wh_ctx* ctx, const wh_expert_route* routes, size_t n_routes, size_t n_sets,
+                      const void* x_dev, int x_is_bf16, float* out_dev, size_t iters,
+                      double* us_per_launch);
+
 /* Test support, no counterpart in the reference: evaluates the device libm
  * emulation on n values.  fn 0: silu(x) = x / (1 + expf(-x)) for x <= 10;
  * fn 1: expf(x) for x >= -10; fn 2: the act-quant block scale

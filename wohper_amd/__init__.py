@@ -62,7 +62,7 @@ EXPORTED = (
     "wh_synth_fp4_host", "wh_store_release", "wh_store_usage", "wh_tensor_dequant",
     "wh_fp8_gemv", "wh_fp8_gemv_multi", "wh_fp4_matvec", "wh_fp4_expert_forward",
     "wh_act_quant_dequant", "wh_routed_experts", "wh_routed_experts_async", "wh_fp8_gemv_async",
-    "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop",
+    "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop", "wh_profile_routed",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
 )
 
@@ -128,6 +128,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_device_free": (c.c_int, [vp, vp]),
         "wh_memcpy": (c.c_int, [vp, vp, vp, sz, c.c_int]),
         "wh_timer_start": (c.c_int, [vp]),
+        "wh_profile_routed": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, sz, vp, c.c_int, vp, sz,
+                                        c.POINTER(c.c_double)]),
         "wh_timer_stop": (c.c_int, [vp, c.POINTER(c.c_double)]),
     }
     for name, (res, args) in sig.items():
@@ -316,6 +318,18 @@ class Context:
     def timer_start(self):
         """Records the start event on the library stream."""
         _check(self.lib.wh_timer_start(self._h), "timer_start")
+
+    def profile_routed(self, route_sets, x_dev: int, x_is_bf16: bool, out_dev: int, iters: int):
+        """Mean microseconds per launch of (gate/up, down) over `iters`
+        back-to-back launches cycling through `route_sets` (lists of
+        (layer, expert, weight) of equal length)."""
+        n = len(route_sets[0])
+        flat = [r for rs in route_sets for r in rs]
+        arr = (WhExpertRoute * len(flat))(*[WhExpertRoute(int(l), int(e), float(w)) for l, e, w in flat])
+        us = (ctypes.c_double * 2)()
+        _check(self.lib.wh_profile_routed(self._h, arr, n, len(route_sets), ctypes.c_void_p(x_dev), int(x_is_bf16),
+                                          ctypes.c_void_p(out_dev), iters, us), "profile_routed")
+        return us[0], us[1]
 
     def timer_stop(self) -> float:
         """Device microseconds since timer_start (waits for the stream)."""

@@ -405,6 +405,51 @@ bool expert_fast(const ExpertView& v) {
            wh_moe_wg_lds(v.w1->cols) <= g_max_lds && wh_moe_wg_lds(v.w1->rows) <= g_max_lds;
 }
 
+// Launches the fast routed-expert kernels for n_tokens rows of x sharing one
+// route list.  stages: bit 0 = gate/up + SwiGLU, bit 1 = down + routed sum.
+int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n, const void* x_dev,
+                    int x_bf16, size_t n_tokens, float* out_dev, unsigned stages) {
+    const size_t hidden = ev[0].w1->cols, inter = ev[0].w1->rows;
+    if (((uintptr_t)x_dev & 15) || ((uintptr_t)out_dev & 3)) return WH_INVALID_ARGUMENT;
+    WH_HIP(c->h.ensure(n_tokens * n * inter * sizeof(float), false));
+    WH_HIP(c->ybuf.ensure(n_tokens * n * hidden * sizeof(float), false));
+    WH_HIP(c->cnt_y.ensure(n_tokens * (hidden / 32) * sizeof(uint32_t), true));
+    wh_moe_args a;
+    std::memset(&a, 0, sizeof a);
+    for (size_t i = 0; i < n; ++i) {
+        a.ex[i].w1 = ev[i].w1->w;
+        a.ex[i].s1 = (const uint8_t*)ev[i].w1->s;
+        a.ex[i].w3 = ev[i].w3->w;
+        a.ex[i].s3 = (const uint8_t*)ev[i].w3->s;
+        a.ex[i].w2 = ev[i].w2->w;
+        a.ex[i].s2 = (const uint8_t*)ev[i].w2->s;
+        a.route_w[i] = route_w[i];
+    }
+    a.n_experts = (uint32_t)n;
+    a.hidden = (uint32_t)hidden;
+    a.inter = (uint32_t)inter;
+    a.n_tokens = (uint32_t)n_tokens;
+    a.x = x_dev;
+    a.x_is_bf16 = x_bf16 ? 1u : 0u;
+    a.h = c->h.as<float>();
+    a.y = c->ybuf.as<float>();
+    a.out = out_dev;
+    a.cnt_y = c->cnt_y.as<uint32_t>();
+    a.status = c->status;
+    if (stages & 1) {
+        dim3 ggrid((unsigned)(n * inter / 16), (unsigned)n_tokens);
+        if (hidden == 4096) k_moe_gateup<16><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
+        else k_moe_gateup<0><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
+    }
+    if (stages & 2) {
+        dim3 dgrid((unsigned)(n * hidden / 32), (unsigned)n_tokens);
+        if (inter == 2048) k_moe_down<8><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
+        else k_moe_down<0><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
+    }
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
 // Routed experts for n_tokens rows of x (all with the same route list).
 // x_dev: device input (f32 or bf16).  out_dev: n_tokens x hidden f32.
 int moe_forward(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n, const void* x_dev,
@@ -416,42 +461,7 @@ int moe_forward(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n,
             return WH_INVALID_SHAPE;
         fast = fast && expert_fast(ev[i]);
     }
-    if (fast && n <= WH_MAX_EXPERTS) {
-        if (((uintptr_t)x_dev & 15) || ((uintptr_t)out_dev & 3)) return WH_INVALID_ARGUMENT;
-        WH_HIP(c->h.ensure(n_tokens * n * inter * sizeof(float), false));
-        WH_HIP(c->ybuf.ensure(n_tokens * n * hidden * sizeof(float), false));
-        WH_HIP(c->cnt_y.ensure(n_tokens * (hidden / 32) * sizeof(uint32_t), true));
-        wh_moe_args a;
-        std::memset(&a, 0, sizeof a);
-        for (size_t i = 0; i < n; ++i) {
-            a.ex[i].w1 = ev[i].w1->w;
-            a.ex[i].s1 = (const uint8_t*)ev[i].w1->s;
-            a.ex[i].w3 = ev[i].w3->w;
-            a.ex[i].s3 = (const uint8_t*)ev[i].w3->s;
-            a.ex[i].w2 = ev[i].w2->w;
-            a.ex[i].s2 = (const uint8_t*)ev[i].w2->s;
-            a.route_w[i] = route_w[i];
-        }
-        a.n_experts = (uint32_t)n;
-        a.hidden = (uint32_t)hidden;
-        a.inter = (uint32_t)inter;
-        a.n_tokens = (uint32_t)n_tokens;
-        a.x = x_dev;
-        a.x_is_bf16 = x_bf16 ? 1u : 0u;
-        a.h = c->h.as<float>();
-        a.y = c->ybuf.as<float>();
-        a.out = out_dev;
-        a.cnt_y = c->cnt_y.as<uint32_t>();
-        a.status = c->status;
-        dim3 ggrid((unsigned)(n * inter / 16), (unsigned)n_tokens);
-        if (hidden == 4096) k_moe_gateup<16><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
-        else k_moe_gateup<0><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
-        dim3 dgrid((unsigned)(n * hidden / 32), (unsigned)n_tokens);
-        if (inter == 2048) k_moe_down<8><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
-        else k_moe_down<0><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
-        WH_HIP(hipGetLastError());
-        return WH_OK;
-    }
+    if (fast && n <= WH_MAX_EXPERTS) return moe_launch_fast(c, ev, route_w, n, x_dev, x_bf16, n_tokens, out_dev, 3u);
     // Generic composition (any shape the reference accepts), one token at a time.
     if (x_bf16) return WH_UNSUPPORTED;
     const size_t per = hidden + 3 * inter + n * osz + n;
@@ -1039,6 +1049,38 @@ int wh_timer_stop(wh_ctx* c, double* elapsed_us) {
     WH_HIP(hipEventElapsedTime(&ms, c->timer[0], c->timer[1]));
     *elapsed_us = (double)ms * 1000.0;
     return WH_OK;
+}
+
+int wh_profile_routed(wh_ctx* c, const wh_expert_route* routes, size_t n_routes, size_t n_sets,
+                      const void* x_dev, int x_bf16, float* out_dev, size_t iters, double* us_per_launch) {
+    if (!c || !routes || !x_dev || !out_dev || !us_per_launch || n_routes == 0 || n_sets == 0 || iters == 0 ||
+        n_routes > WH_MAX_EXPERTS)
+        return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    std::vector<ExpertView> ev(n_sets * n_routes);
+    std::vector<float> wts(n_sets * n_routes);
+    for (size_t s = 0; s < n_sets; ++s) {
+        WH_TRY(routed_common(c, routes + s * n_routes, n_routes, &ev[s * n_routes], &wts[s * n_routes]));
+        const ExpertView* e = &ev[s * n_routes];
+        for (size_t i = 0; i < n_routes; ++i)
+            if (!expert_fast(e[i]) || e[i].w1->cols != e[0].w1->cols || e[i].w1->rows != e[0].w1->rows ||
+                e[i].w2->rows != e[0].w1->cols)
+                return WH_UNSUPPORTED;
+    }
+    for (unsigned stage = 1; stage <= 2; ++stage) {
+        WH_HIP(hipEventRecord(c->timer[0], c->stream));
+        for (size_t it = 0; it < iters; ++it) {
+            const size_t s = it % n_sets;
+            WH_TRY(moe_launch_fast(c, &ev[s * n_routes], &wts[s * n_routes], n_routes, x_dev, x_bf16, 1, out_dev, stage));
+        }
+        WH_HIP(hipEventRecord(c->timer[1], c->stream));
+        WH_HIP(hipEventSynchronize(c->timer[1]));
+        float ms = 0.0f;
+        WH_HIP(hipEventElapsedTime(&ms, c->timer[0], c->timer[1]));
+        us_per_launch[stage - 1] = (double)ms * 1000.0 / (double)iters;
+    }
+    return read_status(c);
 }
 
 int wh_debug_eval(wh_ctx* c, int fn, const float* in, float* out, size_t n) {
