@@ -109,6 +109,90 @@ def fp8_dense(ctx, steps: int, warmup: int):
             "note": "back-to-back launches over 40 rotating weight copies; wall clock and HIP events on the library stream"}
 
 
+def decode_stack(n_layers: int, steps: int, warmup: int, seed: int):
+    """Full-depth synthetic stack at batch 1: per layer the FP8 projections
+    of one decode layer (wq_a, wq_b, wkv, wo_a in 8 row groups, wo_b; f32
+    128x128 block scales) and the MoE FFN (1 shared + top-6 of 256 routed
+    FP4 experts), all resident.  A step runs every layer once; the per-layer
+    average is the single decode layer's figure."""
+    import wohper_amd
+    from wohper_amd import workloads as wl
+
+    ctx = wohper_amd.Context(0)
+    t0 = time.perf_counter()
+    layers = []
+    for L in range(n_layers):
+        hs = {}
+        for i, (name, r, c, _) in enumerate(wl.DECODE_LAYER_FP8):
+            hs[name] = ctx.store_fp8_synthetic(r, c, seed, wl.fp8_stream(L, i),
+                                               wl.fp8_block_scales(seed * 100003 + L * 7 + i, r, c))
+        for e in range(wl.N_ROUTED + 1):  # expert id N_ROUTED is the layer's shared expert
+            ctx.store_expert_synthetic(L, e, wl.HIDDEN, wl.INTER, seed)
+        layers.append(hs)
+    dev_bytes, _, n_exp = ctx.usage()
+    log(f"stack: {n_layers} layers, {n_exp} experts, {dev_bytes / 1e9:.1f} GB resident in {time.perf_counter() - t0:.1f} s")
+    rng = np.random.default_rng(seed)
+    vec = lambda n: rng.standard_normal(n).astype(np.float32)
+    bufs = {"x": vec(4096), "qlat": vec(1024), "oa": vec(8 * 4096), "ob": vec(8192)}
+    dev = {}
+    for k, v in bufs.items():
+        dev[k] = ctx.device_alloc(v.nbytes)
+        ctx.to_device(dev[k], v)
+    y = ctx.device_alloc((1024 + 32768 + 512 + 8192 + 4096) * 4)
+    y_off = {"wq_a": 0, "wq_b": 1024, "wkv": 1024 + 32768, "wo_a": 1024 + 32768 + 512, "wo_b": 1024 + 32768 + 512 + 8192}
+    moe_x = ctx.device_alloc(4096 * 2)
+    ctx.to_device(moe_x, wl.bf16_bits(vec(4096)))
+    moe_out = ctx.device_alloc(4096 * 4)
+    descs = []
+    for hs in layers:
+        d = [(hs["wq_a"], 0, 1024, dev["x"], y), (hs["wq_b"], 0, 32768, dev["qlat"], y + y_off["wq_b"] * 4),
+             (hs["wkv"], 0, 512, dev["x"], y + y_off["wkv"] * 4)]
+        d += [(hs["wo_a"], 1024 * g, 1024 * (g + 1), dev["oa"] + g * 4096 * 4, y + (y_off["wo_a"] + 1024 * g) * 4)
+              for g in range(8)]
+        d += [(hs["wo_b"], 0, 4096, dev["ob"], y + y_off["wo_b"] * 4)]
+        descs.append(ctx.gemv_descs(d))
+    total = warmup + steps
+    route_arrays = []
+    for s_ in range(total):
+        per = []
+        for L in range(n_layers):
+            idx, w = wl.route_topk_sigmoid(rng.standard_normal(wl.N_ROUTED).astype(np.float32))
+            per.append(ctx.route_array([(L, int(e), float(wt)) for e, wt in zip(idx, w)]))
+        route_arrays.append(per)
+
+    def step(s_):
+        for L in range(n_layers):
+            ctx.fp8_gemv_batch_async(descs[L])
+            ctx.routed_and_shared_experts_async(route_arrays[s_][L], (L, wl.N_ROUTED), moe_x, True, 1, moe_out,
+                                                n_routes=wl.TOPK)
+
+    for s_ in range(warmup):
+        step(s_)
+    ctx.synchronize()
+    t1 = time.perf_counter()
+    ctx.timer_start()
+    for s_ in range(warmup, total):
+        step(s_)
+    dev_us = ctx.timer_stop()
+    ctx.synchronize()
+    wall = time.perf_counter() - t1
+    vec_bytes = (4096 + 1024 + 1024 + 32768 + 4096 + 512 + 8 * (4096 + 1024) + 8192 + 4096) * 4 + 4096 * 2 + 4096 * 4
+    layer_bytes = wl.DECODE_LAYER_FP8_BYTES + 7 * wl.FP4_EXPERT_BYTES + vec_bytes
+    step_us = dev_us / steps
+    res = {"workload": f"{n_layers} decode layers at batch 1: FP8 projections (wq_a 1024x4096, wq_b 32768x1024, "
+                       "wkv 512x4096, wo_a 8192x4096 in 8 groups, wo_b 4096x8192; f32 block scales) + MoE "
+                       "(1 shared + top-6 of 256 routed FP4 experts) per layer",
+           "resident_GB": round(dev_bytes / 1e9, 2), "bytes_per_layer": layer_bytes,
+           "step_us": round(step_us, 1), "wall_step_us": round(wall / steps * 1e6, 1),
+           "layer_us": round(step_us / n_layers, 2),
+           "GBps": round(layer_bytes * n_layers / (step_us * 1e-6) / 1e9, 1)}
+    res["frac_of_hbm_peak"] = round(res["GBps"] / HBM_PEAK_GBS, 4)
+    for k in list(dev.values()) + [y, moe_x, moe_out]:
+        ctx.device_free(k)
+    ctx.close()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -118,6 +202,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fp8", action="store_true")
+    ap.add_argument("--stack-layers", type=int, default=43, help="layers of the full-depth stack leg (0: skip)")
+    ap.add_argument("--stack-steps", type=int, default=20)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 5 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -199,6 +285,12 @@ def main():
         cpu = cpu_baseline(ctx.lib, seed, args.cpu_seconds)
         log(f"cpu baseline: {cpu}")
 
+    if args.stack_layers > 0:
+        ctx.close()
+        ctx = None
+        extra["decode_stack"] = decode_stack(args.stack_layers, args.stack_steps, 3, seed)
+        log(f"decode stack: {extra['decode_stack']}")
+
     line = {
         "metric": "HBM GB/s (% of peak) for FP4 expert + FP8 dense matvec; batch-1 decode step us",
         "value": round(value, 2),
@@ -225,9 +317,10 @@ def main():
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
-    ctx.device_free(x_dev)
-    ctx.device_free(out_dev)
-    ctx.close()
+    if ctx is not None:
+        ctx.device_free(x_dev)
+        ctx.device_free(out_dev)
+        ctx.close()
 
 
 if __name__ == "__main__":

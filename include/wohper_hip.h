@@ -110,6 +110,15 @@ int wh_store_expert(wh_ctx* ctx, uint32_t layer_id, uint32_t expert_id, wh_tenso
 int wh_store_expert_synthetic(wh_ctx* ctx, uint32_t layer_id, uint32_t expert_id, size_t hidden,
                               size_t inter, uint64_t seed, uint32_t scale_lo, uint32_t scale_hi);
 
+/* Synthetic FP8 tensor generated on the device straight into the resident
+ * layout (no host copy of the bytes), for stacks too large to upload: byte i
+ * of the row-major original is wh_synth_fp8_host's byte i, approximately
+ * uniform over the 254 finite E4M3 codes.  Scales are f32, 128x128 blocks.
+ * No counterpart in the reference (its weights come from checkpoints). */
+int wh_store_fp8_synthetic(wh_ctx* ctx, size_t rows, size_t cols, uint64_t seed, uint64_t stream,
+                           const float* scales, size_t scale_rows, size_t scale_cols, wh_tensor* out);
+void wh_synth_fp8_host(uint64_t seed, uint64_t stream, uint8_t* weight, size_t n);
+
 /* Host generator of the same bytes (original reference layout). */
 void wh_synth_fp4_host(uint64_t seed, uint64_t stream, uint8_t* packed, size_t packed_len,
                        uint8_t* scales, size_t scales_len, uint32_t scale_lo, uint32_t scale_hi);
@@ -156,11 +165,36 @@ int wh_act_quant_dequant(wh_ctx* ctx, float* values, size_t n, size_t block_size
 int wh_routed_experts(wh_ctx* ctx, const wh_expert_route* routes, size_t n_routes, float* hidden,
                       size_t hidden_len);
 
+/* Routed experts plus the shared expert, replacing
+ * compute_active_and_shared_experts (E/compute.rs:1872-1946): hidden =
+ * shared(x), then hidden += the routed sum of wh_routed_experts.  The shared
+ * expert is a resident expert keyed (shared_layer, shared_expert); n may be 0
+ * (shared expert only).  The async variant takes device pointers like
+ * wh_routed_experts_async. */
+int wh_routed_and_shared_experts(wh_ctx* ctx, const wh_expert_route* routes, size_t n_routes,
+                                 uint32_t shared_layer, uint32_t shared_expert, float* hidden,
+                                 size_t hidden_len);
+int wh_routed_and_shared_experts_async(wh_ctx* ctx, const wh_expert_route* routes, size_t n_routes,
+                                       uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
+                                       int x_is_bf16, size_t n_tokens, float* out_dev);
+
 /* Device-pointer variant for the resident decode path: x_dev holds n_tokens
  * rows of `hidden` values (f32, or bf16 when x_is_bf16), all routed to the same
  * expert list; out_dev gets n_tokens rows of f32.  Stream-ordered. */
 int wh_routed_experts_async(wh_ctx* ctx, const wh_expert_route* routes, size_t n_routes,
                             const void* x_dev, int x_is_bf16, size_t n_tokens, float* out_dev);
+
+/* Several device-pointer FP8 GEMVs enqueued by one call, in order (a decode
+ * layer's projections: the reference calls gemv_fp8_e4m3_ue8m0_rows once per
+ * projection and per wo_a group, E/compute.rs:4005-4265).  Every descriptor
+ * is validated before the first launch. */
+typedef struct {
+    wh_tensor weight;
+    size_t row_start, row_end;
+    const float* x_dev; /* cols floats */
+    float* y_dev;       /* row_end - row_start floats */
+} wh_gemv_desc;
+int wh_fp8_gemv_batch_async(wh_ctx* ctx, const wh_gemv_desc* descs, size_t n);
 
 /* Device-pointer FP8 GEMV (rows [row_start,row_end) of w, x_dev f32 or bf16). */
 int wh_fp8_gemv_async(wh_ctx* ctx, wh_tensor w, size_t row_start, size_t row_end,

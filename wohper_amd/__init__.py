@@ -63,6 +63,8 @@ EXPORTED = (
     "wh_fp8_gemv", "wh_fp8_gemv_multi", "wh_fp4_matvec", "wh_fp4_expert_forward",
     "wh_act_quant_dequant", "wh_routed_experts", "wh_routed_experts_async", "wh_fp8_gemv_async",
     "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop", "wh_profile_routed",
+    "wh_store_fp8_synthetic", "wh_synth_fp8_host", "wh_routed_and_shared_experts", "wh_fp8_gemv_batch_async",
+    "wh_routed_and_shared_experts_async",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
 )
 
@@ -75,6 +77,11 @@ class DeepSeekV4KernelError(RuntimeError):
         self.code = int(code)
         self.name = STATUS_NAMES.get(self.code, f"status {code}")
         super().__init__(f"{self.name}" + (f" ({where})" if where else ""))
+
+
+class WhGemvDesc(ctypes.Structure):
+    _fields_ = [("weight", ctypes.c_uint64), ("row_start", ctypes.c_size_t), ("row_end", ctypes.c_size_t),
+                ("x_dev", ctypes.c_void_p), ("y_dev", ctypes.c_void_p)]
 
 
 class WhExpertRoute(ctypes.Structure):
@@ -128,6 +135,14 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_device_free": (c.c_int, [vp, vp]),
         "wh_memcpy": (c.c_int, [vp, vp, vp, sz, c.c_int]),
         "wh_timer_start": (c.c_int, [vp]),
+        "wh_fp8_gemv_batch_async": (c.c_int, [vp, c.POINTER(WhGemvDesc), sz]),
+        "wh_store_fp8_synthetic": (c.c_int, [vp, sz, sz, c.c_uint64, c.c_uint64, f32p, sz, sz,
+                                             c.POINTER(c.c_uint64)]),
+        "wh_synth_fp8_host": (None, [c.c_uint64, c.c_uint64, u8p, sz]),
+        "wh_routed_and_shared_experts": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, c.c_uint32, c.c_uint32,
+                                                   f32p, sz]),
+        "wh_routed_and_shared_experts_async": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, c.c_uint32,
+                                                         c.c_uint32, vp, c.c_int, sz, vp]),
         "wh_profile_routed": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, sz, vp, c.c_int, vp, sz,
                                         c.POINTER(c.c_double)]),
         "wh_timer_stop": (c.c_int, [vp, c.POINTER(c.c_double)]),
@@ -330,6 +345,49 @@ class Context:
         _check(self.lib.wh_profile_routed(self._h, arr, n, len(route_sets), ctypes.c_void_p(x_dev), int(x_is_bf16),
                                           ctypes.c_void_p(out_dev), iters, us), "profile_routed")
         return us[0], us[1]
+
+    @staticmethod
+    def gemv_descs(descs):
+        """ctypes array of (tensor, row_start, row_end, x_ptr, y_ptr) descriptors."""
+        return (WhGemvDesc * len(descs))(*[WhGemvDesc(t, r0, r1, x, y) for t, r0, r1, x, y in descs])
+
+    @staticmethod
+    def route_array(routes):
+        """ctypes array of (layer, expert, weight) routes (at least one slot)."""
+        return (WhExpertRoute * max(1, len(routes)))(*[WhExpertRoute(int(a), int(b), float(w)) for a, b, w in routes])
+
+    def fp8_gemv_batch_async(self, descs):
+        """descs: sequence of (tensor, row_start, row_end, x_ptr, y_ptr), or a
+        prebuilt gemv_descs() array."""
+        arr = descs if isinstance(descs, ctypes.Array) else self.gemv_descs(descs)
+        _check(self.lib.wh_fp8_gemv_batch_async(self._h, arr, len(arr)), "fp8_gemv_batch_async")
+
+    def store_fp8_synthetic(self, rows: int, cols: int, seed: int, stream: int, scales) -> int:
+        """Device-generated FP8 tensor (bytes = synth_fp8_host's) with f32
+        128x128 block scales `scales` [rows/128][cols/128]."""
+        sc = _f32(scales)
+        h = ctypes.c_uint64()
+        _check(self.lib.wh_store_fp8_synthetic(self._h, rows, cols, seed, stream, _p(sc, ctypes.c_float),
+                                               sc.shape[0], sc.shape[1], ctypes.byref(h)), "store_fp8_synthetic")
+        return h.value
+
+    def routed_and_shared_experts(self, routes, shared_key, x) -> np.ndarray:
+        """out = shared(x) + routed(x) (compute_active_and_shared_experts)."""
+        arr = (WhExpertRoute * max(1, len(routes)))(*[WhExpertRoute(int(a), int(b), float(w)) for a, b, w in routes])
+        h = _f32(x).copy()
+        _check(self.lib.wh_routed_and_shared_experts(self._h, arr, len(routes), shared_key[0], shared_key[1],
+                                                     _p(h, ctypes.c_float), h.size), "routed_and_shared_experts")
+        return h
+
+    def routed_and_shared_experts_async(self, routes, shared_key, x_ptr: int, x_is_bf16: bool, n_tokens: int,
+                                        out_ptr: int, n_routes=None):
+        """routes: sequence of (layer, expert, weight), or a prebuilt
+        route_array() with n_routes entries."""
+        arr = routes if isinstance(routes, ctypes.Array) else self.route_array(routes)
+        n = n_routes if n_routes is not None else len(routes)
+        _check(self.lib.wh_routed_and_shared_experts_async(self._h, arr, n, shared_key[0], shared_key[1],
+                                                           ctypes.c_void_p(x_ptr), int(x_is_bf16), n_tokens,
+                                                           ctypes.c_void_p(out_ptr)), "routed_and_shared_experts_async")
 
     def timer_stop(self) -> float:
         """Device microseconds since timer_start (waits for the stream)."""

@@ -696,7 +696,8 @@ struct wh_expert_ptrs {
 struct wh_moe_args {
     wh_expert_ptrs ex[WH_MAX_EXPERTS];
     float route_w[WH_MAX_EXPERTS];
-    uint32_t n_experts;
+    uint32_t n_experts;            // routed experts, plus the shared one when has_shared
+    uint32_t has_shared;           // the last expert slot is the shared expert
     uint32_t hidden, inter;        // w1/w3: inter x hidden, w2: hidden x inter
     uint32_t n_tokens;             // tokens sharing the same expert list
     const void* x;                 // [n_tokens][hidden], f32 or bf16
@@ -964,26 +965,31 @@ __global__ void __launch_bounds__(256) k_moe_down(wh_moe_args a) {
     if (!last || threadIdx.x >= 32) return;
     const uint32_t r_out = rb * 32 + threadIdx.x;
     const size_t t0 = (size_t)tok * a.n_experts * a.hidden;
-    float o;
-    if (a.n_experts == 1) {
+    const uint32_t nr = a.n_experts - a.has_shared;  // routed experts
+    float o = 0.0f;
+    if (nr == 1) {
         o = wh_load_coherent(a.y + t0 + r_out);
-    } else {
+    } else if (nr > 1) {
         // valid_route_weight_sum (E/compute.rs:2014-2030)
         float sum = 0.0f;
         bool valid = true;
-        for (uint32_t i = 0; i < a.n_experts; ++i) {
+        for (uint32_t i = 0; i < nr; ++i) {
             float w = a.route_w[i];
             if (!(fabsf(w) <= 3.4028235e38f && w >= 0.0f)) valid = false;
             sum = sum + w;
         }
         if (sum <= 1.1920929e-07f) valid = false;
-        const float uniform = 1.0f / (float)a.n_experts;
-        o = 0.0f;
-        for (uint32_t i = 0; i < a.n_experts; ++i) {
+        const float uniform = 1.0f / (float)nr;
+        for (uint32_t i = 0; i < nr; ++i) {
             float w = valid ? a.route_w[i] / sum : uniform;
             float p = wh_load_coherent(a.y + t0 + (size_t)i * a.hidden + r_out) * w;
             o = o + p;
         }
+    }
+    if (a.has_shared) {
+        // hidden = shared(x); hidden += routed (E/compute.rs:1929-1941)
+        const float sh = wh_load_coherent(a.y + t0 + (size_t)nr * a.hidden + r_out);
+        o = nr == 0 ? sh : sh + o;
     }
     a.out[(size_t)tok * a.hidden + r_out] = o;
     if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

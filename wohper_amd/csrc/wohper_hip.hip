@@ -360,28 +360,36 @@ __global__ void k_swiglu_generic(const float* g, const float* u, float* h, uint3
     if (i < n) h[i] = wh_swiglu(g[i], u[i], kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
 }
 
-__global__ void k_combine_generic(const float* y, const float* w, uint32_t n_experts,
+// Ordered routed sum (E/compute.rs:1948-2030) of the first n_experts -
+// has_shared outputs; with has_shared the last output is the shared expert's
+// and out = shared + routed (E/compute.rs:1929-1941).
+__global__ void k_combine_generic(const float* y, const float* w, uint32_t n_experts, uint32_t has_shared,
                                   uint32_t hidden, float* out) {
     uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= hidden) return;
-    if (n_experts == 1) {
-        out[r] = y[r];
-        return;
-    }
-    float sum = 0.0f;
-    bool valid = true;
-    for (uint32_t i = 0; i < n_experts; ++i) {
-        float wi = w[i];
-        if (!(fabsf(wi) <= 3.4028235e38f && wi >= 0.0f)) valid = false;
-        sum = sum + wi;
-    }
-    if (sum <= 1.1920929e-07f) valid = false;
-    float uniform = 1.0f / (float)n_experts;
+    const uint32_t nr = n_experts - has_shared;
     float o = 0.0f;
-    for (uint32_t i = 0; i < n_experts; ++i) {
-        float wi = valid ? w[i] / sum : uniform;
-        float p = y[(size_t)i * hidden + r] * wi;
-        o = o + p;
+    if (nr == 1) {
+        o = y[r];
+    } else if (nr > 1) {
+        float sum = 0.0f;
+        bool valid = true;
+        for (uint32_t i = 0; i < nr; ++i) {
+            float wi = w[i];
+            if (!(fabsf(wi) <= 3.4028235e38f && wi >= 0.0f)) valid = false;
+            sum = sum + wi;
+        }
+        if (sum <= 1.1920929e-07f) valid = false;
+        float uniform = 1.0f / (float)nr;
+        for (uint32_t i = 0; i < nr; ++i) {
+            float wi = valid ? w[i] / sum : uniform;
+            float p = y[(size_t)i * hidden + r] * wi;
+            o = o + p;
+        }
+    }
+    if (has_shared) {
+        const float sh = y[(size_t)nr * hidden + r];
+        o = nr == 0 ? sh : sh + o;
     }
     out[r] = o;
 }
@@ -407,8 +415,8 @@ bool expert_fast(const ExpertView& v) {
 
 // Launches the fast routed-expert kernels for n_tokens rows of x sharing one
 // route list.  stages: bit 0 = gate/up + SwiGLU, bit 1 = down + routed sum.
-int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n, const void* x_dev,
-                    int x_bf16, size_t n_tokens, float* out_dev, unsigned stages) {
+int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n, bool has_shared,
+                    const void* x_dev, int x_bf16, size_t n_tokens, float* out_dev, unsigned stages) {
     const size_t hidden = ev[0].w1->cols, inter = ev[0].w1->rows;
     if (((uintptr_t)x_dev & 15) || ((uintptr_t)out_dev & 3)) return WH_INVALID_ARGUMENT;
     WH_HIP(c->h.ensure(n_tokens * n * inter * sizeof(float), false));
@@ -426,6 +434,7 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
         a.route_w[i] = route_w[i];
     }
     a.n_experts = (uint32_t)n;
+    a.has_shared = has_shared ? 1u : 0u;
     a.hidden = (uint32_t)hidden;
     a.inter = (uint32_t)inter;
     a.n_tokens = (uint32_t)n_tokens;
@@ -452,8 +461,10 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
 
 // Routed experts for n_tokens rows of x (all with the same route list).
 // x_dev: device input (f32 or bf16).  out_dev: n_tokens x hidden f32.
-int moe_forward(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n, const void* x_dev,
-                int x_bf16, size_t n_tokens, float* out_dev) {
+// ev[0..n): the experts; with has_shared the last one is the shared expert
+// (weights route_w cover the routed ones).
+int moe_forward(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n, bool has_shared,
+                const void* x_dev, int x_bf16, size_t n_tokens, float* out_dev) {
     const size_t hidden = ev[0].w1->cols, inter = ev[0].w1->rows, osz = ev[0].w2->rows;
     bool fast = osz == hidden;
     for (size_t i = 0; i < n; ++i) {
@@ -461,7 +472,8 @@ int moe_forward(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n,
             return WH_INVALID_SHAPE;
         fast = fast && expert_fast(ev[i]);
     }
-    if (fast && n <= WH_MAX_EXPERTS) return moe_launch_fast(c, ev, route_w, n, x_dev, x_bf16, n_tokens, out_dev, 3u);
+    if (fast && n <= WH_MAX_EXPERTS)
+        return moe_launch_fast(c, ev, route_w, n, has_shared, x_dev, x_bf16, n_tokens, out_dev, 3u);
     // Generic composition (any shape the reference accepts), one token at a time.
     if (x_bf16) return WH_UNSUPPORTED;
     const size_t per = hidden + 3 * inter + n * osz + n;
@@ -485,7 +497,7 @@ int moe_forward(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n,
             WH_TRY(launch_fp4(c, *ev[i].w2, hh, ys + i * osz));
         }
         k_combine_generic<<<(unsigned)((osz + 255) / 256), 256, 0, c->stream>>>(
-            ys, wdev, (uint32_t)n, (uint32_t)osz, out_dev + tok * osz);
+            ys, wdev, (uint32_t)n, has_shared ? 1u : 0u, (uint32_t)osz, out_dev + tok * osz);
         WH_HIP(hipGetLastError());
     }
     return WH_OK;
@@ -535,6 +547,25 @@ __global__ void k_synth_fp4(uint8_t* w, uint8_t* s, uint32_t rows, uint32_t cols
         uint32_t span = shi - slo + 1;
         s[id] = (uint8_t)(slo + wh_synth_byte(seed, stream ^ 0x5ca1e5ull, id) % span);
     }
+}
+
+// Synthetic FP8 byte: approximately uniform over the 254 finite E4M3 codes
+// (0x7F and 0xFF excluded), from the same counter-based generator.
+__host__ __device__ inline uint8_t wh_fp8_synth_code(uint64_t seed, uint64_t stream, uint64_t i) {
+    const uint32_t r = wh_synth_byte(seed, stream, i) % 254u;
+    return (uint8_t)(r < 127u ? r : r + 1u);
+}
+
+// Device synthetic FP8 tensor straight into the resident lane layout: one
+// thread per resident byte, reading the generated byte of its original column.
+__global__ void k_synth_fp8(uint8_t* w, uint32_t rows, uint32_t cols, uint64_t seed, uint64_t stream) {
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= (size_t)rows * cols) return;
+    const size_t row = id / cols;
+    const uint32_t rc = (uint32_t)(id - row * cols);
+    const uint32_t g = rc >> 7, l = (rc & 127) >> 4, i = rc & 15;
+    const uint32_t col = g * 128 + (i & 7) * 16 + (i >> 3) * 8 + l;
+    w[id] = wh_fp8_synth_code(seed, stream, row * cols + col);
 }
 
 int store_tensor_common(wh_ctx* c, Tensor&& t, wh_tensor* out) {
@@ -782,6 +813,42 @@ int wh_store_expert_synthetic(wh_ctx* c, uint32_t layer, uint32_t expert, size_t
     return WH_OK;
 }
 
+void wh_synth_fp8_host(uint64_t seed, uint64_t stream, uint8_t* weight, size_t n) {
+    for (size_t i = 0; i < n; ++i) weight[i] = wh_fp8_synth_code(seed, stream, i);
+}
+
+int wh_store_fp8_synthetic(wh_ctx* c, size_t rows, size_t cols, uint64_t seed, uint64_t stream,
+                           const float* scales, size_t scale_rows, size_t scale_cols, wh_tensor* out) {
+    if (!c || !out || !scales) return WH_INVALID_ARGUMENT;
+    if (rows == 0 || cols == 0 || scale_rows == 0 || scale_cols == 0 || rows % scale_rows || cols % scale_cols ||
+        cols / scale_cols != 128)
+        return WH_INVALID_SHAPE;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    Tensor t;
+    t.kind = kFp8;
+    t.rows = rows;
+    t.cols = cols;
+    t.scale_rows = scale_rows;
+    t.scale_cols = scale_cols;
+    t.scale_fmt = WH_SCALE_F32;
+    t.fast = cols * 4 <= g_max_lds;
+    if (!t.fast) return WH_UNSUPPORTED;
+    const size_t sbytes = scale_rows * scale_cols * sizeof(float);
+    t.bytes = rows * cols + sbytes;
+    void* wd = nullptr;
+    void* sd = nullptr;
+    WH_TRY(alloc_device(c, rows * cols, &wd));
+    WH_TRY(alloc_device(c, sbytes, &sd));
+    t.w = (uint8_t*)wd;
+    t.s = sd;
+    const size_t n = rows * cols;
+    k_synth_fp8<<<(unsigned)((n + 255) / 256), 256, 0, c->stream>>>(t.w, (uint32_t)rows, (uint32_t)cols, seed, stream);
+    WH_HIP(hipGetLastError());
+    WH_TRY(upload(c, t.s, scales, sbytes));
+    return store_tensor_common(c, std::move(t), out);
+}
+
 int wh_store_release(wh_ctx* c, wh_tensor t) {
     if (!c) return WH_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lk(c->mu);
@@ -888,6 +955,27 @@ int wh_fp8_gemv_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end,
     return launch_fp8(c, *t, row_start, row_end, x_dev, y_dev, 1, t->cols, row_end - row_start);
 }
 
+int wh_fp8_gemv_batch_async(wh_ctx* c, const wh_gemv_desc* descs, size_t n) {
+    if (!c || (n && !descs)) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    // validate everything before launching anything
+    for (size_t i = 0; i < n; ++i) {
+        const wh_gemv_desc& d = descs[i];
+        Tensor* t = find_tensor(c, d.weight);
+        if (!t) return WH_NOT_RESIDENT;
+        if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
+        if (!d.x_dev || !d.y_dev) return WH_INVALID_ARGUMENT;
+        if (d.row_start >= d.row_end || d.row_end > t->rows) return WH_INVALID_SHAPE;
+    }
+    for (size_t i = 0; i < n; ++i) {
+        const wh_gemv_desc& d = descs[i];
+        const Tensor* t = find_tensor(c, d.weight);
+        WH_TRY(launch_fp8(c, *t, d.row_start, d.row_end, d.x_dev, d.y_dev, 1, t->cols, d.row_end - d.row_start));
+    }
+    return WH_OK;
+}
+
 int wh_fp4_matvec(wh_ctx* c, wh_tensor w, const float* input, size_t input_len, float* output,
                   size_t output_len) {
     if (!c || !input || !output) return WH_INVALID_ARGUMENT;
@@ -953,7 +1041,7 @@ int wh_routed_experts(wh_ctx* c, const wh_expert_route* routes, size_t n, float*
     WH_HIP(c->y_out.ensure(osz * sizeof(float), false));
     WH_HIP(c->stage_out.ensure(osz * sizeof(float)));
     WH_HIP(hipMemcpyAsync(c->x_in.p, hidden, hsz * sizeof(float), hipMemcpyHostToDevice, c->stream));
-    WH_TRY(moe_forward(c, ev, wts, n, c->x_in.p, 0, 1, c->y_out.as<float>()));
+    WH_TRY(moe_forward(c, ev, wts, n, false, c->x_in.p, 0, 1, c->y_out.as<float>()));
     WH_HIP(hipMemcpyAsync(c->stage_out.p, c->y_out.p, osz * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     int st = read_status(c);
     if (st != WH_OK) return st;
@@ -969,7 +1057,50 @@ int wh_routed_experts_async(wh_ctx* c, const wh_expert_route* routes, size_t n, 
     ExpertView ev[WH_MAX_EXPERTS];
     float wts[WH_MAX_EXPERTS];
     WH_TRY(routed_common(c, routes, n, ev, wts));
-    return moe_forward(c, ev, wts, n, x_dev, x_bf16, n_tokens, out_dev);
+    return moe_forward(c, ev, wts, n, false, x_dev, x_bf16, n_tokens, out_dev);
+}
+
+// Routed experts plus the shared expert keyed (shared_layer, shared_expert).
+static int routed_shared_common(wh_ctx* c, const wh_expert_route* routes, size_t n, uint32_t shared_layer,
+                                uint32_t shared_expert, ExpertView* ev, float* wts) {
+    if (n + 1 > WH_MAX_EXPERTS) return WH_UNSUPPORTED;
+    if (n) WH_TRY(routed_common(c, routes, n, ev, wts));
+    return resolve_expert(c, shared_layer, shared_expert, &ev[n]);
+}
+
+int wh_routed_and_shared_experts(wh_ctx* c, const wh_expert_route* routes, size_t n, uint32_t shared_layer,
+                                 uint32_t shared_expert, float* hidden, size_t hidden_len) {
+    if (!c || !hidden || (n && !routes)) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    ExpertView ev[WH_MAX_EXPERTS];
+    float wts[WH_MAX_EXPERTS];
+    WH_TRY(routed_shared_common(c, routes, n, shared_layer, shared_expert, ev, wts));
+    const size_t hsz = ev[n].w1->cols, osz = ev[n].w2->rows;
+    if (hidden_len < hsz) return WH_INVALID_SHAPE;  // "hidden_states is empty" / input dim
+    if (osz > hidden_len) return WH_OUTPUT_TOO_SMALL;
+    WH_HIP(c->x_in.ensure(hsz * sizeof(float), false));
+    WH_HIP(c->y_out.ensure(osz * sizeof(float), false));
+    WH_HIP(c->stage_out.ensure(osz * sizeof(float)));
+    WH_HIP(hipMemcpyAsync(c->x_in.p, hidden, hsz * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    WH_TRY(moe_forward(c, ev, wts, n + 1, true, c->x_in.p, 0, 1, c->y_out.as<float>()));
+    WH_HIP(hipMemcpyAsync(c->stage_out.p, c->y_out.p, osz * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    int st = read_status(c);
+    if (st != WH_OK) return st;
+    std::memcpy(hidden, c->stage_out.p, osz * sizeof(float));
+    return WH_OK;
+}
+
+int wh_routed_and_shared_experts_async(wh_ctx* c, const wh_expert_route* routes, size_t n, uint32_t shared_layer,
+                                       uint32_t shared_expert, const void* x_dev, int x_bf16, size_t n_tokens,
+                                       float* out_dev) {
+    if (!c || !x_dev || !out_dev || n_tokens == 0 || (n && !routes)) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    ExpertView ev[WH_MAX_EXPERTS];
+    float wts[WH_MAX_EXPERTS];
+    WH_TRY(routed_shared_common(c, routes, n, shared_layer, shared_expert, ev, wts));
+    return moe_forward(c, ev, wts, n + 1, true, x_dev, x_bf16, n_tokens, out_dev);
 }
 
 int wh_fp4_expert_forward(wh_ctx* c, uint32_t layer, uint32_t expert, const float* input,
@@ -994,7 +1125,7 @@ int wh_fp4_expert_forward(wh_ctx* c, uint32_t layer, uint32_t expert, const floa
     WH_HIP(c->stage_out.ensure(osz * sizeof(float)));
     WH_HIP(hipMemcpyAsync(c->x_in.p, input, hsz * sizeof(float), hipMemcpyHostToDevice, c->stream));
     float one = 1.0f;
-    WH_TRY(moe_forward(c, &ev, &one, 1, c->x_in.p, 0, 1, c->y_out.as<float>()));
+    WH_TRY(moe_forward(c, &ev, &one, 1, false, c->x_in.p, 0, 1, c->y_out.as<float>()));
     WH_HIP(hipMemcpyAsync(c->stage_out.p, c->y_out.p, osz * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     int st = read_status(c);
     if (st != WH_OK) return st;
@@ -1072,7 +1203,8 @@ int wh_profile_routed(wh_ctx* c, const wh_expert_route* routes, size_t n_routes,
         WH_HIP(hipEventRecord(c->timer[0], c->stream));
         for (size_t it = 0; it < iters; ++it) {
             const size_t s = it % n_sets;
-            WH_TRY(moe_launch_fast(c, &ev[s * n_routes], &wts[s * n_routes], n_routes, x_dev, x_bf16, 1, out_dev, stage));
+            WH_TRY(moe_launch_fast(c, &ev[s * n_routes], &wts[s * n_routes], n_routes, false, x_dev, x_bf16, 1,
+                                   out_dev, stage));
         }
         WH_HIP(hipEventRecord(c->timer[1], c->stream));
         WH_HIP(hipEventSynchronize(c->timer[1]));

@@ -91,3 +91,33 @@ def synth_expert_host(lib, seed: int, layer: int, expert: int, hidden=HIDDEN, in
     w2 = synth_fp4_host(lib, seed, layer, expert, 2, hidden, inter)
     return ((w1[0], w1[1], inter, hidden, hidden // 32), (w3[0], w3[1], inter, hidden, hidden // 32),
             (w2[0], w2[1], hidden, inter, inter // 32))
+
+
+# One decode layer's FP8 projections (the engine's V4-Flash set,
+# E/compute.rs:659-684): (name, rows, cols, row groups with distinct inputs).
+DECODE_LAYER_FP8 = (
+    ("wq_a", 1024, 4096, 1),
+    ("wq_b", 32768, 1024, 1),
+    ("wkv", 512, 4096, 1),
+    ("wo_a", 8192, 4096, 8),     # 8 groups of 1024 rows, E/compute.rs:4244-4258
+    ("wo_b", 4096, 8192, 1),
+)
+DECODE_LAYER_FP8_BYTES = sum(r * c + (r // 128) * (c // 128) * 4 for _, r, c, _ in DECODE_LAYER_FP8)  # 106,980,864
+
+
+def fp8_block_scales(seed: int, rows: int, cols: int) -> np.ndarray:
+    """f32 128x128 block scales 2^U, U ~ U[-10, -4]."""
+    rng = np.random.default_rng(seed)
+    return np.exp2(rng.uniform(-10.0, -4.0, size=(rows // 128, cols // 128))).astype(np.float32)
+
+
+def synth_fp8_host(lib, seed: int, stream: int, rows: int, cols: int) -> np.ndarray:
+    """Host copy of the bytes wh_store_fp8_synthetic generates, row-major."""
+    w = np.empty(rows * cols, np.uint8)
+    lib.wh_synth_fp8_host(seed, stream, w.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), w.size)
+    return w.reshape(rows, cols)
+
+
+def fp8_stream(layer: int, index: int) -> int:
+    """Generator stream of FP8 projection `index` of `layer`."""
+    return (1 << 62) ^ (layer << 16) ^ index
