@@ -36,6 +36,19 @@ def test_fp8_synthetic_store_and_batched_gemv(ctx, oracle):
     for i, (r0, r1) in enumerate(ranges):
         want = oracle.fp8_gemv(w, rows, cols, scales, rows // 128, cols // 128, xs[i], r0, r1)
         assert np.array_equal(bits(ys[i, :r1 - r0]), bits(want)), (r0, r1)
+    # wo_a-style row groups with their own inputs (one merged launch)
+    xg = rng.standard_normal((4, cols)).astype(np.float32)
+    xg_dev = ctx.device_alloc(xg.nbytes)
+    ctx.to_device(xg_dev, xg)
+    ctx.fp8_gemv_batch_async([(t, 256 * g, 256 * (g + 1), xg_dev + g * cols * 4, y_dev + g * 256 * 4)
+                              for g in range(4)])
+    ctx.synchronize()
+    yg = np.empty(rows, np.float32)
+    ctx.from_device(yg, y_dev)
+    for g in range(4):
+        want = oracle.fp8_gemv(w, rows, cols, scales, rows // 128, cols // 128, xg[g], 256 * g, 256 * (g + 1))
+        assert np.array_equal(bits(yg[256 * g:256 * (g + 1)]), bits(want)), g
+    ctx.device_free(xg_dev)
     with pytest.raises(wohper_amd.DeepSeekV4KernelError) as e:
         ctx.fp8_gemv_batch_async([(t, 0, rows + 1, x_dev, y_dev)])
     assert e.value.name == "InvalidShape"

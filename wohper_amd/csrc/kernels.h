@@ -158,6 +158,10 @@ struct wh_fp8_args {
     uint32_t* status;
     uint32_t cols, scale_cols, row_group, row_start, row_end;
     uint32_t x_stride, y_stride;  // batch strides (multi-input variant)
+    // row groups with their own input (wo_a, E/compute.rs:4244-4258): rows
+    // row_start + [g*x_group_rows, (g+1)*x_group_rows) read x + g*x_group_stride;
+    // 0 = one input for all rows (split-K path only, x_group_rows % 4 == 0)
+    uint32_t x_group_rows, x_group_stride;
 };
 
 template <bool kSpecial, bool kScaleU8>
@@ -277,7 +281,8 @@ template <bool kSpecial, bool kScaleU8, int kGps>
 __global__ void __launch_bounds__(256) k_fp8_gemv_sk(wh_fp8_args a) {
     extern __shared__ __align__(16) float lds[];
     const uint32_t batch = blockIdx.y;
-    const float* x = a.x + (size_t)batch * a.x_stride;
+    const float* x = a.x + (size_t)batch * a.x_stride +
+                     (a.x_group_rows ? (size_t)(blockIdx.x * 4 / a.x_group_rows) * a.x_group_stride : 0);
     const uint32_t lane = threadIdx.x & 7, seg = (threadIdx.x >> 3) & 7, rr = threadIdx.x >> 6;
     const uint32_t row = a.row_start + blockIdx.x * 4 + rr;
     const bool active = row < a.row_end;

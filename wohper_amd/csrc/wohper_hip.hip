@@ -279,8 +279,17 @@ hipError_t kernel_setup_once(int device) {
 // and the 4 rows' group scales.
 size_t fp8_sk_lds(size_t cols) { return sizeof(float) * (cols + 36 * (cols / 128)); }
 
+// Whether launch_fp8 takes the split-K path for this tensor (which also
+// supports per-row-group inputs).
+bool fp8_split_k(const Tensor& t) {
+    return t.fast && (t.cols / 128) % 8 == 0 && fp8_sk_lds(t.cols) <= g_max_lds;
+}
+
+// x_group_rows / x_group_stride: row groups with their own input (split-K
+// path only; see wh_fp8_args).
 int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x, float* y,
-               size_t n_batch, size_t x_stride, size_t y_stride) {
+               size_t n_batch, size_t x_stride, size_t y_stride, size_t x_group_rows = 0,
+               size_t x_group_stride = 0) {
     wh_fp8_args a;
     a.w = t.w;
     a.scales = t.s;
@@ -294,8 +303,11 @@ int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x,
     a.row_end = (uint32_t)r1;
     a.x_stride = (uint32_t)x_stride;
     a.y_stride = (uint32_t)y_stride;
+    a.x_group_rows = (uint32_t)x_group_rows;
+    a.x_group_stride = (uint32_t)x_group_stride;
+    if (x_group_rows && (!fp8_split_k(t) || x_group_rows % 4)) return WH_UNSUPPORTED;
     bool u8 = t.scale_fmt == WH_SCALE_UE8M0;
-    if (t.fast && (t.cols / 128) % 8 == 0 && fp8_sk_lds(t.cols) <= g_max_lds) {
+    if (fp8_split_k(t)) {
         dim3 grid((unsigned)((r1 - r0 + 3) / 4), (unsigned)n_batch);
         const size_t lds = fp8_sk_lds(t.cols);
         const bool g4 = t.cols == 4096;
@@ -968,10 +980,28 @@ int wh_fp8_gemv_batch_async(wh_ctx* c, const wh_gemv_desc* descs, size_t n) {
         if (!d.x_dev || !d.y_dev) return WH_INVALID_ARGUMENT;
         if (d.row_start >= d.row_end || d.row_end > t->rows) return WH_INVALID_SHAPE;
     }
-    for (size_t i = 0; i < n; ++i) {
+    for (size_t i = 0; i < n;) {
         const wh_gemv_desc& d = descs[i];
         const Tensor* t = find_tensor(c, d.weight);
-        WH_TRY(launch_fp8(c, *t, d.row_start, d.row_end, d.x_dev, d.y_dev, 1, t->cols, d.row_end - d.row_start));
+        const size_t rows = d.row_end - d.row_start;
+        // a run of equal, consecutive row groups of one tensor with evenly
+        // spaced inputs and back-to-back outputs goes out as one launch
+        size_t j = i + 1;
+        const ptrdiff_t xs = j < n ? descs[j].x_dev - d.x_dev : 0;
+        if (fp8_split_k(*t) && rows % 4 == 0 && xs >= 0) {
+            while (j < n && descs[j].weight == d.weight && descs[j].row_start == descs[j - 1].row_end &&
+                   descs[j].row_end - descs[j].row_start == rows && descs[j].x_dev - descs[j - 1].x_dev == xs &&
+                   descs[j].y_dev == descs[j - 1].y_dev + rows)
+                ++j;
+        } else {
+            j = i + 1;
+        }
+        if (j - i > 1)
+            WH_TRY(launch_fp8(c, *t, d.row_start, descs[j - 1].row_end, d.x_dev, d.y_dev, 1, t->cols,
+                              descs[j - 1].row_end - d.row_start, rows, (size_t)xs));
+        else
+            WH_TRY(launch_fp8(c, *t, d.row_start, d.row_end, d.x_dev, d.y_dev, 1, t->cols, rows));
+        i = j;
     }
     return WH_OK;
 }
