@@ -109,6 +109,48 @@ def fp8_dense(ctx, steps: int, warmup: int):
             "note": "back-to-back launches over 40 rotating weight copies; wall clock and HIP events on the library stream"}
 
 
+def ragged_batch(ctx, n_layers: int, steps: int, warmup: int):
+    """Ragged batched MoE: 64 bf16 tokens, each top-6 of 256 FP4 experts under
+    Zipf(1.1) popularity over a seeded permutation (seed 4), one launch
+    sequence per step (device packing, act-quant, grouped gate/up, grouped
+    down, expert-major weighted sum), rotating over the resident layers."""
+    from wohper_amd import workloads as wl
+
+    ids, sc, x = wl.zipf_batch_routes(seed=4, n_tokens=64)
+    npos, topk = ids.shape
+    used, counts = np.unique(ids, return_counts=True)
+    n_used = int(used.size)
+    nbytes = n_used * EXPERT_BYTES + npos * wl.HIDDEN * (2 + 4)
+    xb = wl.bf16_bits(x)
+    x_dev = ctx.device_alloc(xb.nbytes)
+    ids_dev = ctx.device_alloc(ids.nbytes)
+    sc_dev = ctx.device_alloc(sc.nbytes)
+    out_dev = ctx.device_alloc(npos * wl.HIDDEN * 4)
+    ctx.to_device(x_dev, xb)
+    ctx.to_device(ids_dev, ids)
+    ctx.to_device(sc_dev, sc)
+    for i in range(warmup):
+        ctx.moe_batch_async(i % n_layers, ids_dev, sc_dev, npos, topk, x_dev, True, out_dev)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    ctx.timer_start()
+    for i in range(steps):
+        ctx.moe_batch_async(i % n_layers, ids_dev, sc_dev, npos, topk, x_dev, True, out_dev)
+    dev_us = ctx.timer_stop() / steps
+    ctx.synchronize()
+    us = (time.perf_counter() - t0) / steps * 1e6
+    for p in (x_dev, ids_dev, sc_dev, out_dev):
+        ctx.device_free(p)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"workload": "ragged batched MoE: 64 bf16 tokens x top-6 of 256 FP4 experts, Zipf(1.1) popularity",
+            "experts_used": n_used, "largest_group": int(counts.max()),
+            "groups_ge_16": int((counts >= 16).sum()), "tokens_in_groups_ge_16": int(counts[counts >= 16].sum()),
+            "bytes_per_step": nbytes, "us_per_step": round(us, 2), "GBps": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "device_us_per_step": round(dev_us, 2),
+            "flops_per_step": npos * topk * 2 * 3 * wl.INTER * wl.HIDDEN,
+            "note": "wall clock and HIP events on the library stream; layers rotate so no step reuses cached weights"}
+
+
 def decode_stack(n_layers: int, steps: int, warmup: int, seed: int):
     """Full-depth synthetic stack at batch 1: per layer the FP8 projections
     of one decode layer (wq_a, wq_b, wkv, wo_a in 8 row groups, wo_b; f32
@@ -204,6 +246,7 @@ def main():
     ap.add_argument("--no-fp8", action="store_true")
     ap.add_argument("--stack-layers", type=int, default=43, help="layers of the full-depth stack leg (0: skip)")
     ap.add_argument("--stack-steps", type=int, default=20)
+    ap.add_argument("--batch-steps", type=int, default=20, help="steps of the ragged batch leg (0: skip)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 5 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -280,6 +323,9 @@ def main():
     if not args.no_fp8:
         extra["fp8_dense_gemv"] = fp8_dense(ctx, max(200, args.steps), 40)
         log(f"fp8 dense: {extra['fp8_dense_gemv']}")
+    if args.batch_steps > 0:
+        extra["ragged_batch"] = ragged_batch(ctx, args.layers, args.batch_steps, 3)
+        log(f"ragged batch: {extra['ragged_batch']}")
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(ctx.lib, seed, args.cpu_seconds)

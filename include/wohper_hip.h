@@ -178,6 +178,30 @@ int wh_routed_and_shared_experts_async(wh_ctx* ctx, const wh_expert_route* route
                                        uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
                                        int x_is_bf16, size_t n_tokens, float* out_dev);
 
+/* Batched routed experts for npos positions, expert-major, replacing the
+ * batch-prefill MoE of the reference: per-position weights score / sum (or
+ * 1 / topk when the sum is not finite and positive or a score is not finite)
+ * and the union of selected experts (E/server/generation.rs:2487-2506), then
+ * for each expert in ascending id and each of its positions
+ * acc_p += y * w, unfused, from 0 (accumulate_expert_for_positions,
+ * E/compute.rs:1779-1810).  With a shared expert (shared_expert !=
+ * WH_NO_SHARED_EXPERT), out_p = shared(x_p) + acc_p
+ * (finish_layer_deepseek_mhc_phase2_batch, E/compute.rs:1838-1852).
+ * route_ids / route_scores: [npos][topk] expert ids of layer_id and their
+ * router scores.  x: [npos][hidden]; out: [npos][hidden].  The reference
+ * takes expert blocks in I/O completion order; this takes them in ascending
+ * id, its submission order.  A route id that is not resident returns
+ * WH_NOT_RESIDENT (the async variant reports it through the stream status).
+ * The async variant takes device pointers (x f32 or bf16) and enqueues on
+ * the library stream; the grouping runs on the device. */
+#define WH_NO_SHARED_EXPERT 0xFFFFFFFFu
+int wh_moe_batch(wh_ctx* ctx, uint32_t layer_id, const uint32_t* route_ids, const float* route_scores, size_t npos,
+                 size_t topk, uint32_t shared_layer, uint32_t shared_expert, const float* x, size_t x_len,
+                 float* out, size_t out_len);
+int wh_moe_batch_async(wh_ctx* ctx, uint32_t layer_id, const uint32_t* route_ids_dev,
+                       const float* route_scores_dev, size_t npos, size_t topk, uint32_t shared_layer,
+                       uint32_t shared_expert, const void* x_dev, int x_is_bf16, float* out_dev);
+
 /* Device-pointer variant for the resident decode path: x_dev holds n_tokens
  * rows of `hidden` values (f32, or bf16 when x_is_bf16), all routed to the same
  * expert list; out_dev gets n_tokens rows of f32.  Stream-ordered. */

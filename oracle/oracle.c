@@ -594,6 +594,25 @@ void or_accumulate_expert(const float* y_per_target, const size_t* positions, co
     }
 }
 
+/* E/server/generation.rs:2491-2503 (the batch union's per-position weights):
+ * sum = sequential f32 sum of the scores; when the sum is finite and > 0
+ * and every score is finite, w_k = score_k / sum, else 1 / topk.  Unlike
+ * valid_route_weight_sum, negative scores and sums below f32::EPSILON pass. */
+void or_batch_route_weights(const float* scores, size_t npos, size_t topk, float* weights) {
+    for (size_t p = 0; p < npos; ++p) {
+        const float* s = scores + p * topk;
+        float sum = 0.0f;
+        int finite = 1;
+        for (size_t k = 0; k < topk; ++k) {
+            sum = sum + s[k];
+            finite = finite && isfinite(s[k]);
+        }
+        finite = finite && isfinite(sum) && sum > 0.0f;
+        float uniform = 1.0f / (float)topk;
+        for (size_t k = 0; k < topk; ++k) weights[p * topk + k] = finite ? s[k] / sum : uniform;
+    }
+}
+
 /* ----------------------------------------------------------- FP8 shared FFN */
 
 /* E/compute.rs:5545-5614 (compute_deepseek_fp8_shared_expert_into_hidden):

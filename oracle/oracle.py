@@ -58,6 +58,7 @@ def lib():
             "or_act_quant_scale": (c.c_float, [c.c_float]),
             "or_silu": (c.c_float, [c.c_float]),
             "or_swiglu": (c.c_float, [c.c_float, c.c_float]),
+            "or_batch_route_weights": (None, [f32p, sz, sz, f32p]),
             "or_fp4_expert_forward": (c.c_int, [c.POINTER(Fp4Spec)] * 3 + [f32p, sz, f32p, sz, f32p, sz, c.c_int]),
             "or_route_weight_sum": (c.c_int, [f32p, sz, f32p]),
             "or_routed_combine": (None, [f32p, f32p, sz, sz, f32p]),
@@ -211,6 +212,43 @@ def accumulate_expert(y_per_target, positions, weights, routed_acc):
     hidden = acc.shape[-1]
     lib().or_accumulate_expert(_pf(y), pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)), _pf(w), w.size,
                                hidden, _pf(acc))
+    return acc
+
+
+def batch_route_weights(scores):
+    """[npos, topk] router scores -> the batch union's weights
+    (E/server/generation.rs:2491-2503)."""
+    sc = _f(scores)
+    w = np.empty_like(sc)
+    npos, topk = sc.shape
+    lib().or_batch_route_weights(_pf(sc), npos, topk, _pf(w))
+    return w
+
+
+def moe_batch(experts, route_ids, route_scores, x, shared=None):
+    """The batch-prefill routed MoE (E/server/generation.rs:2487-2569): union
+    of the selected experts keyed by id, each expert's targets in position
+    order, experts taken in ascending id (the reference's submission order),
+    acc_p += y * w per target (accumulate_expert_for_positions,
+    E/compute.rs:1779-1810); with a shared expert out_p = shared(x_p) + acc_p
+    (E/compute.rs:1838-1852).  experts: id -> (w1, w3, w2) matrices as taken
+    by fp4_expert_forward; shared: one such triple or None."""
+    ids = np.asarray(route_ids)
+    x = _f(x)
+    npos, topk = ids.shape
+    w = batch_route_weights(route_scores)
+    union = {}
+    for p in range(npos):
+        for k in range(topk):
+            union.setdefault(int(ids[p, k]), []).append((p, w[p, k]))
+    acc = np.zeros_like(x)
+    for e in sorted(union):
+        targets = union[e]
+        ys = np.stack([fp4_expert_forward(*experts[e], x[p]) for p, _ in targets])
+        acc = accumulate_expert(ys, [p for p, _ in targets], [wt for _, wt in targets], acc)
+    if shared is not None:
+        sh = np.stack([fp4_expert_forward(*shared, x[p]) for p in range(npos)])
+        acc = (sh + acc).astype(np.float32)
     return acc
 
 

@@ -1,0 +1,137 @@
+"""GPU parity of the ragged batched routed experts (the batch-prefill MoE of
+E/server/generation.rs:2487-2569 with accumulate_expert_for_positions,
+E/compute.rs:1779-1810) against the oracle, bit-exact: device packing of the
+per-expert token lists, the per-position weight rule, ascending-id
+accumulation, the shared expert, chunking of large batches and the generic
+shapes."""
+import numpy as np
+import pytest
+
+import wohper_amd
+from wohper_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _store(ctx, layer, n, hidden, inter, seed):
+    for e in range(n):
+        ctx.store_expert_synthetic(layer, e, hidden, inter, seed)
+
+
+def _host(ctx, layer, ids, seed, hidden, inter):
+    return {int(e): wl.synth_expert_host(ctx.lib, seed, layer, int(e), hidden, inter) for e in np.unique(ids)}
+
+
+def _special_rows(ids, sc):
+    """Rows that exercise every branch of the weight rule."""
+    sc = sc.copy()
+    sc[0, 1] = np.nan                       # non-finite score -> uniform
+    sc[1, :] = 0.0                          # zero sum -> uniform
+    sc[2, 0] = -0.25                        # negative score, positive sum -> score / sum
+    sc[3, :] = -1.0                         # negative sum -> uniform
+    ids = ids.copy()
+    ids[4, 1] = ids[4, 0]                   # the same expert twice in one position
+    return ids, sc
+
+
+def test_batch_small_shapes_bit_exact(ctx, oracle):
+    hidden, inter, n_exp, seed = 512, 256, 24, 31
+    _store(ctx, 40, n_exp, hidden, inter, seed)
+    ctx.store_expert_synthetic(41, 0, hidden, inter, seed)  # shared
+    ids, sc, x = wl.zipf_batch_routes(seed=5, n_tokens=40, n_experts=n_exp, hidden=hidden)
+    ids, sc = _special_rows(ids, sc)
+    experts = _host(ctx, 40, ids, seed, hidden, inter)
+    want = oracle.moe_batch(experts, ids, sc, x)
+    got = ctx.moe_batch(40, ids, sc, x)
+    assert np.array_equal(bits(got), bits(want))
+    shared = wl.synth_expert_host(ctx.lib, seed, 41, 0, hidden, inter)
+    want_sh = oracle.moe_batch(experts, ids, sc, x, shared=shared)
+    got_sh = ctx.moe_batch(40, ids, sc, x, shared_key=(41, 0))
+    assert np.array_equal(bits(got_sh), bits(want_sh))
+
+
+def test_batch_one_position_one_route(ctx, oracle):
+    """A group of one token and a batch of one position."""
+    hidden, inter, seed = 512, 256, 31
+    _store(ctx, 40, 24, hidden, inter, seed)
+    x = np.random.default_rng(8).standard_normal((1, hidden)).astype(np.float32)
+    ids = np.array([[17]], np.uint32)
+    got = ctx.moe_batch(40, ids, np.array([[0.3]], np.float32), x)
+    want = oracle.fp4_expert_forward(*wl.synth_expert_host(ctx.lib, seed, 40, 17, hidden, inter), x[0])
+    assert np.array_equal(bits(got[0]), bits(want))
+
+
+def test_batch_real_shape_bf16_async(ctx, oracle):
+    """Expert shapes of the model (4096 x 2048), bf16 input, device pointers."""
+    n_exp, seed, npos = 16, 44, 8
+    _store(ctx, 42, n_exp, wl.HIDDEN, wl.INTER, seed)
+    ids, sc, x = wl.zipf_batch_routes(seed=6, n_tokens=npos, n_experts=n_exp)
+    experts = _host(ctx, 42, ids, seed, wl.HIDDEN, wl.INTER)
+    want = oracle.moe_batch(experts, ids, sc, x)
+    xb = wl.bf16_bits(x)
+    x_dev = ctx.device_alloc(xb.nbytes)
+    ids_dev = ctx.device_alloc(ids.nbytes)
+    sc_dev = ctx.device_alloc(sc.nbytes)
+    out_dev = ctx.device_alloc(x.nbytes)
+    ctx.to_device(x_dev, xb)
+    ctx.to_device(ids_dev, ids)
+    ctx.to_device(sc_dev, sc)
+    ctx.moe_batch_async(42, ids_dev, sc_dev, npos, ids.shape[1], x_dev, True, out_dev)
+    ctx.synchronize()
+    got = np.empty_like(x)
+    ctx.from_device(got, out_dev)
+    assert np.array_equal(bits(got), bits(want))
+    # the host-slice variant (f32 input) agrees
+    assert np.array_equal(bits(ctx.moe_batch(42, ids, sc, x)), bits(want))
+    # a route to an expert id that is not resident is reported by the stream
+    bad = ids.copy()
+    bad[3, 2] = 200
+    ctx.to_device(ids_dev, bad)
+    ctx.moe_batch_async(42, ids_dev, sc_dev, npos, ids.shape[1], x_dev, True, out_dev)
+    with pytest.raises(wohper_amd.DeepSeekV4KernelError) as e:
+        ctx.synchronize()
+    assert e.value.name == "NotResident"
+    with pytest.raises(wohper_amd.DeepSeekV4KernelError) as e:
+        ctx.moe_batch(42, bad, sc, x)
+    assert e.value.name == "NotResident"
+    for p in (x_dev, ids_dev, sc_dev, out_dev):
+        ctx.device_free(p)
+
+
+def test_batch_chunked_positions(ctx, oracle):
+    """More than 4096 slots: the positions are split into chunks."""
+    hidden, inter, n_exp, seed = 512, 256, 24, 31
+    _store(ctx, 40, n_exp, hidden, inter, seed)
+    ctx.store_expert_synthetic(41, 0, hidden, inter, seed)
+    ids, sc, x = wl.zipf_batch_routes(seed=9, n_tokens=700, n_experts=n_exp, hidden=hidden)
+    experts = _host(ctx, 40, ids, seed, hidden, inter)
+    shared = wl.synth_expert_host(ctx.lib, seed, 41, 0, hidden, inter)
+    got = ctx.moe_batch(40, ids, sc, x, shared_key=(41, 0))
+    want = oracle.moe_batch(experts, ids, sc, x, shared=shared)
+    assert np.array_equal(bits(got), bits(want))
+
+
+def test_batch_generic_shapes(ctx, oracle):
+    """Shapes outside the fast layout take the host-built union."""
+    rng = np.random.default_rng(12)
+    hidden, inter = 96, 40
+    experts = {}
+    for e in range(5):
+        m = []
+        for rows, cols in ((inter, hidden), (inter, hidden), (hidden, inter)):
+            p = rng.integers(0, 256, (rows, cols // 2)).astype(np.uint8)
+            s = rng.integers(118, 130, (rows, cols // 8)).astype(np.uint8)
+            m.append((p, s, rows, cols, cols // 8))
+        experts[e] = tuple(m)
+        ctx.store_fp4_expert(43, e, wohper_amd.DeepSeekV4Fp4Expert(*[wohper_amd.Fp4Matvec(*t) for t in m]))
+    ids = np.array([[4, 0, 2], [1, 4, 3], [2, 2, 0], [3, 1, 4], [0, 1, 2]], np.uint32)
+    sc = rng.uniform(0.1, 1.0, ids.shape).astype(np.float32)
+    sc[1, 0] = np.inf
+    x = rng.standard_normal((5, hidden)).astype(np.float32)
+    got = ctx.moe_batch(43, ids, sc, x)
+    want = oracle.moe_batch(experts, ids, sc, x)
+    assert np.array_equal(bits(got), bits(want))

@@ -69,3 +69,70 @@ def test_accumulate_expert_for_positions(oracle):
     assert np.array_equal(out[2], np.full(4, 0.5, np.float32))
     assert np.array_equal(out[0], np.full(4, 0.25, np.float32))
     assert np.array_equal(out[1], np.zeros(4, np.float32))
+
+
+def test_batch_route_weights_rules(oracle):
+    """The batch union's weights (E/server/generation.rs:2491-2503) differ from
+    valid_route_weight_sum: negative scores and tiny sums pass, only a sum
+    that is not finite and positive or a non-finite score goes uniform."""
+    f = oracle.batch_route_weights
+    assert f([[0.75, 0.25]]).tolist() == [[0.75, 0.25]]
+    assert f([[-0.5, 1.0]]).tolist() == [[-1.0, 2.0]]
+    assert f([[1e-30, 0.0]]).tolist() == [[1.0, 0.0]]
+    assert f([[0.3]]).tolist() == [[1.0]]
+    for bad in ([np.nan, 1.0], [np.inf, 1.0], [0.0, 0.0], [-1.0, -1.0], [3e38, 3e38], [1.0, -1.0]):
+        assert f([bad]).tolist() == [[0.5, 0.5]], bad
+    rng = np.random.default_rng(1)
+    s = rng.uniform(0.01, 1.0, (64, 6)).astype(np.float32)
+    w = f(s)
+    assert np.allclose(w.sum(axis=1), 1.0, rtol=0, atol=4e-7)
+    ratio = w / s
+    assert np.allclose(ratio, ratio[:, :1], rtol=2e-7, atol=0)
+
+
+def _small_expert(rng, hidden=64, inter=32):
+    mats = []
+    for rows, cols in ((inter, hidden), (inter, hidden), (hidden, inter)):
+        p = rng.integers(0, 256, (rows, cols // 2)).astype(np.uint8)
+        s = rng.integers(120, 132, (rows, cols // 32)).astype(np.uint8)
+        mats.append((p, s, rows, cols, cols // 32))
+    return tuple(mats)
+
+
+def test_moe_batch_order_and_independence(oracle):
+    """Experts are taken in ascending id whatever the route order, positions
+    do not mix, and a position's result is its weighted expert sum."""
+    rng = np.random.default_rng(5)
+    experts = {e: _small_expert(rng) for e in range(8)}
+    ids = np.array([[5, 1, 7, 2], [0, 3, 6, 4], [2, 7, 1, 5]], np.uint32)
+    sc = rng.uniform(0.1, 1.0, ids.shape).astype(np.float32)
+    x = (rng.standard_normal((3, 64)) * 4).astype(np.float32)
+    out = oracle.moe_batch(experts, ids, sc, x)
+    # the same routes listed in another order give the same bits
+    perm = np.array([3, 0, 2, 1])
+    assert np.array_equal(oracle.moe_batch(experts, ids[:, perm], sc[:, perm], x).view(np.uint32),
+                          out.view(np.uint32))
+    # positions are independent
+    for p in range(3):
+        one = oracle.moe_batch(experts, ids[p:p + 1], sc[p:p + 1], x[p:p + 1])
+        assert np.array_equal(one.view(np.uint32), out[p:p + 1].view(np.uint32))
+    # ... and each is the weighted sum of its experts' outputs
+    w = oracle.batch_route_weights(sc)
+    for p in range(3):
+        ys = np.stack([oracle.fp4_expert_forward(*experts[int(e)], x[p]) for e in ids[p]]).astype(np.float64)
+        want = (ys * w[p][:, None]).sum(axis=0)
+        assert np.allclose(out[p], want, rtol=1e-5, atol=1e-5 * np.abs(ys).max())
+    # summing in route order instead changes some bits on this case, so the
+    # permutation check above is a real constraint
+    route_order = np.zeros_like(x)
+    for p in range(3):
+        for k in range(4):
+            y = oracle.fp4_expert_forward(*experts[int(ids[p, k])], x[p])
+            route_order[p] = route_order[p] + y * w[p, k]
+    assert not np.array_equal(route_order.view(np.uint32), out.view(np.uint32))
+    # the shared expert adds after the routed sum
+    sh = _small_expert(rng)
+    with_sh = oracle.moe_batch(experts, ids, sc, x, shared=sh)
+    for p in range(3):
+        ys = oracle.fp4_expert_forward(*sh, x[p])
+        assert np.array_equal((ys + out[p]).view(np.uint32), with_sh[p].view(np.uint32))

@@ -54,6 +54,7 @@ STATUS_NAMES = {
 
 SCALE_UE8M0 = 0
 SCALE_F32 = 1
+NO_SHARED_EXPERT = 0xFFFFFFFF
 
 # every symbol include/wohper_hip.h declares
 EXPORTED = (
@@ -64,7 +65,7 @@ EXPORTED = (
     "wh_act_quant_dequant", "wh_routed_experts", "wh_routed_experts_async", "wh_fp8_gemv_async",
     "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop", "wh_profile_routed",
     "wh_store_fp8_synthetic", "wh_synth_fp8_host", "wh_routed_and_shared_experts", "wh_fp8_gemv_batch_async",
-    "wh_routed_and_shared_experts_async",
+    "wh_routed_and_shared_experts_async", "wh_moe_batch", "wh_moe_batch_async",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
 )
 
@@ -146,6 +147,10 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_profile_routed": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, sz, vp, c.c_int, vp, sz,
                                         c.POINTER(c.c_double)]),
         "wh_timer_stop": (c.c_int, [vp, c.POINTER(c.c_double)]),
+        "wh_moe_batch": (c.c_int, [vp, c.c_uint32, c.POINTER(c.c_uint32), f32p, sz, sz, c.c_uint32, c.c_uint32,
+                                   f32p, sz, f32p, sz]),
+        "wh_moe_batch_async": (c.c_int, [vp, c.c_uint32, vp, vp, sz, sz, c.c_uint32, c.c_uint32, vp, c.c_int,
+                                         vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -388,6 +393,32 @@ class Context:
         _check(self.lib.wh_routed_and_shared_experts_async(self._h, arr, n, shared_key[0], shared_key[1],
                                                            ctypes.c_void_p(x_ptr), int(x_is_bf16), n_tokens,
                                                            ctypes.c_void_p(out_ptr)), "routed_and_shared_experts_async")
+
+    def moe_batch(self, layer_id: int, route_ids, route_scores, x, shared_key=None) -> np.ndarray:
+        """Batched routed experts, expert-major (the batch-prefill MoE of
+        E/server/generation.rs:2487-2569 with accumulate_expert_for_positions,
+        E/compute.rs:1779-1810).  route_ids / route_scores: [npos, topk];
+        x: [npos, hidden] f32.  shared_key: (layer, expert) of the shared
+        expert, added as out = shared + routed."""
+        ids = np.ascontiguousarray(route_ids, dtype=np.uint32)
+        sc = _f32(route_scores)
+        x = _f32(x)
+        if ids.ndim != 2 or sc.shape != ids.shape or x.ndim != 2 or x.shape[0] != ids.shape[0]:
+            raise ValueError("route_ids/route_scores must be [npos, topk] and x [npos, hidden]")
+        out = np.zeros_like(x)
+        sl, se = shared_key if shared_key is not None else (0, NO_SHARED_EXPERT)
+        _check(self.lib.wh_moe_batch(self._h, layer_id, _p(ids, ctypes.c_uint32), _p(sc, ctypes.c_float),
+                                     ids.shape[0], ids.shape[1], sl, se, _p(x, ctypes.c_float), x.size,
+                                     _p(out, ctypes.c_float), out.size), "moe_batch")
+        return out
+
+    def moe_batch_async(self, layer_id: int, ids_ptr: int, scores_ptr: int, npos: int, topk: int, x_ptr: int,
+                        x_is_bf16: bool, out_ptr: int, shared_key=None):
+        """Device-pointer variant of moe_batch, enqueued on the library stream."""
+        sl, se = shared_key if shared_key is not None else (0, NO_SHARED_EXPERT)
+        _check(self.lib.wh_moe_batch_async(self._h, layer_id, ctypes.c_void_p(ids_ptr), ctypes.c_void_p(scores_ptr),
+                                           npos, topk, sl, se, ctypes.c_void_p(x_ptr), int(x_is_bf16),
+                                           ctypes.c_void_p(out_ptr)), "moe_batch_async")
 
     def timer_stop(self) -> float:
         """Device microseconds since timer_start (waits for the stream)."""

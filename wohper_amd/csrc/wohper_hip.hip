@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -103,6 +104,17 @@ struct Scratch {
     T* as() const { return (T*)p; }
 };
 
+// A layer's experts as a device array indexed by expert id, rebuilt after the
+// layer's store entries change.
+struct LayerTable {
+    wh_expert_ptrs* dev = nullptr;
+    uint32_t cap = 0;  // entries allocated
+    uint32_t n = 0;    // ids < n
+    bool valid = false;
+    bool fast = false;  // every resident expert has one fast shape
+    size_t hidden = 0, inter = 0;
+};
+
 struct HostBuf {
     void* p = nullptr;
     size_t n = 0;
@@ -130,8 +142,9 @@ struct wh_ctx {
     size_t device_bytes = 0;
     uint32_t* status = nullptr;  // device status word
     uint32_t* status_host = nullptr;
-    Scratch x_in, y_out, h, ybuf, cnt_y, tmp;
+    Scratch x_in, y_out, h, ybuf, cnt_y, tmp, batch, routes, bout;
     HostBuf stage_in, stage_out;
+    std::map<uint32_t, LayerTable> tables;  // device expert tables of the batch path
     std::mutex mu;
     hipEvent_t timer[2] = {nullptr, nullptr};  // wh_timer_start / wh_timer_stop
 };
@@ -171,6 +184,7 @@ int read_status(wh_ctx* c) {
         WH_HIP(hipMemsetAsync(c->status, 0, sizeof(uint32_t), c->stream));
         WH_HIP(hipStreamSynchronize(c->stream));
     }
+    if (st & WH_ST_NOT_RESIDENT) return WH_NOT_RESIDENT;
     if (st & WH_ST_NONFINITE_INPUT) return WH_NON_FINITE_INPUT;
     if (st & WH_ST_NONFINITE_OUTPUT) return WH_NON_FINITE_OUTPUT;
     return WH_OK;
@@ -264,6 +278,10 @@ hipError_t kernel_setup_once(int device) {
         set((const void*)k_moe_gateup<16>);
         set((const void*)k_moe_down<0>);
         set((const void*)k_moe_down<8>);
+        set((const void*)k_moe_batch_gateup<0>);
+        set((const void*)k_moe_batch_gateup<16>);
+        set((const void*)k_moe_batch_down<0>);
+        set((const void*)k_moe_batch_down<8>);
         if (e == hipSuccess) {
             g_max_lds = (size_t)lds;
         } else {
@@ -580,6 +598,248 @@ __global__ void k_synth_fp8(uint8_t* w, uint32_t rows, uint32_t cols, uint64_t s
     w[id] = wh_fp8_synth_code(seed, stream, row * cols + col);
 }
 
+// ------------------------------------------------------ batched routed experts
+// Device table of a layer's experts (ids < n), rebuilt when the layer's store
+// entries changed.  Experts of any shape may be resident; the fast batch
+// path needs one fast shape for all of them.
+int layer_table(wh_ctx* c, uint32_t layer, LayerTable** out) {
+    LayerTable& t = c->tables[layer];
+    *out = &t;
+    if (t.valid) return WH_OK;
+    auto lo = c->experts.lower_bound({layer, 0u});
+    auto hi = c->experts.upper_bound({layer, 0xffffffffu});
+    uint32_t n = 0;
+    for (auto it = lo; it != hi; ++it) n = std::max(n, it->first.second + 1);
+    std::vector<wh_expert_ptrs> host(n);
+    std::memset(host.data(), 0, n * sizeof(wh_expert_ptrs));
+    bool fast = n > 0 && n < WH_BATCH_MAX_TABLE;  // one id stays free for the shared expert
+    size_t hidden = 0, inter = 0;
+    for (auto it = lo; it != hi; ++it) {
+        ExpertView v;
+        if (resolve_expert(c, layer, it->first.second, &v) != WH_OK) continue;  // released tensors
+        if (hidden == 0) {
+            hidden = v.w1->cols;
+            inter = v.w1->rows;
+        }
+        fast = fast && expert_fast(v) && v.w1->cols == hidden && v.w1->rows == inter && v.w2->rows == hidden;
+        wh_expert_ptrs& p = host[it->first.second];
+        p.w1 = v.w1->w;
+        p.s1 = (const uint8_t*)v.w1->s;
+        p.w3 = v.w3->w;
+        p.s3 = (const uint8_t*)v.w3->s;
+        p.w2 = v.w2->w;
+        p.s2 = (const uint8_t*)v.w2->s;
+    }
+    // kernels of earlier calls may still read the old table
+    WH_HIP(hipStreamSynchronize(c->stream));
+    if (n > t.cap) {
+        if (t.dev) (void)hipFree(t.dev);
+        t.dev = nullptr;
+        t.cap = 0;
+        WH_HIP(hipMalloc((void**)&t.dev, n * sizeof(wh_expert_ptrs)));
+        t.cap = n;
+    }
+    if (n) WH_HIP(hipMemcpy(t.dev, host.data(), n * sizeof(wh_expert_ptrs), hipMemcpyHostToDevice));
+    t.n = n;
+    t.fast = fast;
+    t.hidden = hidden;
+    t.inter = inter;
+    t.valid = true;
+    return WH_OK;
+}
+
+// Workgroups of a persistent kernel that fit on the device at once.
+int persistent_grid(const void* kernel, size_t lds, unsigned* grid) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, size_t>, unsigned> cache;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find({kernel, lds});
+    if (it != cache.end()) {
+        *grid = it->second;
+        return WH_OK;
+    }
+    int dev = 0, cus = 0, per_cu = 0;
+    WH_HIP(hipGetDevice(&dev));
+    WH_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    WH_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds));
+    *grid = (unsigned)std::max(1, cus * std::max(1, per_cu));
+    cache[{kernel, lds}] = *grid;
+    return WH_OK;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// Device layout of one batch chunk inside c->batch.
+struct BatchBufs {
+    float* wgt;
+    uint32_t *sorted, *uexp, *uoff, *uorder, *acc_order, *meta;
+    float *xq, *h, *y;
+};
+int batch_bufs(wh_ctx* c, size_t npos, size_t slots, size_t hidden, size_t inter, BatchBufs* b) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = off;
+        off += align256(bytes);
+        return o;
+    };
+    const size_t o_w = take(slots * 4), o_so = take(slots * 4), o_ue = take(slots * 4), o_uo = take((slots + 1) * 4),
+                 o_ur = take(slots * 4), o_ac = take(slots * 4), o_me = take(16 * 4),
+                 o_xq = take(npos * hidden * 4), o_h = take(slots * inter * 4), o_y = take(slots * hidden * 4);
+    WH_HIP(c->batch.ensure(off, false));
+    uint8_t* base = c->batch.as<uint8_t>();
+    b->wgt = (float*)(base + o_w);
+    b->sorted = (uint32_t*)(base + o_so);
+    b->uexp = (uint32_t*)(base + o_ue);
+    b->uoff = (uint32_t*)(base + o_uo);
+    b->uorder = (uint32_t*)(base + o_ur);
+    b->acc_order = (uint32_t*)(base + o_ac);
+    b->meta = (uint32_t*)(base + o_me);
+    b->xq = (float*)(base + o_xq);
+    b->h = (float*)(base + o_h);
+    b->y = (float*)(base + o_y);
+    return WH_OK;
+}
+
+// Fast batch path over positions [0, npos) in chunks of at most
+// WH_BATCH_MAX_ASSIGN slots; positions are independent, so chunking changes
+// no result.  ids/scores/x/out are device pointers.
+int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const float* scores, size_t npos,
+                   size_t topk, const ExpertView* shared, const void* x, int x_bf16, float* out) {
+    const size_t hidden = t.hidden, inter = t.inter;
+    const size_t per_pos = topk + (shared ? 1 : 0);
+    const size_t chunk = WH_BATCH_MAX_ASSIGN / per_pos;
+    BatchBufs b;
+    WH_TRY(batch_bufs(c, std::min(npos, chunk), std::min(npos, chunk) * per_pos, hidden, inter, &b));
+    const void* kg = hidden == 4096 ? (const void*)k_moe_batch_gateup<16> : (const void*)k_moe_batch_gateup<0>;
+    const void* kd = inter == 2048 ? (const void*)k_moe_batch_down<8> : (const void*)k_moe_batch_down<0>;
+    const size_t lds_g = wh_batch_wg_lds(hidden), lds_d = wh_batch_wg_lds(inter);
+    unsigned grid_g = 0, grid_d = 0;
+    WH_TRY(persistent_grid(kg, lds_g, &grid_g));
+    WH_TRY(persistent_grid(kd, lds_d, &grid_d));
+    for (size_t p0 = 0; p0 < npos; p0 += chunk) {
+        const size_t n = std::min(chunk, npos - p0), slots = n * per_pos;
+        wh_batch_args a;
+        std::memset(&a, 0, sizeof a);
+        a.table = t.dev;
+        a.n_table = t.n;
+        a.route_ids = ids + p0 * topk;
+        a.route_scores = scores + p0 * topk;
+        a.npos = (uint32_t)n;
+        a.topk = (uint32_t)topk;
+        a.hidden = (uint32_t)hidden;
+        a.inter = (uint32_t)inter;
+        a.x = x_bf16 ? (const void*)((const uint16_t*)x + p0 * hidden) : (const void*)((const float*)x + p0 * hidden);
+        a.x_is_bf16 = x_bf16 ? 1u : 0u;
+        if (shared) {
+            a.has_shared = 1;
+            a.shared.w1 = shared->w1->w;
+            a.shared.s1 = (const uint8_t*)shared->w1->s;
+            a.shared.w3 = shared->w3->w;
+            a.shared.s3 = (const uint8_t*)shared->w3->s;
+            a.shared.w2 = shared->w2->w;
+            a.shared.s2 = (const uint8_t*)shared->w2->s;
+        }
+        a.wgt = b.wgt;
+        a.sorted = b.sorted;
+        a.uexp = b.uexp;
+        a.uoff = b.uoff;
+        a.uorder = b.uorder;
+        a.acc_order = b.acc_order;
+        a.meta = b.meta;
+        a.xq = b.xq;
+        a.h = b.h;
+        a.y = b.y;
+        a.out = out + p0 * hidden;
+        a.status = c->status;
+        // the most items the queues can hold: used experts <= min(slots, ids)
+        const size_t max_used = std::min(slots, (size_t)t.n + (shared ? 1 : 0));
+        const unsigned gg = (unsigned)std::min<size_t>(grid_g, max_used * (inter / 16));
+        const unsigned gd = (unsigned)std::min<size_t>(grid_d, max_used * (hidden / 32));
+        k_moe_batch_pack<<<1, 256, 0, c->stream>>>(a);
+        k_moe_batch_xq<<<(unsigned)((n * hidden / 16 + 255) / 256), 256, 0, c->stream>>>(a);
+        if (hidden == 4096) k_moe_batch_gateup<16><<<gg, 256, lds_g, c->stream>>>(a);
+        else k_moe_batch_gateup<0><<<gg, 256, lds_g, c->stream>>>(a);
+        if (inter == 2048) k_moe_batch_down<8><<<gd, 256, lds_d, c->stream>>>(a);
+        else k_moe_batch_down<0><<<gd, 256, lds_d, c->stream>>>(a);
+        k_moe_batch_accumulate<<<dim3((unsigned)((hidden + 255) / 256), (unsigned)n), 256, 0, c->stream>>>(a);
+        WH_HIP(hipGetLastError());
+    }
+    return WH_OK;
+}
+
+// acc[i] = acc[i] + y[i] * w, unfused (E/compute.rs:1804-1807)
+__global__ void k_axpy_unfused(float* acc, const float* y, float w, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float v = y[i] * w;
+        acc[i] = acc[i] + v;
+    }
+}
+// out[i] = shared[i] + out[i] (E/compute.rs:1845-1848)
+__global__ void k_add_shared(float* out, const float* sh, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = sh[i] + out[i];
+}
+
+// Per-position weights of the batch path (E/server/generation.rs:2495-2503).
+void batch_weights(const float* sc, size_t topk, float* w) {
+    float sum = 0.0f;
+    bool finite = true;
+    for (size_t k = 0; k < topk; ++k) {
+        finite = finite && std::fabs(sc[k]) <= 3.4028235e38f;
+        sum = sum + sc[k];
+    }
+    finite = finite && std::fabs(sum) <= 3.4028235e38f && sum > 0.0f;
+    const float uniform = 1.0f / (float)topk;
+    for (size_t k = 0; k < topk; ++k) w[k] = finite ? sc[k] / sum : uniform;
+}
+
+// Generic batch path (any shape the single-expert path accepts): the union
+// is built on the host and each (expert, position) runs the expert forward.
+// ids/scores are host arrays; x (f32) and out are device pointers.
+int moe_batch_generic(wh_ctx* c, uint32_t layer, const uint32_t* ids, const float* scores, size_t npos,
+                      size_t topk, const ExpertView* shared, const float* x, float* out) {
+    std::map<uint32_t, std::vector<std::pair<size_t, float>>> uni;
+    std::vector<float> w(topk);
+    size_t hidden = 0, osz = 0;
+    for (size_t p = 0; p < npos; ++p) {
+        batch_weights(scores + p * topk, topk, w.data());
+        for (size_t k = 0; k < topk; ++k) uni[ids[p * topk + k]].push_back({p, w[k]});
+    }
+    std::vector<std::pair<uint32_t, ExpertView>> ev;
+    for (auto& kv : uni) {
+        ExpertView v;
+        WH_TRY(resolve_expert(c, layer, kv.first, &v));
+        if (hidden == 0) {
+            hidden = v.w1->cols;
+            osz = v.w2->rows;
+        }
+        if (v.w1->cols != hidden || v.w2->rows != osz) return WH_INVALID_SHAPE;
+        ev.push_back({kv.first, v});
+    }
+    if (shared && (shared->w1->cols != hidden || shared->w2->rows != osz)) return WH_INVALID_SHAPE;
+    if (osz != hidden) return WH_INVALID_SHAPE;  // routed_acc rows are hidden wide
+    WH_HIP(c->y_out.ensure(osz * sizeof(float), false));
+    float* y = c->y_out.as<float>();
+    WH_HIP(hipMemsetAsync(out, 0, npos * osz * sizeof(float), c->stream));
+    const float one = 1.0f;
+    const unsigned blocks = (unsigned)((osz + 255) / 256);
+    for (auto& e : ev) {
+        for (auto& tgt : uni[e.first]) {
+            WH_TRY(moe_forward(c, &e.second, &one, 1, false, x + tgt.first * hidden, 0, 1, y));
+            k_axpy_unfused<<<blocks, 256, 0, c->stream>>>(out + tgt.first * osz, y, tgt.second, (uint32_t)osz);
+        }
+    }
+    if (shared) {
+        for (size_t p = 0; p < npos; ++p) {
+            WH_TRY(moe_forward(c, shared, &one, 1, false, x + p * hidden, 0, 1, y));
+            k_add_shared<<<blocks, 256, 0, c->stream>>>(out + p * osz, y, (uint32_t)osz);
+        }
+    }
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
 int store_tensor_common(wh_ctx* c, Tensor&& t, wh_tensor* out) {
     wh_tensor id = c->next_id++;
     c->tensors.emplace(id, std::move(t));
@@ -652,8 +912,10 @@ int wh_shutdown(wh_ctx* c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     c->arena.release_all();
-    for (Scratch* s : {&c->x_in, &c->y_out, &c->h, &c->ybuf, &c->cnt_y, &c->tmp})
+    for (Scratch* s : {&c->x_in, &c->y_out, &c->h, &c->ybuf, &c->cnt_y, &c->tmp, &c->batch, &c->routes, &c->bout})
         if (s->p) (void)hipFree(s->p);
+    for (auto& kv : c->tables)
+        if (kv.second.dev) (void)hipFree(kv.second.dev);
     for (HostBuf* h : {&c->stage_in, &c->stage_out})
         if (h->p) (void)hipHostFree(h->p);
     for (hipEvent_t e : c->timer)
@@ -778,6 +1040,7 @@ int wh_store_expert(wh_ctx* c, uint32_t layer, uint32_t expert, wh_tensor w1, wh
     // E/compute.rs:1263-1265
     if (t1->cols != t3->cols || t1->rows != t3->rows || t2->cols != t1->rows) return WH_INVALID_SHAPE;
     c->experts[{layer, expert}] = Expert{w1, w3, w2};
+    c->tables[layer].valid = false;
     return WH_OK;
 }
 
@@ -822,6 +1085,7 @@ int wh_store_expert_synthetic(wh_ctx* c, uint32_t layer, uint32_t expert, size_t
     }
     WH_HIP(hipStreamSynchronize(c->stream));
     c->experts[{layer, expert}] = Expert{ids[0], ids[1], ids[2]};
+    c->tables[layer].valid = false;
     return WH_OK;
 }
 
@@ -868,6 +1132,7 @@ int wh_store_release(wh_ctx* c, wh_tensor t) {
     if (it == c->tensors.end()) return WH_NOT_RESIDENT;
     // arena memory is reclaimed at shutdown; the handle stops resolving now
     c->tensors.erase(it);
+    for (auto& kv : c->tables) kv.second.valid = false;
     return WH_OK;
 }
 
@@ -1131,6 +1396,96 @@ int wh_routed_and_shared_experts_async(wh_ctx* c, const wh_expert_route* routes,
     float wts[WH_MAX_EXPERTS];
     WH_TRY(routed_shared_common(c, routes, n, shared_layer, shared_expert, ev, wts));
     return moe_forward(c, ev, wts, n + 1, true, x_dev, x_bf16, n_tokens, out_dev);
+}
+
+// ------------------------------------------------------ batched routed experts
+// Shared lookups of both batch entry points: the layer table, the shared
+// expert, and whether the fast path applies.
+static int batch_setup(wh_ctx* c, uint32_t layer, size_t npos, size_t topk, uint32_t shared_layer,
+                       uint32_t shared_expert, LayerTable** t, ExpertView* shared, bool* has_shared, bool* fast) {
+    if (npos == 0 || topk == 0) return WH_INVALID_ARGUMENT;
+    WH_TRY(layer_table(c, layer, t));
+    if ((*t)->n == 0) return WH_NOT_RESIDENT;
+    *has_shared = shared_expert != WH_NO_SHARED_EXPERT;
+    if (*has_shared) WH_TRY(resolve_expert(c, shared_layer, shared_expert, shared));
+    *fast = (*t)->fast && topk <= WH_BATCH_MAX_TOPK && topk + (*has_shared ? 1 : 0) <= WH_BATCH_MAX_ASSIGN &&
+            wh_batch_wg_lds((*t)->hidden) <= g_max_lds && wh_batch_wg_lds((*t)->inter) <= g_max_lds;
+    if (*has_shared)
+        *fast = *fast && expert_fast(*shared) && shared->w1->cols == (*t)->hidden &&
+                shared->w1->rows == (*t)->inter && shared->w2->rows == (*t)->hidden;
+    return WH_OK;
+}
+
+int wh_moe_batch(wh_ctx* c, uint32_t layer_id, const uint32_t* route_ids, const float* route_scores, size_t npos,
+                 size_t topk, uint32_t shared_layer, uint32_t shared_expert, const float* x, size_t x_len,
+                 float* out, size_t out_len) {
+    if (!c || !route_ids || !route_scores || !x || !out) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    LayerTable* t = nullptr;
+    ExpertView sh;
+    bool has_shared = false, fast = false;
+    WH_TRY(batch_setup(c, layer_id, npos, topk, shared_layer, shared_expert, &t, &sh, &has_shared, &fast));
+    for (size_t i = 0; i < npos * topk; ++i)
+        if (!c->experts.count({layer_id, route_ids[i]})) return WH_NOT_RESIDENT;
+    size_t hidden = t->hidden;
+    if (!fast) {
+        ExpertView v;
+        WH_TRY(resolve_expert(c, layer_id, route_ids[0], &v));
+        hidden = v.w1->cols;
+    }
+    if (x_len < npos * hidden) return WH_INPUT_TOO_SMALL;
+    if (out_len < npos * hidden) return WH_OUTPUT_TOO_SMALL;
+    WH_HIP(c->x_in.ensure(npos * hidden * sizeof(float), false));
+    WH_HIP(c->bout.ensure(npos * hidden * sizeof(float), false));
+    WH_HIP(c->stage_out.ensure(npos * hidden * sizeof(float)));
+    WH_HIP(hipMemcpyAsync(c->x_in.p, x, npos * hidden * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    if (fast) {
+        WH_HIP(c->routes.ensure(npos * topk * 8, false));
+        uint32_t* ids_dev = c->routes.as<uint32_t>();
+        float* sc_dev = (float*)(ids_dev + npos * topk);
+        WH_HIP(hipMemcpyAsync(ids_dev, route_ids, npos * topk * 4, hipMemcpyHostToDevice, c->stream));
+        WH_HIP(hipMemcpyAsync(sc_dev, route_scores, npos * topk * 4, hipMemcpyHostToDevice, c->stream));
+        WH_TRY(moe_batch_fast(c, *t, ids_dev, sc_dev, npos, topk, has_shared ? &sh : nullptr, c->x_in.p, 0,
+                              c->bout.as<float>()));
+    } else {
+        WH_TRY(moe_batch_generic(c, layer_id, route_ids, route_scores, npos, topk, has_shared ? &sh : nullptr,
+                                 c->x_in.as<float>(), c->bout.as<float>()));
+    }
+    WH_HIP(hipMemcpyAsync(c->stage_out.p, c->bout.p, npos * hidden * sizeof(float), hipMemcpyDeviceToHost,
+                          c->stream));
+    int st = read_status(c);
+    if (st != WH_OK) return st;
+    std::memcpy(out, c->stage_out.p, npos * hidden * sizeof(float));
+    return WH_OK;
+}
+
+int wh_moe_batch_async(wh_ctx* c, uint32_t layer_id, const uint32_t* route_ids_dev, const float* route_scores_dev,
+                       size_t npos, size_t topk, uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
+                       int x_is_bf16, float* out_dev) {
+    if (!c || !route_ids_dev || !route_scores_dev || !x_dev || !out_dev) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    LayerTable* t = nullptr;
+    ExpertView sh;
+    bool has_shared = false, fast = false;
+    WH_TRY(batch_setup(c, layer_id, npos, topk, shared_layer, shared_expert, &t, &sh, &has_shared, &fast));
+    if (fast) {
+        if (((uintptr_t)x_dev & 15) || ((uintptr_t)out_dev & 3) || ((uintptr_t)route_ids_dev & 3) ||
+            ((uintptr_t)route_scores_dev & 3))
+            return WH_INVALID_ARGUMENT;
+        return moe_batch_fast(c, *t, route_ids_dev, route_scores_dev, npos, topk, has_shared ? &sh : nullptr, x_dev,
+                              x_is_bf16, out_dev);
+    }
+    // generic shapes: the union is built on the host
+    if (x_is_bf16) return WH_UNSUPPORTED;
+    std::vector<uint32_t> ids(npos * topk);
+    std::vector<float> sc(npos * topk);
+    WH_HIP(hipMemcpyAsync(ids.data(), route_ids_dev, ids.size() * 4, hipMemcpyDeviceToHost, c->stream));
+    WH_HIP(hipMemcpyAsync(sc.data(), route_scores_dev, sc.size() * 4, hipMemcpyDeviceToHost, c->stream));
+    WH_HIP(hipStreamSynchronize(c->stream));
+    return moe_batch_generic(c, layer_id, ids.data(), sc.data(), npos, topk, has_shared ? &sh : nullptr,
+                             (const float*)x_dev, out_dev);
 }
 
 int wh_fp4_expert_forward(wh_ctx* c, uint32_t layer, uint32_t expert, const float* input,

@@ -72,6 +72,30 @@ def moe_token_case(seed=2, n_experts=N_ROUTED):
     return idx, w, x
 
 
+def zipf_batch_routes(seed=4, n_tokens=64, n_experts=N_ROUTED, k=TOPK, s=1.1, hidden=HIDDEN):
+    """Ragged batch: expert popularity p(perm[r]) proportional to (r + 1)^-s
+    over a seeded permutation; each token draws k distinct experts by
+    sequential weighted sampling without replacement; router scores are the
+    sigmoid of per-token N(0,1) logits (the batch rule normalizes them);
+    x ~ N(0,1) rounded to bf16.  Returns (ids [n, k] u32, scores [n, k] f32,
+    x [n, hidden] f32)."""
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(n_experts)
+    pop = np.empty(n_experts)
+    pop[perm] = np.arange(1, n_experts + 1, dtype=np.float64) ** -s
+    ids = np.empty((n_tokens, k), np.uint32)
+    for t in range(n_tokens):
+        avail = pop.copy()
+        for j in range(k):
+            e = rng.choice(n_experts, p=avail / avail.sum())
+            ids[t, j] = e
+            avail[e] = 0.0
+    logits = rng.standard_normal((n_tokens, k))
+    scores = (1.0 / (1.0 + np.exp(-logits))).astype(np.float32)
+    x = bf16_round(rng.standard_normal((n_tokens, hidden)).astype(np.float32))
+    return ids, scores, x
+
+
 def synth_fp4_host(lib, seed: int, layer: int, expert: int, matrix: int, rows: int, cols: int,
                    scale_lo=SCALE_LO, scale_hi=SCALE_HI):
     """Host copy of the bytes wh_store_expert_synthetic writes for matrix 0/1/2
