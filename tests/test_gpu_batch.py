@@ -1,9 +1,13 @@
 """GPU parity of the ragged batched routed experts (the batch-prefill MoE of
 E/server/generation.rs:2487-2569 with accumulate_expert_for_positions,
-E/compute.rs:1779-1810) against the oracle, bit-exact: device packing of the
-per-expert token lists, the per-position weight rule, ascending-id
-accumulation, the shared expert, chunking of large batches and the generic
-shapes."""
+E/compute.rs:1779-1810) against the oracle.
+
+Exact path (every expert below the MFMA threshold): bit-exact - device
+packing of the per-expert token lists, the per-position weight rule,
+ascending-id accumulation, the shared expert, chunking of large batches and
+the generic shapes.  MFMA path (experts at or above the threshold): every
+matvec within max|diff| <= 1e-5 * ||w_row||_2 * ||x||_2 of the oracle on the
+same input, every other stage bit-exact."""
 import numpy as np
 import pytest
 
@@ -11,6 +15,15 @@ import wohper_amd
 from wohper_amd import workloads as wl
 
 pytestmark = pytest.mark.gpu
+DEFAULT_MFMA_MIN = 16
+
+
+@pytest.fixture(autouse=True)
+def exact_path(ctx):
+    """Tests compare bit-exactly unless they opt into MFMA groups."""
+    ctx.set_moe_mfma_min(0)
+    yield
+    ctx.set_moe_mfma_min(DEFAULT_MFMA_MIN)
 
 
 def bits(a):
@@ -135,3 +148,93 @@ def test_batch_generic_shapes(ctx, oracle):
     got = ctx.moe_batch(43, ids, sc, x)
     want = oracle.moe_batch(experts, ids, sc, x)
     assert np.array_equal(bits(got), bits(want))
+
+
+def _dequant(oracle, m):
+    """Reference dequantized FP4 matrix (float64) of (packed, scales, rows, cols, scale_cols)."""
+    packed, scales, rows, cols, scale_cols = m
+    _, ue, fp4, _ = oracle.luts()
+    packed = np.asarray(packed, np.uint8).reshape(rows, cols // 2)
+    nib = np.empty((rows, cols), np.uint8)
+    nib[:, 0::2] = packed & 15
+    nib[:, 1::2] = packed >> 4
+    sc = ue[np.asarray(scales, np.uint8).reshape(rows, scale_cols)].astype(np.float64)
+    return fp4[nib].astype(np.float64) * np.repeat(sc, cols // scale_cols, axis=1)
+
+
+_ROW_NORMS = {}
+
+
+def _row_norms(oracle, m):
+    key = (id(m[0]), id(m[1]))
+    if key not in _ROW_NORMS:
+        w = _dequant(oracle, m)
+        _ROW_NORMS[key] = (m, np.sqrt((w * w).sum(axis=1)))
+    return _ROW_NORMS[key][1]
+
+
+def _check_matvec(oracle, m, x, got, exact, what):
+    want = oracle.fp4_matvec(*m, x)
+    if exact:
+        assert np.array_equal(bits(got), bits(want)), what
+        return 0.0
+    tol = 1e-5 * _row_norms(oracle, m) * np.linalg.norm(np.asarray(x, np.float64))
+    diff = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.all(diff <= tol), (what, float((diff / tol).max()))
+    return float((diff / tol).max())
+
+
+def _mfma_case(ctx, oracle, layer, n_exp, hidden, inter, seed, npos, mfma_min):
+    _store(ctx, layer, n_exp, hidden, inter, seed)
+    ids, sc, x = wl.zipf_batch_routes(seed=seed, n_tokens=npos, n_experts=n_exp, hidden=hidden)
+    experts = _host(ctx, layer, ids, seed, hidden, inter)
+    topk, S = ids.shape[1], ids.size
+    ctx.set_moe_mfma_min(mfma_min)
+    rd = ctx.debug_moe_batch_read
+    # gate and up matvecs, raw
+    ctx.debug_moe_batch(wohper_amd.DEBUG_RAW_GATEUP)
+    ctx.moe_batch(layer, ids, sc, x)
+    srt, gate, up = rd(0, S, np.uint32), rd(1, (S, inter), np.float32), rd(2, (S, inter), np.float32)
+    meta, uoff, uexp, uorder = rd(4, 8, np.uint32), rd(5, S + 1, np.uint32), rd(6, S, np.uint32), rd(7, S, np.uint32)
+    n_used, n_mfma = int(meta[0]), int(meta[4])
+    assert 0 < n_mfma < n_used, (n_used, n_mfma)  # both paths run
+    on_mfma = {int(uexp[j]) for j in uorder[:n_mfma]}
+    xq = {p: oracle.act_quant(x[p], 64) for p in range(npos)}
+    worst = 0.0
+    for j in range(n_used):
+        e = int(uexp[j])
+        w1, w3, _ = experts[e]
+        for s in range(int(uoff[j]), int(uoff[j + 1])):
+            p = int(srt[s]) // topk
+            worst = max(worst, _check_matvec(oracle, w1, xq[p], gate[s], e not in on_mfma, ("gate", e, p)))
+            worst = max(worst, _check_matvec(oracle, w3, xq[p], up[s], e not in on_mfma, ("up", e, p)))
+    # the full call: act-quant of the SwiGLU outputs, down, weighted sum
+    out = ctx.moe_batch(layer, ids, sc, x)
+    h, hq, y = rd(1, (S, inter), np.float32), rd(2, (S, inter), np.float32), rd(3, (S, hidden), np.float32)
+    wts = oracle.batch_route_weights(sc)
+    acc = np.zeros_like(x)
+    for j in range(n_used):
+        e = int(uexp[j])
+        rng_ = range(int(uoff[j]), int(uoff[j + 1]))
+        for s in rng_:
+            assert np.array_equal(bits(hq[s]), bits(oracle.act_quant(h[s], 64))), ("act-quant", s)
+            worst = max(worst, _check_matvec(oracle, experts[e][2], hq[s], y[s], e not in on_mfma, ("down", e, s)))
+        pos = [int(srt[s]) // topk for s in rng_]
+        acc = oracle.accumulate_expert(y[list(rng_)], pos, [wts[int(srt[s]) // topk, int(srt[s]) % topk] for s in rng_],
+                                       acc)
+    assert np.array_equal(bits(out), bits(acc))
+    # end to end, the act-quant of h may round a near-tie the other way, so
+    # the oracle's output is compared in norm only
+    want = oracle.moe_batch(experts, ids, sc, x)
+    assert np.linalg.norm(out - want) <= 1e-3 * np.linalg.norm(want)
+    return worst
+
+
+def test_batch_mfma_small_shapes(ctx, oracle):
+    worst = _mfma_case(ctx, oracle, 44, 12, 512, 256, 33, 48, 8)
+    print(f"worst MFMA matvec |diff| / tolerance: {worst:.3f}")
+
+
+def test_batch_mfma_real_shapes(ctx, oracle):
+    worst = _mfma_case(ctx, oracle, 45, 8, wl.HIDDEN, wl.INTER, 34, 24, DEFAULT_MFMA_MIN)
+    print(f"worst MFMA matvec |diff| / tolerance: {worst:.3f}")

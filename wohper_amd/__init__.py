@@ -55,6 +55,7 @@ STATUS_NAMES = {
 SCALE_UE8M0 = 0
 SCALE_F32 = 1
 NO_SHARED_EXPERT = 0xFFFFFFFF
+DEBUG_RAW_GATEUP = 1
 
 # every symbol include/wohper_hip.h declares
 EXPORTED = (
@@ -65,7 +66,8 @@ EXPORTED = (
     "wh_act_quant_dequant", "wh_routed_experts", "wh_routed_experts_async", "wh_fp8_gemv_async",
     "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop", "wh_profile_routed",
     "wh_store_fp8_synthetic", "wh_synth_fp8_host", "wh_routed_and_shared_experts", "wh_fp8_gemv_batch_async",
-    "wh_routed_and_shared_experts_async", "wh_moe_batch", "wh_moe_batch_async",
+    "wh_routed_and_shared_experts_async", "wh_moe_batch", "wh_moe_batch_async", "wh_set_moe_mfma_min",
+    "wh_debug_moe_batch", "wh_debug_moe_batch_read",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
 )
 
@@ -151,6 +153,9 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
                                    f32p, sz, f32p, sz]),
         "wh_moe_batch_async": (c.c_int, [vp, c.c_uint32, vp, vp, sz, sz, c.c_uint32, c.c_uint32, vp, c.c_int,
                                          vp]),
+        "wh_set_moe_mfma_min": (c.c_int, [vp, c.c_uint32]),
+        "wh_debug_moe_batch": (c.c_int, [vp, c.c_uint32]),
+        "wh_debug_moe_batch_read": (c.c_int, [vp, c.c_int, vp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -419,6 +424,19 @@ class Context:
         _check(self.lib.wh_moe_batch_async(self._h, layer_id, ctypes.c_void_p(ids_ptr), ctypes.c_void_p(scores_ptr),
                                            npos, topk, sl, se, ctypes.c_void_p(x_ptr), int(x_is_bf16),
                                            ctypes.c_void_p(out_ptr)), "moe_batch_async")
+
+    def set_moe_mfma_min(self, min_tokens: int):
+        """Batch experts with at least min_tokens tokens run on MFMA (0: none)."""
+        _check(self.lib.wh_set_moe_mfma_min(self._h, min_tokens), "set_moe_mfma_min")
+
+    def debug_moe_batch(self, flags: int):
+        _check(self.lib.wh_debug_moe_batch(self._h, flags), "debug_moe_batch")
+
+    def debug_moe_batch_read(self, which: int, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        _check(self.lib.wh_debug_moe_batch_read(self._h, which, out.ctypes.data_as(ctypes.c_void_p), out.nbytes),
+               "debug_moe_batch_read")
+        return out
 
     def timer_stop(self) -> float:
         """Device microseconds since timer_start (waits for the stream)."""

@@ -1001,493 +1001,6 @@ __global__ void __launch_bounds__(256) k_moe_down(wh_moe_args a) {
     if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ------------------------------------------ ragged batched routed experts
-// The expert-major batch path of the reference: per-position weights and the
-// union of selected experts (E/server/generation.rs:2487-2506), then for each
-// expert in ascending id and each of its positions acc_p += y * w
-// (accumulate_expert_for_positions, E/compute.rs:1779-1810).  One packing
-// workgroup builds the ragged per-expert token lists on the device; the
-// expert kernels are persistent workgroups that take (expert, row tile)
-// items from a queue, heaviest experts first, and decode each weight once
-// per pair of tokens.
-#define WH_BATCH_MAX_TABLE 1024u   // expert ids per layer
-#define WH_BATCH_MAX_ASSIGN 4096u  // positions x topk per pack
-#define WH_BATCH_MAX_TOPK 16u
-
-struct wh_batch_args {
-    const wh_expert_ptrs* table;   // the layer's experts by id (null w1 = not resident)
-    uint32_t n_table;              // valid ids are < n_table
-    const uint32_t* route_ids;     // [npos][topk]
-    const float* route_scores;     // [npos][topk]
-    uint32_t npos, topk, hidden, inter;
-    uint32_t has_shared;           // the shared expert runs on every position
-    wh_expert_ptrs shared;         // ... under the id n_table
-    const void* x;                 // [npos][hidden], f32 or bf16
-    uint32_t x_is_bf16;
-    // assignments: i = p * topk + k for the routes, A + p for the shared
-    // expert (A = npos * topk); S = A + has_shared * npos slots
-    float* wgt;                    // [A] weight of route assignment i
-    uint32_t* sorted;              // [S] assignments by (expert id, i): the slots
-    uint32_t* uexp;                // [S] used expert ids, ascending
-    uint32_t* uoff;                // [S + 1] their slot ranges
-    uint32_t* uorder;              // [S] used-expert indices, most slots first
-    uint32_t* acc_order;           // [A] per position: its route slots by ascending expert id
-    uint32_t* meta;                // [0] used experts, [1] routes valid, [2]/[3] work queues
-    float* xq;                     // [npos][hidden] act-quantized inputs
-    float* h;                      // [S][inter] SwiGLU outputs by slot
-    float* y;                      // [S][hidden] expert outputs by slot
-    float* out;                    // [npos][hidden]
-    uint32_t* status;
-};
-
-__device__ __forceinline__ uint32_t wh_slot_pos(const wh_batch_args& a, uint32_t i) {
-    const uint32_t A = a.npos * a.topk;
-    return i < A ? i / a.topk : i - A;
-}
-__device__ __forceinline__ wh_expert_ptrs wh_batch_expert(const wh_batch_args& a, uint32_t id) {
-    return id == a.n_table ? a.shared : a.table[id];
-}
-
-// Packing: one workgroup of 256 threads; S <= 4096 slots, n_table < 1024.
-__global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
-    __shared__ __align__(16) uint32_t ids[WH_BATCH_MAX_ASSIGN];
-    __shared__ uint32_t slot_of[WH_BATCH_MAX_ASSIGN];
-    __shared__ uint32_t cnt[WH_BATCH_MAX_TABLE], off[WH_BATCH_MAX_TABLE], uid[WH_BATCH_MAX_TABLE];
-    __shared__ uint32_t chunk_tot[256];
-    __shared__ uint32_t bad, n_used;
-    const uint32_t A = a.npos * a.topk, S = A + a.has_shared * a.npos, S4 = (S + 3) & ~3u, tid = threadIdx.x;
-    const uint32_t n_ids = a.n_table + a.has_shared;
-    if (tid == 0) bad = 0;
-    __syncthreads();
-    for (uint32_t i = tid; i < S4; i += 256) {
-        uint32_t e = 0xffffffffu;
-        if (i < A) {
-            e = a.route_ids[i];
-            if (e >= a.n_table || a.table[e].w1 == nullptr) {
-                bad = 1;
-                e = 0xffffffffu;
-            }
-        } else if (i < S) {
-            e = a.n_table;
-        }
-        ids[i] = e;
-    }
-    // per-position weights: score / sum, or 1 / len when the sequential sum
-    // is not finite and positive or a score is not finite
-    // (E/server/generation.rs:2495-2503)
-    for (uint32_t p = tid; p < a.npos; p += 256) {
-        const float* sc = a.route_scores + (size_t)p * a.topk;
-        float sum = 0.0f;
-        bool finite = true;
-        for (uint32_t k = 0; k < a.topk; ++k) {
-            finite = finite && fabsf(sc[k]) <= 3.4028235e38f;
-            sum = sum + sc[k];
-        }
-        finite = finite && fabsf(sum) <= 3.4028235e38f && sum > 0.0f;
-        const float uniform = 1.0f / (float)a.topk;
-        for (uint32_t k = 0; k < a.topk; ++k) a.wgt[(size_t)p * a.topk + k] = finite ? sc[k] / sum : uniform;
-    }
-    __syncthreads();
-    if (bad) {
-        if (tid == 0) {
-            a.meta[0] = 0;
-            a.meta[1] = 0;
-            a.meta[2] = 0;
-            a.meta[3] = 0;
-            atomicOr(a.status, WH_ST_NOT_RESIDENT);
-        }
-        return;
-    }
-    // per-expert counts
-    for (uint32_t e = tid; e < n_ids; e += 256) {
-        uint32_t c = 0;
-        for (uint32_t i = 0; i < S4; i += 4) {
-            const uint4 v = *(const uint4*)&ids[i];
-            c += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
-        }
-        cnt[e] = c;
-    }
-    __syncthreads();
-    // exclusive prefix sums of the counts and of the used flags over 256
-    // contiguous chunks of ids (slots < 2^13, used experts < 2^11)
-    const uint32_t per = (n_ids + 255) / 256, b0 = min(tid * per, n_ids), b1 = min(b0 + per, n_ids);
-    uint32_t tc = 0, tu = 0;
-    for (uint32_t e = b0; e < b1; ++e) {
-        tc += cnt[e];
-        tu += cnt[e] != 0;
-    }
-    chunk_tot[tid] = tc | (tu << 16);
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t rc = 0, ru = 0;
-        for (uint32_t i = 0; i < 256; ++i) {
-            const uint32_t v = chunk_tot[i];
-            chunk_tot[i] = rc | (ru << 16);
-            rc += v & 0xffffu;
-            ru += v >> 16;
-        }
-        n_used = ru;
-        a.uoff[ru] = rc;
-    }
-    __syncthreads();
-    {
-        uint32_t rc = chunk_tot[tid] & 0xffffu, ru = chunk_tot[tid] >> 16;
-        for (uint32_t e = b0; e < b1; ++e) {
-            off[e] = rc;
-            if (cnt[e]) {
-                uid[ru] = e;
-                a.uexp[ru] = e;
-                a.uoff[ru] = rc;
-                ++ru;
-            }
-            rc += cnt[e];
-        }
-    }
-    __syncthreads();
-    const uint32_t U = n_used;
-    // work order: most slots first, ties by ascending id
-    for (uint32_t u = tid; u < U; u += 256) {
-        const uint32_t cu = cnt[uid[u]];
-        uint32_t r = 0;
-        for (uint32_t v = 0; v < U; ++v) {
-            const uint32_t cv = cnt[uid[v]];
-            r += cv > cu || (cv == cu && v < u);
-        }
-        a.uorder[r] = u;
-    }
-    // stable placement: an expert's slots in assignment order
-    for (uint32_t e = tid; e < n_ids; e += 256) {
-        const uint32_t c = cnt[e];
-        if (!c) continue;
-        uint32_t j = off[e];
-        const uint32_t j_end = j + c;
-        for (uint32_t i = 0; i < S && j < j_end; ++i)
-            if (ids[i] == e) {
-                a.sorted[j] = i;
-                slot_of[i] = j;
-                ++j;
-            }
-    }
-    __syncthreads();
-    // each position's slots in ascending expert id, equal ids in route order
-    for (uint32_t p = tid; p < a.npos; p += 256) {
-        uint32_t kid[WH_BATCH_MAX_TOPK], ksl[WH_BATCH_MAX_TOPK];
-        const uint32_t k0 = p * a.topk;
-        for (uint32_t k = 0; k < a.topk; ++k) {
-            const uint32_t id = ids[k0 + k], s = slot_of[k0 + k];
-            uint32_t j = k;
-            while (j > 0 && kid[j - 1] > id) {
-                kid[j] = kid[j - 1];
-                ksl[j] = ksl[j - 1];
-                --j;
-            }
-            kid[j] = id;
-            ksl[j] = s;
-        }
-        for (uint32_t k = 0; k < a.topk; ++k) a.acc_order[k0 + k] = ksl[k];
-    }
-    if (tid == 0) {
-        a.meta[0] = U;
-        a.meta[1] = 1;
-        a.meta[2] = 0;
-        a.meta[3] = 0;
-    }
-}
-
-// Act-quant (block 64) of every position's input: thread t of a position
-// takes 16 values, a quad one 64-block.  Grid: npos * hidden / 4096 blocks.
-__global__ void __launch_bounds__(256) k_moe_batch_xq(wh_batch_args a) {
-    __shared__ uint32_t thr[256];
-    wh_thr_stage ts;
-    wh_thr_stage_load(ts);
-    wh_thr_stage_store(ts, thr);
-    __syncthreads();
-    const uint32_t per_pos = a.hidden / 16;
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t p = i / per_pos, t = i - p * per_pos;
-    const bool on = p < a.npos;
-    const bool bf16 = a.x_is_bf16 != 0;
-    const size_t base = (size_t)(on ? p : 0) * a.hidden;
-    const void* xt = bf16 ? (const void*)((const uint16_t*)a.x + base) : (const void*)((const float*)a.x + base);
-    wh_xq_stage st;
-    wh_xq_stage_load(st, xt, bf16, on ? a.hidden : 0u, t);
-    float v[16];
-    if (bf16) {
-        const uint32_t w[8] = {st.raw[0].x, st.raw[0].y, st.raw[0].z, st.raw[0].w,
-                               st.raw[1].x, st.raw[1].y, st.raw[1].z, st.raw[1].w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            v[2 * j] = __uint_as_float(w[j] << 16);
-            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            v[4 * j] = __uint_as_float(st.raw[j].x);
-            v[4 * j + 1] = __uint_as_float(st.raw[j].y);
-            v[4 * j + 2] = __uint_as_float(st.raw[j].z);
-            v[4 * j + 3] = __uint_as_float(st.raw[j].w);
-        }
-    }
-    float amax = 0.0f;
-    bool bad = false;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const float m = fabsf(v[j]);
-        bad |= !(m <= 3.4028235e38f);
-        amax = fmaxf(amax, m);
-    }
-    amax = fmaxf(amax, wh_dpp_quad_swap1(amax));
-    amax = fmaxf(amax, wh_dpp_quad_swap2(amax));
-    if (!st.on) return;
-    if (bad) atomicOr(a.status, WH_ST_NONFINITE_INPUT);
-    if (!(amax <= 3.4028235e38f)) amax = 1.0f;
-    const int k = wh_aq_scale_exp(amax, thr);
-    const float inv = wh_pow2f(-k), sc = wh_pow2f(k);
-    float4* dst = (float4*)(a.xq + base + 16 * t);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        dst[j] = make_float4(wh_e4m3_round(wh_clamp448(v[4 * j] * inv)) * sc,
-                             wh_e4m3_round(wh_clamp448(v[4 * j + 1] * inv)) * sc,
-                             wh_e4m3_round(wh_clamp448(v[4 * j + 2] * inv)) * sc,
-                             wh_e4m3_round(wh_clamp448(v[4 * j + 3] * inv)) * sc);
-}
-
-// An act-quantized vector (column order, n floats, n % 32 == 0) into LDS in
-// FP4 lane order: one 32-col group per thread and pass.
-__device__ __forceinline__ void wh_stage_xq_lanes(const float* __restrict__ src, uint32_t n, float* xs) {
-    for (uint32_t g = threadIdx.x; g < n / 32; g += 256) {
-        const float4* p = (const float4*)(src + 32 * g);
-        float v[32];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const float4 f = p[q];
-            v[4 * q] = f.x;
-            v[4 * q + 1] = f.y;
-            v[4 * q + 2] = f.z;
-            v[4 * q + 3] = f.w;
-        }
-        wh_stage_fp4_store_group(xs, g, v);
-    }
-}
-
-// One dword of one lane (two groups) against two inputs: one decode, and
-// each input keeps the reference chain of the single-input path.
-__device__ __forceinline__ void wh_fp4_lane_pair2(uint32_t word, const float4* xg0, const float4* xg1, uint32_t ja,
-                                                  uint32_t jb, float sa, float sb, bool two, float& acc0,
-                                                  float& acc1) {
-    const wh_fp4x8 e = wh_fp4_decode8(word);
-    {
-        const float4 xa = xg0[ja], xb = xg0[jb];
-        float ga = __builtin_fmaf(e.a01.x, xa.x, 0.0f);
-        ga = __builtin_fmaf(e.a01.y, xa.y, ga);
-        ga = __builtin_fmaf(e.a23.x, xa.z, ga);
-        ga = __builtin_fmaf(e.a23.y, xa.w, ga);
-        acc0 = __builtin_fmaf(ga, sa, acc0);
-        float gb = __builtin_fmaf(e.b01.x, xb.x, 0.0f);
-        gb = __builtin_fmaf(e.b01.y, xb.y, gb);
-        gb = __builtin_fmaf(e.b23.x, xb.z, gb);
-        gb = __builtin_fmaf(e.b23.y, xb.w, gb);
-        acc0 = __builtin_fmaf(gb, sb, acc0);
-    }
-    if (two) {
-        const float4 xa = xg1[ja], xb = xg1[jb];
-        float ga = __builtin_fmaf(e.a01.x, xa.x, 0.0f);
-        ga = __builtin_fmaf(e.a01.y, xa.y, ga);
-        ga = __builtin_fmaf(e.a23.x, xa.z, ga);
-        ga = __builtin_fmaf(e.a23.y, xa.w, ga);
-        acc1 = __builtin_fmaf(ga, sa, acc1);
-        float gb = __builtin_fmaf(e.b01.x, xb.x, 0.0f);
-        gb = __builtin_fmaf(e.b01.y, xb.y, gb);
-        gb = __builtin_fmaf(e.b23.x, xb.z, gb);
-        gb = __builtin_fmaf(e.b23.y, xb.w, gb);
-        acc1 = __builtin_fmaf(gb, sb, acc1);
-    }
-}
-__device__ __forceinline__ void wh_fp4_lane_block2(uint4 w, const float4* xp0, const float4* xp1, const float* s8row,
-                                                   uint32_t b, bool two, float& acc0, float& acc1) {
-    const float4 s0 = ((const float4*)s8row)[2 * b], s1 = ((const float4*)s8row)[2 * b + 1];
-    const float4* g0 = xp0 + 68 * b;
-    const float4* g1 = xp1 + 68 * b;
-    wh_fp4_lane_pair2(w.x, g0, g1, wh_xs_f4(0, 0), wh_xs_f4(1, 0), s0.x, s0.y, two, acc0, acc1);
-    wh_fp4_lane_pair2(w.y, g0, g1, wh_xs_f4(2, 0), wh_xs_f4(3, 0), s0.z, s0.w, two, acc0, acc1);
-    wh_fp4_lane_pair2(w.z, g0, g1, wh_xs_f4(4, 0), wh_xs_f4(5, 0), s1.x, s1.y, two, acc0, acc1);
-    wh_fp4_lane_pair2(w.w, g0, g1, wh_xs_f4(6, 0), wh_xs_f4(7, 0), s1.z, s1.w, two, acc0, acc1);
-}
-// A lane's row (registers for kBlk > 0, else read per block) against one or
-// two staged inputs.
-template <int kBlk>
-__device__ __forceinline__ void wh_fp4_lane_dot2(const wh_fp4_lane_row<(kBlk > 0 ? kBlk : 1)>& r,
-                                                 const uint8_t* __restrict__ wrow, uint32_t blocks, const float* xs0,
-                                                 const float* xs1, const float* s8row, uint32_t lane, bool two,
-                                                 float& acc0, float& acc1) {
-    const float4* xp0 = (const float4*)xs0 + lane;
-    const float4* xp1 = (const float4*)xs1 + lane;
-    acc0 = 0.0f;
-    acc1 = 0.0f;
-    if constexpr (kBlk > 0) {
-        // each block's LDS reads are tied to the running sum, so they cannot
-        // all be hoisted ahead of the arithmetic (which would spill)
-#pragma unroll
-        for (int b = 0; b < kBlk; ++b) {
-            const uint32_t dep = wh_opaque_zero(acc0);
-            wh_fp4_lane_block2(r.w[b], xp0 + dep, xp1 + dep, s8row + dep, b, two, acc0, acc1);
-        }
-    } else {
-        const uint4* p = (const uint4*)wrow + lane;
-        for (uint32_t b = 0; b < blocks; ++b) wh_fp4_lane_block2(p[8 * b], xp0, xp1, s8row, b, two, acc0, acc1);
-    }
-}
-
-// LDS bytes of a batched routed-expert workgroup over `cols` input columns:
-// two staged inputs, the 32-row scale table and the log2f thresholds.
-__host__ __device__ constexpr size_t wh_batch_wg_lds(size_t cols) {
-    return wh_moe_wg_lds(cols) + sizeof(float) * wh_xs_floats((uint32_t)cols);
-}
-
-// Next item of a persistent workgroup's queue (counter zeroed by the pack).
-__device__ __forceinline__ uint32_t wh_next_item(uint32_t* queue, uint32_t* item_s) {
-    __syncthreads();  // the previous item is done with the LDS and item_s
-    if (threadIdx.x == 0) *item_s = atomicAdd(queue, 1u);
-    __syncthreads();
-    return *item_s;
-}
-
-// Gate/up + SwiGLU over (used expert, 16 rows of inter) items; octet 2r runs
-// the w1 row r of the tile, octet 2r+1 the w3 row r.
-template <int kBlk>
-__global__ void __launch_bounds__(256) k_moe_batch_gateup(wh_batch_args a) {
-    extern __shared__ __align__(16) float lds[];
-    __shared__ uint32_t item_s;
-    const uint32_t G = a.hidden >> 5, xsf = wh_xs_floats(a.hidden);
-    float* xs0 = lds;
-    float* xs1 = lds + xsf;
-    const uint32_t lane = threadIdx.x & 7, oct = threadIdx.x >> 3;
-    float* s8row = lds + 2 * xsf + oct * wh_s8_stride(G);
-    const uint32_t tiles = a.inter >> 4, n_items = a.meta[0] * tiles;
-    for (;;) {
-        const uint32_t item = wh_next_item(a.meta + 2, &item_s);
-        if (item >= n_items) break;
-        const uint32_t u = a.uorder[item / tiles], tile = item % tiles;
-        const wh_expert_ptrs ep = wh_batch_expert(a, a.uexp[u]);
-        const uint32_t row = tile * 16 + (oct >> 1);
-        const bool up = oct & 1;
-        const uint8_t* wrow = (up ? ep.w3 : ep.w1) + (size_t)row * (a.hidden >> 1);
-        const uint8_t* srow = (up ? ep.s3 : ep.s1) + (size_t)row * G;
-        const uint32_t s_beg = a.uoff[u], s_end = a.uoff[u + 1];
-        wh_fp4_lane_row<(kBlk > 0 ? kBlk : 1)> r;
-        if constexpr (kBlk > 0) {
-            wh_s8_stage<kBlk> ss;
-            wh_s8_stage_load<kBlk>(ss, srow, lane);
-            wh_fp4_lane_row_load<kBlk>(r, wrow, lane);
-            wh_s8_stage_store<kBlk>(ss, s8row, lane);
-        } else {
-            wh_s8_stage_rt(srow, G, s8row, lane);
-        }
-        for (uint32_t s = s_beg; s < s_end; s += 2) {
-            const bool two = s + 1 < s_end;
-            if (s != s_beg) __syncthreads();  // the previous pair is done with xs
-            wh_stage_xq_lanes(a.xq + (size_t)wh_slot_pos(a, a.sorted[s]) * a.hidden, a.hidden, xs0);
-            if (two) wh_stage_xq_lanes(a.xq + (size_t)wh_slot_pos(a, a.sorted[s + 1]) * a.hidden, a.hidden, xs1);
-            __syncthreads();
-            float acc0, acc1;
-            wh_fp4_lane_dot2<kBlk>(r, wrow, G >> 3, xs0, xs1, s8row, lane, two, acc0, acc1);
-            const float v0 = wh_hsum8(acc0) + 0.0f, v1 = wh_hsum8(acc1) + 0.0f;
-            const float u0 = wh_dpp_row_shl8(v0), u1 = wh_dpp_row_shl8(v1);  // the w3 rows
-            if ((threadIdx.x & 15) == 0) {
-                bool nf = !(fabsf(v0) <= 3.4028235e38f) || !(fabsf(u0) <= 3.4028235e38f);
-                a.h[(size_t)s * a.inter + row] = wh_swiglu(v0, u0, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
-                if (two) {
-                    nf = nf || !(fabsf(v1) <= 3.4028235e38f) || !(fabsf(u1) <= 3.4028235e38f);
-                    a.h[(size_t)(s + 1) * a.inter + row] =
-                        wh_swiglu(v1, u1, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
-                }
-                if (nf) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
-            }
-        }
-    }
-}
-
-// Down over (used expert, 32 output rows) items; each slot's hidden vector
-// is act-quantized while staged.
-template <int kBlk>
-__global__ void __launch_bounds__(256) k_moe_batch_down(wh_batch_args a) {
-    extern __shared__ __align__(16) float lds[];
-    __shared__ uint32_t item_s;
-    const uint32_t G = a.inter >> 5, xsf = wh_xs_floats(a.inter);
-    float* xs0 = lds;
-    float* xs1 = lds + xsf;
-    const uint32_t lane = threadIdx.x & 7, oct = threadIdx.x >> 3;
-    float* s8row = lds + 2 * xsf + oct * wh_s8_stride(G);
-    uint32_t* thr = (uint32_t*)(lds + 2 * xsf + 32 * wh_s8_stride(G));
-    wh_thr_stage ts;
-    wh_thr_stage_load(ts);
-    wh_thr_stage_store(ts, thr);
-    const uint32_t tiles = a.hidden >> 5, n_items = a.meta[0] * tiles;
-    for (;;) {
-        const uint32_t item = wh_next_item(a.meta + 3, &item_s);
-        if (item >= n_items) break;
-        const uint32_t u = a.uorder[item / tiles], tile = item % tiles;
-        const wh_expert_ptrs ep = wh_batch_expert(a, a.uexp[u]);
-        const uint32_t row = tile * 32 + oct;
-        const uint8_t* wrow = ep.w2 + (size_t)row * (a.inter >> 1);
-        const uint8_t* srow = ep.s2 + (size_t)row * G;
-        const uint32_t s_beg = a.uoff[u], s_end = a.uoff[u + 1];
-        wh_fp4_lane_row<(kBlk > 0 ? kBlk : 1)> r;
-        if constexpr (kBlk > 0) {
-            wh_s8_stage<kBlk> ss;
-            wh_s8_stage_load<kBlk>(ss, srow, lane);
-            wh_fp4_lane_row_load<kBlk>(r, wrow, lane);
-            wh_s8_stage_store<kBlk>(ss, s8row, lane);
-        } else {
-            wh_s8_stage_rt(srow, G, s8row, lane);
-        }
-        for (uint32_t s = s_beg; s < s_end; s += 2) {
-            const bool two = s + 1 < s_end;
-            if (s != s_beg) __syncthreads();
-            for (uint32_t t = threadIdx.x; t < a.inter / 8; t += 256) {
-                wh_h_stage hst;
-                wh_h_stage_load(hst, a.h + (size_t)s * a.inter, a.inter, t);
-                wh_h_stage_store(hst, xs0, thr);
-                if (two) {
-                    wh_h_stage_load(hst, a.h + (size_t)(s + 1) * a.inter, a.inter, t);
-                    wh_h_stage_store(hst, xs1, thr);
-                }
-            }
-            __syncthreads();
-            float acc0, acc1;
-            wh_fp4_lane_dot2<kBlk>(r, wrow, G >> 3, xs0, xs1, s8row, lane, two, acc0, acc1);
-            const float v0 = wh_hsum8(acc0) + 0.0f, v1 = wh_hsum8(acc1) + 0.0f;
-            if (lane == 0) {
-                bool nf = !(fabsf(v0) <= 3.4028235e38f);
-                a.y[(size_t)s * a.hidden + row] = v0;
-                if (two) {
-                    nf = nf || !(fabsf(v1) <= 3.4028235e38f);
-                    a.y[(size_t)(s + 1) * a.hidden + row] = v1;
-                }
-                if (nf) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
-            }
-        }
-    }
-}
-
-// out_p = sum over p's experts in ascending id of y * w, from 0, unfused
-// (E/compute.rs:1804-1807: `*slot += *value * weight`), then with the shared
-// expert out_p = shared + routed (E/compute.rs:1838-1848).  Grid
-// (hidden / 256, npos).  Nothing is written when a route was not resident.
-__global__ void __launch_bounds__(256) k_moe_batch_accumulate(wh_batch_args a) {
-    const uint32_t p = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
-    if (r >= a.hidden || a.meta[1] == 0) return;
-    float acc = 0.0f;
-    for (uint32_t k = 0; k < a.topk; ++k) {
-        const uint32_t s = a.acc_order[p * a.topk + k];
-        const float v = a.y[(size_t)s * a.hidden + r] * a.wgt[a.sorted[s]];
-        acc = acc + v;
-    }
-    if (a.has_shared) acc = a.y[(size_t)(a.npos * a.topk + p) * a.hidden + r] + acc;
-    a.out[(size_t)p * a.hidden + r] = acc;
-}
-
 // Bit-exact dequant of a resident FP4 tensor back to reference values
 // (decode_fp4_e2m1(nibble, scale), E/deepseek_v4.rs:358-372), through the
 // same decode the matvec uses: out = (x8 value) * 0.125 * scale.
