@@ -202,18 +202,14 @@ int wh_routed_and_shared_experts_async(wh_ctx* ctx, const wh_expert_route* route
  * 0 keeps every expert on the exact path.  No counterpart in the reference
  * (its batch path has one kernel). */
 int wh_set_moe_mfma_min(wh_ctx* ctx, uint32_t min_tokens);
-/* Test support for the batch path, no counterpart in the reference.
- * wh_debug_moe_batch sets flags for the next batch call: WH_DEBUG_RAW_GATEUP
- * makes the gate/up kernels store the gate matvec into the SwiGLU buffer and
- * the up matvec into the act-quant buffer (the call's output is then
- * meaningless).  wh_debug_moe_batch_read copies a device buffer of the last
- * single-chunk fast batch call (S = its slots): 0 sorted assignments (u32
- * [S]), 1 SwiGLU outputs (f32 [S][inter]), 2 their act-quant (f32
- * [S][inter]), 3 expert outputs (f32 [S][hidden]), 4 meta (u32 [8]: used
- * experts, routes valid, queues, experts on MFMA), 5 slot ranges (u32
- * [S + 1]), 6 used expert ids (u32 [S]), 7 work order (u32 [S]). */
-#define WH_DEBUG_RAW_GATEUP 1u
-int wh_debug_moe_batch(wh_ctx* ctx, uint32_t flags);
+/* Test support for the batch path, no counterpart in the reference:
+ * copies a device buffer of the last single-chunk fast batch call (S = its
+ * slots) to host.  which: 0 assignment of each slot (u32 [S]), 1 gate
+ * matvecs (f32 [S][inter]), 2 up matvecs (f32 [S][inter]), 3 expert outputs
+ * (f32 [S][hidden]), 4 meta (u32 [8]: used experts, routes valid, queues,
+ * experts on MFMA), 5 slot ranges of the used experts (u32 [S + 1]), 6 used
+ * expert ids (u32 [S]), 7 work order (u32 [S]), 8 act-quantized SwiGLU
+ * outputs (f32 [S][inter]). */
 int wh_debug_moe_batch_read(wh_ctx* ctx, int which, void* out, size_t bytes);
 #define WH_NO_SHARED_EXPERT 0xFFFFFFFFu
 int wh_moe_batch(wh_ctx* ctx, uint32_t layer_id, const uint32_t* route_ids, const float* route_scores, size_t npos,

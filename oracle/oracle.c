@@ -643,6 +643,10 @@ int or_fp8_shared_expert(const uint8_t* w1, const float* s1, const uint8_t* w3, 
 /* ------------------------------------------------------- array helpers */
 
 /* Element-wise glibc silu / expf, for exhaustive-style device checks. */
+void or_swiglu_array(const float* g, const float* u, float* h, size_t n) {
+    for (size_t i = 0; i < n; ++i) h[i] = or_swiglu(g[i], u[i]);
+}
+
 void or_silu_array(const float* x, float* y, size_t n) {
     for (size_t i = 0; i < n; ++i) y[i] = or_silu(x[i]);
 }

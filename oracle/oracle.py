@@ -64,6 +64,7 @@ def lib():
             "or_routed_combine": (None, [f32p, f32p, sz, sz, f32p]),
             "or_accumulate_expert": (None, [f32p, c.POINTER(c.c_size_t), f32p, sz, sz, f32p]),
             "or_silu_array": (None, [f32p, f32p, sz]),
+            "or_swiglu_array": (None, [f32p, f32p, f32p, sz]),
             "or_expf_array": (None, [f32p, f32p, sz]),
             "or_act_quant_scale_array": (None, [f32p, f32p, sz]),
             "or_fp8_shared_expert": (c.c_int, [u8p, f32p, u8p, f32p, u8p, f32p, sz, sz, sz, sz, sz, sz, f32p, f32p]),
@@ -250,6 +251,14 @@ def moe_batch(experts, route_ids, route_scores, x, shared=None):
         sh = np.stack([fp4_expert_forward(*shared, x[p]) for p in range(npos)])
         acc = (sh + acc).astype(np.float32)
     return acc
+
+
+def swiglu_array(g, u):
+    """DeepSeek-V4 SwiGLU elementwise (E/deepseek_v4.rs:590-594)."""
+    g, u = _f(g), _f(u)
+    h = np.empty_like(g)
+    lib().or_swiglu_array(_pf(g), _pf(u), _pf(h), g.size)
+    return h
 
 
 def silu_array(x):

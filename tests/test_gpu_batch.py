@@ -190,37 +190,33 @@ def _mfma_case(ctx, oracle, layer, n_exp, hidden, inter, seed, npos, mfma_min):
     experts = _host(ctx, layer, ids, seed, hidden, inter)
     topk, S = ids.shape[1], ids.size
     ctx.set_moe_mfma_min(mfma_min)
+    out = ctx.moe_batch(layer, ids, sc, x)
     rd = ctx.debug_moe_batch_read
-    # gate and up matvecs, raw
-    ctx.debug_moe_batch(wohper_amd.DEBUG_RAW_GATEUP)
-    ctx.moe_batch(layer, ids, sc, x)
     srt, gate, up = rd(0, S, np.uint32), rd(1, (S, inter), np.float32), rd(2, (S, inter), np.float32)
+    y, hq = rd(3, (S, hidden), np.float32), rd(8, (S, inter), np.float32)
     meta, uoff, uexp, uorder = rd(4, 8, np.uint32), rd(5, S + 1, np.uint32), rd(6, S, np.uint32), rd(7, S, np.uint32)
     n_used, n_mfma = int(meta[0]), int(meta[4])
     assert 0 < n_mfma < n_used, (n_used, n_mfma)  # both paths run
     on_mfma = {int(uexp[j]) for j in uorder[:n_mfma]}
     xq = {p: oracle.act_quant(x[p], 64) for p in range(npos)}
+    wts = oracle.batch_route_weights(sc)
+    acc = np.zeros_like(x)
     worst = 0.0
     for j in range(n_used):
         e = int(uexp[j])
-        w1, w3, _ = experts[e]
-        for s in range(int(uoff[j]), int(uoff[j + 1])):
+        w1, w3, w2 = experts[e]
+        exact = e not in on_mfma
+        slots = range(int(uoff[j]), int(uoff[j + 1]))
+        for s in slots:
             p = int(srt[s]) // topk
-            worst = max(worst, _check_matvec(oracle, w1, xq[p], gate[s], e not in on_mfma, ("gate", e, p)))
-            worst = max(worst, _check_matvec(oracle, w3, xq[p], up[s], e not in on_mfma, ("up", e, p)))
-    # the full call: act-quant of the SwiGLU outputs, down, weighted sum
-    out = ctx.moe_batch(layer, ids, sc, x)
-    h, hq, y = rd(1, (S, inter), np.float32), rd(2, (S, inter), np.float32), rd(3, (S, hidden), np.float32)
-    wts = oracle.batch_route_weights(sc)
-    acc = np.zeros_like(x)
-    for j in range(n_used):
-        e = int(uexp[j])
-        rng_ = range(int(uoff[j]), int(uoff[j + 1]))
-        for s in rng_:
-            assert np.array_equal(bits(hq[s]), bits(oracle.act_quant(h[s], 64))), ("act-quant", s)
-            worst = max(worst, _check_matvec(oracle, experts[e][2], hq[s], y[s], e not in on_mfma, ("down", e, s)))
-        pos = [int(srt[s]) // topk for s in rng_]
-        acc = oracle.accumulate_expert(y[list(rng_)], pos, [wts[int(srt[s]) // topk, int(srt[s]) % topk] for s in rng_],
+            # each matvec on the same input as the oracle's
+            worst = max(worst, _check_matvec(oracle, w1, xq[p], gate[s], exact, ("gate", e, p)))
+            worst = max(worst, _check_matvec(oracle, w3, xq[p], up[s], exact, ("up", e, p)))
+            want_hq = oracle.act_quant(oracle.swiglu_array(gate[s], up[s]), 64)
+            assert np.array_equal(bits(hq[s]), bits(want_hq)), ("swiglu + act-quant", s)
+            worst = max(worst, _check_matvec(oracle, w2, hq[s], y[s], exact, ("down", e, p)))
+        pos = [int(srt[s]) // topk for s in slots]
+        acc = oracle.accumulate_expert(y[list(slots)], pos, [wts[int(srt[s]) // topk, int(srt[s]) % topk] for s in slots],
                                        acc)
     assert np.array_equal(bits(out), bits(acc))
     # end to end, the act-quant of h may round a near-tie the other way, so

@@ -55,7 +55,6 @@ STATUS_NAMES = {
 SCALE_UE8M0 = 0
 SCALE_F32 = 1
 NO_SHARED_EXPERT = 0xFFFFFFFF
-DEBUG_RAW_GATEUP = 1
 
 # every symbol include/wohper_hip.h declares
 EXPORTED = (
@@ -67,7 +66,7 @@ EXPORTED = (
     "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop", "wh_profile_routed",
     "wh_store_fp8_synthetic", "wh_synth_fp8_host", "wh_routed_and_shared_experts", "wh_fp8_gemv_batch_async",
     "wh_routed_and_shared_experts_async", "wh_moe_batch", "wh_moe_batch_async", "wh_set_moe_mfma_min",
-    "wh_debug_moe_batch", "wh_debug_moe_batch_read",
+    "wh_debug_moe_batch_read",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
 )
 
@@ -154,7 +153,6 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_moe_batch_async": (c.c_int, [vp, c.c_uint32, vp, vp, sz, sz, c.c_uint32, c.c_uint32, vp, c.c_int,
                                          vp]),
         "wh_set_moe_mfma_min": (c.c_int, [vp, c.c_uint32]),
-        "wh_debug_moe_batch": (c.c_int, [vp, c.c_uint32]),
         "wh_debug_moe_batch_read": (c.c_int, [vp, c.c_int, vp, sz]),
     }
     for name, (res, args) in sig.items():
@@ -428,9 +426,6 @@ class Context:
     def set_moe_mfma_min(self, min_tokens: int):
         """Batch experts with at least min_tokens tokens run on MFMA (0: none)."""
         _check(self.lib.wh_set_moe_mfma_min(self._h, min_tokens), "set_moe_mfma_min")
-
-    def debug_moe_batch(self, flags: int):
-        _check(self.lib.wh_debug_moe_batch(self._h, flags), "debug_moe_batch")
 
     def debug_moe_batch_read(self, which: int, shape, dtype) -> np.ndarray:
         out = np.empty(shape, dtype)

@@ -8,11 +8,13 @@
 //
 // Launch sequence (one stream):
 //   k_moe_batch_pack     one workgroup: weights, the per-expert token lists
-//                        (a bitonic sort of (expert id, assignment) keys), the
-//                        used experts, their work order, per-position
+//                        (counts, offsets, placement), the used experts in
+//                        ascending id, their work order, each position's
 //                        accumulation order
 //   k_moe_batch_quant    act-quant (block 64) of every position's input
-//   k_moe_batch_gateup   persistent: (expert, row tile) items from a queue
+//   k_moe_batch_gateup   persistent: (expert, row tile) items from a queue,
+//                        gate and up matvecs of every slot
+//   k_moe_batch_swiglu   SwiGLU of every slot
 //   k_moe_batch_quant    act-quant of every slot's SwiGLU output
 //   k_moe_batch_down     persistent, as gate/up
 //   k_moe_batch_accumulate
@@ -39,23 +41,24 @@ struct wh_batch_args {
     uint32_t has_shared;           // the shared expert runs on every position
     wh_expert_ptrs shared;         // ... under the id n_table
     uint32_t mfma_min;             // experts with this many slots take MFMA items (0: never)
-    uint32_t debug_raw;            // test support: gate/up write gate into h and up into hq
     const void* x;                 // [npos][hidden], f32 or bf16
     uint32_t x_is_bf16;
     // assignments: i = p * topk + k for the routes, A + p for the shared
     // expert (A = npos * topk); S = A + has_shared * npos slots
     float* wgt;                    // [A] weight of route assignment i
-    uint32_t* sorted;              // [S] assignments by (expert id, i): the slots
+    uint32_t* sorted;              // [S] assignments grouped by expert id: the slots
     uint32_t* uexp;                // [S] used expert ids, ascending
     uint32_t* uoff;                // [S + 1] their slot ranges
     uint32_t* uorder;              // [S] used-expert indices, most slots first
     uint32_t* acc_order;           // [A] per position: its route slots by ascending expert id
-    uint32_t* meta;                // [0] used experts, [1] routes valid, [2]/[3] exact-item
-                                   // queues, [4] experts on MFMA items, [5]/[6] MFMA queues
+    uint32_t* meta;                // [0] used experts, [1] routes valid, [2]/[3] work queues
+                                   // of gate/up and down, [4] experts on MFMA items
     float* xq;                     // [npos][hidden] act-quantized inputs (column order)
     uint8_t* xq8;                  // [npos][hidden] their E4M3 codes, MFMA group order
     uint8_t* xs8;                  // [npos][hidden / 32] E8M0 scale bytes (x 1/8)
-    float* h;                      // [S][inter] SwiGLU outputs by slot
+    float* g;                      // [S][inter] gate matvec (w1) by slot
+    float* u;                      // [S][inter] up matvec (w3) by slot
+    float* h;                      // [S][inter] SwiGLU(g, u)
     float* hq;                     // [S][inter] act-quantized
     uint8_t* hq8;                  // [S][inter] codes
     uint8_t* hs8;                  // [S][inter / 32] scale bytes
@@ -73,32 +76,55 @@ __device__ __forceinline__ wh_expert_ptrs wh_batch_expert(const wh_batch_args& a
 }
 
 // ------------------------------------------------------------------ packing
-// One workgroup of 256 threads; S <= 4096 slots, n_table < 1024.
+// Exclusive prefix sum over the 256 threads of a workgroup (wave scans, then
+// the four wave totals); `tot` is 4 words of LDS.  Returns the thread's
+// exclusive prefix; *total receives the sum.
+__device__ __forceinline__ uint32_t wh_wg_exclusive_scan(uint32_t v, uint32_t* tot, uint32_t* total) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t incl = v;
+    for (uint32_t off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+    }
+    if (lane == 63) tot[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+    for (uint32_t w = 0; w < 4; ++w) {
+        before += w < wave ? tot[w] : 0u;
+        all += tot[w];
+    }
+    *total = all;
+    __syncthreads();  // tot may be reused
+    return before + incl - v;
+}
+
+// One workgroup of 256 threads; S <= 4096 slots, n_table < 1024.  An
+// expert's slots come in no particular order (each slot is computed on its
+// own); the accumulation order of a position is fixed by acc_order alone.
 __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
-    __shared__ uint32_t key[WH_BATCH_MAX_ASSIGN];
+    __shared__ uint32_t ids[WH_BATCH_MAX_ASSIGN];
     __shared__ uint32_t slot_of[WH_BATCH_MAX_ASSIGN];
-    __shared__ uint32_t ubeg[WH_BATCH_MAX_TABLE + 1];  // slot ranges of the used experts
-    __shared__ uint32_t scan[256];
-    __shared__ uint32_t bad, n_used, n_mfma;
+    __shared__ uint32_t cnt[WH_BATCH_MAX_TABLE], off[WH_BATCH_MAX_TABLE], ucnt[WH_BATCH_MAX_TABLE];
+    __shared__ uint32_t tot[4];
+    __shared__ uint32_t bad, n_mfma;
     const uint32_t A = a.npos * a.topk, S = A + a.has_shared * a.npos, tid = threadIdx.x;
-    uint32_t N = 1;
-    while (N < S) N <<= 1;
+    const uint32_t n_ids = a.n_table + a.has_shared;  // the shared expert is id n_table
     if (tid == 0) {
         bad = 0;
         n_mfma = 0;
     }
-    __syncthreads();
-    // keys (expert id << 13 | assignment); ids are checked against the table
-    for (uint32_t i = tid; i < N; i += 256) {
-        uint32_t k = 0xffffffffu;
+    for (uint32_t e = tid; e < n_ids; e += 256) cnt[e] = 0;
+    // ids, checked against the table
+    for (uint32_t i = tid; i < S; i += 256) {
+        uint32_t e = a.n_table;
         if (i < A) {
-            const uint32_t e = a.route_ids[i];
-            if (e >= a.n_table || a.table[e].w1 == nullptr) bad = 1;
-            else k = (e << 13) | i;
-        } else if (i < S) {
-            k = (a.n_table << 13) | i;
+            e = a.route_ids[i];
+            if (e >= a.n_table || a.table[e].w1 == nullptr) {
+                bad = 1;
+                e = 0;
+            }
         }
-        key[i] = k;
+        ids[i] = e;
     }
     // per-position weights: score / sum, or 1 / len when the sequential sum
     // is not finite and positive or a score is not finite
@@ -118,117 +144,85 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
     __syncthreads();
     if (bad) {
         if (tid == 0) {
-            for (int i = 0; i < 7; ++i) a.meta[i] = 0;
+            for (int i = 0; i < 5; ++i) a.meta[i] = 0;
             atomicOr(a.status, WH_ST_NOT_RESIDENT);
         }
         return;
     }
-    // bitonic sort, ascending: slots in (expert id, assignment) order
-    for (uint32_t k = 2; k <= N; k <<= 1) {
-        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            for (uint32_t i = tid; i < N; i += 256) {
-                const uint32_t o = i ^ j;
-                if (o > i) {
-                    const uint32_t x0 = key[i], x1 = key[o];
-                    if ((x0 > x1) == ((i & k) == 0)) {
-                        key[i] = x1;
-                        key[o] = x0;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
-    // runs of equal ids: the used experts.  Thread t scans slots
-    // [t * per, (t + 1) * per).
-    const uint32_t per = (S + 255) / 256, s0 = min(tid * per, S), s1 = min(s0 + per, S);
-    uint32_t starts = 0;
-    for (uint32_t s = s0; s < s1; ++s) {
-        const uint32_t i = key[s] & 0x1fffu;
-        a.sorted[s] = i;
-        slot_of[i] = s;
-        starts += s == 0 || (key[s] >> 13) != (key[s - 1] >> 13);
-    }
-    scan[tid] = starts;
+    for (uint32_t i = tid; i < S; i += 256) atomicAdd(&cnt[ids[i]], 1u);
     __syncthreads();
-    if (tid == 0) {
-        uint32_t run = 0;
-        for (uint32_t t = 0; t < 256; ++t) {
-            const uint32_t v = scan[t];
-            scan[t] = run;
-            run += v;
-        }
-        n_used = run;
-        a.uoff[run] = S;
-        ubeg[run] = S;
+    // slot offsets and used-expert indices in ascending id: thread t owns
+    // ids [4t, 4t + 4)
+    uint32_t c4[4], sum4 = 0, used4 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t e = 4 * tid + j;
+        c4[j] = e < n_ids ? cnt[e] : 0u;
+        sum4 += c4[j];
+        used4 += c4[j] != 0;
     }
-    __syncthreads();
-    {
-        uint32_t u = scan[tid];
-        for (uint32_t s = s0; s < s1; ++s) {
-            if (s == 0 || (key[s] >> 13) != (key[s - 1] >> 13)) {
-                a.uexp[u] = key[s] >> 13;
-                a.uoff[u] = s;
-                ubeg[u] = s;
+    uint32_t S_total, U;
+    uint32_t o = wh_wg_exclusive_scan(sum4, tot, &S_total);
+    uint32_t u = wh_wg_exclusive_scan(used4, tot, &U);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t e = 4 * tid + j;
+        if (e < n_ids) {
+            off[e] = o;
+            cnt[e] = 0;  // reused as the placement cursor
+            if (c4[j]) {
+                a.uexp[u] = e;
+                a.uoff[u] = o;
+                ucnt[u] = c4[j];
+                if (a.mfma_min && c4[j] >= a.mfma_min) atomicAdd(&n_mfma, 1u);
                 ++u;
             }
         }
+        o += c4[j];
+    }
+    if (tid == 0) a.uoff[U] = S;
+    __syncthreads();
+    // placement; the shared expert (the largest id, offset A) keeps position
+    // order, so position p's shared slot is A + p
+    for (uint32_t i = tid; i < S; i += 256) {
+        const uint32_t e = ids[i];
+        const uint32_t s = i >= A ? i : off[e] + atomicAdd(&cnt[e], 1u);
+        a.sorted[s] = i;
+        slot_of[i] = s;
+    }
+    // work order: most slots first, ties by ascending id (rank counting)
+    for (uint32_t v = tid; v < U; v += 256) {
+        const uint32_t cv = ucnt[v];
+        uint32_t r = 0;
+        for (uint32_t w = 0; w < U; ++w) {
+            const uint32_t cw = ucnt[w];
+            r += cw > cv || (cw == cv && w < v);
+        }
+        a.uorder[r] = v;
     }
     __syncthreads();
-    const uint32_t U = n_used;
-    // each position's route slots in ascending slot order = ascending expert
-    // id, equal ids in route order
+    // each position's route slots by ascending expert id, equal ids in route
+    // order (E/server/generation.rs:2491-2506 pushes targets in that order)
     for (uint32_t p = tid; p < a.npos; p += 256) {
-        uint32_t sl[WH_BATCH_MAX_TOPK];
+        uint32_t key[WH_BATCH_MAX_TOPK];
         const uint32_t k0 = p * a.topk;
         for (uint32_t k = 0; k < a.topk; ++k) {
-            const uint32_t s = slot_of[k0 + k];
+            const uint32_t kk = (ids[k0 + k] << 4) | k;
             uint32_t j = k;
-            while (j > 0 && sl[j - 1] > s) {
-                sl[j] = sl[j - 1];
+            while (j > 0 && key[j - 1] > kk) {
+                key[j] = key[j - 1];
                 --j;
             }
-            sl[j] = s;
+            key[j] = kk;
         }
-        for (uint32_t k = 0; k < a.topk; ++k) a.acc_order[k0 + k] = sl[k];
+        for (uint32_t k = 0; k < a.topk; ++k) a.acc_order[k0 + k] = slot_of[k0 + (key[k] & 15u)];
     }
-    // work order: most slots first, ties by ascending id (keys reused)
-    uint32_t N2 = 1;
-    while (N2 < U) N2 <<= 1;
-    for (uint32_t u = tid; u < N2; u += 256) {
-        uint32_t k = 0xffffffffu;
-        if (u < U) {
-            const uint32_t c = ubeg[u + 1] - ubeg[u];
-            k = ((WH_BATCH_MAX_ASSIGN - c) << 11) | u;
-            if (a.mfma_min && c >= a.mfma_min) atomicAdd(&n_mfma, 1u);
-        }
-        key[u] = k;
-    }
-    __syncthreads();
-    for (uint32_t k = 2; k <= N2; k <<= 1) {
-        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            for (uint32_t i = tid; i < N2; i += 256) {
-                const uint32_t o = i ^ j;
-                if (o > i) {
-                    const uint32_t x0 = key[i], x1 = key[o];
-                    if ((x0 > x1) == ((i & k) == 0)) {
-                        key[i] = x1;
-                        key[o] = x0;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
-    for (uint32_t r = tid; r < U; r += 256) a.uorder[r] = key[r] & 0x7ffu;
     if (tid == 0) {
         a.meta[0] = U;
         a.meta[1] = 1;
         a.meta[2] = 0;
         a.meta[3] = 0;
         a.meta[4] = n_mfma;
-        a.meta[5] = 0;
-        a.meta[6] = 0;
     }
 }
 
@@ -316,12 +310,59 @@ __global__ void __launch_bounds__(256) k_moe_batch_quant(const void* __restrict_
     if (!h) s8[(size_t)(on ? r : 0) * (n / 32) + g] = (uint8_t)(127 + k - 3);
 }
 
+// SwiGLU (E/deepseek_v4.rs:590-594) of the gate and up matvecs, one value
+// per thread: h = silu(min(g, 10)) * clamp(u, -10, 10).
+__global__ void __launch_bounds__(256) k_moe_batch_swiglu(const float* __restrict__ g, const float* __restrict__ u,
+                                                          float* __restrict__ h, uint32_t n) {
+    __shared__ uint64_t exp_tab[35];
+    if (threadIdx.x < 35) exp_tab[threadIdx.x] = kExpTab[threadIdx.x];
+    __syncthreads();
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) h[i] = wh_swiglu(g[i], u[i], exp_tab, kExpfFlip, WH_EXPF_FLIP_COUNT);
+}
+
 // ------------------------------------------------------------ exact items
-// An act-quantized vector (column order, n floats, n % 32 == 0) into LDS in
-// FP4 lane order: one 32-col group per thread and pass.
-__device__ __forceinline__ void wh_stage_xq_lanes(const float* __restrict__ src, uint32_t n, float* xs) {
-    for (uint32_t g = threadIdx.x; g < n / 32; g += 256) {
-        const float4* p = (const float4*)(src + 32 * g);
+// One 32-col group of one of two act-quantized vectors, loaded early: thread
+// t takes group t of the first vector or group t - G of the second (2G <=
+// 256), so the loads can be issued before the weight row's.
+struct wh_xq_group_stage {
+    float4 v[8];
+    float* dst;
+    uint32_t g;
+    bool on;
+};
+__device__ __forceinline__ void wh_xq_group_load(wh_xq_group_stage& st, const float* __restrict__ src0,
+                                                 const float* __restrict__ src1, bool two, uint32_t G, float* xs0,
+                                                 float* xs1) {
+    const uint32_t i = threadIdx.x;
+    st.on = i < (two ? 2 * G : G);
+    const bool second = i >= G;
+    st.g = second ? i - G : i;
+    st.dst = second ? xs1 : xs0;
+    if (st.on) {
+        const float4* p = (const float4*)((second ? src1 : src0) + 32 * st.g);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) st.v[q] = p[q];
+    }
+}
+__device__ __forceinline__ void wh_xq_group_store(const wh_xq_group_stage& st) {
+    if (!st.on) return;
+    float v[32];
+#pragma unroll
+    for (int m = 0; m < 32; ++m) v[m] = wh_f4_get(st.v[m >> 2], m & 3);
+    wh_stage_fp4_store_group(st.dst, st.g, v);
+}
+
+// One or two act-quantized vectors (column order, n floats, n % 32 == 0)
+// into LDS in FP4 lane order: one 32-col group per thread and pass, the
+// groups of both vectors spread over the workgroup.
+__device__ __forceinline__ void wh_stage_xq_lanes2(const float* __restrict__ src0, const float* __restrict__ src1,
+                                                   bool two, uint32_t n, float* xs0, float* xs1) {
+    const uint32_t G = n / 32;
+    for (uint32_t i = threadIdx.x; i < (two ? 2 * G : G); i += 256) {
+        const bool second = i >= G;
+        const uint32_t g = second ? i - G : i;
+        const float4* p = (const float4*)((second ? src1 : src0) + 32 * g);
         float v[32];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -331,7 +372,7 @@ __device__ __forceinline__ void wh_stage_xq_lanes(const float* __restrict__ src,
             v[4 * q + 2] = f.z;
             v[4 * q + 3] = f.w;
         }
-        wh_stage_fp4_store_group(xs, g, v);
+        wh_stage_fp4_store_group(second ? xs1 : xs0, g, v);
     }
 }
 
@@ -339,8 +380,8 @@ __device__ __forceinline__ void wh_stage_xq_lanes(const float* __restrict__ src,
 // each input keeps the reference chain of the single-input path.
 __device__ __forceinline__ void wh_fp4_lane_pair2(uint32_t word, const float4* xg0, const float4* xg1, uint32_t ja,
                                                   uint32_t jb, float sa, float sb, bool two, float& acc0,
-                                                  float& acc1) {
-    const wh_fp4x8 e = wh_fp4_decode8(word);
+                                                  float& acc1, uint32_t lut_hi = WH_FP4_LUT_HI) {
+    const wh_fp4x8 e = wh_fp4_decode8(word, lut_hi);
     {
         const float4 xa = xg0[ja], xb = xg0[jb];
         float ga = __builtin_fmaf(e.a01.x, xa.x, 0.0f);
@@ -390,12 +431,24 @@ __device__ __forceinline__ void wh_fp4_lane_dot2(const wh_fp4_lane_row<(kBlk > 0
     acc0 = 0.0f;
     acc1 = 0.0f;
     if constexpr (kBlk > 0) {
-        // each block's LDS reads are tied to the running sum, so they cannot
-        // all be hoisted ahead of the arithmetic (which would spill)
+
+        // the LDS reads of each half block are tied to the running sum, so
+        // they cannot be hoisted ahead of the arithmetic before them (which
+        // would keep every block's operands live)
 #pragma unroll
         for (int b = 0; b < kBlk; ++b) {
-            const uint32_t dep = wh_opaque_zero(acc0);
-            wh_fp4_lane_block2(r.w[b], xp0 + dep, xp1 + dep, s8row + dep, b, two, acc0, acc1);
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+                const uint32_t dep = wh_opaque_zero(acc0);
+                const float4 sv = ((const float4*)(s8row + dep))[2 * b + hb];
+                const float4* g0 = xp0 + dep + 68 * b;
+                const float4* g1 = xp1 + dep + 68 * b;
+                const uint32_t w0 = hb ? r.w[b].z : r.w[b].x, w1 = hb ? r.w[b].w : r.w[b].y;
+                wh_fp4_lane_pair2(w0, g0, g1, wh_xs_f4(4 * hb, 0), wh_xs_f4(4 * hb + 1, 0), sv.x, sv.y, two, acc0,
+                                  acc1);
+                wh_fp4_lane_pair2(w1, g0, g1, wh_xs_f4(4 * hb + 2, 0), wh_xs_f4(4 * hb + 3, 0), sv.z, sv.w, two,
+                                  acc0, acc1);
+            }
         }
     } else {
         const uint4* p = (const uint4*)wrow + lane;
@@ -422,21 +475,39 @@ __device__ __forceinline__ void wh_exact_item(const uint8_t* wrow, const uint8_t
     const uint32_t lane = threadIdx.x & 7, oct = threadIdx.x >> 3;
     float* s8row = lds + 2 * xsf + oct * wh_s8_stride(G);
     wh_fp4_lane_row<(kBlk > 0 ? kBlk : 1)> r;
+    const bool early = kBlk > 0 && 2 * G <= 256;
     if constexpr (kBlk > 0) {
+        // the first pair's inputs and the scales are loaded before the row,
+        // so waiting for them does not wait for the row's bytes (loads
+        // complete in issue order)
+        const bool two = s_beg + 1 < s_end;
+        wh_xq_group_stage xst;
+        if (early) wh_xq_group_load(xst, in(s_beg), in(two ? s_beg + 1 : s_beg), two, G, xs0, xs1);
         wh_s8_stage<kBlk> ss;
         wh_s8_stage_load<kBlk>(ss, srow, lane);
         wh_fp4_lane_row_load<kBlk>(r, wrow, lane);
+        __builtin_amdgcn_sched_barrier(0);
         wh_s8_stage_store<kBlk>(ss, s8row, lane);
+        if (early) wh_xq_group_store(xst);
     } else {
         wh_s8_stage_rt(srow, G, s8row, lane);
     }
     for (uint32_t s = s_beg; s < s_end; s += 2) {
         const bool two = s + 1 < s_end;
-        if (s != s_beg) __syncthreads();  // the previous pair is done with xs
-        wh_stage_xq_lanes(in(s), cols, xs0);
-        if (two) wh_stage_xq_lanes(in(s + 1), cols, xs1);
+        if (s != s_beg) {
+            __syncthreads();  // the previous pair is done with xs
+            wh_stage_xq_lanes2(in(s), in(two ? s + 1 : s), two, cols, xs0, xs1);
+        } else if (!early) {
+            wh_stage_xq_lanes2(in(s), in(two ? s + 1 : s), two, cols, xs0, xs1);
+        }
         __syncthreads();
         float acc0, acc1;
+        if constexpr (kBlk > 0) {
+            // the row's words are opaque per pass: hoisted out of this loop,
+            // their decoded codes would double the row's registers
+#pragma unroll
+            for (int b = 0; b < kBlk; ++b) asm volatile("" : "+v"(r.w[b].x), "+v"(r.w[b].y), "+v"(r.w[b].z), "+v"(r.w[b].w));
+        }
         wh_fp4_lane_dot2<kBlk>(r, wrow, G >> 3, xs0, xs1, s8row, lane, two, acc0, acc1);
         emit(s, two, wh_hsum8(acc0) + 0.0f, wh_hsum8(acc1) + 0.0f);
     }
@@ -625,77 +696,97 @@ __device__ __forceinline__ void wh_mfma_item(const uint8_t* const* wmat, const u
 
 // ------------------------------------------------------- persistent kernels
 
-// Next item of a persistent workgroup's queue (counter zeroed by the pack).
-__device__ __forceinline__ uint32_t wh_next_item(uint32_t* queue, uint32_t* item_s) {
-    __syncthreads();  // the previous item is done with the LDS and item_s
-    if (threadIdx.x == 0) *item_s = atomicAdd(queue, 1u);
-    __syncthreads();
-    return *item_s;
+// LDS of a persistent routed-expert workgroup over `cols` input columns:
+// the larger of the exact and the MFMA items'.
+__host__ __device__ constexpr size_t wh_batch_wg_lds(size_t cols) {
+    return wh_exact_item_lds(cols) > wh_mfma_item_lds() ? wh_exact_item_lds(cols) : wh_mfma_item_lds();
 }
 
-// Gate/up + SwiGLU, MFMA items: (expert, 64 rows of inter), w1 and w3 on the
-// same rows, for the experts at the head of the work order.
-__global__ void __launch_bounds__(256) k_moe_batch_gateup_mfma(wh_batch_args a) {
-    extern __shared__ __align__(16) float lds[];
-    __shared__ uint32_t item_s;
-    const uint32_t mt = a.inter >> 6, n_items = a.meta[4] * mt;
-    for (;;) {
-        const uint32_t item = wh_next_item(a.meta + 5, &item_s);
-        if (item >= n_items) break;
-        const uint32_t u = a.uorder[item / mt], tile = item % mt;
-        const wh_expert_ptrs ep = wh_batch_expert(a, a.uexp[u]);
-        const uint8_t* wm[2] = {ep.w1, ep.w3};
-        const uint8_t* sm[2] = {ep.s1, ep.s3};
-        const uint32_t row0 = tile * 64;
-        wh_mfma_item<2>(
-            wm, sm, row0, a.hidden, a.uoff[u], a.uoff[u + 1], (uint8_t*)lds,
-            [&](uint32_t s, const uint8_t*& rec, const uint8_t*& srec) {
-                const uint32_t p = wh_slot_pos(a, a.sorted[s]);
-                rec = a.xq8 + (size_t)p * a.hidden;
-                srec = a.xs8 + (size_t)p * (a.hidden / 32);
-            },
-            [&](uint32_t s0, uint32_t count, const wh_v4f (&acc)[2][4]) {
-                const uint32_t L = threadIdx.x & 63, wave = threadIdx.x >> 6;
-                const uint32_t r0 = row0 + wave * 16 + 4 * (L >> 4);
-                bool nf = false;
-#pragma unroll
-                for (int nt = 0; nt < 4; ++nt) {
-                    const uint32_t n = nt * 16 + (L & 15);
-                    if (n < count) {
-                        float o[4];
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const float gv = acc[0][nt][r] + 0.0f, uv = acc[1][nt][r] + 0.0f;
-                            nf = nf || !(fabsf(gv) <= 3.4028235e38f) || !(fabsf(uv) <= 3.4028235e38f);
-                            o[r] = wh_swiglu(gv, uv, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
-                        }
-                        float* hp = a.h + (size_t)(s0 + n) * a.inter + r0;
-                        if (a.debug_raw) {
-                            *(float4*)hp = make_float4(acc[0][nt][0], acc[0][nt][1], acc[0][nt][2], acc[0][nt][3]);
-                            *(float4*)(a.hq + (size_t)(s0 + n) * a.inter + r0) =
-                                make_float4(acc[1][nt][0], acc[1][nt][1], acc[1][nt][2], acc[1][nt][3]);
-                        } else {
-                            *(float4*)hp = make_float4(o[0], o[1], o[2], o[3]);
-                        }
-                    }
-                }
-                if (nf) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
-            });
+// Work queue of a persistent workgroup (counter zeroed by the pack).  The
+// next item's index is fetched when an item starts, so the atomic's round
+// trip overlaps the item's own loads.
+struct wh_queue {
+    uint32_t* counter;
+    uint32_t* item_s;  // LDS broadcast slot
+    uint32_t next;     // thread 0: the fetched index
+    __device__ __forceinline__ uint32_t first() {
+        if (threadIdx.x == 0) *item_s = atomicAdd(counter, 1u);
+        __syncthreads();
+        return *item_s;
     }
+    __device__ __forceinline__ void prefetch() {
+        if (threadIdx.x == 0) next = atomicAdd(counter, 1u);
+    }
+    __device__ __forceinline__ uint32_t advance() {
+        __syncthreads();  // the item is done with the LDS and item_s
+        if (threadIdx.x == 0) *item_s = next;
+        __syncthreads();
+        return *item_s;
+    }
+};
+
+// MFMA item epilogue: the accumulators of a pass into dst[slot][row]
+// (C register r of lane L = row 4 * (L / 16) + r of the wave's 16, token
+// L % 16 of the N-tile).
+__device__ __forceinline__ void wh_mfma_store(const wh_batch_args& a, float* dst, uint32_t ld, uint32_t row0,
+                                              uint32_t s0, uint32_t count, const wh_v4f (&acc)[1][4]) {
+    const uint32_t L = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t r0 = row0 + wave * 16 + 4 * (L >> 4);
+    bool nf = false;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+        const uint32_t n = nt * 16 + (L & 15);
+        if (n < count) {
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                o[r] = acc[0][nt][r] + 0.0f;
+                nf = nf || !(fabsf(o[r]) <= 3.4028235e38f);
+            }
+            *(float4*)(dst + (size_t)(s0 + n) * ld + r0) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+    }
+    if (nf) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
 }
 
-// Gate/up + SwiGLU, exact items: (expert, 16 rows of inter) for the experts
-// after the MFMA ones; octet 2r runs the w1 row r of the tile and octet
-// 2r + 1 the w3 row r.
+// Gate and up matvecs of every slot.  The queue holds the MFMA items first -
+// (expert, matrix w1 or w3, 64 rows of inter) for the experts at the head of
+// the work order - then the exact items - (expert, 16 rows of inter), octet
+// 2r running the w1 row r of the tile and octet 2r + 1 the w3 row r.  One
+// queue keeps the MFMA items, few and bound by memory, running beside the
+// exact ones, bound by VALU issue.
+// Three workgroups per CU: the register budget (168) is what the LDS allows.
 template <int kBlk>
-__global__ void __launch_bounds__(256) k_moe_batch_gateup(wh_batch_args a) {
+__global__ void __launch_bounds__(256, 3) k_moe_batch_gateup(wh_batch_args a) {
     extern __shared__ __align__(16) float lds[];
     __shared__ uint32_t item_s;
-    const uint32_t n_mfma = a.meta[4], et = a.inter >> 4, n_items = (a.meta[0] - n_mfma) * et;
-    for (;;) {
-        const uint32_t item = wh_next_item(a.meta + 2, &item_s);
-        if (item >= n_items) break;
-        const uint32_t u = a.uorder[n_mfma + item / et], tile = item % et;
+    const uint32_t n_mfma = a.meta[4], mt = a.inter >> 6, et = a.inter >> 4;
+    const uint32_t n_m = n_mfma * 2 * mt, n_items = n_m + (a.meta[0] - n_mfma) * et;
+    wh_queue q{a.meta + 2, &item_s, 0};
+    for (uint32_t item = q.first(); item < n_items; item = q.advance()) {
+        q.prefetch();
+        if (item < n_m) {
+            const uint32_t u = a.uorder[item / (2 * mt)], rest = item % (2 * mt);
+            const bool up = rest >= mt;
+            const uint32_t row0 = (up ? rest - mt : rest) * 64;
+            const wh_expert_ptrs ep = wh_batch_expert(a, a.uexp[u]);
+            const uint8_t* wm[1] = {up ? ep.w3 : ep.w1};
+            const uint8_t* sm[1] = {up ? ep.s3 : ep.s1};
+            float* dst = up ? a.u : a.g;
+            wh_mfma_item<1>(
+                wm, sm, row0, a.hidden, a.uoff[u], a.uoff[u + 1], (uint8_t*)lds,
+                [&](uint32_t s, const uint8_t*& rec, const uint8_t*& srec) {
+                    const uint32_t p = wh_slot_pos(a, a.sorted[s]);
+                    rec = a.xq8 + (size_t)p * a.hidden;
+                    srec = a.xs8 + (size_t)p * (a.hidden / 32);
+                },
+                [&](uint32_t s0, uint32_t count, const wh_v4f (&acc)[1][4]) {
+                    wh_mfma_store(a, dst, a.inter, row0, s0, count, acc);
+                });
+            continue;
+        }
+        const uint32_t e = item - n_m;
+        const uint32_t u = a.uorder[n_mfma + e / et], tile = e % et;
         const wh_expert_ptrs ep = wh_batch_expert(a, a.uexp[u]);
         const uint32_t oct = threadIdx.x >> 3;
         const uint32_t row = tile * 16 + (oct >> 1);
@@ -706,24 +797,13 @@ __global__ void __launch_bounds__(256) k_moe_batch_gateup(wh_batch_args a) {
             a.uoff[u], a.uoff[u + 1], lds,
             [&](uint32_t s) { return a.xq + (size_t)wh_slot_pos(a, a.sorted[s]) * a.hidden; },
             [&](uint32_t s, bool two, float v0, float v1) {
-                const float u0 = wh_dpp_row_shl8(v0), u1 = wh_dpp_row_shl8(v1);  // the w3 rows
-                if ((threadIdx.x & 15) == 0) {
-                    bool nf = !(fabsf(v0) <= 3.4028235e38f) || !(fabsf(u0) <= 3.4028235e38f);
-                    if (a.debug_raw) {
-                        a.h[(size_t)s * a.inter + row] = v0;
-                        a.hq[(size_t)s * a.inter + row] = u0;
-                    } else {
-                        a.h[(size_t)s * a.inter + row] = wh_swiglu(v0, u0, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
-                    }
+                if ((threadIdx.x & 7) == 0) {
+                    float* dst = up ? a.u : a.g;
+                    bool nf = !(fabsf(v0) <= 3.4028235e38f);
+                    dst[(size_t)s * a.inter + row] = v0;
                     if (two) {
-                        nf = nf || !(fabsf(v1) <= 3.4028235e38f) || !(fabsf(u1) <= 3.4028235e38f);
-                        if (a.debug_raw) {
-                            a.h[(size_t)(s + 1) * a.inter + row] = v1;
-                            a.hq[(size_t)(s + 1) * a.inter + row] = u1;
-                        } else {
-                            a.h[(size_t)(s + 1) * a.inter + row] =
-                                wh_swiglu(v1, u1, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
-                        }
+                        nf = nf || !(fabsf(v1) <= 3.4028235e38f);
+                        dst[(size_t)(s + 1) * a.inter + row] = v1;
                     }
                     if (nf) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
                 }
@@ -731,61 +811,40 @@ __global__ void __launch_bounds__(256) k_moe_batch_gateup(wh_batch_args a) {
     }
 }
 
-// Down, MFMA items: (expert, 64 output rows); inputs are the act-quantized
-// SwiGLU outputs of the slots.
-__global__ void __launch_bounds__(256) k_moe_batch_down_mfma(wh_batch_args a) {
-    extern __shared__ __align__(16) float lds[];
-    __shared__ uint32_t item_s;
-    const uint32_t mt = a.hidden >> 6, n_items = a.meta[4] * mt;
-    for (;;) {
-        const uint32_t item = wh_next_item(a.meta + 6, &item_s);
-        if (item >= n_items) break;
-        const uint32_t u = a.uorder[item / mt], tile = item % mt;
-        const wh_expert_ptrs ep = wh_batch_expert(a, a.uexp[u]);
-        const uint8_t* wm[1] = {ep.w2};
-        const uint8_t* sm[1] = {ep.s2};
-        const uint32_t row0 = tile * 64;
-        wh_mfma_item<1>(
-            wm, sm, row0, a.inter, a.uoff[u], a.uoff[u + 1], (uint8_t*)lds,
-            [&](uint32_t s, const uint8_t*& rec, const uint8_t*& srec) {
-                rec = a.hq8 + (size_t)s * a.inter;
-                srec = a.hs8 + (size_t)s * (a.inter / 32);
-            },
-            [&](uint32_t s0, uint32_t count, const wh_v4f (&acc)[1][4]) {
-                const uint32_t L = threadIdx.x & 63, wave = threadIdx.x >> 6;
-                const uint32_t r0 = row0 + wave * 16 + 4 * (L >> 4);
-                bool nf = false;
-#pragma unroll
-                for (int nt = 0; nt < 4; ++nt) {
-                    const uint32_t n = nt * 16 + (L & 15);
-                    if (n < count) {
-                        float o[4];
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            o[r] = acc[0][nt][r] + 0.0f;
-                            nf = nf || !(fabsf(o[r]) <= 3.4028235e38f);
-                        }
-                        *(float4*)(a.y + (size_t)(s0 + n) * a.hidden + r0) = make_float4(o[0], o[1], o[2], o[3]);
-                    }
-                }
-                if (nf) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
-            });
-    }
-}
-
-// Down, exact items: (expert, 32 output rows).
+// Down of every slot: MFMA items (expert, 64 output rows) first, then exact
+// items (expert, 32 output rows); inputs are the act-quantized SwiGLU
+// outputs of the slots.
+// Four workgroups per CU (128 registers).
 template <int kBlk>
-__global__ void __launch_bounds__(256) k_moe_batch_down(wh_batch_args a) {
+__global__ void __launch_bounds__(256, 4) k_moe_batch_down(wh_batch_args a) {
     extern __shared__ __align__(16) float lds[];
     __shared__ uint32_t item_s;
-    const uint32_t n_mfma = a.meta[4], et = a.hidden >> 5, n_items = (a.meta[0] - n_mfma) * et;
-    for (;;) {
-        const uint32_t item = wh_next_item(a.meta + 3, &item_s);
-        if (item >= n_items) break;
-        const uint32_t u = a.uorder[n_mfma + item / et], tile = item % et;
+    const uint32_t n_mfma = a.meta[4], mt = a.hidden >> 6, et = a.hidden >> 5;
+    const uint32_t n_m = n_mfma * mt, n_items = n_m + (a.meta[0] - n_mfma) * et;
+    wh_queue q{a.meta + 3, &item_s, 0};
+    for (uint32_t item = q.first(); item < n_items; item = q.advance()) {
+        q.prefetch();
+        if (item < n_m) {
+            const uint32_t u = a.uorder[item / mt], row0 = (item % mt) * 64;
+            const wh_expert_ptrs ep = wh_batch_expert(a, a.uexp[u]);
+            const uint8_t* wm[1] = {ep.w2};
+            const uint8_t* sm[1] = {ep.s2};
+            wh_mfma_item<1>(
+                wm, sm, row0, a.inter, a.uoff[u], a.uoff[u + 1], (uint8_t*)lds,
+                [&](uint32_t s, const uint8_t*& rec, const uint8_t*& srec) {
+                    rec = a.hq8 + (size_t)s * a.inter;
+                    srec = a.hs8 + (size_t)s * (a.inter / 32);
+                },
+                [&](uint32_t s0, uint32_t count, const wh_v4f (&acc)[1][4]) {
+                    wh_mfma_store(a, a.y, a.hidden, row0, s0, count, acc);
+                });
+            continue;
+        }
+        const uint32_t e = item - n_m;
+        const uint32_t u = a.uorder[n_mfma + e / et], tile = e % et;
         const wh_expert_ptrs ep = wh_batch_expert(a, a.uexp[u]);
-        const uint32_t row = tile * 32 + (threadIdx.x >> 3);
         const uint32_t G = a.inter >> 5;
+        const uint32_t row = tile * 32 + (threadIdx.x >> 3);
         wh_exact_item<kBlk>(
             ep.w2 + (size_t)row * (a.inter >> 1), ep.s2 + (size_t)row * G, a.inter, a.uoff[u], a.uoff[u + 1], lds,
             [&](uint32_t s) { return a.hq + (size_t)s * a.inter; },

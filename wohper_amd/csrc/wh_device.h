@@ -58,13 +58,14 @@ struct wh_fp4x8 {
     wh_f2 a01, a23, b01, b23;
 };
 
-__device__ __forceinline__ wh_fp4x8 wh_fp4_decode8(uint32_t w) {
+__device__ __forceinline__ wh_fp4x8 wh_fp4_decode8(uint32_t w, uint32_t lut_hi = WH_FP4_LUT_HI,
+                                                   uint32_t lut_lo = WH_FP4_LUT_LO) {
     uint32_t sel_a = w & 0x07070707u;
-    uint32_t fa = __builtin_amdgcn_perm(WH_FP4_LUT_HI, WH_FP4_LUT_LO, sel_a);
+    uint32_t fa = __builtin_amdgcn_perm(lut_hi, lut_lo, sel_a);
     uint32_t r = __builtin_amdgcn_alignbit(w, w, 4);  // rotate right by 4
     fa |= r & 0x80808080u;
     uint32_t sel_b = r & 0x07070707u;
-    uint32_t fb = __builtin_amdgcn_perm(WH_FP4_LUT_HI, WH_FP4_LUT_LO, sel_b);
+    uint32_t fb = __builtin_amdgcn_perm(lut_hi, lut_lo, sel_b);
     fb |= w & 0x80808080u;
     wh_fp4x8 o;
     o.a01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)fa, false);

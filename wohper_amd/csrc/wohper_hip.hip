@@ -147,7 +147,6 @@ struct wh_ctx {
     HostBuf stage_in, stage_out;
     std::map<uint32_t, LayerTable> tables;  // device expert tables of the batch path
     uint32_t moe_mfma_min = 16;             // batch experts with this many tokens use MFMA (0: never)
-    uint32_t moe_debug = 0;                 // test support flags of the next batch call
     size_t moe_last_slots = 0, moe_last_npos = 0;  // sizes of the last single-chunk batch call
     size_t moe_last_hidden = 0, moe_last_inter = 0;
     std::mutex mu;
@@ -263,6 +262,8 @@ hipError_t kernel_setup_once(int device) {
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) == hipSuccess && v > lds)
             lds = v;
         hipError_t e = hipSuccess;
+        // leave room for the kernels' own static LDS (a few words each)
+        lds -= 1024;
         auto set = [&](const void* f) {
             hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
             if (r != hipSuccess && e == hipSuccess) e = r;
@@ -287,8 +288,6 @@ hipError_t kernel_setup_once(int device) {
         set((const void*)k_moe_batch_gateup<16>);
         set((const void*)k_moe_batch_down<0>);
         set((const void*)k_moe_batch_down<8>);
-        set((const void*)k_moe_batch_gateup_mfma);
-        set((const void*)k_moe_batch_down_mfma);
         if (e == hipSuccess) {
             g_max_lds = (size_t)lds;
         } else {
@@ -680,7 +679,7 @@ size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 struct BatchBufs {
     float* wgt;
     uint32_t *sorted, *uexp, *uoff, *uorder, *acc_order, *meta;
-    float *xq, *h, *hq, *y;
+    float *xq, *g, *u, *h, *hq, *y;
     uint8_t *xq8, *xs8, *hq8, *hs8;
 };
 int batch_bufs(wh_ctx* c, size_t npos, size_t slots, size_t hidden, size_t inter, BatchBufs* b) {
@@ -692,7 +691,9 @@ int batch_bufs(wh_ctx* c, size_t npos, size_t slots, size_t hidden, size_t inter
     };
     const size_t o_w = take(slots * 4), o_so = take(slots * 4), o_ue = take(slots * 4), o_uo = take((slots + 1) * 4),
                  o_ur = take(slots * 4), o_ac = take(slots * 4), o_me = take(16 * 4),
-                 o_xq = take(npos * hidden * 4), o_h = take(slots * inter * 4), o_y = take(slots * hidden * 4),
+                 o_xq = take(npos * hidden * 4), o_g = take(slots * inter * 4), o_u = take(slots * inter * 4),
+                 o_h = take(slots * inter * 4),
+                 o_y = take(slots * hidden * 4),
                  o_hq = take(slots * inter * 4), o_xq8 = take(npos * hidden), o_xs8 = take(npos * hidden / 32),
                  o_hq8 = take(slots * inter), o_hs8 = take(slots * inter / 32);
     WH_HIP(c->batch.ensure(off, false));
@@ -705,6 +706,8 @@ int batch_bufs(wh_ctx* c, size_t npos, size_t slots, size_t hidden, size_t inter
     b->acc_order = (uint32_t*)(base + o_ac);
     b->meta = (uint32_t*)(base + o_me);
     b->xq = (float*)(base + o_xq);
+    b->g = (float*)(base + o_g);
+    b->u = (float*)(base + o_u);
     b->h = (float*)(base + o_h);
     b->y = (float*)(base + o_y);
     b->hq = (float*)(base + o_hq);
@@ -727,13 +730,10 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
     WH_TRY(batch_bufs(c, std::min(npos, chunk), std::min(npos, chunk) * per_pos, hidden, inter, &b));
     const void* kg = hidden == 4096 ? (const void*)k_moe_batch_gateup<16> : (const void*)k_moe_batch_gateup<0>;
     const void* kd = inter == 2048 ? (const void*)k_moe_batch_down<8> : (const void*)k_moe_batch_down<0>;
-    const size_t lds_g = wh_exact_item_lds(hidden), lds_d = wh_exact_item_lds(inter), lds_m = wh_mfma_item_lds();
-    unsigned grid_g = 0, grid_d = 0, grid_mg = 0, grid_md = 0;
+    const size_t lds_g = wh_batch_wg_lds(hidden), lds_d = wh_batch_wg_lds(inter);
+    unsigned grid_g = 0, grid_d = 0;
     WH_TRY(persistent_grid(kg, lds_g, &grid_g));
     WH_TRY(persistent_grid(kd, lds_d, &grid_d));
-    WH_TRY(persistent_grid((const void*)k_moe_batch_gateup_mfma, lds_m, &grid_mg));
-    WH_TRY(persistent_grid((const void*)k_moe_batch_down_mfma, lds_m, &grid_md));
-    const uint32_t mfma_min = c->moe_mfma_min;
     for (size_t p0 = 0; p0 < npos; p0 += chunk) {
         const size_t n = std::min(chunk, npos - p0), slots = n * per_pos;
         wh_batch_args a;
@@ -767,43 +767,39 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         a.xq = b.xq;
         a.xq8 = b.xq8;
         a.xs8 = b.xs8;
+        a.g = b.g;
+        a.u = b.u;
         a.h = b.h;
         a.hq = b.hq;
         a.hq8 = b.hq8;
         a.hs8 = b.hs8;
         a.y = b.y;
         a.mfma_min = c->moe_mfma_min;
-        a.debug_raw = c->moe_debug & WH_DEBUG_RAW_GATEUP;
         a.out = out + p0 * hidden;
         a.status = c->status;
-        // the most items the queues can hold: used experts <= min(slots, ids)
+        // the most items the queues can hold: used experts <= min(slots, ids),
+        // and an expert has fewer MFMA items than exact ones
         const size_t max_used = std::min(slots, (size_t)t.n + (shared ? 1 : 0));
         const unsigned gg = (unsigned)std::min<size_t>(grid_g, max_used * (inter / 16));
         const unsigned gd = (unsigned)std::min<size_t>(grid_d, max_used * (hidden / 32));
-        // experts on MFMA items hold at least mfma_min slots each
-        const size_t max_mfma = mfma_min ? std::min(max_used, slots / mfma_min) : 0;
-        const unsigned gmg = (unsigned)std::min<size_t>(grid_mg, max_mfma * (inter / 64));
-        const unsigned gmd = (unsigned)std::min<size_t>(grid_md, max_mfma * (hidden / 64));
         k_moe_batch_pack<<<1, 256, 0, c->stream>>>(a);
         k_moe_batch_quant<<<(unsigned)((n * hidden / 16 + 255) / 256), 256, 0, c->stream>>>(
             a.x, a.x_is_bf16, (uint32_t)n, (uint32_t)hidden, a.xq, a.xq8, a.xs8, c->status, 1u);
-        if (gmg) k_moe_batch_gateup_mfma<<<gmg, 256, lds_m, c->stream>>>(a);
         if (hidden == 4096) k_moe_batch_gateup<16><<<gg, 256, lds_g, c->stream>>>(a);
         else k_moe_batch_gateup<0><<<gg, 256, lds_g, c->stream>>>(a);
         c->moe_last_slots = npos <= chunk ? slots : 0;
         c->moe_last_npos = n;
         c->moe_last_hidden = hidden;
         c->moe_last_inter = inter;
-        if (a.debug_raw) continue;  // test support: stop after the raw gate/up matvecs
+        k_moe_batch_swiglu<<<(unsigned)((slots * inter + 255) / 256), 256, 0, c->stream>>>(
+            a.g, a.u, a.h, (uint32_t)(slots * inter));
         k_moe_batch_quant<<<(unsigned)((slots * inter / 16 + 255) / 256), 256, 0, c->stream>>>(
             a.h, 0u, (uint32_t)slots, (uint32_t)inter, a.hq, a.hq8, a.hs8, c->status, 0u);
-        if (gmd) k_moe_batch_down_mfma<<<gmd, 256, lds_m, c->stream>>>(a);
         if (inter == 2048) k_moe_batch_down<8><<<gd, 256, lds_d, c->stream>>>(a);
         else k_moe_batch_down<0><<<gd, 256, lds_d, c->stream>>>(a);
         k_moe_batch_accumulate<<<dim3((unsigned)((hidden + 255) / 256), (unsigned)n), 256, 0, c->stream>>>(a);
         WH_HIP(hipGetLastError());
     }
-    c->moe_debug = 0;
     return WH_OK;
 }
 
@@ -1449,17 +1445,10 @@ static int batch_setup(wh_ctx* c, uint32_t layer, size_t npos, size_t topk, uint
     *has_shared = shared_expert != WH_NO_SHARED_EXPERT;
     if (*has_shared) WH_TRY(resolve_expert(c, shared_layer, shared_expert, shared));
     *fast = (*t)->fast && topk <= WH_BATCH_MAX_TOPK && topk + (*has_shared ? 1 : 0) <= WH_BATCH_MAX_ASSIGN &&
-            wh_exact_item_lds((*t)->hidden) <= g_max_lds && wh_exact_item_lds((*t)->inter) <= g_max_lds;
+            wh_batch_wg_lds((*t)->hidden) <= g_max_lds && wh_batch_wg_lds((*t)->inter) <= g_max_lds;
     if (*has_shared)
         *fast = *fast && expert_fast(*shared) && shared->w1->cols == (*t)->hidden &&
                 shared->w1->rows == (*t)->inter && shared->w2->rows == (*t)->hidden;
-    return WH_OK;
-}
-
-int wh_debug_moe_batch(wh_ctx* c, uint32_t flags) {
-    if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
-    c->moe_debug = flags;
     return WH_OK;
 }
 
@@ -1475,8 +1464,9 @@ int wh_debug_moe_batch_read(wh_ctx* c, int which, void* out, size_t bytes) {
     size_t n = 0;
     switch (which) {
         case 0: src = b.sorted; n = S * 4; break;
-        case 1: src = b.h; n = S * inter * 4; break;
-        case 2: src = b.hq; n = S * inter * 4; break;
+        case 1: src = b.g; n = S * inter * 4; break;
+        case 2: src = b.u; n = S * inter * 4; break;
+        case 8: src = b.hq; n = S * inter * 4; break;
         case 3: src = b.y; n = S * hidden * 4; break;
         case 4: src = b.meta; n = 8 * 4; break;
         case 5: src = b.uoff; n = (S + 1) * 4; break;
