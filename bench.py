@@ -151,7 +151,7 @@ def ragged_batch(ctx, n_layers: int, steps: int, warmup: int):
             "note": "wall clock and HIP events on the library stream; layers rotate so no step reuses cached weights"}
 
 
-def decode_stack(n_layers: int, steps: int, warmup: int, seed: int):
+def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps: int = 0):
     """Full-depth synthetic stack at batch 1: per layer the FP8 projections
     of one decode layer (wq_a, wq_b, wkv, wo_a in 8 row groups, wo_b; f32
     128x128 block scales) and the MoE FFN (1 shared + top-6 of 256 routed
@@ -231,8 +231,95 @@ def decode_stack(n_layers: int, steps: int, warmup: int, seed: int):
     res["frac_of_hbm_peak"] = round(res["GBps"] / HBM_PEAK_GBS, 4)
     for k in list(dev.values()) + [y, moe_x, moe_out]:
         ctx.device_free(k)
+    if batch_steps > 0:
+        res["batch16"] = decode_stack_batch16(ctx, layers, n_layers, batch_steps, seed)
     ctx.close()
     return res
+
+
+def decode_stack_batch16(ctx, layers, n_layers: int, steps: int, seed: int, batch: int = 16):
+    """The same resident stack at batch 16: per layer every FP8 projection
+    over 16 inputs (each bit-identical to its single-input GEMV) and the MoE
+    FFN of 16 positions through the expert-major batch path (shared expert on
+    all 16, routed experts grouped on the device; groups of 16 or more tokens
+    on MFMA).  Per-layer routing: top-6 of 256 sigmoid scores of N(0,1)
+    logits per position."""
+    from wohper_amd import workloads as wl
+
+    rng = np.random.default_rng(seed + 16)
+    sizes = {"x": 4096, "qlat": 1024, "oa": 8 * 4096, "ob": 8192}
+    dev = {}
+    for k, n in sizes.items():
+        dev[k] = ctx.device_alloc(batch * n * 4)
+        ctx.to_device(dev[k], rng.standard_normal((batch, n)).astype(np.float32))
+    outs = {"wq_a": 1024, "wq_b": 32768, "wkv": 512, "wo_a": 8192, "wo_b": 4096}
+    ydev = {k: ctx.device_alloc(batch * n * 4) for k, n in outs.items()}
+    moe_x = ctx.device_alloc(batch * 4096 * 2)
+    ctx.to_device(moe_x, wl.bf16_bits(rng.standard_normal((batch, 4096)).astype(np.float32)))
+    moe_out = ctx.device_alloc(batch * 4096 * 4)
+    total = steps + 1
+    ids_dev, sc_dev, used = [], [], []
+    for s_ in range(total):
+        per_i, per_s = [], []
+        for L in range(n_layers):
+            ids = np.empty((batch, wl.TOPK), np.uint32)
+            sc = np.empty((batch, wl.TOPK), np.float32)
+            for p in range(batch):
+                logits = rng.standard_normal(wl.N_ROUTED).astype(np.float32)
+                s_all = (1.0 / (1.0 + np.exp(-logits.astype(np.float64)))).astype(np.float32)
+                idx = np.argsort(-s_all, kind="stable")[:wl.TOPK]
+                ids[p], sc[p] = idx, s_all[idx]
+            if s_ > 0:
+                used.append(len(np.unique(ids)))
+            di, ds = ctx.device_alloc(ids.nbytes), ctx.device_alloc(sc.nbytes)
+            ctx.to_device(di, ids)
+            ctx.to_device(ds, sc)
+            per_i.append(di)
+            per_s.append(ds)
+        ids_dev.append(per_i)
+        sc_dev.append(per_s)
+
+    def step(s_):
+        for L in range(n_layers):
+            hs = layers[L]
+            ctx.fp8_gemv_multi_async(hs["wq_a"], 0, 1024, dev["x"], batch, 4096, ydev["wq_a"], 1024)
+            ctx.fp8_gemv_multi_async(hs["wq_b"], 0, 32768, dev["qlat"], batch, 1024, ydev["wq_b"], 32768)
+            ctx.fp8_gemv_multi_async(hs["wkv"], 0, 512, dev["x"], batch, 4096, ydev["wkv"], 512)
+            for g in range(8):
+                ctx.fp8_gemv_multi_async(hs["wo_a"], 1024 * g, 1024 * (g + 1), dev["oa"] + g * 4096 * 4, batch,
+                                         8 * 4096, ydev["wo_a"] + g * 1024 * 4, 8192)
+            ctx.fp8_gemv_multi_async(hs["wo_b"], 0, 4096, dev["ob"], batch, 8192, ydev["wo_b"], 4096)
+            ctx.moe_batch_async(L, ids_dev[s_][L], sc_dev[s_][L], batch, wl.TOPK, moe_x, True, moe_out,
+                                shared_key=(L, wl.N_ROUTED))
+
+    step(0)
+    ctx.synchronize()
+    t1 = time.perf_counter()
+    ctx.timer_start()
+    for s_ in range(1, total):
+        step(s_)
+    dev_us = ctx.timer_stop()
+    ctx.synchronize()
+    wall = time.perf_counter() - t1
+    step_us = dev_us / steps
+    mean_used = float(np.mean(used))
+    vec_bytes = batch * ((4096 + 1024 + 1024 + 32768 + 4096 + 512 + 8 * (4096 + 1024) + 8192 + 4096) * 4
+                         + 4096 * 2 + 4096 * 4)
+    step_bytes = n_layers * (wl.DECODE_LAYER_FP8_BYTES + wl.FP4_EXPERT_BYTES + vec_bytes) \
+        + sum(used) / steps * wl.FP4_EXPERT_BYTES
+    for per in ids_dev + sc_dev:
+        for d in per:
+            ctx.device_free(d)
+    for d in list(dev.values()) + list(ydev.values()) + [moe_x, moe_out]:
+        ctx.device_free(d)
+    gbs = step_bytes / (step_us * 1e-6) / 1e9
+    return {"workload": f"{n_layers} decode layers at batch {batch}: FP8 projections over {batch} inputs, "
+                        f"MoE of {batch} positions (shared + top-6 of 256 routed, expert-major batch path)",
+            "routed_experts_per_layer": round(mean_used, 1), "bytes_per_step": int(step_bytes),
+            "step_us": round(step_us, 1), "wall_step_us": round(wall / steps * 1e6, 1),
+            "layer_us": round(step_us / n_layers, 2), "GBps": round(gbs, 1),
+            "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "tokens_per_s": round(batch / (step_us * 1e-6), 1)}
 
 
 def main():
@@ -247,6 +334,8 @@ def main():
     ap.add_argument("--stack-layers", type=int, default=43, help="layers of the full-depth stack leg (0: skip)")
     ap.add_argument("--stack-steps", type=int, default=20)
     ap.add_argument("--batch-steps", type=int, default=20, help="steps of the ragged batch leg (0: skip)")
+    ap.add_argument("--stack-batch-steps", type=int, default=3,
+                    help="steps of the batch-16 full-depth stack (0: skip)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 5 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -334,7 +423,7 @@ def main():
     if args.stack_layers > 0:
         ctx.close()
         ctx = None
-        extra["decode_stack"] = decode_stack(args.stack_layers, args.stack_steps, 3, seed)
+        extra["decode_stack"] = decode_stack(args.stack_layers, args.stack_steps, 3, seed, args.stack_batch_steps)
         log(f"decode stack: {extra['decode_stack']}")
 
     line = {

@@ -237,6 +237,12 @@ typedef struct {
 } wh_gemv_desc;
 int wh_fp8_gemv_batch_async(wh_ctx* ctx, const wh_gemv_desc* descs, size_t n);
 
+/* Device-pointer variant of wh_fp8_gemv_multi (gemv_fp8_e4m3_ue8m0_rows_multi,
+ * E/compute.rs:6384-6577): n f32 inputs at x_dev + i * x_stride, outputs at
+ * y_dev + i * y_stride, each bit-identical to the single-input GEMV. */
+int wh_fp8_gemv_multi_async(wh_ctx* ctx, wh_tensor w, size_t row_start, size_t row_end, const float* x_dev, size_t n,
+                            size_t x_stride, float* y_dev, size_t y_stride);
+
 /* Device-pointer FP8 GEMV (rows [row_start,row_end) of w, x_dev f32 or bf16). */
 int wh_fp8_gemv_async(wh_ctx* ctx, wh_tensor w, size_t row_start, size_t row_end,
                       const float* x_dev, float* y_dev);

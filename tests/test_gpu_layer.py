@@ -49,6 +49,20 @@ def test_fp8_synthetic_store_and_batched_gemv(ctx, oracle):
         want = oracle.fp8_gemv(w, rows, cols, scales, rows // 128, cols // 128, xg[g], 256 * g, 256 * (g + 1))
         assert np.array_equal(bits(yg[256 * g:256 * (g + 1)]), bits(want)), g
     ctx.device_free(xg_dev)
+    # several inputs through one row range, device pointers
+    xm = rng.standard_normal((5, cols + 4)).astype(np.float32)
+    xm_dev = ctx.device_alloc(xm.nbytes)
+    ym_dev = ctx.device_alloc(5 * 700 * 4)
+    ctx.to_device(xm_dev, xm)
+    ctx.fp8_gemv_multi_async(t, 100, 700, xm_dev, 5, cols + 4, ym_dev, 700)
+    ctx.synchronize()
+    ym = np.empty((5, 700), np.float32)
+    ctx.from_device(ym, ym_dev)
+    for i in range(5):
+        want = oracle.fp8_gemv(w, rows, cols, scales, rows // 128, cols // 128, xm[i, :cols], 100, 700)
+        assert np.array_equal(bits(ym[i, :600]), bits(want)), i
+    ctx.device_free(xm_dev)
+    ctx.device_free(ym_dev)
     with pytest.raises(wohper_amd.DeepSeekV4KernelError) as e:
         ctx.fp8_gemv_batch_async([(t, 0, rows + 1, x_dev, y_dev)])
     assert e.value.name == "InvalidShape"

@@ -66,7 +66,7 @@ EXPORTED = (
     "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop", "wh_profile_routed",
     "wh_store_fp8_synthetic", "wh_synth_fp8_host", "wh_routed_and_shared_experts", "wh_fp8_gemv_batch_async",
     "wh_routed_and_shared_experts_async", "wh_moe_batch", "wh_moe_batch_async", "wh_set_moe_mfma_min",
-    "wh_debug_moe_batch_read",
+    "wh_debug_moe_batch_read", "wh_fp8_gemv_multi_async",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
 )
 
@@ -153,6 +153,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_moe_batch_async": (c.c_int, [vp, c.c_uint32, vp, vp, sz, sz, c.c_uint32, c.c_uint32, vp, c.c_int,
                                          vp]),
         "wh_set_moe_mfma_min": (c.c_int, [vp, c.c_uint32]),
+        "wh_fp8_gemv_multi_async": (c.c_int, [vp, c.c_uint64, sz, sz, vp, sz, sz, vp, sz]),
         "wh_debug_moe_batch_read": (c.c_int, [vp, c.c_int, vp, sz]),
     }
     for name, (res, args) in sig.items():
@@ -422,6 +423,13 @@ class Context:
         _check(self.lib.wh_moe_batch_async(self._h, layer_id, ctypes.c_void_p(ids_ptr), ctypes.c_void_p(scores_ptr),
                                            npos, topk, sl, se, ctypes.c_void_p(x_ptr), int(x_is_bf16),
                                            ctypes.c_void_p(out_ptr)), "moe_batch_async")
+
+    def fp8_gemv_multi_async(self, t: int, row_start: int, row_end: int, x_ptr: int, n: int, x_stride: int,
+                             y_ptr: int, y_stride: int):
+        """n inputs (f32, stride x_stride floats) through rows [row_start,
+        row_end) of an FP8 tensor, outputs at stride y_stride floats."""
+        _check(self.lib.wh_fp8_gemv_multi_async(self._h, t, row_start, row_end, ctypes.c_void_p(x_ptr), n, x_stride,
+                                                ctypes.c_void_p(y_ptr), y_stride), "fp8_gemv_multi_async")
 
     def set_moe_mfma_min(self, min_tokens: int):
         """Batch experts with at least min_tokens tokens run on MFMA (0: none)."""

@@ -1268,6 +1268,21 @@ int wh_fp8_gemv_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end,
     return launch_fp8(c, *t, row_start, row_end, x_dev, y_dev, 1, t->cols, row_end - row_start);
 }
 
+int wh_fp8_gemv_multi_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end, const float* x_dev, size_t n,
+                            size_t x_stride, float* y_dev, size_t y_stride) {
+    if (!c || !x_dev || !y_dev) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    Tensor* t = find_tensor(c, w);
+    if (!t) return WH_NOT_RESIDENT;
+    if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
+    if (n == 0 || row_start >= row_end || row_end > t->rows) return WH_INVALID_SHAPE;  // E/compute.rs:6400-6430
+    if (x_stride < t->cols) return WH_INPUT_TOO_SMALL;
+    if (y_stride < row_end - row_start) return WH_OUTPUT_TOO_SMALL;
+    if (((uintptr_t)x_dev & 15) || (x_stride & 3)) return WH_INVALID_ARGUMENT;
+    WH_HIP(hipSetDevice(c->device));
+    return launch_fp8(c, *t, row_start, row_end, x_dev, y_dev, n, x_stride, y_stride);
+}
+
 int wh_fp8_gemv_batch_async(wh_ctx* c, const wh_gemv_desc* descs, size_t n) {
     if (!c || (n && !descs)) return WH_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lk(c->mu);
