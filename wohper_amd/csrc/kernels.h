@@ -523,6 +523,46 @@ __device__ __forceinline__ float wh_fp4_lane_row_dot(const wh_fp4_lane_row<kBlk>
     }
     return acc;
 }
+// A lane's row streamed through a ring of kDepth blocks: the prologue issues
+// blocks 0..kDepth-1, the dot issues block b + kDepth once block b is
+// consumed.  Issuing a whole row at once stalls the wave behind the memory
+// system's back-pressure (loads issue in order, and nothing after them runs
+// until they have issued); kDepth blocks per wave are enough in flight to
+// keep HBM busy.
+template <int kDepth>
+struct wh_fp4_ring {
+    uint4 w[kDepth];
+};
+template <int kDepth>
+__device__ __forceinline__ void wh_fp4_ring_prologue(wh_fp4_ring<kDepth>& r, const uint8_t* __restrict__ wrow,
+                                                     uint32_t lane) {
+    const uint4* p = (const uint4*)wrow + lane;
+#pragma unroll
+    for (int b = 0; b < kDepth; ++b) r.w[b] = p[8 * b];
+}
+template <int kBlk, int kDepth>
+__device__ __forceinline__ float wh_fp4_ring_dot(wh_fp4_ring<kDepth>& r, const uint8_t* __restrict__ wrow,
+                                                 const float* xs, const float* s8row, uint32_t lane) {
+    static_assert(kBlk % 2 == 0 && kDepth % 2 == 0 && kDepth <= kBlk, "blocks are processed in pairs");
+    const uint4* p = (const uint4*)wrow + lane;
+    const float4* xp = (const float4*)xs + lane;
+    wh_fp4_blk_lds ba, bb;
+    float acc = 0.0f;
+    wh_fp4_blk_lds_read(ba, xp, s8row, 0, 0);
+#pragma unroll
+    for (int b = 0; b < kBlk; b += 2) {
+        wh_fp4_blk_lds_read(bb, xp, s8row, b + 1, wh_opaque_zero(acc));
+        __builtin_amdgcn_sched_barrier(0);
+        acc = wh_fp4_blk_compute(r.w[b % kDepth], ba, acc);
+        if (b + kDepth < kBlk) r.w[b % kDepth] = p[8 * (b + kDepth)];
+        if (b + 2 < kBlk) wh_fp4_blk_lds_read(ba, xp, s8row, b + 2, wh_opaque_zero(acc));
+        __builtin_amdgcn_sched_barrier(0);
+        acc = wh_fp4_blk_compute(r.w[(b + 1) % kDepth], bb, acc);
+        if (b + 1 + kDepth < kBlk) r.w[(b + 1) % kDepth] = p[8 * (b + 1 + kDepth)];
+    }
+    return acc;
+}
+
 // Runtime block count: weights streamed one block ahead.
 __device__ __forceinline__ float wh_fp4_lane_dot_rt(const uint8_t* __restrict__ wrow, uint32_t blocks,
                                                     const float* xs, const float* s8row, uint32_t lane) {
@@ -795,7 +835,7 @@ __device__ __forceinline__ void wh_xq_stage_store(const wh_xq_stage& st, bool bf
     float q[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        q[i] = wh_e4m3_round(wh_clamp448(v[i] * inv)) * sc;
+        q[i] = wh_e4m3_round(wh_clamp448_finite(v[i] * inv)) * sc;
     }
     // columns c0 + j: group c0/32, lane j % 8, k = 2*((c0/16) & 1) + j/8
     const uint32_t g = st.c0 >> 5, h = (st.c0 >> 4) & 1;
@@ -810,7 +850,7 @@ __device__ __forceinline__ float wh_dpp_row_shl8(float v) {  // lane i <- lane i
 // Gate/up: grid (n_experts * inter / 16, n_tokens), 256 threads = 32 rows =
 // 16 hidden rows x {w1, w3}; octet 2r runs w1 row r, octet 2r+1 the w3 row r.
 // kBlk = hidden / 256 when the rows fit in registers, else 0.
-template <int kBlk>
+template <int kBlk, int kRing = (kBlk < 4 ? 2 : 4)>
 __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
     extern __shared__ __align__(16) float lds[];
     const uint32_t tok = blockIdx.y;
@@ -840,15 +880,15 @@ __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
         wh_xq_stage_load(xst, xt, bf16, a.hidden, threadIdx.x);
         wh_s8_stage<kBlk> ss;
         wh_s8_stage_load<kBlk>(ss, srow, lane);
-        wh_fp4_lane_row<kBlk> r;
-        wh_fp4_lane_row_load<kBlk>(r, wrow, lane);
+        wh_fp4_ring<kRing> r;
+        wh_fp4_ring_prologue<kRing>(r, wrow, lane);
         __builtin_amdgcn_sched_barrier(0);
         wh_thr_stage_store(ts, thr);
         __syncthreads();
         wh_xq_stage_store(xst, bf16, xs, thr, a.status);
         wh_s8_stage_store<kBlk>(ss, s8row, lane);
         __syncthreads();
-        acc = wh_fp4_lane_row_dot<kBlk>(r, xs, s8row, lane);
+        acc = wh_fp4_ring_dot<kBlk, kRing>(r, wrow, xs, s8row, lane);
     } else {
         wh_thr_stage_store(ts, thr);
         __syncthreads();
@@ -904,13 +944,13 @@ __device__ __forceinline__ void wh_h_stage_store(const wh_h_stage& st, float* xs
     const float inv = wh_pow2f(-k), sc = wh_pow2f(k);
     const uint32_t g = st.t >> 2, kk = st.t & 3;  // columns 32g + 8kk + j: lane j, slot kk
 #pragma unroll
-    for (int j = 0; j < 8; ++j) xs[wh_xs_f4(g, j) * 4 + kk] = wh_e4m3_round(wh_clamp448(v[j] * inv)) * sc;
+    for (int j = 0; j < 8; ++j) xs[wh_xs_f4(g, j) * 4 + kk] = wh_e4m3_round(wh_clamp448_finite(v[j] * inv)) * sc;
 }
 
 // Down + ordered routed sum: grid (n_experts * hidden / 32, n_tokens), 256
 // threads = 32 output rows of one expert.  The last expert to finish a
 // 32-row slice sums all experts in route order (E/compute.rs:1948-2012).
-template <int kBlk>
+template <int kBlk, int kRing = (kBlk < 4 ? 2 : 4)>
 __global__ void __launch_bounds__(256) k_moe_down(wh_moe_args a) {
     extern __shared__ __align__(16) float lds[];
     __shared__ uint32_t last;
@@ -936,15 +976,15 @@ __global__ void __launch_bounds__(256) k_moe_down(wh_moe_args a) {
         wh_h_stage_load(hst, hrow, a.inter, threadIdx.x);  // inter == 2048: one pass
         wh_s8_stage<kBlk> ss;
         wh_s8_stage_load<kBlk>(ss, srow, lane);
-        wh_fp4_lane_row<kBlk> r;
-        wh_fp4_lane_row_load<kBlk>(r, wrow, lane);
+        wh_fp4_ring<kRing> r;
+        wh_fp4_ring_prologue<kRing>(r, wrow, lane);
         __builtin_amdgcn_sched_barrier(0);
         wh_thr_stage_store(ts, thr);
         __syncthreads();
         wh_h_stage_store(hst, xs, thr);
         wh_s8_stage_store<kBlk>(ss, s8row, lane);
         __syncthreads();
-        acc = wh_fp4_lane_row_dot<kBlk>(r, xs, s8row, lane);
+        acc = wh_fp4_ring_dot<kBlk, kRing>(r, wrow, xs, s8row, lane);
     } else {
         wh_thr_stage_store(ts, thr);
         __syncthreads();

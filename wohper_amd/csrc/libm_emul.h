@@ -152,17 +152,19 @@ WH_HD float wh_pow2f(int k) { return wh_bits_to_float((uint32_t)(k + 127) << 23)
 // +0.  For |t| >= 2^-6 the grid has 3 mantissa bits at t's own exponent, so
 // rounding is an integer add on the f32 bits: 0x7ffff below the dropped
 // half for positive t (ties stay low), 0x80000 for negative t (ties move the
-// magnitude up, i.e. toward -inf).  Below 2^-6 the grid is m * 2^-9.  The
-// generator checks this against a brute-force nearest over every float in
-// [-448, 448].
+// magnitude up, i.e. toward -inf).  Below 2^-6 the grid is n * 2^-9: |t| *
+// 2^33 as an integer holds every bit of |t| down to 2^-33 (all that can
+// decide a rounding there), and the same integer add rounds it to a multiple
+// of 2^24.  Both results are formed and one is selected, so a wave never
+// diverges.  The generator checks this against a brute-force nearest over
+// every float in [-448, 448].
 WH_HD float wh_e4m3_round(float t) {
     const uint32_t b = wh_float_to_bits(t);
-    const uint32_t s = b & 0x80000000u, a = b & 0x7fffffffu;
-    if (a >= 0x3c800000u) return wh_bits_to_float(((a + 0x7ffffu + (s >> 31)) & 0xfff00000u) | s);
-    const float r = wh_bits_to_float(a) * 512.0f;  // exact
-    const float n = floorf(r);
-    const float f = r - n;  // exact
-    const float m = (f > 0.5f || (f == 0.5f && s)) ? n + 1.0f : n;
-    if (m == 0.0f) return 0.0f;
-    return wh_bits_to_float(wh_float_to_bits(m * 0.001953125f) | s);
+    const uint32_t s = b & 0x80000000u, a = b & 0x7fffffffu, up = s >> 31;
+    const uint32_t normal = ((a + 0x7ffffu + up) & 0xfff00000u) | s;
+    const float at = wh_bits_to_float(a < 0x3c800000u ? a : 0x3c800000u);  // min(|t|, 2^-6)
+    const uint32_t u = (uint32_t)(at * 8589934592.0f);                        // * 2^33, < 2^28
+    const uint32_t n = (u + 0x7fffffu + up) >> 24;
+    const uint32_t sub = wh_float_to_bits((float)n * 0.001953125f) | (n ? s : 0u);
+    return wh_bits_to_float(a >= 0x3c800000u ? normal : sub);
 }

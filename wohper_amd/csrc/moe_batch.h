@@ -284,7 +284,7 @@ __global__ void __launch_bounds__(256) k_moe_batch_quant(const void* __restrict_
     const float inv = wh_pow2f(-k), sc = wh_pow2f(k);
     float q[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) q[j] = wh_e4m3_round(wh_clamp448(v[j] * inv));
+    for (int j = 0; j < 16; ++j) q[j] = wh_e4m3_round(wh_clamp448_finite(v[j] * inv));
     // codes: column c + 8k of the group sits at byte 4c + k; this thread
     // holds k = 2h + (j >> 3) for c = j & 7 (h = which half of the group)
     const uint32_t h = t & 1;

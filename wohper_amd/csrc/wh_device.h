@@ -128,6 +128,9 @@ __device__ __forceinline__ int wh_aq_scale_exp(float amax, const uint32_t* log2_
 __device__ __forceinline__ float wh_clamp448(float v) {
     return v < -448.0f ? -448.0f : (v > 448.0f ? 448.0f : v);
 }
+// The same clamp for finite v as one min/max pair; NaN maps to -448 (the
+// staging paths that use it report non-finite inputs as errors).
+__device__ __forceinline__ float wh_clamp448_finite(float v) { return fminf(fmaxf(v, -448.0f), 448.0f); }
 
 // DeepSeek-V4 SwiGLU on one gate/up pair (E/deepseek_v4.rs:590-594)
 __device__ __forceinline__ float wh_swiglu(float g, float u, const uint64_t* exp_tab,
