@@ -44,6 +44,18 @@ def test_fp8_gemv_4096_bit_exact(ctx, oracle, ue8m0):
     ctx.release(t)
 
 
+@pytest.mark.parametrize("rows,cols", [(1024, 1024), (256, 8192), (128, 3072), (512, 2048)])
+def test_fp8_decode_layer_widths_bit_exact(ctx, oracle, rows, cols):
+    """Every split-K width of the decode layer's projections (8, 16, 32 and
+    64 groups of 128 per row) plus a width that takes the runtime loop."""
+    case = wl.fp8_gemv_case(rows, cols, seed=cols)
+    t = ctx.store_fp8(case.w, rows, cols, case.scales, rows // 128, cols // 128, wohper_amd.SCALE_F32)
+    y, _ = ctx.fp8_gemv(t, case.x, rows)
+    want = oracle.fp8_gemv(case.w, rows, cols, case.scales, rows // 128, cols // 128, case.x)
+    assert np.array_equal(bits(y), bits(want))
+    ctx.release(t)
+
+
 def test_fp8_row_ranges_and_multi(ctx, oracle):
     """wo_a-style row groups (E/compute.rs:4244-4258) and the T2 multi-input GEMV."""
     rng = np.random.default_rng(5)

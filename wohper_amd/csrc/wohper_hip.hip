@@ -268,11 +268,16 @@ hipError_t kernel_setup_once(int device) {
             hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
             if (r != hipSuccess && e == hipSuccess) e = r;
         };
-        for (const void* f : {(const void*)k_fp8_gemv_sk<false, false, 4>, (const void*)k_fp8_gemv_sk<false, true, 4>,
-                              (const void*)k_fp8_gemv_sk<true, false, 4>, (const void*)k_fp8_gemv_sk<true, true, 4>,
-                              (const void*)k_fp8_gemv_sk<false, false, 0>, (const void*)k_fp8_gemv_sk<false, true, 0>,
-                              (const void*)k_fp8_gemv_sk<true, false, 0>, (const void*)k_fp8_gemv_sk<true, true, 0>})
-            set(f);
+#define WH_SK_SET(G)                                                                              \
+    for (const void* f : {(const void*)k_fp8_gemv_sk<false, false, G>, (const void*)k_fp8_gemv_sk<false, true, G>, \
+                          (const void*)k_fp8_gemv_sk<true, false, G>, (const void*)k_fp8_gemv_sk<true, true, G>})    \
+        set(f);
+        WH_SK_SET(0)
+        WH_SK_SET(1)
+        WH_SK_SET(2)
+        WH_SK_SET(4)
+        WH_SK_SET(8)
+#undef WH_SK_SET
         set((const void*)k_fp8_gemv<false, false>);
         set((const void*)k_fp8_gemv<false, true>);
         set((const void*)k_fp8_gemv<true, false>);
@@ -334,10 +339,14 @@ int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x,
     if (fp8_split_k(t)) {
         dim3 grid((unsigned)((r1 - r0 + 3) / 4), (unsigned)n_batch);
         const size_t lds = fp8_sk_lds(t.cols);
-        const bool g4 = t.cols == 4096;
+        // groups per segment known at compile time for the common widths
+        const size_t gps = t.cols / 128 / 8;
 #define WH_SK(SP, U8)                                                                             \
     do {                                                                                          \
-        if (g4) k_fp8_gemv_sk<SP, U8, 4><<<grid, 256, lds, c->stream>>>(a);                      \
+        if (gps == 1) k_fp8_gemv_sk<SP, U8, 1><<<grid, 256, lds, c->stream>>>(a);                 \
+        else if (gps == 2) k_fp8_gemv_sk<SP, U8, 2><<<grid, 256, lds, c->stream>>>(a);            \
+        else if (gps == 4) k_fp8_gemv_sk<SP, U8, 4><<<grid, 256, lds, c->stream>>>(a);            \
+        else if (gps == 8) k_fp8_gemv_sk<SP, U8, 8><<<grid, 256, lds, c->stream>>>(a);            \
         else k_fp8_gemv_sk<SP, U8, 0><<<grid, 256, lds, c->stream>>>(a);                         \
     } while (0)
         if (t.special) {
