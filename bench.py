@@ -36,10 +36,12 @@ TOKEN_BYTES = 6 * EXPERT_BYTES + 4096 * 2 + 4096 * 4   # + bf16 x + f32 y = 80,2
 # scales once, plus the vectors each kernel must read and write
 GATEUP_BYTES = 6 * 2 * (4_194_304 + 262_144) + 4096 * 2 + 6 * 2048 * 4     # 53,534,720
 DOWN_BYTES = 6 * (4_194_304 + 262_144) + 6 * 2048 * 4 + 4096 * 4           # 26,804,224
-# HBM bytes per k_moe_gateup<16> launch: rocprofv3 FETCH_SIZE 26,319 KiB and
-# WRITE_SIZE 48 KiB per dispatch, scaled by what the same counters read for a
-# 268,435,456-byte copy (FETCH x2.00, WRITE x1.00); see profiles/
-GATEUP_TRAFFIC_BYTES = (26_319 * 2 + 48) * 1024
+# The routed-expert kernels of each numerics mode (trace names).
+KERNELS = {False: ("k_moe_gateup_sk<2>", "k_moe_down_sk"), True: ("k_moe_gateup<16, 4>", "k_moe_down<8, 4>")}
+# HBM bytes per gate/up launch: rocprofv3 FETCH_SIZE and WRITE_SIZE KiB per
+# dispatch, scaled by what the same counters read for a 268,435,456-byte copy
+# (FETCH x2.00, WRITE x1.00); see profiles/.  None: not measured.
+GATEUP_TRAFFIC_BYTES = {False: None, True: (26_299 * 2 + 48) * 1024}
 FP8_BYTES = 4096 * 4096 + 32 * 32 * 4 + 4096 * 4 + 4096 * 4
 
 
@@ -109,6 +111,40 @@ def fp8_dense(ctx, steps: int, warmup: int):
             "note": "back-to-back launches over 40 rotating weight copies; wall clock and HIP events on the library stream"}
 
 
+def fp8_decode_layer(ctx, steps: int):
+    """Each FP8 projection of one decode layer on its own (wq_a, wq_b, wkv,
+    wo_a as 8 row groups with their own inputs in one launch, wo_b; f32
+    128x128 block scales), back to back over 8 rotating weight copies."""
+    from wohper_amd import workloads as wl
+
+    res = {}
+    copies = 8
+    rng = np.random.default_rng(7)
+    for i, (name, r, c, groups) in enumerate(wl.DECODE_LAYER_FP8):
+        hs = [ctx.store_fp8_synthetic(r, c, 3, wl.fp8_stream(1000 + k, i), wl.fp8_block_scales(11 + k, r, c))
+              for k in range(copies)]
+        xd, yd = ctx.device_alloc(groups * c * 4), ctx.device_alloc(r * 4)
+        ctx.to_device(xd, rng.standard_normal(groups * c).astype(np.float32))
+        rows = r // groups
+        descs = [ctx.gemv_descs([(h, rows * g, rows * (g + 1), xd + g * c * 4, yd + rows * g * 4)
+                                 for g in range(groups)]) for h in hs]
+        for k in range(10):
+            ctx.fp8_gemv_batch_async(descs[k % copies])
+        ctx.synchronize()
+        ctx.timer_start()
+        for k in range(steps):
+            ctx.fp8_gemv_batch_async(descs[k % copies])
+        us = ctx.timer_stop() / steps
+        nbytes = r * c + (r // 128) * (c // 128) * 4 + groups * c * 4 + r * 4
+        res[name] = {"shape": f"{r}x{c}", "groups": groups, "bytes": nbytes, "device_us": round(us, 2),
+                     "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        for h in hs:
+            ctx.release(h)
+        ctx.device_free(xd)
+        ctx.device_free(yd)
+    return res
+
+
 def ragged_batch(ctx, n_layers: int, steps: int, warmup: int):
     """Ragged batched MoE: 64 bf16 tokens, each top-6 of 256 FP4 experts under
     Zipf(1.1) popularity over a seeded permutation (seed 4), one launch
@@ -151,7 +187,7 @@ def ragged_batch(ctx, n_layers: int, steps: int, warmup: int):
             "note": "wall clock and HIP events on the library stream; layers rotate so no step reuses cached weights"}
 
 
-def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps: int = 0):
+def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps: int = 0, exact: bool = False):
     """Full-depth synthetic stack at batch 1: per layer the FP8 projections
     of one decode layer (wq_a, wq_b, wkv, wo_a in 8 row groups, wo_b; f32
     128x128 block scales) and the MoE FFN (1 shared + top-6 of 256 routed
@@ -161,6 +197,7 @@ def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps:
     from wohper_amd import workloads as wl
 
     ctx = wohper_amd.Context(0)
+    ctx.set_exact_numerics(exact)
     t0 = time.perf_counter()
     layers = []
     for L in range(n_layers):
@@ -336,6 +373,8 @@ def main():
     ap.add_argument("--batch-steps", type=int, default=20, help="steps of the ragged batch leg (0: skip)")
     ap.add_argument("--stack-batch-steps", type=int, default=3,
                     help="steps of the batch-16 full-depth stack (0: skip)")
+    ap.add_argument("--split-k", dest="exact", action="store_false",
+                    help="routed experts on the split-K kernels (summation order freed) instead of the bit-exact ones")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 5 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -349,6 +388,7 @@ def main():
 
     seed = 2
     ctx = wohper_amd.Context(0)
+    ctx.set_exact_numerics(args.exact)
     if args.copy_calibration:
         buf = np.arange(64 << 20, dtype=np.float32)
         for _ in range(5):
@@ -404,14 +444,26 @@ def main():
     dn_gbs = DOWN_BYTES / (dn_us * 1e-6) / 1e9
     log(f"kernels: k_moe_gateup {gu_us:.2f} us ({gu_gbs:.0f} GB/s), k_moe_down {dn_us:.2f} us ({dn_gbs:.0f} GB/s)")
 
-    extra = {"kernels": {"k_moe_gateup<16>": {"us": round(gu_us, 3), "GBps": round(gu_gbs, 1),
-                                              "bytes_per_launch": GATEUP_BYTES},
-                         "k_moe_down<8>": {"us": round(dn_us, 3), "GBps": round(dn_gbs, 1),
-                                           "bytes_per_launch": DOWN_BYTES},
+    gu_name, dn_name = KERNELS[args.exact]
+    extra = {"numerics": "exact (the reference kernel's summation order)" if args.exact else
+             "split-K (each matvec within 1e-5 * ||w_row|| * ||x|| of the reference kernel)",
+             "kernels": {gu_name: {"us": round(gu_us, 3), "GBps": round(gu_gbs, 1), "bytes_per_launch": GATEUP_BYTES},
+                         dn_name: {"us": round(dn_us, 3), "GBps": round(dn_gbs, 1), "bytes_per_launch": DOWN_BYTES},
                          "token_device_us": round(launch_us, 3)}}
+    # the other numerics mode's kernels on the same route lists
+    ctx.set_exact_numerics(not args.exact)
+    o_gu, o_dn = ctx.profile_routed(routes[args.warmup:args.warmup + min(args.steps, 64)], x_dev, True, out_dev,
+                                    max(200, args.steps))
+    ctx.set_exact_numerics(args.exact)
+    og, od = KERNELS[not args.exact]
+    extra["other_numerics_kernels"] = {og: {"us": round(o_gu, 3), "GBps": round(GATEUP_BYTES / (o_gu * 1e-6) / 1e9, 1)},
+                                       od: {"us": round(o_dn, 3), "GBps": round(DOWN_BYTES / (o_dn * 1e-6) / 1e9, 1)}}
+    log(f"other numerics: {extra['other_numerics_kernels']}")
     if not args.no_fp8:
         extra["fp8_dense_gemv"] = fp8_dense(ctx, max(200, args.steps), 40)
         log(f"fp8 dense: {extra['fp8_dense_gemv']}")
+        extra["fp8_decode_layer"] = fp8_decode_layer(ctx, 200)
+        log(f"fp8 decode layer: {extra['fp8_decode_layer']}")
     if args.batch_steps > 0:
         extra["ragged_batch"] = ragged_batch(ctx, args.layers, args.batch_steps, 3)
         log(f"ragged batch: {extra['ragged_batch']}")
@@ -423,7 +475,8 @@ def main():
     if args.stack_layers > 0:
         ctx.close()
         ctx = None
-        extra["decode_stack"] = decode_stack(args.stack_layers, args.stack_steps, 3, seed, args.stack_batch_steps)
+        extra["decode_stack"] = decode_stack(args.stack_layers, args.stack_steps, 3, seed, args.stack_batch_steps,
+                                             args.exact)
         log(f"decode stack: {extra['decode_stack']}")
 
     line = {
@@ -445,8 +498,8 @@ def main():
                    "bytes_per_step": TOKEN_BYTES, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
-                     "kernel": "k_moe_gateup<16>", "bytes_per_launch": GATEUP_BYTES,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES[args.exact],
+                     "kernel": gu_name, "bytes_per_launch": GATEUP_BYTES,
                      "avg_launch_us": round(gu_us, 3)},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -178,6 +178,26 @@ int wh_routed_and_shared_experts_async(wh_ctx* ctx, const wh_expert_route* route
                                        uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
                                        int x_is_bf16, size_t n_tokens, float* out_dev);
 
+/* Numerics of the routed/shared expert entry points above (and
+ * wh_fp4_expert_forward).  on = 1 (the default): every matvec follows the
+ * reference CPU kernel's summation order (E/deepseek_v4.rs:294-347), so
+ * outputs are bit-identical to it.  on = 0: for the model's expert shapes
+ * (hidden 2048 or 4096, inter 2048) split-K kernels free the summation
+ * order; the dequantized weights are the reference's values exactly and each
+ * matvec agrees with the reference kernel on the same input within
+ * max|diff| <= 1e-5 * ||w_row||_2 * ||x||_2 (fp32 accumulation), while
+ * act-quant, SwiGLU and the route-weighted sum stay bit-exact given the
+ * matvec outputs.  No counterpart in the reference (it has one CPU kernel). */
+int wh_set_exact_numerics(wh_ctx* ctx, int on);
+/* Test support, no counterpart in the reference: with capture on, the
+ * routed-expert entry points also keep each expert's gate and up matvec
+ * outputs; wh_debug_moe_token_read copies a buffer of the last call (T
+ * tokens, n experts including the shared one) to host.  which: 0 gate/up
+ * (f32 [T][n][2][inter], gate then up; capture must be on), 1 SwiGLU
+ * outputs (f32 [T][n][inter]), 2 expert outputs (f32 [T][n][hidden]). */
+int wh_debug_moe_token_capture(wh_ctx* ctx, int on);
+int wh_debug_moe_token_read(wh_ctx* ctx, int which, void* out, size_t bytes);
+
 /* Batched routed experts for npos positions, expert-major, replacing the
  * batch-prefill MoE of the reference: per-position weights score / sum (or
  * 1 / topk when the sum is not finite and positive or a score is not finite)

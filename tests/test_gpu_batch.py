@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 import wohper_amd
+from parity_util import check_matvec as _check_matvec
 from wohper_amd import workloads as wl
 
 pytestmark = pytest.mark.gpu
@@ -148,40 +149,6 @@ def test_batch_generic_shapes(ctx, oracle):
     got = ctx.moe_batch(43, ids, sc, x)
     want = oracle.moe_batch(experts, ids, sc, x)
     assert np.array_equal(bits(got), bits(want))
-
-
-def _dequant(oracle, m):
-    """Reference dequantized FP4 matrix (float64) of (packed, scales, rows, cols, scale_cols)."""
-    packed, scales, rows, cols, scale_cols = m
-    _, ue, fp4, _ = oracle.luts()
-    packed = np.asarray(packed, np.uint8).reshape(rows, cols // 2)
-    nib = np.empty((rows, cols), np.uint8)
-    nib[:, 0::2] = packed & 15
-    nib[:, 1::2] = packed >> 4
-    sc = ue[np.asarray(scales, np.uint8).reshape(rows, scale_cols)].astype(np.float64)
-    return fp4[nib].astype(np.float64) * np.repeat(sc, cols // scale_cols, axis=1)
-
-
-_ROW_NORMS = {}
-
-
-def _row_norms(oracle, m):
-    key = (id(m[0]), id(m[1]))
-    if key not in _ROW_NORMS:
-        w = _dequant(oracle, m)
-        _ROW_NORMS[key] = (m, np.sqrt((w * w).sum(axis=1)))
-    return _ROW_NORMS[key][1]
-
-
-def _check_matvec(oracle, m, x, got, exact, what):
-    want = oracle.fp4_matvec(*m, x)
-    if exact:
-        assert np.array_equal(bits(got), bits(want)), what
-        return 0.0
-    tol = 1e-5 * _row_norms(oracle, m) * np.linalg.norm(np.asarray(x, np.float64))
-    diff = np.abs(got.astype(np.float64) - want.astype(np.float64))
-    assert np.all(diff <= tol), (what, float((diff / tol).max()))
-    return float((diff / tol).max())
 
 
 def _mfma_case(ctx, oracle, layer, n_exp, hidden, inter, seed, npos, mfma_min):

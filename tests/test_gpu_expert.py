@@ -11,6 +11,14 @@ import wohper_amd
 from wohper_amd import workloads as wl
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def exact_numerics(ctx):
+    """These tests pin the kernels that follow the reference's summation
+    order, bit for bit."""
+    ctx.set_exact_numerics(True)
+    yield
 KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
 
 

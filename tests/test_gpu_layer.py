@@ -10,6 +10,14 @@ from wohper_amd import workloads as wl
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def exact_numerics(ctx):
+    """These tests pin the kernels that follow the reference's summation
+    order, bit for bit."""
+    ctx.set_exact_numerics(True)
+    yield
+
+
 def bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 

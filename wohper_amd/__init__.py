@@ -66,7 +66,8 @@ EXPORTED = (
     "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop", "wh_profile_routed",
     "wh_store_fp8_synthetic", "wh_synth_fp8_host", "wh_routed_and_shared_experts", "wh_fp8_gemv_batch_async",
     "wh_routed_and_shared_experts_async", "wh_moe_batch", "wh_moe_batch_async", "wh_set_moe_mfma_min",
-    "wh_debug_moe_batch_read", "wh_fp8_gemv_multi_async",
+    "wh_debug_moe_batch_read", "wh_fp8_gemv_multi_async", "wh_set_exact_numerics", "wh_debug_moe_token_capture",
+    "wh_debug_moe_token_read",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
 )
 
@@ -155,6 +156,9 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_set_moe_mfma_min": (c.c_int, [vp, c.c_uint32]),
         "wh_fp8_gemv_multi_async": (c.c_int, [vp, c.c_uint64, sz, sz, vp, sz, sz, vp, sz]),
         "wh_debug_moe_batch_read": (c.c_int, [vp, c.c_int, vp, sz]),
+        "wh_set_exact_numerics": (c.c_int, [vp, c.c_int]),
+        "wh_debug_moe_token_capture": (c.c_int, [vp, c.c_int]),
+        "wh_debug_moe_token_read": (c.c_int, [vp, c.c_int, vp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -434,6 +438,23 @@ class Context:
     def set_moe_mfma_min(self, min_tokens: int):
         """Batch experts with at least min_tokens tokens run on MFMA (0: none)."""
         _check(self.lib.wh_set_moe_mfma_min(self._h, min_tokens), "set_moe_mfma_min")
+
+    def set_exact_numerics(self, on: bool):
+        """True (default): routed-expert matvecs in the reference kernel's
+        summation order (bit-identical); False: split-K kernels, each matvec
+        within 1e-5 * ||w_row|| * ||x|| of it."""
+        _check(self.lib.wh_set_exact_numerics(self._h, int(bool(on))), "set_exact_numerics")
+
+    def debug_moe_token_capture(self, on: bool):
+        _check(self.lib.wh_debug_moe_token_capture(self._h, int(bool(on))), "debug_moe_token_capture")
+
+    def debug_moe_token_read(self, which: int, shape) -> np.ndarray:
+        """Last routed-expert call: 0 gate/up [T][n][2][inter], 1 SwiGLU
+        [T][n][inter], 2 expert outputs [T][n][hidden] (f32)."""
+        out = np.empty(shape, np.float32)
+        _check(self.lib.wh_debug_moe_token_read(self._h, which, out.ctypes.data_as(ctypes.c_void_p), out.nbytes),
+               "debug_moe_token_read")
+        return out
 
     def debug_moe_batch_read(self, which: int, shape, dtype) -> np.ndarray:
         out = np.empty(shape, dtype)

@@ -753,6 +753,9 @@ struct wh_moe_args {
     float* out;                    // [n_tokens][hidden] routed sum
     uint32_t* cnt_y;               // [n_tokens][hidden/32] arrivals per 32-row slice
     uint32_t* status;
+    float* gu;                     // null, or [n_tokens][n_experts][2][inter]: gate and up captured
+    const uint32_t* xq;            // split-K kernels: act-quant codes of x, f16 pairs in lane order
+    const float* xk;               // split-K kernels: [n_tokens][hidden/64] block scales of x
 };
 
 // The per-binade log2f thresholds of the act-quant scale, staged in LDS: a
@@ -795,10 +798,11 @@ __device__ __forceinline__ void wh_xq_stage_load(wh_xq_stage& st, const void* x,
     }
 }
 // Act-quant of the 64-block the thread's quad covers (E/compute.rs:2504-2521,
-// block 64), result written to LDS in FP4 lane order.  Non-finite input is
-// reported through the status word.
-__device__ __forceinline__ void wh_xq_stage_store(const wh_xq_stage& st, bool bf16, float* xs,
-                                                  const uint32_t* log2_thr, uint32_t* status) {
+// block 64): q = the E4M3 values before the block scale sc.  All lanes take
+// part in the block's amax; returns false for a thread without columns.
+// Non-finite input is reported through the status word.
+__device__ __forceinline__ bool wh_xq_quant16(const wh_xq_stage& st, bool bf16, const uint32_t* log2_thr,
+                                              uint32_t* status, float (&q)[16], float& sc) {
     float v[16];
     if (bf16) {
         const uint32_t w[8] = {st.raw[0].x, st.raw[0].y, st.raw[0].z, st.raw[0].w,
@@ -827,20 +831,25 @@ __device__ __forceinline__ void wh_xq_stage_store(const wh_xq_stage& st, bool bf
     }
     amax = fmaxf(amax, wh_dpp_quad_swap1(amax));  // the quad holds one 64-block
     amax = fmaxf(amax, wh_dpp_quad_swap2(amax));
-    if (!st.on) return;
+    if (!st.on) return false;
     if (bad) atomicOr(status, WH_ST_NONFINITE_INPUT);
     if (!(amax <= 3.4028235e38f)) amax = 1.0f;
     const int k = wh_aq_scale_exp(amax, log2_thr);
-    const float inv = wh_pow2f(-k), sc = wh_pow2f(k);
-    float q[16];
+    const float inv = wh_pow2f(-k);
+    sc = wh_pow2f(k);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        q[i] = wh_e4m3_round(wh_clamp448_finite(v[i] * inv)) * sc;
-    }
+    for (int i = 0; i < 16; ++i) q[i] = wh_e4m3_round(wh_clamp448_finite(v[i] * inv));
+    return true;
+}
+// The same, result written to LDS in FP4 lane order (scaled values).
+__device__ __forceinline__ void wh_xq_stage_store(const wh_xq_stage& st, bool bf16, float* xs,
+                                                  const uint32_t* log2_thr, uint32_t* status) {
+    float q[16], sc;
+    if (!wh_xq_quant16(st, bf16, log2_thr, status, q, sc)) return;
     // columns c0 + j: group c0/32, lane j % 8, k = 2*((c0/16) & 1) + j/8
     const uint32_t g = st.c0 >> 5, h = (st.c0 >> 4) & 1;
 #pragma unroll
-    for (int l = 0; l < 8; ++l) ((float2*)xs)[wh_xs_f4(g, l) * 2 + h] = make_float2(q[l], q[8 + l]);
+    for (int l = 0; l < 8; ++l) ((float2*)xs)[wh_xs_f4(g, l) * 2 + h] = make_float2(q[l] * sc, q[8 + l] * sc);
 }
 
 __device__ __forceinline__ float wh_dpp_row_shl8(float v) {  // lane i <- lane i+8 (within 16)
@@ -906,6 +915,11 @@ __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
     if ((threadIdx.x & 15) == 0) {
         if (!(fabsf(v) <= 3.4028235e38f) || !(fabsf(u) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
         a.h[((size_t)tok * a.n_experts + e) * a.inter + row] = wh_swiglu(v, u, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
+        if (a.gu) {
+            float* gu = a.gu + ((size_t)tok * a.n_experts + e) * 2 * a.inter;
+            gu[row] = v;
+            gu[a.inter + row] = u;
+        }
     }
 }
 
@@ -928,7 +942,9 @@ __device__ __forceinline__ void wh_h_stage_load(wh_h_stage& st, const float* __r
         st.p = st.q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 }
-__device__ __forceinline__ void wh_h_stage_store(const wh_h_stage& st, float* xs, const uint32_t* log2_thr) {
+template <bool kCodes = false>
+__device__ __forceinline__ void wh_h_stage_store(const wh_h_stage& st, float* xs, const uint32_t* log2_thr,
+                                                 float* xk = nullptr) {
     const float v[8] = {st.p.x, st.p.y, st.p.z, st.p.w, st.q.x, st.q.y, st.q.z, st.q.w};
     float amax = 0.0f;
 #pragma unroll
@@ -944,7 +960,55 @@ __device__ __forceinline__ void wh_h_stage_store(const wh_h_stage& st, float* xs
     const float inv = wh_pow2f(-k), sc = wh_pow2f(k);
     const uint32_t g = st.t >> 2, kk = st.t & 3;  // columns 32g + 8kk + j: lane j, slot kk
 #pragma unroll
-    for (int j = 0; j < 8; ++j) xs[wh_xs_f4(g, j) * 4 + kk] = wh_e4m3_round(wh_clamp448_finite(v[j] * inv)) * sc;
+    for (int j = 0; j < 8; ++j) {
+        const float q = wh_e4m3_round(wh_clamp448_finite(v[j] * inv));
+        xs[wh_xs_f4(g, j) * 4 + kk] = kCodes ? q : q * sc;
+    }
+    if constexpr (kCodes) {
+        if ((st.t & 7) == 0) xk[st.t >> 3] = sc;
+    }
+}
+
+// After this workgroup's y stores of 32-row slice rb: the last expert
+// workgroup of the slice to arrive sums all experts' rows in route order
+// (E/compute.rs:1948-2012).  All threads of the workgroup call it.
+__device__ __forceinline__ void wh_moe_routed_sum(const wh_moe_args& a, uint32_t tok, uint32_t rb, uint32_t* last) {
+    wh_stores_done();
+    __syncthreads();
+    uint32_t* cnt = a.cnt_y + (size_t)tok * (a.hidden >> 5) + rb;
+    if (threadIdx.x == 0) *last = wh_arrive(cnt) == a.n_experts - 1;
+    __syncthreads();
+    if (!*last || threadIdx.x >= 32) return;
+    const uint32_t r_out = rb * 32 + threadIdx.x;
+    const size_t t0 = (size_t)tok * a.n_experts * a.hidden;
+    const uint32_t nr = a.n_experts - a.has_shared;  // routed experts
+    float o = 0.0f;
+    if (nr == 1) {
+        o = wh_load_coherent(a.y + t0 + r_out);
+    } else if (nr > 1) {
+        // valid_route_weight_sum (E/compute.rs:2014-2030)
+        float sum = 0.0f;
+        bool valid = true;
+        for (uint32_t i = 0; i < nr; ++i) {
+            float w = a.route_w[i];
+            if (!(fabsf(w) <= 3.4028235e38f && w >= 0.0f)) valid = false;
+            sum = sum + w;
+        }
+        if (sum <= 1.1920929e-07f) valid = false;
+        const float uniform = 1.0f / (float)nr;
+        for (uint32_t i = 0; i < nr; ++i) {
+            float w = valid ? a.route_w[i] / sum : uniform;
+            float p = wh_load_coherent(a.y + t0 + (size_t)i * a.hidden + r_out) * w;
+            o = o + p;
+        }
+    }
+    if (a.has_shared) {
+        // hidden = shared(x); hidden += routed (E/compute.rs:1929-1941)
+        const float sh = wh_load_coherent(a.y + t0 + (size_t)nr * a.hidden + r_out);
+        o = nr == 0 ? sh : sh + o;
+    }
+    a.out[(size_t)tok * a.hidden + r_out] = o;
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Down + ordered routed sum: grid (n_experts * hidden / 32, n_tokens), 256
@@ -1003,42 +1067,7 @@ __global__ void __launch_bounds__(256) k_moe_down(wh_moe_args a) {
         if (!(fabsf(yv) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
         wh_store_coherent(a.y + yb + row, yv);
     }
-    wh_stores_done();
-    __syncthreads();
-    uint32_t* cnt = a.cnt_y + (size_t)tok * (a.hidden >> 5) + rb;
-    if (threadIdx.x == 0) last = wh_arrive(cnt) == a.n_experts - 1;
-    __syncthreads();
-    if (!last || threadIdx.x >= 32) return;
-    const uint32_t r_out = rb * 32 + threadIdx.x;
-    const size_t t0 = (size_t)tok * a.n_experts * a.hidden;
-    const uint32_t nr = a.n_experts - a.has_shared;  // routed experts
-    float o = 0.0f;
-    if (nr == 1) {
-        o = wh_load_coherent(a.y + t0 + r_out);
-    } else if (nr > 1) {
-        // valid_route_weight_sum (E/compute.rs:2014-2030)
-        float sum = 0.0f;
-        bool valid = true;
-        for (uint32_t i = 0; i < nr; ++i) {
-            float w = a.route_w[i];
-            if (!(fabsf(w) <= 3.4028235e38f && w >= 0.0f)) valid = false;
-            sum = sum + w;
-        }
-        if (sum <= 1.1920929e-07f) valid = false;
-        const float uniform = 1.0f / (float)nr;
-        for (uint32_t i = 0; i < nr; ++i) {
-            float w = valid ? a.route_w[i] / sum : uniform;
-            float p = wh_load_coherent(a.y + t0 + (size_t)i * a.hidden + r_out) * w;
-            o = o + p;
-        }
-    }
-    if (a.has_shared) {
-        // hidden = shared(x); hidden += routed (E/compute.rs:1929-1941)
-        const float sh = wh_load_coherent(a.y + t0 + (size_t)nr * a.hidden + r_out);
-        o = nr == 0 ? sh : sh + o;
-    }
-    a.out[(size_t)tok * a.hidden + r_out] = o;
-    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wh_moe_routed_sum(a, tok, rb, &last);
 }
 
 // Bit-exact dequant of a resident FP4 tensor back to reference values

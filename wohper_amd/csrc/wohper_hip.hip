@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -16,6 +17,7 @@
 #define WH_LIBM_TABLES_INCLUDED 1
 #include "kernels.h"
 #include "moe_batch.h"
+#include "moe_token.h"
 #include "wohper_hip.h"
 
 namespace {
@@ -143,10 +145,13 @@ struct wh_ctx {
     size_t device_bytes = 0;
     uint32_t* status = nullptr;  // device status word
     uint32_t* status_host = nullptr;
-    Scratch x_in, y_out, h, ybuf, cnt_y, tmp, batch, routes, bout;
+    Scratch x_in, y_out, h, ybuf, cnt_y, tmp, batch, routes, bout, gu, xq;
     HostBuf stage_in, stage_out;
     std::map<uint32_t, LayerTable> tables;  // device expert tables of the batch path
     uint32_t moe_mfma_min = 16;             // batch experts with this many tokens use MFMA (0: never)
+    bool exact = true;                      // routed experts in the reference's summation order
+    bool capture_gu = false;                // routed experts keep gate/up in `gu` (test support)
+    size_t tok_last_n = 0, tok_last_tokens = 0, tok_last_hidden = 0, tok_last_inter = 0;
     size_t moe_last_slots = 0, moe_last_npos = 0;  // sizes of the last single-chunk batch call
     size_t moe_last_hidden = 0, moe_last_inter = 0;
     std::mutex mu;
@@ -156,6 +161,13 @@ struct wh_ctx {
 namespace {
 
 thread_local char g_last_error[256] = "";
+
+// Rows per wave of the split-K gate/up kernel (8 or 16); WH_SK_ROWS
+// overrides the default for tuning runs.
+const int g_sk_rows = [] {
+    const char* v = std::getenv("WH_SK_ROWS");
+    return (v && std::atoi(v) == 8) ? 8 : 16;
+}();
 
 int hip_status_at(hipError_t e, const char* what, int line) {
     if (e == hipSuccess) return WH_OK;
@@ -490,14 +502,46 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
     a.out = out_dev;
     a.cnt_y = c->cnt_y.as<uint32_t>();
     a.status = c->status;
+    if (c->capture_gu) {
+        WH_HIP(c->gu.ensure(n_tokens * n * 2 * inter * sizeof(float), false));
+        a.gu = c->gu.as<float>();
+    }
+    c->tok_last_n = n, c->tok_last_tokens = n_tokens, c->tok_last_hidden = hidden, c->tok_last_inter = inter;
+    // split-K kernels (summation order freed) for the model's shapes unless
+    // the context asks for the reference's order
+    const bool sk = !c->exact && (hidden == 2048 || hidden == 4096) && inter == 2048;
     if (stages & 1) {
-        dim3 ggrid((unsigned)(n * inter / 16), (unsigned)n_tokens);
-        if (hidden == 4096) k_moe_gateup<16><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
-        else k_moe_gateup<0><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
+        if (sk) {
+            // x act-quantized once per token, then the split-K gate/up
+            WH_HIP(c->xq.ensure(n_tokens * (hidden * 2 + hidden / 16), false));
+            uint32_t* xq = c->xq.as<uint32_t>();
+            float* xk = (float*)(xq + n_tokens * hidden / 2);
+            a.xq = xq;
+            a.xk = xk;
+            const unsigned tok = (unsigned)n_tokens;
+            const int rows = g_sk_rows;
+            dim3 ggrid((unsigned)(n * inter / rows), tok);
+            if (hidden == 4096) {
+                k_moe_xquant<2><<<tok, 256, 0, c->stream>>>(x_dev, a.x_is_bf16, xq, xk, c->status);
+                if (rows == 8) k_moe_gateup_sk<2, 8><<<ggrid, 256, 0, c->stream>>>(a);
+                else k_moe_gateup_sk<2, 16><<<ggrid, 256, 0, c->stream>>>(a);
+            } else {
+                k_moe_xquant<1><<<tok, 128, 0, c->stream>>>(x_dev, a.x_is_bf16, xq, xk, c->status);
+                if (rows == 8) k_moe_gateup_sk<1, 8><<<ggrid, 128, 0, c->stream>>>(a);
+                else k_moe_gateup_sk<1, 16><<<ggrid, 128, 0, c->stream>>>(a);
+            }
+        } else if (hidden == 4096) {
+            dim3 ggrid((unsigned)(n * inter / 16), (unsigned)n_tokens);
+            k_moe_gateup<16><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
+        } else {
+            dim3 ggrid((unsigned)(n * inter / 16), (unsigned)n_tokens);
+            k_moe_gateup<0><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
+        }
     }
     if (stages & 2) {
         dim3 dgrid((unsigned)(n * hidden / 32), (unsigned)n_tokens);
-        if (inter == 2048) k_moe_down<8><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
+        if (sk) k_moe_down_sk<<<dgrid, 256, wh_moe_down_sk_lds(inter), c->stream>>>(a);
+        else if (inter == 2048) k_moe_down<8><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
         else k_moe_down<0><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
     }
     WH_HIP(hipGetLastError());
@@ -1501,6 +1545,43 @@ int wh_debug_moe_batch_read(wh_ctx* c, int which, void* out, size_t bytes) {
     if (bytes < n) return WH_OUTPUT_TOO_SMALL;
     WH_HIP(hipStreamSynchronize(c->stream));
     WH_HIP(hipMemcpy(out, src, n, hipMemcpyDeviceToHost));
+    return WH_OK;
+}
+
+int wh_set_exact_numerics(wh_ctx* c, int on) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->exact = on != 0;
+    return WH_OK;
+}
+
+int wh_debug_moe_token_capture(wh_ctx* c, int on) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->capture_gu = on != 0;
+    return WH_OK;
+}
+
+int wh_debug_moe_token_read(wh_ctx* c, int which, void* out, size_t bytes) {
+    if (!c || !out) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    const size_t T = c->tok_last_tokens, n = c->tok_last_n, hidden = c->tok_last_hidden, inter = c->tok_last_inter;
+    if (T == 0) return WH_INVALID_ARGUMENT;
+    const void* src = nullptr;
+    size_t len = 0;
+    switch (which) {
+        case 0:
+            if (!c->capture_gu || c->gu.n < T * n * 2 * inter * sizeof(float)) return WH_INVALID_ARGUMENT;
+            src = c->gu.p, len = T * n * 2 * inter * sizeof(float);
+            break;
+        case 1: src = c->h.p, len = T * n * inter * sizeof(float); break;
+        case 2: src = c->ybuf.p, len = T * n * hidden * sizeof(float); break;
+        default: return WH_INVALID_ARGUMENT;
+    }
+    if (bytes < len) return WH_OUTPUT_TOO_SMALL;
+    WH_HIP(hipStreamSynchronize(c->stream));
+    WH_HIP(hipMemcpy(out, src, len, hipMemcpyDeviceToHost));
     return WH_OK;
 }
 

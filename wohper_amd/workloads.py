@@ -109,10 +109,11 @@ def synth_fp4_host(lib, seed: int, layer: int, expert: int, matrix: int, rows: i
     return packed.reshape(rows, cols // 2), scales.reshape(rows, cols // 32)
 
 
-def synth_expert_host(lib, seed: int, layer: int, expert: int, hidden=HIDDEN, inter=INTER):
-    w1 = synth_fp4_host(lib, seed, layer, expert, 0, inter, hidden)
-    w3 = synth_fp4_host(lib, seed, layer, expert, 1, inter, hidden)
-    w2 = synth_fp4_host(lib, seed, layer, expert, 2, hidden, inter)
+def synth_expert_host(lib, seed: int, layer: int, expert: int, hidden=HIDDEN, inter=INTER, scale_lo=SCALE_LO,
+                      scale_hi=SCALE_HI):
+    w1 = synth_fp4_host(lib, seed, layer, expert, 0, inter, hidden, scale_lo, scale_hi)
+    w3 = synth_fp4_host(lib, seed, layer, expert, 1, inter, hidden, scale_lo, scale_hi)
+    w2 = synth_fp4_host(lib, seed, layer, expert, 2, hidden, inter, scale_lo, scale_hi)
     return ((w1[0], w1[1], inter, hidden, hidden // 32), (w3[0], w3[1], inter, hidden, hidden // 32),
             (w2[0], w2[1], hidden, inter, inter // 32))
 
