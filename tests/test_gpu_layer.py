@@ -96,3 +96,72 @@ def test_shared_plus_routed_bit_exact(ctx, oracle, n_routed):
     else:
         want = sh
     assert np.array_equal(bits(got), bits(want.astype(np.float32)))
+
+
+def test_fp8_batched_decode_layer_set_order_and_formats(ctx, oracle):
+    """A decode layer's projection set in one call (one grouped launch),
+    bit-exact per projection; a descriptor reading an earlier one's output
+    in the same call sees it (in-order semantics); f32 and UE8M0 scales
+    mixed in one call."""
+    rng = np.random.default_rng(31)
+    host, dev, descs, want = {}, [], [], []
+
+    def alloc(arr):
+        p = ctx.device_alloc(arr.nbytes)
+        ctx.to_device(p, arr)
+        dev.append(p)
+        return p
+
+    for i, (name, r, c, groups) in enumerate(wl.DECODE_LAYER_FP8):
+        sc = wl.fp8_block_scales(40 + i, r, c)
+        t = ctx.store_fp8_synthetic(r, c, 5, wl.fp8_stream(90, i), sc)
+        host[name] = (t, wl.synth_fp8_host(ctx.lib, 5, wl.fp8_stream(90, i), r, c), sc, r, c)
+    y_all = ctx.device_alloc(64 * 1024 * 4)
+    dev.append(y_all)
+    off = 0
+    for name, r, c, groups in wl.DECODE_LAYER_FP8:
+        t, w, sc, _, _ = host[name]
+        rows = r // groups
+        x = rng.standard_normal((groups, c)).astype(np.float32)
+        xp = alloc(x)
+        for g in range(groups):
+            descs.append((t, rows * g, rows * (g + 1), xp + g * c * 4, y_all + (off + rows * g) * 4))
+            want.append((off + rows * g, oracle.fp8_gemv(w, r, c, sc, r // 128, c // 128, x[g], rows * g, rows * (g + 1))))
+        off += r
+    # chained: wq_b reads the output of wq_a within the same call
+    t_a, w_a, sc_a, r_a, c_a = host["wq_a"]
+    t_b, w_b, sc_b, r_b, c_b = host["wq_b"]
+    xa = rng.standard_normal(c_a).astype(np.float32)
+    xa_p = alloc(xa)
+    mid = ctx.device_alloc(r_a * 4)
+    out = ctx.device_alloc(r_b * 4)
+    dev += [mid, out]
+    descs.append((t_a, 0, r_a, xa_p, mid))
+    descs.append((t_b, 0, r_b, mid, out))
+    y_mid = oracle.fp8_gemv(w_a, r_a, c_a, sc_a, r_a // 128, c_a // 128, xa)
+    y_chain = oracle.fp8_gemv(w_b, r_b, c_b, sc_b, r_b // 128, c_b // 128, y_mid)
+    # a UE8M0-scaled tensor between f32-scaled ones
+    case = wl.fp8_gemv_case(1024, 2048, seed=3, ue8m0_compatible=True)
+    sbytes = (np.log2(case.scales).astype(np.int32) + 127).astype(np.uint8)
+    t_u = ctx.store_fp8(case.w, 1024, 2048, sbytes, 8, 16, wohper_amd.SCALE_UE8M0)
+    xu_p = alloc(case.x)
+    yu = ctx.device_alloc(1024 * 4)
+    dev.append(yu)
+    descs.insert(3, (t_u, 0, 1024, xu_p, yu))
+    ctx.fp8_gemv_batch_async(descs)
+    ctx.synchronize()
+    got = np.empty(64 * 1024, np.float32)
+    ctx.from_device(got, y_all)
+    for o, w_ in want:
+        assert np.array_equal(bits(got[o:o + w_.size]), bits(w_)), o
+    got_chain = np.empty(r_b, np.float32)
+    ctx.from_device(got_chain, out)
+    assert np.array_equal(bits(got_chain), bits(y_chain))
+    got_u = np.empty(1024, np.float32)
+    ctx.from_device(got_u, yu)
+    assert np.array_equal(bits(got_u), bits(oracle.fp8_gemv(case.w, 1024, 2048, case.scales, 8, 16, case.x)))
+    for p in dev:
+        ctx.device_free(p)
+    for t, *_ in host.values():
+        ctx.release(t)
+    ctx.release(t_u)
