@@ -178,6 +178,19 @@ int wh_routed_and_shared_experts_async(wh_ctx* ctx, const wh_expert_route* route
                                        uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
                                        int x_is_bf16, size_t n_tokens, float* out_dev);
 
+/* compute_deepseek_fp8_shared_expert_into_hidden (E/compute.rs:5545-5614):
+ * output[..w2 rows] = W2 act_quant(swiglu(W1 xq, W3 xq)) with
+ * xq = act_quant(input) (block 64), each stage bit-identical to the
+ * reference.  w1/w3/w2 are resident FP8 tensors (wh_store_fp8); shapes are
+ * checked as the reference does ("DeepSeek shared expert input dim",
+ * "... projection shape" -> WH_INVALID_SHAPE; w2 rows beyond output_len ->
+ * WH_OUTPUT_TOO_SMALL).  The async variant takes device pointers (f32; x and
+ * y may alias, like the reference's in-place hidden_states). */
+int wh_fp8_shared_expert(wh_ctx* ctx, wh_tensor w1, wh_tensor w3, wh_tensor w2, const float* input,
+                         size_t input_len, float* output, size_t output_len);
+int wh_fp8_shared_expert_async(wh_ctx* ctx, wh_tensor w1, wh_tensor w3, wh_tensor w2, const float* x_dev,
+                               float* y_dev);
+
 /* Numerics of the routed/shared expert entry points above (and
  * wh_fp4_expert_forward).  on = 1 (the default): every matvec follows the
  * reference CPU kernel's summation order (E/deepseek_v4.rs:294-347), so

@@ -253,6 +253,20 @@ def moe_batch(experts, route_ids, route_scores, x, shared=None):
     return acc
 
 
+def fp8_shared_expert(w1, s1, w3, s3, w2, s2, hidden, inter, x):
+    """compute_deepseek_fp8_shared_expert_into_hidden (E/compute.rs:5545-5614):
+    W* are E4M3 bytes [rows][cols], s* f32 128x128 block scales."""
+    w1, w3, w2 = _u(w1), _u(w3), _u(w2)
+    s1, s3, s2 = _f(s1), _f(s3), _f(s2)
+    x = _f(x)
+    y = np.zeros(hidden, np.float32)
+    st = lib().or_fp8_shared_expert(_pu(w1), _pf(s1), _pu(w3), _pf(s3), _pu(w2), _pf(s2), hidden, inter,
+                                    s1.shape[0], s1.shape[1], s2.shape[0], s2.shape[1], _pf(x), _pf(y))
+    if st:
+        raise OracleError(st)
+    return y
+
+
 def swiglu_array(g, u):
     """DeepSeek-V4 SwiGLU elementwise (E/deepseek_v4.rs:590-594)."""
     g, u = _f(g), _f(u)

@@ -165,3 +165,50 @@ def test_fp8_batched_decode_layer_set_order_and_formats(ctx, oracle):
     for t, *_ in host.values():
         ctx.release(t)
     ctx.release(t_u)
+
+
+def test_fp8_shared_expert_bit_exact(ctx, oracle):
+    """compute_deepseek_fp8_shared_expert_into_hidden (E/compute.rs:5545-5614)
+    at the model's shapes, host-slice and in-place device variants, plus the
+    closed-form case of the oracle's tests and the reference's shape errors."""
+    hidden, inter = 4096, 2048
+    cases = [wl.fp8_gemv_case(inter, hidden, seed=61), wl.fp8_gemv_case(inter, hidden, seed=62),
+             wl.fp8_gemv_case(hidden, inter, seed=63)]
+    t = [ctx.store_fp8(c.w, c.w.shape[0], c.w.shape[1], c.scales, c.scales.shape[0], c.scales.shape[1],
+                       wohper_amd.SCALE_F32) for c in cases]
+    x = (np.random.default_rng(64).standard_normal(hidden) * 2.0).astype(np.float32)
+    want = oracle.fp8_shared_expert(cases[0].w, cases[0].scales, cases[1].w, cases[1].scales, cases[2].w,
+                                    cases[2].scales, hidden, inter, x)
+    got = ctx.fp8_shared_expert(t[0], t[1], t[2], x, hidden)
+    assert np.array_equal(bits(got), bits(want))
+    # in place on the device, like the reference's hidden_states
+    h_dev = ctx.device_alloc(x.nbytes)
+    ctx.to_device(h_dev, x)
+    ctx.fp8_shared_expert_async(t[0], t[1], t[2], h_dev, h_dev)
+    ctx.synchronize()
+    got_dev = np.empty_like(x)
+    ctx.from_device(got_dev, h_dev)
+    ctx.device_free(h_dev)
+    assert np.array_equal(bits(got_dev), bits(want))
+    with pytest.raises(wohper_amd.DeepSeekV4KernelError) as e:
+        ctx.fp8_shared_expert(t[0], t[2], t[2], x, hidden)  # w3 is 4096 x 2048
+    assert e.value.name == "InvalidShape"
+    with pytest.raises(wohper_amd.DeepSeekV4KernelError) as e:
+        ctx.fp8_shared_expert(t[0], t[1], t[2], x, hidden - 1)
+    assert e.value.name == "OutputTooSmall"
+    for h in t:
+        ctx.release(h)
+    # the oracle's closed-form case
+    n = 128
+    w1, w3, w2 = (np.zeros((n, n), np.uint8) for _ in range(3))
+    w1[0, 0], w3[0, 0], w2[5, 0] = 0x38, 0x3C, 0x40
+    w1[1, 1], w3[1, 1], w2[6, 1] = 0x38, 0x38, 0x38
+    one = np.ones((1, 1), np.float32)
+    tk = [ctx.store_fp8(w, n, n, one, 1, 1, wohper_amd.SCALE_F32) for w in (w1, w3, w2)]
+    xk = np.zeros(n, np.float32)
+    xk[0], xk[1] = 2.0, 0.3
+    wk = np.zeros(n, np.float32)
+    wk[5], wk[6] = 11.0, 0.0546875
+    assert np.array_equal(ctx.fp8_shared_expert(*tk, xk, n), wk)
+    for h in tk:
+        ctx.release(h)

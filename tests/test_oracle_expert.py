@@ -136,3 +136,36 @@ def test_moe_batch_order_and_independence(oracle):
     for p in range(3):
         ys = oracle.fp4_expert_forward(*sh, x[p])
         assert np.array_equal((ys + out[p]).view(np.uint32), with_sh[p].view(np.uint32))
+
+
+def _fp8_shared_kat():
+    """A sparse FP8 shared expert whose output follows in closed form
+    (hidden = inter = 128, one 128x128 block, scales 1):
+      w1[0,0] = 1, w3[0,0] = 1.5, w2[5,0] = 2 and w1[1,1] = w3[1,1] = w2[6,1] = 1;
+      x[0] = 2, x[1] = 0.3.
+    act_quant(x) (block 64): scale 2^ceil(log2(2/448)) = 2^-7, so x0 -> 256 * 2^-7
+    = 2 and x1 -> 38.4 -> nearest E4M3 40 -> 0.3125.  gate = (2, 0.3125),
+    up = (3, 0.3125); h0 = silu(2) * 3 = 5.28478, h1 = silu(0.3125) * 0.3125
+    = 0.0563938.  act_quant(h): scale 2^ceil(log2(5.28478/448)) = 2^-6; h0 * 64
+    = 338.23 -> 352 (grid step 32) -> 5.5; h1 * 64 = 3.6092 -> 3.5 (step 0.25)
+    -> 0.0546875.  y[5] = 2 * 5.5 = 11, y[6] = 0.0546875, every other y is 0."""
+    n = 128
+    w1 = np.zeros((n, n), np.uint8)
+    w3 = np.zeros((n, n), np.uint8)
+    w2 = np.zeros((n, n), np.uint8)
+    w1[0, 0], w3[0, 0], w2[5, 0] = 0x38, 0x3C, 0x40  # E4M3 1.0, 1.5, 2.0
+    w1[1, 1], w3[1, 1], w2[6, 1] = 0x38, 0x38, 0x38
+    x = np.zeros(n, np.float32)
+    x[0], x[1] = 2.0, 0.3
+    want = np.zeros(n, np.float32)
+    want[5], want[6] = 11.0, 0.0546875
+    return w1, w3, w2, np.ones((1, 1), np.float32), x, want
+
+
+def test_fp8_shared_expert_closed_form(oracle):
+    """Pins the stage order of E/compute.rs:5585-5612: a swapped w1/w3
+    (silu(3) * 2), a skipped act-quant of x (x1 stays 0.3) or of h (y5 =
+    10.57) each changes the result."""
+    w1, w3, w2, s, x, want = _fp8_shared_kat()
+    got = oracle.fp8_shared_expert(w1, s, w3, s, w2, s, 128, 128, x)
+    assert np.array_equal(got, want)

@@ -67,7 +67,7 @@ EXPORTED = (
     "wh_store_fp8_synthetic", "wh_synth_fp8_host", "wh_routed_and_shared_experts", "wh_fp8_gemv_batch_async",
     "wh_routed_and_shared_experts_async", "wh_moe_batch", "wh_moe_batch_async", "wh_set_moe_mfma_min",
     "wh_debug_moe_batch_read", "wh_fp8_gemv_multi_async", "wh_set_exact_numerics", "wh_debug_moe_token_capture",
-    "wh_debug_moe_token_read",
+    "wh_debug_moe_token_read", "wh_fp8_shared_expert", "wh_fp8_shared_expert_async",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
 )
 
@@ -157,6 +157,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_fp8_gemv_multi_async": (c.c_int, [vp, c.c_uint64, sz, sz, vp, sz, sz, vp, sz]),
         "wh_debug_moe_batch_read": (c.c_int, [vp, c.c_int, vp, sz]),
         "wh_set_exact_numerics": (c.c_int, [vp, c.c_int]),
+        "wh_fp8_shared_expert": (c.c_int, [vp, c.c_uint64, c.c_uint64, c.c_uint64, f32p, sz, f32p, sz]),
+        "wh_fp8_shared_expert_async": (c.c_int, [vp, c.c_uint64, c.c_uint64, c.c_uint64, vp, vp]),
         "wh_debug_moe_token_capture": (c.c_int, [vp, c.c_int]),
         "wh_debug_moe_token_read": (c.c_int, [vp, c.c_int, vp, sz]),
     }
@@ -438,6 +440,19 @@ class Context:
     def set_moe_mfma_min(self, min_tokens: int):
         """Batch experts with at least min_tokens tokens run on MFMA (0: none)."""
         _check(self.lib.wh_set_moe_mfma_min(self._h, min_tokens), "set_moe_mfma_min")
+
+    def fp8_shared_expert(self, w1: int, w3: int, w2: int, x, out_len: int) -> np.ndarray:
+        """compute_deepseek_fp8_shared_expert_into_hidden on resident FP8
+        tensors: returns the w2-rows output."""
+        x = _f32(x)
+        y = np.empty(out_len, np.float32)
+        _check(self.lib.wh_fp8_shared_expert(self._h, w1, w3, w2, _p(x, ctypes.c_float), x.size,
+                                             _p(y, ctypes.c_float), y.size), "fp8_shared_expert")
+        return y
+
+    def fp8_shared_expert_async(self, w1: int, w3: int, w2: int, x_ptr: int, y_ptr: int):
+        _check(self.lib.wh_fp8_shared_expert_async(self._h, w1, w3, w2, ctypes.c_void_p(x_ptr),
+                                                   ctypes.c_void_p(y_ptr)), "fp8_shared_expert_async")
 
     def set_exact_numerics(self, on: bool):
         """True (default): routed-expert matvecs in the reference kernel's

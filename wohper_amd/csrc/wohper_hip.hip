@@ -1694,6 +1694,78 @@ int wh_fp4_expert_forward(wh_ctx* c, uint32_t layer, uint32_t expert, const floa
     return WH_OK;
 }
 
+namespace {
+// compute_deepseek_fp8_shared_expert_into_hidden (E/compute.rs:5545-5614) on
+// device pointers: xq = act_quant(x); gate = W1 xq; up = W3 xq;
+// h = act_quant(swiglu(gate, up)); y = W2 h.  Every stage is the bit-exact
+// kernel of its own entry point.  x and y may alias (the reference works in
+// place): x is copied to scratch first.
+int fp8_shared_launch(wh_ctx* c, const Tensor& w1, const Tensor& w3, const Tensor& w2, const float* x_dev,
+                      float* y_dev) {
+    const size_t hidden = w1.cols, inter = w1.rows;
+    WH_HIP(c->tmp.ensure((hidden + 3 * inter) * sizeof(float), false));
+    float* xq = c->tmp.as<float>();
+    float* gate = xq + hidden;
+    float* up = gate + inter;
+    float* h = up + inter;
+    WH_HIP(hipMemcpyAsync(xq, x_dev, hidden * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
+    k_act_quant_inplace<<<(unsigned)((hidden + 63) / 64), 256, 0, c->stream>>>(xq, (uint32_t)hidden, 64);
+    WH_TRY(launch_fp8(c, w1, 0, inter, xq, gate, 1, hidden, inter));
+    WH_TRY(launch_fp8(c, w3, 0, inter, xq, up, 1, hidden, inter));
+    k_swiglu_generic<<<(unsigned)((inter + 255) / 256), 256, 0, c->stream>>>(gate, up, h, (uint32_t)inter, c->status);
+    k_act_quant_inplace<<<(unsigned)((inter + 63) / 64), 256, 0, c->stream>>>(h, (uint32_t)inter, 64);
+    WH_TRY(launch_fp8(c, w2, 0, w2.rows, h, y_dev, 1, inter, w2.rows));
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// Shape rules of E/compute.rs:5558-5570.
+int fp8_shared_check(wh_ctx* c, wh_tensor h1, wh_tensor h3, wh_tensor h2, const Tensor** w1, const Tensor** w3,
+                     const Tensor** w2) {
+    *w1 = find_tensor(c, h1);
+    *w3 = find_tensor(c, h3);
+    *w2 = find_tensor(c, h2);
+    if (!*w1 || !*w3 || !*w2) return WH_NOT_RESIDENT;
+    if ((*w1)->kind != kFp8 || (*w3)->kind != kFp8 || (*w2)->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
+    if ((*w3)->cols != (*w1)->cols) return WH_INVALID_SHAPE;  // "DeepSeek shared expert input dim"
+    if ((*w1)->rows != (*w3)->rows || (*w2)->cols != (*w1)->rows)
+        return WH_INVALID_SHAPE;  // "DeepSeek shared expert projection shape"
+    return WH_OK;
+}
+}  // namespace
+
+int wh_fp8_shared_expert(wh_ctx* c, wh_tensor w1, wh_tensor w3, wh_tensor w2, const float* input, size_t input_len,
+                         float* output, size_t output_len) {
+    if (!c || !input || !output) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    const Tensor *t1, *t3, *t2;
+    WH_TRY(fp8_shared_check(c, w1, w3, w2, &t1, &t3, &t2));
+    if (t1->cols != input_len) return WH_INVALID_SHAPE;  // "DeepSeek shared expert input dim"
+    if (t2->rows > output_len) return WH_OUTPUT_TOO_SMALL;
+    const size_t hidden = t1->cols, osz = t2->rows;
+    WH_HIP(c->x_in.ensure(hidden * sizeof(float), false));
+    WH_HIP(c->y_out.ensure(osz * sizeof(float), false));
+    WH_HIP(c->stage_out.ensure(osz * sizeof(float)));
+    WH_HIP(hipMemcpyAsync(c->x_in.p, input, hidden * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    WH_TRY(fp8_shared_launch(c, *t1, *t3, *t2, c->x_in.as<float>(), c->y_out.as<float>()));
+    WH_HIP(hipMemcpyAsync(c->stage_out.p, c->y_out.p, osz * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    const int st = read_status(c);
+    if (st != WH_OK) return st;
+    std::memcpy(output, c->stage_out.p, osz * sizeof(float));
+    return WH_OK;
+}
+
+int wh_fp8_shared_expert_async(wh_ctx* c, wh_tensor w1, wh_tensor w3, wh_tensor w2, const float* x_dev,
+                               float* y_dev) {
+    if (!c || !x_dev || !y_dev) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    const Tensor *t1, *t3, *t2;
+    WH_TRY(fp8_shared_check(c, w1, w3, w2, &t1, &t3, &t2));
+    return fp8_shared_launch(c, *t1, *t3, *t2, x_dev, y_dev);
+}
+
 int wh_device_alloc(wh_ctx* c, size_t bytes, void** out) {
     if (!c || !out) return WH_INVALID_ARGUMENT;
     *out = nullptr;
