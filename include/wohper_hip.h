@@ -46,7 +46,17 @@ enum wh_status {
     WH_HIP_ERROR = 12,
     WH_INVALID_ARGUMENT = 13,
     WH_NON_FINITE_INPUT = 14,      /* an activation block held inf/NaN */
-    WH_UNSUPPORTED = 15
+    WH_UNSUPPORTED = 15,
+    /* ZCBLK01 block errors: ComputeError (E/compute.rs:330-344); the
+     * reference's Display text of the error is in wh_last_error() */
+    WH_TRUNCATED_QUANT_BLOCK = 16,           /* TruncatedQuantBlock(field) */
+    WH_INVALID_QUANT_BLOCK_MAGIC = 17,       /* InvalidQuantBlockMagic */
+    WH_UNSUPPORTED_QUANT_BLOCK_VERSION = 18, /* UnsupportedQuantBlockVersion */
+    WH_INVALID_QUANT_BLOCK = 19,             /* InvalidQuantBlock(reason) */
+    WH_TENSOR_INDEX_OUT_OF_RANGE = 20,       /* TensorIndexOutOfRange */
+    /* experts-pack errors: ModelFormatError (E/model_format.rs:32-56) */
+    WH_UNALIGNED = 21,                       /* Unaligned{field, value} */
+    WH_IO_ERROR = 22                         /* Io: open/read of the pack file */
 };
 
 /* Scale formats of an FP8 block-scaled tensor. */
@@ -102,6 +112,79 @@ int wh_store_fp4(wh_ctx* ctx, const uint8_t* packed, size_t packed_len, const ui
  * as in deepseek_v4_fp4_expert_from_quant_block (E/compute.rs:1249-1268). */
 int wh_store_expert(wh_ctx* ctx, uint32_t layer_id, uint32_t expert_id, wh_tensor w1, wh_tensor w3,
                     wh_tensor w2);
+
+/* ------------------------------------------------------ ZCBLK01 blocks
+ * The engine's expert blocks as they come off disk (one ZCBLK01 block per
+ * (layer, expert), E/direct_io.rs ReadTicket -> IoBlockPtr{ptr, len}).
+ * Parsing follows parse_quant_block (E/compute.rs:1099-1148) and
+ * QuantBlockLayout::tensor (E/compute.rs:545-600) check for check; a bad
+ * block returns the status of the reference's error and wh_last_error()
+ * holds its Display text (e.g. "truncated ZCBLK field: record table").
+ * The three functions below read only host memory and need no device. */
+
+/* One tensor record (QuantTensorLayout, E/compute.rs:441-451) resolved
+ * against the block: offsets are absolute byte offsets into the block. */
+typedef struct {
+    uint16_t dtype_original;
+    uint16_t quant_format;  /* 2401 FP8 E4M3, 2402 FP4 E2M1 packed, 2403 UE8M0 */
+    uint32_t rank;
+    uint32_t flags;         /* TensorRole code in the low 16 bits */
+    float scale;
+    float zero_point;
+    size_t name_offset;     /* name bytes (no terminator) */
+    size_t name_len;
+    size_t shape_offset;    /* {u32 rank, rank x u64 dims} */
+    size_t data_offset;
+    size_t data_bytes;
+} wh_quant_tensor;
+
+/* One FP4 projection of an expert block (Fp4Matvec, E/deepseek_v4.rs:411-417):
+ * packed weight [rows x cols/2] and UE8M0 scales [rows x scale_cols] as byte
+ * ranges of the block. */
+typedef struct {
+    size_t rows, cols, scale_cols;
+    size_t weight_offset, weight_bytes;
+    size_t scale_offset, scale_bytes;
+} wh_fp4_view;
+
+/* parse_quant_block (E/compute.rs:1099-1148): header fields of a block. */
+int wh_quant_block_header(const uint8_t* block, size_t block_len, uint32_t* tensor_count,
+                          uint32_t* quant_format, uint32_t* flags);
+/* parse_quant_block + QuantBlockLayout::tensor(index) (E/compute.rs:545-600). */
+int wh_quant_block_tensor(const uint8_t* block, size_t block_len, size_t index, wh_quant_tensor* out);
+/* deepseek_v4_fp4_expert_from_quant_block (E/compute.rs:1249-1268): the
+ * w1 (gate), w3 (up), w2 (down) projections found by name suffix. */
+int wh_quant_block_fp4_expert(const uint8_t* block, size_t block_len, wh_fp4_view out[3]);
+
+/* Makes the FP4 expert of a ZCBLK01 block resident under (layer_id,
+ * expert_id).  Replaces the per-decode parse of the block the IO scheduler
+ * delivered (compute_expert_block -> deepseek_v4_fp4_expert_from_quant_block,
+ * E/compute.rs:5467-5478, 5636): the block is parsed and uploaded once.
+ * An expert already stored under the key is replaced. */
+int wh_store_expert_block(wh_ctx* ctx, uint32_t layer_id, uint32_t expert_id, const uint8_t* block,
+                          size_t block_len);
+
+/* One entry of the experts-pack index <model>.experts_pack.index.json
+ * (ExpertPackEntryDisk, E/model_format.rs:448-455). */
+typedef struct {
+    uint32_t layer_id;
+    uint32_t expert_id;
+    uint64_t offset;        /* 2 MB aligned */
+    uint64_t disk_bytes;    /* 2 MB aligned */
+    uint64_t payload_bytes; /* the ZCBLK01 block: the first payload_bytes at offset */
+} wh_expert_pack_entry;
+
+/* Loads the listed experts of a consolidated experts pack into the store:
+ * the reads the reference's scheduler queues per decode step
+ * (E/scheduler.rs:163-176, fixed file #1) done once, each block parsed as by
+ * wh_store_expert_block.  Entries are checked as load_optional_expert_pack
+ * does (E/model_format.rs:488-491: offset and disk_bytes 2 MB aligned) before
+ * any read; payload_bytes > disk_bytes is rejected too.  Reads of the next
+ * block overlap the upload of the previous one.  *stored counts the experts
+ * made resident (all of them on WH_OK; the ones before the failing entry
+ * otherwise). */
+int wh_store_expert_pack(wh_ctx* ctx, const char* pack_path, const wh_expert_pack_entry* entries, size_t n,
+                         size_t* stored);
 
 /* Device-side synthetic fill of an FP4 expert with the counter-based RNG of
  * the benchmark (uniform packed bytes, UE8M0 bytes in [scale_lo, scale_hi]),

@@ -14,6 +14,9 @@ include/wohper_hip.h (libwohper_hip.so, built from wohper_amd/csrc):
   fp8_act_quant_dequant_in_place   compute.rs:2504             fp8_act_quant_dequant_in_place
   compute_active_experts           compute.rs:1948             Context.routed_experts
   DeepSeekV4KernelError            deepseek_v4.rs:398-408      DeepSeekV4KernelError
+  parse_quant_block                compute.rs:1099             quant_block_header / quant_block_tensor
+  deepseek_v4_fp4_expert_from_quant_block compute.rs:1249      deepseek_v4_fp4_expert_from_quant_block
+  load_optional_expert_pack        model_format.rs:458         model_format.load_optional_expert_pack
 
 The slice-based functions upload the weights for the call, as the reference
 reads them from its I/O buffers; the resident path (Context.store_* plus the
@@ -50,7 +53,17 @@ STATUS_NAMES = {
     13: "InvalidArgument",
     14: "NonFiniteInput",
     15: "Unsupported",
+    16: "TruncatedQuantBlock",
+    17: "InvalidQuantBlockMagic",
+    18: "UnsupportedQuantBlockVersion",
+    19: "InvalidQuantBlock",
+    20: "TensorIndexOutOfRange",
+    21: "Unaligned",
+    22: "Io",
 }
+
+# codes whose wh_last_error() text says what failed
+_DETAILED = {2, 11, 12, 13, 16, 17, 18, 19, 20, 21, 22}
 
 SCALE_UE8M0 = 0
 SCALE_F32 = 1
@@ -69,6 +82,8 @@ EXPORTED = (
     "wh_debug_moe_batch_read", "wh_fp8_gemv_multi_async", "wh_set_exact_numerics", "wh_debug_moe_token_capture",
     "wh_debug_moe_token_read", "wh_fp8_shared_expert", "wh_fp8_shared_expert_async",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
+    "wh_quant_block_header", "wh_quant_block_tensor", "wh_quant_block_fp4_expert", "wh_store_expert_block",
+    "wh_store_expert_pack",
 )
 
 
@@ -76,10 +91,12 @@ class DeepSeekV4KernelError(RuntimeError):
     """Mirror of the reference's error enum (E/deepseek_v4.rs:398-408) plus
     the store/runtime codes of the C ABI."""
 
-    def __init__(self, code: int, where: str = ""):
+    def __init__(self, code: int, where: str = "", detail: str = ""):
         self.code = int(code)
         self.name = STATUS_NAMES.get(self.code, f"status {code}")
-        super().__init__(f"{self.name}" + (f" ({where})" if where else ""))
+        self.detail = detail
+        text = self.name + (f" ({where})" if where else "") + (f": {detail}" if detail else "")
+        super().__init__(text)
 
 
 class WhGemvDesc(ctypes.Structure):
@@ -90,6 +107,24 @@ class WhGemvDesc(ctypes.Structure):
 class WhExpertRoute(ctypes.Structure):
     _fields_ = [("layer_id", ctypes.c_uint32), ("expert_id", ctypes.c_uint32),
                 ("route_weight", ctypes.c_float)]
+
+
+class WhQuantTensor(ctypes.Structure):
+    _fields_ = [("dtype_original", ctypes.c_uint16), ("quant_format", ctypes.c_uint16), ("rank", ctypes.c_uint32),
+                ("flags", ctypes.c_uint32), ("scale", ctypes.c_float), ("zero_point", ctypes.c_float),
+                ("name_offset", ctypes.c_size_t), ("name_len", ctypes.c_size_t), ("shape_offset", ctypes.c_size_t),
+                ("data_offset", ctypes.c_size_t), ("data_bytes", ctypes.c_size_t)]
+
+
+class WhFp4View(ctypes.Structure):
+    _fields_ = [("rows", ctypes.c_size_t), ("cols", ctypes.c_size_t), ("scale_cols", ctypes.c_size_t),
+                ("weight_offset", ctypes.c_size_t), ("weight_bytes", ctypes.c_size_t),
+                ("scale_offset", ctypes.c_size_t), ("scale_bytes", ctypes.c_size_t)]
+
+
+class WhExpertPackEntry(ctypes.Structure):
+    _fields_ = [("layer_id", ctypes.c_uint32), ("expert_id", ctypes.c_uint32), ("offset", ctypes.c_uint64),
+                ("disk_bytes", ctypes.c_uint64), ("payload_bytes", ctypes.c_uint64)]
 
 
 _lib: Optional[ctypes.CDLL] = None
@@ -161,6 +196,12 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_fp8_shared_expert_async": (c.c_int, [vp, c.c_uint64, c.c_uint64, c.c_uint64, vp, vp]),
         "wh_debug_moe_token_capture": (c.c_int, [vp, c.c_int]),
         "wh_debug_moe_token_read": (c.c_int, [vp, c.c_int, vp, sz]),
+        "wh_quant_block_header": (c.c_int, [u8p, sz, c.POINTER(c.c_uint32), c.POINTER(c.c_uint32),
+                                            c.POINTER(c.c_uint32)]),
+        "wh_quant_block_tensor": (c.c_int, [u8p, sz, sz, c.POINTER(WhQuantTensor)]),
+        "wh_quant_block_fp4_expert": (c.c_int, [u8p, sz, c.POINTER(WhFp4View)]),
+        "wh_store_expert_block": (c.c_int, [vp, c.c_uint32, c.c_uint32, u8p, sz]),
+        "wh_store_expert_pack": (c.c_int, [vp, c.c_char_p, c.POINTER(WhExpertPackEntry), sz, c.POINTER(sz)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -185,9 +226,10 @@ def _p(a: np.ndarray, ct):
 
 def _check(code: int, where: str = ""):
     if code != 0:
-        if code in (11, 12) and _lib is not None:
-            where = f"{where}: {_lib.wh_last_error().decode(errors='replace')}"
-        raise DeepSeekV4KernelError(code, where)
+        detail = ""
+        if code in _DETAILED and _lib is not None:
+            detail = _lib.wh_last_error().decode(errors="replace")
+        raise DeepSeekV4KernelError(code, where, detail)
 
 
 class Context:
@@ -254,6 +296,27 @@ class Context:
                                seed: int, scale_lo: int = 119, scale_hi: int = 127):
         _check(self.lib.wh_store_expert_synthetic(self._h, layer_id, expert_id, hidden, inter, seed,
                                                   scale_lo, scale_hi), "store_expert_synthetic")
+
+    def store_expert_block(self, layer_id: int, expert_id: int, block) -> None:
+        """Makes the FP4 expert of a ZCBLK01 block (bytes-like) resident under
+        (layer_id, expert_id); a malformed block raises the reference's error."""
+        b = _block_array(block)
+        _check(self.lib.wh_store_expert_block(self._h, layer_id, expert_id, _p(b, ctypes.c_uint8), b.size),
+               "store_expert_block")
+
+    def store_expert_pack(self, pack, keys=None) -> int:
+        """Loads experts of a consolidated pack (model_format.ExpertPackInfo)
+        into the store, all of them or the (layer_id, expert_id) keys given,
+        in file order.  Returns the number stored."""
+        if keys is None:
+            keys = list(pack.entries)
+        chosen = sorted(((k, pack.entries[k]) for k in keys), key=lambda kv: kv[1].offset)
+        arr = (WhExpertPackEntry * max(1, len(chosen)))(
+            *[WhExpertPackEntry(k[0], k[1], e.offset, e.disk_bytes, e.payload_bytes) for k, e in chosen])
+        stored = ctypes.c_size_t()
+        _check(self.lib.wh_store_expert_pack(self._h, os.fsencode(str(pack.file)), arr, len(chosen),
+                                             ctypes.byref(stored)), "store_expert_pack")
+        return stored.value
 
     def release(self, t: int):
         _check(self.lib.wh_store_release(self._h, t), "release")
@@ -508,6 +571,68 @@ class DeepSeekV4Fp4Expert:
     w1: Fp4Matvec
     w3: Fp4Matvec
     w2: Fp4Matvec
+
+
+def _block_array(block) -> np.ndarray:
+    if isinstance(block, np.ndarray):
+        return np.ascontiguousarray(block, dtype=np.uint8).reshape(-1)
+    return np.frombuffer(bytes(block), dtype=np.uint8)
+
+
+@dataclass
+class QuantTensor:
+    """QuantTensorLayout (E/compute.rs:441-451) with its name, shape and data
+    read out of the block."""
+    dtype_original: int
+    quant_format: int
+    rank: int
+    flags: int
+    name: bytes
+    shape: tuple
+    data: np.ndarray
+    scale: float
+    zero_point: float
+
+    @property
+    def role(self) -> int:
+        """TensorRole code (E/compute.rs:455-471)."""
+        return self.flags & 0xFFFF
+
+
+def quant_block_header(block):
+    """parse_quant_block (E/compute.rs:1099-1148): (tensor_count,
+    quant_format, flags).  Host only."""
+    lib = load_library()
+    b = _block_array(block)
+    n, q, f = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint32()
+    _check(lib.wh_quant_block_header(_p(b, ctypes.c_uint8), b.size, ctypes.byref(n), ctypes.byref(q),
+                                     ctypes.byref(f)), "parse_quant_block")
+    return n.value, q.value, f.value
+
+
+def quant_block_tensor(block, index: int) -> QuantTensor:
+    """QuantBlockLayout::tensor (E/compute.rs:545-600).  Host only."""
+    lib = load_library()
+    b = _block_array(block)
+    t = WhQuantTensor()
+    _check(lib.wh_quant_block_tensor(_p(b, ctypes.c_uint8), b.size, index, ctypes.byref(t)), "quant_block_tensor")
+    dims = b[t.shape_offset + 4:t.shape_offset + 4 + 8 * t.rank].view("<u8") if t.rank else np.zeros(0, np.uint64)
+    return QuantTensor(t.dtype_original, t.quant_format, t.rank, t.flags,
+                       b[t.name_offset:t.name_offset + t.name_len].tobytes(), tuple(int(d) for d in dims),
+                       b[t.data_offset:t.data_offset + t.data_bytes], t.scale, t.zero_point)
+
+
+def deepseek_v4_fp4_expert_from_quant_block(block) -> DeepSeekV4Fp4Expert:
+    """E/compute.rs:1249-1268: the w1/w3/w2 FP4 projections of an expert
+    block, as views of the block's bytes.  Host only."""
+    lib = load_library()
+    b = _block_array(block)
+    views = (WhFp4View * 3)()
+    _check(lib.wh_quant_block_fp4_expert(_p(b, ctypes.c_uint8), b.size, views),
+           "deepseek_v4_fp4_expert_from_quant_block")
+    ms = [Fp4Matvec(b[v.weight_offset:v.weight_offset + v.weight_bytes],
+                    b[v.scale_offset:v.scale_offset + v.scale_bytes], v.rows, v.cols, v.scale_cols) for v in views]
+    return DeepSeekV4Fp4Expert(*ms)
 
 
 _default_ctx: Optional[Context] = None

@@ -1,8 +1,11 @@
 // Host side of the MI355X decode hot path: context, HBM weight store,
 // resident layouts, and the C ABI declared in include/wohper_hip.h.
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <unistd.h>
 
 #include <algorithm>
+#include <cerrno>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -18,6 +21,7 @@
 #include "kernels.h"
 #include "moe_batch.h"
 #include "moe_token.h"
+#include "quant_block.h"
 #include "wohper_hip.h"
 
 namespace {
@@ -37,6 +41,7 @@ struct Tensor {
 
 struct Expert {
     wh_tensor w1 = 0, w3 = 0, w2 = 0;
+    bool owned = false;  // tensors created by a block store, released on replacement
 };
 
 // Bump allocator over large hipMalloc chunks: tensors of a weight store are
@@ -146,7 +151,9 @@ struct wh_ctx {
     uint32_t* status = nullptr;  // device status word
     uint32_t* status_host = nullptr;
     Scratch x_in, y_out, h, ybuf, cnt_y, tmp, batch, routes, bout, gu, xq;
+    Scratch relayout;  // raw FP4 rows on their way into the resident layout
     HostBuf stage_in, stage_out;
+    HostBuf pack[2];   // experts-pack read buffers (one filling while the other uploads)
     std::map<uint32_t, LayerTable> tables;  // device expert tables of the batch path
     uint32_t moe_mfma_min = 16;             // batch experts with this many tokens use MFMA (0: never)
     bool exact = true;                      // routed experts in the reference's summation order
@@ -233,32 +240,6 @@ void fp8_permute_row(const uint8_t* src, uint8_t* dst, size_t cols) {
         for (int l = 0; l < 8; ++l)
             for (int i = 0; i < 16; ++i) d[l * 16 + i] = s[(i & 7) * 16 + (i >> 3) * 8 + l];
     }
-}
-
-// FP4 resident encoding of one row (layout described with the FP4 kernels
-// in kernels.h): per 256-column block, lane l's 16 bytes hold its values of
-// the block's 8 groups, two groups per dword.  Scales keep their order.
-void fp4_encode_row(const uint8_t* src, const uint8_t* ssrc, uint8_t* dst, uint8_t* sdst, size_t cols) {
-    auto nib = [src](size_t col) -> uint32_t {
-        uint8_t b = src[col >> 1];
-        return (col & 1) ? (b >> 4) : (b & 15);
-    };
-    const size_t blocks = cols / 256;
-    for (size_t blk = 0; blk < blocks; ++blk) {
-        for (uint32_t l = 0; l < 8; ++l) {
-            for (uint32_t d = 0; d < 4; ++d) {
-                const size_t g = 8 * blk + 2 * d;
-                uint32_t a[4], b[4];
-                for (uint32_t k = 0; k < 4; ++k) {
-                    a[k] = nib(32 * g + l + 8 * k);
-                    b[k] = nib(32 * (g + 1) + l + 8 * k);
-                }
-                uint32_t word = wh_fp4_encode_word(a, b);
-                std::memcpy(dst + blk * 128 + l * 16 + 4 * d, &word, 4);
-            }
-        }
-    }
-    std::memcpy(sdst, ssrc, cols / 32);
 }
 
 // Dynamic LDS a workgroup may use: the device's per-block limit (160 KB on
@@ -605,6 +586,39 @@ __host__ __device__ inline uint8_t wh_synth_byte(uint64_t seed, uint64_t stream,
     return (uint8_t)(v >> (8 * (i & 7)));
 }
 
+// Resident dword (blk, l, d) of one FP4 row (layout described with the FP4
+// kernels in kernels.h) from the row's original nibbles, nib(col).
+template <class Nib>
+__host__ __device__ inline uint32_t wh_fp4_resident_word(const Nib& nib, uint32_t blk, uint32_t l, uint32_t d) {
+    const size_t g = (size_t)8 * blk + 2 * d;
+    uint32_t a[4], b[4];
+    for (uint32_t k = 0; k < 4; ++k) {
+        a[k] = nib(32 * g + l + 8 * k);
+        b[k] = nib(32 * (g + 1) + l + 8 * k);
+    }
+    return wh_fp4_encode_word(a, b);
+}
+
+// Raw FP4 rows (the reference's [row][cols/2] bytes, low nibble = even
+// column) -> the resident layout: one thread per resident dword.  cols is a
+// multiple of 256; raw and w both hold `rows` rows of cols/2 bytes.
+__global__ void k_fp4_relayout(const uint8_t* __restrict__ raw, uint8_t* __restrict__ w, uint32_t rows,
+                               uint32_t cols) {
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t blocks = cols / 256;
+    if (id >= (size_t)rows * blocks * 32) return;
+    const uint32_t d = id & 3, l = (id >> 2) & 7;
+    const size_t rb = id >> 5;
+    const uint32_t blk = rb % blocks;
+    const size_t rowbase = (rb / blocks) * (cols / 2);
+    const uint8_t* src = raw + rowbase;
+    auto nib = [src](size_t col) -> uint32_t {
+        const uint8_t b = src[col >> 1];
+        return (col & 1) ? (b >> 4) : (b & 15);
+    };
+    ((uint32_t*)(w + rowbase + (size_t)blk * 128 + l * 16))[d] = wh_fp4_resident_word(nib, blk, l, d);
+}
+
 // Device synthetic FP4 tensor straight into the resident layout: each
 // thread builds one weight dword (or one scale byte) from the generated
 // original bytes.
@@ -623,13 +637,7 @@ __global__ void k_synth_fp4(uint8_t* w, uint8_t* s, uint32_t rows, uint32_t cols
             uint8_t b = wh_synth_byte(seed, stream, rowbase + (col >> 1));
             return (col & 1) ? (b >> 4) : (b & 15);
         };
-        const size_t g = (size_t)8 * blk + 2 * d;
-        uint32_t a[4], b[4];
-        for (uint32_t k = 0; k < 4; ++k) {
-            a[k] = nib(32 * g + l + 8 * k);
-            b[k] = nib(32 * (g + 1) + l + 8 * k);
-        }
-        ((uint32_t*)(w + rowbase + (size_t)blk * 128 + l * 16))[d] = wh_fp4_encode_word(a, b);
+        ((uint32_t*)(w + rowbase + (size_t)blk * 128 + l * 16))[d] = wh_fp4_resident_word(nib, blk, l, d);
     }
     const size_t nscale = (size_t)rows * G;
     if (id < nscale) {
@@ -936,6 +944,136 @@ int store_tensor_common(wh_ctx* c, Tensor&& t, wh_tensor* out) {
     return WH_OK;
 }
 
+// Host -> device copy on the context stream.  A pinned source is queued; a
+// pageable one goes through the pinned staging buffer in 64 MB pieces and
+// has landed when the call returns.
+int h2d(wh_ctx* c, void* dst, const uint8_t* src, size_t n, bool pinned) {
+    if (n == 0) return WH_OK;
+    if (pinned) {
+        WH_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream));
+        return WH_OK;
+    }
+    const size_t piece = size_t(64) << 20;
+    WH_HIP(c->stage_in.ensure(std::min(n, piece)));
+    for (size_t o = 0; o < n; o += piece) {
+        const size_t k = std::min(piece, n - o);
+        std::memcpy(c->stage_in.p, src + o, k);
+        WH_HIP(hipMemcpyAsync((uint8_t*)dst + o, c->stage_in.p, k, hipMemcpyHostToDevice, c->stream));
+        WH_HIP(hipStreamSynchronize(c->stream));
+    }
+    return WH_OK;
+}
+
+// One FP4 tensor from host bytes in the reference layout into a new
+// resident tensor.  Shapes the fast kernels take (32 columns per scale,
+// cols % 256 == 0) go up raw through the `relayout` scratch and
+// k_fp4_relayout writes the lane layout; other shapes keep the row-major
+// bytes.  With a pinned source the copies stay queued on the stream (the
+// caller keeps the source alive until the stream passes them); otherwise the
+// tensor is complete on return.  Shape rules are validate_fp4_matvec's
+// (E/deepseek_v4.rs:434-462) minus the per-call input/output lengths.
+int store_fp4_upload(wh_ctx* c, const uint8_t* packed, size_t packed_len, const uint8_t* scales, size_t scales_len,
+                     size_t rows, size_t cols, size_t scale_cols, bool pinned, wh_tensor* out) {
+    if (rows == 0 || cols == 0 || scale_cols == 0) return WH_EMPTY_SHAPE;
+    if (cols % scale_cols != 0) return WH_INVALID_SHAPE;
+    const size_t row_bytes = (cols + 1) / 2;
+    if (rows > SIZE_MAX / row_bytes || rows > SIZE_MAX / scale_cols) return WH_INVALID_SHAPE;
+    if (packed_len < rows * row_bytes) return WH_PACKED_WEIGHT_TOO_SMALL;
+    if (scales_len < rows * scale_cols) return WH_SCALE_TOO_SMALL;
+    Tensor t;
+    t.kind = kFp4;
+    t.rows = rows;
+    t.cols = cols;
+    t.scale_rows = rows;
+    t.scale_cols = scale_cols;
+    t.fast = (cols / scale_cols == 32) && cols % 256 == 0 && wh_fp4_wg_lds(cols) <= g_max_lds &&
+             rows <= UINT32_MAX && cols <= UINT32_MAX;
+    t.bytes = rows * row_bytes + rows * scale_cols;
+    void* wd = nullptr;
+    void* sd = nullptr;
+    WH_TRY(alloc_device(c, rows * row_bytes, &wd));
+    WH_TRY(alloc_device(c, rows * scale_cols, &sd));
+    t.w = (uint8_t*)wd;
+    t.s = sd;
+    if (t.fast) {
+        const size_t piece = size_t(64) << 20;
+        const size_t chunk_rows = std::max<size_t>(1, piece / row_bytes);
+        const size_t need = std::max(piece, row_bytes);
+        if (need > c->relayout.n) WH_HIP(hipStreamSynchronize(c->stream));  // queued relayouts may read it
+        WH_HIP(c->relayout.ensure(need, false));
+        for (size_t r = 0; r < rows; r += chunk_rows) {
+            const size_t nr = std::min(chunk_rows, rows - r);
+            // stream order keeps this copy behind the previous piece's relayout
+            WH_TRY(h2d(c, c->relayout.p, packed + r * row_bytes, nr * row_bytes, pinned));
+            const size_t words = nr * (cols / 256) * 32;
+            k_fp4_relayout<<<(unsigned)((words + 255) / 256), 256, 0, c->stream>>>(
+                c->relayout.as<uint8_t>(), t.w + r * row_bytes, (uint32_t)nr, (uint32_t)cols);
+            WH_HIP(hipGetLastError());
+        }
+    } else {
+        WH_TRY(h2d(c, t.w, packed, rows * row_bytes, pinned));
+    }
+    WH_TRY(h2d(c, t.s, scales, rows * scale_cols, pinned));
+    if (!pinned) WH_HIP(hipStreamSynchronize(c->stream));
+    return store_tensor_common(c, std::move(t), out);
+}
+
+// Thread's error text: the reference's Display string of a block error,
+// prefixed with `where` when given.
+void set_block_error(const whqb::Error& e, const char* where) {
+    char text[200];
+    whqb::describe(e, text, sizeof text);
+    if (where && *where)
+        std::snprintf(g_last_error, sizeof g_last_error, "%s: %s", where, text);
+    else
+        std::snprintf(g_last_error, sizeof g_last_error, "%s", text);
+}
+
+int block_status(const whqb::Error& e) {
+    switch (e.kind) {
+        case whqb::Fail::None: return WH_OK;
+        case whqb::Fail::Truncated: return WH_TRUNCATED_QUANT_BLOCK;
+        case whqb::Fail::Magic: return WH_INVALID_QUANT_BLOCK_MAGIC;
+        case whqb::Fail::Version: return WH_UNSUPPORTED_QUANT_BLOCK_VERSION;
+        case whqb::Fail::Invalid: return WH_INVALID_QUANT_BLOCK;
+        case whqb::Fail::Shape: return WH_INVALID_SHAPE;
+    }
+    return WH_INVALID_QUANT_BLOCK;
+}
+
+// Keys an expert whose tensors the library created; the tensors of an
+// expert it replaces go with it if the library created those too.
+void register_owned_expert(wh_ctx* c, uint32_t layer, uint32_t expert, const wh_tensor ids[3]) {
+    auto it = c->experts.find({layer, expert});
+    if (it != c->experts.end() && it->second.owned)
+        for (wh_tensor old : {it->second.w1, it->second.w3, it->second.w2}) c->tensors.erase(old);
+    c->experts[{layer, expert}] = Expert{ids[0], ids[1], ids[2], true};
+    c->tables[layer].valid = false;
+}
+
+// Parses a ZCBLK01 expert block and makes its three FP4 projections
+// resident under (layer, expert).  The caller holds c->mu.
+int store_block_locked(wh_ctx* c, uint32_t layer, uint32_t expert, const uint8_t* block, size_t len, bool pinned,
+                       const char* where) {
+    whqb::Fp4 p[3];
+    whqb::Error err;
+    if (!whqb::fp4_expert(block, len, p, &err)) {
+        set_block_error(err, where);
+        return block_status(err);
+    }
+    wh_tensor ids[3] = {0, 0, 0};
+    for (int m = 0; m < 3; ++m) {
+        int st = store_fp4_upload(c, block + p[m].weight_off, p[m].weight_len, block + p[m].scale_off,
+                                  p[m].scale_len, p[m].rows, p[m].cols, p[m].scale_cols, pinned, &ids[m]);
+        if (st != WH_OK) {
+            for (int k = 0; k < m; ++k) c->tensors.erase(ids[k]);
+            return st;
+        }
+    }
+    register_owned_expert(c, layer, expert, ids);
+    return WH_OK;
+}
+
 }  // namespace
 
 // ===================================================================== ABI
@@ -959,6 +1097,13 @@ const char* wh_status_string(int s) {
         case WH_INVALID_ARGUMENT: return "InvalidArgument";
         case WH_NON_FINITE_INPUT: return "NonFiniteInput";
         case WH_UNSUPPORTED: return "Unsupported";
+        case WH_TRUNCATED_QUANT_BLOCK: return "TruncatedQuantBlock";
+        case WH_INVALID_QUANT_BLOCK_MAGIC: return "InvalidQuantBlockMagic";
+        case WH_UNSUPPORTED_QUANT_BLOCK_VERSION: return "UnsupportedQuantBlockVersion";
+        case WH_INVALID_QUANT_BLOCK: return "InvalidQuantBlock";
+        case WH_TENSOR_INDEX_OUT_OF_RANGE: return "TensorIndexOutOfRange";
+        case WH_UNALIGNED: return "Unaligned";
+        case WH_IO_ERROR: return "Io";
         default: return "unknown";
     }
 }
@@ -1001,11 +1146,12 @@ int wh_shutdown(wh_ctx* c) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     c->arena.release_all();
-    for (Scratch* s : {&c->x_in, &c->y_out, &c->h, &c->ybuf, &c->cnt_y, &c->tmp, &c->batch, &c->routes, &c->bout})
+    for (Scratch* s : {&c->x_in, &c->y_out, &c->h, &c->ybuf, &c->cnt_y, &c->tmp, &c->batch, &c->routes, &c->bout,
+                       &c->gu, &c->xq, &c->relayout})
         if (s->p) (void)hipFree(s->p);
     for (auto& kv : c->tables)
         if (kv.second.dev) (void)hipFree(kv.second.dev);
-    for (HostBuf* h : {&c->stage_in, &c->stage_out})
+    for (HostBuf* h : {&c->stage_in, &c->stage_out, &c->pack[0], &c->pack[1]})
         if (h->p) (void)hipHostFree(h->p);
     for (hipEvent_t e : c->timer)
         if (e) (void)hipEventDestroy(e);
@@ -1075,48 +1221,9 @@ int wh_store_fp8(wh_ctx* c, const uint8_t* weight, size_t weight_len, size_t row
 int wh_store_fp4(wh_ctx* c, const uint8_t* packed, size_t packed_len, const uint8_t* scales,
                  size_t scales_len, size_t rows, size_t cols, size_t scale_cols, wh_tensor* out) {
     if (!c || !out || !packed || !scales) return WH_INVALID_ARGUMENT;
-    // validate_fp4_matvec, E/deepseek_v4.rs:434-462 (input/output lengths are
-    // checked per call)
-    if (rows == 0 || cols == 0 || scale_cols == 0) return WH_EMPTY_SHAPE;
-    if (cols % scale_cols != 0) return WH_INVALID_SHAPE;
-    const size_t row_bytes = (cols + 1) / 2;
-    if (packed_len < rows * row_bytes) return WH_PACKED_WEIGHT_TOO_SMALL;
-    if (scales_len < rows * scale_cols) return WH_SCALE_TOO_SMALL;
     std::lock_guard<std::mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
-    Tensor t;
-    t.kind = kFp4;
-    t.rows = rows;
-    t.cols = cols;
-    t.scale_rows = rows;
-    t.scale_cols = scale_cols;
-    t.fast = (cols / scale_cols == 32) && cols % 256 == 0 && wh_fp4_wg_lds(cols) <= g_max_lds;
-    t.bytes = rows * row_bytes + rows * scale_cols;
-    void* wd = nullptr;
-    void* sd = nullptr;
-    WH_TRY(alloc_device(c, rows * row_bytes, &wd));
-    WH_TRY(alloc_device(c, rows * scale_cols, &sd));
-    t.w = (uint8_t*)wd;
-    t.s = sd;
-    const size_t chunk_rows = std::max<size_t>(1, (size_t(64) << 20) / row_bytes);
-    const size_t nr0 = std::min(rows, chunk_rows);
-    WH_HIP(c->stage_in.ensure(nr0 * (row_bytes + scale_cols)));
-    for (size_t r = 0; r < rows; r += chunk_rows) {
-        size_t nr = std::min(chunk_rows, rows - r);
-        uint8_t* st = (uint8_t*)c->stage_in.p;
-        uint8_t* ss = st + nr0 * row_bytes;
-        if (t.fast) {
-            for (size_t i = 0; i < nr; ++i)
-                fp4_encode_row(packed + (r + i) * row_bytes, scales + (r + i) * scale_cols, st + i * row_bytes,
-                               ss + i * scale_cols, cols);
-        } else {
-            std::memcpy(st, packed + r * row_bytes, nr * row_bytes);
-            std::memcpy(ss, scales + r * scale_cols, nr * scale_cols);
-        }
-        WH_TRY(upload(c, t.w + r * row_bytes, st, nr * row_bytes));
-        WH_TRY(upload(c, (uint8_t*)t.s + r * scale_cols, ss, nr * scale_cols));
-    }
-    return store_tensor_common(c, std::move(t), out);
+    return store_fp4_upload(c, packed, packed_len, scales, scales_len, rows, cols, scale_cols, false, out);
 }
 
 int wh_store_expert(wh_ctx* c, uint32_t layer, uint32_t expert, wh_tensor w1, wh_tensor w3,
@@ -1128,6 +1235,10 @@ int wh_store_expert(wh_ctx* c, uint32_t layer, uint32_t expert, wh_tensor w1, wh
     if (t1->kind != kFp4 || t3->kind != kFp4 || t2->kind != kFp4) return WH_INVALID_QUANT_FORMAT;
     // E/compute.rs:1263-1265
     if (t1->cols != t3->cols || t1->rows != t3->rows || t2->cols != t1->rows) return WH_INVALID_SHAPE;
+    auto it = c->experts.find({layer, expert});
+    if (it != c->experts.end() && it->second.owned)
+        for (wh_tensor old : {it->second.w1, it->second.w3, it->second.w2})
+            if (old != w1 && old != w3 && old != w2) c->tensors.erase(old);
     c->experts[{layer, expert}] = Expert{w1, w3, w2};
     c->tables[layer].valid = false;
     return WH_OK;
@@ -1173,8 +1284,145 @@ int wh_store_expert_synthetic(wh_ctx* c, uint32_t layer, uint32_t expert, size_t
         WH_TRY(store_tensor_common(c, std::move(t), &ids[m]));
     }
     WH_HIP(hipStreamSynchronize(c->stream));
-    c->experts[{layer, expert}] = Expert{ids[0], ids[1], ids[2]};
-    c->tables[layer].valid = false;
+    register_owned_expert(c, layer, expert, ids);
+    return WH_OK;
+}
+
+int wh_quant_block_header(const uint8_t* block, size_t block_len, uint32_t* tensor_count, uint32_t* quant_format,
+                          uint32_t* flags) {
+    if (!block && block_len) return WH_INVALID_ARGUMENT;
+    whqb::Reader r(block, block_len);
+    whqb::Header h;
+    whqb::Error err;
+    if (!whqb::parse_header(r, &h, &err)) {
+        set_block_error(err, nullptr);
+        return block_status(err);
+    }
+    if (tensor_count) *tensor_count = h.tensor_count;
+    if (quant_format) *quant_format = h.quant_format;
+    if (flags) *flags = h.flags;
+    return WH_OK;
+}
+
+int wh_quant_block_tensor(const uint8_t* block, size_t block_len, size_t index, wh_quant_tensor* out) {
+    if ((!block && block_len) || !out) return WH_INVALID_ARGUMENT;
+    whqb::Reader r(block, block_len);
+    whqb::Header h;
+    whqb::Error err;
+    whqb::Tensor t;
+    if (!whqb::parse_header(r, &h, &err) || (index < h.tensor_count && !whqb::tensor_at(r, h, index, &t, &err))) {
+        set_block_error(err, nullptr);
+        return block_status(err);
+    }
+    if (index >= h.tensor_count) {
+        // TensorIndexOutOfRange, E/compute.rs:546-550
+        std::snprintf(g_last_error, sizeof g_last_error, "tensor index out of range: index=%zu, count=%u", index,
+                      h.tensor_count);
+        return WH_TENSOR_INDEX_OUT_OF_RANGE;
+    }
+    *out = wh_quant_tensor{};
+    out->dtype_original = t.dtype_original;
+    out->quant_format = t.quant_format;
+    out->rank = t.rank;
+    out->flags = t.flags;
+    out->scale = t.scale;
+    out->zero_point = t.zero_point;
+    out->name_offset = t.name_off;
+    out->name_len = t.name_len;
+    out->shape_offset = t.shape_off;
+    out->data_offset = t.data_off;
+    out->data_bytes = t.data_len;
+    return WH_OK;
+}
+
+int wh_quant_block_fp4_expert(const uint8_t* block, size_t block_len, wh_fp4_view out[3]) {
+    if ((!block && block_len) || !out) return WH_INVALID_ARGUMENT;
+    whqb::Fp4 p[3];
+    whqb::Error err;
+    if (!whqb::fp4_expert(block, block_len, p, &err)) {
+        set_block_error(err, nullptr);
+        return block_status(err);
+    }
+    for (int m = 0; m < 3; ++m)
+        out[m] = wh_fp4_view{p[m].rows,       p[m].cols,      p[m].scale_cols, p[m].weight_off,
+                             p[m].weight_len, p[m].scale_off, p[m].scale_len};
+    return WH_OK;
+}
+
+int wh_store_expert_block(wh_ctx* c, uint32_t layer, uint32_t expert, const uint8_t* block, size_t block_len) {
+    if (!c || (!block && block_len)) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    return store_block_locked(c, layer, expert, block, block_len, false, nullptr);
+}
+
+int wh_store_expert_pack(wh_ctx* c, const char* pack_path, const wh_expert_pack_entry* entries, size_t n,
+                         size_t* stored) {
+    if (stored) *stored = 0;
+    if (!c || !pack_path || (!entries && n)) return WH_INVALID_ARGUMENT;
+    // the index checks of load_optional_expert_pack (E/model_format.rs:488-491)
+    constexpr uint64_t kAlign = uint64_t(2) << 20;
+    for (size_t i = 0; i < n; ++i) {
+        const wh_expert_pack_entry& e = entries[i];
+        const char* field = e.offset % kAlign ? "expert_pack.offset" : e.disk_bytes % kAlign ? "expert_pack.disk_bytes" : nullptr;
+        if (field) {
+            std::snprintf(g_last_error, sizeof g_last_error, "unaligned field %s: value=%llu, required=%llu", field,
+                          (unsigned long long)(e.offset % kAlign ? e.offset : e.disk_bytes),
+                          (unsigned long long)kAlign);
+            return WH_UNALIGNED;
+        }
+        // the reader hands compute the first payload_bytes of the disk_bytes it read
+        if (e.payload_bytes > e.disk_bytes) {
+            std::snprintf(g_last_error, sizeof g_last_error,
+                          "layer %u expert %u: payload_bytes %llu exceeds disk_bytes %llu", e.layer_id, e.expert_id,
+                          (unsigned long long)e.payload_bytes, (unsigned long long)e.disk_bytes);
+            return WH_INVALID_ARGUMENT;
+        }
+    }
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    const int fd = open(pack_path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) {
+        std::snprintf(g_last_error, sizeof g_last_error, "experts pack file %s: %s", pack_path, std::strerror(errno));
+        return WH_IO_ERROR;
+    }
+    struct Guard {
+        int fd;
+        hipStream_t stream;
+        hipEvent_t ev[2] = {nullptr, nullptr};
+        ~Guard() {
+            (void)hipStreamSynchronize(stream);  // no copy from the read buffers outlives the call
+            for (hipEvent_t e : ev)
+                if (e) (void)hipEventDestroy(e);
+            close(fd);
+        }
+    } g{fd, c->stream};
+    for (hipEvent_t& e : g.ev) WH_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    for (size_t i = 0; i < n; ++i) {
+        const wh_expert_pack_entry& e = entries[i];
+        HostBuf& buf = c->pack[i & 1];
+        // the uploads queued from this buffer two experts ago must have left it
+        if (i >= 2) WH_HIP(hipEventSynchronize(g.ev[i & 1]));
+        WH_HIP(buf.ensure(std::max<size_t>((size_t)e.payload_bytes, 1)));
+        uint8_t* p = (uint8_t*)buf.p;
+        for (size_t got = 0; got < e.payload_bytes;) {
+            const ssize_t k = pread(fd, p + got, (size_t)e.payload_bytes - got, (off_t)(e.offset + got));
+            if (k < 0 && errno == EINTR) continue;
+            if (k <= 0) {
+                std::snprintf(g_last_error, sizeof g_last_error, "experts pack read (layer %u expert %u at %llu): %s",
+                              e.layer_id, e.expert_id, (unsigned long long)e.offset,
+                              k < 0 ? std::strerror(errno) : "unexpected end of file");
+                return WH_IO_ERROR;
+            }
+            got += (size_t)k;
+        }
+        char where[64];
+        std::snprintf(where, sizeof where, "layer %u expert %u", e.layer_id, e.expert_id);
+        WH_TRY(store_block_locked(c, e.layer_id, e.expert_id, p, (size_t)e.payload_bytes, true, where));
+        WH_HIP(hipEventRecord(g.ev[i & 1], c->stream));
+        if (stored) ++*stored;
+    }
+    WH_HIP(hipStreamSynchronize(c->stream));
     return WH_OK;
 }
 
