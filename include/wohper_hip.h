@@ -186,6 +186,54 @@ typedef struct {
 int wh_store_expert_pack(wh_ctx* ctx, const char* pack_path, const wh_expert_pack_entry* entries, size_t n,
                          size_t* stored);
 
+/* ---------------------------------------------------------------- router
+ * route_experts_from_dense_block (E/compute.rs:2129-2268) on the GPU: the
+ * gate GEMV (bf16 in the x86 lane order of dot_bf16_row_avx2,
+ * E/compute.rs:6116-6136, or the FP8 GEMV), sqrt-softplus, the biased top-k
+ * or the hash layer's tid2eid row, and finalize_route_weights - bit-exact,
+ * so the routed experts can follow without a host round trip. */
+
+/* RouterMath (E/compute.rs:408-417) */
+enum wh_router_math {
+    WH_ROUTER_RAW_LOGITS = 0,     /* raw gate outputs, no bias, no normalisation */
+    WH_ROUTER_SQRT_SOFTPLUS = 1   /* DeepSeekV4SqrtSoftplus */
+};
+
+/* RouteOptions (E/compute.rs:2096-2127). hash_token_id < 0: none. */
+typedef struct {
+    int32_t math;
+    float route_scale;
+    int64_t hash_token_id;
+} wh_route_options;
+
+/* Makes the router of a layer's dense ZCBLK01 block resident: the gate
+ * (router_gate_tensor, E/compute.rs:2444-2467: the Router-role matrix whose
+ * cols equal hidden_len, else the first; bf16 or FP8 with its UE8M0 scale),
+ * the selection bias (router_bias_values, E/compute.rs:2335-2376) and the
+ * tid2eid table (router_tid2eid_tensor, E/compute.rs:2270-2285).  *found = 0
+ * when the block has no gate (the reference's Ok(None)); a router already
+ * stored for the layer is replaced.  Up to 1024 experts. */
+int wh_store_router(wh_ctx* ctx, uint32_t layer_id, const uint8_t* block, size_t block_len, size_t hidden_len,
+                    int* found);
+
+/* route_experts_from_dense_block on host slices: hidden [hidden_len] in,
+ * the selected experts' ids and weights out (*n_out <= active_experts).
+ * available = NULL means every gate row, in id order; ids past the gate's
+ * rows have no score and are dropped.  active_experts <= 64,
+ * n_available <= 1024.  WH_NOT_RESIDENT when the layer has no router. */
+int wh_route_experts(wh_ctx* ctx, uint32_t layer_id, const float* hidden, size_t hidden_len, size_t active_experts,
+                     const uint32_t* available, size_t n_available, const wh_route_options* options,
+                     uint32_t* expert_ids, float* scores, size_t out_cap, size_t* n_out);
+
+/* The same on device pointers, ordered on the context stream: x_dev
+ * [hidden_len] f32, available_dev (or NULL), outputs ids_dev / scores_dev
+ * [active_experts] and count_dev.  Argument and table errors are returned
+ * here, before anything is queued. */
+int wh_route_experts_async(wh_ctx* ctx, uint32_t layer_id, const float* x_dev, size_t hidden_len,
+                           size_t active_experts, const uint32_t* available_dev, size_t n_available,
+                           const wh_route_options* options, uint32_t* ids_dev, float* scores_dev,
+                           uint32_t* count_dev);
+
 /* Device-side synthetic fill of an FP4 expert with the counter-based RNG of
  * the benchmark (uniform packed bytes, UE8M0 bytes in [scale_lo, scale_hi]),
  * written directly in the resident layout - for stacks too large to stage
@@ -399,7 +447,9 @@ int wh_profile_routed(wh_ctx* ctx, const wh_expert_route* routes, size_t n_route
  * emulation on n values.  fn 0: silu(x) = x / (1 + expf(-x)) for x <= 10;
  * fn 1: expf(x) for x >= -10; fn 2: the act-quant block scale
  * exp2f(ceilf(log2f(max(x, 1e-4) / 448))) for finite x >= 0; fn 3: a plain
- * device copy out = in (n a multiple of 4) that calibrates HBM byte counters. */
+ * device copy out = in (n a multiple of 4) that calibrates HBM byte counters;
+ * fn 4: the router's sqrt_softplus(x); fn 5: log1pf(x) for x >= 0; fn 6:
+ * expf(x) for any x. */
 int wh_debug_eval(wh_ctx* ctx, int fn, const float* in, float* out, size_t n);
 
 #ifdef __cplusplus

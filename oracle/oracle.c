@@ -658,3 +658,135 @@ void or_expf_array(const float* x, float* y, size_t n) {
 void or_act_quant_scale_array(const float* amax, float* out, size_t n) {
     for (size_t i = 0; i < n; ++i) out[i] = or_act_quant_scale(amax[i]);
 }
+
+/* ------------------------------------------------------------------ router */
+
+enum { OR_ROUTER_RAW_LOGITS = 0, OR_ROUTER_SQRT_SOFTPLUS = 1 };
+
+static inline float bf16_value(uint16_t raw) {
+    union { uint32_t u; float f; } v;
+    v.u = (uint32_t)raw << 16;
+    return v.f;
+}
+
+/* dot_bf16_row on x86 = dot_bf16_row_avx2 (E/compute.rs:2910-2919,
+ * 6116-6136): two 8-lane fused accumulators over 16-column chunks, hsum256
+ * of their sum, then an unfused sequential tail. */
+float or_bf16_dot_row_avx2(const uint16_t* row, const float* x, size_t cols) {
+    __m256 acc0 = _mm256_setzero_ps(), acc1 = _mm256_setzero_ps();
+    const size_t chunks = cols / 16;
+    for (size_t c = 0; c < chunks; ++c) {
+        const __m128i r0 = _mm_loadu_si128((const __m128i*)(row + 16 * c));
+        const __m128i r1 = _mm_loadu_si128((const __m128i*)(row + 16 * c + 8));
+        const __m256 w0 = _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(r0), 16));
+        const __m256 w1 = _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(r1), 16));
+        acc0 = _mm256_fmadd_ps(w0, _mm256_loadu_ps(x + 16 * c), acc0);
+        acc1 = _mm256_fmadd_ps(w1, _mm256_loadu_ps(x + 16 * c + 8), acc1);
+    }
+    float tail = 0.0f;
+    for (size_t i = chunks * 16; i < cols; ++i) tail += bf16_value(row[i]) * x[i];
+    return hsum256(_mm256_add_ps(acc0, acc1)) + tail;
+}
+
+/* gemv_bf16_tensorwise (E/compute.rs:6139-6172): one dot per row. */
+void or_bf16_gemv(const uint16_t* w, size_t rows, size_t cols, const float* x, float* y) {
+    for (size_t r = 0; r < rows; ++r) y[r] = or_bf16_dot_row_avx2(w + r * cols, x, cols);
+}
+
+/* sqrt_softplus, E/compute.rs:2239-2249 (Rust f32::exp / ln_1p are libm
+ * expf / log1pf; max(NaN, 0) is 0; sqrt is the IEEE square root). */
+float or_sqrt_softplus(float v) {
+    float sp;
+    if (v > 20.0f) sp = v;
+    else if (v < -20.0f) sp = expf(v);
+    else sp = log1pf(expf(v));
+    return sqrtf(fmaxf(sp, 0.0f));
+}
+
+void or_sqrt_softplus_array(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = or_sqrt_softplus(x[i]);
+}
+
+void or_log1pf_array(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = log1pf(x[i]);
+}
+
+/* f32::total_cmp as a signed integer key. */
+static inline int32_t total_key(float f) {
+    union { uint32_t u; float f; } v;
+    v.f = f;
+    int32_t k = (int32_t)v.u;
+    return k ^ (int32_t)(((uint32_t)(k >> 31)) >> 1);
+}
+
+/* finalize_route_weights, E/compute.rs:2254-2268. */
+static void finalize_routes(float* scores, size_t n, int math, float route_scale) {
+    if (math != OR_ROUTER_SQRT_SOFTPLUS || n == 0) return;
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; ++i) sum += scores[i];
+    if (sum > 0.0f && isfinite(sum)) {
+        for (size_t i = 0; i < n; ++i) scores[i] = scores[i] / sum * route_scale;
+    } else {
+        const float uniform = route_scale / (float)n;
+        for (size_t i = 0; i < n; ++i) scores[i] = uniform;
+    }
+}
+
+/* route_experts_from_dense_block after its gate GEMV (E/compute.rs:2129-2237):
+ * `logits` are the gate rows' outputs.  sqrt-softplus for the DeepSeek math;
+ * with `hash_ids` (the token's tid2eid row) the experts are those ids that
+ * are available, in table order; otherwise the available experts sorted
+ * (stable) by score + bias, descending in total_cmp order.  Truncated to
+ * `active`, then finalized.  Available ids at or past `rows` have no score
+ * and are dropped. */
+int or_route_select(const float* logits, size_t rows, const float* bias, const uint32_t* available, size_t n_avail,
+                    size_t active, int math, float route_scale, const uint32_t* hash_ids, size_t n_hash,
+                    uint32_t* out_ids, float* out_scores, size_t* n_out) {
+    *n_out = 0;
+    if (active == 0 || n_avail == 0) return OR_OK;
+    float* scores = (float*)malloc((rows ? rows : 1) * sizeof(float));
+    for (size_t i = 0; i < rows; ++i)
+        scores[i] = math == OR_ROUTER_SQRT_SOFTPLUS ? or_sqrt_softplus(logits[i]) : logits[i];
+    size_t n = 0;
+    if (hash_ids) {
+        for (size_t h = 0; h < n_hash && n < active; ++h) {
+            const uint32_t id = hash_ids[h];
+            int avail = 0;
+            for (size_t a = 0; a < n_avail; ++a) avail |= available[a] == id;
+            if (!avail || id >= rows) continue;
+            out_ids[n] = id;
+            out_scores[n] = scores[id];
+            ++n;
+        }
+    } else {
+        /* stable insertion sort of (key, id, score) by key, descending */
+        int32_t* keys = (int32_t*)malloc(n_avail * sizeof(int32_t));
+        uint32_t* ids = (uint32_t*)malloc(n_avail * sizeof(uint32_t));
+        size_t m = 0;
+        for (size_t a = 0; a < n_avail; ++a) {
+            const uint32_t id = available[a];
+            if (id >= rows) continue;
+            const float sel = (math == OR_ROUTER_SQRT_SOFTPLUS && bias) ? scores[id] + bias[id] : scores[id];
+            const int32_t k = total_key(sel);
+            size_t j = m;
+            while (j > 0 && keys[j - 1] < k) {
+                keys[j] = keys[j - 1];
+                ids[j] = ids[j - 1];
+                --j;
+            }
+            keys[j] = k;
+            ids[j] = id;
+            ++m;
+        }
+        for (n = 0; n < m && n < active; ++n) {
+            out_ids[n] = ids[n];
+            out_scores[n] = scores[ids[n]];
+        }
+        free(keys);
+        free(ids);
+    }
+    free(scores);
+    finalize_routes(out_scores, n, math, route_scale);
+    *n_out = n;
+    return OR_OK;
+}

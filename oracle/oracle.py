@@ -68,6 +68,14 @@ def lib():
             "or_expf_array": (None, [f32p, f32p, sz]),
             "or_act_quant_scale_array": (None, [f32p, f32p, sz]),
             "or_fp8_shared_expert": (c.c_int, [u8p, f32p, u8p, f32p, u8p, f32p, sz, sz, sz, sz, sz, sz, f32p, f32p]),
+            "or_bf16_dot_row_avx2": (c.c_float, [c.POINTER(c.c_uint16), f32p, sz]),
+            "or_bf16_gemv": (None, [c.POINTER(c.c_uint16), sz, sz, f32p, f32p]),
+            "or_sqrt_softplus": (c.c_float, [c.c_float]),
+            "or_sqrt_softplus_array": (None, [f32p, f32p, sz]),
+            "or_log1pf_array": (None, [f32p, f32p, sz]),
+            "or_route_select": (c.c_int, [f32p, sz, f32p, c.POINTER(c.c_uint32), sz, sz, c.c_int, c.c_float,
+                                          c.POINTER(c.c_uint32), sz, c.POINTER(c.c_uint32), f32p,
+                                          c.POINTER(sz)]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -294,3 +302,53 @@ def act_quant_scale_array(amax):
     y = np.empty_like(a)
     lib().or_act_quant_scale_array(_pf(a), _pf(y), a.size)
     return y
+
+
+# ------------------------------------------------------------------ router
+ROUTER_RAW_LOGITS = 0
+ROUTER_SQRT_SOFTPLUS = 1
+
+
+def bf16_gemv(w_bits, x):
+    """gemv_bf16_tensorwise (E/compute.rs:6139-6172) on bf16 bit patterns
+    [rows, cols] (uint16)."""
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    rows, cols = w.shape
+    x = _f(x)
+    y = np.zeros(rows, np.float32)
+    lib().or_bf16_gemv(w.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), rows, cols, _pf(x), _pf(y))
+    return y
+
+
+def sqrt_softplus(x):
+    x = _f(np.atleast_1d(x))
+    y = np.empty_like(x)
+    lib().or_sqrt_softplus_array(_pf(x), _pf(y), x.size)
+    return y
+
+
+def log1pf(x):
+    x = _f(np.atleast_1d(x))
+    y = np.empty_like(x)
+    lib().or_log1pf_array(_pf(x), _pf(y), x.size)
+    return y
+
+
+def route_select(logits, active, available=None, bias=None, math=ROUTER_SQRT_SOFTPLUS, route_scale=1.5,
+                 hash_ids=None):
+    """route_experts_from_dense_block after the gate GEMV (E/compute.rs:2129-2268):
+    returns (expert ids, weights)."""
+    lg = _f(logits)
+    rows = lg.size
+    av = np.ascontiguousarray(np.arange(rows) if available is None else available, dtype=np.uint32)
+    b = None if bias is None else _f(bias)
+    h = None if hash_ids is None else np.ascontiguousarray(hash_ids, dtype=np.uint32)
+    cap = max(1, int(active))
+    ids = np.zeros(cap, np.uint32)
+    sc = np.zeros(cap, np.float32)
+    n = ctypes.c_size_t()
+    u32p = ctypes.POINTER(ctypes.c_uint32)
+    lib().or_route_select(_pf(lg), rows, None if b is None else _pf(b), av.ctypes.data_as(u32p), av.size, active,
+                          math, route_scale, None if h is None else h.ctypes.data_as(u32p),
+                          0 if h is None else h.size, ids.ctypes.data_as(u32p), _pf(sc), ctypes.byref(n))
+    return ids[:n.value].copy(), sc[:n.value].copy()

@@ -17,6 +17,7 @@ include/wohper_hip.h (libwohper_hip.so, built from wohper_amd/csrc):
   parse_quant_block                compute.rs:1099             quant_block_header / quant_block_tensor
   deepseek_v4_fp4_expert_from_quant_block compute.rs:1249      deepseek_v4_fp4_expert_from_quant_block
   load_optional_expert_pack        model_format.rs:458         model_format.load_optional_expert_pack
+  route_experts_from_dense_block   compute.rs:2129             Context.store_router + Context.route_experts
 
 The slice-based functions upload the weights for the call, as the reference
 reads them from its I/O buffers; the resident path (Context.store_* plus the
@@ -83,8 +84,11 @@ EXPORTED = (
     "wh_debug_moe_token_read", "wh_fp8_shared_expert", "wh_fp8_shared_expert_async",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
     "wh_quant_block_header", "wh_quant_block_tensor", "wh_quant_block_fp4_expert", "wh_store_expert_block",
-    "wh_store_expert_pack",
+    "wh_store_expert_pack", "wh_store_router", "wh_route_experts", "wh_route_experts_async",
 )
+
+ROUTER_RAW_LOGITS = 0
+ROUTER_SQRT_SOFTPLUS = 1
 
 
 class DeepSeekV4KernelError(RuntimeError):
@@ -120,6 +124,10 @@ class WhFp4View(ctypes.Structure):
     _fields_ = [("rows", ctypes.c_size_t), ("cols", ctypes.c_size_t), ("scale_cols", ctypes.c_size_t),
                 ("weight_offset", ctypes.c_size_t), ("weight_bytes", ctypes.c_size_t),
                 ("scale_offset", ctypes.c_size_t), ("scale_bytes", ctypes.c_size_t)]
+
+
+class WhRouteOptions(ctypes.Structure):
+    _fields_ = [("math", ctypes.c_int32), ("route_scale", ctypes.c_float), ("hash_token_id", ctypes.c_int64)]
 
 
 class WhExpertPackEntry(ctypes.Structure):
@@ -202,6 +210,11 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_quant_block_fp4_expert": (c.c_int, [u8p, sz, c.POINTER(WhFp4View)]),
         "wh_store_expert_block": (c.c_int, [vp, c.c_uint32, c.c_uint32, u8p, sz]),
         "wh_store_expert_pack": (c.c_int, [vp, c.c_char_p, c.POINTER(WhExpertPackEntry), sz, c.POINTER(sz)]),
+        "wh_store_router": (c.c_int, [vp, c.c_uint32, u8p, sz, sz, c.POINTER(c.c_int)]),
+        "wh_route_experts": (c.c_int, [vp, c.c_uint32, f32p, sz, sz, c.POINTER(c.c_uint32), sz,
+                                       c.POINTER(WhRouteOptions), c.POINTER(c.c_uint32), f32p, sz, c.POINTER(sz)]),
+        "wh_route_experts_async": (c.c_int, [vp, c.c_uint32, vp, sz, sz, vp, sz, c.POINTER(WhRouteOptions), vp, vp,
+                                             vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -317,6 +330,46 @@ class Context:
         _check(self.lib.wh_store_expert_pack(self._h, os.fsencode(str(pack.file)), arr, len(chosen),
                                              ctypes.byref(stored)), "store_expert_pack")
         return stored.value
+
+    # ------------------------------------------------------------ router
+    def store_router(self, layer_id: int, dense_block, hidden_len: int) -> bool:
+        """Makes a layer's router (gate, bias, tid2eid) resident from its
+        dense ZCBLK01 block; False when the block has no gate."""
+        b = _block_array(dense_block)
+        found = ctypes.c_int()
+        _check(self.lib.wh_store_router(self._h, layer_id, _p(b, ctypes.c_uint8), b.size, hidden_len,
+                                        ctypes.byref(found)), "store_router")
+        return bool(found.value)
+
+    @staticmethod
+    def route_options(math: int = ROUTER_SQRT_SOFTPLUS, route_scale: float = 1.0, hash_token_id=None):
+        return WhRouteOptions(math, route_scale, -1 if hash_token_id is None else int(hash_token_id))
+
+    def route_experts(self, layer_id: int, hidden, active: int, available=None, math: int = ROUTER_SQRT_SOFTPLUS,
+                      route_scale: float = 1.0, hash_token_id=None):
+        """route_experts_from_dense_block (E/compute.rs:2129-2237) for a
+        resident router: returns (expert ids, weights)."""
+        h = _f32(hidden)
+        av = None if available is None else np.ascontiguousarray(available, dtype=np.uint32)
+        cap = max(1, int(active))
+        ids = np.zeros(cap, np.uint32)
+        sc = np.zeros(cap, np.float32)
+        n = ctypes.c_size_t()
+        opt = self.route_options(math, route_scale, hash_token_id)
+        _check(self.lib.wh_route_experts(self._h, layer_id, _p(h, ctypes.c_float), h.size, active,
+                                         None if av is None else _p(av, ctypes.c_uint32), 0 if av is None else av.size,
+                                         ctypes.byref(opt), _p(ids, ctypes.c_uint32), _p(sc, ctypes.c_float), cap,
+                                         ctypes.byref(n)), "route_experts")
+        return ids[:n.value].copy(), sc[:n.value].copy()
+
+    def route_experts_async(self, layer_id: int, x_ptr: int, hidden_len: int, active: int, avail_ptr: int,
+                            n_available: int, ids_ptr: int, scores_ptr: int, count_ptr: int,
+                            math: int = ROUTER_SQRT_SOFTPLUS, route_scale: float = 1.0, hash_token_id=None):
+        opt = self.route_options(math, route_scale, hash_token_id)
+        _check(self.lib.wh_route_experts_async(self._h, layer_id, ctypes.c_void_p(x_ptr), hidden_len, active,
+                                               ctypes.c_void_p(avail_ptr) if avail_ptr else None, n_available,
+                                               ctypes.byref(opt), ctypes.c_void_p(ids_ptr), ctypes.c_void_p(scores_ptr),
+                                               ctypes.c_void_p(count_ptr)), "route_experts_async")
 
     def release(self, t: int):
         _check(self.lib.wh_store_release(self._h, t), "release")

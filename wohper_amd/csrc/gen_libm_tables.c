@@ -1,7 +1,9 @@
 // Build-time generator for the glibc-exact libm tables used by the device
 // code (see libm_emul.h).  It runs the exact same emulation code on the host
 // and compares it with the host glibc over every float input of each domain:
-//   expf : every float in [-10, +inf)   (silu's argument after min(g, 10))
+//   expf : every non-NaN float (silu's argument after min(g, 10) lies in
+//          [-10, +inf); the router's sqrt-softplus takes any value <= 20)
+//   log1pf: every non-negative float     (log1p(expf(v)) of the router)
 //   log2f: every normal float            (ceil(log2f(r)) for r = amax / 448)
 //   exp2f: every integral k in [-126, 127]
 // and aborts if any input disagrees, so a written table is a verified one.
@@ -46,6 +48,8 @@ static void* exp_scan(void* p) {
         double d = 0.0;
         if (y > 89.0f) {
             f = wh_bits_to_float(0x7f800000u);
+        } else if (y < -104.0f) {
+            f = 0.0f;
         } else {
             d = wh_exp_double(y, g_tab);
             f = (float)d;
@@ -57,7 +61,7 @@ static void* exp_scan(void* p) {
         uint32_t want;
         if ((fb & 0x7fffffffu) == 0x7f800000u) want = 0x7f7fffffu;
         else want = diff > 0.0 ? fb + 1 : fb - 1;
-        if (y > 89.0f || !wh_expf_near_midpoint(d, f) || want != wh_float_to_bits(g)) {
+        if (y > 89.0f || y < -104.0f || !wh_expf_near_midpoint(d, f) || want != wh_float_to_bits(g)) {
             if (j->bad < 5)
                 fprintf(stderr, "expf: unrepresentable mismatch y=%a glibc=%a emul=%a d=%a\n", y, g, f, d);
             j->bad++;
@@ -75,6 +79,23 @@ static void* exp_scan(void* p) {
 static int cmp_u32(const void* a, const void* b) {
     uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
     return (x > y) - (x < y);
+}
+
+typedef struct {
+    uint64_t lo, hi;
+    long bad;
+} log1p_job;
+
+static void* log1p_verify(void* p) {
+    log1p_job* j = (log1p_job*)p;
+    for (uint64_t b = j->lo; b < j->hi; ++b) {
+        float x = wh_bits_to_float((uint32_t)b);
+        if (wh_float_to_bits(wh_log1pf(x)) != wh_float_to_bits(log1pf(x))) {
+            if (j->bad < 5) fprintf(stderr, "log1pf: mismatch x=%a glibc=%a emul=%a\n", x, log1pf(x), wh_log1pf(x));
+            j->bad++;
+        }
+    }
+    return NULL;
 }
 
 typedef struct {
@@ -138,9 +159,8 @@ int main(int argc, char** argv) {
     enum { T = 8 };
     build_exp_constants();
 
-    // expf over [-10, -0] and [+0, +inf]
-    uint64_t ranges[2][2] = {{0x80000000ull, (uint64_t)wh_float_to_bits(-10.0f) + 1},
-                             {0x00000000ull, 0x7f800001ull}};
+    // expf over [-inf, -0] and [+0, +inf]
+    uint64_t ranges[2][2] = {{0x80000000ull, 0xff800001ull}, {0x00000000ull, 0x7f800001ull}};
     uint32_t* flips = NULL;
     size_t nflips = 0;
     long bad = 0;
@@ -225,6 +245,28 @@ int main(int argc, char** argv) {
     }
 
     if (check_e4m3_round()) return 1;
+
+    // log1pf over [+0, +inf]
+    {
+        log1p_job js[T];
+        pthread_t ts[T];
+        const uint64_t n = 0x7f800001ull;
+        for (int i = 0; i < T; ++i) {
+            js[i].lo = n * i / T;
+            js[i].hi = n * (i + 1) / T;
+            js[i].bad = 0;
+            pthread_create(&ts[i], NULL, log1p_verify, &js[i]);
+        }
+        for (int i = 0; i < T; ++i) {
+            pthread_join(ts[i], NULL);
+            bad += js[i].bad;
+        }
+        if (bad) {
+            fprintf(stderr, "log1pf: %ld mismatches\n", bad);
+            return 1;
+        }
+        fprintf(stderr, "log1pf: every non-negative float matches the host glibc\n");
+    }
 
     FILE* out = fopen(argv[1], "w");
     if (!out) {

@@ -108,11 +108,13 @@ WH_HD int wh_table_contains(const uint32_t* tab, uint32_t n, uint32_t key) {
     return 0;
 }
 
-// glibc-exact expf(y) for y in [-10, +inf) (the silu domain); y is never NaN
-// there.  `flip` lists (sorted) the inputs whose glibc result is the other
+// glibc-exact expf(y) for every non-NaN float y (the silu domain is
+// [-10, +inf); the router's sqrt-softplus also takes y < -10, where results
+// go subnormal and then zero).  `flip` lists (sorted) the inputs whose glibc result is the other
 // neighbour of the nearby rounding midpoint.
 WH_HD float wh_expf_glibc(float y, const uint64_t* exp2_tab, const uint32_t* flip, uint32_t nflip) {
     if (y > 89.0f) return wh_bits_to_float(0x7f800000u);
+    if (y < -104.0f) return 0.0f;  // below half the least subnormal
     double d = wh_exp_double(y, exp2_tab);
     float f = (float)d;
     if (wh_expf_near_midpoint(d, f) && wh_table_contains(flip, nflip, wh_float_to_bits(y))) {
@@ -142,6 +144,83 @@ WH_HD int wh_ceil_log2f(float r, const uint32_t* thr) {
     uint32_t m = b & 0x7fffff;
     if (m == 0) return e;
     return m > thr[e + 126] ? e + 1 : e;
+}
+
+// glibc-exact log1pf(x) for x >= 0 (Rust's f32::ln_1p): the float form of
+// the published fdlibm log1p method (Sun Microsystems; s_log1pf.c as carried
+// by FreeBSD msun and glibc's sysdeps/ieee754/flt-32), evaluated in float
+// with every operation rounded on its own (no contraction), which host and
+// device do alike.  With k and f such that 1+x = 2^k (1+f), sqrt(2)/2 <=
+// 1+f < sqrt(2), and c the rounding error of 1+x:
+//   log1p(x) = k ln2_hi + (f - (hfsq - (s (hfsq + R(s^2)) + (k ln2_lo + c))))
+// where hfsq = f^2/2, s = f/(2+f) and R is a degree-7 polynomial in s^2 for
+// log((1+s)/(1-s)) - 2s.  The generator compares it with the host glibc on
+// every non-negative float.
+WH_HD float wh_log1pf(float x) {
+    const float ln2_hi = wh_bits_to_float(0x3f317180u), ln2_lo = wh_bits_to_float(0x3717f7d1u);
+    const float lp1 = wh_bits_to_float(0x3f2aaaabu), lp2 = wh_bits_to_float(0x3ecccccdu),
+                lp3 = wh_bits_to_float(0x3e924925u), lp4 = wh_bits_to_float(0x3e638e29u),
+                lp5 = wh_bits_to_float(0x3e3a3325u), lp6 = wh_bits_to_float(0x3e1cd04fu),
+                lp7 = wh_bits_to_float(0x3e178897u);
+    const int32_t hx = (int32_t)wh_float_to_bits(x);
+    const int32_t ax = hx & 0x7fffffff;
+    int32_t k = 1, hu = 0;
+    float f = 0.0f, c = 0.0f;
+    if (hx < 0x3ed413d7) {                         // x < 0.41422
+        if (ax >= 0x3f800000) return wh_bits_to_float(0x7fc00000u);  // x <= -1: not on this path
+        if (ax < 0x31000000) {                     // |x| < 2^-29
+            if (ax < 0x24800000) return x;         // |x| < 2^-54
+            return x - x * x * 0.5f;
+        }
+        if (hx > 0 || hx <= (int32_t)0xbe95f61f) { // -0.2929 < x < 0.41422
+            k = 0;
+            f = x;
+            hu = 1;
+        }
+    } else if (hx >= 0x7f800000) {
+        return x + x;                              // +inf, NaN
+    }
+    if (k != 0) {
+        float u;
+        if (hx < 0x5a000000) {                     // 1+x is inexact below 2^53
+            u = 1.0f + x;
+            hu = (int32_t)wh_float_to_bits(u);
+            k = (hu >> 23) - 127;
+            c = k > 0 ? 1.0f - (u - x) : x - (u - 1.0f);
+            c /= u;
+        } else {
+            u = x;
+            hu = (int32_t)wh_float_to_bits(u);
+            k = (hu >> 23) - 127;
+            c = 0.0f;
+        }
+        hu &= 0x007fffff;
+        if (hu < 0x3504f7) {                       // mantissa below sqrt(2): u in [1, sqrt(2))
+            u = wh_bits_to_float((uint32_t)hu | 0x3f800000u);
+        } else {                                   // halve: u in [sqrt(2)/2, 1)
+            k += 1;
+            u = wh_bits_to_float((uint32_t)hu | 0x3f000000u);
+            hu = (0x00800000 - hu) >> 2;
+        }
+        f = u - 1.0f;
+    }
+    const float hfsq = 0.5f * f * f;
+    const float kf = (float)k;
+    if (hu == 0) {                                 // |f| < 2^-20
+        if (f == 0.0f) {
+            if (k == 0) return 0.0f;
+            c += kf * ln2_lo;
+            return kf * ln2_hi + c;
+        }
+        const float r = hfsq * (1.0f - 0.66666666666666666f * f);
+        if (k == 0) return f - r;
+        return kf * ln2_hi - ((r - (kf * ln2_lo + c)) - f);
+    }
+    const float s = f / (2.0f + f);
+    const float z = s * s;
+    const float r = z * (lp1 + z * (lp2 + z * (lp3 + z * (lp4 + z * (lp5 + z * (lp6 + z * lp7))))));
+    if (k == 0) return f - (hfsq - s * (hfsq + r));
+    return kf * ln2_hi - ((hfsq - (s * (hfsq + r) + (kf * ln2_lo + c))) - f);
 }
 
 // 2^k as float for -126 <= k <= 127 (exp2f of an integral float is exact there).

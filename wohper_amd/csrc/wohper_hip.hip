@@ -5,6 +5,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <cctype>
 #include <cerrno>
 #include <cmath>
 #include <cstdio>
@@ -22,6 +23,7 @@
 #include "moe_batch.h"
 #include "moe_token.h"
 #include "quant_block.h"
+#include "router.h"
 #include "wohper_hip.h"
 
 namespace {
@@ -43,6 +45,30 @@ struct Expert {
     wh_tensor w1 = 0, w3 = 0, w2 = 0;
     bool owned = false;  // tensors created by a block store, released on replacement
 };
+
+// Outcome of one of the reference's router tensor lookups, kept for the
+// route calls that would run it (the reference repeats the lookup per call).
+struct LookupError {
+    int status = WH_OK;
+    std::string text;  // wh_last_error text when status != WH_OK
+};
+
+// A layer's router: the tensors route_experts_from_dense_block reads
+// (E/compute.rs:2129-2237), resident.
+struct Router {
+    int gate = 0;                 // kGateBf16 (lane layout), kGateBf16Rows (row-major), kGateFp8
+    uint16_t* bf16 = nullptr;     // device bf16 gate
+    wh_tensor fp8 = 0;            // FP8 gate in the weight store
+    size_t rows = 0, cols = 0;
+    float* bias = nullptr;        // device f32 selection bias [rows], or null
+    LookupError bias_err;         // router_bias_values failed (raised in sqrt-softplus math)
+    bool has_table = false;       // a tid2eid table exists (hash layers)
+    LookupError table_err;        // router_tid2eid_tensor failed (raised when hashing)
+    int table_dtype = 0;          // dtype_original of the table
+    size_t table_rows = 0, table_cols = 0;
+    std::vector<uint8_t> table;   // its bytes, host side: one row is read per call
+};
+constexpr int kGateBf16 = 1, kGateBf16Rows = 2, kGateFp8 = 3;
 
 // Bump allocator over large hipMalloc chunks: tensors of a weight store are
 // never freed individually in the hot path, and a 150 GB stack would
@@ -152,6 +178,8 @@ struct wh_ctx {
     uint32_t* status_host = nullptr;
     Scratch x_in, y_out, h, ybuf, cnt_y, tmp, batch, routes, bout, gu, xq;
     Scratch relayout;  // raw FP4 rows on their way into the resident layout
+    Scratch rtr;       // router: logits, available ids, outputs of the host-slice call
+    std::map<uint32_t, Router> routers;
     HostBuf stage_in, stage_out;
     HostBuf pack[2];   // experts-pack read buffers (one filling while the other uploads)
     std::map<uint32_t, LayerTable> tables;  // device expert tables of the batch path
@@ -1051,6 +1079,165 @@ void register_owned_expert(wh_ctx* c, uint32_t layer, uint32_t expert, const wh_
     c->tables[layer].valid = false;
 }
 
+// ---------------------------------------------------------------- router
+
+// The reference's InvalidShape(what) / InvalidQuantBlock(what) as a status
+// and the Display text in the thread's error string.
+int shape_error(const char* what) {
+    std::snprintf(g_last_error, sizeof g_last_error, "invalid compute shape: %s", what);
+    return WH_INVALID_SHAPE;
+}
+
+bool name_contains_ci(const whqb::Reader& r, const whqb::Tensor& t, const char* needle) {
+    const size_t n = std::strlen(needle);
+    const uint8_t* p = r.data() + t.name_off;
+    for (size_t i = 0; i + n <= t.name_len; ++i) {
+        size_t k = 0;
+        while (k < n && std::tolower(p[i + k]) == needle[k]) ++k;
+        if (k == n) return true;
+    }
+    return false;
+}
+
+constexpr uint32_t kRoleRouter = 9;  // TensorRole::Router, E/compute.rs:455-471
+
+// bf16 row-major [rows][cols] -> the router kernel's lane layout (cols % 64
+// == 0): per 64-column block, lane l's values of chunks 0..3, acc0 then acc1.
+void bf16_router_layout(const uint16_t* src, uint16_t* dst, size_t rows, size_t cols) {
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t b = 0; b < cols / 64; ++b)
+            for (size_t l = 0; l < 8; ++l)
+                for (size_t j = 0; j < 4; ++j)
+                    for (size_t a = 0; a < 2; ++a)
+                        dst[r * cols + 64 * b + 8 * l + 2 * j + a] = src[r * cols + 64 * b + 16 * j + 8 * a + l];
+}
+
+// router_bias_values (E/compute.rs:2335-2376): the first Router-role rank-1
+// tensor named *bias* with at least `rows` values in f32 (dtype 12) or bf16
+// (dtype 11), as f32.
+int router_bias(const whqb::Reader& r, const whqb::Header& h, size_t rows, std::vector<float>* out, bool* found,
+                LookupError* err) {
+    *found = false;
+    for (size_t i = 0; i < h.tensor_count; ++i) {
+        whqb::Tensor t;
+        whqb::Error e;
+        if (!whqb::tensor_at(r, h, i, &t, &e)) {
+            set_block_error(e, nullptr);
+            err->status = block_status(e);
+            err->text = g_last_error;
+            return err->status;
+        }
+        if ((t.flags & 0xffff) != kRoleRouter || t.rank != 1 || !name_contains_ci(r, t, "bias")) continue;
+        if ((size_t)t.dim(r, 0) < rows) continue;
+        if (t.dtype_original != 12 && t.dtype_original != 11) continue;
+        const size_t elem = t.dtype_original == 12 ? 4 : 2;
+        if (t.data_len < rows * elem) {
+            err->status = shape_error(elem == 4 ? "router bias out of range" : "BF16 tensor value out of range");
+            err->text = g_last_error;
+            return err->status;
+        }
+        out->resize(rows);
+        const uint8_t* d = r.data() + t.data_off;
+        for (size_t k = 0; k < rows; ++k) {
+            if (elem == 4) {
+                std::memcpy(&(*out)[k], d + 4 * k, 4);
+            } else {
+                uint16_t v;
+                std::memcpy(&v, d + 2 * k, 2);
+                const uint32_t bits = (uint32_t)v << 16;
+                std::memcpy(&(*out)[k], &bits, 4);
+            }
+        }
+        *found = true;
+        return WH_OK;
+    }
+    return WH_OK;
+}
+
+// The token's tid2eid row (tid2eid_expert_ids, E/compute.rs:2287-2333).
+int router_hash_row(const Router& rt, uint64_t token, uint32_t* ids, uint32_t* n) {
+    size_t elem = 0;
+    if (rt.table_dtype == 7) elem = 4;
+    else if (rt.table_dtype == 9) elem = 8;
+    else return shape_error("tid2eid table has unsupported dtype");
+    if (token >= rt.table_rows) return shape_error("tid2eid token id out of range");
+    const size_t top_k = rt.table_cols;
+    const size_t row_bytes = top_k * elem, start = (size_t)token * row_bytes;
+    if (start + row_bytes > rt.table.size()) return shape_error("tid2eid row out of range");
+    if (top_k > WH_ROUTER_MAX_HASH) {
+        std::snprintf(g_last_error, sizeof g_last_error, "tid2eid rows of %zu ids exceed %u", top_k, WH_ROUTER_MAX_HASH);
+        return WH_UNSUPPORTED;
+    }
+    for (size_t k = 0; k < top_k; ++k) {
+        int64_t v;
+        if (elem == 4) {
+            int32_t v32;
+            std::memcpy(&v32, rt.table.data() + start + 4 * k, 4);
+            v = v32;
+        } else {
+            std::memcpy(&v, rt.table.data() + start + 8 * k, 8);
+        }
+        if (v < 0) return shape_error("tid2eid negative expert id");
+        ids[k] = (uint32_t)v;
+    }
+    *n = (uint32_t)top_k;
+    return WH_OK;
+}
+
+// Everything of route_experts_from_dense_block that runs on the host before
+// the kernels: the argument checks in the reference's order, the hash row,
+// the bias lookup's outcome.  Fills the selection arguments except the
+// pointers.
+int router_prepare(const Router& rt, const wh_route_options& o, size_t hidden_len, size_t active, size_t n_avail,
+                   wh_router_sel* sa) {
+    if (hidden_len < rt.cols) return shape_error("router input too small");
+    std::memset(sa, 0, sizeof *sa);
+    sa->rows = (uint32_t)rt.rows;
+    sa->active = (uint32_t)active;
+    sa->n_avail = (uint32_t)n_avail;
+    sa->math = o.math == WH_ROUTER_SQRT_SOFTPLUS ? 1u : 0u;
+    sa->route_scale = o.route_scale;
+    if (o.hash_token_id >= 0 && rt.has_table) {
+        if (rt.table_err.status != WH_OK) {
+            std::snprintf(g_last_error, sizeof g_last_error, "%s", rt.table_err.text.c_str());
+            return rt.table_err.status;
+        }
+        WH_TRY(router_hash_row(rt, (uint64_t)o.hash_token_id, sa->hash, &sa->n_hash));
+        if (sa->n_hash == 0) sa->active = 0;  // an empty row routes nowhere
+        return WH_OK;
+    }
+    if (sa->math && rt.bias_err.status != WH_OK) {
+        std::snprintf(g_last_error, sizeof g_last_error, "%s", rt.bias_err.text.c_str());
+        return rt.bias_err.status;
+    }
+    return WH_OK;
+}
+
+// Gate GEMV then selection, on the context stream.  x: device f32 [cols];
+// avail: device ids or null; logits: device scratch [rows].
+int router_launch(wh_ctx* c, const Router& rt, wh_router_sel sa, const float* x, const uint32_t* avail,
+                  float* logits, uint32_t* ids, float* scores, uint32_t* count) {
+    const unsigned rows = (unsigned)rt.rows, cols = (unsigned)rt.cols;
+    if (rt.gate == kGateBf16) {
+        k_router_gemv_bf16<<<(rows + 7) / 8, 64, cols * sizeof(float), c->stream>>>(rt.bf16, x, rows, cols, logits);
+    } else if (rt.gate == kGateBf16Rows) {
+        k_router_gemv_bf16_generic<<<(rows + 63) / 64, 64, 0, c->stream>>>(rt.bf16, x, rows, cols, logits);
+    } else {
+        Tensor* t = find_tensor(c, rt.fp8);
+        if (!t) return WH_NOT_RESIDENT;
+        WH_TRY(launch_fp8(c, *t, 0, t->rows, x, logits, 1, 0, 0));
+    }
+    sa.logits = logits;
+    sa.bias = sa.math ? rt.bias : nullptr;
+    sa.avail = avail;
+    sa.out_ids = ids;
+    sa.out_scores = scores;
+    sa.out_count = count;
+    k_router_select<<<1, 64, 0, c->stream>>>(sa);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
 // Parses a ZCBLK01 expert block and makes its three FP4 projections
 // resident under (layer, expert).  The caller holds c->mu.
 int store_block_locked(wh_ctx* c, uint32_t layer, uint32_t expert, const uint8_t* block, size_t len, bool pinned,
@@ -1147,7 +1334,7 @@ int wh_shutdown(wh_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     c->arena.release_all();
     for (Scratch* s : {&c->x_in, &c->y_out, &c->h, &c->ybuf, &c->cnt_y, &c->tmp, &c->batch, &c->routes, &c->bout,
-                       &c->gu, &c->xq, &c->relayout})
+                       &c->gu, &c->xq, &c->relayout, &c->rtr})
         if (s->p) (void)hipFree(s->p);
     for (auto& kv : c->tables)
         if (kv.second.dev) (void)hipFree(kv.second.dev);
@@ -1424,6 +1611,216 @@ int wh_store_expert_pack(wh_ctx* c, const char* pack_path, const wh_expert_pack_
     }
     WH_HIP(hipStreamSynchronize(c->stream));
     return WH_OK;
+}
+
+int wh_store_router(wh_ctx* c, uint32_t layer, const uint8_t* block, size_t block_len, size_t hidden_len,
+                    int* found) {
+    if (found) *found = 0;
+    if (!c || (!block && block_len)) return WH_INVALID_ARGUMENT;
+    whqb::Reader r(block, block_len);
+    whqb::Header h;
+    whqb::Error e;
+    auto fail = [&]() {
+        set_block_error(e, nullptr);
+        return block_status(e);
+    };
+    if (!whqb::parse_header(r, &h, &e)) return fail();
+    // router_gate_tensor (E/compute.rs:2444-2467): the Router-role matrix
+    // whose cols match the hidden size, else the first one; never tid2eid
+    whqb::Tensor gate;
+    bool have_gate = false, exact = false;
+    for (size_t i = 0; i < h.tensor_count && !exact; ++i) {
+        whqb::Tensor t;
+        if (!whqb::tensor_at(r, h, i, &t, &e)) return fail();
+        if ((t.flags & 0xffff) != kRoleRouter || t.rank != 2 || name_contains_ci(r, t, "tid2eid")) continue;
+        if ((size_t)t.dim(r, 1) == hidden_len) {
+            gate = t;
+            have_gate = exact = true;
+        } else if (!have_gate) {
+            gate = t;
+            have_gate = true;
+        }
+    }
+    if (!have_gate) {  // Ok(None): the engine falls back to its own routing
+        std::lock_guard<std::mutex> lk(c->mu);
+        c->routers.erase(layer);
+        return WH_OK;
+    }
+    Router rt;
+    rt.rows = (size_t)gate.dim(r, 0);
+    rt.cols = (size_t)gate.dim(r, 1);
+    if (rt.rows == 0 || rt.rows > WH_ROUTER_MAX_ROWS) {
+        std::snprintf(g_last_error, sizeof g_last_error, "router of %zu experts (1..%u supported)", rt.rows,
+                      WH_ROUTER_MAX_ROWS);
+        return WH_UNSUPPORTED;
+    }
+    const bool fp8 = gate.quant_format == 2401;
+    const bool bf16 = gate.quant_format == 2404 && gate.dtype_original == 11;
+    if (!fp8 && !bf16) {
+        std::snprintf(g_last_error, sizeof g_last_error, "router gate quant format %u (dtype %u) is not on the GPU path",
+                      gate.quant_format, gate.dtype_original);
+        return WH_UNSUPPORTED;
+    }
+    if (bf16 && gate.data_len / 2 / rt.cols < rt.rows) return shape_error("BF16 GEMV tensor data too small");
+    wh_tensor fp8_handle = 0;
+    if (fp8) {
+        // fp8_scale_for_weight (E/compute.rs:1184-1199), then the checks of
+        // gemv_fp8_e4m3_ue8m0_tensorwise (E/compute.rs:6174-6215)
+        static const char kW[] = ".weight";
+        if (gate.name_len < 7 || std::memcmp(r.data() + gate.name_off + gate.name_len - 7, kW, 7) != 0) {
+            whqb::Reader::fail(&e, whqb::Fail::Invalid, "DeepSeek FP8 weight name does not end with .weight");
+            return fail();
+        }
+        const size_t stem = gate.name_len - 7;
+        whqb::Tensor sc;
+        bool have_scale = false;
+        for (size_t i = 0; i < h.tensor_count && !have_scale; ++i) {
+            whqb::Tensor t;
+            if (!whqb::tensor_at(r, h, i, &t, &e)) return fail();
+            have_scale = t.name_len == stem + 6 &&
+                         std::memcmp(r.data() + t.name_off, r.data() + gate.name_off, stem) == 0 &&
+                         std::memcmp(r.data() + t.name_off + stem, ".scale", 6) == 0;
+            if (have_scale) sc = t;
+        }
+        if (!have_scale) {
+            whqb::Reader::fail(&e, whqb::Fail::Invalid, "missing DeepSeek FP8 scale tensor");
+            return fail();
+        }
+        if (sc.quant_format != whqb::kQuantUe8m0) {
+            whqb::Reader::fail(&e, whqb::Fail::Invalid, "DeepSeek FP8 scale is not UE8M0");
+            return fail();
+        }
+        if (sc.rank != 2) return shape_error("DeepSeek FP8 scale rank");
+        const size_t srows = (size_t)sc.dim(r, 0), scols = (size_t)sc.dim(r, 1);
+        if (srows == 0 || scols == 0 || rt.rows % srows || rt.cols % scols) return shape_error("DeepSeek FP8 scale shape");
+        if (gate.data_len / rt.cols < rt.rows) return shape_error("DeepSeek FP8 weight data too small");
+        if (sc.data_len < srows * scols) return shape_error("DeepSeek FP8 scale data too small");
+        WH_TRY(wh_store_fp8(c, r.data() + gate.data_off, gate.data_len, rt.rows, rt.cols, r.data() + sc.data_off,
+                            sc.data_len, WH_SCALE_UE8M0, srows, scols, &fp8_handle));
+    }
+    // the bias and tid2eid lookups run per route call in the reference;
+    // their outcome is the same every time, so it is kept
+    std::vector<float> bias;
+    bool have_bias = false;
+    router_bias(r, h, rt.rows, &bias, &have_bias, &rt.bias_err);
+    for (size_t i = 0; i < h.tensor_count; ++i) {  // router_tid2eid_tensor, E/compute.rs:2270-2285
+        whqb::Tensor t;
+        if (!whqb::tensor_at(r, h, i, &t, &e)) {
+            rt.has_table = true;
+            set_block_error(e, nullptr);
+            rt.table_err.status = block_status(e);
+            rt.table_err.text = g_last_error;
+            break;
+        }
+        if ((t.flags & 0xffff) != kRoleRouter || t.rank != 2 || !name_contains_ci(r, t, "tid2eid")) continue;
+        rt.has_table = true;
+        rt.table_dtype = t.dtype_original;
+        rt.table_rows = (size_t)t.dim(r, 0);
+        rt.table_cols = (size_t)t.dim(r, 1);
+        rt.table.assign(r.data() + t.data_off, r.data() + t.data_off + t.data_len);
+        break;
+    }
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    if (fp8) {
+        rt.gate = kGateFp8;
+        rt.fp8 = fp8_handle;
+    } else {
+        const size_t n = rt.rows * rt.cols;
+        void* d = nullptr;
+        WH_TRY(alloc_device(c, n * 2, &d));
+        rt.bf16 = (uint16_t*)d;
+        std::vector<uint16_t> tmp(n);  // the block's bytes need not be 2-byte aligned
+        std::memcpy(tmp.data(), r.data() + gate.data_off, n * 2);
+        if (rt.cols % 64 == 0 && rt.cols * sizeof(float) <= g_max_lds) {
+            std::vector<uint16_t> lane(n);
+            bf16_router_layout(tmp.data(), lane.data(), rt.rows, rt.cols);
+            tmp.swap(lane);
+            rt.gate = kGateBf16;
+        } else {
+            rt.gate = kGateBf16Rows;
+        }
+        WH_TRY(h2d(c, rt.bf16, reinterpret_cast<const uint8_t*>(tmp.data()), n * 2, false));
+    }
+    if (have_bias) {
+        void* d = nullptr;
+        WH_TRY(alloc_device(c, rt.rows * sizeof(float), &d));
+        rt.bias = (float*)d;
+        WH_TRY(h2d(c, rt.bias, reinterpret_cast<const uint8_t*>(bias.data()), rt.rows * sizeof(float), false));
+    }
+    auto old = c->routers.find(layer);
+    if (old != c->routers.end() && old->second.fp8) c->tensors.erase(old->second.fp8);
+    c->routers[layer] = std::move(rt);
+    if (found) *found = 1;
+    return WH_OK;
+}
+
+int wh_route_experts(wh_ctx* c, uint32_t layer, const float* hidden, size_t hidden_len, size_t active,
+                     const uint32_t* available, size_t n_available, const wh_route_options* opts, uint32_t* expert_ids,
+                     float* scores, size_t out_cap, size_t* n_out) {
+    if (n_out) *n_out = 0;
+    if (!c || !opts || !n_out || (!hidden && hidden_len)) return WH_INVALID_ARGUMENT;
+    if (active == 0 || (available && n_available == 0)) return WH_OK;  // E/compute.rs:2138-2140
+    if (!expert_ids || !scores) return WH_INVALID_ARGUMENT;
+    if (out_cap < active) return WH_OUTPUT_TOO_SMALL;
+    if (active > WH_ROUTER_MAX_ACTIVE || n_available > WH_ROUTER_MAX_ROWS) return WH_UNSUPPORTED;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    auto it = c->routers.find(layer);
+    if (it == c->routers.end()) return WH_NOT_RESIDENT;
+    const Router& rt = it->second;
+    wh_router_sel sa;
+    WH_TRY(router_prepare(rt, *opts, hidden_len, active, available ? n_available : rt.rows, &sa));
+    // scratch: x [cols], logits [rows], available ids, then the outputs
+    const size_t nav = available ? n_available : 0;
+    const size_t words = rt.cols + rt.rows + nav + 2 * WH_ROUTER_MAX_ACTIVE + 1;
+    WH_HIP(c->rtr.ensure(words * 4, false));
+    float* x = c->rtr.as<float>();
+    float* logits = x + rt.cols;
+    uint32_t* av = reinterpret_cast<uint32_t*>(logits + rt.rows);
+    uint32_t* ids = av + nav;
+    float* sc = reinterpret_cast<float*>(ids + WH_ROUTER_MAX_ACTIVE);
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(sc + WH_ROUTER_MAX_ACTIVE);
+    WH_TRY(h2d(c, x, reinterpret_cast<const uint8_t*>(hidden), rt.cols * sizeof(float), false));
+    if (nav) WH_TRY(h2d(c, av, reinterpret_cast<const uint8_t*>(available), nav * 4, false));
+    WH_TRY(router_launch(c, rt, sa, x, nav ? av : nullptr, logits, ids, sc, cnt));
+    const size_t back = (2 * WH_ROUTER_MAX_ACTIVE + 1) * 4;
+    WH_HIP(c->stage_out.ensure(back));
+    WH_HIP(hipMemcpyAsync(c->stage_out.p, ids, back, hipMemcpyDeviceToHost, c->stream));
+    WH_HIP(hipStreamSynchronize(c->stream));
+    const uint32_t* hb = (const uint32_t*)c->stage_out.p;
+    const uint32_t n = hb[2 * WH_ROUTER_MAX_ACTIVE];
+    std::memcpy(expert_ids, hb, n * 4);
+    std::memcpy(scores, hb + WH_ROUTER_MAX_ACTIVE, n * 4);
+    *n_out = n;
+    return read_status(c);
+}
+
+int wh_route_experts_async(wh_ctx* c, uint32_t layer, const float* x_dev, size_t hidden_len, size_t active,
+                           const uint32_t* available_dev, size_t n_available, const wh_route_options* opts,
+                           uint32_t* ids_dev, float* scores_dev, uint32_t* count_dev) {
+    if (!c || !opts || !x_dev || !ids_dev || !scores_dev || !count_dev) return WH_INVALID_ARGUMENT;
+    if (active > WH_ROUTER_MAX_ACTIVE || n_available > WH_ROUTER_MAX_ROWS) return WH_UNSUPPORTED;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    auto it = c->routers.find(layer);
+    if (it == c->routers.end()) return WH_NOT_RESIDENT;
+    const Router& rt = it->second;
+    wh_router_sel sa;
+    if (active == 0 || (available_dev && n_available == 0)) {
+        // no routes: the selection kernel only writes the zero count
+        std::memset(&sa, 0, sizeof sa);
+        sa.out_ids = ids_dev;
+        sa.out_scores = scores_dev;
+        sa.out_count = count_dev;
+        k_router_select<<<1, 64, 0, c->stream>>>(sa);
+        WH_HIP(hipGetLastError());
+        return WH_OK;
+    }
+    WH_TRY(router_prepare(rt, *opts, hidden_len, active, available_dev ? n_available : rt.rows, &sa));
+    WH_HIP(c->rtr.ensure((rt.cols + rt.rows + 2 * WH_ROUTER_MAX_ACTIVE + 1) * 4, false));
+    float* logits = c->rtr.as<float>() + rt.cols;
+    return router_launch(c, rt, sa, x_dev, available_dev, logits, ids_dev, scores_dev, count_dev);
 }
 
 void wh_synth_fp8_host(uint64_t seed, uint64_t stream, uint8_t* weight, size_t n) {
@@ -2097,7 +2494,7 @@ int wh_profile_routed(wh_ctx* c, const wh_expert_route* routes, size_t n_routes,
 }
 
 int wh_debug_eval(wh_ctx* c, int fn, const float* in, float* out, size_t n) {
-    if (!c || !in || !out || fn < 0 || fn > 3) return WH_INVALID_ARGUMENT;
+    if (!c || !in || !out || fn < 0 || fn > 6) return WH_INVALID_ARGUMENT;
     if (fn == 3 && n % 4) return WH_INVALID_ARGUMENT;
     if (n == 0) return WH_OK;
     std::lock_guard<std::mutex> lk(c->mu);
@@ -2108,6 +2505,9 @@ int wh_debug_eval(wh_ctx* c, int fn, const float* in, float* out, size_t n) {
     if (fn == 3)
         k_copy_f32x4<<<(unsigned)std::min<size_t>((n / 4 + 255) / 256, 8192), 256, 0, c->stream>>>(
             reinterpret_cast<const float4*>(c->x_in.p), reinterpret_cast<float4*>(c->y_out.p), (uint32_t)(n / 4));
+    else if (fn >= 4)
+        k_debug_eval_router<<<(unsigned)((n + 255) / 256), 256, 0, c->stream>>>(fn, c->x_in.as<float>(),
+                                                                               c->y_out.as<float>(), (uint32_t)n);
     else
         k_debug_eval<<<(unsigned)((n + 255) / 256), 256, 0, c->stream>>>(fn, c->x_in.as<float>(), c->y_out.as<float>(), (uint32_t)n);
     WH_HIP(hipGetLastError());
