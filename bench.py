@@ -145,6 +145,81 @@ def fp8_decode_layer(ctx, steps: int):
     return res
 
 
+def router(ctx, steps: int):
+    """The DeepSeek-V4 router of a layer (bf16 gate 256x4096, f32 bias,
+    sqrt-softplus, top-6, route_scale 1.5) on device pointers, over 8
+    rotating layers."""
+    from wohper_amd import model_format as mf
+
+    rows, cols, layers = 256, 4096, 8
+    rng = np.random.default_rng(31)
+    for k in range(layers):
+        gate = ((rng.standard_normal((rows, cols)).astype(np.float32) * 0.02).view(np.uint32) >> 16).astype(np.uint16)
+        bias = (rng.standard_normal(rows) * 0.05).astype(np.float32)
+        blk = mf.build_synthetic_quant_block([
+            mf.SyntheticTensor(f"layers.{k}.ffn.gate.weight", 9, (rows, cols), gate.tobytes(), 11, 2404),
+            mf.SyntheticTensor(f"layers.{k}.ffn.gate.bias", 9, (rows,), bias.tobytes(), 12, 2405)])
+        ctx.store_router(1000 + k, blk, cols)
+    xd, out = ctx.device_alloc(cols * 4), ctx.device_alloc(256)
+    ctx.to_device(xd, rng.standard_normal(cols).astype(np.float32))
+    call = lambda i: ctx.route_experts_async(1000 + i % layers, xd, cols, 6, 0, 0, out, out + 64, out + 128,
+                                             route_scale=1.5)
+    for i in range(20):
+        call(i)
+    ctx.synchronize()
+    ctx.timer_start()
+    for i in range(steps):
+        call(i)
+    us = ctx.timer_stop() / steps
+    ctx.synchronize()
+    ctx.device_free(xd)
+    ctx.device_free(out)
+    nbytes = rows * cols * 2 + rows * 4 + cols * 4
+    return {"workload": "router: bf16 gate 256x4096 + f32 bias, sqrt-softplus, top-6 (gate GEMV + selection launch)",
+            "bytes": nbytes, "us_per_route": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "note": "HIP events around back-to-back asynchronous calls; includes the host's per-call launch cost"}
+
+
+def expert_pack_load(ctx, n_experts: int = 24):
+    """Loads a consolidated experts pack (ZCBLK01 blocks at 2 MiB-aligned
+    offsets) into the store with wh_store_expert_pack; the file was just
+    written, so it is read from the page cache."""
+    import tempfile
+
+    from wohper_amd import model_format as mf
+    from wohper_amd import workloads as wl
+
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        pack = Path(d) / "m.experts_pack.bin"
+        entries, off, payload = [], 0, 0
+        with pack.open("wb") as f:
+            for e in range(n_experts):
+                mats = wl.synth_expert_host(ctx.lib, 41, 2000, e)
+                ts = []
+                for name, (p, s, r, c, sc), role in zip(("w1", "w3", "w2"), mats, (6, 7, 8)):
+                    ts.append(mf.SyntheticTensor(f"layers.2000.ffn.experts.{e}.{name}.weight", role, (r, c // 2),
+                                                 p.tobytes(), 12, 2402))
+                    ts.append(mf.SyntheticTensor(f"layers.2000.ffn.experts.{e}.{name}.scale", role, (r, sc),
+                                                 s.tobytes(), 1, 2403))
+                blk = mf.build_synthetic_quant_block(ts)
+                disk = (len(blk) + mf.ALIGN_2MB - 1) // mf.ALIGN_2MB * mf.ALIGN_2MB
+                f.seek(off)
+                f.write(blk)
+                entries.append({"layer_id": 2000, "expert_id": e, "offset": off, "disk_bytes": disk,
+                                "payload_bytes": len(blk)})
+                off += disk
+                payload += len(blk)
+            f.truncate(off)
+        (Path(d) / "m.experts_pack.index.json").write_text(json.dumps(
+            {"format": "wohper-experts-pack", "pack_file": pack.name, "entries": entries}))
+        info = mf.load_optional_expert_pack(Path(d) / "m.zcinf")
+        t0 = time.perf_counter()
+        stored = ctx.store_expert_pack(info)
+        el = time.perf_counter() - t0
+    return {"workload": f"experts pack load: {stored} FP4 experts (ZCBLK01 blocks, 13.4 MB each) from the page cache",
+            "payload_bytes": payload, "seconds": round(el, 4), "GBps": round(payload / el / 1e9, 2)}
+
+
 def ragged_batch(ctx, n_layers: int, steps: int, warmup: int):
     """Ragged batched MoE: 64 bf16 tokens, each top-6 of 256 FP4 experts under
     Zipf(1.1) popularity over a seeded permutation (seed 4), one launch
@@ -368,6 +443,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fp8", action="store_true")
+    ap.add_argument("--no-aux", action="store_true", help="skip the router and experts-pack load legs")
     ap.add_argument("--stack-layers", type=int, default=43, help="layers of the full-depth stack leg (0: skip)")
     ap.add_argument("--stack-steps", type=int, default=20)
     ap.add_argument("--batch-steps", type=int, default=20, help="steps of the ragged batch leg (0: skip)")
@@ -464,6 +540,11 @@ def main():
         log(f"fp8 dense: {extra['fp8_dense_gemv']}")
         extra["fp8_decode_layer"] = fp8_decode_layer(ctx, 200)
         log(f"fp8 decode layer: {extra['fp8_decode_layer']}")
+    if not args.no_aux:
+        extra["router"] = router(ctx, 400)
+        log(f"router: {extra['router']}")
+        extra["expert_pack_load"] = expert_pack_load(ctx)
+        log(f"expert pack load: {extra['expert_pack_load']}")
     if args.batch_steps > 0:
         extra["ragged_batch"] = ragged_batch(ctx, args.layers, args.batch_steps, 3)
         log(f"ragged batch: {extra['ragged_batch']}")

@@ -445,7 +445,7 @@ int wh_profile_routed(wh_ctx* ctx, const wh_expert_route* routes, size_t n_route
 
 /* Test support, no counterpart in the reference: evaluates the device libm
  * emulation on n values.  fn 0: silu(x) = x / (1 + expf(-x)) for x <= 10;
- * fn 1: expf(x) for x >= -10; fn 2: the act-quant block scale
+ * fn 1: expf(x); fn 2: the act-quant block scale
  * exp2f(ceilf(log2f(max(x, 1e-4) / 448))) for finite x >= 0; fn 3: a plain
  * device copy out = in (n a multiple of 4) that calibrates HBM byte counters;
  * fn 4: the router's sqrt_softplus(x); fn 5: log1pf(x) for x >= 0; fn 6:

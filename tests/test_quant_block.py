@@ -292,3 +292,16 @@ def test_expert_pack_index_errors(tmp_path):
     info = mf.load_optional_expert_pack(_index(tmp_path, entries=[e0, dict(e0, offset=2 << 20)]))
     assert info.entries[(0, 0)].offset == 2 << 20  # a later duplicate replaces the earlier one
     assert mf.load_optional_expert_pack(_index(tmp_path, entries=None)).entries == {}
+
+
+def test_package_block_builder_matches_the_test_writer():
+    """model_format.build_synthetic_quant_block (the product's builder) lays
+    out bytes exactly as the test writer does for the reference's layout."""
+    w1, w3, w2 = _small_expert(4, 64)
+    ts = [zcblk.tensor("e.w1.weight", w1[0].shape, w1[0], 2402, 6, 12),
+          zcblk.tensor("e.w1.scale", w1[1].shape, w1[1], 2403, 6, 1, 0.5, 0.25)]
+    want = zcblk.build_block(ts, 4)
+    got = mf.build_synthetic_quant_block([mf.SyntheticTensor(t["name"].decode(), t["role"], t["shape"], t["data"],
+                                                             t["dtype_original"], t["quant_format"], t["scale"],
+                                                             t["zero_point"]) for t in ts])
+    assert got == want

@@ -1,12 +1,13 @@
 // Build-time generator for the glibc-exact libm tables used by the device
 // code (see libm_emul.h).  It runs the exact same emulation code on the host
 // and compares it with the host glibc over every float input of each domain:
-//   expf : every non-NaN float (silu's argument after min(g, 10) lies in
-//          [-10, +inf); the router's sqrt-softplus takes any value <= 20)
+//   expf : every non-NaN float; the few inputs where the restated method
+//          still differs are listed with glibc's result (at most 4096)
 //   log1pf: every non-negative float     (log1p(expf(v)) of the router)
 //   log2f: every normal float            (ceil(log2f(r)) for r = amax / 448)
 //   exp2f: every integral k in [-126, 127]
-// and aborts if any input disagrees, so a written table is a verified one.
+// and aborts if any other input disagrees, so a written table is a verified
+// one.
 //
 // Usage: gen_libm_tables <out.inc>
 #include <math.h>
@@ -17,61 +18,47 @@
 
 #include "libm_emul.h"
 
-static uint64_t g_tab[35];
+static uint64_t g_tab[WH_EXP_TAB_LEN];
 
+// The constants of glibc's expf method: 2^(i/32) from long double (then
+// less i << 47, so that adding k << 47 scales by 2^(k/32)), 32/ln2, the
+// rounding shift 1.5 * 2^52 and the published cubic, scaled for r in units
+// of 1/32.
 static void build_exp_constants(void) {
-    for (int j = 0; j < 32; ++j) g_tab[j] = wh_double_to_bits((double)exp2l((long double)j / 32.0L));
-    long double ln2 = logl(2.0L);
-    g_tab[32] = wh_double_to_bits((double)(32.0L / ln2));
-    long double l = ln2 / 32.0L;
-    // head: l rounded to 32 significant bits, so n * head is exact for |n| < 2^21
-    int ex;
-    long double m = frexpl(l, &ex);
-    long double head = ldexpl(roundl(ldexpl(m, 32)), ex - 32);
-    g_tab[33] = wh_double_to_bits((double)head);
-    g_tab[34] = wh_double_to_bits((double)(l - head));
+    for (int i = 0; i < 32; ++i)
+        g_tab[i] = wh_double_to_bits((double)exp2l((long double)i / 32.0L)) - ((uint64_t)i << 47);
+    const double n = 32.0;
+    g_tab[32] = wh_double_to_bits(0x1.71547652b82fep+0 * n);
+    g_tab[33] = wh_double_to_bits(0x1.8p+52);
+    g_tab[34] = wh_double_to_bits(0x1.c6af84b912394p-5 / n / n / n);
+    g_tab[35] = wh_double_to_bits(0x1.ebfce50fac4f3p-3 / n / n);
+    g_tab[36] = wh_double_to_bits(0x1.62e42ff0c52d6p-1 / n);
 }
+
+enum { EXC_MAX = 4096 };
 
 typedef struct {
     uint64_t lo, hi;  // float bit range [lo, hi)
-    uint32_t* flips;
-    size_t nflips, cap;
-    long bad;
+    uint32_t exc[2 * EXC_MAX];
+    size_t nexc;
+    long over;
 } exp_job;
 
 static void* exp_scan(void* p) {
     exp_job* j = (exp_job*)p;
     for (uint64_t b = j->lo; b < j->hi; ++b) {
-        float y = wh_bits_to_float((uint32_t)b);
-        float g = expf(y);
-        float f;
-        double d = 0.0;
-        if (y > 89.0f) {
-            f = wh_bits_to_float(0x7f800000u);
-        } else if (y < -104.0f) {
-            f = 0.0f;
-        } else {
-            d = wh_exp_double(y, g_tab);
-            f = (float)d;
-        }
-        if (wh_float_to_bits(g) == wh_float_to_bits(f)) continue;
-        // a mismatch must be a flip across a nearby midpoint
-        uint32_t fb = wh_float_to_bits(f);
-        double diff = d - (double)f;
-        uint32_t want;
-        if ((fb & 0x7fffffffu) == 0x7f800000u) want = 0x7f7fffffu;
-        else want = diff > 0.0 ? fb + 1 : fb - 1;
-        if (y > 89.0f || y < -104.0f || !wh_expf_near_midpoint(d, f) || want != wh_float_to_bits(g)) {
-            if (j->bad < 5)
-                fprintf(stderr, "expf: unrepresentable mismatch y=%a glibc=%a emul=%a d=%a\n", y, g, f, d);
-            j->bad++;
+        const uint32_t u = (uint32_t)b;
+        if ((u & 0x7fffffffu) > 0x7f800000u) continue;  // NaN
+        const float y = wh_bits_to_float(u);
+        const uint32_t g = wh_float_to_bits(expf(y));
+        if (wh_float_to_bits(wh_expf_glibc(y, g_tab, NULL, 0)) == g) continue;
+        if (j->nexc == EXC_MAX) {
+            j->over++;
             continue;
         }
-        if (j->nflips == j->cap) {
-            j->cap = j->cap ? j->cap * 2 : 4096;
-            j->flips = (uint32_t*)realloc(j->flips, j->cap * sizeof(uint32_t));
-        }
-        j->flips[j->nflips++] = (uint32_t)b;
+        j->exc[2 * j->nexc] = u;
+        j->exc[2 * j->nexc + 1] = g;
+        j->nexc++;
     }
     return NULL;
 }
@@ -159,53 +146,59 @@ int main(int argc, char** argv) {
     enum { T = 8 };
     build_exp_constants();
 
-    // expf over [-inf, -0] and [+0, +inf]
-    uint64_t ranges[2][2] = {{0x80000000ull, 0xff800001ull}, {0x00000000ull, 0x7f800001ull}};
-    uint32_t* flips = NULL;
-    size_t nflips = 0;
+    // expf over every float: the restated method, and the inputs where it
+    // still differs from the host glibc
+    static exp_job js[T];
+    pthread_t ts[T];
+    uint32_t* exc = NULL;
+    size_t nexc = 0;
     long bad = 0;
-    for (int r = 0; r < 2; ++r) {
-        exp_job js[T];
-        pthread_t ts[T];
-        uint64_t lo = ranges[r][0], n = ranges[r][1] - ranges[r][0];
-        for (int i = 0; i < T; ++i) {
-            memset(&js[i], 0, sizeof js[i]);
-            js[i].lo = lo + n * i / T;
-            js[i].hi = lo + n * (i + 1) / T;
-            pthread_create(&ts[i], NULL, exp_scan, &js[i]);
-        }
-        for (int i = 0; i < T; ++i) {
-            pthread_join(ts[i], NULL);
-            bad += js[i].bad;
-            flips = (uint32_t*)realloc(flips, (nflips + js[i].nflips + 1) * sizeof(uint32_t));
-            memcpy(flips + nflips, js[i].flips, js[i].nflips * sizeof(uint32_t));
-            nflips += js[i].nflips;
-            free(js[i].flips);
-        }
+    for (int i = 0; i < T; ++i) {
+        js[i].lo = (0x100000000ull * i) / T;
+        js[i].hi = (0x100000000ull * (i + 1)) / T;
+        js[i].nexc = 0;
+        js[i].over = 0;
+        pthread_create(&ts[i], NULL, exp_scan, &js[i]);
     }
-    if (bad) {
-        fprintf(stderr, "expf: %ld inputs not representable by the flip scheme\n", bad);
+    for (int i = 0; i < T; ++i) {
+        pthread_join(ts[i], NULL);
+        bad += js[i].over;
+        exc = (uint32_t*)realloc(exc, (nexc + js[i].nexc + 1) * 2 * sizeof(uint32_t));
+        memcpy(exc + 2 * nexc, js[i].exc, js[i].nexc * 2 * sizeof(uint32_t));
+        nexc += js[i].nexc;
+    }
+    if (bad || nexc > EXC_MAX) {
+        fprintf(stderr, "expf: more than %d inputs differ from the host glibc\n", EXC_MAX);
         return 1;
     }
-    qsort(flips, nflips, sizeof(uint32_t), cmp_u32);
-    // re-check the table-driven function on every flipped input and on a
-    // stride sample of the rest (the scan above already covered every input)
-    for (size_t i = 0; i < nflips; ++i) {
-        float y = wh_bits_to_float(flips[i]);
-        if (wh_float_to_bits(wh_expf_glibc(y, g_tab, flips, (uint32_t)nflips)) != wh_float_to_bits(expf(y))) {
+    // sort the (input, result) pairs by input (ranges above were ascending
+    // in bit order per thread; the sign bit splits them, so sort anyway)
+    for (size_t a = 1; a < nexc; ++a)
+        for (size_t b2 = a; b2 > 0 && exc[2 * (b2 - 1)] > exc[2 * b2]; --b2) {
+            uint32_t k = exc[2 * b2], v = exc[2 * b2 + 1];
+            exc[2 * b2] = exc[2 * (b2 - 1)];
+            exc[2 * b2 + 1] = exc[2 * (b2 - 1) + 1];
+            exc[2 * (b2 - 1)] = k;
+            exc[2 * (b2 - 1) + 1] = v;
+        }
+    // verify the table-driven function on every listed input and on a
+    // stride sample of the rest (the scan above covered every input)
+    for (size_t i = 0; i < nexc; ++i) {
+        float y = wh_bits_to_float(exc[2 * i]);
+        if (wh_float_to_bits(wh_expf_glibc(y, g_tab, exc, (uint32_t)nexc)) != wh_float_to_bits(expf(y))) {
             fprintf(stderr, "expf: verification failed at %a\n", y);
             return 1;
         }
     }
-    for (int r = 0; r < 2; ++r) {
-        for (uint64_t b = ranges[r][0]; b < ranges[r][1]; b += 997) {
-            float y = wh_bits_to_float((uint32_t)b);
-            if (wh_float_to_bits(wh_expf_glibc(y, g_tab, flips, (uint32_t)nflips)) != wh_float_to_bits(expf(y))) {
-                fprintf(stderr, "expf: verification failed at %a\n", y);
-                return 1;
-            }
+    for (uint64_t b = 0; b < 0x100000000ull; b += 997) {
+        if (((uint32_t)b & 0x7fffffffu) > 0x7f800000u) continue;
+        float y = wh_bits_to_float((uint32_t)b);
+        if (wh_float_to_bits(wh_expf_glibc(y, g_tab, exc, (uint32_t)nexc)) != wh_float_to_bits(expf(y))) {
+            fprintf(stderr, "expf: verification failed at %a\n", y);
+            return 1;
         }
     }
+    fprintf(stderr, "expf: every float matches the host glibc (%zu listed exceptions)\n", nexc);
 
     // log2f thresholds per binade: largest mantissa for which log2f(r) == e
     static uint32_t thr[254];
@@ -274,19 +267,18 @@ int main(int argc, char** argv) {
         return 1;
     }
     fprintf(out, "// Generated by gen_libm_tables.c from the host glibc; verified exhaustively.\n");
-    fprintf(out, "#define WH_EXP2_TAB_INIT \\\n");
-    for (int j = 0; j < 35; ++j) fprintf(out, "  0x%016llxull%s\n", (unsigned long long)g_tab[j], j < 34 ? ", \\" : "");
+    fprintf(out, "#define WH_EXP_TAB_INIT \\\n");
+    for (int j = 0; j < WH_EXP_TAB_LEN; ++j)
+        fprintf(out, "  0x%016llxull%s\n", (unsigned long long)g_tab[j], j < WH_EXP_TAB_LEN - 1 ? ", \\" : "");
     fprintf(out, "#define WH_LOG2F_THR_INIT \\\n");
     for (int i = 0; i < 254; ++i) fprintf(out, "  %uu%s\n", thr[i], i < 253 ? ", \\" : "");
-    fprintf(out, "#define WH_EXPF_FLIP_COUNT %zuu\n", nflips);
-    fprintf(out, "#define WH_EXPF_FLIP_INIT \\\n");
-    for (size_t i = 0; i < nflips; ++i) {
-        fprintf(out, "0x%08xu%s", flips[i], i + 1 < nflips ? "," : "");
-        if (i % 12 == 11 && i + 1 < nflips) fprintf(out, " \\\n");
-    }
+    fprintf(out, "#define WH_EXPF_EXC_COUNT %zuu\n", nexc);
+    fprintf(out, "#define WH_EXPF_EXC_INIT");
+    if (nexc == 0) fprintf(out, " 0u, 0u");  // placeholder pair, never read
+    for (size_t i = 0; i < nexc; ++i) fprintf(out, "%s 0x%08xu, 0x%08xu", i ? "," : "", exc[2 * i], exc[2 * i + 1]);
     fprintf(out, "\n");
     fclose(out);
-    fprintf(stderr, "libm tables: %zu expf flips, log2f thresholds written to %s\n", nflips, argv[1]);
-    free(flips);
+    fprintf(stderr, "libm tables: %zu expf exceptions, log2f thresholds written to %s\n", nexc, argv[1]);
+    free(exc);
     return 0;
 }

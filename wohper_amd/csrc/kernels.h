@@ -9,9 +9,9 @@
 #endif
 
 // glibc-exact libm tables (generated at build time, see gen_libm_tables.c)
-__device__ const uint64_t kExpTab[35] = {WH_EXP2_TAB_INIT};
+__device__ const uint64_t kExpTab[WH_EXP_TAB_LEN] = {WH_EXP_TAB_INIT};
 __device__ const uint32_t kLog2Thr[254] = {WH_LOG2F_THR_INIT};
-__device__ const uint32_t kExpfFlip[WH_EXPF_FLIP_COUNT] = {WH_EXPF_FLIP_INIT};
+__device__ const uint32_t kExpfExc[WH_EXPF_EXC_COUNT ? 2 * WH_EXPF_EXC_COUNT : 2] = {WH_EXPF_EXC_INIT};
 
 // status word bits, OR-ed by kernels, read by the host after the stream syncs
 #define WH_ST_NONFINITE_OUTPUT 1u
@@ -914,7 +914,7 @@ __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
     const float u = wh_dpp_row_shl8(v);  // lane 16k <- lane 16k + 8: the w3 row
     if ((threadIdx.x & 15) == 0) {
         if (!(fabsf(v) <= 3.4028235e38f) || !(fabsf(u) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
-        a.h[((size_t)tok * a.n_experts + e) * a.inter + row] = wh_swiglu(v, u, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
+        a.h[((size_t)tok * a.n_experts + e) * a.inter + row] = wh_swiglu(v, u, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
         if (a.gu) {
             float* gu = a.gu + ((size_t)tok * a.n_experts + e) * 2 * a.inter;
             gu[row] = v;
@@ -1121,14 +1121,14 @@ __global__ void __launch_bounds__(256) k_fp8_dequant(const uint8_t* __restrict__
 }
 
 // Test support: evaluates the device libm emulation on an array.
-// fn 0: silu(x), 1: expf(x) (x >= -10), 2: 2^ceil(log2f(max(x,1e-4)/448)).
+// fn 0: silu(x), 1: expf(x), 2: 2^ceil(log2f(max(x,1e-4)/448)).
 __global__ void k_debug_eval(int fn, const float* __restrict__ in, float* __restrict__ out, uint32_t n) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     float x = in[i];
     float r;
-    if (fn == 0) r = wh_silu(x, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
-    else if (fn == 1) r = wh_expf_glibc(x, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
+    if (fn == 0) r = wh_silu(x, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
+    else if (fn == 1) r = wh_expf_glibc(x, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
     else r = wh_pow2f(wh_aq_scale_exp(x, kLog2Thr));
     out[i] = r;
 }

@@ -4,20 +4,19 @@
 // The reference engine calls the platform libm through Rust's f32 methods:
 //   silu(x) = x / (1 + expf(-x))                 E/deepseek_v4.rs:551-554
 //   act-quant block scale exp2f(ceilf(log2f(r)))  E/compute.rs:2514
-// glibc's expf is not correctly rounded (it misrounds roughly 7e-5 of the
-// inputs in [-10, 89]), so matching it bit for bit needs more than an
-// accurate exp.  The scheme here:
-//   1. wh_exp_double(y): exp(y) in double, relative error below 1e-15
-//      (Cody-Waite reduction by ln2/32, 32-entry 2^(j/32) table, degree-6
-//      Taylor polynomial), built only from IEEE add/mul/fma/rint, so host
-//      and device evaluate it to the same bits.
-//   2. Round to float.  If the double result lies within
-//      WH_EXPF_WINDOW ulp of a float rounding midpoint, look the input up in
-//      a sorted table of inputs where glibc's result is the other neighbour
-//      of that midpoint, and flip.  The generator builds that table by
-//      comparing this exact code with the host glibc expf over every float
-//      input of the silu domain [-10, +inf), and then re-verifies the whole
-//      domain.
+//   router sqrt(log1pf(expf(v)))                  E/compute.rs:2238-2249
+// glibc's expf and log1pf are not correctly rounded, so a correctly rounded
+// device function would not match them.  Instead:
+//   1. expf restates glibc's own method (the exp of ARM's optimized-routines
+//      by Szabolcs Nagy, glibc's sysdeps/ieee754/flt-32/e_expf.c since 2.27):
+//      x*32/ln2 = k + r, 2^(k/32) from a 32-entry table, a cubic in r, all
+//      in IEEE double with each operation rounded on its own, which host and
+//      device evaluate alike.  The generator compares it with the host
+//      glibc on every float and lists the few inputs where the two still
+//      differ (different contraction of the polynomial in the host build)
+//      with glibc's result; the device checks that short sorted list.
+//   2. log1pf restates fdlibm's float log1p (see wh_log1pf), which matches
+//      glibc on every non-negative float.
 //   3. ceil(log2f(r)) for normal r is e + (mantissa > T[e]), where the
 //      per-binade thresholds T[] are found by scanning the host log2f and
 //      verified over every mantissa of every binade.
@@ -30,7 +29,11 @@
 #define WH_HD static inline
 #endif
 
-#define WH_EXPF_WINDOW 0.003  // in float ulps; must exceed glibc's error beyond 0.5 ulp
+// Layout of the expf table (doubles as bit patterns): entries 0..31 are
+// asuint64(2^(i/32)) - (i << 47), then 32/ln2, 1.5 * 2^52 (the rounding
+// shift) and the cubic's coefficients for r in units of 1/32 (c0 r^3 +
+// c1 r^2 + c2 r + 1).
+#define WH_EXP_TAB_LEN 37
 
 WH_HD double wh_bits_to_double(uint64_t b) {
     union { uint64_t u; double d; } v;
@@ -53,85 +56,48 @@ WH_HD uint32_t wh_float_to_bits(float f) {
     return v.u;
 }
 
-// exp(y) for finite y with |y| < 104 (callers clamp).  exp2_tab holds, as
-// double bit patterns, 2^(j/32) for j = 0..31, then 32/ln2, then ln2/32 split
-// into a 32-significant-bit head (so n*head is exact) and a tail; the
-// generator derives them from long double arithmetic.
-WH_HD double wh_exp_double(float yf, const uint64_t* exp2_tab) {
-    const double inv_l = wh_bits_to_double(exp2_tab[32]);
-    const double l_hi = wh_bits_to_double(exp2_tab[33]);
-    const double l_lo = wh_bits_to_double(exp2_tab[34]);
-    double x = (double)yf;
-    double nd = __builtin_rint(x * inv_l);
-    double r = __builtin_fma(-nd, l_hi, x);
-    r = __builtin_fma(-nd, l_lo, r);
-    // Taylor polynomial of exp(r) on |r| <= ln2/64, Horner with fma
-    double p = 1.0 / 720.0;
-    p = __builtin_fma(p, r, 1.0 / 120.0);
-    p = __builtin_fma(p, r, 1.0 / 24.0);
-    p = __builtin_fma(p, r, 1.0 / 6.0);
-    p = __builtin_fma(p, r, 0.5);
-    p = __builtin_fma(p, r, 1.0);
-    p = __builtin_fma(p, r, 1.0);
-    int64_t n = (int64_t)nd;
-    int64_t j = n & 31;
-    int64_t k = (n - j) / 32;  // exact floor division
-    double t = wh_bits_to_double(exp2_tab[j]);
-    double s = wh_bits_to_double((uint64_t)(k + 1023) << 52);  // 2^k, |k| < 160 here
-    return (t * p) * s;
-}
-
-// Returns 1 if the double result `d` (positive, finite) is within the window
-// of the rounding midpoint between float(d) and its neighbour on d's side.
-WH_HD int wh_expf_near_midpoint(double d, float f) {
-    double fd = (double)f;
-    double diff = d - fd;
-    uint32_t fb = wh_float_to_bits(f);
-    int ex = (int)((fb >> 23) & 0xff);
-    if (ex == 0 || ex == 0xff) return 1;  // subnormal / inf: always consult the table
-    double ulp = wh_bits_to_double((uint64_t)(ex - 127 - 23 + 1023) << 52);
-    // below a power of two the neighbour spacing halves
-    double ulp_side = (diff < 0.0 && (fb & 0x7fffff) == 0) ? ulp * 0.5 : ulp;
-    double dist = 0.5 * ulp_side - (diff < 0.0 ? -diff : diff);
-    return dist < WH_EXPF_WINDOW * ulp_side;
-}
-
-WH_HD int wh_table_contains(const uint32_t* tab, uint32_t n, uint32_t key) {
-    uint32_t lo = 0, hi = n;
-    while (lo < hi) {
-        uint32_t mid = (lo + hi) >> 1;
-        uint32_t v = tab[mid];
-        if (v == key) return 1;
-        if (v < key) lo = mid + 1;
-        else hi = mid;
+// glibc's expf(x) for every float x.  `exc` holds n_exc (input bits, glibc
+// result bits) pairs sorted by input: the inputs where this restatement and
+// the host glibc differ.
+WH_HD float wh_expf_glibc(float x, const uint64_t* tab, const uint32_t* exc, uint32_t n_exc) {
+    const uint32_t ux = wh_float_to_bits(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ff;
+    if (abstop >= 0x42b) {                                 // |x| >= 88 (top 12 bits of 88.0f)
+        if (ux == 0xff800000u) return 0.0f;                // -inf
+        if (abstop >= 0x7f8) return x + x;                 // +inf, NaN
+        if (x > wh_bits_to_float(0x42b17217u)) return wh_bits_to_float(0x7f800000u);  // > log(2^128)
+        if (x < wh_bits_to_float(0xc2cff1b4u)) return 0.0f;                            // < log(2^-150)
     }
-    return 0;
-}
-
-// glibc-exact expf(y) for every non-NaN float y (the silu domain is
-// [-10, +inf); the router's sqrt-softplus also takes y < -10, where results
-// go subnormal and then zero).  `flip` lists (sorted) the inputs whose glibc result is the other
-// neighbour of the nearby rounding midpoint.
-WH_HD float wh_expf_glibc(float y, const uint64_t* exp2_tab, const uint32_t* flip, uint32_t nflip) {
-    if (y > 89.0f) return wh_bits_to_float(0x7f800000u);
-    if (y < -104.0f) return 0.0f;  // below half the least subnormal
-    double d = wh_exp_double(y, exp2_tab);
-    float f = (float)d;
-    if (wh_expf_near_midpoint(d, f) && wh_table_contains(flip, nflip, wh_float_to_bits(y))) {
-        uint32_t fb = wh_float_to_bits(f);
-        double diff = d - (double)f;
-        if ((fb & 0x7fffffffu) == 0x7f800000u) {
-            f = wh_bits_to_float(0x7f7fffffu);  // inf -> FLT_MAX
-        } else {
-            f = wh_bits_to_float(diff > 0.0 ? fb + 1 : fb - 1);  // positive f: +1 bit = next up
+    const double xd = (double)x;
+    const double z = wh_bits_to_double(tab[32]) * xd;
+    double kd = z + wh_bits_to_double(tab[33]);            // round to the nearest integer
+    const uint64_t ki = wh_double_to_bits(kd);
+    kd -= wh_bits_to_double(tab[33]);
+    const double r = z - kd;
+    const uint64_t t = tab[ki % 32] + (ki << 47);
+    const double s = wh_bits_to_double(t);                 // 2^(k/32)
+    const double zz = wh_bits_to_double(tab[34]) * r + wh_bits_to_double(tab[35]);
+    const double r2 = r * r;
+    double y = wh_bits_to_double(tab[36]) * r + 1.0;
+    y = zz * r2 + y;
+    y = y * s;
+    float f = (float)y;
+    if (n_exc) {
+        uint32_t lo = 0, hi = n_exc;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            const uint32_t k = exc[2 * mid];
+            if (k == ux) return wh_bits_to_float(exc[2 * mid + 1]);
+            if (k < ux) lo = mid + 1;
+            else hi = mid;
         }
     }
     return f;
 }
 
 // silu exactly as the reference computes it in f32: x / (1 + expf(-x)).
-WH_HD float wh_silu(float x, const uint64_t* exp2_tab, const uint32_t* flip, uint32_t nflip) {
-    float e = wh_expf_glibc(-x, exp2_tab, flip, nflip);
+WH_HD float wh_silu(float x, const uint64_t* exp_tab, const uint32_t* exc, uint32_t n_exc) {
+    float e = wh_expf_glibc(-x, exp_tab, exc, n_exc);
     float den = 1.0f + e;
     return x / den;
 }

@@ -314,11 +314,11 @@ __global__ void __launch_bounds__(256) k_moe_batch_quant(const void* __restrict_
 // per thread: h = silu(min(g, 10)) * clamp(u, -10, 10).
 __global__ void __launch_bounds__(256) k_moe_batch_swiglu(const float* __restrict__ g, const float* __restrict__ u,
                                                           float* __restrict__ h, uint32_t n) {
-    __shared__ uint64_t exp_tab[35];
-    if (threadIdx.x < 35) exp_tab[threadIdx.x] = kExpTab[threadIdx.x];
+    __shared__ uint64_t exp_tab[WH_EXP_TAB_LEN];
+    if (threadIdx.x < WH_EXP_TAB_LEN) exp_tab[threadIdx.x] = kExpTab[threadIdx.x];
     __syncthreads();
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) h[i] = wh_swiglu(g[i], u[i], exp_tab, kExpfFlip, WH_EXPF_FLIP_COUNT);
+    if (i < n) h[i] = wh_swiglu(g[i], u[i], exp_tab, kExpfExc, WH_EXPF_EXC_COUNT);
 }
 
 // ------------------------------------------------------------ exact items

@@ -304,7 +304,7 @@ __global__ void __launch_bounds__(128 * kSl) k_moe_gateup_sk(wh_moe_args a) {
         }
         if (!(fabsf(g) <= 3.4028235e38f) || !(fabsf(u) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
         const size_t he = ((size_t)tok * a.n_experts + e) * a.inter;
-        a.h[he + row0 + r] = wh_swiglu(g, u, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
+        a.h[he + row0 + r] = wh_swiglu(g, u, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
         if (a.gu) {
             a.gu[2 * he + row0 + r] = g;
             a.gu[2 * he + a.inter + row0 + r] = u;

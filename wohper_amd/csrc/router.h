@@ -51,8 +51,8 @@ __device__ __forceinline__ float wh_sqrt_softplus(float v) {
     if (v != v) return 0.0f;
     float sp;
     if (v > 20.0f) sp = v;
-    else if (v < -20.0f) sp = wh_expf_glibc(v, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
-    else sp = wh_log1pf(wh_expf_glibc(v, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT));
+    else if (v < -20.0f) sp = wh_expf_glibc(v, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
+    else sp = wh_log1pf(wh_expf_glibc(v, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT));
     const float m = fmaxf(sp, 0.0f);
     return (m > 0.0f && m <= 3.4028235e38f) ? wh_sqrt_rn(m) : m;  // sqrt(+0) = +0, sqrt(inf) = inf
 }
@@ -249,5 +249,5 @@ __global__ void k_debug_eval_router(int fn, const float* __restrict__ in, float*
     if (i >= n) return;
     const float x = in[i];
     out[i] = fn == 4 ? wh_sqrt_softplus(x)
-                     : fn == 5 ? wh_log1pf(x) : wh_expf_glibc(x, kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
+                     : fn == 5 ? wh_log1pf(x) : wh_expf_glibc(x, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
 }

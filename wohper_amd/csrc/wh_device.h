@@ -134,8 +134,8 @@ __device__ __forceinline__ float wh_clamp448_finite(float v) { return fminf(fmax
 
 // DeepSeek-V4 SwiGLU on one gate/up pair (E/deepseek_v4.rs:590-594)
 __device__ __forceinline__ float wh_swiglu(float g, float u, const uint64_t* exp_tab,
-                                           const uint32_t* flip, uint32_t nflip) {
+                                           const uint32_t* exc, uint32_t n_exc) {
     float gated = fminf(g, 10.0f);
     float upped = u < -10.0f ? -10.0f : (u > 10.0f ? 10.0f : u);
-    return wh_silu(gated, exp_tab, flip, nflip) * upped;
+    return wh_silu(gated, exp_tab, exc, n_exc) * upped;
 }

@@ -423,7 +423,7 @@ int launch_fp4(wh_ctx* c, const Tensor& t, const float* x, float* y) {
 __global__ void k_swiglu_generic(const float* g, const float* u, float* h, uint32_t n,
                                  uint32_t* status) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) h[i] = wh_swiglu(g[i], u[i], kExpTab, kExpfFlip, WH_EXPF_FLIP_COUNT);
+    if (i < n) h[i] = wh_swiglu(g[i], u[i], kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
 }
 
 // Ordered routed sum (E/compute.rs:1948-2030) of the first n_experts -
@@ -1299,8 +1299,8 @@ const char* wh_last_error(void) { return g_last_error; }
 
 const char* wh_build_info(void) {
     static char buf[160];
-    std::snprintf(buf, sizeof buf, "wohper_hip gfx950; expf flip table %u entries; max experts %d; lds %zu",
-                  (unsigned)WH_EXPF_FLIP_COUNT, WH_MAX_EXPERTS, g_max_lds);
+    std::snprintf(buf, sizeof buf, "wohper_hip gfx950; expf exceptions %u; max experts %d; lds %zu",
+                  (unsigned)WH_EXPF_EXC_COUNT, WH_MAX_EXPERTS, g_max_lds);
     return buf;
 }
 

@@ -1,5 +1,6 @@
-"""Experts-pack index of a converted model: the host-side reader that hands
-wh_store_expert_pack its entries.
+"""Host-side pieces of the engine's model format: the experts-pack index
+reader that hands wh_store_expert_pack its entries, and the in-memory
+ZCBLK01 block builder.
 
 Mirrors load_optional_expert_pack (engine/zc_infer_core/src/model_format.rs:458-504):
 `<model>.experts_pack.index.json` beside the model file (the model path with
@@ -14,9 +15,10 @@ disk_bytes must be a multiple of 2 MiB.  A later entry with the same
 from __future__ import annotations
 
 import json
+import struct
 from dataclasses import dataclass
 from pathlib import Path
-from typing import Dict, Optional, Tuple
+from typing import Dict, Optional, Sequence, Tuple
 
 ALIGN_2MB = 2 * 1024 * 1024  # engine/zc_infer_core/src/lib.rs:10
 PACK_FORMATS = ("wohper-experts-pack", "zeroclaw-experts-pack")
@@ -100,3 +102,45 @@ def load_optional_expert_pack(model_path) -> Optional[ExpertPackInfo]:
                                        f"unaligned field {field}: value={value}, required={ALIGN_2MB}")
         entries[(layer_id, expert_id)] = ExpertPackEntry(offset, disk_bytes, payload_bytes)
     return ExpertPackInfo(pack, entries)
+
+
+@dataclass
+class SyntheticTensor:
+    """SyntheticTensor (engine/zc_infer_core/src/compute.rs:3255-3264)."""
+    name: str
+    role_code: int
+    shape: Sequence[int]
+    data: bytes
+    dtype_original: int
+    quant_format: int
+    scale: float = 1.0
+    zero_point: float = 0.0
+
+
+def build_synthetic_quant_block(tensors: Sequence[SyntheticTensor]) -> bytes:
+    """A ZCBLK01 block in memory from loose tensors, laid out as
+    build_synthetic_quant_block does (compute.rs:3272-3320): the 40-byte
+    header (quant_format 4, flags 0), one 52-byte record per tensor, the
+    names blob ({u16 len, bytes} each), then each tensor's data followed by
+    its shape blob ({u32 rank, u64 dims})."""
+    names = bytearray()
+    name_offsets = []
+    for t in tensors:
+        raw = t.name.encode()
+        name_offsets.append(len(names))
+        names += struct.pack("<H", len(raw)) + raw
+    names_offset = 40 + 52 * len(tensors)
+    cursor = names_offset + len(names)
+    body = bytearray()
+    places = []
+    for t in tensors:
+        data_off = cursor + len(body)
+        body += bytes(t.data)
+        shape_off = cursor + len(body)
+        body += struct.pack("<I", len(t.shape)) + b"".join(struct.pack("<Q", int(d)) for d in t.shape)
+        places.append((data_off, shape_off))
+    out = bytearray(struct.pack("<8sIIIIQQ", b"ZCBLK01\0", 1, len(tensors), 4, 0, 40, names_offset))
+    for t, off, (data_off, shape_off) in zip(tensors, name_offsets, places):
+        out += struct.pack("<HHIIQQQQff", t.dtype_original, t.quant_format, len(t.shape), t.role_code, off,
+                           shape_off, data_off, len(t.data), t.scale, t.zero_point)
+    return bytes(out + names + body)
