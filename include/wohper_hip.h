@@ -226,7 +226,7 @@ int wh_route_experts(wh_ctx* ctx, uint32_t layer_id, const float* hidden, size_t
                      uint32_t* expert_ids, float* scores, size_t out_cap, size_t* n_out);
 
 /* The same on device pointers, ordered on the context stream: x_dev
- * [hidden_len] f32, available_dev (or NULL), outputs ids_dev / scores_dev
+ * [hidden_len] f32 (16-byte aligned), available_dev (or NULL), outputs ids_dev / scores_dev
  * [active_experts] and count_dev.  Argument and table errors are returned
  * here, before anything is queued. */
 int wh_route_experts_async(wh_ctx* ctx, uint32_t layer_id, const float* x_dev, size_t hidden_len,

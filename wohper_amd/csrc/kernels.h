@@ -770,8 +770,27 @@ __device__ __forceinline__ void wh_thr_stage_load(wh_thr_stage& st) {
 __device__ __forceinline__ void wh_thr_stage_store(const wh_thr_stage& st, uint32_t* thr) {
     if (threadIdx.x < 254) thr[threadIdx.x] = st.v;
 }
+
+// The expf table staged in LDS the same way (needs >= 74 threads), so the
+// SwiGLU epilogue reads no global memory behind the weight stream.
+struct wh_exp_stage {
+    uint32_t v;
+};
+__device__ __forceinline__ void wh_exp_stage_load(wh_exp_stage& st) {
+    st.v = threadIdx.x < 2 * WH_EXP_TAB_LEN ? reinterpret_cast<const uint32_t*>(kExpTab)[threadIdx.x] : 0u;
+}
+__device__ __forceinline__ void wh_exp_stage_store(const wh_exp_stage& st, uint64_t* tab) {
+    if (threadIdx.x < 2 * WH_EXP_TAB_LEN) reinterpret_cast<uint32_t*>(tab)[threadIdx.x] = st.v;
+}
 // LDS bytes of a routed-expert workgroup over `cols` input columns.
-__host__ __device__ constexpr size_t wh_moe_wg_lds(size_t cols) { return wh_fp4_wg_lds(cols) + 256 * sizeof(uint32_t); }
+__host__ __device__ constexpr size_t wh_moe_wg_lds(size_t cols) {
+    return wh_fp4_wg_lds(cols) + (256 + 2 + 2 * WH_EXP_TAB_LEN) * sizeof(uint32_t);
+}
+// The staged expf table of a workgroup whose log2f thresholds sit at thr
+// (256 words), 8-byte aligned.
+__device__ __forceinline__ uint64_t* wh_exp_tab_after(uint32_t* thr) {
+    return reinterpret_cast<uint64_t*>((reinterpret_cast<uintptr_t>(thr + 256) + 7) & ~uintptr_t(7));
+}
 
 // 16 consecutive x values of one thread (bf16 or f32), loaded early.
 struct wh_xq_stage {
@@ -876,11 +895,14 @@ __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
     float* xs = lds;
     float* s8row = lds + wh_xs_floats(a.hidden) + oct * wh_s8_stride(G);
     uint32_t* thr = (uint32_t*)(lds + wh_fp4_wg_lds(a.hidden) / sizeof(float));
+    uint64_t* exp_tab = wh_exp_tab_after(thr);
     const bool bf16 = a.x_is_bf16 != 0;
     const void* xt = bf16 ? (const void*)((const uint16_t*)a.x + (size_t)tok * a.hidden)
                           : (const void*)((const float*)a.x + (size_t)tok * a.hidden);
     wh_thr_stage ts;
     wh_thr_stage_load(ts);
+    wh_exp_stage es;
+    wh_exp_stage_load(es);
     float acc;
     if constexpr (kBlk > 0) {
         // staging loads first, then the weight row; the staging waits below
@@ -893,6 +915,7 @@ __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
         wh_fp4_ring_prologue<kRing>(r, wrow, lane);
         __builtin_amdgcn_sched_barrier(0);
         wh_thr_stage_store(ts, thr);
+        wh_exp_stage_store(es, exp_tab);
         __syncthreads();
         wh_xq_stage_store(xst, bf16, xs, thr, a.status);
         wh_s8_stage_store<kBlk>(ss, s8row, lane);
@@ -900,6 +923,7 @@ __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
         acc = wh_fp4_ring_dot<kBlk, kRing>(r, wrow, xs, s8row, lane);
     } else {
         wh_thr_stage_store(ts, thr);
+        wh_exp_stage_store(es, exp_tab);
         __syncthreads();
         for (uint32_t i = threadIdx.x; i < (a.hidden >> 4); i += 256) {
             wh_xq_stage xst;
@@ -914,7 +938,7 @@ __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
     const float u = wh_dpp_row_shl8(v);  // lane 16k <- lane 16k + 8: the w3 row
     if ((threadIdx.x & 15) == 0) {
         if (!(fabsf(v) <= 3.4028235e38f) || !(fabsf(u) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
-        a.h[((size_t)tok * a.n_experts + e) * a.inter + row] = wh_swiglu(v, u, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
+        a.h[((size_t)tok * a.n_experts + e) * a.inter + row] = wh_swiglu(v, u, exp_tab, kExpfExc, WH_EXPF_EXC_COUNT);
         if (a.gu) {
             float* gu = a.gu + ((size_t)tok * a.n_experts + e) * 2 * a.inter;
             gu[row] = v;

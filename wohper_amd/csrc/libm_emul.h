@@ -82,7 +82,11 @@ WH_HD float wh_expf_glibc(float x, const uint64_t* tab, const uint32_t* exc, uin
     y = zz * r2 + y;
     y = y * s;
     float f = (float)y;
-    if (n_exc) {
+    if (n_exc <= 32) {
+        // a short list: uniform loads the compiler keeps in scalar registers
+        for (uint32_t i = 0; i < n_exc; ++i)
+            if (exc[2 * i] == ux) return wh_bits_to_float(exc[2 * i + 1]);
+    } else {
         uint32_t lo = 0, hi = n_exc;
         while (lo < hi) {
             const uint32_t mid = (lo + hi) >> 1;

@@ -259,6 +259,9 @@ __global__ void __launch_bounds__(128 * kSl) k_moe_gateup_sk(wh_moe_args a) {
     constexpr uint32_t kCols = 2048 * kSl, G = kCols / 32;
     __shared__ __align__(16) float sct_all[kWaves * kRows * WH_SK_SCT_STRIDE];
     __shared__ float red[kWaves * kRows];
+    __shared__ uint64_t exp_tab[WH_EXP_TAB_LEN];
+    wh_exp_stage es;
+    wh_exp_stage_load(es);
     const uint32_t tok = blockIdx.y;
     const uint32_t per_e = a.inter / kRows;
     const uint32_t e = blockIdx.x / per_e;
@@ -285,6 +288,7 @@ __global__ void __launch_bounds__(128 * kSl) k_moe_gateup_sk(wh_moe_args a) {
     __builtin_amdgcn_sched_barrier(0);
     float* sct = sct_all + wave * kRows * WH_SK_SCT_STRIDE;
     wh_sk_scales_store<kRows>(ss, xks.v, sct, L);
+    wh_exp_stage_store(es, exp_tab);
     const uint32_t xr[8][2] = {{xv[0].x, xv[0].y}, {xv[0].z, xv[0].w}, {xv[1].x, xv[1].y}, {xv[1].z, xv[1].w},
                                {xv[2].x, xv[2].y}, {xv[2].z, xv[2].w}, {xv[3].x, xv[3].y}, {xv[3].z, xv[3].w}};
     __syncthreads();
@@ -304,7 +308,7 @@ __global__ void __launch_bounds__(128 * kSl) k_moe_gateup_sk(wh_moe_args a) {
         }
         if (!(fabsf(g) <= 3.4028235e38f) || !(fabsf(u) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
         const size_t he = ((size_t)tok * a.n_experts + e) * a.inter;
-        a.h[he + row0 + r] = wh_swiglu(g, u, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
+        a.h[he + row0 + r] = wh_swiglu(g, u, exp_tab, kExpfExc, WH_EXPF_EXC_COUNT);
         if (a.gu) {
             a.gu[2 * he + row0 + r] = g;
             a.gu[2 * he + a.inter + row0 + r] = u;

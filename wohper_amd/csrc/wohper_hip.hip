@@ -179,6 +179,7 @@ struct wh_ctx {
     Scratch x_in, y_out, h, ybuf, cnt_y, tmp, batch, routes, bout, gu, xq;
     Scratch relayout;  // raw FP4 rows on their way into the resident layout
     Scratch rtr;       // router: logits, available ids, outputs of the host-slice call
+    Scratch rtr_cnt;   // router: arrival counter of the one-launch bf16 kernel (kept at 0)
     std::map<uint32_t, Router> routers;
     HostBuf stage_in, stage_out;
     HostBuf pack[2];   // experts-pack read buffers (one filling while the other uploads)
@@ -1101,15 +1102,15 @@ bool name_contains_ci(const whqb::Reader& r, const whqb::Tensor& t, const char* 
 
 constexpr uint32_t kRoleRouter = 9;  // TensorRole::Router, E/compute.rs:455-471
 
-// bf16 row-major [rows][cols] -> the router kernel's lane layout (cols % 64
-// == 0): per 64-column block, lane l's values of chunks 0..3, acc0 then acc1.
+// bf16 row-major [rows][cols] -> the router kernel's layout (cols % 128 ==
+// 0): per 128-column block, chain q = 8a + l (accumulator a, AVX lane l)
+// holds its values of chunks 0..7 in 16 contiguous bytes.
 void bf16_router_layout(const uint16_t* src, uint16_t* dst, size_t rows, size_t cols) {
     for (size_t r = 0; r < rows; ++r)
-        for (size_t b = 0; b < cols / 64; ++b)
-            for (size_t l = 0; l < 8; ++l)
-                for (size_t j = 0; j < 4; ++j)
-                    for (size_t a = 0; a < 2; ++a)
-                        dst[r * cols + 64 * b + 8 * l + 2 * j + a] = src[r * cols + 64 * b + 16 * j + 8 * a + l];
+        for (size_t b = 0; b < cols / 128; ++b)
+            for (size_t q = 0; q < 16; ++q)
+                for (size_t j = 0; j < 8; ++j)
+                    dst[r * cols + 128 * b + 8 * q + j] = src[r * cols + 128 * b + 16 * j + 8 * (q >> 3) + (q & 7)];
 }
 
 // router_bias_values (E/compute.rs:2335-2376): the first Router-role rank-1
@@ -1218,22 +1219,27 @@ int router_prepare(const Router& rt, const wh_route_options& o, size_t hidden_le
 int router_launch(wh_ctx* c, const Router& rt, wh_router_sel sa, const float* x, const uint32_t* avail,
                   float* logits, uint32_t* ids, float* scores, uint32_t* count) {
     const unsigned rows = (unsigned)rt.rows, cols = (unsigned)rt.cols;
-    if (rt.gate == kGateBf16) {
-        k_router_gemv_bf16<<<(rows + 7) / 8, 64, cols * sizeof(float), c->stream>>>(rt.bf16, x, rows, cols, logits);
-    } else if (rt.gate == kGateBf16Rows) {
-        k_router_gemv_bf16_generic<<<(rows + 63) / 64, 64, 0, c->stream>>>(rt.bf16, x, rows, cols, logits);
-    } else {
-        Tensor* t = find_tensor(c, rt.fp8);
-        if (!t) return WH_NOT_RESIDENT;
-        WH_TRY(launch_fp8(c, *t, 0, t->rows, x, logits, 1, 0, 0));
-    }
     sa.logits = logits;
     sa.bias = sa.math ? rt.bias : nullptr;
     sa.avail = avail;
     sa.out_ids = ids;
     sa.out_scores = scores;
     sa.out_count = count;
-    k_router_select<<<1, 64, 0, c->stream>>>(sa);
+    if (rt.gate == kGateBf16) {  // one launch: the last workgroup selects
+        WH_HIP(c->rtr_cnt.ensure(sizeof(uint32_t), true));
+        k_router_bf16<<<(rows + 3) / 4, 64, cols * sizeof(float), c->stream>>>(rt.bf16, x, cols, sa,
+                                                                               c->rtr_cnt.as<uint32_t>());
+        WH_HIP(hipGetLastError());
+        return WH_OK;
+    }
+    if (rt.gate == kGateBf16Rows) {
+        k_router_gemv_bf16_generic<<<(rows + 63) / 64, 64, 0, c->stream>>>(rt.bf16, x, rows, cols, logits);
+    } else {
+        Tensor* t = find_tensor(c, rt.fp8);
+        if (!t) return WH_NOT_RESIDENT;
+        WH_TRY(launch_fp8(c, *t, 0, t->rows, x, logits, 1, 0, 0));
+    }
+    k_router_select<<<1, 256, 0, c->stream>>>(sa);
     WH_HIP(hipGetLastError());
     return WH_OK;
 }
@@ -1334,7 +1340,7 @@ int wh_shutdown(wh_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     c->arena.release_all();
     for (Scratch* s : {&c->x_in, &c->y_out, &c->h, &c->ybuf, &c->cnt_y, &c->tmp, &c->batch, &c->routes, &c->bout,
-                       &c->gu, &c->xq, &c->relayout, &c->rtr})
+                       &c->gu, &c->xq, &c->relayout, &c->rtr, &c->rtr_cnt})
         if (s->p) (void)hipFree(s->p);
     for (auto& kv : c->tables)
         if (kv.second.dev) (void)hipFree(kv.second.dev);
@@ -1732,7 +1738,7 @@ int wh_store_router(wh_ctx* c, uint32_t layer, const uint8_t* block, size_t bloc
         rt.bf16 = (uint16_t*)d;
         std::vector<uint16_t> tmp(n);  // the block's bytes need not be 2-byte aligned
         std::memcpy(tmp.data(), r.data() + gate.data_off, n * 2);
-        if (rt.cols % 64 == 0 && rt.cols * sizeof(float) <= g_max_lds) {
+        if (rt.cols % 128 == 0 && rt.cols * sizeof(float) <= g_max_lds) {
             std::vector<uint16_t> lane(n);
             bf16_router_layout(tmp.data(), lane.data(), rt.rows, rt.cols);
             tmp.swap(lane);
@@ -1773,11 +1779,11 @@ int wh_route_experts(wh_ctx* c, uint32_t layer, const float* hidden, size_t hidd
     WH_TRY(router_prepare(rt, *opts, hidden_len, active, available ? n_available : rt.rows, &sa));
     // scratch: x [cols], logits [rows], available ids, then the outputs
     const size_t nav = available ? n_available : 0;
-    const size_t words = rt.cols + rt.rows + nav + 2 * WH_ROUTER_MAX_ACTIVE + 1;
+    const size_t words = rt.cols + 2 * rt.rows + nav + 2 * WH_ROUTER_MAX_ACTIVE + 1;
     WH_HIP(c->rtr.ensure(words * 4, false));
     float* x = c->rtr.as<float>();
-    float* logits = x + rt.cols;
-    uint32_t* av = reinterpret_cast<uint32_t*>(logits + rt.rows);
+    float* logits = x + rt.cols;  // [2 * rows]: scores and selection keys
+    uint32_t* av = reinterpret_cast<uint32_t*>(logits + 2 * rt.rows);
     uint32_t* ids = av + nav;
     float* sc = reinterpret_cast<float*>(ids + WH_ROUTER_MAX_ACTIVE);
     uint32_t* cnt = reinterpret_cast<uint32_t*>(sc + WH_ROUTER_MAX_ACTIVE);
@@ -1800,6 +1806,7 @@ int wh_route_experts_async(wh_ctx* c, uint32_t layer, const float* x_dev, size_t
                            const uint32_t* available_dev, size_t n_available, const wh_route_options* opts,
                            uint32_t* ids_dev, float* scores_dev, uint32_t* count_dev) {
     if (!c || !opts || !x_dev || !ids_dev || !scores_dev || !count_dev) return WH_INVALID_ARGUMENT;
+    if ((uintptr_t)x_dev & 15) return WH_INVALID_ARGUMENT;  // x is read in 16-byte pieces
     if (active > WH_ROUTER_MAX_ACTIVE || n_available > WH_ROUTER_MAX_ROWS) return WH_UNSUPPORTED;
     std::lock_guard<std::mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
@@ -1813,12 +1820,12 @@ int wh_route_experts_async(wh_ctx* c, uint32_t layer, const float* x_dev, size_t
         sa.out_ids = ids_dev;
         sa.out_scores = scores_dev;
         sa.out_count = count_dev;
-        k_router_select<<<1, 64, 0, c->stream>>>(sa);
+        k_router_select<<<1, 256, 0, c->stream>>>(sa);
         WH_HIP(hipGetLastError());
         return WH_OK;
     }
     WH_TRY(router_prepare(rt, *opts, hidden_len, active, available_dev ? n_available : rt.rows, &sa));
-    WH_HIP(c->rtr.ensure((rt.cols + rt.rows + 2 * WH_ROUTER_MAX_ACTIVE + 1) * 4, false));
+    WH_HIP(c->rtr.ensure((rt.cols + 2 * rt.rows + 2 * WH_ROUTER_MAX_ACTIVE + 1) * 4, false));
     float* logits = c->rtr.as<float>() + rt.cols;
     return router_launch(c, rt, sa, x_dev, available_dev, logits, ids_dev, scores_dev, count_dev);
 }
