@@ -158,11 +158,13 @@ struct wh_fp8_args {
     float* y;               // row_end - row_start
     uint32_t* status;
     uint32_t cols, scale_cols, row_group, row_start, row_end;
+    uint32_t row_group_shift;     // log2(row_group) when it is a power of two (split-K path), else 32
     uint32_t x_stride, y_stride;  // batch strides (multi-input variant)
     // row groups with their own input (wo_a, E/compute.rs:4244-4258): rows
     // row_start + [g*x_group_rows, (g+1)*x_group_rows) read x + g*x_group_stride;
-    // 0 = one input for all rows (split-K path only, x_group_rows % 4 == 0)
-    uint32_t x_group_rows, x_group_stride;
+    // 0 = one input for all rows (split-K path only: a power of two, at least
+    // WH_FP8_SK_ROWS); x_group_shift = log2(x_group_rows), 32 for one input
+    uint32_t x_group_rows, x_group_stride, x_group_shift;
 };
 
 template <bool kSpecial, bool kScaleU8>
@@ -271,85 +273,119 @@ __global__ void __launch_bounds__(256) k_fp8_gemv(wh_fp8_args a) {
     }
 }
 
-// Split-K path (col_group == 128, groups % 8 == 0): 256 threads = 4 rows x 8
-// column segments x 8 AVX lanes; wave w runs row w.  Each thread forms
-// g0 + g1 for its segment's groups into LDS, then the 8 lane threads of
-// each row run the reference's sequential acc = fma(g0 + g1, scale, acc)
-// over all groups - the same operations in the same order as the one-thread
-// row, with 8x the threads in flight.  kGps = groups per segment when the
-// segment's weights fit in registers (4 for 4096 columns), else 0.
+// Split-K path (col_group == 128, groups % 8 == 0): 256 threads = 4 waves x
+// 8 column segments x 8 AVX lanes; wave w runs rows 2w and 2w + 1 of the
+// workgroup's WH_FP8_SK_ROWS, so every x value read from LDS serves two rows.
+// Each thread forms g0 + g1 for its segment's groups of both rows into LDS,
+// then wave 0 runs the reference's sequential acc = fma(g0 + g1, scale, acc)
+// over all groups for the 8 rows x 8 lanes - the same operations in the same
+// order as the one-thread row.  kGps = groups per segment when the segment's
+// weights fit in registers (4 for 4096 columns), else 0.
+#define WH_FP8_SK_ROWS 8u
 template <bool kSpecial, bool kScaleU8, int kGps>
 __global__ void __launch_bounds__(256) k_fp8_gemv_sk(wh_fp8_args a) {
+    constexpr uint32_t kR = WH_FP8_SK_ROWS / 4;  // rows per wave
     extern __shared__ __align__(16) float lds[];
     const uint32_t batch = blockIdx.y;
+    const uint32_t rb = blockIdx.x * WH_FP8_SK_ROWS;  // first row, relative to row_start
     const float* x = a.x + (size_t)batch * a.x_stride +
-                     (a.x_group_rows ? (size_t)(blockIdx.x * 4 / a.x_group_rows) * a.x_group_stride : 0);
-    const uint32_t lane = threadIdx.x & 7, seg = (threadIdx.x >> 3) & 7, rr = threadIdx.x >> 6;
-    const uint32_t row = a.row_start + blockIdx.x * 4 + rr;
-    const bool active = row < a.row_end;
-    const uint32_t srow_idx = active ? row : a.row_start;
-    const uint32_t G = a.cols >> 7, gps = G >> 3, gbeg = seg * gps;
-    const uint4* wp = (const uint4*)(a.w + (size_t)srow_idx * a.cols) + lane;  // group g at wp[8 g]
-    const uint32_t sbase = (srow_idx / a.row_group) * a.scale_cols;
+                     (a.x_group_shift < 32 ? (size_t)(rb >> a.x_group_shift) * a.x_group_stride : 0);
+    const uint32_t lane = threadIdx.x & 7, seg = (threadIdx.x >> 3) & 7;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // rows and scale rows stay scalar
+    // widths known at compile time for kGps > 0 (cols = 1024 kGps)
+    const uint32_t cols = kGps > 0 ? 1024u * kGps : a.cols;
+    const uint32_t G = cols >> 7, gps = G >> 3, gbeg = seg * gps;
     float* xs = lds;
-    float* gsum = lds + a.cols + (rr * 8 + lane) * G;  // per (row, lane): g0 + g1 of every group
-    float* scl = lds + a.cols + 32 * G + rr * G;        // per row: the group scales
-    const float4* xp = (const float4*)xs + lane * 4;   // group g at xp[32 g]
-    // staging loads (x chunk, this lane's share of the row's scales) go out
+    float* gsum = lds + cols;     // [8 rows][8 lanes][G]: g0 + g1 of every group
+    float* scl = gsum + 64 * G;   // [8 rows][G]: the group scales
+    const float4* xp = (const float4*)xs + lane * 4;  // group g at xp[32 g]
+    const uint4* wp[kR];
+    uint32_t sbase[kR];
+#pragma unroll
+    for (uint32_t j = 0; j < kR; ++j) {
+        const uint32_t r = a.row_start + rb + wv * kR + j;
+        const uint32_t rc = r < a.row_end ? r : a.row_start;  // rows past the end load row_start
+        wp[j] = (const uint4*)(a.w + (size_t)rc * cols) + lane;  // group g at wp[8 g]
+        sbase[j] = (rc >> a.row_group_shift) * a.scale_cols;
+    }
+    // staging loads (x chunk, this lane's share of the rows' scales) go out
     // before the weight loads, so waiting for them never waits for weights
     wh_stage_f32_fp8 st;
-    wh_stage_f32_fp8_load(st, x, a.cols, threadIdx.x);
+    wh_stage_f32_fp8_load(st, x, cols, threadIdx.x);
     const uint32_t sg = seg * 8 + lane;  // scales g = sg, sg + 64, ...
-    float sv = sg < G ? wh_fp8_scale<kSpecial, kScaleU8>(a.scales, sbase + sg) : 0.0f;
+    float sv[kR];
+#pragma unroll
+    for (uint32_t j = 0; j < kR; ++j) sv[j] = sg < G ? wh_fp8_scale<kSpecial, kScaleU8>(a.scales, sbase[j] + sg) : 0.0f;
+    auto stage_rest = [&]() {
+        wh_stage_f32_fp8_store(st, xs);
+        for (uint32_t q = threadIdx.x + 256; q < cols / 16; q += 256) {  // cols > 4096
+            wh_stage_f32_fp8 s2;
+            wh_stage_f32_fp8_load(s2, x, cols, q);
+            wh_stage_f32_fp8_store(s2, xs);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kR; ++j) {
+            float* srow = scl + (wv * kR + j) * G;
+            if (sg < G) srow[sg] = sv[j];
+            for (uint32_t g = sg + 64; g < G; g += 64) srow[g] = wh_fp8_scale<kSpecial, kScaleU8>(a.scales, sbase[j] + g);
+        }
+    };
     if constexpr (kGps > 0) {
-        uint4 w[kGps];
+        uint4 w[kR][kGps];
 #pragma unroll
-        for (int i = 0; i < kGps; ++i) w[i] = wp[8 * (gbeg + i)];
+        for (uint32_t j = 0; j < kR; ++j)
+#pragma unroll
+            for (int i = 0; i < kGps; ++i) w[j][i] = wp[j][8 * (gbeg + i)];
         __builtin_amdgcn_sched_barrier(0);
-        wh_stage_f32_fp8_store(st, xs);
-        if (sg < G) scl[sg] = sv;
-        for (uint32_t q = threadIdx.x + 256; q < a.cols / 16; q += 256) {
-            wh_stage_f32_fp8 s2;
-            wh_stage_f32_fp8_load(s2, x, a.cols, q);
-            wh_stage_f32_fp8_store(s2, xs);
-        }
-        for (uint32_t g = sg + 64; g < G; g += 64) scl[g] = wh_fp8_scale<kSpecial, kScaleU8>(a.scales, sbase + g);
+        stage_rest();
         __syncthreads();
+        // a thread's kGps sums of one row are adjacent in LDS: computed in
+        // registers, then stored as vectors
+        float gs[kR][kGps];
 #pragma unroll
-        for (int i = 0; i < kGps; ++i) gsum[gbeg + i] = wh_fp8_lane_gsum<kSpecial>(w[i], xp + 32 * (gbeg + i));
-    } else {
-        wh_stage_f32_fp8_store(st, xs);
-        for (uint32_t q = threadIdx.x + 256; q < a.cols / 16; q += 256) {
-            wh_stage_f32_fp8 s2;
-            wh_stage_f32_fp8_load(s2, x, a.cols, q);
-            wh_stage_f32_fp8_store(s2, xs);
+        for (int i = 0; i < kGps; ++i)
+#pragma unroll
+            for (uint32_t j = 0; j < kR; ++j) gs[j][i] = wh_fp8_lane_gsum<kSpecial>(w[j][i], xp + 32 * (gbeg + i));
+#pragma unroll
+        for (uint32_t j = 0; j < kR; ++j) {
+            float* dst = gsum + ((wv * kR + j) * 8 + lane) * G + gbeg;
+            if constexpr (kGps % 4 == 0) {
+#pragma unroll
+                for (int i = 0; i < kGps; i += 4) *(float4*)(dst + i) = make_float4(gs[j][i], gs[j][i + 1], gs[j][i + 2], gs[j][i + 3]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < kGps; ++i) dst[i] = gs[j][i];
+            }
         }
-        for (uint32_t g = sg; g < G; g += 64) scl[g] = wh_fp8_scale<kSpecial, kScaleU8>(a.scales, sbase + g);
+    } else {
+        stage_rest();
         __syncthreads();
-        for (uint32_t g = gbeg; g < gbeg + gps; ++g) gsum[g] = wh_fp8_lane_gsum<kSpecial>(wp[8 * g], xp + 32 * g);
+        for (uint32_t g = gbeg; g < gbeg + gps; ++g)
+#pragma unroll
+            for (uint32_t j = 0; j < kR; ++j)
+                gsum[((wv * kR + j) * 8 + lane) * G + g] = wh_fp8_lane_gsum<kSpecial>(wp[j][8 * g], xp + 32 * g);
     }
     __syncthreads();
-    if (seg != 0) return;
+    if (threadIdx.x >= 64) return;  // wave 0: row rl = thread / 8, AVX lane thread % 8
+    const uint32_t rl = threadIdx.x >> 3, ln = threadIdx.x & 7;
+    const float* gs = gsum + (rl * 8 + ln) * G;
+    const float* sc = scl + rl * G;
     float acc = 0.0f;
-    if constexpr (kGps > 0) {  // G = 8 kGps known: all operands read as vectors first
-        float4 gv[2 * kGps], sv4[2 * kGps];
+    if constexpr (kGps > 0) {  // G = 8 kGps known
 #pragma unroll
         for (int i = 0; i < 2 * kGps; ++i) {
-            gv[i] = ((const float4*)gsum)[i];
-            sv4[i] = ((const float4*)scl)[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 2 * kGps; ++i) {
-            acc = __builtin_fmaf(gv[i].x, sv4[i].x, acc);
-            acc = __builtin_fmaf(gv[i].y, sv4[i].y, acc);
-            acc = __builtin_fmaf(gv[i].z, sv4[i].z, acc);
-            acc = __builtin_fmaf(gv[i].w, sv4[i].w, acc);
+            const float4 g = ((const float4*)gs)[i], s = ((const float4*)sc)[i];
+            acc = __builtin_fmaf(g.x, s.x, acc);
+            acc = __builtin_fmaf(g.y, s.y, acc);
+            acc = __builtin_fmaf(g.z, s.z, acc);
+            acc = __builtin_fmaf(g.w, s.w, acc);
         }
     } else {
-        for (uint32_t g = 0; g < G; ++g) acc = __builtin_fmaf(gsum[g], scl[g], acc);
+        for (uint32_t g = 0; g < G; ++g) acc = __builtin_fmaf(gs[g], sc[g], acc);
     }
     const float sum = wh_hsum8(acc) + 0.0f;  // + tail (0 for col_group % 16 == 0)
-    if (active && lane == 0) {
+    const uint32_t row = a.row_start + rb + rl;
+    if (row < a.row_end && ln == 0) {
         a.y[(size_t)batch * a.y_stride + (row - a.row_start)] = sum;
         if (!(fabsf(sum) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
     }

@@ -326,14 +326,20 @@ hipError_t kernel_setup_once(int device) {
 }
 
 // ------------------------------------------------------------ FP8 launch
-// LDS of a split-K FP8 workgroup: staged x, the 4 x 8 x groups partial sums
-// and the 4 rows' group scales.
-size_t fp8_sk_lds(size_t cols) { return sizeof(float) * (cols + 36 * (cols / 128)); }
+// LDS of a split-K FP8 workgroup: staged x, the 8 rows x 8 lanes x groups
+// partial sums and the 8 rows' group scales.
+size_t fp8_sk_lds(size_t cols) { return sizeof(float) * (cols + 72 * (cols / 128)); }
 
 // Whether launch_fp8 takes the split-K path for this tensor (which also
 // supports per-row-group inputs).
+bool is_pow2(size_t v) { return v && !(v & (v - 1)); }
+uint32_t log2_of(size_t v) {
+    uint32_t k = 0;
+    while ((size_t(1) << k) < v) ++k;
+    return k;
+}
 bool fp8_split_k(const Tensor& t) {
-    return t.fast && (t.cols / 128) % 8 == 0 && fp8_sk_lds(t.cols) <= g_max_lds;
+    return t.fast && (t.cols / 128) % 8 == 0 && fp8_sk_lds(t.cols) <= g_max_lds && is_pow2(t.rows / t.scale_rows);
 }
 
 // x_group_rows / x_group_stride: row groups with their own input (split-K
@@ -350,16 +356,19 @@ int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x,
     a.cols = (uint32_t)t.cols;
     a.scale_cols = (uint32_t)t.scale_cols;
     a.row_group = (uint32_t)(t.rows / t.scale_rows);
+    a.row_group_shift = is_pow2(a.row_group) ? log2_of(a.row_group) : 32u;
     a.row_start = (uint32_t)r0;
     a.row_end = (uint32_t)r1;
     a.x_stride = (uint32_t)x_stride;
     a.y_stride = (uint32_t)y_stride;
     a.x_group_rows = (uint32_t)x_group_rows;
     a.x_group_stride = (uint32_t)x_group_stride;
-    if (x_group_rows && (!fp8_split_k(t) || x_group_rows % 4)) return WH_UNSUPPORTED;
+    a.x_group_shift = x_group_rows ? log2_of(x_group_rows) : 32u;
+    if (x_group_rows && (!fp8_split_k(t) || !is_pow2(x_group_rows) || x_group_rows < WH_FP8_SK_ROWS))
+        return WH_UNSUPPORTED;
     bool u8 = t.scale_fmt == WH_SCALE_UE8M0;
     if (fp8_split_k(t)) {
-        dim3 grid((unsigned)((r1 - r0 + 3) / 4), (unsigned)n_batch);
+        dim3 grid((unsigned)((r1 - r0 + WH_FP8_SK_ROWS - 1) / WH_FP8_SK_ROWS), (unsigned)n_batch);
         const size_t lds = fp8_sk_lds(t.cols);
         // groups per segment known at compile time for the common widths
         const size_t gps = t.cols / 128 / 8;
@@ -2009,7 +2018,7 @@ int wh_fp8_gemv_batch_async(wh_ctx* c, const wh_gemv_desc* descs, size_t n) {
         // spaced inputs and back-to-back outputs goes out as one launch
         size_t j = i + 1;
         const ptrdiff_t xs = j < n ? descs[j].x_dev - d.x_dev : 0;
-        if (fp8_split_k(*t) && rows % 4 == 0 && xs >= 0) {
+        if (fp8_split_k(*t) && is_pow2(rows) && rows >= WH_FP8_SK_ROWS && xs >= 0) {
             while (j < n && descs[j].weight == d.weight && descs[j].row_start == descs[j - 1].row_end &&
                    descs[j].row_end - descs[j].row_start == rows && descs[j].x_dev - descs[j - 1].x_dev == xs &&
                    descs[j].y_dev == descs[j - 1].y_dev + rows)
