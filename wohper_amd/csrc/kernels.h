@@ -1042,9 +1042,15 @@ __device__ __forceinline__ void wh_moe_routed_sum(const wh_moe_args& a, uint32_t
     const uint32_t r_out = rb * 32 + threadIdx.x;
     const size_t t0 = (size_t)tok * a.n_experts * a.hidden;
     const uint32_t nr = a.n_experts - a.has_shared;  // routed experts
+    // every expert's row is requested before any is used: one round trip
+    // to the coherent level instead of one per expert
+    float yv[WH_MAX_EXPERTS];
+#pragma unroll
+    for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i)
+        yv[i] = i < a.n_experts ? wh_load_coherent(a.y + t0 + (size_t)i * a.hidden + r_out) : 0.0f;
     float o = 0.0f;
     if (nr == 1) {
-        o = wh_load_coherent(a.y + t0 + r_out);
+        o = yv[0];
     } else if (nr > 1) {
         // valid_route_weight_sum (E/compute.rs:2014-2030)
         float sum = 0.0f;
@@ -1056,15 +1062,21 @@ __device__ __forceinline__ void wh_moe_routed_sum(const wh_moe_args& a, uint32_t
         }
         if (sum <= 1.1920929e-07f) valid = false;
         const float uniform = 1.0f / (float)nr;
-        for (uint32_t i = 0; i < nr; ++i) {
-            float w = valid ? a.route_w[i] / sum : uniform;
-            float p = wh_load_coherent(a.y + t0 + (size_t)i * a.hidden + r_out) * w;
-            o = o + p;
+#pragma unroll
+        for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i) {
+            if (i < nr) {
+                float w = valid ? a.route_w[i] / sum : uniform;
+                float p = yv[i] * w;
+                o = o + p;
+            }
         }
     }
     if (a.has_shared) {
         // hidden = shared(x); hidden += routed (E/compute.rs:1929-1941)
-        const float sh = wh_load_coherent(a.y + t0 + (size_t)nr * a.hidden + r_out);
+        float sh = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i)
+            if (i == nr) sh = yv[i];
         o = nr == 0 ? sh : sh + o;
     }
     a.out[(size_t)tok * a.hidden + r_out] = o;

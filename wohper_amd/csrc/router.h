@@ -367,9 +367,25 @@ __global__ void __launch_bounds__(64) k_router_bf16(const uint16_t* __restrict__
     if (threadIdx.x == 0) last = wh_arrive(counter) == gridDim.x - 1;
     last = __shfl(last, 0, 64);
     if (!last) return;
-    for (uint32_t i = threadIdx.x; i < a.rows; i += 64) {
-        sc[i] = wh_load_coherent(a.logits + i);
-        sk[i] = wh_load_coherent(a.logits + a.rows + i);
+    // all published scores and keys are requested before the first LDS
+    // store, so the wave waits for one round trip, not one per pass
+    constexpr uint32_t kPass = WH_ROUTER_MAX_ROWS / 64;
+    float rs[kPass], rk[kPass];
+#pragma unroll
+    for (uint32_t k = 0; k < kPass; ++k) {
+        const uint32_t i = threadIdx.x + 64 * k;
+        if (i < a.rows) {
+            rs[k] = wh_load_coherent(a.logits + i);
+            rk[k] = wh_load_coherent(a.logits + a.rows + i);
+        }
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kPass; ++k) {
+        const uint32_t i = threadIdx.x + 64 * k;
+        if (i < a.rows) {
+            sc[i] = rs[k];
+            sk[i] = rk[k];
+        }
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
