@@ -41,7 +41,7 @@ KERNELS = {False: ("k_moe_gateup_sk<2>", "k_moe_down_sk"), True: ("k_moe_gateup<
 # HBM bytes per gate/up launch: rocprofv3 FETCH_SIZE and WRITE_SIZE KiB per
 # dispatch, scaled by what the same counters read for a 268,435,456-byte copy
 # (FETCH x2.00, WRITE x1.00); see profiles/.  None: not measured.
-GATEUP_TRAFFIC_BYTES = {False: round((26_242.0 * 2 + 48.0) * 1024), True: round((26_273.1 * 2 + 48.0) * 1024)}
+GATEUP_TRAFFIC_BYTES = {False: round((26_245.0 * 2 + 48.0) * 1024), True: round((26_278.6 * 2 + 48.0) * 1024)}
 FP8_BYTES = 4096 * 4096 + 32 * 32 * 4 + 4096 * 4 + 4096 * 4
 
 
