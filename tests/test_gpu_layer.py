@@ -78,6 +78,34 @@ def test_fp8_synthetic_store_and_batched_gemv(ctx, oracle):
     ctx.device_free(y_dev)
 
 
+def test_fp8_row_group_sizes(ctx, oracle):
+    """Runs of equal row groups with their own inputs merge into one launch
+    when the group is a power of two of at least 8 rows (8, 64), and go out
+    one launch per group otherwise (4, 24); every group matches the oracle."""
+    rows, cols = 1024, 2048
+    scales = wl.fp8_block_scales(9, rows, cols)
+    t = ctx.store_fp8_synthetic(rows, cols, 13, wl.fp8_stream(0, 4), scales)
+    w = wl.synth_fp8_host(ctx.lib, 13, wl.fp8_stream(0, 4), rows, cols)
+    rng = np.random.default_rng(9)
+    for gsize, n, r0 in ((8, 6, 40), (64, 3, 128), (24, 5, 8), (4, 7, 3)):
+        xg = rng.standard_normal((n, cols)).astype(np.float32)
+        x_dev = ctx.device_alloc(xg.nbytes)
+        y_dev = ctx.device_alloc(n * gsize * 4)
+        ctx.to_device(x_dev, xg)
+        ctx.fp8_gemv_batch_async([(t, r0 + gsize * g, r0 + gsize * (g + 1), x_dev + g * cols * 4,
+                                   y_dev + g * gsize * 4) for g in range(n)])
+        ctx.synchronize()
+        y = np.empty(n * gsize, np.float32)
+        ctx.from_device(y, y_dev)
+        for g in range(n):
+            a, b = r0 + gsize * g, r0 + gsize * (g + 1)
+            want = oracle.fp8_gemv(w, rows, cols, scales, rows // 128, cols // 128, xg[g], a, b)
+            assert np.array_equal(bits(y[gsize * g:gsize * (g + 1)]), bits(want)), (gsize, g)
+        ctx.device_free(x_dev)
+        ctx.device_free(y_dev)
+    ctx.release(t)
+
+
 @pytest.mark.parametrize("n_routed", [6, 1, 0])
 def test_shared_plus_routed_bit_exact(ctx, oracle, n_routed):
     seed = 4
