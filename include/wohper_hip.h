@@ -392,7 +392,11 @@ int wh_routed_experts_async(wh_ctx* ctx, const wh_expert_route* routes, size_t n
 /* Several device-pointer FP8 GEMVs enqueued by one call, in order (a decode
  * layer's projections: the reference calls gemv_fp8_e4m3_ue8m0_rows once per
  * projection and per wo_a group, E/compute.rs:4005-4265).  Every descriptor
- * is validated before the first launch. */
+ * is validated before the first launch.  A run of consecutive descriptors on
+ * one tensor with equal, adjacent row groups (a power of two of at least 8
+ * rows), evenly spaced inputs and back-to-back outputs goes out as one
+ * launch; any other descriptor is a launch of its own.  Results are the
+ * same either way. */
 typedef struct {
     wh_tensor weight;
     size_t row_start, row_end;
