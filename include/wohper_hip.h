@@ -45,7 +45,9 @@ enum wh_status {
     WH_OUT_OF_MEMORY = 11,
     WH_HIP_ERROR = 12,
     WH_INVALID_ARGUMENT = 13,
-    WH_NON_FINITE_INPUT = 14,      /* an activation block held inf/NaN */
+    WH_NON_FINITE_INPUT = 14,      /* reserved: inputs with inf/NaN follow the reference's
+                                      act-quant (NaN -> -480 x scale; an inf makes the
+                                      block scale inf and surfaces as NonFiniteOutput) */
     WH_UNSUPPORTED = 15,
     /* ZCBLK01 block errors: ComputeError (E/compute.rs:330-344); the
      * reference's Display text of the error is in wh_last_error() */
@@ -81,7 +83,7 @@ int wh_init(int device, wh_ctx** out);
 int wh_shutdown(wh_ctx* ctx);
 const char* wh_status_string(int status);
 /* Blocks until the stream drains; returns the first deferred kernel status
- * (WH_NON_FINITE_OUTPUT / WH_NON_FINITE_INPUT) raised since the last call. */
+ * (WH_NON_FINITE_OUTPUT, WH_NOT_RESIDENT) raised since the last call. */
 int wh_synchronize(wh_ctx* ctx);
 /* The context's hipStream_t, for callers that interleave their own work. */
 void* wh_stream(wh_ctx* ctx);

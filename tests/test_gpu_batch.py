@@ -201,3 +201,30 @@ def test_batch_mfma_small_shapes(ctx, oracle):
 def test_batch_mfma_real_shapes(ctx, oracle):
     worst = _mfma_case(ctx, oracle, 45, 8, wl.HIDDEN, wl.INTER, 34, 24, DEFAULT_MFMA_MIN)
     print(f"worst MFMA matvec |diff| / tolerance: {worst:.3f}")
+
+
+def test_batch_nonfinite_inputs_follow_the_reference(ctx, oracle):
+    """A NaN input quantizes to -480 x its block scale (E/compute.rs:2504-2545)
+    and the batch stays finite and bit-exact against the oracle, with every
+    expert kept off MFMA (-480 has no E4M3 code); an inf makes its block's
+    scale infinite and the batch ends in NonFiniteOutput.  The next finite
+    batch takes MFMA items again."""
+    layer, n_exp, hidden, inter, seed, npos = 46, 12, 512, 256, 35, 48
+    _store(ctx, layer, n_exp, hidden, inter, seed)
+    ids, sc, x = wl.zipf_batch_routes(seed=seed, n_tokens=npos, n_experts=n_exp, hidden=hidden)
+    experts = _host(ctx, layer, ids, seed, hidden, inter)
+    ctx.set_moe_mfma_min(8)
+    xn = x.copy()
+    xn[3, [0, 70, 71]] = np.nan
+    xn[9, 64:128] = np.nan
+    got = ctx.moe_batch(layer, ids, sc, xn)
+    assert int(ctx.debug_moe_batch_read(4, 8, np.uint32)[4]) == 0  # no MFMA item ran
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(bits(got), bits(oracle.moe_batch(experts, ids, sc, xn)))
+    xi = x.copy()
+    xi[5, 200] = np.inf
+    with pytest.raises(wohper_amd.DeepSeekV4KernelError) as e:
+        ctx.moe_batch(layer, ids, sc, xi)
+    assert e.value.name == "NonFiniteOutput"
+    ctx.moe_batch(layer, ids, sc, x)
+    assert int(ctx.debug_moe_batch_read(4, 8, np.uint32)[4]) > 0

@@ -137,9 +137,9 @@ def test_fast_single_expert_forward(ctx, oracle):
                  wl.HIDDEN, wl.INTER)
 
 
-def test_fast_wide_scales_and_nonfinite_input(ctx, oracle):
+def test_fast_wide_scales(ctx, oracle):
     """UE8M0 exponents over [-20, 6] and x over six decades stay within
-    tolerance; a NaN input is reported, not returned."""
+    tolerance."""
     seed = 23
     ctx.store_expert_synthetic(19, 1, wl.HIDDEN, wl.INTER, seed, 107, 133)
     rng = np.random.default_rng(seed)
@@ -147,10 +147,44 @@ def test_fast_wide_scales_and_nonfinite_input(ctx, oracle):
     got = ctx.routed_experts([(19, 1, 1.0)], x)
     ex = [wl.synth_expert_host(ctx.lib, seed, 19, 1, scale_lo=107, scale_hi=133)]
     _check_token(ctx, oracle, ex, [1.0], x, got, 0, 1, 0, wl.HIDDEN, wl.INTER)
-    x[100] = np.nan
-    with pytest.raises(wohper_amd.DeepSeekV4KernelError) as e:
-        ctx.routed_experts([(19, 1, 1.0)], x)
-    assert e.value.name == "NonFiniteInput"
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_nonfinite_inputs_follow_the_reference(ctx, oracle, exact):
+    """fp8_act_quant_dequant_in_place (E/compute.rs:2504-2545) inside the
+    expert forward: NaN inputs quantize to -480 x the block scale and the
+    token stays finite (checked against the oracle: bit for bit in exact
+    mode, per matvec within tolerance in split-K mode); an inf makes its
+    block's scale infinite, and the forward ends in NonFiniteOutput
+    (E/deepseek_v4.rs:597-599), as the oracle does."""
+    ctx.set_exact_numerics(exact)
+    seed = 24
+    ctx.store_expert_synthetic(19, 2, wl.HIDDEN, wl.INTER, seed)
+    ctx.store_expert_synthetic(19, 3, wl.HIDDEN, wl.INTER, seed)
+    ex = [wl.synth_expert_host(ctx.lib, seed, 19, e) for e in (2, 3)]
+    routes, w = [(19, 2, 0.6), (19, 3, 0.4)], [0.6, 0.4]
+    x = np.random.default_rng(seed).standard_normal(wl.HIDDEN).astype(np.float32)
+    x[[5, 64, 700, 701, 4095]] = np.nan   # several blocks, two NaN in one
+    x[128:192] = np.nan                   # a block of NaN only: amax 0 -> scale of 1e-4
+    got = ctx.routed_experts(routes, x)
+    assert np.all(np.isfinite(got))
+    want = _oracle_forward(oracle, ex, w, x, 0)
+    if exact:
+        assert np.array_equal(bits(got), bits(want))
+    else:
+        _check_token(ctx, oracle, ex, w, x, got, 0, 1, 0, wl.HIDDEN, wl.INTER)
+    for bad in (np.inf, -np.inf):
+        xi = x.copy()
+        xi[300] = bad
+        with pytest.raises(oracle.OracleError) as oe:
+            oracle.fp4_expert_forward(*ex[0], xi)
+        assert oe.value.code == 8  # NonFiniteOutput
+        with pytest.raises(wohper_amd.DeepSeekV4KernelError) as e:
+            ctx.routed_experts(routes, xi)
+        assert e.value.name == "NonFiniteOutput"
+    # the context recovers: the next finite token is exact again
+    got = ctx.routed_experts(routes, np.nan_to_num(x))
+    assert np.all(np.isfinite(got))
 
 
 def test_exact_switch_restores_bit_exact(ctx, oracle):

@@ -64,7 +64,7 @@ STATUS_NAMES = {
 }
 
 # codes whose wh_last_error() text says what failed
-_DETAILED = {2, 11, 12, 13, 16, 17, 18, 19, 20, 21, 22}
+_DETAILED = {2, 7, 11, 12, 13, 15, 16, 17, 18, 19, 20, 21, 22}
 
 SCALE_UE8M0 = 0
 SCALE_F32 = 1

@@ -855,9 +855,14 @@ __device__ __forceinline__ void wh_xq_stage_load(wh_xq_stage& st, const void* x,
 // Act-quant of the 64-block the thread's quad covers (E/compute.rs:2504-2521,
 // block 64): q = the E4M3 values before the block scale sc.  All lanes take
 // part in the block's amax; returns false for a thread without columns.
-// Non-finite input is reported through the status word.
+// Non-finite inputs keep the reference's f32 semantics: the amax skips NaN
+// (f32::max), a NaN quantizes to the lowest sorted-LUT entry, -480
+// (partition_point over NaN is 0), and an infinite amax makes the scale
+// infinite, so every value of that block dequantizes to a non-finite value
+// and the matvecs downstream report NonFiniteOutput.  *nonfinite is set when
+// the block held an inf or NaN (the batch path keeps such inputs off MFMA).
 __device__ __forceinline__ bool wh_xq_quant16(const wh_xq_stage& st, bool bf16, const uint32_t* log2_thr,
-                                              uint32_t* status, float (&q)[16], float& sc) {
+                                              float (&q)[16], float& sc, bool* nonfinite = nullptr) {
     float v[16];
     if (bf16) {
         const uint32_t w[8] = {st.raw[0].x, st.raw[0].y, st.raw[0].z, st.raw[0].w,
@@ -882,25 +887,29 @@ __device__ __forceinline__ bool wh_xq_quant16(const wh_xq_stage& st, bool bf16, 
     for (int i = 0; i < 16; ++i) {
         float m = fabsf(v[i]);
         bad |= !(m <= 3.4028235e38f);
-        amax = fmaxf(amax, m);
+        amax = fmaxf(amax, m);  // a NaN operand is skipped
     }
     amax = fmaxf(amax, wh_dpp_quad_swap1(amax));  // the quad holds one 64-block
     amax = fmaxf(amax, wh_dpp_quad_swap2(amax));
     if (!st.on) return false;
-    if (bad) atomicOr(status, WH_ST_NONFINITE_INPUT);
-    if (!(amax <= 3.4028235e38f)) amax = 1.0f;
-    const int k = wh_aq_scale_exp(amax, log2_thr);
-    const float inv = wh_pow2f(-k);
-    sc = wh_pow2f(k);
+    if (nonfinite) *nonfinite = bad;
+    const bool inf_scale = !(amax <= 3.4028235e38f);
+    const int k = inf_scale ? 0 : wh_aq_scale_exp(amax, log2_thr);
+    // v / inf is v * 0 for every v: +-0 for finite v, NaN for +-inf
+    const float inv = inf_scale ? 0.0f : wh_pow2f(-k);
+    sc = inf_scale ? __uint_as_float(0x7f800000u) : wh_pow2f(k);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) q[i] = wh_e4m3_round(wh_clamp448_finite(v[i] * inv));
+    for (int i = 0; i < 16; ++i) {
+        const float t = v[i] * inv;
+        q[i] = t != t ? -480.0f : wh_e4m3_round(wh_clamp448_finite(t));
+    }
     return true;
 }
 // The same, result written to LDS in FP4 lane order (scaled values).
 __device__ __forceinline__ void wh_xq_stage_store(const wh_xq_stage& st, bool bf16, float* xs,
-                                                  const uint32_t* log2_thr, uint32_t* status) {
+                                                  const uint32_t* log2_thr) {
     float q[16], sc;
-    if (!wh_xq_quant16(st, bf16, log2_thr, status, q, sc)) return;
+    if (!wh_xq_quant16(st, bf16, log2_thr, q, sc)) return;
     // columns c0 + j: group c0/32, lane j % 8, k = 2*((c0/16) & 1) + j/8
     const uint32_t g = st.c0 >> 5, h = (st.c0 >> 4) & 1;
 #pragma unroll
@@ -909,6 +918,16 @@ __device__ __forceinline__ void wh_xq_stage_store(const wh_xq_stage& st, bool bf
 
 __device__ __forceinline__ float wh_dpp_row_shl8(float v) {  // lane i <- lane i+8 (within 16)
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x108, 0xf, 0xf, false));
+}
+
+// The first gate/up workgroup of a token clears the token's routed-sum
+// arrival counters, which the down launch after it counts with: whatever
+// the counters' memory held before, every call starts from zero.
+__device__ __forceinline__ void wh_moe_clear_arrivals(const wh_moe_args& a, uint32_t tok) {
+    if (blockIdx.x != 0) return;
+    uint32_t* cnt = a.cnt_y + (size_t)tok * (a.hidden >> 5);
+    for (uint32_t i = threadIdx.x; i < (a.hidden >> 5); i += blockDim.x)
+        __hip_atomic_store(cnt + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Gate/up: grid (n_experts * inter / 16, n_tokens), 256 threads = 32 rows =
@@ -935,6 +954,7 @@ __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
     const bool bf16 = a.x_is_bf16 != 0;
     const void* xt = bf16 ? (const void*)((const uint16_t*)a.x + (size_t)tok * a.hidden)
                           : (const void*)((const float*)a.x + (size_t)tok * a.hidden);
+    wh_moe_clear_arrivals(a, tok);
     wh_thr_stage ts;
     wh_thr_stage_load(ts);
     wh_exp_stage es;
@@ -953,7 +973,7 @@ __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
         wh_thr_stage_store(ts, thr);
         wh_exp_stage_store(es, exp_tab);
         __syncthreads();
-        wh_xq_stage_store(xst, bf16, xs, thr, a.status);
+        wh_xq_stage_store(xst, bf16, xs, thr);
         wh_s8_stage_store<kBlk>(ss, s8row, lane);
         __syncthreads();
         acc = wh_fp4_ring_dot<kBlk, kRing>(r, wrow, xs, s8row, lane);
@@ -964,7 +984,7 @@ __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
         for (uint32_t i = threadIdx.x; i < (a.hidden >> 4); i += 256) {
             wh_xq_stage xst;
             wh_xq_stage_load(xst, xt, bf16, a.hidden, i);
-            wh_xq_stage_store(xst, bf16, xs, thr, a.status);
+            wh_xq_stage_store(xst, bf16, xs, thr);
         }
         wh_s8_stage_rt(srow, G, s8row, lane);
         __syncthreads();

@@ -7,11 +7,11 @@
 // shared expert out_p = shared(x_p) + acc_p (E/compute.rs:1838-1852).
 //
 // Launch sequence (one stream):
+//   k_moe_batch_quant    act-quant (block 64) of every position's input
 //   k_moe_batch_pack     one workgroup: weights, the per-expert token lists
 //                        (counts, offsets, placement), the used experts in
 //                        ascending id, their work order, each position's
 //                        accumulation order
-//   k_moe_batch_quant    act-quant (block 64) of every position's input
 //   k_moe_batch_gateup   persistent: (expert, row tile) items from a queue,
 //                        gate and up matvecs of every slot
 //   k_moe_batch_swiglu   SwiGLU of every slot
@@ -52,7 +52,9 @@ struct wh_batch_args {
     uint32_t* uorder;              // [S] used-expert indices, most slots first
     uint32_t* acc_order;           // [A] per position: its route slots by ascending expert id
     uint32_t* meta;                // [0] used experts, [1] routes valid, [2]/[3] work queues
-                                   // of gate/up and down, [4] experts on MFMA items
+                                   // of gate/up and down, [4] experts on MFMA items, [6] an
+                                   // input block held an inf or NaN (set by the quant of x,
+                                   // read and cleared by the pack)
     float* xq;                     // [npos][hidden] act-quantized inputs (column order)
     uint8_t* xq8;                  // [npos][hidden] their E4M3 codes, MFMA group order
     uint8_t* xs8;                  // [npos][hidden / 32] E8M0 scale bytes (x 1/8)
@@ -106,12 +108,16 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
     __shared__ uint32_t slot_of[WH_BATCH_MAX_ASSIGN];
     __shared__ uint32_t cnt[WH_BATCH_MAX_TABLE], off[WH_BATCH_MAX_TABLE], ucnt[WH_BATCH_MAX_TABLE];
     __shared__ uint32_t tot[4];
-    __shared__ uint32_t bad, n_mfma;
+    __shared__ uint32_t bad, n_mfma, mfma_min;
     const uint32_t A = a.npos * a.topk, S = A + a.has_shared * a.npos, tid = threadIdx.x;
     const uint32_t n_ids = a.n_table + a.has_shared;  // the shared expert is id n_table
     if (tid == 0) {
         bad = 0;
         n_mfma = 0;
+        // an input block with an inf or NaN (flagged by k_moe_batch_quant,
+        // which runs first) keeps every expert on the exact items
+        mfma_min = a.meta[6] ? 0u : a.mfma_min;
+        a.meta[6] = 0;
     }
     for (uint32_t e = tid; e < n_ids; e += 256) cnt[e] = 0;
     // ids, checked against the table
@@ -174,7 +180,7 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
                 a.uexp[u] = e;
                 a.uoff[u] = o;
                 ucnt[u] = c4[j];
-                if (a.mfma_min && c4[j] >= a.mfma_min) atomicAdd(&n_mfma, 1u);
+                if (mfma_min && c4[j] >= mfma_min) atomicAdd(&n_mfma, 1u);
                 ++u;
             }
         }
@@ -232,11 +238,14 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
 // in column order, their E4M3 codes in MFMA group order (per 32-col group,
 // byte 4c + k holds column c + 8k) and one E8M0 byte per group: the block
 // scale divided by 8, which takes the x8 of the FP4 integer LUT values.
-// Grid: rows * n / 4096 blocks of 256 threads.
+// Non-finite inputs follow the reference (wh_xq_quant16); a block that held
+// one sets *nonfinite (when given), and the pack then keeps every expert on
+// the exact items: -480 (a NaN's code) and an infinite scale have no E4M3 /
+// E8M0 encoding.  Grid: rows * n / 4096 blocks of 256 threads.
 __global__ void __launch_bounds__(256) k_moe_batch_quant(const void* __restrict__ src, uint32_t src_bf16,
                                                          uint32_t rows, uint32_t n, float* __restrict__ q32,
                                                          uint8_t* __restrict__ q8, uint8_t* __restrict__ s8,
-                                                         uint32_t* status, uint32_t report_nonfinite) {
+                                                         uint32_t* nonfinite) {
     __shared__ uint32_t thr[256];
     wh_thr_stage ts;
     wh_thr_stage_load(ts);
@@ -251,40 +260,12 @@ __global__ void __launch_bounds__(256) k_moe_batch_quant(const void* __restrict_
     const void* row = bf16 ? (const void*)((const uint16_t*)src + base) : (const void*)((const float*)src + base);
     wh_xq_stage st;
     wh_xq_stage_load(st, row, bf16, on ? n : 0u, t);
-    float v[16];
-    if (bf16) {
-        const uint32_t w[8] = {st.raw[0].x, st.raw[0].y, st.raw[0].z, st.raw[0].w,
-                               st.raw[1].x, st.raw[1].y, st.raw[1].z, st.raw[1].w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            v[2 * j] = __uint_as_float(w[j] << 16);
-            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            v[4 * j] = __uint_as_float(st.raw[j].x);
-            v[4 * j + 1] = __uint_as_float(st.raw[j].y);
-            v[4 * j + 2] = __uint_as_float(st.raw[j].z);
-            v[4 * j + 3] = __uint_as_float(st.raw[j].w);
-        }
-    }
-    float amax = 0.0f;
+    float q[16], sc = 1.0f;
     bool bad = false;
+    if (!wh_xq_quant16(st, bf16, thr, q, sc, &bad)) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const float m = fabsf(v[j]);
-        bad |= !(m <= 3.4028235e38f);
-        amax = fmaxf(amax, m);
+        for (int j = 0; j < 16; ++j) q[j] = 0.0f;  // rows past the end: the DPP partner below still reads
     }
-    amax = fmaxf(amax, wh_dpp_quad_swap1(amax));
-    amax = fmaxf(amax, wh_dpp_quad_swap2(amax));
-    if (!(amax <= 3.4028235e38f)) amax = 1.0f;
-    const int k = wh_aq_scale_exp(amax, thr);
-    const float inv = wh_pow2f(-k), sc = wh_pow2f(k);
-    float q[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) q[j] = wh_e4m3_round(wh_clamp448_finite(v[j] * inv));
     // codes: column c + 8k of the group sits at byte 4c + k; this thread
     // holds k = 2h + (j >> 3) for c = j & 7 (h = which half of the group)
     const uint32_t h = t & 1;
@@ -300,14 +281,17 @@ __global__ void __launch_bounds__(256) k_moe_batch_quant(const void* __restrict_
         dw[j] = h ? (recv | (pair[4 + j] << 16)) : (pair[j] | (recv << 16));
     }
     if (!on) return;
-    if (bad && report_nonfinite) atomicOr(status, WH_ST_NONFINITE_INPUT);
+    if (bad && nonfinite) atomicOr(nonfinite, 1u);
     float4* d32 = (float4*)(q32 + base + 16 * t);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         d32[j] = make_float4(q[4 * j] * sc, q[4 * j + 1] * sc, q[4 * j + 2] * sc, q[4 * j + 3] * sc);
     const uint32_t g = t >> 1;  // 32-col group of the row
     *(uint4*)(q8 + base + 32 * g + 16 * h) = make_uint4(dw[0], dw[1], dw[2], dw[3]);
-    if (!h) s8[(size_t)(on ? r : 0) * (n / 32) + g] = (uint8_t)(127 + k - 3);
+    // sc = 2^k: E8M0 byte 127 + k - 3 is its biased exponent - 3 (0xFF for an
+    // infinite scale, never read: such a batch runs no MFMA item)
+    const uint32_t be = (__float_as_uint(sc) >> 23) & 0xffu;
+    if (!h) s8[(size_t)r * (n / 32) + g] = (uint8_t)(be == 0xffu ? 0xffu : be - 3u);
 }
 
 // SwiGLU (E/deepseek_v4.rs:590-594) of the gate and up matvecs, one value

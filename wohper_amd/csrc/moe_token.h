@@ -239,7 +239,7 @@ __global__ void __launch_bounds__(128 * kSl) k_moe_xquant(const void* x, uint32_
     wh_thr_stage_store(ts, thr);
     __syncthreads();
     float q[16], sc;
-    if (!wh_xq_quant16(xst, bf16, thr, status, q, sc)) return;
+    if (!wh_xq_quant16(xst, bf16, thr, q, sc)) return;
     const uint32_t c0 = xst.c0, g = c0 >> 5, hh = (c0 >> 4) & 1, b = g >> 3, j = g & 7;
     uint32_t* d = xq + (size_t)tok * (kCols / 2) + b * 128 + 2 * j + hh;  // 2 halves per dword
 #pragma unroll
@@ -263,6 +263,7 @@ __global__ void __launch_bounds__(128 * kSl) k_moe_gateup_sk(wh_moe_args a) {
     wh_exp_stage es;
     wh_exp_stage_load(es);
     const uint32_t tok = blockIdx.y;
+    wh_moe_clear_arrivals(a, tok);
     const uint32_t per_e = a.inter / kRows;
     const uint32_t e = blockIdx.x / per_e;
     const uint32_t rb = blockIdx.x - e * per_e;

@@ -30,6 +30,8 @@ namespace {
 
 constexpr int kFp8 = 1, kFp4 = 2;
 
+
+
 struct Tensor {
     int kind = 0;
     uint8_t* w = nullptr;  // device
@@ -39,6 +41,7 @@ struct Tensor {
     bool fast = false;     // resident lane layout (else original row-major)
     bool special = false;  // FP8 codes 0x7F/0xFF present
     size_t bytes = 0;
+    size_t w_alloc = 0, s_alloc = 0;  // arena bytes behind w and s
 };
 
 struct Expert {
@@ -70,48 +73,111 @@ struct Router {
 };
 constexpr int kGateBf16 = 1, kGateBf16Rows = 2, kGateFp8 = 3;
 
-// Bump allocator over large hipMalloc chunks: tensors of a weight store are
-// never freed individually in the hot path, and a 150 GB stack would
-// otherwise need ~10^5 separate allocations.
+// HBM of the weight store: large hipMalloc chunks (a 150 GB stack would
+// otherwise need ~10^5 separate allocations), sub-allocated in 256-byte
+// units.  Released ranges go back to a free list - best fit, split, merged
+// with free neighbours of the same chunk - so replacing experts, or storing
+// and releasing transient tensors, reuses the same bytes.
 struct Arena {
+    struct Range {
+        size_t size;
+        uint32_t chunk;
+    };
     std::vector<void*> chunks;
-    uint8_t* cur = nullptr;
-    size_t left = 0;
-    size_t total = 0;
+    std::map<uintptr_t, Range> free_at;            // start -> free range
+    std::multimap<size_t, uintptr_t> free_sizes;   // size -> start
+    size_t total = 0;  // bytes of all chunks
+    size_t live = 0;   // bytes handed out
     static constexpr size_t kChunk = size_t(4) << 30;
 
+    static size_t round(size_t n) { return (n + 255) & ~size_t(255); }
+
+    void insert(uintptr_t p, Range r) {
+        free_at[p] = r;
+        free_sizes.emplace(r.size, p);
+    }
+    void erase(std::map<uintptr_t, Range>::iterator it) {
+        auto rng = free_sizes.equal_range(it->second.size);
+        for (auto s = rng.first; s != rng.second; ++s)
+            if (s->second == it->first) {
+                free_sizes.erase(s);
+                break;
+            }
+        free_at.erase(it);
+    }
+    // Returns [p, p + r.size) of chunk r.chunk to the list, merged with
+    // free neighbours of the same chunk.
+    void give_back(uintptr_t p, Range r) {
+        auto next = free_at.lower_bound(p);
+        if (next != free_at.end() && next->second.chunk == r.chunk && p + r.size == next->first) {
+            r.size += next->second.size;
+            erase(next);
+        }
+        auto it = free_at.lower_bound(p);
+        if (it != free_at.begin()) {
+            auto prev = std::prev(it);
+            if (prev->second.chunk == r.chunk && prev->first + prev->second.size == p) {
+                p = prev->first;
+                r.size += prev->second.size;
+                erase(prev);
+            }
+        }
+        insert(p, r);
+    }
+    uint32_t chunk_of(uintptr_t p) const {
+        // chunks are few (one per 4 GiB): a scan is enough
+        for (size_t i = 0; i < chunk_sizes.size(); ++i) {
+            const uintptr_t b = (uintptr_t)chunks[i];
+            if (p >= b && p < b + chunk_sizes[i]) return (uint32_t)i;
+        }
+        return UINT32_MAX;
+    }
+    std::vector<size_t> chunk_sizes;
+
     hipError_t alloc(size_t n, void** out) {
-        n = (n + 255) & ~size_t(255);
-        if (n > left) {
+        n = round(std::max<size_t>(n, 1));
+        auto best = free_sizes.lower_bound(n);
+        if (best == free_sizes.end()) {
             size_t sz = std::max(n, kChunk);
             void* p = nullptr;
             hipError_t e = hipMalloc(&p, sz);
-            if (e != hipSuccess) {
-                // retry with an exact-size chunk before giving up
-                if (sz != n && hipMalloc(&p, n) == hipSuccess) {
-                    (void)hipGetLastError();
-                    chunks.push_back(p);
-                    total += n;
-                    *out = p;
-                    return hipSuccess;
-                }
-                return e;
+            if (e != hipSuccess && sz != n) {  // retry with an exact-size chunk before giving up
+                (void)hipGetLastError();
+                sz = n;
+                e = hipMalloc(&p, sz);
             }
+            if (e != hipSuccess) return e;
             chunks.push_back(p);
-            cur = (uint8_t*)p;
-            left = sz;
+            chunk_sizes.push_back(sz);
             total += sz;
+            insert((uintptr_t)p, Range{sz, (uint32_t)(chunks.size() - 1)});
+            best = free_sizes.lower_bound(n);
         }
-        *out = cur;
-        cur += n;
-        left -= n;
+        const uintptr_t p = best->second;
+        auto it = free_at.find(p);
+        const Range r = it->second;
+        erase(it);
+        if (r.size > n) insert(p + n, Range{r.size - n, r.chunk});
+        live += n;
+        *out = (void*)p;
         return hipSuccess;
+    }
+    // Returns a range alloc() handed out (n as passed to alloc).
+    void free(void* ptr, size_t n) {
+        if (!ptr) return;
+        n = round(std::max<size_t>(n, 1));
+        const uint32_t ch = chunk_of((uintptr_t)ptr);
+        if (ch == UINT32_MAX) return;
+        give_back((uintptr_t)ptr, Range{n, ch});
+        live -= std::min(live, n);
     }
     void release_all() {
         for (void* p : chunks) (void)hipFree(p);
         chunks.clear();
-        cur = nullptr;
-        left = total = 0;
+        chunk_sizes.clear();
+        free_at.clear();
+        free_sizes.clear();
+        total = live = 0;
     }
 };
 
@@ -128,7 +194,10 @@ struct Scratch {
         hipError_t e = hipMalloc(&p, bytes);
         if (e != hipSuccess) return e;
         if (zero) {
+            // the null-stream fill does not order against the library's
+            // non-blocking stream: wait for it here
             e = hipMemset(p, 0, bytes);
+            if (e == hipSuccess) e = hipDeviceSynchronize();
             if (e != hipSuccess) return e;
         }
         n = bytes;
@@ -173,7 +242,6 @@ struct wh_ctx {
     std::unordered_map<wh_tensor, Tensor> tensors;
     std::map<std::pair<uint32_t, uint32_t>, Expert> experts;
     wh_tensor next_id = 1;
-    size_t device_bytes = 0;
     uint32_t* status = nullptr;  // device status word
     uint32_t* status_host = nullptr;
     Scratch x_in, y_out, h, ybuf, cnt_y, tmp, batch, routes, bout, gu, xq;
@@ -250,8 +318,35 @@ Tensor* find_tensor(wh_ctx* c, wh_tensor t) {
 int alloc_device(wh_ctx* c, size_t n, void** out) {
     hipError_t e = c->arena.alloc(n, out);
     if (e != hipSuccess) return hip_status(e);
-    c->device_bytes += n;
     return WH_OK;
+}
+
+// The weight and scale buffers of a new tensor, recorded for its release.
+int alloc_tensor(wh_ctx* c, Tensor& t, size_t wbytes, size_t sbytes) {
+    void* wd = nullptr;
+    void* sd = nullptr;
+    WH_TRY(alloc_device(c, wbytes, &wd));
+    const int st = alloc_device(c, sbytes, &sd);
+    if (st != WH_OK) {
+        c->arena.free(wd, wbytes);
+        return st;
+    }
+    t.w = (uint8_t*)wd;
+    t.s = sd;
+    t.w_alloc = wbytes;
+    t.s_alloc = sbytes;
+    return WH_OK;
+}
+
+// Drops a tensor handle and returns its HBM to the arena.  Work already
+// queued on the library stream may still read the bytes; every later write
+// to a reused range (uploads, fills) is queued behind it on the same stream.
+void drop_tensor(wh_ctx* c, wh_tensor id) {
+    auto it = c->tensors.find(id);
+    if (it == c->tensors.end()) return;
+    c->arena.free(it->second.w, it->second.w_alloc);
+    c->arena.free(it->second.s, it->second.s_alloc);
+    c->tensors.erase(it);
 }
 
 int upload(wh_ctx* c, void* dst, const void* src, size_t n) {
@@ -489,15 +584,64 @@ bool expert_fast(const ExpertView& v) {
            wh_moe_wg_lds(v.w1->cols) <= g_max_lds && wh_moe_wg_lds(v.w1->rows) <= g_max_lds;
 }
 
+// Working memory of the fast routed-expert kernels for one call.
+struct MoeBufs {
+    float* h = nullptr;       // [T][n][inter] SwiGLU outputs
+    float* y = nullptr;       // [T][n][hidden] per-expert outputs
+    uint32_t* cnt = nullptr;  // [T][hidden / 32] routed-sum arrivals (cleared by gate/up)
+    uint32_t* xq = nullptr;   // split-K only: [T][hidden / 2] input codes, then [T][hidden / 64] scales
+    float* gu = nullptr;      // test capture of gate and up, or null
+};
+
+// Split-K kernels (summation order freed) serve the model's shapes unless
+// the context asks for the reference's order.
+bool moe_split_k(const wh_ctx* c, size_t hidden, size_t inter) {
+    return !c->exact && (hidden == 2048 || hidden == 4096) && inter == 2048;
+}
+
+// Bytes of each MoeBufs region (each rounded up to 256).
+struct MoeSizes {
+    size_t h, y, cnt, xq;
+    size_t total() const { return h + y + cnt + xq; }
+};
+MoeSizes moe_sizes(size_t n, size_t n_tokens, size_t hidden, size_t inter, bool sk) {
+    auto r = [](size_t b) { return (b + 255) & ~size_t(255); };
+    MoeSizes z;
+    z.h = r(n_tokens * n * inter * sizeof(float));
+    z.y = r(n_tokens * n * hidden * sizeof(float));
+    z.cnt = r(n_tokens * (hidden / 32) * sizeof(uint32_t));
+    z.xq = sk ? r(n_tokens * (hidden * 2 + hidden / 16)) : 0;
+    return z;
+}
+
+// The context's own (growing) buffers.
+int moe_bufs_ctx(wh_ctx* c, size_t n, size_t n_tokens, size_t hidden, size_t inter, MoeBufs* b) {
+    const MoeSizes z = moe_sizes(n, n_tokens, hidden, inter, moe_split_k(c, hidden, inter));
+    WH_HIP(c->h.ensure(z.h, false));
+    WH_HIP(c->ybuf.ensure(z.y, false));
+    WH_HIP(c->cnt_y.ensure(z.cnt, true));
+    b->h = c->h.as<float>();
+    b->y = c->ybuf.as<float>();
+    b->cnt = c->cnt_y.as<uint32_t>();
+    if (z.xq) {
+        WH_HIP(c->xq.ensure(z.xq, false));
+        b->xq = c->xq.as<uint32_t>();
+    }
+    if (c->capture_gu) {
+        WH_HIP(c->gu.ensure(n_tokens * n * 2 * inter * sizeof(float), false));
+        b->gu = c->gu.as<float>();
+    }
+    return WH_OK;
+}
+
 // Launches the fast routed-expert kernels for n_tokens rows of x sharing one
 // route list.  stages: bit 0 = gate/up + SwiGLU, bit 1 = down + routed sum.
+// record: keep the call's sizes for the debug reads of the context buffers.
 int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n, bool has_shared,
-                    const void* x_dev, int x_bf16, size_t n_tokens, float* out_dev, unsigned stages) {
+                    const void* x_dev, int x_bf16, size_t n_tokens, float* out_dev, unsigned stages,
+                    const MoeBufs& bufs, bool record) {
     const size_t hidden = ev[0].w1->cols, inter = ev[0].w1->rows;
     if (((uintptr_t)x_dev & 15) || ((uintptr_t)out_dev & 3)) return WH_INVALID_ARGUMENT;
-    WH_HIP(c->h.ensure(n_tokens * n * inter * sizeof(float), false));
-    WH_HIP(c->ybuf.ensure(n_tokens * n * hidden * sizeof(float), false));
-    WH_HIP(c->cnt_y.ensure(n_tokens * (hidden / 32) * sizeof(uint32_t), true));
     wh_moe_args a;
     std::memset(&a, 0, sizeof a);
     for (size_t i = 0; i < n; ++i) {
@@ -516,24 +660,19 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
     a.n_tokens = (uint32_t)n_tokens;
     a.x = x_dev;
     a.x_is_bf16 = x_bf16 ? 1u : 0u;
-    a.h = c->h.as<float>();
-    a.y = c->ybuf.as<float>();
+    a.h = bufs.h;
+    a.y = bufs.y;
     a.out = out_dev;
-    a.cnt_y = c->cnt_y.as<uint32_t>();
+    a.cnt_y = bufs.cnt;
     a.status = c->status;
-    if (c->capture_gu) {
-        WH_HIP(c->gu.ensure(n_tokens * n * 2 * inter * sizeof(float), false));
-        a.gu = c->gu.as<float>();
-    }
-    c->tok_last_n = n, c->tok_last_tokens = n_tokens, c->tok_last_hidden = hidden, c->tok_last_inter = inter;
-    // split-K kernels (summation order freed) for the model's shapes unless
-    // the context asks for the reference's order
-    const bool sk = !c->exact && (hidden == 2048 || hidden == 4096) && inter == 2048;
+    a.gu = bufs.gu;
+    if (record)
+        c->tok_last_n = n, c->tok_last_tokens = n_tokens, c->tok_last_hidden = hidden, c->tok_last_inter = inter;
+    const bool sk = moe_split_k(c, hidden, inter);
     if (stages & 1) {
         if (sk) {
             // x act-quantized once per token, then the split-K gate/up
-            WH_HIP(c->xq.ensure(n_tokens * (hidden * 2 + hidden / 16), false));
-            uint32_t* xq = c->xq.as<uint32_t>();
+            uint32_t* xq = bufs.xq;
             float* xk = (float*)(xq + n_tokens * hidden / 2);
             a.xq = xq;
             a.xk = xk;
@@ -567,6 +706,19 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
     return WH_OK;
 }
 
+// Shape rules shared by the routed-expert entry points; *fast: every expert
+// takes the fast kernels.
+int moe_shapes(const ExpertView* ev, size_t n, bool* fast) {
+    const size_t hidden = ev[0].w1->cols, inter = ev[0].w1->rows, osz = ev[0].w2->rows;
+    bool f = osz == hidden && n <= WH_MAX_EXPERTS;
+    for (size_t i = 0; i < n; ++i) {
+        if (ev[i].w1->cols != hidden || ev[i].w1->rows != inter || ev[i].w2->rows != osz) return WH_INVALID_SHAPE;
+        f = f && expert_fast(ev[i]);
+    }
+    *fast = f;
+    return WH_OK;
+}
+
 // Routed experts for n_tokens rows of x (all with the same route list).
 // x_dev: device input (f32 or bf16).  out_dev: n_tokens x hidden f32.
 // ev[0..n): the experts; with has_shared the last one is the shared expert
@@ -574,14 +726,13 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
 int moe_forward(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n, bool has_shared,
                 const void* x_dev, int x_bf16, size_t n_tokens, float* out_dev) {
     const size_t hidden = ev[0].w1->cols, inter = ev[0].w1->rows, osz = ev[0].w2->rows;
-    bool fast = osz == hidden;
-    for (size_t i = 0; i < n; ++i) {
-        if (ev[i].w1->cols != hidden || ev[i].w1->rows != inter || ev[i].w2->rows != osz)
-            return WH_INVALID_SHAPE;
-        fast = fast && expert_fast(ev[i]);
+    bool fast = false;
+    WH_TRY(moe_shapes(ev, n, &fast));
+    if (fast) {
+        MoeBufs bufs;
+        WH_TRY(moe_bufs_ctx(c, n, n_tokens, hidden, inter, &bufs));
+        return moe_launch_fast(c, ev, route_w, n, has_shared, x_dev, x_bf16, n_tokens, out_dev, 3u, bufs, true);
     }
-    if (fast && n <= WH_MAX_EXPERTS)
-        return moe_launch_fast(c, ev, route_w, n, has_shared, x_dev, x_bf16, n_tokens, out_dev, 3u);
     // Generic composition (any shape the reference accepts), one token at a time.
     if (x_bf16) return WH_UNSUPPORTED;
     const size_t per = hidden + 3 * inter + n * osz + n;
@@ -788,14 +939,15 @@ int batch_bufs(wh_ctx* c, size_t npos, size_t slots, size_t hidden, size_t inter
         off += align256(bytes);
         return o;
     };
-    const size_t o_w = take(slots * 4), o_so = take(slots * 4), o_ue = take(slots * 4), o_uo = take((slots + 1) * 4),
-                 o_ur = take(slots * 4), o_ac = take(slots * 4), o_me = take(16 * 4),
+    // meta first: its flag word keeps its place whatever the sizes
+    const size_t o_me = take(16 * 4), o_w = take(slots * 4), o_so = take(slots * 4), o_ue = take(slots * 4),
+                 o_uo = take((slots + 1) * 4), o_ur = take(slots * 4), o_ac = take(slots * 4),
                  o_xq = take(npos * hidden * 4), o_g = take(slots * inter * 4), o_u = take(slots * inter * 4),
                  o_h = take(slots * inter * 4),
                  o_y = take(slots * hidden * 4),
                  o_hq = take(slots * inter * 4), o_xq8 = take(npos * hidden), o_xs8 = take(npos * hidden / 32),
                  o_hq8 = take(slots * inter), o_hs8 = take(slots * inter / 32);
-    WH_HIP(c->batch.ensure(off, false));
+    WH_HIP(c->batch.ensure(off, true));  // zeroed when (re)allocated: meta's flag starts clear
     uint8_t* base = c->batch.as<uint8_t>();
     b->wgt = (float*)(base + o_w);
     b->sorted = (uint32_t*)(base + o_so);
@@ -881,9 +1033,11 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         const size_t max_used = std::min(slots, (size_t)t.n + (shared ? 1 : 0));
         const unsigned gg = (unsigned)std::min<size_t>(grid_g, max_used * (inter / 16));
         const unsigned gd = (unsigned)std::min<size_t>(grid_d, max_used * (hidden / 32));
-        k_moe_batch_pack<<<1, 256, 0, c->stream>>>(a);
+        // the quant of x runs first: the pack keeps every expert off MFMA when
+        // an input block held an inf or NaN
         k_moe_batch_quant<<<(unsigned)((n * hidden / 16 + 255) / 256), 256, 0, c->stream>>>(
-            a.x, a.x_is_bf16, (uint32_t)n, (uint32_t)hidden, a.xq, a.xq8, a.xs8, c->status, 1u);
+            a.x, a.x_is_bf16, (uint32_t)n, (uint32_t)hidden, a.xq, a.xq8, a.xs8, a.meta + 6);
+        k_moe_batch_pack<<<1, 256, 0, c->stream>>>(a);
         if (hidden == 4096) k_moe_batch_gateup<16><<<gg, 256, lds_g, c->stream>>>(a);
         else k_moe_batch_gateup<0><<<gg, 256, lds_g, c->stream>>>(a);
         c->moe_last_slots = npos <= chunk ? slots : 0;
@@ -893,7 +1047,7 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         k_moe_batch_swiglu<<<(unsigned)((slots * inter + 255) / 256), 256, 0, c->stream>>>(
             a.g, a.u, a.h, (uint32_t)(slots * inter));
         k_moe_batch_quant<<<(unsigned)((slots * inter / 16 + 255) / 256), 256, 0, c->stream>>>(
-            a.h, 0u, (uint32_t)slots, (uint32_t)inter, a.hq, a.hq8, a.hs8, c->status, 0u);
+            a.h, 0u, (uint32_t)slots, (uint32_t)inter, a.hq, a.hq8, a.hs8, nullptr);
         if (inter == 2048) k_moe_batch_down<8><<<gd, 256, lds_d, c->stream>>>(a);
         else k_moe_batch_down<0><<<gd, 256, lds_d, c->stream>>>(a);
         k_moe_batch_accumulate<<<dim3((unsigned)((hidden + 255) / 256), (unsigned)n), 256, 0, c->stream>>>(a);
@@ -1027,12 +1181,7 @@ int store_fp4_upload(wh_ctx* c, const uint8_t* packed, size_t packed_len, const 
     t.fast = (cols / scale_cols == 32) && cols % 256 == 0 && wh_fp4_wg_lds(cols) <= g_max_lds &&
              rows <= UINT32_MAX && cols <= UINT32_MAX;
     t.bytes = rows * row_bytes + rows * scale_cols;
-    void* wd = nullptr;
-    void* sd = nullptr;
-    WH_TRY(alloc_device(c, rows * row_bytes, &wd));
-    WH_TRY(alloc_device(c, rows * scale_cols, &sd));
-    t.w = (uint8_t*)wd;
-    t.s = sd;
+    WH_TRY(alloc_tensor(c, t, rows * row_bytes, rows * scale_cols));
     if (t.fast) {
         const size_t piece = size_t(64) << 20;
         const size_t chunk_rows = std::max<size_t>(1, piece / row_bytes);
@@ -1084,7 +1233,7 @@ int block_status(const whqb::Error& e) {
 void register_owned_expert(wh_ctx* c, uint32_t layer, uint32_t expert, const wh_tensor ids[3]) {
     auto it = c->experts.find({layer, expert});
     if (it != c->experts.end() && it->second.owned)
-        for (wh_tensor old : {it->second.w1, it->second.w3, it->second.w2}) c->tensors.erase(old);
+        for (wh_tensor old : {it->second.w1, it->second.w3, it->second.w2}) drop_tensor(c, old);
     c->experts[{layer, expert}] = Expert{ids[0], ids[1], ids[2], true};
     c->tables[layer].valid = false;
 }
@@ -1253,6 +1402,16 @@ int router_launch(wh_ctx* c, const Router& rt, wh_router_sel sa, const float* x,
     return WH_OK;
 }
 
+// Drops a layer's router and returns its HBM to the arena.
+void drop_router(wh_ctx* c, uint32_t layer) {
+    auto it = c->routers.find(layer);
+    if (it == c->routers.end()) return;
+    if (it->second.fp8) drop_tensor(c, it->second.fp8);
+    c->arena.free(it->second.bf16, it->second.rows * it->second.cols * 2);
+    c->arena.free(it->second.bias, it->second.rows * sizeof(float));
+    c->routers.erase(it);
+}
+
 // Parses a ZCBLK01 expert block and makes its three FP4 projections
 // resident under (layer, expert).  The caller holds c->mu.
 int store_block_locked(wh_ctx* c, uint32_t layer, uint32_t expert, const uint8_t* block, size_t len, bool pinned,
@@ -1268,7 +1427,7 @@ int store_block_locked(wh_ctx* c, uint32_t layer, uint32_t expert, const uint8_t
         int st = store_fp4_upload(c, block + p[m].weight_off, p[m].weight_len, block + p[m].scale_off,
                                   p[m].scale_len, p[m].rows, p[m].cols, p[m].scale_cols, pinned, &ids[m]);
         if (st != WH_OK) {
-            for (int k = 0; k < m; ++k) c->tensors.erase(ids[k]);
+            for (int k = 0; k < m; ++k) drop_tensor(c, ids[k]);
             return st;
         }
     }
@@ -1399,12 +1558,7 @@ int wh_store_fp8(wh_ctx* c, const uint8_t* weight, size_t weight_len, size_t row
     t.fast = (cols / scale_cols == 128) && cols * 4 <= g_max_lds;
     for (size_t i = 0; i < rows * cols && !t.special; ++i) t.special = (weight[i] & 0x7f) == 0x7f;
     t.bytes = rows * cols + sbytes;
-    void* wd = nullptr;
-    void* sd = nullptr;
-    WH_TRY(alloc_device(c, rows * cols, &wd));
-    WH_TRY(alloc_device(c, sbytes, &sd));
-    t.w = (uint8_t*)wd;
-    t.s = sd;
+    WH_TRY(alloc_tensor(c, t, rows * cols, sbytes));
     const size_t chunk_rows = std::max<size_t>(1, (size_t(64) << 20) / cols);
     WH_HIP(c->stage_in.ensure(std::min(rows, chunk_rows) * cols));
     for (size_t r = 0; r < rows; r += chunk_rows) {
@@ -1440,7 +1594,7 @@ int wh_store_expert(wh_ctx* c, uint32_t layer, uint32_t expert, wh_tensor w1, wh
     auto it = c->experts.find({layer, expert});
     if (it != c->experts.end() && it->second.owned)
         for (wh_tensor old : {it->second.w1, it->second.w3, it->second.w2})
-            if (old != w1 && old != w3 && old != w2) c->tensors.erase(old);
+            if (old != w1 && old != w3 && old != w2) drop_tensor(c, old);
     c->experts[{layer, expert}] = Expert{w1, w3, w2};
     c->tables[layer].valid = false;
     return WH_OK;
@@ -1471,12 +1625,11 @@ int wh_store_expert_synthetic(wh_ctx* c, uint32_t layer, uint32_t expert, size_t
         t.scale_cols = t.cols / 32;
         t.fast = true;
         t.bytes = t.rows * t.cols / 2 + t.rows * t.scale_cols;
-        void* wd = nullptr;
-        void* sd = nullptr;
-        WH_TRY(alloc_device(c, t.rows * t.cols / 2, &wd));
-        WH_TRY(alloc_device(c, t.rows * t.scale_cols, &sd));
-        t.w = (uint8_t*)wd;
-        t.s = sd;
+        const int st = alloc_tensor(c, t, t.rows * t.cols / 2, t.rows * t.scale_cols);
+        if (st != WH_OK) {
+            for (int k = 0; k < m; ++k) drop_tensor(c, ids[k]);
+            return st;
+        }
         uint64_t stream = ((uint64_t)layer << 40) ^ ((uint64_t)expert << 8) ^ (uint64_t)m;
         size_t words = t.rows * (t.cols / 256) * 32;
         size_t work = std::max(words, t.rows * t.scale_cols);
@@ -1658,7 +1811,7 @@ int wh_store_router(wh_ctx* c, uint32_t layer, const uint8_t* block, size_t bloc
     }
     if (!have_gate) {  // Ok(None): the engine falls back to its own routing
         std::lock_guard<std::mutex> lk(c->mu);
-        c->routers.erase(layer);
+        drop_router(c, layer);
         return WH_OK;
     }
     Router rt;
@@ -1764,7 +1917,7 @@ int wh_store_router(wh_ctx* c, uint32_t layer, const uint8_t* block, size_t bloc
         WH_TRY(h2d(c, rt.bias, reinterpret_cast<const uint8_t*>(bias.data()), rt.rows * sizeof(float), false));
     }
     auto old = c->routers.find(layer);
-    if (old != c->routers.end() && old->second.fp8) c->tensors.erase(old->second.fp8);
+    drop_router(c, layer);
     c->routers[layer] = std::move(rt);
     if (found) *found = 1;
     return WH_OK;
@@ -1862,12 +2015,7 @@ int wh_store_fp8_synthetic(wh_ctx* c, size_t rows, size_t cols, uint64_t seed, u
     if (!t.fast) return WH_UNSUPPORTED;
     const size_t sbytes = scale_rows * scale_cols * sizeof(float);
     t.bytes = rows * cols + sbytes;
-    void* wd = nullptr;
-    void* sd = nullptr;
-    WH_TRY(alloc_device(c, rows * cols, &wd));
-    WH_TRY(alloc_device(c, sbytes, &sd));
-    t.w = (uint8_t*)wd;
-    t.s = sd;
+    WH_TRY(alloc_tensor(c, t, rows * cols, sbytes));
     const size_t n = rows * cols;
     k_synth_fp8<<<(unsigned)((n + 255) / 256), 256, 0, c->stream>>>(t.w, (uint32_t)rows, (uint32_t)cols, seed, stream);
     WH_HIP(hipGetLastError());
@@ -1880,8 +2028,7 @@ int wh_store_release(wh_ctx* c, wh_tensor t) {
     std::lock_guard<std::mutex> lk(c->mu);
     auto it = c->tensors.find(t);
     if (it == c->tensors.end()) return WH_NOT_RESIDENT;
-    // arena memory is reclaimed at shutdown; the handle stops resolving now
-    c->tensors.erase(it);
+    drop_tensor(c, t);
     for (auto& kv : c->tables) kv.second.valid = false;
     return WH_OK;
 }
@@ -1889,7 +2036,7 @@ int wh_store_release(wh_ctx* c, wh_tensor t) {
 int wh_store_usage(wh_ctx* c, size_t* bytes, size_t* tensors, size_t* experts) {
     if (!c) return WH_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lk(c->mu);
-    if (bytes) *bytes = c->device_bytes;
+    if (bytes) *bytes = c->arena.live;
     if (tensors) *tensors = c->tensors.size();
     if (experts) *experts = c->experts.size();
     return WH_OK;
@@ -1971,6 +2118,15 @@ int wh_fp8_gemv(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end, const 
                              values_out);
 }
 
+// Pointer rules of the device-pointer FP8 entry points: the lane-layout
+// kernels stage x with 16-byte loads, so x must be 16-byte aligned for them
+// (any float alignment for the generic row-major kernel); y takes floats.
+static int fp8_ptr_check(const Tensor& t, const float* x, const float* y) {
+    if (t.fast && ((uintptr_t)x & 15)) return WH_INVALID_ARGUMENT;
+    if (((uintptr_t)x & 3) || ((uintptr_t)y & 3)) return WH_INVALID_ARGUMENT;
+    return WH_OK;
+}
+
 int wh_fp8_gemv_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end,
                       const float* x_dev, float* y_dev) {
     if (!c || !x_dev || !y_dev) return WH_INVALID_ARGUMENT;
@@ -1979,6 +2135,8 @@ int wh_fp8_gemv_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end,
     if (!t) return WH_NOT_RESIDENT;
     if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
     if (row_start >= row_end || row_end > t->rows) return WH_INVALID_SHAPE;
+    WH_TRY(fp8_ptr_check(*t, x_dev, y_dev));
+    WH_HIP(hipSetDevice(c->device));
     return launch_fp8(c, *t, row_start, row_end, x_dev, y_dev, 1, t->cols, row_end - row_start);
 }
 
@@ -1992,7 +2150,10 @@ int wh_fp8_gemv_multi_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row
     if (n == 0 || row_start >= row_end || row_end > t->rows) return WH_INVALID_SHAPE;  // E/compute.rs:6400-6430
     if (x_stride < t->cols) return WH_INPUT_TOO_SMALL;
     if (y_stride < row_end - row_start) return WH_OUTPUT_TOO_SMALL;
-    if (((uintptr_t)x_dev & 15) || (x_stride & 3)) return WH_INVALID_ARGUMENT;
+    // the kernels take 32-bit strides and the inputs on grid.y
+    if (x_stride > UINT32_MAX || y_stride > UINT32_MAX || n > 65535) return WH_UNSUPPORTED;
+    WH_TRY(fp8_ptr_check(*t, x_dev, y_dev));
+    if (t->fast && (x_stride & 3)) return WH_INVALID_ARGUMENT;  // every input 16-byte aligned
     WH_HIP(hipSetDevice(c->device));
     return launch_fp8(c, *t, row_start, row_end, x_dev, y_dev, n, x_stride, y_stride);
 }
@@ -2009,22 +2170,30 @@ int wh_fp8_gemv_batch_async(wh_ctx* c, const wh_gemv_desc* descs, size_t n) {
         if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
         if (!d.x_dev || !d.y_dev) return WH_INVALID_ARGUMENT;
         if (d.row_start >= d.row_end || d.row_end > t->rows) return WH_INVALID_SHAPE;
+        WH_TRY(fp8_ptr_check(*t, d.x_dev, d.y_dev));
     }
     for (size_t i = 0; i < n;) {
         const wh_gemv_desc& d = descs[i];
         const Tensor* t = find_tensor(c, d.weight);
         const size_t rows = d.row_end - d.row_start;
-        // a run of equal, consecutive row groups of one tensor with evenly
-        // spaced inputs and back-to-back outputs goes out as one launch
+        // A run of equal, consecutive row groups of one tensor with evenly
+        // spaced inputs and back-to-back outputs goes out as one launch.  The
+        // kernel takes the input step as a 32-bit count of floats, and the
+        // run's outputs must not overlap its inputs: the descriptors are
+        // ordered, so an output that feeds a later input keeps its own launch.
         size_t j = i + 1;
-        const ptrdiff_t xs = j < n ? descs[j].x_dev - d.x_dev : 0;
-        if (fp8_split_k(*t) && is_pow2(rows) && rows >= WH_FP8_SK_ROWS && xs >= 0) {
-            while (j < n && descs[j].weight == d.weight && descs[j].row_start == descs[j - 1].row_end &&
-                   descs[j].row_end - descs[j].row_start == rows && descs[j].x_dev - descs[j - 1].x_dev == xs &&
-                   descs[j].y_dev == descs[j - 1].y_dev + rows)
-                ++j;
-        } else {
-            j = i + 1;
+        ptrdiff_t xs = 0;
+        if (j < n && fp8_split_k(*t) && is_pow2(rows) && rows >= WH_FP8_SK_ROWS) {
+            xs = descs[j].x_dev - d.x_dev;
+            if (xs >= 0 && (uint64_t)xs <= UINT32_MAX) {
+                while (j < n && descs[j].weight == d.weight && descs[j].row_start == descs[j - 1].row_end &&
+                       descs[j].row_end - descs[j].row_start == rows && descs[j].x_dev - descs[j - 1].x_dev == xs &&
+                       descs[j].y_dev == descs[j - 1].y_dev + rows)
+                    ++j;
+                const uintptr_t x_lo = (uintptr_t)d.x_dev, x_hi = (uintptr_t)(descs[j - 1].x_dev + t->cols);
+                const uintptr_t y_lo = (uintptr_t)d.y_dev, y_hi = (uintptr_t)(descs[j - 1].y_dev + rows);
+                if (j - i > 1 && y_lo < x_hi && x_lo < y_hi) j = i + 1;
+            }
         }
         if (j - i > 1)
             WH_TRY(launch_fp8(c, *t, d.row_start, descs[j - 1].row_end, d.x_dev, d.y_dev, 1, t->cols,
@@ -2493,12 +2662,14 @@ int wh_profile_routed(wh_ctx* c, const wh_expert_route* routes, size_t n_routes,
                 e[i].w2->rows != e[0].w1->cols)
                 return WH_UNSUPPORTED;
     }
+    MoeBufs bufs;
+    WH_TRY(moe_bufs_ctx(c, n_routes, 1, ev[0].w1->cols, ev[0].w1->rows, &bufs));
     for (unsigned stage = 1; stage <= 2; ++stage) {
         WH_HIP(hipEventRecord(c->timer[0], c->stream));
         for (size_t it = 0; it < iters; ++it) {
             const size_t s = it % n_sets;
             WH_TRY(moe_launch_fast(c, &ev[s * n_routes], &wts[s * n_routes], n_routes, false, x_dev, x_bf16, 1,
-                                   out_dev, stage));
+                                   out_dev, stage, bufs, true));
         }
         WH_HIP(hipEventRecord(c->timer[1], c->stream));
         WH_HIP(hipEventSynchronize(c->timer[1]));
