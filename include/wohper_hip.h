@@ -311,6 +311,25 @@ int wh_routed_and_shared_experts_async(wh_ctx* ctx, const wh_expert_route* route
                                        uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
                                        int x_is_bf16, size_t n_tokens, float* out_dev);
 
+/* Allocation-free variant of wh_routed_and_shared_experts_async, same
+ * arguments and results.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  It calls no allocating
+ * routine; its working memory (SwiGLU outputs, per-expert outputs, routed-sum
+ * arrival counters, split-K input codes) is one fixed array of
+ * WH_NOALLOC_SCRATCH_BYTES per GPU, set up by wh_init and held until the
+ * process ends.  Every call on a GPU shares that GPU's array, so calls that
+ * overlap on one GPU (other contexts, other threads' streams) race; calls on
+ * one context's stream are ordered.  Only experts on the fast kernels'
+ * shapes are taken (else WH_UNSUPPORTED); a call whose working memory,
+ * about n_tokens x (n_routes + 1) x 4 x (hidden + intermediate) bytes,
+ * exceeds the array returns WH_SCRATCH_TOO_SMALL before anything is
+ * queued, with the sizes in wh_last_error(). */
+#define WH_NOALLOC_SCRATCH_BYTES (8u << 20)
+int wh_routed_and_shared_experts_noalloc_async(wh_ctx* ctx, const wh_expert_route* routes, size_t n_routes,
+                                               uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
+                                               int x_is_bf16, size_t n_tokens, float* out_dev);
+
 /* compute_deepseek_fp8_shared_expert_into_hidden (E/compute.rs:5545-5614):
  * output[..w2 rows] = W2 act_quant(swiglu(W1 xq, W3 xq)) with
  * xq = act_quant(input) (block 64), each stage bit-identical to the

@@ -85,6 +85,7 @@ EXPORTED = (
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
     "wh_quant_block_header", "wh_quant_block_tensor", "wh_quant_block_fp4_expert", "wh_store_expert_block",
     "wh_store_expert_pack", "wh_store_router", "wh_route_experts", "wh_route_experts_async",
+    "wh_routed_and_shared_experts_noalloc_async",
 )
 
 ROUTER_RAW_LOGITS = 0
@@ -189,6 +190,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
                                                    f32p, sz]),
         "wh_routed_and_shared_experts_async": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, c.c_uint32,
                                                          c.c_uint32, vp, c.c_int, sz, vp]),
+        "wh_routed_and_shared_experts_noalloc_async": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, c.c_uint32,
+                                                                 c.c_uint32, vp, c.c_int, sz, vp]),
         "wh_profile_routed": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, sz, vp, c.c_int, vp, sz,
                                         c.POINTER(c.c_double)]),
         "wh_timer_stop": (c.c_int, [vp, c.POINTER(c.c_double)]),
@@ -519,6 +522,15 @@ class Context:
         _check(self.lib.wh_routed_and_shared_experts_async(self._h, arr, n, shared_key[0], shared_key[1],
                                                            ctypes.c_void_p(x_ptr), int(x_is_bf16), n_tokens,
                                                            ctypes.c_void_p(out_ptr)), "routed_and_shared_experts_async")
+
+    def routed_and_shared_experts_noalloc_async(self, routes, shared_key, x_ptr: int, x_is_bf16: bool,
+                                                n_tokens: int, out_ptr: int):
+        """The allocation-free variant of routed_and_shared_experts_async: its
+        working memory is the library's fixed per-GPU array."""
+        arr = self.route_array(routes)
+        _check(self.lib.wh_routed_and_shared_experts_noalloc_async(
+            self._h, arr, len(routes), shared_key[0], shared_key[1], ctypes.c_void_p(x_ptr), int(x_is_bf16),
+            n_tokens, ctypes.c_void_p(out_ptr)), "routed_and_shared_experts_noalloc_async")
 
     def moe_batch(self, layer_id: int, route_ids, route_scores, x, shared_key=None) -> np.ndarray:
         """Batched routed experts, expert-major (the batch-prefill MoE of

@@ -26,11 +26,21 @@
 #include "router.h"
 #include "wohper_hip.h"
 
+// Working memory of wh_routed_and_shared_experts_noalloc_async: one array on
+// every GPU the library runs on, held until the process ends.  In host code
+// this name is a stand-in for the device symbol, not a device address: the
+// address on each GPU comes from hipGetSymbolAddress (noalloc_setup).
+static __device__ __align__(256) uint8_t noalloc_scratch[WH_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 constexpr int kFp8 = 1, kFp4 = 2;
 
-
+// Device address of noalloc_scratch on each GPU (null until wh_init ran on
+// it with that GPU current).
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices] = {};
 
 struct Tensor {
     int kind = 0;
@@ -1402,6 +1412,18 @@ int router_launch(wh_ctx* c, const Router& rt, wh_router_sel sa, const float* x,
     return WH_OK;
 }
 
+// Once per GPU, with that GPU current: the device address of its copy of
+// noalloc_scratch.
+int noalloc_setup(int device) {
+    if (device >= kMaxDevices) return WH_OK;  // the allocation-free entry point then reports Unsupported
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (g_noalloc_ptr[device]) return WH_OK;
+    void* p = nullptr;
+    WH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch)));
+    g_noalloc_ptr[device] = p;
+    return WH_OK;
+}
+
 // Drops a layer's router and returns its HBM to the arena.
 void drop_router(wh_ctx* c, uint32_t layer) {
     auto it = c->routers.find(layer);
@@ -1486,6 +1508,7 @@ int wh_init(int device, wh_ctx** out) {
     if (device < 0 || device >= n) return WH_INVALID_ARGUMENT;
     WH_HIP(hipSetDevice(device));
     WH_HIP(kernel_setup_once(device));
+    WH_TRY(noalloc_setup(device));
     wh_ctx* c = new wh_ctx();
     c->device = device;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
@@ -2330,6 +2353,49 @@ int wh_routed_and_shared_experts_async(wh_ctx* c, const wh_expert_route* routes,
     float wts[WH_MAX_EXPERTS];
     WH_TRY(routed_shared_common(c, routes, n, shared_layer, shared_expert, ev, wts));
     return moe_forward(c, ev, wts, n + 1, true, x_dev, x_bf16, n_tokens, out_dev);
+}
+
+int wh_routed_and_shared_experts_noalloc_async(wh_ctx* c, const wh_expert_route* routes, size_t n,
+                                               uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
+                                               int x_bf16, size_t n_tokens, float* out_dev) {
+    if (!c || !x_dev || !out_dev || n_tokens == 0 || (n && !routes)) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    ExpertView ev[WH_MAX_EXPERTS];
+    float wts[WH_MAX_EXPERTS];
+    WH_TRY(routed_shared_common(c, routes, n, shared_layer, shared_expert, ev, wts));
+    bool fast = false;
+    WH_TRY(moe_shapes(ev, n + 1, &fast));
+    if (!fast) {
+        std::snprintf(g_last_error, sizeof g_last_error,
+                      "allocation-free routed experts: the experts are not on the fast kernels' shapes");
+        return WH_UNSUPPORTED;
+    }
+    const size_t hidden = ev[0].w1->cols, inter = ev[0].w1->rows;
+    const MoeSizes z = moe_sizes(n + 1, n_tokens, hidden, inter, moe_split_k(c, hidden, inter));
+    if (z.total() > WH_NOALLOC_SCRATCH_BYTES) {
+        std::snprintf(g_last_error, sizeof g_last_error,
+                      "allocation-free routed experts: %zu tokens x %zu experts need %zu bytes of working memory, "
+                      "the fixed array holds %zu",
+                      n_tokens, n + 1, z.total(), (size_t)WH_NOALLOC_SCRATCH_BYTES);
+        return WH_SCRATCH_TOO_SMALL;
+    }
+    uint8_t* base = nullptr;
+    {
+        std::lock_guard<std::mutex> g(g_noalloc_mu);
+        if (c->device < kMaxDevices) base = (uint8_t*)g_noalloc_ptr[c->device];
+    }
+    if (!base) {
+        std::snprintf(g_last_error, sizeof g_last_error, "allocation-free routed experts: no working memory on device %d",
+                      c->device);
+        return WH_UNSUPPORTED;
+    }
+    MoeBufs b;
+    b.h = (float*)base;
+    b.y = (float*)(base + z.h);
+    b.cnt = (uint32_t*)(base + z.h + z.y);
+    b.xq = z.xq ? (uint32_t*)(base + z.h + z.y + z.cnt) : nullptr;
+    return moe_launch_fast(c, ev, wts, n + 1, true, x_dev, x_bf16, n_tokens, out_dev, 3u, b, false);
 }
 
 // ------------------------------------------------------ batched routed experts
