@@ -37,7 +37,7 @@ TOKEN_BYTES = 6 * EXPERT_BYTES + 4096 * 2 + 4096 * 4   # + bf16 x + f32 y = 80,2
 GATEUP_BYTES = 6 * 2 * (4_194_304 + 262_144) + 4096 * 2 + 6 * 2048 * 4     # 53,534,720
 DOWN_BYTES = 6 * (4_194_304 + 262_144) + 6 * 2048 * 4 + 4096 * 4           # 26,804,224
 # The routed-expert kernels of each numerics mode (trace names).
-KERNELS = {False: ("k_moe_gateup_sk<2>", "k_moe_down_sk"), True: ("k_moe_gateup<16, 4>", "k_moe_down<8, 4>")}
+KERNELS = {False: ("k_moe_gateup_mx<2>", "k_moe_down_mx"), True: ("k_moe_gateup<16, 4>", "k_moe_down<8, 4>")}
 # HBM bytes per gate/up launch: rocprofv3 FETCH_SIZE and WRITE_SIZE KiB per
 # dispatch, scaled by what the same counters read for a 268,435,456-byte copy
 # (FETCH x2.00, WRITE x1.00); see profiles/.  None: not measured.
@@ -456,7 +456,7 @@ def main():
     ap.add_argument("--stack-batch-steps", type=int, default=3,
                     help="steps of the batch-16 full-depth stack (0: skip)")
     ap.add_argument("--split-k", dest="exact", action="store_false",
-                    help="routed experts on the split-K kernels (summation order freed) instead of the bit-exact ones")
+                    help="routed experts on the MFMA kernels (summation order freed) instead of the bit-exact ones")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 5 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -528,7 +528,7 @@ def main():
 
     gu_name, dn_name = KERNELS[args.exact]
     extra = {"numerics": "exact (the reference kernel's summation order)" if args.exact else
-             "split-K (each matvec within 1e-5 * ||w_row|| * ||x|| of the reference kernel)",
+             "MFMA (each matvec within 1e-5 * ||w_row|| * ||x|| of the reference kernel)",
              "kernels": {gu_name: {"us": round(gu_us, 3), "GBps": round(gu_gbs, 1), "bytes_per_launch": GATEUP_BYTES},
                          dn_name: {"us": round(dn_us, 3), "GBps": round(dn_gbs, 1), "bytes_per_launch": DOWN_BYTES},
                          "token_device_us": round(launch_us, 3)}}

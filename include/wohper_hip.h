@@ -316,7 +316,7 @@ int wh_routed_and_shared_experts_async(wh_ctx* ctx, const wh_expert_route* route
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  It calls no allocating
  * routine; its working memory (SwiGLU outputs, per-expert outputs, routed-sum
- * arrival counters, split-K input codes) is one fixed array of
+ * arrival counters) is one fixed array of
  * WH_NOALLOC_SCRATCH_BYTES per GPU, set up by wh_init and held until the
  * process ends.  Every call on a GPU shares that GPU's array, so calls that
  * overlap on one GPU (other contexts, other threads' streams) race; calls on
@@ -347,7 +347,9 @@ int wh_fp8_shared_expert_async(wh_ctx* ctx, wh_tensor w1, wh_tensor w3, wh_tenso
  * wh_fp4_expert_forward).  on = 1 (the default): every matvec follows the
  * reference CPU kernel's summation order (E/deepseek_v4.rs:294-347), so
  * outputs are bit-identical to it.  on = 0: for the model's expert shapes
- * (hidden 2048 or 4096, inter 2048) split-K kernels free the summation
+ * (hidden 2048 or 4096, inter 2048) block-scaled FP8 MFMA kernels take the
+ * reference's exact operands (E4M3 codes of the act-quantized inputs and of
+ * the FP4 LUT values, UE8M0 / E8M0 block scales) and free only the summation
  * order; the dequantized weights are the reference's values exactly and each
  * matvec agrees with the reference kernel on the same input within
  * max|diff| <= 1e-5 * ||w_row||_2 * ||x||_2 (fp32 accumulation), while

@@ -1,4 +1,4 @@
-"""GPU parity of the split-K routed-expert kernels (set_exact_numerics(False))
+"""GPU parity of the MFMA routed-expert kernels (set_exact_numerics(False))
 of the routed/shared expert entry points (compute_active_experts and
 compute_active_and_shared_experts, E/compute.rs:1872-2030, over
 deepseek_v4_fp4_expert_forward_scalar, E/deepseek_v4.rs:551-601).
@@ -154,7 +154,7 @@ def test_nonfinite_inputs_follow_the_reference(ctx, oracle, exact):
     """fp8_act_quant_dequant_in_place (E/compute.rs:2504-2545) inside the
     expert forward: NaN inputs quantize to -480 x the block scale and the
     token stays finite (checked against the oracle: bit for bit in exact
-    mode, per matvec within tolerance in split-K mode); an inf makes its
+    mode, per matvec within tolerance in MFMA mode); an inf makes its
     block's scale infinite, and the forward ends in NonFiniteOutput
     (E/deepseek_v4.rs:597-599), as the oracle does."""
     ctx.set_exact_numerics(exact)

@@ -790,8 +790,6 @@ struct wh_moe_args {
     uint32_t* cnt_y;               // [n_tokens][hidden/32] arrivals per 32-row slice
     uint32_t* status;
     float* gu;                     // null, or [n_tokens][n_experts][2][inter]: gate and up captured
-    const uint32_t* xq;            // split-K kernels: act-quant codes of x, f16 pairs in lane order
-    const float* xk;               // split-K kernels: [n_tokens][hidden/64] block scales of x
 };
 
 // The per-binade log2f thresholds of the act-quant scale, staged in LDS: a

@@ -21,7 +21,7 @@
 #define WH_LIBM_TABLES_INCLUDED 1
 #include "kernels.h"
 #include "moe_batch.h"
-#include "moe_token.h"
+#include "moe_mx.h"
 #include "quant_block.h"
 #include "router.h"
 #include "wohper_hip.h"
@@ -254,7 +254,7 @@ struct wh_ctx {
     wh_tensor next_id = 1;
     uint32_t* status = nullptr;  // device status word
     uint32_t* status_host = nullptr;
-    Scratch x_in, y_out, h, ybuf, cnt_y, tmp, batch, routes, bout, gu, xq;
+    Scratch x_in, y_out, h, ybuf, cnt_y, tmp, batch, routes, bout, gu;
     Scratch relayout;  // raw FP4 rows on their way into the resident layout
     Scratch rtr;       // router: logits, available ids, outputs of the host-slice call
     Scratch rtr_cnt;   // router: arrival counter of the one-launch bf16 kernel (kept at 0)
@@ -275,13 +275,6 @@ struct wh_ctx {
 namespace {
 
 thread_local char g_last_error[256] = "";
-
-// Rows per wave of the split-K gate/up kernel (8 or 16); WH_SK_ROWS
-// overrides the default for tuning runs.
-const int g_sk_rows = [] {
-    const char* v = std::getenv("WH_SK_ROWS");
-    return (v && std::atoi(v) == 8) ? 8 : 16;
-}();
 
 int hip_status_at(hipError_t e, const char* what, int line) {
     if (e == hipSuccess) return WH_OK;
@@ -599,44 +592,38 @@ struct MoeBufs {
     float* h = nullptr;       // [T][n][inter] SwiGLU outputs
     float* y = nullptr;       // [T][n][hidden] per-expert outputs
     uint32_t* cnt = nullptr;  // [T][hidden / 32] routed-sum arrivals (cleared by gate/up)
-    uint32_t* xq = nullptr;   // split-K only: [T][hidden / 2] input codes, then [T][hidden / 64] scales
     float* gu = nullptr;      // test capture of gate and up, or null
 };
 
-// Split-K kernels (summation order freed) serve the model's shapes unless
-// the context asks for the reference's order.
-bool moe_split_k(const wh_ctx* c, size_t hidden, size_t inter) {
+// The MFMA token kernels (summation order freed) serve the model's shapes
+// unless the context asks for the reference's order.
+bool moe_mfma(const wh_ctx* c, size_t hidden, size_t inter) {
     return !c->exact && (hidden == 2048 || hidden == 4096) && inter == 2048;
 }
 
 // Bytes of each MoeBufs region (each rounded up to 256).
 struct MoeSizes {
-    size_t h, y, cnt, xq;
-    size_t total() const { return h + y + cnt + xq; }
+    size_t h, y, cnt;
+    size_t total() const { return h + y + cnt; }
 };
-MoeSizes moe_sizes(size_t n, size_t n_tokens, size_t hidden, size_t inter, bool sk) {
+MoeSizes moe_sizes(size_t n, size_t n_tokens, size_t hidden, size_t inter) {
     auto r = [](size_t b) { return (b + 255) & ~size_t(255); };
     MoeSizes z;
     z.h = r(n_tokens * n * inter * sizeof(float));
     z.y = r(n_tokens * n * hidden * sizeof(float));
     z.cnt = r(n_tokens * (hidden / 32) * sizeof(uint32_t));
-    z.xq = sk ? r(n_tokens * (hidden * 2 + hidden / 16)) : 0;
     return z;
 }
 
 // The context's own (growing) buffers.
 int moe_bufs_ctx(wh_ctx* c, size_t n, size_t n_tokens, size_t hidden, size_t inter, MoeBufs* b) {
-    const MoeSizes z = moe_sizes(n, n_tokens, hidden, inter, moe_split_k(c, hidden, inter));
+    const MoeSizes z = moe_sizes(n, n_tokens, hidden, inter);
     WH_HIP(c->h.ensure(z.h, false));
     WH_HIP(c->ybuf.ensure(z.y, false));
     WH_HIP(c->cnt_y.ensure(z.cnt, true));
     b->h = c->h.as<float>();
     b->y = c->ybuf.as<float>();
     b->cnt = c->cnt_y.as<uint32_t>();
-    if (z.xq) {
-        WH_HIP(c->xq.ensure(z.xq, false));
-        b->xq = c->xq.as<uint32_t>();
-    }
     if (c->capture_gu) {
         WH_HIP(c->gu.ensure(n_tokens * n * 2 * inter * sizeof(float), false));
         b->gu = c->gu.as<float>();
@@ -678,26 +665,13 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
     a.gu = bufs.gu;
     if (record)
         c->tok_last_n = n, c->tok_last_tokens = n_tokens, c->tok_last_hidden = hidden, c->tok_last_inter = inter;
-    const bool sk = moe_split_k(c, hidden, inter);
+    const bool sk = moe_mfma(c, hidden, inter);
     if (stages & 1) {
         if (sk) {
-            // x act-quantized once per token, then the split-K gate/up
-            uint32_t* xq = bufs.xq;
-            float* xk = (float*)(xq + n_tokens * hidden / 2);
-            a.xq = xq;
-            a.xk = xk;
-            const unsigned tok = (unsigned)n_tokens;
-            const int rows = g_sk_rows;
-            dim3 ggrid((unsigned)(n * inter / rows), tok);
-            if (hidden == 4096) {
-                k_moe_xquant<2><<<tok, 256, 0, c->stream>>>(x_dev, a.x_is_bf16, xq, xk, c->status);
-                if (rows == 8) k_moe_gateup_sk<2, 8><<<ggrid, 256, 0, c->stream>>>(a);
-                else k_moe_gateup_sk<2, 16><<<ggrid, 256, 0, c->stream>>>(a);
-            } else {
-                k_moe_xquant<1><<<tok, 128, 0, c->stream>>>(x_dev, a.x_is_bf16, xq, xk, c->status);
-                if (rows == 8) k_moe_gateup_sk<1, 8><<<ggrid, 128, 0, c->stream>>>(a);
-                else k_moe_gateup_sk<1, 16><<<ggrid, 128, 0, c->stream>>>(a);
-            }
+            // block-scaled FP8 MFMA over the act-quantized x, 16 rows per workgroup
+            dim3 ggrid((unsigned)(n * inter / 16), (unsigned)n_tokens);
+            if (hidden == 4096) k_moe_gateup_mx<2><<<ggrid, 256, 0, c->stream>>>(a);
+            else k_moe_gateup_mx<1><<<ggrid, 128, 0, c->stream>>>(a);
         } else if (hidden == 4096) {
             dim3 ggrid((unsigned)(n * inter / 16), (unsigned)n_tokens);
             k_moe_gateup<16><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
@@ -708,7 +682,7 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
     }
     if (stages & 2) {
         dim3 dgrid((unsigned)(n * hidden / 32), (unsigned)n_tokens);
-        if (sk) k_moe_down_sk<<<dgrid, 256, wh_moe_down_sk_lds(inter), c->stream>>>(a);
+        if (sk) k_moe_down_mx<<<dgrid, 256, 0, c->stream>>>(a);
         else if (inter == 2048) k_moe_down<8><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
         else k_moe_down<0><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
     }
@@ -1531,7 +1505,7 @@ int wh_shutdown(wh_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     c->arena.release_all();
     for (Scratch* s : {&c->x_in, &c->y_out, &c->h, &c->ybuf, &c->cnt_y, &c->tmp, &c->batch, &c->routes, &c->bout,
-                       &c->gu, &c->xq, &c->relayout, &c->rtr, &c->rtr_cnt})
+                       &c->gu, &c->relayout, &c->rtr, &c->rtr_cnt})
         if (s->p) (void)hipFree(s->p);
     for (auto& kv : c->tables)
         if (kv.second.dev) (void)hipFree(kv.second.dev);
@@ -2372,7 +2346,7 @@ int wh_routed_and_shared_experts_noalloc_async(wh_ctx* c, const wh_expert_route*
         return WH_UNSUPPORTED;
     }
     const size_t hidden = ev[0].w1->cols, inter = ev[0].w1->rows;
-    const MoeSizes z = moe_sizes(n + 1, n_tokens, hidden, inter, moe_split_k(c, hidden, inter));
+    const MoeSizes z = moe_sizes(n + 1, n_tokens, hidden, inter);
     if (z.total() > WH_NOALLOC_SCRATCH_BYTES) {
         std::snprintf(g_last_error, sizeof g_last_error,
                       "allocation-free routed experts: %zu tokens x %zu experts need %zu bytes of working memory, "
@@ -2394,7 +2368,6 @@ int wh_routed_and_shared_experts_noalloc_async(wh_ctx* c, const wh_expert_route*
     b.h = (float*)base;
     b.y = (float*)(base + z.h);
     b.cnt = (uint32_t*)(base + z.h + z.y);
-    b.xq = z.xq ? (uint32_t*)(base + z.h + z.y + z.cnt) : nullptr;
     return moe_launch_fast(c, ev, wts, n + 1, true, x_dev, x_bf16, n_tokens, out_dev, 3u, b, false);
 }
 
