@@ -226,12 +226,17 @@ def expert_pack_load(ctx, n_experts: int = 24):
             "payload_bytes": payload, "seconds": round(el, 4), "GBps": round(payload / el / 1e9, 2)}
 
 
-def ragged_batch(ctx, n_layers: int, steps: int, warmup: int):
+def ragged_batch(ctx, n_layers: int, steps: int, warmup: int, exact: bool = False, mfma_min: int = 1):
     """Ragged batched MoE: 64 bf16 tokens, each top-6 of 256 FP4 experts under
     Zipf(1.1) popularity over a seeded permutation (seed 4), one launch
     sequence per step (device packing, act-quant, grouped gate/up, grouped
-    down, expert-major weighted sum), rotating over the resident layers."""
+    down, expert-major weighted sum), rotating over the resident layers.
+    exact: every expert on the bit-exact items; else experts with at least
+    mfma_min tokens on MFMA items."""
     from wohper_amd import workloads as wl
+
+    ctx.set_exact_numerics(exact)
+    ctx.set_moe_mfma_min(mfma_min)
 
     ids, sc, x = wl.zipf_batch_routes(seed=4, n_tokens=64)
     npos, topk = ids.shape
@@ -256,10 +261,12 @@ def ragged_batch(ctx, n_layers: int, steps: int, warmup: int):
     dev_us = ctx.timer_stop() / steps
     ctx.synchronize()
     us = (time.perf_counter() - t0) / steps * 1e6
+    n_mfma = int(ctx.debug_moe_batch_read(4, 8, np.uint32)[4])
     for p in (x_dev, ids_dev, sc_dev, out_dev):
         ctx.device_free(p)
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"workload": "ragged batched MoE: 64 bf16 tokens x top-6 of 256 FP4 experts, Zipf(1.1) popularity",
+            "numerics": "exact" if exact else f"MFMA for experts with >= {mfma_min} tokens", "experts_on_mfma": n_mfma,
             "experts_used": n_used, "largest_group": int(counts.max()),
             "groups_ge_16": int((counts >= 16).sum()), "tokens_in_groups_ge_16": int(counts[counts >= 16].sum()),
             "bytes_per_step": nbytes, "us_per_step": round(us, 2), "GBps": round(gbs, 1),
@@ -457,6 +464,9 @@ def main():
                     help="steps of the batch-16 full-depth stack (0: skip)")
     ap.add_argument("--split-k", dest="exact", action="store_false",
                     help="routed experts on the MFMA kernels (summation order freed) instead of the bit-exact ones")
+    ap.add_argument("--batch-mfma-sweep", type=str, default="",
+                    help="only time the ragged batch leg: exact items, then each MFMA threshold of this "
+                         "comma-separated list (one JSON line each)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 5 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -484,6 +494,12 @@ def main():
             ctx.store_expert_synthetic(layer, e, wl.HIDDEN, wl.INTER, seed)
     dev_bytes, _, n_exp = ctx.usage()
     log(f"resident: {n_exp} experts, {dev_bytes / 1e9:.1f} GB in {time.perf_counter() - t0:.1f} s")
+    if args.batch_mfma_sweep:
+        modes = [(True, 0)] + [(False, int(m)) for m in args.batch_mfma_sweep.split(",")]
+        for exact, m in modes:
+            print(json.dumps(ragged_batch(ctx, args.layers, args.batch_steps, 3, exact, m)), flush=True)
+        ctx.close()
+        return
 
     total = args.warmup + args.steps
     rng = np.random.default_rng(seed)
@@ -552,7 +568,8 @@ def main():
         extra["expert_pack_load"] = expert_pack_load(ctx)
         log(f"expert pack load: {extra['expert_pack_load']}")
     if args.batch_steps > 0:
-        extra["ragged_batch"] = ragged_batch(ctx, args.layers, args.batch_steps, 3)
+        extra["ragged_batch"] = ragged_batch(ctx, args.layers, args.batch_steps, 3, args.exact)
+        ctx.set_exact_numerics(args.exact)
         log(f"ragged batch: {extra['ragged_batch']}")
     cpu = None
     if not args.no_cpu:

@@ -343,8 +343,9 @@ int wh_fp8_shared_expert(wh_ctx* ctx, wh_tensor w1, wh_tensor w3, wh_tensor w2, 
 int wh_fp8_shared_expert_async(wh_ctx* ctx, wh_tensor w1, wh_tensor w3, wh_tensor w2, const float* x_dev,
                                float* y_dev);
 
-/* Numerics of the routed/shared expert entry points above (and
- * wh_fp4_expert_forward).  on = 1 (the default): every matvec follows the
+/* Numerics of the routed/shared expert entry points above, of
+ * wh_fp4_expert_forward and of the batch entry points below.  on = 1 (the
+ * default): every matvec follows the
  * reference CPU kernel's summation order (E/deepseek_v4.rs:294-347), so
  * outputs are bit-identical to it.  on = 0: for the model's expert shapes
  * (hidden 2048 or 4096, inter 2048) block-scaled FP8 MFMA kernels take the
@@ -381,13 +382,16 @@ int wh_debug_moe_token_read(wh_ctx* ctx, int which, void* out, size_t bytes);
  * WH_NOT_RESIDENT (the async variant reports it through the stream status).
  * The async variant takes device pointers (x f32 or bf16) and enqueues on
  * the library stream; the grouping runs on the device. */
-/* Experts of a batch with at least min_tokens tokens run on block-scaled
- * FP8 MFMA (E4M3 codes of the weights' x8 LUT values and of the act-quantized
- * inputs, E8M0 block scales, fp32 accumulation): their outputs agree with the
- * reference within fp32 rounding of a different summation order; the other
- * experts stay bit-identical to the reference's AVX2 kernel.  Default 16;
- * 0 keeps every expert on the exact path.  No counterpart in the reference
- * (its batch path has one kernel). */
+/* With exact numerics off (wh_set_exact_numerics(ctx, 0)), experts of a
+ * batch with at least min_tokens tokens run on block-scaled FP8 MFMA (E4M3
+ * codes of the weights' x8 LUT values and of the act-quantized inputs, E8M0
+ * block scales, fp32 accumulation): their outputs agree with the reference
+ * within fp32 rounding of a different summation order; the other experts
+ * stay bit-identical to the reference's AVX2 kernel.  Default 1 (every
+ * expert: the MFMA items stream the weights faster than the exact ones even
+ * for one token); 0 keeps every expert on the exact path, as exact numerics
+ * do whatever the threshold.  No counterpart in the reference (its batch
+ * path has one kernel). */
 int wh_set_moe_mfma_min(wh_ctx* ctx, uint32_t min_tokens);
 /* Test support for the batch path, no counterpart in the reference:
  * copies a device buffer of the last single-chunk fast batch call (S = its

@@ -2,12 +2,12 @@
 E/server/generation.rs:2487-2569 with accumulate_expert_for_positions,
 E/compute.rs:1779-1810) against the oracle.
 
-Exact path (every expert below the MFMA threshold): bit-exact - device
-packing of the per-expert token lists, the per-position weight rule,
-ascending-id accumulation, the shared expert, chunking of large batches and
-the generic shapes.  MFMA path (experts at or above the threshold): every
-matvec within max|diff| <= 1e-5 * ||w_row||_2 * ||x||_2 of the oracle on the
-same input, every other stage bit-exact."""
+Exact path (exact numerics, or every expert below the MFMA threshold):
+bit-exact - device packing of the per-expert token lists, the per-position
+weight rule, ascending-id accumulation, the shared expert, chunking of large
+batches and the generic shapes.  MFMA path (exact numerics off, experts at or
+above the threshold): every matvec within max|diff| <= 1e-5 * ||w_row||_2 *
+||x||_2 of the oracle on the same input, every other stage bit-exact."""
 import numpy as np
 import pytest
 
@@ -16,14 +16,15 @@ from parity_util import check_matvec as _check_matvec
 from wohper_amd import workloads as wl
 
 pytestmark = pytest.mark.gpu
-DEFAULT_MFMA_MIN = 16
+DEFAULT_MFMA_MIN = 1
 
 
 @pytest.fixture(autouse=True)
 def exact_path(ctx):
     """Tests compare bit-exactly unless they opt into MFMA groups."""
-    ctx.set_moe_mfma_min(0)
+    ctx.set_exact_numerics(True)
     yield
+    ctx.set_exact_numerics(True)
     ctx.set_moe_mfma_min(DEFAULT_MFMA_MIN)
 
 
@@ -156,14 +157,20 @@ def _mfma_case(ctx, oracle, layer, n_exp, hidden, inter, seed, npos, mfma_min):
     ids, sc, x = wl.zipf_batch_routes(seed=seed, n_tokens=npos, n_experts=n_exp, hidden=hidden)
     experts = _host(ctx, layer, ids, seed, hidden, inter)
     topk, S = ids.shape[1], ids.size
+    ctx.set_exact_numerics(False)
     ctx.set_moe_mfma_min(mfma_min)
-    out = ctx.moe_batch(layer, ids, sc, x)
+    try:
+        out = ctx.moe_batch(layer, ids, sc, x)
+    finally:
+        ctx.set_exact_numerics(True)
     rd = ctx.debug_moe_batch_read
     srt, gate, up = rd(0, S, np.uint32), rd(1, (S, inter), np.float32), rd(2, (S, inter), np.float32)
     y, hq = rd(3, (S, hidden), np.float32), rd(8, (S, inter), np.float32)
     meta, uoff, uexp, uorder = rd(4, 8, np.uint32), rd(5, S + 1, np.uint32), rd(6, S, np.uint32), rd(7, S, np.uint32)
     n_used, n_mfma = int(meta[0]), int(meta[4])
-    assert 0 < n_mfma < n_used, (n_used, n_mfma)  # both paths run
+    assert 0 < n_mfma <= n_used, (n_used, n_mfma)
+    if mfma_min > 1:
+        assert n_mfma < n_used, (n_used, n_mfma)  # both paths run
     on_mfma = {int(uexp[j]) for j in uorder[:n_mfma]}
     xq = {p: oracle.act_quant(x[p], 64) for p in range(npos)}
     wts = oracle.batch_route_weights(sc)
@@ -198,9 +205,23 @@ def test_batch_mfma_small_shapes(ctx, oracle):
     print(f"worst MFMA matvec |diff| / tolerance: {worst:.3f}")
 
 
-def test_batch_mfma_real_shapes(ctx, oracle):
-    worst = _mfma_case(ctx, oracle, 45, 8, wl.HIDDEN, wl.INTER, 34, 24, DEFAULT_MFMA_MIN)
+@pytest.mark.parametrize("mfma_min", [16, DEFAULT_MFMA_MIN])
+def test_batch_mfma_real_shapes(ctx, oracle, mfma_min):
+    worst = _mfma_case(ctx, oracle, 45, 8, wl.HIDDEN, wl.INTER, 34, 24, mfma_min)
     print(f"worst MFMA matvec |diff| / tolerance: {worst:.3f}")
+
+
+def test_batch_exact_numerics_override_the_threshold(ctx, oracle):
+    """Exact numerics keep every expert on the exact items whatever the
+    threshold: bit-exact against the oracle."""
+    layer, n_exp, hidden, inter, seed, npos = 44, 12, 512, 256, 33, 48
+    _store(ctx, layer, n_exp, hidden, inter, seed)
+    ids, sc, x = wl.zipf_batch_routes(seed=seed, n_tokens=npos, n_experts=n_exp, hidden=hidden)
+    ctx.set_moe_mfma_min(1)
+    got = ctx.moe_batch(layer, ids, sc, x)
+    assert int(ctx.debug_moe_batch_read(4, 8, np.uint32)[4]) == 0
+    want = oracle.moe_batch(_host(ctx, layer, ids, seed, hidden, inter), ids, sc, x)
+    assert np.array_equal(bits(got), bits(want))
 
 
 def test_batch_nonfinite_inputs_follow_the_reference(ctx, oracle):
@@ -213,6 +234,7 @@ def test_batch_nonfinite_inputs_follow_the_reference(ctx, oracle):
     _store(ctx, layer, n_exp, hidden, inter, seed)
     ids, sc, x = wl.zipf_batch_routes(seed=seed, n_tokens=npos, n_experts=n_exp, hidden=hidden)
     experts = _host(ctx, layer, ids, seed, hidden, inter)
+    ctx.set_exact_numerics(False)
     ctx.set_moe_mfma_min(8)
     xn = x.copy()
     xn[3, [0, 70, 71]] = np.nan

@@ -2,12 +2,12 @@
 
 * Ragged batched MoE: 64 tokens routed top-6 over 256 experts of the model's
   shapes (w1/w3 2048x4096, w2 4096x2048) with Zipf(1.1) popularity, seed 4,
-  through wh_moe_batch with the default MFMA threshold (16): groups of 16 or
-  more tokens run on MFMA (every matvec within 1e-5 * ||w_row|| * ||x|| of the
-  oracle on the same input), all others bit-exact; every later stage
-  bit-exact given the matvec outputs (the batch-prefill MoE of
-  E/server/generation.rs:2487-2569, accumulate_expert_for_positions,
-  E/compute.rs:1779-1810).
+  through wh_moe_batch with exact numerics off at MFMA thresholds 16, 2 and
+  the default 1: groups at or above the threshold run on MFMA (every matvec
+  within 1e-5 * ||w_row|| * ||x|| of the oracle on the same input), all
+  others bit-exact; every later stage bit-exact given the matvec outputs
+  (the batch-prefill MoE of E/server/generation.rs:2487-2569,
+  accumulate_expert_for_positions, E/compute.rs:1779-1810).
 * The full-depth stack: 43 layers of 256 routed + 1 shared FP4 experts and
   one decode layer's FP8 projections each (152 GB resident), seed 5.  On
   three sampled layers: at batch 1 every FP8 projection (the row ranges and
@@ -15,9 +15,8 @@
   (E/compute.rs:1872-1946) bit-exact against the oracle; at batch 16 every
   projection over 16 inputs (gemv_fp8_e4m3_ue8m0_rows_multi,
   E/compute.rs:6384-6577) bit-exact, and the batch MoE of 16 positions with
-  the shared expert bit-exact on the exact items; with the default MFMA
-  threshold the shared expert (16 tokens) runs on MFMA and the output is
-  compared in norm."""
+  the shared expert bit-exact under exact numerics; with exact numerics off
+  every expert runs on MFMA and the output is compared in norm."""
 import numpy as np
 import pytest
 
@@ -32,13 +31,14 @@ def bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-def test_ragged_batch_full_workload(ctx, oracle):
-    """64 Zipf-routed tokens over 256 model-shape experts, MFMA threshold 16."""
+@pytest.mark.parametrize("mfma_min", [16, 2, 1])
+def test_ragged_batch_full_workload(ctx, oracle, mfma_min):
+    """64 Zipf-routed tokens over 256 model-shape experts."""
     try:
-        worst = _mfma_case(ctx, oracle, 80, wl.N_ROUTED, wl.HIDDEN, wl.INTER, 4, 64, 16)
-        print(f"ragged batch: worst MFMA matvec |diff| / tolerance {worst:.3f}")
+        worst = _mfma_case(ctx, oracle, 80, wl.N_ROUTED, wl.HIDDEN, wl.INTER, 4, 64, mfma_min)
+        print(f"ragged batch, MFMA threshold {mfma_min}: worst MFMA matvec |diff| / tolerance {worst:.3f}")
     finally:
-        ctx.set_moe_mfma_min(16)
+        ctx.set_moe_mfma_min(1)
 
 
 STACK_SEED = 5
@@ -153,16 +153,17 @@ def test_stack_layer_batch16(stack, oracle, L):
     experts = {int(e): wl.synth_expert_host(c.lib, STACK_SEED, L, int(e)) for e in np.unique(ids)}
     shared = wl.synth_expert_host(c.lib, STACK_SEED, L, wl.N_ROUTED)
     want = oracle.moe_batch(experts, ids, sc, x, shared=shared)
+    # exact numerics: every expert on the exact items, bit for bit
+    got = c.moe_batch(L, ids, sc, x, shared_key=(L, wl.N_ROUTED))
+    assert int(c.debug_moe_batch_read(4, 8, np.uint32)[4]) == 0
+    assert np.array_equal(bits(got), bits(want)), L
     try:
-        # every expert on the exact items: bit for bit
-        c.set_moe_mfma_min(0)
+        # exact numerics off, default threshold: every expert on MFMA, each
+        # matvec within tolerance, so the output is compared in norm
+        c.set_exact_numerics(False)
         got = c.moe_batch(L, ids, sc, x, shared_key=(L, wl.N_ROUTED))
-        assert np.array_equal(bits(got), bits(want)), L
-        # the default threshold puts the shared expert (16 tokens) on MFMA:
-        # its matvecs are within tolerance, so the output is compared in norm
-        c.set_moe_mfma_min(16)
-        got = c.moe_batch(L, ids, sc, x, shared_key=(L, wl.N_ROUTED))
-        assert int(c.debug_moe_batch_read(4, 8, np.uint32)[4]) >= 1
+        meta = c.debug_moe_batch_read(4, 8, np.uint32)
+        assert int(meta[4]) == int(meta[0])
         assert np.linalg.norm(got - want) <= 1e-3 * np.linalg.norm(want), L
     finally:
-        c.set_moe_mfma_min(16)
+        c.set_exact_numerics(True)

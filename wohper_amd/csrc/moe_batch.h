@@ -534,11 +534,6 @@ struct wh_mfma_a {
     uint2 c[4];
     uint2 s;  // the row's 8 scale bytes of the block
 };
-__device__ __forceinline__ void wh_mfma_a_load(wh_mfma_a& a, const uint8_t* wlane, const uint8_t* srow, uint32_t blk) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) a.c[j] = *(const uint2*)(wlane + blk * 128 + j * 16);
-    a.s = *(const uint2*)(srow + blk * 8);
-}
 template <int u>
 __device__ __forceinline__ wh_v8i wh_mfma_a_codes(const wh_mfma_a& a) {
     wh_v8i v;
@@ -550,6 +545,41 @@ __device__ __forceinline__ wh_v8i wh_mfma_a_codes(const wh_mfma_a& a) {
         v[4 + j] = (int)fb;
     }
     return v;
+}
+
+// A operand loads.  The MFMA lane (m, g) needs, per 256-col block of row m,
+// the dword pair 2(g/2), 2(g/2) + 1 of the four 16-byte chunks
+// 4(g%2) .. 4(g%2) + 3 (wh_mfma_a): four 8-byte pieces 16 bytes apart.  As
+// loads those stream at ~4 TB/s; instead each lane loads 32 contiguous bytes
+// - chunks 4(g%2) + 2(g/2) and the next - and lanes L and L ^ 32 (the two
+// values of g/2) trade the dword pairs each needs from the other's chunks
+// with v_permlane32_swap, at ~5.4 TB/s.
+struct wh_mx_raw {
+    uint4 p, q;  // the lane's two chunks as loaded
+    uint2 s;     // the row's 8 scale bytes of the block
+};
+// wlane = row base + 64 (g % 2) + 32 (g / 2); srow = the row's scale bytes.
+__device__ __forceinline__ void wh_mx_raw_load(wh_mx_raw& r, const uint8_t* wlane, const uint8_t* srow, uint32_t blk) {
+    r.p = *(const uint4*)(wlane + blk * 128);
+    r.q = *(const uint4*)(wlane + blk * 128 + 16);
+    r.s = *(const uint2*)(srow + blk * 8);
+}
+// The exchange: the lower half of the wave (g / 2 = 0) keeps dwords 0, 1 and
+// takes dwords 0, 1 of the upper lanes' chunks; the upper half keeps
+// dwords 2, 3 and takes dwords 2, 3 of the lower lanes' chunks.  All 64
+// lanes must take part.
+__device__ __forceinline__ wh_mfma_a wh_mx_fix(const wh_mx_raw& r) {
+    const auto sp0 = __builtin_amdgcn_permlane32_swap(r.p.x, r.p.z, false, false);
+    const auto sp1 = __builtin_amdgcn_permlane32_swap(r.p.y, r.p.w, false, false);
+    const auto sq0 = __builtin_amdgcn_permlane32_swap(r.q.x, r.q.z, false, false);
+    const auto sq1 = __builtin_amdgcn_permlane32_swap(r.q.y, r.q.w, false, false);
+    wh_mfma_a a;
+    a.c[0] = make_uint2(sp0[0], sp1[0]);  // chunk 4(g%2):     own (lower) or from lower (upper)
+    a.c[1] = make_uint2(sq0[0], sq1[0]);  // chunk 4(g%2) + 1
+    a.c[2] = make_uint2(sp0[1], sp1[1]);  // chunk 4(g%2) + 2: from upper (lower) or own (upper)
+    a.c[3] = make_uint2(sq0[1], sq1[1]);  // chunk 4(g%2) + 3
+    a.s = r.s;
+    return a;
 }
 
 // B staging: thread t copies 64 code bytes (groups 2q, 2q + 1 of the block,
@@ -612,7 +642,7 @@ __device__ __forceinline__ void wh_mfma_item(const uint8_t* const* wmat, const u
     const uint8_t* sr[kMat];
 #pragma unroll
     for (int i = 0; i < kMat; ++i) {
-        wl[i] = wmat[i] + (size_t)row * (cols / 2) + (4 * (g & 1)) * 16 + (g >> 1) * 8;
+        wl[i] = wmat[i] + (size_t)row * (cols / 2) + 64 * (g & 1) + 32 * (g >> 1);
         sr[i] = smat[i] + (size_t)row * G;
     }
     for (uint32_t s0 = s_beg; s0 < s_end; s0 += WH_MFMA_TOK) {
@@ -627,10 +657,10 @@ __device__ __forceinline__ void wh_mfma_item(const uint8_t* const* wmat, const u
         for (int i = 0; i < kMat; ++i)
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) acc[i][nt] = wh_v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        wh_mfma_a ra[kMat], na[kMat];
+        wh_mx_raw ra[kMat], na[kMat];
         wh_mfma_b rb;
 #pragma unroll
-        for (int i = 0; i < kMat; ++i) wh_mfma_a_load(ra[i], wl[i], sr[i], 0);
+        for (int i = 0; i < kMat; ++i) wh_mx_raw_load(ra[i], wl[i], sr[i], 0);
         wh_mfma_b_load(rb, brec, bsrec, ton, 0);
         if (s0 != s_beg) __syncthreads();  // the previous pass is done with the LDS
         wh_mfma_b_store(rb, lds);
@@ -639,19 +669,22 @@ __device__ __forceinline__ void wh_mfma_item(const uint8_t* const* wmat, const u
             const bool more = blk + 1 < nblk;
             if (more) {
 #pragma unroll
-                for (int i = 0; i < kMat; ++i) wh_mfma_a_load(na[i], wl[i], sr[i], blk + 1);
+                for (int i = 0; i < kMat; ++i) wh_mx_raw_load(na[i], wl[i], sr[i], blk + 1);
                 wh_mfma_b_load(rb, brec, bsrec, ton, blk + 1);
             }
             const uint8_t* buf = lds + (blk & 1) * WH_MFMA_BUF;
             const uint8_t* bsc = buf + WH_MFMA_TOK * WH_MFMA_TSTRIDE;
+            wh_mfma_a fa[kMat];
+#pragma unroll
+            for (int i = 0; i < kMat; ++i) fa[i] = wh_mx_fix(ra[i]);
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 wh_v8i av[kMat];
                 uint32_t as[kMat];
 #pragma unroll
                 for (int i = 0; i < kMat; ++i) {
-                    av[i] = u ? wh_mfma_a_codes<1>(ra[i]) : wh_mfma_a_codes<0>(ra[i]);
-                    as[i] = u ? wh_mfma_sbyte<1>(ra[i].s, g) : wh_mfma_sbyte<0>(ra[i].s, g);
+                    av[i] = u ? wh_mfma_a_codes<1>(fa[i]) : wh_mfma_a_codes<0>(fa[i]);
+                    as[i] = u ? wh_mfma_sbyte<1>(fa[i].s, g) : wh_mfma_sbyte<0>(fa[i].s, g);
                 }
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) {

@@ -36,41 +36,6 @@
 #define WH_MX_GU_DEPTH 8  // 256-col blocks of a gate/up wave's row slice in flight
 #endif
 
-// A operand loads.  The MFMA lane (m, g) needs, per 256-col block of row m,
-// the dword pair 2(g/2), 2(g/2) + 1 of the four 16-byte chunks
-// 4(g%2) .. 4(g%2) + 3 (wh_mfma_a): four 8-byte pieces 16 bytes apart.  As
-// loads those stream at ~4 TB/s; instead each lane loads 32 contiguous bytes
-// - chunks 4(g%2) + 2(g/2) and the next - and lanes L and L ^ 32 (the two
-// values of g/2) trade the dword pairs each needs from the other's chunks
-// with v_permlane32_swap, at ~5.4 TB/s.
-struct wh_mx_raw {
-    uint4 p, q;  // the lane's two chunks as loaded
-    uint2 s;     // the row's 8 scale bytes of the block
-};
-// wlane = row base + 64 (g % 2) + 32 (g / 2); srow = the row's scale bytes.
-__device__ __forceinline__ void wh_mx_raw_load(wh_mx_raw& r, const uint8_t* wlane, const uint8_t* srow, uint32_t blk) {
-    r.p = *(const uint4*)(wlane + blk * 128);
-    r.q = *(const uint4*)(wlane + blk * 128 + 16);
-    r.s = *(const uint2*)(srow + blk * 8);
-}
-// The exchange: the lower half of the wave (g / 2 = 0) keeps dwords 0, 1 and
-// takes dwords 0, 1 of the upper lanes' chunks; the upper half keeps
-// dwords 2, 3 and takes dwords 2, 3 of the lower lanes' chunks.  All 64
-// lanes must take part.
-__device__ __forceinline__ wh_mfma_a wh_mx_fix(const wh_mx_raw& r) {
-    const auto sp0 = __builtin_amdgcn_permlane32_swap(r.p.x, r.p.z, false, false);
-    const auto sp1 = __builtin_amdgcn_permlane32_swap(r.p.y, r.p.w, false, false);
-    const auto sq0 = __builtin_amdgcn_permlane32_swap(r.q.x, r.q.z, false, false);
-    const auto sq1 = __builtin_amdgcn_permlane32_swap(r.q.y, r.q.w, false, false);
-    wh_mfma_a a;
-    a.c[0] = make_uint2(sp0[0], sp1[0]);  // chunk 4(g%2):     own (lower) or from lower (upper)
-    a.c[1] = make_uint2(sq0[0], sq1[0]);  // chunk 4(g%2) + 1
-    a.c[2] = make_uint2(sp0[1], sp1[1]);  // chunk 4(g%2) + 2: from upper (lower) or own (upper)
-    a.c[3] = make_uint2(sq0[1], sq1[1]);  // chunk 4(g%2) + 3
-    a.s = r.s;
-    return a;
-}
-
 // The A blocks of a wave's 16 rows held in registers (a ring of kBlocks).
 template <int kBlocks>
 struct wh_mx_rows {

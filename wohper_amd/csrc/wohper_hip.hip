@@ -262,7 +262,7 @@ struct wh_ctx {
     HostBuf stage_in, stage_out;
     HostBuf pack[2];   // experts-pack read buffers (one filling while the other uploads)
     std::map<uint32_t, LayerTable> tables;  // device expert tables of the batch path
-    uint32_t moe_mfma_min = 16;             // batch experts with this many tokens use MFMA (0: never)
+    uint32_t moe_mfma_min = 1;              // batch experts with this many tokens use MFMA (0: never)
     bool exact = true;                      // routed experts in the reference's summation order
     bool capture_gu = false;                // routed experts keep gate/up in `gu` (test support)
     size_t tok_last_n = 0, tok_last_tokens = 0, tok_last_hidden = 0, tok_last_inter = 0;
@@ -1009,7 +1009,7 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         a.hq8 = b.hq8;
         a.hs8 = b.hs8;
         a.y = b.y;
-        a.mfma_min = c->moe_mfma_min;
+        a.mfma_min = c->exact ? 0u : c->moe_mfma_min;  // exact numerics: every expert on the exact items
         a.out = out + p0 * hidden;
         a.status = c->status;
         // the most items the queues can hold: used experts <= min(slots, ids),
