@@ -483,6 +483,88 @@ int wh_profile_routed(wh_ctx* ctx, const wh_expert_route* routes, size_t n_route
  * expf(x) for any x. */
 int wh_debug_eval(wh_ctx* ctx, int fn, const float* in, float* out, size_t n);
 
+/* ------------------------------------------------------------------
+ * MLA attention glue at decode (compute_deepseek_v4_mla_attention,
+ * E/compute.rs:3924-4293): the non-GEMV steps between the FP8 projections,
+ * bit-identical to the reference's f32 arithmetic (sequential sums, separate
+ * roundings, glibc-exact expf / sinf / cosf, the block-64 act-quant).
+ * Positions must be below 2^24 (WH_UNSUPPORTED otherwise).
+ * ------------------------------------------------------------------ */
+
+/* YarnRope (E/compute.rs:2558-2572). */
+typedef struct {
+    float factor, beta_fast, beta_slow;
+    size_t original_seq_len;
+} wh_yarn;
+
+/* rope_inv_freqs (E/compute.rs:2591-2620), on the host with the platform
+ * libm as the reference computes it: rope_dim / 2 values; yarn NULL = plain
+ * theta^(-2i/dim). */
+int wh_rope_inv_freqs(size_t rope_dim, float theta, const wh_yarn* yarn, float* out, size_t out_len);
+/* deepseek_rope_for_layer (E/compute.rs:2575-2586): theta 160000 with
+ * DEEPSEEK_V4_YARN on layers with a compress ratio, else 10000 without. */
+int wh_deepseek_rope_for_layer(uint32_t physical_layer, float* theta, wh_yarn* yarn, int* has_yarn);
+
+/* rms_norm_in_place (E/compute.rs:7110-7122) of each of `rows` rows of n
+ * values (weight_bf16_dev NULL), or apply_weighted_rms_norm
+ * (E/compute.rs:3077-3107) with a bf16 weight of n values; eps 1e-6.
+ * out_dev may equal x_dev.  n <= 4096. */
+int wh_rms_norm_async(wh_ctx* ctx, const float* x_dev, float* out_dev, size_t rows, size_t n,
+                      const uint16_t* weight_bf16_dev);
+
+/* apply_rope_interleaved_with_freqs (E/compute.rs:2623-2649) on
+ * values[r * row_stride + offset .. + 2 * pairs) of each row r, at
+ * `position`, with inverse frequencies inv_freqs_dev[pairs]; inverse != 0
+ * rotates back.  offset + 2 * pairs > row_stride -> WH_INVALID_SHAPE
+ * ("RoPE input shorter than dim").  row_stride <= 4096. */
+int wh_rope_async(wh_ctx* ctx, float* values_dev, size_t rows, size_t row_stride, size_t offset,
+                  const float* inv_freqs_dev, size_t pairs, size_t position, int inverse);
+
+/* Device-pointer fp8_act_quant_dequant_in_place (E/compute.rs:2504-2521). */
+int wh_act_quant_dequant_async(wh_ctx* ctx, float* values_dev, size_t n, size_t block_size);
+
+/* The window softmax of the MLA layer (E/compute.rs:4106-4197) for one
+ * decode position: per head h the keys are the n_window rows at window_dev
+ * (row stride window_stride; the KV cache from the window start) then the
+ * n_comp compressed rows (head_dim apart); score = (q . key in order) *
+ * head_dim^-0.5, softmax against the largest score with the optional sink
+ * logit sink_dev[h] in the denominator, out = sum of weight * key in key
+ * order, divided by the denominator when positive, then the inverse RoPE of
+ * the rope dims [nope_dim, nope_dim + 2 pairs) at token_pos.  scores_dev:
+ * heads * (n_window + n_comp) floats of scratch.  head_dim a multiple of 64,
+ * at most 1024; at most 2048 keys; window_dev and comp_dev 16-byte aligned
+ * and window_stride a multiple of 4 (WH_INVALID_ARGUMENT otherwise). */
+int wh_window_attention_async(wh_ctx* ctx, const float* q_dev, size_t heads, size_t head_dim, size_t nope_dim,
+                              const float* window_dev, size_t n_window, size_t window_stride, const float* comp_dev,
+                              size_t n_comp, const float* sink_dev, const float* inv_freqs_dev, size_t pairs,
+                              size_t token_pos, float* scores_dev, float* out_dev);
+
+/* One decode MLA attention layer (compute_deepseek_v4_mla_attention,
+ * E/compute.rs:3924-4293) with resident FP8 projections: act-quant x; q_lora
+ * = wq_a x; q norm (weighted if q_norm_bf16, else plain) + act-quant; q =
+ * wq_b q_lora; per-head RMS norm and RoPE; kv = wkv x; kv norm, RoPE,
+ * act-quant of the non-rope dims, stored as the KV cache row of token_pos;
+ * the window softmax over the cached rows [max(0, token_pos - 127),
+ * token_pos] and the n_comp compressed rows the caller passes (the
+ * compressor's visible blocks, E/compute.rs:4087-4100); act-quant; wo_a per
+ * output group; act-quant; hidden = wo_b o_mid (in place).  RoPE theta and
+ * YaRN follow physical_layer.  Shapes: wq_a [q_lora x hidden], wq_b
+ * [heads*head_dim x q_lora], wkv [head_dim x hidden], wo_a [o_groups*o_lora
+ * x heads*head_dim/o_groups], wo_b [hidden x o_groups*o_lora]; a mismatch
+ * is WH_INVALID_SHAPE.  hidden_dev, kv_cache_dev and comp_dev 16-byte
+ * aligned, kv_stride a multiple of 4. */
+typedef struct {
+    uint32_t physical_layer;
+    size_t heads, nope_dim, rope_dim, o_groups, o_lora_rank;
+    wh_tensor wq_a, wq_b, wkv, wo_a, wo_b;
+    const uint16_t* q_norm_bf16;  /* device [q_lora] or NULL */
+    const uint16_t* kv_norm_bf16; /* device [head_dim] or NULL */
+    const float* sink;            /* device [heads] or NULL */
+} wh_mla_layer;
+int wh_mla_attention_decode_async(wh_ctx* ctx, const wh_mla_layer* layer, size_t token_pos, float* hidden_dev,
+                                  float* kv_cache_dev, size_t kv_stride, size_t kv_capacity, const float* comp_dev,
+                                  size_t n_comp);
+
 #ifdef __cplusplus
 }
 #endif

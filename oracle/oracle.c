@@ -790,3 +790,96 @@ int or_route_select(const float* logits, size_t rows, const float* bias, const u
     *n_out = n;
     return OR_OK;
 }
+
+/* ---------------------------------------------------------------- MLA glue */
+
+/* rms_norm_in_place (E/compute.rs:7110-7122) when w is NULL, else
+ * apply_weighted_rms_norm (E/compute.rs:3077-3107) with bf16 weights:
+ * the squares summed in order (Iterator::sum), mean_square = s / n,
+ * inv_rms = 1 / sqrt(mean_square + 1e-6), out = x * inv_rms (* w). */
+void or_rms_norm(const float* x, size_t n, const uint16_t* w, float* out) {
+    if (n == 0) return;
+    float s = 0.0f;
+    for (size_t i = 0; i < n; ++i) s += x[i] * x[i];
+    const float ms = s / (float)n;
+    const float inv = 1.0f / sqrtf(ms + 1.0e-6f);
+    for (size_t i = 0; i < n; ++i) out[i] = w ? x[i] * inv * bf16_value(w[i]) : x[i] * inv;
+}
+
+/* rope_inv_freqs (E/compute.rs:2591-2620): theta^(-(2i)/dim) per pair, then
+ * with YaRN the linear ramp between the beta_fast / beta_slow correction
+ * dims blends freq / factor and freq. */
+void or_rope_inv_freqs(size_t rope_dim, float theta, int yarn, float factor, float beta_fast, float beta_slow,
+                       size_t original_seq_len, float* out) {
+    const size_t pairs = rope_dim / 2;
+    for (size_t p = 0; p < pairs; ++p) out[p] = powf(theta, -(float)(2 * p) / (float)rope_dim);
+    if (!yarn || original_seq_len == 0) return;
+    const float dim = (float)rope_dim;
+    const float base_ln = logf(theta);
+    const float pi = 3.14159265358979323846f;
+    const float cf = dim * logf((float)original_seq_len / (beta_fast * 2.0f * pi)) / (2.0f * base_ln);
+    const float cs = dim * logf((float)original_seq_len / (beta_slow * 2.0f * pi)) / (2.0f * base_ln);
+    const float low = fmaxf(floorf(cf), 0.0f);
+    float high = fminf(ceilf(cs), dim - 1.0f);
+    if (fabsf(low - high) < 1.1920929e-7f) high = low + 0.001f;
+    for (size_t p = 0; p < pairs; ++p) {
+        float ramp = ((float)p - low) / (high - low);
+        if (ramp < 0.0f) ramp = 0.0f;
+        else if (ramp > 1.0f) ramp = 1.0f;
+        const float smooth = 1.0f - ramp;
+        out[p] = out[p] / factor * (1.0f - smooth) + out[p] * smooth;
+    }
+}
+
+/* apply_rope_interleaved_with_freqs (E/compute.rs:2623-2649): pair i of
+ * values rotated by position * inv[i] (f32 sin / cos of the host libm). */
+void or_rope_apply(float* v, size_t position, const float* inv, size_t pairs, int inverse) {
+    const float pos = (float)position;
+    for (size_t p = 0; p < pairs; ++p) {
+        const float ang = pos * inv[p];
+        float s = sinf(ang);
+        const float c = cosf(ang);
+        if (inverse) s = -s;
+        const float e = v[2 * p], o = v[2 * p + 1];
+        v[2 * p] = e * c - o * s;
+        v[2 * p + 1] = e * s + o * c;
+    }
+}
+
+/* The window loop of compute_deepseek_v4_mla_attention (E/compute.rs:
+ * 4106-4197) for every head: keys = the n_win window rows (stride win_ld)
+ * then the n_comp compressed rows (head_dim apart). */
+void or_window_attention(const float* q, size_t heads, size_t head_dim, size_t nope_dim, const float* win,
+                         size_t n_win, size_t win_ld, const float* comp, size_t n_comp, const float* sink,
+                         const float* inv, size_t pairs, size_t token_pos, float* out) {
+    const size_t nk = n_win + n_comp;
+    const float scale = powf((float)head_dim, -0.5f);  /* (head_dim as f32).powf(-0.5), E/compute.rs:4083 */
+    for (size_t h = 0; h < heads; ++h) {
+        const float* qh = q + h * head_dim;
+        float mx = -INFINITY;
+        for (size_t j = 0; j < nk; ++j) {
+            const float* key = j < n_win ? win + j * win_ld : comp + (j - n_win) * head_dim;
+            float s = 0.0f;
+            for (size_t d = 0; d < head_dim; ++d) s += qh[d] * key[d];
+            s *= scale;
+            if (s > mx) mx = s;
+        }
+        float denom = 0.0f;
+        if (sink) denom += expf(sink[h] - mx);
+        float* oh = out + h * head_dim;
+        for (size_t d = 0; d < head_dim; ++d) oh[d] = 0.0f;
+        float wsum = 0.0f;
+        for (size_t j = 0; j < nk; ++j) {
+            const float* key = j < n_win ? win + j * win_ld : comp + (j - n_win) * head_dim;
+            float s = 0.0f;
+            for (size_t d = 0; d < head_dim; ++d) s += qh[d] * key[d];
+            const float w = expf((s * scale) - mx);
+            wsum += w;
+            for (size_t d = 0; d < head_dim; ++d) oh[d] += w * key[d];
+        }
+        denom += wsum;
+        if (denom > 0.0f)
+            for (size_t d = 0; d < head_dim; ++d) oh[d] /= denom;
+        or_rope_apply(oh + nope_dim, token_pos, inv, pairs, 1);
+    }
+}

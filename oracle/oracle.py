@@ -73,6 +73,10 @@ def lib():
             "or_sqrt_softplus": (c.c_float, [c.c_float]),
             "or_sqrt_softplus_array": (None, [f32p, f32p, sz]),
             "or_log1pf_array": (None, [f32p, f32p, sz]),
+            "or_rms_norm": (None, [f32p, sz, c.POINTER(c.c_uint16), f32p]),
+            "or_rope_inv_freqs": (None, [sz, c.c_float, c.c_int, c.c_float, c.c_float, c.c_float, sz, f32p]),
+            "or_rope_apply": (None, [f32p, sz, f32p, sz, c.c_int]),
+            "or_window_attention": (None, [f32p, sz, sz, sz, f32p, sz, sz, f32p, sz, f32p, f32p, sz, sz, f32p]),
             "or_route_select": (c.c_int, [f32p, sz, f32p, c.POINTER(c.c_uint32), sz, sz, c.c_int, c.c_float,
                                           c.POINTER(c.c_uint32), sz, c.POINTER(c.c_uint32), f32p,
                                           c.POINTER(sz)]),
@@ -352,3 +356,96 @@ def route_select(logits, active, available=None, bias=None, math=ROUTER_SQRT_SOF
                           math, route_scale, None if h is None else h.ctypes.data_as(u32p),
                           0 if h is None else h.size, ids.ctypes.data_as(u32p), _pf(sc), ctypes.byref(n))
     return ids[:n.value].copy(), sc[:n.value].copy()
+
+
+# ----------------------------------------------------------------- MLA glue
+
+DEEPSEEK_V4_YARN = (16.0, 32.0, 1.0, 65536)  # factor, beta_fast, beta_slow, original_seq_len
+COMPRESS_RATIOS = [0, 0] + [4, 128] * 20 + [4, 0]  # E/compute.rs:2552-2555
+
+
+def rope_for_layer(physical_layer: int):
+    """deepseek_rope_for_layer, E/compute.rs:2575-2586: (theta, yarn or None)."""
+    ratio = COMPRESS_RATIOS[physical_layer] if physical_layer < len(COMPRESS_RATIOS) else 0
+    return (160000.0, DEEPSEEK_V4_YARN) if ratio > 0 else (10000.0, None)
+
+
+def rms_norm(x, w_bf16=None):
+    """Rows of x (last axis) through rms_norm_in_place / apply_weighted_rms_norm."""
+    x = _f(x)
+    out = np.empty_like(x)
+    rows = x.reshape(-1, x.shape[-1])
+    o = out.reshape(-1, x.shape[-1])
+    wp = None
+    if w_bf16 is not None:
+        w_bf16 = np.ascontiguousarray(w_bf16, np.uint16)
+        wp = w_bf16.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))
+    for r in range(rows.shape[0]):
+        xr = np.ascontiguousarray(rows[r])
+        yr = np.empty_like(xr)
+        lib().or_rms_norm(_pf(xr), xr.size, wp, _pf(yr))
+        o[r] = yr
+    return out
+
+
+def rope_inv_freqs(rope_dim: int, theta: float, yarn=None):
+    out = np.zeros(max(rope_dim // 2, 1), np.float32)
+    f, bf, bs, n = yarn if yarn is not None else (0.0, 0.0, 0.0, 0)
+    lib().or_rope_inv_freqs(rope_dim, theta, 1 if yarn is not None else 0, f, bf, bs, n, _pf(out))
+    return out[:rope_dim // 2]
+
+
+def rope_apply(values, position: int, inv_freqs, inverse=False):
+    v = _f(values).copy()
+    inv = _f(inv_freqs)
+    lib().or_rope_apply(_pf(v), position, _pf(inv), inv.size, 1 if inverse else 0)
+    return v
+
+
+def window_attention(q, head_dim, nope_dim, win, comp, sink, inv_freqs, token_pos):
+    """q [heads, head_dim]; win [n_win, >= head_dim] (cache rows); comp
+    [n_comp, head_dim]; sink [heads] or None."""
+    q = _f(q)
+    heads = q.shape[0]
+    win = _f(win)
+    comp = _f(comp) if comp is not None and len(comp) else np.zeros((0, head_dim), np.float32)
+    inv = _f(inv_freqs)
+    out = np.zeros((heads, head_dim), np.float32)
+    s_arr = _f(sink) if sink is not None else None
+    sp = _pf(s_arr) if s_arr is not None else None
+    lib().or_window_attention(_pf(q), heads, head_dim, nope_dim, _pf(win), win.shape[0], win.shape[1], _pf(comp),
+                              comp.shape[0], sp, _pf(inv), inv.size, token_pos, _pf(out))
+    return out
+
+
+def mla_attention_decode(x, proj, q_norm, kv_norm, sink, heads, nope_dim, rope_dim, o_groups, o_lora,
+                         physical_layer, token_pos, kv_cache, comp=None):
+    """compute_deepseek_v4_mla_attention (E/compute.rs:3924-4293) for one
+    position.  proj: callables name -> (input -> output) for wq_a, wq_b,
+    wkv, wo_a_group(g, input) and wo_b; q_norm / kv_norm: bf16 weights or
+    None; kv_cache [capacity, >= head_dim] is updated at token_pos.  Returns
+    the new hidden state."""
+    head_dim = nope_dim + rope_dim
+    theta, yarn = rope_for_layer(physical_layer)
+    inv = rope_inv_freqs(rope_dim, theta, yarn)
+    xq = act_quant(x, 64)
+    ql = proj["wq_a"](xq)
+    ql = rms_norm(ql, q_norm)
+    ql = act_quant(ql, 64)
+    q = proj["wq_b"](ql).reshape(heads, head_dim)
+    q = rms_norm(q)
+    for h in range(heads):
+        q[h, nope_dim:] = rope_apply(q[h, nope_dim:], token_pos, inv)
+    kv = proj["wkv"](xq)
+    kv = rms_norm(kv, kv_norm)
+    kv[nope_dim:] = rope_apply(kv[nope_dim:], token_pos, inv)
+    kv[:nope_dim] = act_quant(kv[:nope_dim], 64)
+    kv_cache[token_pos, :head_dim] = kv
+    context = token_pos + 1
+    ws = max(0, context - 128)
+    att = window_attention(q, head_dim, nope_dim, kv_cache[ws:context], comp, sink, inv, token_pos)
+    att = act_quant(att.reshape(-1), 64)
+    group_in = heads * head_dim // o_groups
+    om = np.concatenate([proj["wo_a_group"](g, att[g * group_in:(g + 1) * group_in]) for g in range(o_groups)])
+    om = act_quant(om, 64)
+    return proj["wo_b"](om)

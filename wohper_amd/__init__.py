@@ -86,6 +86,8 @@ EXPORTED = (
     "wh_quant_block_header", "wh_quant_block_tensor", "wh_quant_block_fp4_expert", "wh_store_expert_block",
     "wh_store_expert_pack", "wh_store_router", "wh_route_experts", "wh_route_experts_async",
     "wh_routed_and_shared_experts_noalloc_async",
+    "wh_rope_inv_freqs", "wh_deepseek_rope_for_layer", "wh_rms_norm_async", "wh_rope_async",
+    "wh_act_quant_dequant_async", "wh_window_attention_async", "wh_mla_attention_decode_async",
 )
 
 ROUTER_RAW_LOGITS = 0
@@ -102,6 +104,19 @@ class DeepSeekV4KernelError(RuntimeError):
         self.detail = detail
         text = self.name + (f" ({where})" if where else "") + (f": {detail}" if detail else "")
         super().__init__(text)
+
+
+class WhYarn(ctypes.Structure):
+    _fields_ = [("factor", ctypes.c_float), ("beta_fast", ctypes.c_float), ("beta_slow", ctypes.c_float),
+                ("original_seq_len", ctypes.c_size_t)]
+
+
+class WhMlaLayer(ctypes.Structure):
+    _fields_ = [("physical_layer", ctypes.c_uint32), ("heads", ctypes.c_size_t), ("nope_dim", ctypes.c_size_t),
+                ("rope_dim", ctypes.c_size_t), ("o_groups", ctypes.c_size_t), ("o_lora_rank", ctypes.c_size_t),
+                ("wq_a", ctypes.c_uint64), ("wq_b", ctypes.c_uint64), ("wkv", ctypes.c_uint64),
+                ("wo_a", ctypes.c_uint64), ("wo_b", ctypes.c_uint64), ("q_norm_bf16", ctypes.c_void_p),
+                ("kv_norm_bf16", ctypes.c_void_p), ("sink", ctypes.c_void_p)]
 
 
 class WhGemvDesc(ctypes.Structure):
@@ -216,6 +231,14 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_store_router": (c.c_int, [vp, c.c_uint32, u8p, sz, sz, c.POINTER(c.c_int)]),
         "wh_route_experts": (c.c_int, [vp, c.c_uint32, f32p, sz, sz, c.POINTER(c.c_uint32), sz,
                                        c.POINTER(WhRouteOptions), c.POINTER(c.c_uint32), f32p, sz, c.POINTER(sz)]),
+        "wh_rope_inv_freqs": (c.c_int, [sz, c.c_float, c.POINTER(WhYarn), f32p, sz]),
+        "wh_deepseek_rope_for_layer": (c.c_int, [c.c_uint32, c.POINTER(c.c_float), c.POINTER(WhYarn),
+                                                 c.POINTER(c.c_int)]),
+        "wh_rms_norm_async": (c.c_int, [vp, vp, vp, sz, sz, vp]),
+        "wh_rope_async": (c.c_int, [vp, vp, sz, sz, sz, vp, sz, sz, c.c_int]),
+        "wh_act_quant_dequant_async": (c.c_int, [vp, vp, sz, sz]),
+        "wh_window_attention_async": (c.c_int, [vp, vp, sz, sz, sz, vp, sz, sz, vp, sz, vp, vp, sz, sz, vp, vp]),
+        "wh_mla_attention_decode_async": (c.c_int, [vp, c.POINTER(WhMlaLayer), sz, vp, vp, sz, sz, vp, sz]),
         "wh_route_experts_async": (c.c_int, [vp, c.c_uint32, vp, sz, sz, vp, sz, c.POINTER(WhRouteOptions), vp, vp,
                                              vp]),
     }
@@ -582,6 +605,33 @@ class Context:
         _check(self.lib.wh_fp8_shared_expert_async(self._h, w1, w3, w2, ctypes.c_void_p(x_ptr),
                                                    ctypes.c_void_p(y_ptr)), "fp8_shared_expert_async")
 
+    # ------------------------------------------------------------ MLA glue
+    def rms_norm_async(self, x_ptr: int, out_ptr: int, rows: int, n: int, weight_bf16_ptr: int = 0):
+        _check(self.lib.wh_rms_norm_async(self._h, x_ptr, out_ptr, rows, n, weight_bf16_ptr or None),
+               "rms_norm_async")
+
+    def rope_async(self, values_ptr: int, rows: int, row_stride: int, offset: int, inv_freqs_ptr: int, pairs: int,
+                   position: int, inverse: bool = False):
+        _check(self.lib.wh_rope_async(self._h, values_ptr, rows, row_stride, offset, inv_freqs_ptr, pairs, position,
+                                      int(bool(inverse))), "rope_async")
+
+    def act_quant_dequant_async(self, values_ptr: int, n: int, block_size: int = 64):
+        _check(self.lib.wh_act_quant_dequant_async(self._h, values_ptr, n, block_size), "act_quant_dequant_async")
+
+    def window_attention_async(self, q_ptr: int, heads: int, head_dim: int, nope_dim: int, win_ptr: int,
+                               n_window: int, window_stride: int, comp_ptr: int, n_comp: int, sink_ptr: int,
+                               inv_freqs_ptr: int, pairs: int, token_pos: int, scores_ptr: int, out_ptr: int):
+        _check(self.lib.wh_window_attention_async(self._h, q_ptr, heads, head_dim, nope_dim, win_ptr or None,
+                                                  n_window, window_stride, comp_ptr or None, n_comp,
+                                                  sink_ptr or None, inv_freqs_ptr or None, pairs, token_pos,
+                                                  scores_ptr, out_ptr), "window_attention_async")
+
+    def mla_attention_decode_async(self, layer: "WhMlaLayer", token_pos: int, hidden_ptr: int, kv_ptr: int,
+                                   kv_stride: int, kv_capacity: int, comp_ptr: int = 0, n_comp: int = 0):
+        _check(self.lib.wh_mla_attention_decode_async(self._h, ctypes.byref(layer), token_pos, hidden_ptr, kv_ptr,
+                                                      kv_stride, kv_capacity, comp_ptr or None, n_comp),
+               "mla_attention_decode_async")
+
     def set_exact_numerics(self, on: bool):
         """True (default): routed-expert matvecs in the reference kernel's
         summation order (bit-identical); False: split-K kernels, each matvec
@@ -780,3 +830,23 @@ def gemv_fp8_e4m3_ue8m0_rows_multi(weight, rows: int, cols: int, scales, scale_r
         return ctx.fp8_gemv_multi(t, inputs, row_start, row_end)
     finally:
         ctx.release(t)
+
+
+def rope_inv_freqs(rope_dim: int, theta: float, yarn=None) -> np.ndarray:
+    """rope_inv_freqs (E/compute.rs:2591-2620): yarn = (factor, beta_fast,
+    beta_slow, original_seq_len) or None."""
+    lib = load_library()
+    out = np.zeros(max(rope_dim // 2, 1), np.float32)
+    y = WhYarn(*yarn) if yarn is not None else None
+    _check(lib.wh_rope_inv_freqs(rope_dim, theta, ctypes.byref(y) if y is not None else None,
+                                 _p(out, ctypes.c_float), out.size), "rope_inv_freqs")
+    return out[:rope_dim // 2]
+
+
+def deepseek_rope_for_layer(physical_layer: int):
+    """deepseek_rope_for_layer (E/compute.rs:2575-2586): (theta, yarn or None)."""
+    lib = load_library()
+    theta, y, has = ctypes.c_float(), WhYarn(), ctypes.c_int()
+    _check(lib.wh_deepseek_rope_for_layer(physical_layer, ctypes.byref(theta), ctypes.byref(y), ctypes.byref(has)),
+           "deepseek_rope_for_layer")
+    return theta.value, ((y.factor, y.beta_fast, y.beta_slow, y.original_seq_len) if has.value else None)

@@ -108,6 +108,55 @@ static void* log_verify(void* p) {
     return NULL;
 }
 
+typedef struct {
+    uint64_t lo, hi, step;
+    long bad;
+} sincos_job;
+
+static void* sincos_verify(void* p) {
+    sincos_job* j = (sincos_job*)p;
+    for (uint64_t b = j->lo; b < j->hi; b += j->step) {
+        const float y = wh_bits_to_float((uint32_t)b);
+        if ((((uint32_t)b) & 0x7fffffffu) > 0x7f800000u) continue;  // NaN
+        const uint32_t gs = wh_float_to_bits(sinf(y)), gc = wh_float_to_bits(cosf(y));
+        if (wh_float_to_bits(wh_sincosf_glibc(y, 0)) != gs || wh_float_to_bits(wh_sincosf_glibc(y, 1)) != gc) {
+            if (j->bad < 5)
+                fprintf(stderr, "sinf/cosf: mismatch y=%a glibc=%a/%a emul=%a/%a\n", y, sinf(y), cosf(y),
+                        wh_sincosf_glibc(y, 0), wh_sincosf_glibc(y, 1));
+            j->bad++;
+        }
+    }
+    return NULL;
+}
+
+// sinf and cosf: every float in [+0, 2^24) (every RoPE angle position x
+// inverse frequency of a position below 2^24 with frequencies <= 1), and
+// every 101st float of the rest (negative, large, inf).
+static int check_sincos(void) {
+    enum { T = 8 };
+    sincos_job js[2 * T];
+    pthread_t ts[2 * T];
+    const uint64_t dense = 0x4b800000ull;  // 2^24
+    for (int i = 0; i < T; ++i) {
+        js[i].lo = dense * i / T;
+        js[i].hi = dense * (i + 1) / T;
+        js[i].step = 1;
+        js[T + i].lo = dense + (0x100000000ull - dense) * i / T;
+        js[T + i].hi = dense + (0x100000000ull - dense) * (i + 1) / T;
+        js[T + i].step = 101;
+        js[i].bad = js[T + i].bad = 0;
+    }
+    for (int i = 0; i < 2 * T; ++i) pthread_create(&ts[i], NULL, sincos_verify, &js[i]);
+    long bad = 0;
+    for (int i = 0; i < 2 * T; ++i) {
+        pthread_join(ts[i], NULL);
+        bad += js[i].bad;
+    }
+    if (bad) fprintf(stderr, "sinf/cosf: %ld mismatches\n", bad);
+    else fprintf(stderr, "sinf/cosf: every float in [0, 2^24) and the sample of the rest match the host glibc\n");
+    return bad != 0;
+}
+
 // Every float t in [-448, 448] against the brute-force nearest E4M3 value
 // (ties to the lower value, +0 for zero), walking the positive grid upward.
 static int check_e4m3_round(void) {
@@ -238,6 +287,7 @@ int main(int argc, char** argv) {
     }
 
     if (check_e4m3_round()) return 1;
+    if (check_sincos()) return 1;
 
     // log1pf over [+0, +inf]
     {

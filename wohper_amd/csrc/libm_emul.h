@@ -193,6 +193,106 @@ WH_HD float wh_log1pf(float x) {
     return kf * ln2_hi - ((hfsq - (s * (hfsq + r) + (kf * ln2_lo + c))) - f);
 }
 
+// glibc-exact sinf / cosf (Rust's f32::sin / f32::cos, which f32::sin_cos
+// calls one after the other; the RoPE angle of E/compute.rs:2623-2649).
+// This restates glibc's method (the sinf/cosf of ARM's optimized-routines by
+// Szabolcs Nagy, glibc's sysdeps/ieee754/flt-32/s_sinf.c, s_cosf.c and
+// s_sincosf.h since 2.28): the float argument is reduced in IEEE double to
+// r in [-pi/4, pi/4] and a quadrant n, then
+//   sin(r) ~ (r + s1 r^3) + r^5 (s2 + s3 r^2),
+//   cos(r) ~ ((c0 + c1 r^2) + c2 r^4) + r^6 (c3 + c4 r^2),
+// with the published minimax coefficients in IEEE double, then rounded to
+// float once.  On CPUs with FMA (every AVX2 machine the reference runs on)
+// glibc selects a build of these functions compiled with FMA contraction, so
+// every a + b*c form below (the reduction x - n pi/2 included) is one fused
+// multiply-add, as there; products stand alone.  Reduction: |x| < 120 multiplies by
+// 2/pi in double (n = nearest integer, r = x - n pi/2); larger |x| takes the
+// exact fixed-point product of the 24-bit mantissa with a 96-bit window of
+// the bits of 2/pi (an integer Payne-Hanek step) to a 2.62 fixed-point
+// fraction.  Odd quadrants swap the two polynomials; quadrants 2 and 3
+// negate them.  The generator compares both with the host glibc on every
+// float in [0, 2^24) and a stride sample of all other floats.
+#define WH_SC_HPI_INV 0x1.45F306DC9C883p+23  /* 2/pi * 2^24 */
+#define WH_SC_HPI 0x1.921FB54442D18p0        /* pi/2 */
+#define WH_SC_PI63 0x1.921FB54442D18p-62     /* pi/2 * 2^-61: one unit of the 2.62 fraction */
+
+// Bits [start, start + 32) of the fraction of 2/pi (zero before bit 0),
+// from its first 224 bits.
+WH_HD uint32_t wh_two_over_pi_bits(int start) {
+    const uint32_t w[7] = {0xA2F9836Eu, 0x4E441529u, 0xFC2757D1u, 0xF534DDC0u,
+                           0xDB629599u, 0x3C439041u, 0xFE5163ABu};
+    if (start <= -32) return 0u;
+    if (start < 0) return w[0] >> (uint32_t)(-start);
+    const int i = start >> 5, s = start & 31;
+    return s == 0 ? w[i] : (w[i] << s) | (w[i + 1] >> (32 - s));
+}
+
+// The two polynomials for reduced r (x2 = r^2): odd n gives the cosine one.
+// neg = 1 negates the coefficients (quadrants 2 and 3).
+WH_HD float wh_sincos_poly(double x, double x2, int n, int neg) {
+    const double sg = neg ? -1.0 : 1.0;
+    if ((n & 1) == 0) {
+        const double s1c = -0x1.555545995a603p-3, s2c = 0x1.1107605230bc4p-7, s3c = -0x1.994eb3774cf24p-13;
+        const double x3 = x * x2;
+        const double s1 = __builtin_fma(x2, s3c, s2c);
+        const double x7 = x3 * x2;
+        const double s = __builtin_fma(x3, s1c, x);
+        return (float)__builtin_fma(x7, s1, s);
+    }
+    const double c0 = sg * 0x1p0, c1 = sg * -0x1.ffffffd0c621cp-2, c2 = sg * 0x1.55553e1068f19p-5,
+                 c3 = sg * -0x1.6c087e89a359dp-10, c4 = sg * 0x1.99343027bf8c3p-16;
+    const double x4 = x2 * x2;
+    const double c2p = __builtin_fma(x2, c4, c3);
+    const double c1p = __builtin_fma(x2, c1, c0);
+    const double x6 = x4 * x2;
+    const double c = __builtin_fma(x4, c2, c1p);
+    return (float)__builtin_fma(x6, c2p, c);
+}
+
+// Large-argument reduction (|x| >= 120, finite): r in double and the
+// quadrant n (mod 4) of the float with bits xi (sign ignored).
+WH_HD double wh_sincos_reduce_large(uint32_t xi, int* np) {
+    const int i0 = (int)((xi >> 26) & 15), shift = (int)((xi >> 23) & 7);
+    const uint32_t a0 = wh_two_over_pi_bits(8 * i0 - 24), a4 = wh_two_over_pi_bits(8 * i0 + 8),
+                   a8 = wh_two_over_pi_bits(8 * i0 + 40);
+    uint32_t m = ((xi & 0xffffffu) | 0x800000u) << shift;
+    uint64_t res0 = (uint64_t)(uint32_t)(m * a0);
+    const uint64_t res1 = (uint64_t)m * a4, res2 = (uint64_t)m * a8;
+    res0 = (res2 >> 32) | (res0 << 32);
+    res0 += res1;
+    const uint64_t n = (res0 + (1ull << 61)) >> 62;
+    res0 -= n << 62;
+    *np = (int)n;
+    return (double)(int64_t)res0 * WH_SC_PI63;
+}
+
+// cosine = 0: sinf(y); cosine = 1: cosf(y).
+WH_HD float wh_sincosf_glibc(float y, int cosine) {
+    const uint32_t top = (wh_float_to_bits(y) >> 20) & 0x7ff;
+    double x = (double)y;
+    int n;
+    if (top < 0x3f4) {                                   // |y| < pi/4
+        if (top < 0x398) return cosine ? 1.0f : y;        // |y| < 2^-12
+        return wh_sincos_poly(x, x * x, cosine, 0);
+    }
+    if (top < 0x42f) {                                   // |y| < 120
+        const double r = x * WH_SC_HPI_INV;
+        n = ((int32_t)r + 0x800000) >> 24;
+        x = __builtin_fma(-(double)n, WH_SC_HPI, x);
+        const double s = ((n + 1) & 2) ? -1.0 : 1.0;     // quadrant signs 1, -1, -1, 1
+        return wh_sincos_poly(x * s, x * x, n ^ cosine, (n & 2) != 0);
+    }
+    if (top < 0x7f8) {                                   // finite
+        const uint32_t xi = wh_float_to_bits(y);
+        const int sign = (int)(xi >> 31);
+        x = wh_sincos_reduce_large(xi, &n);
+        const int q = n + sign;
+        const double s = ((q + 1) & 2) ? -1.0 : 1.0;
+        return wh_sincos_poly(x * s, x * x, n ^ cosine, (q & 2) != 0);
+    }
+    return y - y;                                        // inf, NaN
+}
+
 // 2^k as float for -126 <= k <= 127 (exp2f of an integral float is exact there).
 WH_HD float wh_pow2f(int k) { return wh_bits_to_float((uint32_t)(k + 127) << 23); }
 

@@ -1,0 +1,238 @@
+// The non-GEMV glue of a DeepSeek-V4 MLA attention layer at decode, on
+// gfx950: RMS norms, interleaved RoPE / YaRN, the act-quant between
+// projections, and the sliding-window softmax with attention sink
+// (compute_deepseek_v4_mla_attention, E/compute.rs:3924-4293).
+//
+// Every value follows the reference's f32 arithmetic bit for bit: sums run
+// in the reference's sequential order (one lane per chain), products and
+// sums are separate roundings (the library is built without contraction),
+// exp / sin / cos are the glibc-exact restatements of libm_emul.h, and the
+// act-quant is the block-64 rule of E/compute.rs:2504-2521.  The data are a
+// few hundred KB per token, so these kernels are latency-bound: they keep
+// the hidden state on the device between the FP8 projections rather than
+// aiming at bandwidth.
+#pragma once
+#include "kernels.h"
+
+#define WH_ROWPOST_MAX 4096u     // values per row of k_rowpost
+#define WH_ATTN_MAX_KEYS 2048u   // window + compressed keys per head
+#define WH_ATTN_MAX_HEAD_DIM 1024u
+
+__device__ __forceinline__ float wh_bf16_value(uint16_t raw) { return __uint_as_float((uint32_t)raw << 16); }
+
+// Act-quant (E/compute.rs:2504-2521) of one 64-value block held one value
+// per lane of a wave; lanes past the block's end pass valid = false (they
+// add nothing to the block maximum, as the reference's shorter tail chunk).
+__device__ __forceinline__ float wh_aq64_wave(float x, bool valid) {
+    float amax = wh_wave_max(valid ? fabsf(x) : 0.0f);
+    amax = fmaxf(amax, 1.0e-4f);
+    const bool inf_scale = !(amax <= 3.4028235e38f);
+    const int k = inf_scale ? 0 : wh_aq_scale_exp(amax, kLog2Thr);
+    const float scale = inf_scale ? __uint_as_float(0x7f800000u) : wh_pow2f(k);
+    const float inv = inf_scale ? 0.0f : wh_pow2f(-k);
+    const float t = inf_scale ? x / scale : x * inv;
+    const float q = t != t ? -480.0f : wh_e4m3_round(wh_clamp448(t));  // NaN -> the lowest LUT entry
+    return q * scale;
+}
+
+// ------------------------------------------------------------- row glue
+// Per row r (one workgroup of 256 threads each), in this order, on
+// x + r * ld_in, n values:
+//   norm:  rms_norm_in_place (E/compute.rs:7110-7122) when w is null, else
+//          apply_weighted_rms_norm (E/compute.rs:3077-3107) with bf16 w:
+//          s = sequential sum of v*v, inv = 1 / sqrt(s / n + 1e-6),
+//          v = v * inv (* w);
+//   rope:  apply_rope_interleaved_with_freqs (E/compute.rs:2623-2649) on
+//          [rope_off, rope_off + 2 pairs) at `position`, inverse or not;
+//   quant: act-quant, block 64, of [0, aq_len);
+// then the row goes to out + r * ld_out (which may be x).
+struct wh_rowpost_args {
+    const float* x;
+    float* out;
+    uint32_t rows, n, ld_in, ld_out;
+    uint32_t norm;              // 0: no norm
+    const uint16_t* w;          // bf16 [n] or null
+    const float* inv_freqs;     // [pairs]
+    uint32_t pairs, rope_off, position, inverse;
+    uint32_t aq_len;            // 0: no act-quant
+};
+
+__global__ void __launch_bounds__(256) k_rowpost(wh_rowpost_args a) {
+    __shared__ __align__(16) float v[WH_ROWPOST_MAX];
+    __shared__ float inv_s;
+    const uint32_t t = threadIdx.x, n = a.n;
+    const float* x = a.x + (size_t)blockIdx.x * a.ld_in;
+    for (uint32_t i = t; i < n; i += 256) v[i] = x[i];
+    __syncthreads();
+    if (a.norm) {
+        if (t == 0) {
+            float s = 0.0f;
+            for (uint32_t i = 0; i < n; ++i) s = s + v[i] * v[i];
+            const float ms = s / (float)n;
+            inv_s = 1.0f / sqrtf(ms + 1.0e-6f);
+        }
+        __syncthreads();
+        const float inv = inv_s;
+        for (uint32_t i = t; i < n; i += 256) {
+            float y = v[i] * inv;
+            if (a.w) y = y * wh_bf16_value(a.w[i]);
+            v[i] = y;
+        }
+        __syncthreads();
+    }
+    if (a.pairs) {
+        const float pos = (float)a.position;
+        for (uint32_t p = t; p < a.pairs; p += 256) {
+            const float ang = pos * a.inv_freqs[p];
+            float sn = wh_sincosf_glibc(ang, 0);
+            const float cs = wh_sincosf_glibc(ang, 1);
+            if (a.inverse) sn = -sn;
+            float* pv = v + a.rope_off + 2 * p;
+            const float e = pv[0], o = pv[1];
+            pv[0] = e * cs - o * sn;
+            pv[1] = e * sn + o * cs;
+        }
+        __syncthreads();
+    }
+    if (a.aq_len) {
+        const uint32_t wave = t >> 6, lane = t & 63;
+        for (uint32_t b = wave; b * 64 < a.aq_len; b += 4) {
+            const uint32_t i = b * 64 + lane;
+            const bool valid = i < a.aq_len;
+            const float q = wh_aq64_wave(valid ? v[i] : 0.0f, valid);
+            if (valid) v[i] = q;
+        }
+        __syncthreads();
+    }
+    float* out = a.out + (size_t)blockIdx.x * a.ld_out;
+    for (uint32_t i = t; i < n; i += 256) out[i] = v[i];
+}
+
+// --------------------------------------------------------- window softmax
+// Keys of one decode position: the window rows (the KV cache at positions
+// [window_start, token_pos], row stride win_ld) then the visible compressed
+// rows (head_dim apart), E/compute.rs:4106-4160.
+struct wh_attn_args {
+    const float* q;        // [heads][head_dim]
+    const float* win;      // first window row
+    const float* comp;     // compressed rows
+    const float* sink;     // [heads] or null
+    const float* inv_freqs;
+    float* scores;         // [heads][n_keys] scratch
+    float* out;            // [heads][head_dim]
+    uint32_t heads, head_dim, nope_dim, pairs;
+    uint32_t n_win, n_comp, win_ld, token_pos;
+    float scale;           // head_dim^-0.5 (host powf, as the reference)
+};
+
+__device__ __forceinline__ const float* wh_attn_key(const wh_attn_args& a, uint32_t j) {
+    return j < a.n_win ? a.win + (size_t)j * a.win_ld : a.comp + (size_t)(j - a.n_win) * a.head_dim;
+}
+
+// scores[h][j] = (sum over d, in order, of q[h][d] * key_j[d]) * scale.
+// Grid (ceil(n_keys / 64), ceil(heads / 4)), 256 threads: wave w takes
+// head 4 * blockIdx.y + w, lane L key 64 * blockIdx.x + L; the 64 keys are
+// staged through LDS 64 dims at a time (row stride 65 floats: the lanes'
+// reads of one dim fall in distinct banks), the four heads' q rows once.
+__global__ void __launch_bounds__(256) k_attn_scores(wh_attn_args a) {
+    __shared__ float qs[4 * WH_ATTN_MAX_HEAD_DIM];
+    __shared__ float tile[64 * 65];
+    const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const uint32_t h0 = blockIdx.y * 4, j0 = blockIdx.x * 64;
+    const uint32_t nk = a.n_win + a.n_comp, hd = a.head_dim;
+    for (uint32_t i = t; i < 4 * hd; i += 256) {
+        const uint32_t h = h0 + i / hd;
+        qs[i] = h < a.heads ? a.q[(size_t)h * hd + i % hd] : 0.0f;
+    }
+    // staging: thread t copies 16 dims (t % 4) of key t / 4
+    const uint32_t kk = t >> 2, part = t & 3;
+    const bool kon = j0 + kk < nk;
+    const float* krow = kon ? wh_attn_key(a, j0 + kk) : nullptr;
+    const float* qrow = qs + wave * hd;
+    float s = 0.0f;
+    for (uint32_t d0 = 0; d0 < hd; d0 += 64) {
+        float4 kv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            kv[i] = kon ? *(const float4*)(krow + d0 + part * 16 + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        __syncthreads();  // the previous chunk's reads are done
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float* d = tile + kk * 65 + part * 16 + 4 * i;
+            d[0] = kv[i].x;
+            d[1] = kv[i].y;
+            d[2] = kv[i].z;
+            d[3] = kv[i].w;
+        }
+        __syncthreads();
+        const float* kr = tile + lane * 65;
+        for (uint32_t d = 0; d < 64; ++d) s = s + qrow[d0 + d] * kr[d];
+    }
+    const uint32_t h = h0 + wave, j = j0 + lane;
+    if (h < a.heads && j < nk) a.scores[(size_t)h * nk + j] = s * a.scale;
+}
+
+// The rest of the window loop for 4 heads x 64 dims per workgroup (grid
+// (head_dim / 64, ceil(heads / 4)), 256 threads; wave w = head, lane = dim):
+//   max = the largest score (NaN scores never win, E/compute.rs:4125-4127);
+//   w_j = expf(score_j - max); denom = expf(sink - max) (if a sink) +
+//   (sequential sum of w_j); out_d = sequential sum of w_j * key_j[d] from 0;
+//   out_d /= denom when denom > 0; then the inverse RoPE of the output's
+//   rope dims at token_pos (E/compute.rs:4160-4197).
+__global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
+    __shared__ float wts[4 * WH_ATTN_MAX_KEYS];
+    __shared__ float res[4 * 64];
+    __shared__ float denom_s[4];
+    const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const uint32_t h = blockIdx.y * 4 + wave, d = blockIdx.x * 64 + lane;
+    const uint32_t nk = a.n_win + a.n_comp;
+    const bool hon = h < a.heads;
+    float* w = wts + wave * WH_ATTN_MAX_KEYS;
+    const float* sc = a.scores + (size_t)(hon ? h : 0) * nk;
+    float mx = -__uint_as_float(0x7f800000u);
+    for (uint32_t j = lane; j < nk; j += 64) {
+        const float v = hon ? sc[j] : 0.0f;
+        w[j] = v;
+        mx = fmaxf(mx, v);
+    }
+    mx = wh_wave_max(mx);
+    for (uint32_t j = lane; j < nk; j += 64) w[j] = wh_expf_glibc(w[j] - mx, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
+    __syncthreads();
+    if (lane == 0) {
+        float ws = 0.0f;
+        for (uint32_t j = 0; j < nk; ++j) ws = ws + w[j];
+        float den = 0.0f;
+        if (a.sink && hon) den = den + wh_expf_glibc(a.sink[h] - mx, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
+        denom_s[wave] = den + ws;
+    }
+    float acc = 0.0f;
+    if (hon) {
+        uint32_t j = 0;
+        for (; j + 4 <= nk; j += 4) {
+            const float k0 = wh_attn_key(a, j)[d], k1 = wh_attn_key(a, j + 1)[d];
+            const float k2 = wh_attn_key(a, j + 2)[d], k3 = wh_attn_key(a, j + 3)[d];
+            acc = acc + w[j] * k0;
+            acc = acc + w[j + 1] * k1;
+            acc = acc + w[j + 2] * k2;
+            acc = acc + w[j + 3] * k3;
+        }
+        for (; j < nk; ++j) acc = acc + w[j] * wh_attn_key(a, j)[d];
+    }
+    __syncthreads();
+    const float den = denom_s[wave];
+    if (den > 0.0f) acc = acc / den;
+    res[wave * 64 + lane] = acc;
+    __syncthreads();
+    // inverse RoPE: the even lane of a pair in [nope_dim, head_dim) rotates it
+    if (d >= a.nope_dim && ((d - a.nope_dim) & 1) == 0 && (d - a.nope_dim) / 2 < a.pairs) {
+        const uint32_t p = (d - a.nope_dim) / 2;
+        const float ang = (float)a.token_pos * a.inv_freqs[p];
+        const float sn = -wh_sincosf_glibc(ang, 0);
+        const float cs = wh_sincosf_glibc(ang, 1);
+        const float e = res[wave * 64 + lane], o = res[wave * 64 + lane + 1];
+        res[wave * 64 + lane] = e * cs - o * sn;
+        res[wave * 64 + lane + 1] = e * sn + o * cs;
+    }
+    __syncthreads();
+    if (hon) a.out[(size_t)h * a.head_dim + d] = res[wave * 64 + lane];
+}

@@ -20,6 +20,7 @@
 #include "libm_tables.inc"
 #define WH_LIBM_TABLES_INCLUDED 1
 #include "kernels.h"
+#include "mla.h"
 #include "moe_batch.h"
 #include "moe_mx.h"
 #include "quant_block.h"
@@ -258,6 +259,8 @@ struct wh_ctx {
     Scratch relayout;  // raw FP4 rows on their way into the resident layout
     Scratch rtr;       // router: logits, available ids, outputs of the host-slice call
     Scratch rtr_cnt;   // router: arrival counter of the one-launch bf16 kernel (kept at 0)
+    Scratch mla;       // MLA decode attention: activations between the projections
+    std::map<std::string, float*> rope_tabs;  // device RoPE inverse frequencies by (dim, theta, YaRN)
     std::map<uint32_t, Router> routers;
     HostBuf stage_in, stage_out;
     HostBuf pack[2];   // experts-pack read buffers (one filling while the other uploads)
@@ -1505,8 +1508,9 @@ int wh_shutdown(wh_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     c->arena.release_all();
     for (Scratch* s : {&c->x_in, &c->y_out, &c->h, &c->ybuf, &c->cnt_y, &c->tmp, &c->batch, &c->routes, &c->bout,
-                       &c->gu, &c->relayout, &c->rtr, &c->rtr_cnt})
+                       &c->gu, &c->relayout, &c->rtr, &c->rtr_cnt, &c->mla})
         if (s->p) (void)hipFree(s->p);
+    for (auto& kv : c->rope_tabs) (void)hipFree(kv.second);
     for (auto& kv : c->tables)
         if (kv.second.dev) (void)hipFree(kv.second.dev);
     for (HostBuf* h : {&c->stage_in, &c->stage_out, &c->pack[0], &c->pack[1]})
@@ -2743,3 +2747,303 @@ int wh_debug_eval(wh_ctx* c, int fn, const float* in, float* out, size_t n) {
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------- MLA glue
+namespace {
+// rope_inv_freqs (E/compute.rs:2591-2620) in the reference's f32 arithmetic
+// with the platform libm (powf, logf), on the host: a per-layer constant.
+void rope_inv_freqs_host(size_t rope_dim, float theta, const wh_yarn* yarn, float* out) {
+    const size_t pairs = rope_dim / 2;
+    for (size_t p = 0; p < pairs; ++p) out[p] = powf(theta, -(float)(2 * p) / (float)rope_dim);
+    if (!yarn || yarn->original_seq_len == 0) return;
+    const float dim = (float)rope_dim;
+    const float base_ln = logf(theta);
+    const float pi = 3.14159265358979323846f;
+    auto correction_dim = [&](float rotations) {
+        return dim * logf((float)yarn->original_seq_len / (rotations * 2.0f * pi)) / (2.0f * base_ln);
+    };
+    const float low = fmaxf(floorf(correction_dim(yarn->beta_fast)), 0.0f);
+    float high = fminf(ceilf(correction_dim(yarn->beta_slow)), dim - 1.0f);
+    if (fabsf(low - high) < 1.1920929e-7f) high = low + 0.001f;
+    for (size_t p = 0; p < pairs; ++p) {
+        float ramp = ((float)p - low) / (high - low);
+        ramp = ramp < 0.0f ? 0.0f : (ramp > 1.0f ? 1.0f : ramp);
+        const float smooth = 1.0f - ramp;
+        out[p] = out[p] / yarn->factor * (1.0f - smooth) + out[p] * smooth;
+    }
+}
+
+// DEEPSEEK_V4_COMPRESS_RATIOS (E/compute.rs:2552-2555): 0 = sliding window only.
+const uint32_t kCompressRatios[44] = {0, 0, 4, 128, 4, 128, 4, 128, 4, 128, 4, 128, 4, 128, 4,
+                                      128, 4, 128, 4, 128, 4, 128, 4, 128, 4, 128, 4, 128, 4, 128,
+                                      4, 128, 4, 128, 4, 128, 4, 128, 4, 128, 4, 128, 4, 0};
+
+// The device copy of a layer type's inverse frequencies, made once.
+int rope_table(wh_ctx* c, size_t rope_dim, float theta, const wh_yarn* yarn, const float** out) {
+    char key[128];
+    snprintf(key, sizeof key, "%zu/%08x/%d/%08x/%08x/%08x/%zu", rope_dim, wh_float_to_bits(theta), yarn != nullptr,
+             yarn ? wh_float_to_bits(yarn->factor) : 0u, yarn ? wh_float_to_bits(yarn->beta_fast) : 0u,
+             yarn ? wh_float_to_bits(yarn->beta_slow) : 0u, yarn ? yarn->original_seq_len : (size_t)0);
+    auto it = c->rope_tabs.find(key);
+    if (it == c->rope_tabs.end()) {
+        std::vector<float> host(rope_dim / 2 + 1);
+        rope_inv_freqs_host(rope_dim, theta, yarn, host.data());
+        float* dev = nullptr;
+        WH_HIP(hipMalloc(&dev, host.size() * sizeof(float)));
+        const hipError_t e = hipMemcpy(dev, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(dev);
+            return WH_HIP_ERROR;
+        }
+        it = c->rope_tabs.emplace(key, dev).first;
+    }
+    *out = it->second;
+    return WH_OK;
+}
+
+int rowpost_launch(wh_ctx* c, const wh_rowpost_args& a) {
+    if (a.rows == 0) return WH_OK;
+    k_rowpost<<<a.rows, 256, 0, c->stream>>>(a);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+wh_rowpost_args rowpost_args(const float* x, float* out, size_t rows, size_t n, size_t ld_in, size_t ld_out) {
+    wh_rowpost_args a{};
+    a.x = x;
+    a.out = out;
+    a.rows = (uint32_t)rows;
+    a.n = (uint32_t)n;
+    a.ld_in = (uint32_t)ld_in;
+    a.ld_out = (uint32_t)ld_out;
+    return a;
+}
+
+int attn_launch(wh_ctx* c, const wh_attn_args& a) {
+    const unsigned gy = (a.heads + 3) / 4, nk = a.n_win + a.n_comp;
+    k_attn_scores<<<dim3((nk + 63) / 64, gy), 256, 0, c->stream>>>(a);
+    k_attn_combine<<<dim3(a.head_dim / 64, gy), 256, 0, c->stream>>>(a);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+int attn_check(size_t heads, size_t head_dim, size_t nope_dim, size_t pairs, size_t n_keys, size_t token_pos) {
+    if (heads == 0 || head_dim == 0) return WH_EMPTY_SHAPE;
+    if (nope_dim + 2 * pairs > head_dim || (nope_dim & 1)) return WH_INVALID_SHAPE;
+    if (head_dim % 64 || head_dim > WH_ATTN_MAX_HEAD_DIM || n_keys == 0 || n_keys > WH_ATTN_MAX_KEYS ||
+        heads > 65535u * 4 || token_pos >= (1u << 24))
+        return WH_UNSUPPORTED;
+    return WH_OK;
+}
+}  // namespace
+
+int wh_rope_inv_freqs(size_t rope_dim, float theta, const wh_yarn* yarn, float* out, size_t out_len) {
+    if (!out && rope_dim / 2) return WH_INVALID_ARGUMENT;
+    if (out_len < rope_dim / 2) return WH_OUTPUT_TOO_SMALL;
+    rope_inv_freqs_host(rope_dim, theta, yarn, out);
+    return WH_OK;
+}
+
+int wh_deepseek_rope_for_layer(uint32_t physical_layer, float* theta, wh_yarn* yarn, int* has_yarn) {
+    if (!theta || !yarn || !has_yarn) return WH_INVALID_ARGUMENT;
+    const uint32_t ratio = physical_layer < 44 ? kCompressRatios[physical_layer] : 0u;
+    *has_yarn = ratio > 0;
+    *theta = ratio > 0 ? 160000.0f : 10000.0f;
+    yarn->factor = 16.0f;
+    yarn->beta_fast = 32.0f;
+    yarn->beta_slow = 1.0f;
+    yarn->original_seq_len = 65536;
+    return WH_OK;
+}
+
+int wh_rms_norm_async(wh_ctx* c, const float* x_dev, float* out_dev, size_t rows, size_t n,
+                      const uint16_t* weight_bf16_dev) {
+    if (!c || !x_dev || !out_dev) return WH_INVALID_ARGUMENT;
+    if (rows == 0 || n == 0) return WH_OK;  // E/compute.rs:7111-7113: an empty slice is left alone
+    if (n > WH_ROWPOST_MAX || rows > 0x7fffffffu) return WH_UNSUPPORTED;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    wh_rowpost_args a = rowpost_args(x_dev, out_dev, rows, n, n, n);
+    a.norm = 1;
+    a.w = weight_bf16_dev;
+    return rowpost_launch(c, a);
+}
+
+int wh_rope_async(wh_ctx* c, float* values_dev, size_t rows, size_t row_stride, size_t offset,
+                  const float* inv_freqs_dev, size_t pairs, size_t position, int inverse) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    if (pairs == 0 || rows == 0) return WH_OK;  // E/compute.rs:2630-2632
+    if (!values_dev || !inv_freqs_dev) return WH_INVALID_ARGUMENT;
+    if (offset + 2 * pairs > row_stride) return WH_INVALID_SHAPE;  // "RoPE input shorter than dim"
+    if (row_stride > WH_ROWPOST_MAX || rows > 0x7fffffffu || position >= (1u << 24)) return WH_UNSUPPORTED;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    wh_rowpost_args a = rowpost_args(values_dev, values_dev, rows, row_stride, row_stride, row_stride);
+    a.inv_freqs = inv_freqs_dev;
+    a.pairs = (uint32_t)pairs;
+    a.rope_off = (uint32_t)offset;
+    a.position = (uint32_t)position;
+    a.inverse = inverse != 0;
+    return rowpost_launch(c, a);
+}
+
+int wh_act_quant_dequant_async(wh_ctx* c, float* values_dev, size_t n, size_t block) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    if (block == 0 || n == 0) return WH_OK;  // E/compute.rs:2505-2507
+    if (!values_dev) return WH_INVALID_ARGUMENT;
+    if (n > 0xffffffffu || (n + block - 1) / block > 0x7fffffffu) return WH_UNSUPPORTED;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    k_act_quant_inplace<<<(unsigned)((n + block - 1) / block), 256, 0, c->stream>>>(values_dev, (uint32_t)n,
+                                                                                     (uint32_t)block);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+int wh_window_attention_async(wh_ctx* c, const float* q_dev, size_t heads, size_t head_dim, size_t nope_dim,
+                              const float* window_dev, size_t n_window, size_t window_stride, const float* comp_dev,
+                              size_t n_comp, const float* sink_dev, const float* inv_freqs_dev, size_t pairs,
+                              size_t token_pos, float* scores_dev, float* out_dev) {
+    if (!c || !q_dev || !out_dev || !scores_dev || (n_window && !window_dev) || (n_comp && !comp_dev) ||
+        (pairs && !inv_freqs_dev))
+        return WH_INVALID_ARGUMENT;
+    WH_TRY(attn_check(heads, head_dim, nope_dim, pairs, n_window + n_comp, token_pos));
+    if (n_window > 1 && window_stride < head_dim) return WH_INVALID_SHAPE;
+    if (window_stride > 0xffffffffu) return WH_UNSUPPORTED;
+    // the score kernel reads keys as float4
+    if ((window_stride & 3) || ((uintptr_t)window_dev & 15) || ((uintptr_t)comp_dev & 15)) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    wh_attn_args a{};
+    a.q = q_dev;
+    a.win = window_dev;
+    a.comp = comp_dev;
+    a.sink = sink_dev;
+    a.inv_freqs = inv_freqs_dev;
+    a.scores = scores_dev;
+    a.out = out_dev;
+    a.heads = (uint32_t)heads;
+    a.head_dim = (uint32_t)head_dim;
+    a.nope_dim = (uint32_t)nope_dim;
+    a.pairs = (uint32_t)pairs;
+    a.n_win = (uint32_t)n_window;
+    a.n_comp = (uint32_t)n_comp;
+    a.win_ld = (uint32_t)window_stride;
+    a.token_pos = (uint32_t)token_pos;
+    a.scale = powf((float)head_dim, -0.5f);
+    return attn_launch(c, a);
+}
+
+int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token_pos, float* hidden_dev,
+                                  float* kv_cache_dev, size_t kv_stride, size_t kv_capacity, const float* comp_dev,
+                                  size_t n_comp) {
+    if (!c || !L || !hidden_dev || !kv_cache_dev || (n_comp && !comp_dev)) return WH_INVALID_ARGUMENT;
+    const size_t heads = L->heads, nope = L->nope_dim, rope = L->rope_dim, head_dim = nope + rope;
+    const size_t q_full = heads * head_dim, groups = L->o_groups, o_lora = L->o_lora_rank;
+    // E/compute.rs:3932-3950
+    if (groups == 0 || o_lora == 0 || q_full == 0 || q_full % groups != 0) return WH_INVALID_SHAPE;
+    if (rope % 2) return WH_INVALID_SHAPE;  // "RoPE dim must be even"
+    const size_t group_in = q_full / groups, o_mid = groups * o_lora, pairs = rope / 2;
+    if (kv_stride < head_dim || token_pos >= kv_capacity) return WH_INVALID_SHAPE;  // "MLA KV cache layout mismatch"
+    const size_t context = token_pos + 1, window_start = context > 128 ? context - 128 : 0;
+    const size_t n_win = context - window_start;
+    WH_TRY(attn_check(heads, head_dim, nope, pairs, n_win + n_comp, token_pos));
+    std::lock_guard<std::mutex> lk(c->mu);
+    const Tensor* wq_a = find_tensor(c, L->wq_a);
+    const Tensor* wq_b = find_tensor(c, L->wq_b);
+    const Tensor* wkv = find_tensor(c, L->wkv);
+    const Tensor* wo_a = find_tensor(c, L->wo_a);
+    const Tensor* wo_b = find_tensor(c, L->wo_b);
+    if (!wq_a || !wq_b || !wkv || !wo_a || !wo_b) return WH_NOT_RESIDENT;
+    for (const Tensor* t : {wq_a, wq_b, wkv, wo_a, wo_b})
+        if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
+    const size_t hidden = wq_a->cols, q_lora = wq_a->rows;
+    if (wkv->cols != hidden || wkv->rows != head_dim || wq_b->cols != q_lora || wq_b->rows != q_full ||
+        wo_a->cols != group_in || wo_a->rows != o_mid || wo_b->cols != o_mid || wo_b->rows != hidden)
+        return WH_INVALID_SHAPE;
+    if (hidden > WH_ROWPOST_MAX || q_lora > WH_ROWPOST_MAX || kv_stride > 0xffffffffu) return WH_UNSUPPORTED;
+    if (((uintptr_t)hidden_dev & 15) || ((uintptr_t)kv_cache_dev & 15) || ((uintptr_t)comp_dev & 15) ||
+        (kv_stride & 3))
+        return WH_INVALID_ARGUMENT;
+    WH_HIP(hipSetDevice(c->device));
+    float theta;
+    wh_yarn yarn;
+    int has_yarn;
+    wh_deepseek_rope_for_layer(L->physical_layer, &theta, &yarn, &has_yarn);
+    const float* inv = nullptr;
+    WH_TRY(rope_table(c, rope, theta, has_yarn ? &yarn : nullptr, &inv));
+    // activations, each 256-byte aligned
+    auto up = [](size_t n) { return (n + 63) & ~(size_t)63; };
+    const size_t nk = n_win + n_comp;
+    const size_t o_xq = 0, o_ql = o_xq + up(hidden), o_q = o_ql + up(q_lora), o_kv = o_q + up(q_full),
+                 o_sc = o_kv + up(head_dim), o_at = o_sc + up(heads * nk), o_om = o_at + up(q_full),
+                 total = o_om + up(o_mid);
+    WH_HIP(c->mla.ensure(total * sizeof(float), false));
+    float* base = c->mla.as<float>();
+    float *xq = base + o_xq, *ql = base + o_ql, *q = base + o_q, *kvt = base + o_kv, *sc = base + o_sc,
+          *at = base + o_at, *om = base + o_om;
+    float* kv_row = kv_cache_dev + token_pos * kv_stride;
+    // q path (E/compute.rs:3998-4040): act-quant of x, wq_a, q norm + act-quant,
+    // wq_b, per-head RMS norm + RoPE
+    wh_rowpost_args a = rowpost_args(hidden_dev, xq, 1, hidden, hidden, hidden);
+    a.aq_len = (uint32_t)hidden;
+    WH_TRY(rowpost_launch(c, a));
+    WH_TRY(launch_fp8(c, *wq_a, 0, q_lora, xq, ql, 1, hidden, q_lora));
+    a = rowpost_args(ql, ql, 1, q_lora, q_lora, q_lora);
+    a.norm = 1;
+    a.w = L->q_norm_bf16;
+    a.aq_len = (uint32_t)q_lora;
+    WH_TRY(rowpost_launch(c, a));
+    WH_TRY(launch_fp8(c, *wq_b, 0, q_full, ql, q, 1, q_lora, q_full));
+    a = rowpost_args(q, q, heads, head_dim, head_dim, head_dim);
+    a.norm = 1;
+    a.inv_freqs = inv;
+    a.pairs = (uint32_t)pairs;
+    a.rope_off = (uint32_t)nope;
+    a.position = (uint32_t)token_pos;
+    WH_TRY(rowpost_launch(c, a));
+    // kv path (E/compute.rs:4046-4075): wkv, kv norm, RoPE, act-quant of the
+    // non-rope dims, into the cache row of this position
+    WH_TRY(launch_fp8(c, *wkv, 0, head_dim, xq, kvt, 1, hidden, head_dim));
+    a = rowpost_args(kvt, kv_row, 1, head_dim, head_dim, head_dim);
+    a.norm = 1;
+    a.w = L->kv_norm_bf16;
+    a.inv_freqs = inv;
+    a.pairs = (uint32_t)pairs;
+    a.rope_off = (uint32_t)nope;
+    a.position = (uint32_t)token_pos;
+    a.aq_len = (uint32_t)nope;
+    WH_TRY(rowpost_launch(c, a));
+    // window softmax with sink (E/compute.rs:4106-4197)
+    wh_attn_args w{};
+    w.q = q;
+    w.win = kv_cache_dev + window_start * kv_stride;
+    w.comp = comp_dev;
+    w.sink = L->sink;
+    w.inv_freqs = inv;
+    w.scores = sc;
+    w.out = at;
+    w.heads = (uint32_t)heads;
+    w.head_dim = (uint32_t)head_dim;
+    w.nope_dim = (uint32_t)nope;
+    w.pairs = (uint32_t)pairs;
+    w.n_win = (uint32_t)n_win;
+    w.n_comp = (uint32_t)n_comp;
+    w.win_ld = (uint32_t)kv_stride;
+    w.token_pos = (uint32_t)token_pos;
+    w.scale = powf((float)head_dim, -0.5f);
+    WH_TRY(attn_launch(c, w));
+    // grouped output projection (E/compute.rs:4222-4270)
+    k_act_quant_inplace<<<(unsigned)((q_full + 63) / 64), 256, 0, c->stream>>>(at, (uint32_t)q_full, 64);
+    if (fp8_split_k(*wo_a) && is_pow2(o_lora) && o_lora >= WH_FP8_SK_ROWS && group_in <= 0xffffffffu) {
+        WH_TRY(launch_fp8(c, *wo_a, 0, o_mid, at, om, 1, group_in, o_mid, o_lora, group_in));
+    } else {
+        for (size_t g = 0; g < groups; ++g)
+            WH_TRY(launch_fp8(c, *wo_a, g * o_lora, (g + 1) * o_lora, at + g * group_in, om + g * o_lora, 1,
+                              group_in, o_lora));
+    }
+    k_act_quant_inplace<<<(unsigned)((o_mid + 63) / 64), 256, 0, c->stream>>>(om, (uint32_t)o_mid, 64);
+    WH_TRY(launch_fp8(c, *wo_b, 0, hidden, om, hidden_dev, 1, o_mid, hidden));
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
