@@ -565,6 +565,41 @@ int wh_mla_attention_decode_async(wh_ctx* ctx, const wh_mla_layer* layer, size_t
                                   float* kv_cache_dev, size_t kv_stride, size_t kv_capacity, const float* comp_dev,
                                   size_t n_comp);
 
+/* ------------------------------------------------------------------
+ * mHC hyper-connections (E/compute.rs:4945-5092), device pointers, f32.
+ * hc copies of the hidden state form a stream of hc * hidden floats;
+ * mix_hc = (2 + hc) * hc; hc <= 14.
+ * ------------------------------------------------------------------ */
+
+/* hc_split_sinkhorn_scalar (E/compute.rs:4945-5014): pre[hc] =
+ * sigmoid(mixes * scale[0] + base) + eps, post[hc] = 2 sigmoid(mixes[hc..] *
+ * scale[1] + base[hc..]), comb[hc][hc] = row softmax(mixes[2hc..] * scale[2]
+ * + base[2hc..]) + eps, normalised by columns once and then by rows and
+ * columns sinkhorn_iters - 1 more times.  Bit-identical to the reference
+ * (glibc-exact expf, sums in order). */
+int wh_hc_split_sinkhorn_async(wh_ctx* ctx, const float* mixes_dev, const float* scale_dev, const float* base_dev,
+                               size_t hc, size_t sinkhorn_iters, float eps, float* pre_dev, float* post_dev,
+                               float* comb_dev);
+
+/* hc_pre_into (E/compute.rs:5016-5050): mixes[j] = (fn row j . x) *
+ * 1 / sqrt(mean(x^2) + eps) for the mix_hc rows of fn_dev ([mix_hc][hc *
+ * hidden]), then hc_split_sinkhorn, then y[d] = sum over i of pre[i] *
+ * x[i * hidden + d].  post_dev[hc] and comb_dev[hc * hc] receive what
+ * hc_post needs.  With exact numerics (the default) the dot products and
+ * the sum of squares run in the reference's order, bit-identical; with
+ * exact numerics off they are summed over many workgroups in a fixed tree
+ * (same value up to rounding, reproducible), everything after them still
+ * in the reference's order. */
+int wh_hc_pre_async(wh_ctx* ctx, const float* fn_dev, const float* scale_dev, const float* base_dev, size_t hc,
+                    size_t hidden, size_t sinkhorn_iters, float eps, const float* x_dev, float* y_dev,
+                    float* post_dev, float* comb_dev);
+
+/* hc_post_into (E/compute.rs:5055-5092): out[k * hidden + d] = post[k] *
+ * y[d] + sum over i (in order) of comb[k * hc + i] * residual[i * hidden +
+ * d].  Bit-identical to the reference. */
+int wh_hc_post_async(wh_ctx* ctx, const float* y_dev, const float* residual_dev, const float* post_dev,
+                     const float* comb_dev, float* out_dev, size_t hc, size_t hidden);
+
 #ifdef __cplusplus
 }
 #endif

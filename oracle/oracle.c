@@ -883,3 +883,94 @@ void or_window_attention(const float* q, size_t heads, size_t head_dim, size_t n
         or_rope_apply(oh + nope_dim, token_pos, inv, pairs, 1);
     }
 }
+
+/* ------------------------------------------------------ mHC (hyper-connections) */
+
+static float or_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+static void or_comb_rows(float* comb, size_t hc, float eps) {
+    for (size_t j = 0; j < hc; ++j) {
+        float s = 0.0f;
+        for (size_t k = 0; k < hc; ++k) s += comb[j * hc + k];
+        for (size_t k = 0; k < hc; ++k) comb[j * hc + k] /= s + eps;
+    }
+}
+
+static void or_comb_cols(float* comb, size_t hc, float eps) {
+    for (size_t k = 0; k < hc; ++k) {
+        float s = 0.0f;
+        for (size_t j = 0; j < hc; ++j) s += comb[j * hc + k];
+        for (size_t j = 0; j < hc; ++j) comb[j * hc + k] /= s + eps;
+    }
+}
+
+/* hc_split_sinkhorn_scalar (E/compute.rs:4945-5000) with normalize_comb_rows
+ * / normalize_comb_cols (E/compute.rs:4992-5014): pre = sigmoid(m*s0 + b) +
+ * eps, post = 2 sigmoid(m*s1 + b), comb = row softmax(m*s2 + b) + eps, one
+ * column normalisation, then iters - 1 rounds of rows then columns. */
+int or_hc_split_sinkhorn(const float* mixes, const float* scale, const float* base, size_t hc, size_t iters,
+                         float eps, float* pre, float* post, float* comb) {
+    for (size_t j = 0; j < hc; ++j) {
+        pre[j] = or_sigmoid(mixes[j] * scale[0] + base[j]) + eps;
+        post[j] = 2.0f * or_sigmoid(mixes[j + hc] * scale[1] + base[j + hc]);
+    }
+    for (size_t j = 0; j < hc; ++j)
+        for (size_t k = 0; k < hc; ++k)
+            comb[j * hc + k] = mixes[2 * hc + j * hc + k] * scale[2] + base[2 * hc + j * hc + k];
+    for (size_t j = 0; j < hc; ++j) {
+        float* row = comb + j * hc;
+        float mx = -INFINITY;
+        for (size_t k = 0; k < hc; ++k) mx = fmaxf(mx, row[k]);
+        float s = 0.0f;
+        for (size_t k = 0; k < hc; ++k) {
+            row[k] = expf(row[k] - mx);
+            s += row[k];
+        }
+        for (size_t k = 0; k < hc; ++k) row[k] = row[k] / s + eps;
+    }
+    or_comb_cols(comb, hc, eps);
+    for (size_t it = 1; it < iters; ++it) {
+        or_comb_rows(comb, hc, eps);
+        or_comb_cols(comb, hc, eps);
+    }
+    return OR_OK;
+}
+
+/* hc_pre_into (E/compute.rs:5016-5050): fn [mix_hc][hc * hidden] f32;
+ * mixes_out (optional) receives the pre-sinkhorn mixes. */
+int or_hc_pre(const float* fn, const float* scale, const float* base, size_t hc, size_t hidden, size_t iters,
+              float eps, const float* x, float* y, float* pre, float* post, float* comb, float* mixes_out) {
+    const size_t hc_dim = hc * hidden, mix_hc = (2 + hc) * hc;
+    float s = 0.0f;
+    for (size_t i = 0; i < hc_dim; ++i) s += x[i] * x[i];
+    const float ms = s / (float)hc_dim;
+    const float inv = 1.0f / sqrtf(ms + eps);
+    float* mixes = (float*)malloc(mix_hc * sizeof(float));
+    if (!mixes) return OR_SCRATCH_TOO_SMALL;
+    for (size_t j = 0; j < mix_hc; ++j) {
+        float acc = 0.0f;
+        for (size_t i = 0; i < hc_dim; ++i) acc += fn[j * hc_dim + i] * x[i];
+        mixes[j] = acc * inv;
+    }
+    if (mixes_out) memcpy(mixes_out, mixes, mix_hc * sizeof(float));
+    or_hc_split_sinkhorn(mixes, scale, base, hc, iters, eps, pre, post, comb);
+    free(mixes);
+    for (size_t d = 0; d < hidden; ++d) {
+        float acc = 0.0f;
+        for (size_t i = 0; i < hc; ++i) acc += pre[i] * x[i * hidden + d];
+        y[d] = acc;
+    }
+    return OR_OK;
+}
+
+/* hc_post_into (E/compute.rs:5055-5092): out[k] = post[k] * y + sum over i
+ * of comb[k][i] * residual[i], the sum from the post term in order of i. */
+void or_hc_post(const float* y, const float* residual, const float* post, const float* comb, float* out, size_t hc,
+                size_t hidden) {
+    for (size_t k = 0; k < hc; ++k)
+        for (size_t d = 0; d < hidden; ++d) {
+            float acc = post[k] * y[d];
+            for (size_t i = 0; i < hc; ++i) acc += comb[k * hc + i] * residual[i * hidden + d];
+            out[k * hidden + d] = acc;
+        }
+}

@@ -77,6 +77,9 @@ def lib():
             "or_rope_inv_freqs": (None, [sz, c.c_float, c.c_int, c.c_float, c.c_float, c.c_float, sz, f32p]),
             "or_rope_apply": (None, [f32p, sz, f32p, sz, c.c_int]),
             "or_window_attention": (None, [f32p, sz, sz, sz, f32p, sz, sz, f32p, sz, f32p, f32p, sz, sz, f32p]),
+            "or_hc_split_sinkhorn": (c.c_int, [f32p, f32p, f32p, sz, sz, c.c_float, f32p, f32p, f32p]),
+            "or_hc_pre": (c.c_int, [f32p, f32p, f32p, sz, sz, sz, c.c_float, f32p, f32p, f32p, f32p, f32p, f32p]),
+            "or_hc_post": (None, [f32p, f32p, f32p, f32p, f32p, sz, sz]),
             "or_route_select": (c.c_int, [f32p, sz, f32p, c.POINTER(c.c_uint32), sz, sz, c.c_int, c.c_float,
                                           c.POINTER(c.c_uint32), sz, c.POINTER(c.c_uint32), f32p,
                                           c.POINTER(sz)]),
@@ -449,3 +452,34 @@ def mla_attention_decode(x, proj, q_norm, kv_norm, sink, heads, nope_dim, rope_d
     om = np.concatenate([proj["wo_a_group"](g, att[g * group_in:(g + 1) * group_in]) for g in range(o_groups)])
     om = act_quant(om, 64)
     return proj["wo_b"](om)
+
+
+# ---------------------------------------------------------------------- mHC
+
+def hc_split_sinkhorn(mixes, scale, base, hc: int, iters: int = 20, eps: float = 1e-6):
+    """hc_split_sinkhorn_scalar (E/compute.rs:4945-5014): (pre, post, comb)."""
+    m, s, b = _f(mixes), _f(scale), _f(base)
+    pre, post, comb = np.zeros(hc, np.float32), np.zeros(hc, np.float32), np.zeros(hc * hc, np.float32)
+    lib().or_hc_split_sinkhorn(_pf(m), _pf(s), _pf(b), hc, iters, eps, _pf(pre), _pf(post), _pf(comb))
+    return pre, post, comb
+
+
+def hc_pre(fn, scale, base, x, hc: int, hidden: int, iters: int = 20, eps: float = 1e-6):
+    """hc_pre_into (E/compute.rs:5016-5050): (y, pre, post, comb, mixes)."""
+    f, s, b, xx = _f(fn), _f(scale), _f(base), _f(x)
+    mix_hc = (2 + hc) * hc
+    y = np.zeros(hidden, np.float32)
+    pre, post, comb = np.zeros(hc, np.float32), np.zeros(hc, np.float32), np.zeros(hc * hc, np.float32)
+    mixes = np.zeros(mix_hc, np.float32)
+    st = lib().or_hc_pre(_pf(f), _pf(s), _pf(b), hc, hidden, iters, eps, _pf(xx), _pf(y), _pf(pre), _pf(post),
+                         _pf(comb), _pf(mixes))
+    if st:
+        raise OracleError(st)
+    return y, pre, post, comb, mixes
+
+
+def hc_post(y, residual, post, comb, hc: int, hidden: int):
+    """hc_post_into (E/compute.rs:5055-5092)."""
+    out = np.zeros(hc * hidden, np.float32)
+    lib().or_hc_post(_pf(_f(y)), _pf(_f(residual)), _pf(_f(post)), _pf(_f(comb)), _pf(out), hc, hidden)
+    return out

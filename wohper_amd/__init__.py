@@ -88,6 +88,7 @@ EXPORTED = (
     "wh_routed_and_shared_experts_noalloc_async",
     "wh_rope_inv_freqs", "wh_deepseek_rope_for_layer", "wh_rms_norm_async", "wh_rope_async",
     "wh_act_quant_dequant_async", "wh_window_attention_async", "wh_mla_attention_decode_async",
+    "wh_hc_split_sinkhorn_async", "wh_hc_pre_async", "wh_hc_post_async",
 )
 
 ROUTER_RAW_LOGITS = 0
@@ -239,6 +240,9 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_act_quant_dequant_async": (c.c_int, [vp, vp, sz, sz]),
         "wh_window_attention_async": (c.c_int, [vp, vp, sz, sz, sz, vp, sz, sz, vp, sz, vp, vp, sz, sz, vp, vp]),
         "wh_mla_attention_decode_async": (c.c_int, [vp, c.POINTER(WhMlaLayer), sz, vp, vp, sz, sz, vp, sz]),
+        "wh_hc_split_sinkhorn_async": (c.c_int, [vp, vp, vp, vp, sz, sz, c.c_float, vp, vp, vp]),
+        "wh_hc_pre_async": (c.c_int, [vp, vp, vp, vp, sz, sz, sz, c.c_float, vp, vp, vp, vp]),
+        "wh_hc_post_async": (c.c_int, [vp, vp, vp, vp, vp, vp, sz, sz]),
         "wh_route_experts_async": (c.c_int, [vp, c.c_uint32, vp, sz, sz, vp, sz, c.POINTER(WhRouteOptions), vp, vp,
                                              vp]),
     }
@@ -631,6 +635,22 @@ class Context:
         _check(self.lib.wh_mla_attention_decode_async(self._h, ctypes.byref(layer), token_pos, hidden_ptr, kv_ptr,
                                                       kv_stride, kv_capacity, comp_ptr or None, n_comp),
                "mla_attention_decode_async")
+
+    # ------------------------------------------------------------------ mHC
+    def hc_split_sinkhorn_async(self, mixes_ptr: int, scale_ptr: int, base_ptr: int, hc: int, iters: int,
+                                eps: float, pre_ptr: int, post_ptr: int, comb_ptr: int):
+        _check(self.lib.wh_hc_split_sinkhorn_async(self._h, mixes_ptr, scale_ptr, base_ptr, hc, iters, eps, pre_ptr,
+                                                   post_ptr, comb_ptr), "hc_split_sinkhorn_async")
+
+    def hc_pre_async(self, fn_ptr: int, scale_ptr: int, base_ptr: int, hc: int, hidden: int, iters: int, eps: float,
+                     x_ptr: int, y_ptr: int, post_ptr: int, comb_ptr: int):
+        _check(self.lib.wh_hc_pre_async(self._h, fn_ptr, scale_ptr, base_ptr, hc, hidden, iters, eps, x_ptr, y_ptr,
+                                        post_ptr, comb_ptr), "hc_pre_async")
+
+    def hc_post_async(self, y_ptr: int, res_ptr: int, post_ptr: int, comb_ptr: int, out_ptr: int, hc: int,
+                      hidden: int):
+        _check(self.lib.wh_hc_post_async(self._h, y_ptr, res_ptr, post_ptr, comb_ptr, out_ptr, hc, hidden),
+               "hc_post_async")
 
     def set_exact_numerics(self, on: bool):
         """True (default): routed-expert matvecs in the reference kernel's

@@ -20,6 +20,7 @@
 #include "libm_tables.inc"
 #define WH_LIBM_TABLES_INCLUDED 1
 #include "kernels.h"
+#include "mhc.h"
 #include "mla.h"
 #include "moe_batch.h"
 #include "moe_mx.h"
@@ -260,6 +261,7 @@ struct wh_ctx {
     Scratch rtr;       // router: logits, available ids, outputs of the host-slice call
     Scratch rtr_cnt;   // router: arrival counter of the one-launch bf16 kernel (kept at 0)
     Scratch mla;       // MLA decode attention: activations between the projections
+    Scratch hcs;       // mHC: chain sums and the internal pre weights
     std::map<std::string, float*> rope_tabs;  // device RoPE inverse frequencies by (dim, theta, YaRN)
     std::map<uint32_t, Router> routers;
     HostBuf stage_in, stage_out;
@@ -1508,7 +1510,7 @@ int wh_shutdown(wh_ctx* c) {
     (void)hipStreamSynchronize(c->stream);
     c->arena.release_all();
     for (Scratch* s : {&c->x_in, &c->y_out, &c->h, &c->ybuf, &c->cnt_y, &c->tmp, &c->batch, &c->routes, &c->bout,
-                       &c->gu, &c->relayout, &c->rtr, &c->rtr_cnt, &c->mla})
+                       &c->gu, &c->relayout, &c->rtr, &c->rtr_cnt, &c->mla, &c->hcs})
         if (s->p) (void)hipFree(s->p);
     for (auto& kv : c->rope_tabs) (void)hipFree(kv.second);
     for (auto& kv : c->tables)
@@ -3044,6 +3046,90 @@ int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token
     }
     k_act_quant_inplace<<<(unsigned)((o_mid + 63) / 64), 256, 0, c->stream>>>(om, (uint32_t)o_mid, 64);
     WH_TRY(launch_fp8(c, *wo_b, 0, hidden, om, hidden_dev, 1, o_mid, hidden));
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// ------------------------------------------------------------------ mHC
+namespace {
+int hc_check(size_t hc, size_t hidden) {
+    if (hc == 0 || hidden == 0) return WH_INVALID_SHAPE;  // "hc_pre sizes"
+    if ((2 + hc) * hc + 1 > WH_HC_MAX_CHAINS || hc * hidden > 0xffffffffu) return WH_UNSUPPORTED;
+    return WH_OK;
+}
+
+wh_hc_args hc_args(size_t hc, size_t hidden, size_t iters, float eps) {
+    wh_hc_args a{};
+    a.hc = (uint32_t)hc;
+    a.hidden = (uint32_t)hidden;
+    a.hc_dim = (uint32_t)(hc * hidden);
+    a.mix_hc = (uint32_t)((2 + hc) * hc);
+    a.iters = (uint32_t)std::min<size_t>(iters, 0x7fffffffu);
+    a.eps = eps;
+    return a;
+}
+}  // namespace
+
+int wh_hc_split_sinkhorn_async(wh_ctx* c, const float* mixes_dev, const float* scale_dev, const float* base_dev,
+                               size_t hc, size_t sinkhorn_iters, float eps, float* pre_dev, float* post_dev,
+                               float* comb_dev) {
+    if (!c || !mixes_dev || !scale_dev || !base_dev || !pre_dev || !post_dev || !comb_dev) return WH_INVALID_ARGUMENT;
+    WH_TRY(hc_check(hc, 1));
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    wh_hc_args a = hc_args(hc, 1, sinkhorn_iters, eps);
+    a.scale = scale_dev;
+    a.base = base_dev;
+    a.mixes_in = mixes_dev;
+    a.pre = pre_dev;
+    a.post = post_dev;
+    a.comb = comb_dev;
+    k_hc_finish<<<1, 256, 0, c->stream>>>(a);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+int wh_hc_pre_async(wh_ctx* c, const float* fn_dev, const float* scale_dev, const float* base_dev, size_t hc,
+                    size_t hidden, size_t sinkhorn_iters, float eps, const float* x_dev, float* y_dev,
+                    float* post_dev, float* comb_dev) {
+    if (!c || !fn_dev || !scale_dev || !base_dev || !x_dev || !y_dev || !post_dev || !comb_dev)
+        return WH_INVALID_ARGUMENT;
+    WH_TRY(hc_check(hc, hidden));
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    wh_hc_args a = hc_args(hc, hidden, sinkhorn_iters, eps);
+    a.fn = fn_dev;
+    a.scale = scale_dev;
+    a.base = base_dev;
+    a.x = x_dev;
+    a.y = y_dev;
+    a.post = post_dev;
+    a.comb = comb_dev;
+    a.parts = c->exact ? 1u : WH_HC_PARTS;
+    const size_t n_sums = (size_t)WH_HC_PARTS * (a.mix_hc + 1);
+    WH_HIP(c->hcs.ensure((n_sums + 16) * sizeof(float), false));
+    a.sums = c->hcs.as<float>();
+    a.pre = a.sums + n_sums;
+    if (c->exact) {
+        k_hc_chains<<<a.mix_hc + 1, 256, 0, c->stream>>>(a);
+    } else {
+        k_hc_partials<<<dim3(WH_HC_PARTS, a.mix_hc + 1), 256, 0, c->stream>>>(a);
+    }
+    k_hc_finish<<<1, 256, 0, c->stream>>>(a);
+    k_hc_y<<<(unsigned)((hidden + 255) / 256), 256, 0, c->stream>>>(a);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+int wh_hc_post_async(wh_ctx* c, const float* y_dev, const float* residual_dev, const float* post_dev,
+                     const float* comb_dev, float* out_dev, size_t hc, size_t hidden) {
+    if (!c || !y_dev || !residual_dev || !post_dev || !comb_dev || !out_dev) return WH_INVALID_ARGUMENT;
+    WH_TRY(hc_check(hc, hidden));
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    const size_t n = hc * hidden;
+    k_hc_post<<<(unsigned)((n + 255) / 256), 256, 0, c->stream>>>(y_dev, residual_dev, post_dev, comb_dev, out_dev,
+                                                                  (uint32_t)hc, (uint32_t)hidden);
     WH_HIP(hipGetLastError());
     return WH_OK;
 }
