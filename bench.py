@@ -37,7 +37,7 @@ TOKEN_BYTES = 6 * EXPERT_BYTES + 4096 * 2 + 4096 * 4   # + bf16 x + f32 y = 80,2
 GATEUP_BYTES = 6 * 2 * (4_194_304 + 262_144) + 4096 * 2 + 6 * 2048 * 4     # 53,534,720
 DOWN_BYTES = 6 * (4_194_304 + 262_144) + 6 * 2048 * 4 + 4096 * 4           # 26,804,224
 # The routed-expert kernels of each numerics mode (trace names).
-KERNELS = {False: ("k_moe_gateup_mx<2>", "k_moe_down_mx"), True: ("k_moe_gateup<16, 4>", "k_moe_down<8, 4>")}
+KERNELS = {False: ("k_moe_gateup_px<4096, 3>", "k_moe_down_px<3>"), True: ("k_moe_gateup<16, 4>", "k_moe_down<8, 4>")}
 # HBM bytes per gate/up launch: rocprofv3 FETCH_SIZE and WRITE_SIZE KiB per
 # dispatch, scaled by what the same counters read for a 268,435,456-byte copy
 # (FETCH x2.00, WRITE x1.00); see profiles/.  None: not measured.

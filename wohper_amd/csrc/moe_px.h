@@ -1,0 +1,541 @@
+// Persistent routed-expert kernels for decode tokens on block-scaled FP8 MFMA
+// (gfx950): the summation-order-free mode of the token entry points.
+//
+// The reference's expert forward (E/deepseek_v4.rs:551-601) act-quantizes x
+// and h (block 64, power-of-two scales, E/compute.rs:2504-2521) before each
+// FP4 matvec, so every product it forms is exact: an E4M3 code times an FP4
+// LUT value.  These kernels feed the same exact operands to
+// v_mfma_scale_f32_16x16x128_f8f6f4:
+//   A = the weights as E4M3 codes of the reference's x8 LUT integers
+//       {0, 1, 8, 12, 16, 24, 32, 48} (E/deepseek_v4.rs:285-287), two v_perm
+//       lookups per resident dword, with the UE8M0 group scale as the E8M0
+//       A scale;
+//   B = the act-quantized input as E4M3 codes with the E8M0 byte
+//       127 + k - 3 of the block scale 2^k (the -3 takes the x8 back out).
+// Only the order of the fp32 sums differs from the CPU kernel, so every
+// matvec stays within max|diff| <= 1e-5 * ||w_row||_2 * ||x||_2 of it, and
+// the dequantized weights are the reference's values exactly.  A decode
+// token is one B column of the 16; the other columns are don't-cares (each
+// C element depends only on its own row and column).
+//
+// A per-wave timeline of the one-tile-per-workgroup kernels (768 workgroups,
+// 3 per CU) showed each wave spending its time in series on staging x,
+// act-quantizing it (every workgroup redoes all 4096 values) and only then
+// the dot, and the down kernel paying the same for h plus a cross-workgroup
+// routed sum.  Two facts of the hardware shape the kernels here:
+//   * a CU's memory loads complete in issue order, so a small load issued
+//     after a wave of weight loads waits for all of them;
+//   * while the memory system is saturated a wave cannot issue a load until
+//     earlier requests drain, so a wave that requests all of its weight
+//     blocks before some arithmetic reaches that arithmetic late.
+// Hence one workgroup of 8 waves per CU (about), staging loads first, only
+// WH_PX_PRO weight blocks per wave requested before the staged input is
+// act-quantized once per workgroup, and then a ring of register blocks:
+//   k_moe_gateup_px: row tiles kTiles*b .. kTiles*b + kTiles - 1 (16 rows of
+//                    w1 and w3 of one expert each); wave (m, s) runs matrix m
+//                    (w1, w3) over 1024-column slice s of every tile.
+//   k_moe_down_px:   output rows 16b .. 16b + 15 of every expert, so the
+//                    routed sum stays in the workgroup; wave w runs (expert,
+//                    512-column quarter) units w, w + 8, ...
+#pragma once
+#include "moe_batch.h"
+
+#ifndef WH_PX_GU_DEPTH
+#define WH_PX_GU_DEPTH 4  // weight blocks of a gate/up wave in flight
+#endif
+#ifndef WH_PX_DN_DEPTH
+#define WH_PX_DN_DEPTH 4  // weight blocks of a down wave in flight
+#endif
+// Weight blocks a wave requests before the workgroup's staged input is in
+// LDS; the rest of its ring goes out after the act-quant.
+#ifndef WH_PX_PRO
+#define WH_PX_PRO 2
+#endif
+
+// Optional per-wave timeline of the two kernels (build with -DWH_TIMELINE):
+// lane 0 of each wave stores the 100 MHz realtime counter at fixed points of
+// the kernel into wh_tl_buf[kernel][(workgroup * 16 + wave) * 8 + point],
+// for the first 512 workgroups of token 0; wh_debug_timeline reads it back.
+#ifdef WH_TIMELINE
+__device__ uint64_t wh_tl_buf[2][512 * 16 * 8];
+#define WH_TL(kern, k)                                                                                    \
+    do {                                                                                                  \
+        if ((threadIdx.x & 63) == 0 && blockIdx.x < 512 && blockIdx.y == 0 && (threadIdx.x >> 6) < 16)     \
+            wh_tl_buf[kern][((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * 8 + (k)] =                    \
+                __builtin_amdgcn_s_memrealtime();                                                         \
+    } while (0)
+#else
+#define WH_TL(kern, k) \
+    do {               \
+    } while (0)
+#endif
+
+// An execution barrier (no memory fence): every wave of the workgroup has
+// issued its loads up to here before any wave issues the next one.
+__device__ __forceinline__ void wh_issue_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// The B operands of one 256-col block of an input in the record layout (32
+// code bytes per 32-col group, byte 4j + k = column j + 8k of the group; one
+// E8M0 byte per group) in registers: lane group g's half h of MFMA u holds
+// the codes of group 4 (g / 2) + 2u + h, bytes 16 (g % 2) .. + 15.
+struct wh_mx_bop {
+    wh_v8i v[2];
+    uint32_t s[2];
+};
+__device__ __forceinline__ void wh_mx_bop_load(wh_mx_bop& b, const uint8_t* xc, const uint8_t* xsb, uint32_t g) {
+    const uint2 bs8 = *(const uint2*)xsb;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const uint8_t* p = xc + (4 * (g >> 1) + 2 * u) * 32 + 16 * (g & 1);
+        const uint4 lo = *(const uint4*)p, hi = *(const uint4*)(p + 32);
+        b.v[u] = wh_v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        b.s[u] = u ? wh_mfma_sbyte<1>(bs8, g) : wh_mfma_sbyte<0>(bs8, g);
+    }
+}
+// One block of a ring: the weights in r against the B operands bo.  The
+// block's words pass through an opaque zero (dep) tied to the previous
+// block's accumulator, so the decode of block b starts after block b - 1's
+// MFMAs: hoisted decodes would make a wave wait for several blocks' bytes
+// before its first MFMA, and would hold them all in registers.
+__device__ __forceinline__ void wh_px_step(wh_v4f& acc, const wh_mx_raw& r, uint32_t& dep, const wh_mx_bop& bo,
+                                           uint32_t g) {
+    wh_mx_raw rb = r;
+    rb.p.x += dep;
+    rb.p.y += dep;
+    rb.q.x += dep;
+    rb.q.y += dep;
+    const wh_mfma_a a = wh_mx_fix(rb);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const wh_v8i av = u ? wh_mfma_a_codes<1>(a) : wh_mfma_a_codes<0>(a);
+        const uint32_t as = u ? wh_mfma_sbyte<1>(a.s, g) : wh_mfma_sbyte<0>(a.s, g);
+        acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bo.v[u], acc, 0, 0, 0, (int)as, 0, (int)bo.s[u]);
+    }
+    dep = wh_opaque_zero(acc[0]);
+}
+
+// amax over the 64 / kV lanes that hold one 64-block, kV values each (kV = 4
+// or 8; NaN skipped, as f32::max does): quad swaps, then the half-row mirror
+// (8 lanes) and, for kV = 4, the row mirror (16 lanes).
+template <int kV>
+__device__ __forceinline__ float wh_amax_block(float m) {
+    static_assert(kV == 4 || kV == 8, "64-block over 16 or 8 lanes");
+    m = fmaxf(m, wh_dpp_quad_swap1(m));
+    m = fmaxf(m, wh_dpp_quad_swap2(m));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x141, 0xf, 0xf, false)));  // row_half_mirror
+    if constexpr (kV == 4)
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x140, 0xf, 0xf, false)));  // row_mirror
+    return m;
+}
+
+// Act-quant (E/compute.rs:2504-2521, block 64) of kV consecutive values held
+// by one thread, the block's threads being 64 / kV consecutive lanes: q = the
+// E4M3 values before the scale 2^k.  The reference's semantics for
+// non-finite inputs, as wh_xq_quant16: NaN quantizes to -480, an infinite
+// amax gives an infinite scale; bad reports an inf or NaN among the kV.
+template <int kV>
+__device__ __forceinline__ void wh_aq_vals(const float (&v)[kV], const uint32_t* log2_thr, float (&q)[kV], int& k,
+                                           float& sc, bool& bad) {
+    float amax = 0.0f;
+    bad = false;
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+        const float m = fabsf(v[i]);
+        bad |= !(m <= 3.4028235e38f);
+        amax = fmaxf(amax, m);
+    }
+    amax = wh_amax_block<kV>(amax);
+    const bool inf_scale = !(amax <= 3.4028235e38f);
+    k = inf_scale ? 0 : wh_aq_scale_exp(amax, log2_thr);
+    const float inv = inf_scale ? 0.0f : wh_pow2f(-k);  // v / inf is v * 0
+    sc = inf_scale ? __uint_as_float(0x7f800000u) : wh_pow2f(k);
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+        const float t = v[i] * inv;
+        q[i] = t != t ? -480.0f : wh_e4m3_round(wh_clamp448_finite(t));
+    }
+}
+
+// 8 consecutive input values of one thread, bf16 or f32.
+struct wh_in8 {
+    uint4 r0, r1;
+};
+__device__ __forceinline__ void wh_in8_load(wh_in8& st, const void* x, bool bf16, uint32_t c) {
+    if (bf16) {
+        st.r0 = ((const uint4*)x)[c];
+        st.r1 = make_uint4(0, 0, 0, 0);
+    } else {
+        st.r0 = ((const uint4*)x)[2 * c];
+        st.r1 = ((const uint4*)x)[2 * c + 1];
+    }
+}
+__device__ __forceinline__ void wh_in8_values(const wh_in8& st, bool bf16, float (&v)[8]) {
+    const uint32_t w[4] = {st.r0.x, st.r0.y, st.r0.z, st.r0.w};
+    if (bf16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    } else {
+        const uint32_t u[4] = {st.r1.x, st.r1.y, st.r1.z, st.r1.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = __uint_as_float(w[i]);
+            v[4 + i] = __uint_as_float(u[i]);
+        }
+    }
+}
+
+// Stores the codes of the 8 values at columns 8c .. 8c + 7 into a record
+// array and, for the first chunk of a group, its E8M0 byte 127 + k - 3 (the
+// -3 takes back the x8 of the weights' integer codes).
+__device__ __forceinline__ void wh_px_store_codes8(uint8_t* rec, uint8_t* sb, uint32_t c, const float (&q)[8], int k) {
+    uint8_t* grp = rec + 32 * (c >> 2) + (c & 3);  // column 8c + j: byte 4j + c % 4 of group c / 4
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        const uint32_t two = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[j], q[j + 1], 0, false);
+        grp[4 * j] = (uint8_t)two;
+        grp[4 * j + 4] = (uint8_t)(two >> 8);
+    }
+    if ((c & 3) == 0) sb[c >> 2] = (uint8_t)(127 + k - 3);
+}
+
+// fp32 fallback of a gate/up wave for a token with a non-finite input: its
+// 16 rows over kB blocks of 256 columns from block blk0, from the dequantized
+// x in LDS (xf, column order); lane group q = L / 16 takes the AVX lanes
+// (16-byte chunks) 2q and 2q + 1 of each block.  Returns the row sums in
+// lanes 0..15.
+__device__ __forceinline__ float wh_px_rows_fp32(const uint8_t* wrow, const uint8_t* srow, const float* xf,
+                                                 uint32_t blk0, uint32_t kB, uint32_t L) {
+    const uint32_t qd = L >> 4;
+    float acc = 0.0f;
+    // rolled loops: this path must not raise the kernel's register count
+#pragma unroll 1
+    for (uint32_t b = blk0; b < blk0 + kB; ++b) {
+#pragma unroll 1
+        for (uint32_t c = 2 * qd; c < 2 * qd + 2; ++c) {
+            const uint4 wv = *(const uint4*)(wrow + b * 128 + c * 16);
+            const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (uint32_t d = 0; d < 4; ++d) {
+                const wh_fp4x8 e = wh_fp4_decode8(words[d]);
+                const uint32_t ga = 8 * b + 2 * d;
+                const float* xa = xf + 32 * ga + c;
+                const float* xb = xa + 32;
+                float sa = xa[0] * e.a01.x;
+                sa = __builtin_fmaf(xa[8], e.a01.y, sa);
+                sa = __builtin_fmaf(xa[16], e.a23.x, sa);
+                sa = __builtin_fmaf(xa[24], e.a23.y, sa);
+                float sb = xb[0] * e.b01.x;
+                sb = __builtin_fmaf(xb[8], e.b01.y, sb);
+                sb = __builtin_fmaf(xb[16], e.b23.x, sb);
+                sb = __builtin_fmaf(xb[24], e.b23.y, sb);
+                acc = __builtin_fmaf(sa, wh_ue8m0(srow[ga]) * 0.125f, acc);
+                acc = __builtin_fmaf(sb, wh_ue8m0(srow[ga + 1]) * 0.125f, acc);
+            }
+        }
+    }
+    acc += __shfl_xor(acc, 16, 64);
+    acc += __shfl_xor(acc, 32, 64);
+    return acc;
+}
+
+// Gate/up + SwiGLU, hidden = kCols (2048 or 4096), inter % 16 == 0: grid
+// (ceil(n_experts * inter / 16 / kTiles), n_tokens), kCols / 8 threads.
+template <int kCols, int kTiles>
+__global__ void __launch_bounds__(kCols / 8, 1) k_moe_gateup_px(wh_moe_args a) {
+    constexpr uint32_t kG = kCols / 32, kSl = kCols / 1024, kWaves = 2 * kSl, kB = 4;
+    constexpr int kJ = kB * kTiles, kDepth = WH_PX_GU_DEPTH < kJ ? WH_PX_GU_DEPTH : kJ;
+    constexpr int kPro = WH_PX_PRO < kDepth ? WH_PX_PRO : kDepth;
+    __shared__ __align__(16) uint8_t xc[kCols];  // codes, 32 B per group
+    __shared__ __align__(16) uint8_t xsb[kG];    // E8M0 byte per group
+    __shared__ float red[kTiles * kWaves * 16];
+    __shared__ uint32_t thr[256];
+    __shared__ uint64_t exp_tab[WH_EXP_TAB_LEN];
+    __shared__ __align__(16) float xf[kCols];  // the dequantized x (non-finite tokens only)
+    WH_TL(0, 0);
+    const uint32_t tok = blockIdx.y;
+    wh_moe_clear_arrivals(a, tok);
+    const uint32_t per_e = a.inter >> 4, n_tiles = a.n_experts * per_e;
+    const uint32_t tile0 = blockIdx.x * kTiles;
+    const uint32_t nt = n_tiles - tile0 < (uint32_t)kTiles ? n_tiles - tile0 : (uint32_t)kTiles;
+    const uint32_t wave = threadIdx.x >> 6, L = threadIdx.x & 63, g = L >> 4;
+    const uint32_t m = wave / kSl, s = wave - m * kSl;
+    const bool bf16 = a.x_is_bf16 != 0;
+    const void* xt = bf16 ? (const void*)((const uint16_t*)a.x + (size_t)tok * kCols)
+                          : (const void*)((const float*)a.x + (size_t)tok * kCols);
+    // staging loads (x, the tables) go out before any weight load of the CU
+    wh_thr_stage ts;
+    wh_thr_stage_load(ts);
+    wh_exp_stage es;
+    wh_exp_stage_load(es);
+    wh_in8 xin;
+    wh_in8_load(xin, xt, bf16, threadIdx.x);
+    // the rows of the workgroup's tiles (a tile past the end repeats the
+    // last one; its results are not stored)
+    const uint8_t* wrow[kTiles];
+    const uint8_t* srow[kTiles];
+#pragma unroll
+    for (int i = 0; i < kTiles; ++i) {
+        const uint32_t t = tile0 + ((uint32_t)i < nt ? (uint32_t)i : nt - 1);
+        const uint32_t e = t / per_e, row = (t - e * per_e) * 16 + (L & 15);
+        const wh_expert_ptrs ep = a.ex[e];
+        wrow[i] = (m ? ep.w3 : ep.w1) + (size_t)row * (kCols / 2);
+        srow[i] = (m ? ep.s3 : ep.s1) + (size_t)row * kG + 32 * s;
+    }
+    const uint32_t lane_off = 512 * s + 64 * (g & 1) + 32 * (g >> 1);
+    wh_issue_barrier();
+    wh_mx_raw ring[kDepth];
+#pragma unroll
+    for (int j = 0; j < kPro; ++j) wh_mx_raw_load(ring[j], wrow[j / kB] + lane_off, srow[j / kB], j % kB);
+    __builtin_amdgcn_sched_barrier(0);
+    wh_thr_stage_store(ts, thr);
+    wh_exp_stage_store(es, exp_tab);
+    __syncthreads();
+    WH_TL(0, 1);
+    // act-quant of x (E/compute.rs:2504-2521): columns 8t .. 8t + 7
+    float v[8], q[8], sc;
+    int k;
+    bool bad;
+    wh_in8_values(xin, bf16, v);
+    wh_aq_vals<8>(v, thr, q, k, sc, bad);
+    wh_px_store_codes8(xc, xsb, threadIdx.x, q, k);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = kPro; j < kDepth; ++j) wh_mx_raw_load(ring[j], wrow[j / kB] + lane_off, srow[j / kB], j % kB);
+    __builtin_amdgcn_sched_barrier(0);
+    if (__syncthreads_or(bad)) {
+        // -480 (a NaN's value) and an infinite scale have no E4M3 / E8M0
+        // code: this token's rows run in fp32 from the dequantized x
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xf[8 * threadIdx.x + j] = q[j] * sc;
+        __syncthreads();
+#pragma unroll 1
+        for (uint32_t i = 0; i < nt; ++i) {
+            const float r = wh_px_rows_fp32(wrow[i], srow[i] - 32 * s, xf, kB * s, kB, L);
+            if (L < 16) red[(i * kWaves + wave) * 16 + L] = r;
+        }
+    } else {
+        WH_TL(0, 2);
+        uint32_t dep = wh_opaque_zero(__uint_as_float(*(const uint32_t*)xsb));
+        wh_v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) {
+            const int b = j % kB, i = j / kB;
+            // the input's operands of the block, read after the previous
+            // block's MFMAs (dep) so that they are not all held at once
+            wh_mx_bop bo;
+            wh_mx_bop_load(bo, xc + 1024 * s + 256 * b + dep, xsb + 32 * s + 8 * b + dep, g);
+            wh_px_step(acc, ring[j % kDepth], dep, bo, g);
+            if (j + kDepth < kJ)
+                wh_mx_raw_load(ring[j % kDepth], wrow[(j + kDepth) / kB] + lane_off + dep,
+                               srow[(j + kDepth) / kB] + dep, (j + kDepth) % kB);
+            if (b == kB - 1) {
+                // every lane's A and B feed the MFMAs: keep them out of the
+                // lane-conditional store below
+                asm volatile("" : "+v"(acc));
+                if ((L & 15) == 0) {  // C[4 (L / 16) + r][0]: column 0 is the token
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) red[(i * kWaves + wave) * 16 + 4 * g + r] = acc[r];
+                }
+                acc = wh_v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                if (i < 4) WH_TL(0, 3 + i);
+            }
+        }
+    }
+    __syncthreads();
+    // SwiGLU of the tiles' rows, thread t: tile t / 16, row t % 16
+    if (threadIdx.x < nt * 16) {
+        const uint32_t i = threadIdx.x >> 4, r = threadIdx.x & 15;
+        const float* ri = red + i * kWaves * 16 + r;
+        float gv = ri[0], uv = ri[kSl * 16];
+#pragma unroll
+        for (uint32_t sl = 1; sl < kSl; ++sl) {
+            gv += ri[sl * 16];
+            uv += ri[(kSl + sl) * 16];
+        }
+        if (!(fabsf(gv) <= 3.4028235e38f) || !(fabsf(uv) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
+        const uint32_t t = tile0 + i, e = t / per_e, row = (t - e * per_e) * 16 + r;
+        const size_t he = ((size_t)tok * a.n_experts + e) * a.inter;
+        a.h[he + row] = wh_swiglu(gv, uv, exp_tab, kExpfExc, WH_EXPF_EXC_COUNT);
+        if (a.gu) {
+            a.gu[2 * he + row] = gv;
+            a.gu[2 * he + a.inter + row] = uv;
+        }
+    }
+    WH_TL(0, 7);
+}
+
+// The ordered routed sum of one output row from the per-expert outputs yv
+// (E/compute.rs:1929-2030): route-weighted in route order with the weight
+// rules of valid_route_weight_sum, then shared + routed.
+// yv is indexed with compile-time indices only (unrolled, guarded loops), so
+// it stays in registers.
+__device__ __forceinline__ float wh_route_combine(const wh_moe_args& a, const float (&yv)[WH_MAX_EXPERTS]) {
+    const uint32_t nr = a.n_experts - a.has_shared;
+    float o = 0.0f;
+    if (nr == 1) {
+        o = yv[0];
+    } else if (nr > 1) {
+        float sum = 0.0f;
+        bool valid = true;
+        for (uint32_t i = 0; i < nr; ++i) {
+            const float w = a.route_w[i];
+            if (!(fabsf(w) <= 3.4028235e38f && w >= 0.0f)) valid = false;
+            sum = sum + w;
+        }
+        if (sum <= 1.1920929e-07f) valid = false;
+        const float uniform = 1.0f / (float)nr;
+#pragma unroll
+        for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i) {
+            if (i < nr) {
+                const float w = valid ? a.route_w[i] / sum : uniform;
+                const float p = yv[i] * w;
+                o = o + p;
+            }
+        }
+    }
+    if (a.has_shared) {
+        float sh = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i)
+            if (i == nr) sh = yv[i];
+        o = nr == 0 ? sh : sh + o;
+    }
+    return o;
+}
+
+// Down + routed sum, inter = 2048: grid (hidden / 16, n_tokens), 512
+// threads.  Unit u = (expert u / 4, column quarter u % 4 of 512 = blocks
+// 2 (u % 4), + 1) of the workgroup's 16 output rows; wave w runs units w,
+// w + 8, ... (kU = ceil(n_experts / 2) of them).  The act-quant of every
+// expert's h is the workgroup's own (8 values per thread and chunk).
+template <int kU>
+__global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
+    constexpr uint32_t kCols = 2048, kG = kCols / 32;
+    constexpr int kJ = 2 * kU, kDepth = WH_PX_DN_DEPTH < kJ ? WH_PX_DN_DEPTH : kJ;
+    constexpr int kPro = WH_PX_PRO < kDepth ? WH_PX_PRO : kDepth;
+    __shared__ __align__(16) uint8_t hc[WH_MAX_EXPERTS * kCols];
+    __shared__ __align__(16) uint8_t hsb[WH_MAX_EXPERTS * kG];
+    __shared__ float red[WH_MAX_EXPERTS * 4 * 16];
+    __shared__ uint32_t thr[256];
+    WH_TL(1, 0);
+    const uint32_t tok = blockIdx.y, n = a.n_experts, n_units = 4 * n;
+    const uint32_t wave = threadIdx.x >> 6, L = threadIdx.x & 63, g = L >> 4;
+    const uint32_t row = blockIdx.x * 16 + (L & 15);
+    const float* htok = a.h + (size_t)tok * n * kCols;
+    wh_thr_stage ts;
+    wh_thr_stage_load(ts);
+    // h of every expert: chunk c = 8 columns, expert c / 256 (kU chunks per
+    // thread cover n * 256)
+    float4 hv[kU][2];
+#pragma unroll
+    for (int i = 0; i < kU; ++i) {
+        const uint32_t c = threadIdx.x + 512 * i;
+        if (c < n * 256) {
+            hv[i][0] = ((const float4*)htok)[2 * c];
+            hv[i][1] = ((const float4*)htok)[2 * c + 1];
+        } else {
+            hv[i][0] = hv[i][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+    // the wave's units (a unit past the end repeats unit n_units - 1; its
+    // result is not stored)
+    const uint8_t* wl[kU];
+    const uint8_t* sr[kU];
+#pragma unroll
+    for (int k = 0; k < kU; ++k) {
+        uint32_t u = wave + 8 * k;
+        u = u < n_units ? u : n_units - 1;
+        const uint32_t e = u >> 2, qt = u & 3;
+        wl[k] = a.ex[e].w2 + (size_t)row * (kCols / 2) + 256 * qt + 64 * (g & 1) + 32 * (g >> 1);
+        sr[k] = a.ex[e].s2 + (size_t)row * kG + 16 * qt;
+    }
+    wh_issue_barrier();
+    wh_mx_raw ring[kDepth];
+#pragma unroll
+    for (int j = 0; j < kPro; ++j) wh_mx_raw_load(ring[j], wl[j >> 1], sr[j >> 1], j & 1);
+    __builtin_amdgcn_sched_barrier(0);
+    wh_thr_stage_store(ts, thr);
+    __syncthreads();
+    WH_TL(1, 1);
+    // act-quant of h (E/deepseek_v4.rs:595, block 64): h is finite whenever
+    // gate/up was (a non-finite gate/up output is already reported); keep
+    // the arithmetic in range regardless
+#pragma unroll
+    for (int i = 0; i < kU; ++i) {
+        const uint32_t c = threadIdx.x + 512 * i;
+        const float v[8] = {hv[i][0].x, hv[i][0].y, hv[i][0].z, hv[i][0].w, hv[i][1].x, hv[i][1].y, hv[i][1].z, hv[i][1].w};
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+        amax = wh_amax_block<8>(amax);
+        if (!(amax <= 3.4028235e38f)) amax = 1.0f;
+        const int k = wh_aq_scale_exp(amax, thr);
+        const float inv = wh_pow2f(-k);
+        float q[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = wh_e4m3_round(wh_clamp448_finite(v[j] * inv));
+        if (c < n * 256) wh_px_store_codes8(hc + kCols * (c >> 8), hsb + kG * (c >> 8), c & 255, q, k);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = kPro; j < kDepth; ++j) wh_mx_raw_load(ring[j], wl[j >> 1], sr[j >> 1], j & 1);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    WH_TL(1, 2);
+    {
+        uint32_t dep = wh_opaque_zero(__uint_as_float(*(const uint32_t*)hsb));
+        wh_v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) {
+            const int b = j & 1, kk = j >> 1;
+            uint32_t u = wave + 8 * kk;
+            u = u < n_units ? u : n_units - 1;
+            const uint32_t e = u >> 2, qt = u & 3;
+            wh_mx_bop bo;
+            wh_mx_bop_load(bo, hc + kCols * e + 512 * qt + 256 * b + dep, hsb + kG * e + 16 * qt + 8 * b + dep, g);
+            wh_px_step(acc, ring[j % kDepth], dep, bo, g);
+            if (j + kDepth < kJ)
+                wh_mx_raw_load(ring[j % kDepth], wl[(j + kDepth) >> 1] + dep, sr[(j + kDepth) >> 1] + dep,
+                               (j + kDepth) & 1);
+            if (b == 1) {
+                asm volatile("" : "+v"(acc));
+                if ((L & 15) == 0 && wave + 8 * kk < n_units) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) red[(wave + 8 * kk) * 16 + 4 * g + r] = acc[r];
+                }
+                acc = wh_v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                if (kk < 4) WH_TL(1, 3 + kk);
+            }
+        }
+    }
+    __syncthreads();
+    // per-expert outputs (the 4 quarters of each expert), then the ordered
+    // routed sum
+    if (threadIdx.x < 16) {
+        const uint32_t r = threadIdx.x, orow = blockIdx.x * 16 + r;
+        float yv[WH_MAX_EXPERTS];
+        bool finite = true;
+#pragma unroll
+        for (uint32_t e = 0; e < WH_MAX_EXPERTS; ++e) {
+            if (e < n) {
+                const float* p = red + 4 * e * 16 + r;
+                const float y = ((p[0] + p[16]) + p[32]) + p[48];
+                finite = finite && fabsf(y) <= 3.4028235e38f;
+                yv[e] = y;
+                a.y[((size_t)tok * n + e) * a.hidden + orow] = y;
+            } else {
+                yv[e] = 0.0f;
+            }
+        }
+        if (!finite) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
+        a.out[(size_t)tok * a.hidden + orow] = wh_route_combine(a, yv);
+    }
+    WH_TL(1, 7);
+}

@@ -23,7 +23,7 @@
 #include "mhc.h"
 #include "mla.h"
 #include "moe_batch.h"
-#include "moe_mx.h"
+#include "moe_px.h"
 #include "quant_block.h"
 #include "router.h"
 #include "wohper_hip.h"
@@ -600,6 +600,21 @@ struct MoeBufs {
     float* gu = nullptr;      // test capture of gate and up, or null
 };
 
+// Compute units of the current device (cached).
+int device_cus() {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    std::lock_guard<std::mutex> lk(mu);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cache[dev] = cus;
+    return cus;
+}
+
 // The MFMA token kernels (summation order freed) serve the model's shapes
 // unless the context asks for the reference's order.
 bool moe_mfma(const wh_ctx* c, size_t hidden, size_t inter) {
@@ -673,10 +688,21 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
     const bool sk = moe_mfma(c, hidden, inter);
     if (stages & 1) {
         if (sk) {
-            // block-scaled FP8 MFMA over the act-quantized x, 16 rows per workgroup
-            dim3 ggrid((unsigned)(n * inter / 16), (unsigned)n_tokens);
-            if (hidden == 4096) k_moe_gateup_mx<2><<<ggrid, 256, 0, c->stream>>>(a);
-            else k_moe_gateup_mx<1><<<ggrid, 128, 0, c->stream>>>(a);
+            // block-scaled FP8 MFMA over the act-quantized x: persistent
+            // workgroups of `per` 16-row tiles, about one per CU
+            const size_t tiles = n * inter / 16, cus = (size_t)device_cus();
+            const size_t per = std::min<size_t>(4, std::max<size_t>(1, (tiles * n_tokens + cus - 1) / cus));
+            dim3 ggrid((unsigned)((tiles + per - 1) / per), (unsigned)n_tokens);
+#define WH_GU_PX(C)                                                                      \
+    do {                                                                                 \
+        if (per == 1) k_moe_gateup_px<C, 1><<<ggrid, C / 8, 0, c->stream>>>(a);          \
+        else if (per == 2) k_moe_gateup_px<C, 2><<<ggrid, C / 8, 0, c->stream>>>(a);     \
+        else if (per == 3) k_moe_gateup_px<C, 3><<<ggrid, C / 8, 0, c->stream>>>(a);     \
+        else k_moe_gateup_px<C, 4><<<ggrid, C / 8, 0, c->stream>>>(a);                   \
+    } while (0)
+            if (hidden == 4096) WH_GU_PX(4096);
+            else WH_GU_PX(2048);
+#undef WH_GU_PX
         } else if (hidden == 4096) {
             dim3 ggrid((unsigned)(n * inter / 16), (unsigned)n_tokens);
             k_moe_gateup<16><<<ggrid, 256, wh_moe_wg_lds(hidden), c->stream>>>(a);
@@ -687,8 +713,21 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
     }
     if (stages & 2) {
         dim3 dgrid((unsigned)(n * hidden / 32), (unsigned)n_tokens);
-        if (sk) k_moe_down_mx<<<dgrid, 256, 0, c->stream>>>(a);
-        else if (inter == 2048) k_moe_down<8><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
+        if (sk) {
+            // every expert of a 16-row output slice per workgroup: the routed
+            // sum stays in the workgroup
+            dim3 pgrid((unsigned)(hidden / 16), (unsigned)n_tokens);
+            switch ((n + 1) / 2) {
+                case 1: k_moe_down_px<1><<<pgrid, 512, 0, c->stream>>>(a); break;
+                case 2: k_moe_down_px<2><<<pgrid, 512, 0, c->stream>>>(a); break;
+                case 3: k_moe_down_px<3><<<pgrid, 512, 0, c->stream>>>(a); break;
+                case 4: k_moe_down_px<4><<<pgrid, 512, 0, c->stream>>>(a); break;
+                case 5: k_moe_down_px<5><<<pgrid, 512, 0, c->stream>>>(a); break;
+                case 6: k_moe_down_px<6><<<pgrid, 512, 0, c->stream>>>(a); break;
+                case 7: k_moe_down_px<7><<<pgrid, 512, 0, c->stream>>>(a); break;
+                default: k_moe_down_px<8><<<pgrid, 512, 0, c->stream>>>(a); break;
+            }
+        } else if (inter == 2048) k_moe_down<8><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
         else k_moe_down<0><<<dgrid, 256, wh_moe_wg_lds(inter), c->stream>>>(a);
     }
     WH_HIP(hipGetLastError());
@@ -2724,6 +2763,17 @@ int wh_profile_routed(wh_ctx* c, const wh_expert_route* routes, size_t n_routes,
     }
     return read_status(c);
 }
+
+#ifdef WH_TIMELINE
+// Timeline of the last persistent token kernels (builds with -DWH_TIMELINE
+// only): which = 0 gate/up, 1 down; n <= 512 * 16 * 8 stamps.
+int wh_debug_timeline(int which, uint64_t* out, size_t n) {
+    if (which < 0 || which > 1 || !out || n > 512 * 16 * 8) return WH_INVALID_ARGUMENT;
+    WH_HIP(hipDeviceSynchronize());
+    WH_HIP(hipMemcpyFromSymbol(out, HIP_SYMBOL(wh_tl_buf), n * sizeof(uint64_t), (size_t)which * 512 * 16 * 8 * sizeof(uint64_t)));
+    return WH_OK;
+}
+#endif
 
 int wh_debug_eval(wh_ctx* c, int fn, const float* in, float* out, size_t n) {
     if (!c || !in || !out || fn < 0 || fn > 6) return WH_INVALID_ARGUMENT;
