@@ -275,6 +275,53 @@ def ragged_batch(ctx, n_layers: int, steps: int, warmup: int, exact: bool = Fals
             "note": "wall clock and HIP events on the library stream; layers rotate so no step reuses cached weights"}
 
 
+def fp8_decode_layer_batch(ctx, steps: int, batch: int = 16):
+    """The decode layer's FP8 projections over `batch` inputs, each on its
+    own, back to back over 8 rotating weight copies: exact numerics (every
+    input bit-identical to the single-input kernel) against the bf16 MFMA
+    path (each weight byte read once for all inputs; each output within
+    1e-5 * ||w_row|| * ||x|| of the reference kernel).  wo_a's 8 row groups
+    read their own inputs in one call."""
+    from wohper_amd import workloads as wl
+
+    res = {}
+    copies = 8
+    rng = np.random.default_rng(9)
+    for i, (name, r, c, groups) in enumerate(wl.DECODE_LAYER_FP8):
+        hs = [ctx.store_fp8_synthetic(r, c, 3, wl.fp8_stream(2000 + k, i), wl.fp8_block_scales(21 + k, r, c))
+              for k in range(copies)]
+        xd, yd = ctx.device_alloc(batch * groups * c * 4), ctx.device_alloc(batch * r * 4)
+        ctx.to_device(xd, rng.standard_normal(batch * groups * c).astype(np.float32))
+        rows = r // groups
+
+        def call(h):
+            if groups > 1:
+                ctx.fp8_gemv_multi_groups_async(h, 0, r, rows, xd, c, batch, groups * c, yd, r)
+            else:
+                ctx.fp8_gemv_multi_async(h, 0, r, xd, batch, c, yd, r)
+
+        nbytes = r * c + (r // 128) * (c // 128) * 4 + batch * (groups * c + r) * 4
+        entry = {"shape": f"{r}x{c}", "groups": groups, "inputs": batch, "bytes": nbytes}
+        for exact in (True, False):
+            ctx.set_exact_numerics(exact)
+            n = steps if not exact else max(8, steps // 8)
+            for k in range(copies):
+                call(hs[k])
+            ctx.synchronize()
+            ctx.timer_start()
+            for k in range(n):
+                call(hs[k % copies])
+            us = ctx.timer_stop() / n
+            entry["exact_us" if exact else "mfma_us"] = round(us, 2)
+            entry["exact_GBps" if exact else "mfma_GBps"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+        res[name] = entry
+        for h in hs:
+            ctx.release(h)
+        ctx.device_free(xd)
+        ctx.device_free(yd)
+    return res
+
+
 def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps: int = 0, exact: bool = False):
     """Full-depth synthetic stack at batch 1: per layer the FP8 projections
     of one decode layer (wq_a, wq_b, wkv, wo_a in 8 row groups, wo_b; f32
@@ -410,9 +457,8 @@ def decode_stack_batch16(ctx, layers, n_layers: int, steps: int, seed: int, batc
             ctx.fp8_gemv_multi_async(hs["wq_a"], 0, 1024, dev["x"], batch, 4096, ydev["wq_a"], 1024)
             ctx.fp8_gemv_multi_async(hs["wq_b"], 0, 32768, dev["qlat"], batch, 1024, ydev["wq_b"], 32768)
             ctx.fp8_gemv_multi_async(hs["wkv"], 0, 512, dev["x"], batch, 4096, ydev["wkv"], 512)
-            for g in range(8):
-                ctx.fp8_gemv_multi_async(hs["wo_a"], 1024 * g, 1024 * (g + 1), dev["oa"] + g * 4096 * 4, batch,
-                                         8 * 4096, ydev["wo_a"] + g * 1024 * 4, 8192)
+            ctx.fp8_gemv_multi_groups_async(hs["wo_a"], 0, 8192, 1024, dev["oa"], 4096, batch, 8 * 4096,
+                                            ydev["wo_a"], 8192)
             ctx.fp8_gemv_multi_async(hs["wo_b"], 0, 4096, dev["ob"], batch, 8192, ydev["wo_b"], 4096)
             ctx.moe_batch_async(L, ids_dev[s_][L], sc_dev[s_][L], batch, wl.TOPK, moe_x, True, moe_out,
                                 shared_key=(L, wl.N_ROUTED))
@@ -562,6 +608,9 @@ def main():
         log(f"fp8 dense: {extra['fp8_dense_gemv']}")
         extra["fp8_decode_layer"] = fp8_decode_layer(ctx, 200)
         log(f"fp8 decode layer: {extra['fp8_decode_layer']}")
+        extra["fp8_decode_layer_batch16"] = fp8_decode_layer_batch(ctx, 200)
+        ctx.set_exact_numerics(args.exact)
+        log(f"fp8 decode layer, batch 16: {extra['fp8_decode_layer_batch16']}")
     if not args.no_aux:
         extra["router"] = router(ctx, 400)
         log(f"router: {extra['router']}")

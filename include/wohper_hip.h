@@ -434,9 +434,33 @@ int wh_fp8_gemv_batch_async(wh_ctx* ctx, const wh_gemv_desc* descs, size_t n);
 
 /* Device-pointer variant of wh_fp8_gemv_multi (gemv_fp8_e4m3_ue8m0_rows_multi,
  * E/compute.rs:6384-6577): n f32 inputs at x_dev + i * x_stride, outputs at
- * y_dev + i * y_stride, each bit-identical to the single-input GEMV. */
+ * y_dev + i * y_stride, each bit-identical to the single-input GEMV.  With
+ * exact numerics off (wh_set_exact_numerics(ctx, 0)) and at least
+ * wh_set_fp8_mfma_min inputs, tensors of a multiple of 256 columns in
+ * 128-column scale groups, scale rows of a power of two >= 16 rows and
+ * row_start % 16 == 0 run on bf16 MFMA instead: each weight byte is read once
+ * for all inputs, the weights are the reference's values exactly and each
+ * input is split exactly into three bf16 parts, so every product is exact
+ * and the outputs differ from the reference kernel's by fp32 accumulation
+ * order only (within 1e-5 * ||w_row||_2 * ||x||_2). */
 int wh_fp8_gemv_multi_async(wh_ctx* ctx, wh_tensor w, size_t row_start, size_t row_end, const float* x_dev, size_t n,
                             size_t x_stride, float* y_dev, size_t y_stride);
+
+/* The reference's grouped batch projection, one rows_multi call per row group
+ * with the group's own inputs (wo_a, E/compute.rs:4599-4622), as one call:
+ * rows row_start + [g * group_rows, (g + 1) * group_rows) read input i of
+ * group g at x_dev + i * x_stride + g * x_group_stride and write
+ * y_dev + i * y_stride + (row - row_start).  Results are those of the
+ * per-group wh_fp8_gemv_multi_async calls; on the MFMA path (as there, plus
+ * group_rows a power of two >= 128) all groups go out as one launch. */
+int wh_fp8_gemv_multi_groups_async(wh_ctx* ctx, wh_tensor w, size_t row_start, size_t row_end, size_t group_rows,
+                                   const float* x_dev, size_t x_group_stride, size_t n, size_t x_stride, float* y_dev,
+                                   size_t y_stride);
+
+/* Multi-input FP8 GEMVs with at least min_inputs inputs take the MFMA path
+ * when exact numerics are off (default 4; 0 = never).  No counterpart in the
+ * reference. */
+int wh_set_fp8_mfma_min(wh_ctx* ctx, uint32_t min_inputs);
 
 /* Device-pointer FP8 GEMV (rows [row_start,row_end) of w, x_dev f32 or bf16). */
 int wh_fp8_gemv_async(wh_ctx* ctx, wh_tensor w, size_t row_start, size_t row_end,

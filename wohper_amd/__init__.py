@@ -80,7 +80,8 @@ EXPORTED = (
     "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop", "wh_profile_routed",
     "wh_store_fp8_synthetic", "wh_synth_fp8_host", "wh_routed_and_shared_experts", "wh_fp8_gemv_batch_async",
     "wh_routed_and_shared_experts_async", "wh_moe_batch", "wh_moe_batch_async", "wh_set_moe_mfma_min",
-    "wh_debug_moe_batch_read", "wh_fp8_gemv_multi_async", "wh_set_exact_numerics", "wh_debug_moe_token_capture",
+    "wh_debug_moe_batch_read", "wh_fp8_gemv_multi_async", "wh_fp8_gemv_multi_groups_async", "wh_set_fp8_mfma_min",
+    "wh_set_exact_numerics", "wh_debug_moe_token_capture",
     "wh_debug_moe_token_read", "wh_fp8_shared_expert", "wh_fp8_shared_expert_async",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
     "wh_quant_block_header", "wh_quant_block_tensor", "wh_quant_block_fp4_expert", "wh_store_expert_block",
@@ -217,6 +218,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
                                          vp]),
         "wh_set_moe_mfma_min": (c.c_int, [vp, c.c_uint32]),
         "wh_fp8_gemv_multi_async": (c.c_int, [vp, c.c_uint64, sz, sz, vp, sz, sz, vp, sz]),
+        "wh_fp8_gemv_multi_groups_async": (c.c_int, [vp, c.c_uint64, sz, sz, sz, vp, sz, sz, sz, vp, sz]),
+        "wh_set_fp8_mfma_min": (c.c_int, [vp, c.c_uint32]),
         "wh_debug_moe_batch_read": (c.c_int, [vp, c.c_int, vp, sz]),
         "wh_set_exact_numerics": (c.c_int, [vp, c.c_int]),
         "wh_fp8_shared_expert": (c.c_int, [vp, c.c_uint64, c.c_uint64, c.c_uint64, f32p, sz, f32p, sz]),
@@ -584,6 +587,19 @@ class Context:
         _check(self.lib.wh_moe_batch_async(self._h, layer_id, ctypes.c_void_p(ids_ptr), ctypes.c_void_p(scores_ptr),
                                            npos, topk, sl, se, ctypes.c_void_p(x_ptr), int(x_is_bf16),
                                            ctypes.c_void_p(out_ptr)), "moe_batch_async")
+
+    def fp8_gemv_multi_groups_async(self, t: int, row_start: int, row_end: int, group_rows: int, x_ptr: int,
+                                    x_group_stride: int, n: int, x_stride: int, y_ptr: int, y_stride: int):
+        """Row groups of group_rows rows, group g reading its n inputs at
+        x_ptr + 4 * g * x_group_stride (strides in floats)."""
+        _check(self.lib.wh_fp8_gemv_multi_groups_async(self._h, t, row_start, row_end, group_rows,
+                                                       ctypes.c_void_p(x_ptr), x_group_stride, n, x_stride,
+                                                       ctypes.c_void_p(y_ptr), y_stride), "fp8_gemv_multi_groups_async")
+
+    def set_fp8_mfma_min(self, n: int):
+        """Multi-input FP8 GEMVs with at least n inputs use MFMA when exact
+        numerics are off (0: never)."""
+        _check(self.lib.wh_set_fp8_mfma_min(self._h, n), "set_fp8_mfma_min")
 
     def fp8_gemv_multi_async(self, t: int, row_start: int, row_end: int, x_ptr: int, n: int, x_stride: int,
                              y_ptr: int, y_stride: int):

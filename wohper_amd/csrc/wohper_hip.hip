@@ -24,6 +24,7 @@
 #include "mla.h"
 #include "moe_batch.h"
 #include "moe_px.h"
+#include "fp8_mm.h"
 #include "quant_block.h"
 #include "router.h"
 #include "wohper_hip.h"
@@ -268,6 +269,8 @@ struct wh_ctx {
     HostBuf pack[2];   // experts-pack read buffers (one filling while the other uploads)
     std::map<uint32_t, LayerTable> tables;  // device expert tables of the batch path
     uint32_t moe_mfma_min = 1;              // batch experts with this many tokens use MFMA (0: never)
+    uint32_t fp8_mm_min = 4;                // multi-input FP8 GEMVs with this many inputs use MFMA
+    Scratch fp8mm_ws, fp8mm_cnt;            // their partial tiles and arrival counters
     bool exact = true;                      // routed experts in the reference's summation order
     bool capture_gu = false;                // routed experts keep gate/up in `gu` (test support)
     size_t tok_last_n = 0, tok_last_tokens = 0, tok_last_hidden = 0, tok_last_inter = 0;
@@ -418,6 +421,15 @@ hipError_t kernel_setup_once(int device) {
         set((const void*)k_moe_batch_gateup<16>);
         set((const void*)k_moe_batch_down<0>);
         set((const void*)k_moe_batch_down<8>);
+#define WH_MM_SET(G_)                                    \
+        set((const void*)k_fp8_mm<false, false, G_>);    \
+        set((const void*)k_fp8_mm<false, true, G_>);     \
+        set((const void*)k_fp8_mm<true, false, G_>);     \
+        set((const void*)k_fp8_mm<true, true, G_>);
+        WH_MM_SET(2)
+        WH_MM_SET(4)
+        WH_MM_SET(8)
+#undef WH_MM_SET
         if (e == hipSuccess) {
             g_max_lds = (size_t)lds;
         } else {
@@ -507,6 +519,83 @@ int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x,
         if (u8) k_fp8_gemv_generic<true><<<grid, 64, 0, c->stream>>>(a, col_group);
         else k_fp8_gemv_generic<false><<<grid, 64, 0, c->stream>>>(a, col_group);
     }
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// Multi-input GEMV on bf16 MFMA (fp8_mm.h): lane-layout tensors of a
+// multiple of 256 columns whose scale rows span a power of two >= 16 rows, ranges starting on a
+// 16-row boundary, and input groups (rows with their own input) of a power
+// of two >= 128 rows.
+bool fp8_mm_ok(const Tensor& t, size_t r0, size_t r1, size_t group_rows) {
+    const size_t rg = t.rows / t.scale_rows;
+    if (!t.fast || t.cols % 256 || !is_pow2(rg) || rg < 16 || r0 % 16) return false;
+    if (group_rows && (!is_pow2(group_rows) || group_rows < 128 || (r1 - r0) % group_rows)) return false;
+    return true;
+}
+
+// y_t = W x_t over rows [r0, r1) for n inputs; with group_rows, rows
+// r0 + [g group_rows, (g + 1) group_rows) read input group g at
+// x + g * xg_stride.  One launch over (row block, k split, token block).
+int launch_fp8_mm(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x, size_t n, size_t x_stride,
+                  float* y, size_t y_stride, size_t group_rows, size_t xg_stride) {
+    const size_t rows = r1 - r0, rb = (rows + WH_FP8MM_ROWS - 1) / WH_FP8MM_ROWS, G = t.cols / 128;
+    const size_t tbs = (n + WH_FP8MM_TOK - 1) / WH_FP8MM_TOK;
+    // groups per k split: 8, 4 or 2 (what divides the width and fits LDS),
+    // the most that still gives ~256 workgroups
+    size_t kg = 0;
+    for (size_t g = WH_FP8MM_MAX_GROUPS; g >= 2; g /= 2) {
+        if (G % g || wh_fp8mm_lds(g * 128) > g_max_lds) continue;
+        kg = g;
+        if (rb * tbs * (G / g) >= 256) break;
+    }
+    if (kg == 0) return WH_UNSUPPORTED;
+    const size_t S = G / kg, kc = kg * 128;
+    if (rb * S > 65535 || tbs > 65535) return WH_UNSUPPORTED;
+    if (S > 1) {
+        WH_HIP(c->fp8mm_ws.ensure(tbs * rb * S * WH_FP8MM_ROWS * 16 * sizeof(float), false));
+        WH_HIP(c->fp8mm_cnt.ensure(tbs * rb * sizeof(uint32_t), true));
+    }
+    wh_fp8mm_args a;
+    std::memset(&a, 0, sizeof a);
+    a.w = t.w;
+    a.scales = t.s;
+    a.x = x;
+    a.y = y;
+    a.ws = c->fp8mm_ws.as<float>();
+    a.cnt = c->fp8mm_cnt.as<uint32_t>();
+    a.status = c->status;
+    a.cols = (uint32_t)t.cols;
+    a.scale_cols = (uint32_t)t.scale_cols;
+    a.row_group_shift = log2_of(t.rows / t.scale_rows);
+    a.row_start = (uint32_t)r0;
+    a.row_end = (uint32_t)r1;
+    a.n = (uint32_t)n;
+    a.x_stride = (uint32_t)x_stride;
+    a.y_stride = (uint32_t)y_stride;
+    a.xg_shift = group_rows ? log2_of(group_rows) : 31u;
+    a.xg_stride = (uint32_t)xg_stride;
+    a.kc = (uint32_t)kc;
+    a.splits = (uint32_t)S;
+    a.row_blocks = (uint32_t)rb;
+    const dim3 grid((unsigned)rb, (unsigned)S, (unsigned)tbs);
+    const size_t lds = wh_fp8mm_lds(kc);
+    const bool u8 = t.scale_fmt == WH_SCALE_UE8M0;
+    auto go = [&](auto kern) { kern<<<grid, 512, lds, c->stream>>>(a); };
+#define WH_MM_GO(G_)                                        \
+    if (kg == G_) {                                         \
+        if (t.special) {                                    \
+            if (u8) go(k_fp8_mm<true, true, G_>);           \
+            else go(k_fp8_mm<true, false, G_>);             \
+        } else {                                            \
+            if (u8) go(k_fp8_mm<false, true, G_>);          \
+            else go(k_fp8_mm<false, false, G_>);            \
+        }                                                   \
+    }
+    WH_MM_GO(2)
+    WH_MM_GO(4)
+    WH_MM_GO(8)
+#undef WH_MM_GO
     WH_HIP(hipGetLastError());
     return WH_OK;
 }
@@ -2134,7 +2223,10 @@ int wh_fp8_gemv_multi(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end,
     float* si = (float*)c->stage_in.p;
     for (size_t b = 0; b < n; ++b) std::memcpy(si + b * t->cols, inputs + b * input_stride, t->cols * sizeof(float));
     WH_HIP(hipMemcpyAsync(c->x_in.p, si, n * t->cols * sizeof(float), hipMemcpyHostToDevice, c->stream));
-    WH_TRY(launch_fp8(c, *t, row_start, row_end, c->x_in.as<float>(), c->y_out.as<float>(), n, t->cols, rows));
+    if (!c->exact && n >= c->fp8_mm_min && fp8_mm_ok(*t, row_start, row_end, 0))
+        WH_TRY(launch_fp8_mm(c, *t, row_start, row_end, c->x_in.as<float>(), n, t->cols, c->y_out.as<float>(), rows, 0, 0));
+    else
+        WH_TRY(launch_fp8(c, *t, row_start, row_end, c->x_in.as<float>(), c->y_out.as<float>(), n, t->cols, rows));
     WH_HIP(hipMemcpyAsync(c->stage_out.p, c->y_out.p, n * rows * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     int st = read_status(c);
     if (st != WH_OK) return st;
@@ -2197,7 +2289,42 @@ int wh_fp8_gemv_multi_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row
     WH_TRY(fp8_ptr_check(*t, x_dev, y_dev));
     if (t->fast && (x_stride & 3)) return WH_INVALID_ARGUMENT;  // every input 16-byte aligned
     WH_HIP(hipSetDevice(c->device));
+    if (!c->exact && n >= c->fp8_mm_min && fp8_mm_ok(*t, row_start, row_end, 0))
+        return launch_fp8_mm(c, *t, row_start, row_end, x_dev, n, x_stride, y_dev, y_stride, 0, 0);
     return launch_fp8(c, *t, row_start, row_end, x_dev, y_dev, n, x_stride, y_stride);
+}
+
+int wh_fp8_gemv_multi_groups_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end, size_t group_rows,
+                                   const float* x_dev, size_t x_group_stride, size_t n, size_t x_stride, float* y_dev,
+                                   size_t y_stride) {
+    if (!c || !x_dev || !y_dev || group_rows == 0) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    Tensor* t = find_tensor(c, w);
+    if (!t) return WH_NOT_RESIDENT;
+    if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
+    if (n == 0 || row_start >= row_end || row_end > t->rows || (row_end - row_start) % group_rows)
+        return WH_INVALID_SHAPE;
+    if (x_stride < t->cols) return WH_INPUT_TOO_SMALL;
+    if (y_stride < row_end - row_start) return WH_OUTPUT_TOO_SMALL;
+    if (x_stride > UINT32_MAX || y_stride > UINT32_MAX || x_group_stride > UINT32_MAX || n > 65535)
+        return WH_UNSUPPORTED;
+    WH_TRY(fp8_ptr_check(*t, x_dev, y_dev));
+    if (t->fast && ((x_stride | x_group_stride) & 3)) return WH_INVALID_ARGUMENT;  // every input 16-byte aligned
+    WH_HIP(hipSetDevice(c->device));
+    if (!c->exact && n >= c->fp8_mm_min && fp8_mm_ok(*t, row_start, row_end, group_rows))
+        return launch_fp8_mm(c, *t, row_start, row_end, x_dev, n, x_stride, y_dev, y_stride, group_rows,
+                             x_group_stride);
+    for (size_t r = row_start, g = 0; r < row_end; r += group_rows, ++g)
+        WH_TRY(launch_fp8(c, *t, r, r + group_rows, x_dev + g * x_group_stride, y_dev + (r - row_start), n, x_stride,
+                          y_stride));
+    return WH_OK;
+}
+
+int wh_set_fp8_mfma_min(wh_ctx* c, uint32_t min_inputs) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->fp8_mm_min = min_inputs ? min_inputs : UINT32_MAX;
+    return WH_OK;
 }
 
 int wh_fp8_gemv_batch_async(wh_ctx* c, const wh_gemv_desc* descs, size_t n) {
