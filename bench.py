@@ -10,10 +10,18 @@ layers of 256 experts (round robin), so no step reuses weights that the
 previous ones left in the 256 MB Infinity Cache.  Inputs are resident in
 HBM before the timed region; value = algorithmic bytes / wall time.
 
+The headline runs the MFMA kernels (each matvec within
+1e-5 * ||w_row|| * ||x|| of the reference kernel); --exact runs the
+bit-exact kernels (the reference's summation order) instead, and each line
+reports the other mode's kernels beside its own.
+
 Also reported: per-kernel mean durations (HIP events on the library stream),
 the FP8 dense GEMV (4096x4096, fp32 128x128 block scales) over 40 rotating
-copies, and the reference's AVX2 algorithm (the CPU oracle) timed on the
-host cores with the reference's thread count.
+copies, the decode layer's FP8 projections at batch 1 and 16, the HBM read
+floor of each kernel's byte count, the router, the ragged batch, the
+43-layer stack at batch 1 and 16, and the reference's AVX2 algorithm (the
+CPU oracle) timed on the host cores at 1 thread, the reference's thread
+count and every CPU.
 """
 from __future__ import annotations
 
@@ -49,35 +57,158 @@ def log(msg: str):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def cpu_host() -> dict:
+    """CPU model, physical cores and logical CPUs of this host (from
+    /proc/cpuinfo), and the CPUs this process may run on."""
+    model, cores = "unknown", set()
+    phys = core = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+        if phys is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"model": model, "physical_cores": len(cores) or None, "logical_cpus": os.cpu_count(),
+            "usable_cpus": usable}
+
+
+def _timed(fn, budget_s: float, min_reps: int = 1):
+    """(reps, seconds) of repeating fn until budget_s has passed."""
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and reps >= min_reps:
+            return reps, el
+
+
 def cpu_baseline(lib, seed: int, budget_s: float):
-    """The oracle's AVX2 restatement of the reference expert path on this host."""
+    """The oracle's AVX2 restatement of the reference kernels on this host's
+    cores.  Returns (headline, per-config figures): the headline is config
+    2's token at the reference's default thread count (available CPUs - 2,
+    E/deepseek_v4.rs:206-277); the others are the token and the FP8 GEMV at
+    1 thread, that count and every usable CPU, one decode layer at batch 1,
+    the 64-token ragged batch (a sample of its token-expert forwards) and
+    the 43-layer stack from the layer figure."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
     from wohper_amd import workloads as wl
 
     oracle.build()
-    threads = max(1, (os.cpu_count() or 3) - 2)  # reference default: available_parallelism - 2
-    # a container's CPU quota can be below os.cpu_count(); respect the affinity mask
-    try:
-        threads = max(1, min(threads, len(os.sched_getaffinity(0)) - 2))
-    except AttributeError:
-        pass
-    oracle.set_threads(threads)
+    host = cpu_host()
+    usable = host["usable_cpus"]
+    ref_threads = max(1, usable - 2)
     idx, w, x = wl.moe_token_case(seed)
     experts = [wl.synth_expert_host(lib, seed, 0, int(e)) for e in idx]
-    tokens = 0
-    t0 = time.perf_counter()
-    while True:
+
+    def token():
         outs = np.stack([oracle.fp4_expert_forward(*ex, x) for ex in experts])
         oracle.routed_combine(outs, w)
-        tokens += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
+
+    oracle.set_threads(ref_threads)
+    tokens, el = _timed(token, budget_s)
     gbs = tokens * TOKEN_BYTES / el / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{tokens} tokens x 6 routed FP4 experts (4096/2048 shapes), oracle AVX2 restatement "
-                      f"of the reference kernel, {threads} threads, {el:.1f} s; {el / tokens * 1e3:.1f} ms/token"}
+    headline = {"value": round(gbs, 3), "unit": "GB/s", "cores": ref_threads, "kind": "port",
+                "sample": f"{tokens} tokens x 6 routed FP4 experts (4096/2048 shapes), oracle AVX2 restatement "
+                          f"of the reference kernel, {ref_threads} threads (usable CPUs - 2, the reference's "
+                          f"default), {el:.1f} s; {el / tokens * 1e3:.1f} ms/token"}
+    extra = {"host": host, "token": {}, "fp8_gemv_4096": {}}
+    short = max(2.0, budget_s / 4)
+    for n in sorted({1, ref_threads, usable}):
+        oracle.set_threads(n)
+        if n != ref_threads:
+            k, e = _timed(token, short)
+            extra["token"][f"{n}_threads"] = {"us_per_token": round(e / k * 1e6, 1),
+                                              "GBps": round(k * TOKEN_BYTES / e / 1e9, 3)}
+        else:
+            extra["token"][f"{n}_threads"] = {"us_per_token": round(el / tokens * 1e6, 1), "GBps": round(gbs, 3)}
+    case = wl.fp8_gemv_case(4096, 4096, seed=0)
+    for n in sorted({1, ref_threads, usable}):
+        oracle.set_threads(n)
+        k, e = _timed(lambda: oracle.fp8_gemv(case.w, 4096, 4096, case.scales, 32, 32, case.x), short / 2, 3)
+        extra["fp8_gemv_4096"][f"{n}_threads"] = {"us_per_gemv": round(e / k * 1e6, 1),
+                                                  "GBps": round(k * FP8_BYTES / e / 1e9, 3)}
+    oracle.set_threads(ref_threads)
+    # one decode layer at batch 1: the FP8 projection set (wo_a as 8 row
+    # groups with their own inputs) and the shared + 6 routed experts
+    rng = np.random.default_rng(seed)
+    projs = []
+    for i, (name, r, c, groups) in enumerate(wl.DECODE_LAYER_FP8):
+        pc = wl.fp8_gemv_case(r, c, seed=100 + i)
+        xs = rng.standard_normal((groups, c)).astype(np.float32)
+        projs.append((pc, r, c, groups, xs))
+    shared = wl.synth_expert_host(lib, seed, 0, wl.N_ROUTED)
+
+    def layer():
+        for pc, r, c, groups, xs in projs:
+            rows = r // groups
+            for g in range(groups):
+                oracle.fp8_gemv(pc.w, r, c, pc.scales, r // 128, c // 128, xs[g], g * rows, (g + 1) * rows)
+        oracle.fp4_expert_forward(*shared, x)
+        token()
+
+    k, e = _timed(layer, short, 2)
+    layer_us = e / k * 1e6
+    vec = (4096 + 1024 + 1024 + 32768 + 4096 + 512 + 8 * (4096 + 1024) + 8192 + 4096) * 4 + 4096 * 2 + 4096 * 4
+    layer_bytes = wl.DECODE_LAYER_FP8_BYTES + 7 * wl.FP4_EXPERT_BYTES + vec
+    extra["decode_layer"] = {"threads": ref_threads, "us_per_layer": round(layer_us, 1),
+                             "GBps": round(layer_bytes / (layer_us * 1e-6) / 1e9, 3)}
+    extra["decode_stack_43"] = {"threads": ref_threads, "us_per_step": round(43 * layer_us, 1),
+                                "note": "43 x the measured layer: the 150 GB stack is not built on the host"}
+    # ragged batch: the reference runs one expert forward per (token, expert)
+    # target, so a sample of the targets scales by their count
+    ids, scores, xb = wl.zipf_batch_routes(seed=4, n_tokens=64)
+    sample_tokens = 4
+    sub = ids[:sample_tokens]
+    sub_experts = {int(e): wl.synth_expert_host(lib, seed, 0, int(e)) for e in np.unique(sub)}
+    k, e = _timed(lambda: oracle.moe_batch(sub_experts, sub, scores[:sample_tokens], xb[:sample_tokens]), 0.0, 1)
+    per_fwd = e / k / sub.size
+    extra["ragged_batch_64"] = {"threads": ref_threads, "us_per_step": round(per_fwd * ids.size * 1e6, 1),
+                                "sample": f"{sample_tokens} of 64 tokens ({sub.size} of {ids.size} token-expert "
+                                          "forwards), scaled by forwards"}
+    extra["decode_stack_43_batch16"] = {
+        "note": "not measured: the reference's rows_multi decodes each FP8 row once for all inputs, which the "
+                "oracle's single-input restatement does not model, so single-input calls would overstate it"}
+    return headline, extra
+
+
+def read_floor(ctx, reps: int = 60):
+    """The HBM read floor of this device: the fastest plain streaming read
+    (wh_probe_read_floor sweeps grid size and loads in flight) of each
+    kernel's byte count as one launch, from rotating windows of a 4 GiB
+    buffer so that no launch is served by the 256 MB Infinity Cache."""
+    buf_bytes = 4 << 30
+    buf = ctx.device_alloc(buf_bytes)
+    res = {}
+    try:
+        for name, nbytes in (("fp8_gemv_4096", FP8_BYTES), ("moe_down", DOWN_BYTES), ("moe_gateup", GATEUP_BYTES),
+                             ("token_one_launch", TOKEN_BYTES), ("256MiB", 256 << 20)):
+            nb = nbytes // 16 * 16
+            us, grid, depth, empty = ctx.probe_read_floor(buf, buf_bytes, nb, reps)
+            res[name] = {"bytes": nb, "us": round(us, 2), "GBps": round(nb / (us * 1e-6) / 1e9, 1),
+                         "frac_of_hbm_peak": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "grid": grid, "loads_in_flight": depth}
+        res["empty_launch_us"] = round(empty, 2)
+    finally:
+        ctx.device_free(buf)
+    return res
 
 
 def fp8_dense(ctx, steps: int, warmup: int):
@@ -405,6 +536,13 @@ def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps:
         ctx.device_free(k)
     if batch_steps > 0:
         res["batch16"] = decode_stack_batch16(ctx, layers, n_layers, batch_steps, seed)
+        res["batch16"]["numerics"] = "exact" if exact else "mfma"
+        ctx.set_exact_numerics(not exact)
+        other = decode_stack_batch16(ctx, layers, n_layers, batch_steps, seed)
+        ctx.set_exact_numerics(exact)
+        res["batch16_other_numerics"] = {"numerics": "mfma" if exact else "exact",
+                                         **{k: other[k] for k in ("step_us", "layer_us", "GBps", "frac_of_hbm_peak",
+                                                                  "tokens_per_s")}}
     ctx.close()
     return res
 
@@ -508,8 +646,9 @@ def main():
     ap.add_argument("--batch-steps", type=int, default=20, help="steps of the ragged batch leg (0: skip)")
     ap.add_argument("--stack-batch-steps", type=int, default=3,
                     help="steps of the batch-16 full-depth stack (0: skip)")
-    ap.add_argument("--split-k", dest="exact", action="store_false",
-                    help="routed experts on the MFMA kernels (summation order freed) instead of the bit-exact ones")
+    ap.add_argument("--exact", action="store_true",
+                    help="headline on the bit-exact kernels (the reference's summation order) instead of the MFMA "
+                         "kernels (each matvec within 1e-5 * ||w_row|| * ||x|| of the reference kernel)")
     ap.add_argument("--batch-mfma-sweep", type=str, default="",
                     help="only time the ragged batch leg: exact items, then each MFMA threshold of this "
                          "comma-separated list (one JSON line each)")
@@ -612,6 +751,8 @@ def main():
         ctx.set_exact_numerics(args.exact)
         log(f"fp8 decode layer, batch 16: {extra['fp8_decode_layer_batch16']}")
     if not args.no_aux:
+        extra["read_floor"] = read_floor(ctx)
+        log(f"read floor: {extra['read_floor']}")
         extra["router"] = router(ctx, 400)
         log(f"router: {extra['router']}")
         extra["expert_pack_load"] = expert_pack_load(ctx)
@@ -622,8 +763,8 @@ def main():
         log(f"ragged batch: {extra['ragged_batch']}")
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(ctx.lib, seed, args.cpu_seconds)
-        log(f"cpu baseline: {cpu}")
+        cpu, extra["cpu_configs"] = cpu_baseline(ctx.lib, seed, args.cpu_seconds)
+        log(f"cpu baseline: {cpu}; {extra['cpu_configs']}")
 
     if args.stack_layers > 0:
         ctx.close()

@@ -485,6 +485,17 @@ int wh_memcpy(wh_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
 int wh_timer_start(wh_ctx* ctx);
 int wh_timer_stop(wh_ctx* ctx, double* elapsed_us);
 
+/* Measurement helper, no counterpart in the reference: the HBM read floor.
+ * Times plain streaming-read launches of `bytes` (a multiple of 16) from
+ * rotating windows of buf_dev (buf_bytes long, 16-byte aligned, at least one
+ * 4 KiB-rounded window), `reps` back-to-back launches per grid size (256 to
+ * 8192 workgroups of 256 threads) and loads in flight (4, 8, 16 x 16 B per
+ * thread), on the library stream.  Writes the fastest mean microseconds per
+ * launch with its grid and depth, and the per-launch cost of an empty
+ * 1024 x 256 launch. */
+int wh_probe_read_floor(wh_ctx* ctx, const void* buf_dev, size_t buf_bytes, size_t bytes, size_t reps,
+                        double* best_us, uint32_t* best_grid, uint32_t* best_depth, double* empty_us);
+
 /* Per-kernel timing of the routed-expert path, no counterpart in the
  * reference (the engine's ZC_PROF timers, E/server/generation.rs:2344-2351,
  * time whole passes on the CPU).  routes holds n_sets route lists of n_routes

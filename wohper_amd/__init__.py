@@ -78,6 +78,7 @@ EXPORTED = (
     "wh_fp8_gemv", "wh_fp8_gemv_multi", "wh_fp4_matvec", "wh_fp4_expert_forward",
     "wh_act_quant_dequant", "wh_routed_experts", "wh_routed_experts_async", "wh_fp8_gemv_async",
     "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop", "wh_profile_routed",
+    "wh_probe_read_floor",
     "wh_store_fp8_synthetic", "wh_synth_fp8_host", "wh_routed_and_shared_experts", "wh_fp8_gemv_batch_async",
     "wh_routed_and_shared_experts_async", "wh_moe_batch", "wh_moe_batch_async", "wh_set_moe_mfma_min",
     "wh_debug_moe_batch_read", "wh_fp8_gemv_multi_async", "wh_fp8_gemv_multi_groups_async", "wh_set_fp8_mfma_min",
@@ -212,6 +213,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_profile_routed": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, sz, vp, c.c_int, vp, sz,
                                         c.POINTER(c.c_double)]),
         "wh_timer_stop": (c.c_int, [vp, c.POINTER(c.c_double)]),
+        "wh_probe_read_floor": (c.c_int, [vp, vp, sz, sz, sz, c.POINTER(c.c_double), c.POINTER(c.c_uint32),
+                                          c.POINTER(c.c_uint32), c.POINTER(c.c_double)]),
         "wh_moe_batch": (c.c_int, [vp, c.c_uint32, c.POINTER(c.c_uint32), f32p, sz, sz, c.c_uint32, c.c_uint32,
                                    f32p, sz, f32p, sz]),
         "wh_moe_batch_async": (c.c_int, [vp, c.c_uint32, vp, vp, sz, sz, c.c_uint32, c.c_uint32, vp, c.c_int,
@@ -509,6 +512,16 @@ class Context:
         _check(self.lib.wh_profile_routed(self._h, arr, n, len(route_sets), ctypes.c_void_p(x_dev), int(x_is_bf16),
                                           ctypes.c_void_p(out_dev), iters, us), "profile_routed")
         return us[0], us[1]
+
+    def probe_read_floor(self, buf_dev: int, buf_bytes: int, nbytes: int, reps: int):
+        """Fastest plain streaming read of nbytes per launch (rotating windows
+        of the device buffer): (us, grid, depth, empty-launch us)."""
+        us, e = ctypes.c_double(), ctypes.c_double()
+        g, d = ctypes.c_uint32(), ctypes.c_uint32()
+        _check(self.lib.wh_probe_read_floor(self._h, ctypes.c_void_p(buf_dev), buf_bytes, nbytes, reps,
+                                            ctypes.byref(us), ctypes.byref(g), ctypes.byref(d), ctypes.byref(e)),
+               "probe_read_floor")
+        return us.value, g.value, d.value, e.value
 
     @staticmethod
     def gemv_descs(descs):

@@ -25,6 +25,7 @@
 #include "moe_batch.h"
 #include "moe_px.h"
 #include "fp8_mm.h"
+#include "probe.h"
 #include "quant_block.h"
 #include "router.h"
 #include "wohper_hip.h"
@@ -2853,6 +2854,54 @@ int wh_timer_stop(wh_ctx* c, double* elapsed_us) {
     float ms = 0.0f;
     WH_HIP(hipEventElapsedTime(&ms, c->timer[0], c->timer[1]));
     *elapsed_us = (double)ms * 1000.0;
+    return WH_OK;
+}
+
+int wh_probe_read_floor(wh_ctx* c, const void* buf_dev, size_t buf_bytes, size_t bytes, size_t reps,
+                        double* best_us, uint32_t* best_grid, uint32_t* best_depth, double* empty_us) {
+    if (!c || !buf_dev || !best_us || !best_grid || !best_depth || !empty_us || reps == 0 || bytes < 16 ||
+        bytes % 16 || ((uintptr_t)buf_dev & 15))
+        return WH_INVALID_ARGUMENT;
+    const size_t stride = (bytes + 4095) & ~(size_t)4095;  // window pitch
+    if (buf_bytes < stride) return WH_INVALID_SHAPE;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    WH_HIP(c->y_out.ensure(8192 * sizeof(uint32_t), false));
+    uint32_t* out = c->y_out.as<uint32_t>();
+    const size_t windows = std::min<size_t>(buf_bytes / stride, 300);
+    const size_t total16 = bytes / 16;
+    auto time_it = [&](auto&& launch, size_t n, double* us) -> int {
+        for (size_t i = 0; i < 5; ++i) launch(i);
+        WH_HIP(hipEventRecord(c->timer[0], c->stream));
+        for (size_t i = 0; i < n; ++i) launch(i + 7);
+        WH_HIP(hipEventRecord(c->timer[1], c->stream));
+        WH_HIP(hipEventSynchronize(c->timer[1]));
+        float ms = 0.0f;
+        WH_HIP(hipEventElapsedTime(&ms, c->timer[0], c->timer[1]));
+        *us = (double)ms * 1000.0 / (double)n;
+        return WH_OK;
+    };
+    WH_TRY(time_it([&](size_t) { k_empty_launch<<<1024, 256, 0, c->stream>>>(out); }, 200, empty_us));
+    *best_us = 0.0;
+    for (uint32_t grid : {256u, 512u, 1024u, 2048u, 4096u, 8192u}) {
+        const size_t chunk16 = (total16 + grid - 1) / grid;  // every unit in [0, total16) is read once
+        for (uint32_t depth : {4u, 8u, 16u}) {
+            auto launch = [&](size_t i) {
+                const uint4* b = (const uint4*)((const uint8_t*)buf_dev + (i % windows) * stride);
+                if (depth == 4) k_read_floor<4><<<grid, 256, 0, c->stream>>>(b, chunk16, total16, out);
+                else if (depth == 8) k_read_floor<8><<<grid, 256, 0, c->stream>>>(b, chunk16, total16, out);
+                else k_read_floor<16><<<grid, 256, 0, c->stream>>>(b, chunk16, total16, out);
+            };
+            double us = 0.0;
+            WH_TRY(time_it(launch, reps, &us));
+            if (*best_us == 0.0 || us < *best_us) {
+                *best_us = us;
+                *best_grid = grid;
+                *best_depth = depth;
+            }
+        }
+    }
+    WH_HIP(hipGetLastError());
     return WH_OK;
 }
 
