@@ -64,3 +64,35 @@ def test_oracle_is_not_imported_by_the_product():
     for p in (ROOT / "wohper_amd").rglob("*"):
         if p.suffix in (".py", ".hip", ".h", ".c", ".cpp"):
             assert "oracle" not in p.read_text().replace("test", ""), p
+
+
+def _c_prototypes():
+    text = (ROOT / "include" / "wohper_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    protos = {}
+    for m in re.finditer(r"\n(?:int|void|const char\*)\s+(wh_\w+)\s*\(([^;]*)\);", text):
+        params = m.group(2).strip()
+        protos[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
+    return protos
+
+
+def test_rust_binding_matches_the_header():
+    """ffi/rust (not compiled in this image) declares every non-debug entry
+    point of the header with the same parameter count, and its Status enum
+    follows the header's codes in order."""
+    protos = _c_prototypes()
+    sys_rs = (ROOT / "ffi" / "rust" / "src" / "sys.rs").read_text()
+    decl = {}
+    for m in re.finditer(r"pub fn (wh_\w+)\((.*?)\)(?: -> [^;]+)?;", sys_rs, flags=re.S):
+        args = " ".join(m.group(2).split())
+        decl[m.group(1)] = 0 if not args else len([a for a in args.split(",") if a.strip()])
+    wanted = {k: v for k, v in protos.items() if not k.startswith("wh_debug_")}
+    assert decl == wanted
+    lib_rs = (ROOT / "ffi" / "rust" / "src" / "lib.rs").read_text()
+    header = (ROOT / "include" / "wohper_hip.h").read_text()
+    codes = {int(v): k for k, v in re.findall(r"\b(WH_[A-Z0-9_]+) = (\d+)", header.split("enum wh_status")[1].split("};")[0])}
+    arms = dict((int(c), n) for c, n in re.findall(r"^\s+(\d+) => (\w+),$", lib_rs, flags=re.M))
+    assert sorted(arms) == list(range(1, max(codes) + 1))
+    for code, name in arms.items():
+        assert codes[code].replace("WH_", "").replace("_", "").lower() == name.lower() or \
+            (code == 22 and name == "Io"), (code, name, codes[code])
