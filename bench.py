@@ -490,8 +490,9 @@ def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps:
     moe_out = ctx.device_alloc(4096 * 4)
     descs = []
     for hs in layers:
-        d = [(hs["wq_a"], 0, 1024, dev["x"], y), (hs["wq_b"], 0, 32768, dev["qlat"], y + y_off["wq_b"] * 4),
-             (hs["wkv"], 0, 512, dev["x"], y + y_off["wkv"] * 4)]
+        # wq_a and wkv read the same input: one launch
+        d = [(hs["wq_a"], 0, 1024, dev["x"], y), (hs["wkv"], 0, 512, dev["x"], y + y_off["wkv"] * 4),
+             (hs["wq_b"], 0, 32768, dev["qlat"], y + y_off["wq_b"] * 4)]
         d += [(hs["wo_a"], 1024 * g, 1024 * (g + 1), dev["oa"] + g * 4096 * 4, y + (y_off["wo_a"] + 1024 * g) * 4)
               for g in range(8)]
         d += [(hs["wo_b"], 0, 4096, dev["ob"], y + y_off["wo_b"] * 4)]

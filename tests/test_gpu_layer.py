@@ -240,3 +240,68 @@ def test_fp8_shared_expert_bit_exact(ctx, oracle):
     assert np.array_equal(ctx.fp8_shared_expert(*tk, xk, n), wk)
     for h in tk:
         ctx.release(h)
+
+
+def test_fp8_pair_of_one_input_bit_exact(ctx, oracle):
+    """Two projections of one input (wq_a and wkv of a decode layer, and a
+    UE8M0 pair with the reference's +-480 codes) go out as one launch; each
+    stays bit-exact."""
+    rng = np.random.default_rng(47)
+    dev = []
+
+    def alloc(arr):
+        p = ctx.device_alloc(arr.nbytes)
+        ctx.to_device(p, arr)
+        dev.append(p)
+        return p
+
+    ta = ctx.store_fp8_synthetic(1024, 4096, 7, wl.fp8_stream(91, 0), wl.fp8_block_scales(60, 1024, 4096))
+    tk = ctx.store_fp8_synthetic(512, 4096, 7, wl.fp8_stream(91, 2), wl.fp8_block_scales(61, 512, 4096))
+    wa = wl.synth_fp8_host(ctx.lib, 7, wl.fp8_stream(91, 0), 1024, 4096)
+    wk = wl.synth_fp8_host(ctx.lib, 7, wl.fp8_stream(91, 2), 512, 4096)
+    x = rng.standard_normal(4096).astype(np.float32)
+    xp = alloc(x)
+    ya, yk = ctx.device_alloc(1024 * 4), ctx.device_alloc(512 * 4)
+    dev += [ya, yk]
+    # rows 200..1000 of the first, all of the second
+    ctx.fp8_gemv_batch_async([(ta, 200, 1000, xp, ya), (tk, 0, 512, xp, yk)])
+    ctx.synchronize()
+    got_a, got_k = np.empty(800, np.float32), np.empty(512, np.float32)
+    ctx.from_device(got_a, ya)
+    ctx.from_device(got_k, yk)
+    want_a = oracle.fp8_gemv(wa, 1024, 4096, wl.fp8_block_scales(60, 1024, 4096), 8, 32, x, 200, 1000)
+    want_k = oracle.fp8_gemv(wk, 512, 4096, wl.fp8_block_scales(61, 512, 4096), 4, 32, x)
+    assert np.array_equal(bits(got_a), bits(want_a))
+    assert np.array_equal(bits(got_k), bits(want_k))
+    # UE8M0 scales and the special codes in both tensors
+    cases, ts = [], []
+    for seed, rows in ((11, 768), (12, 256)):
+        case = wl.fp8_gemv_case(rows, 2048, seed=seed, ue8m0_compatible=True)
+        w = case.w.copy()
+        w[::7, ::11] = 0x7F
+        w[3::7, 5::11] = 0xFF
+        sb = (np.log2(case.scales).astype(np.int32) + 127).astype(np.uint8)
+        ts.append(ctx.store_fp8(w, rows, 2048, sb, rows // 128, 16, wohper_amd.SCALE_UE8M0))
+        cases.append((w, case.scales, rows))
+    x2 = rng.standard_normal(2048).astype(np.float32)
+    x2p = alloc(x2)
+    ys = [ctx.device_alloc(r * 4) for _, _, r in cases]
+    dev += ys
+    ctx.fp8_gemv_batch_async([(ts[0], 0, 768, x2p, ys[0]), (ts[1], 0, 256, x2p, ys[1])])
+    ctx.synchronize()
+    for (w, sc, rows), yp in zip(cases, ys):
+        got = np.empty(rows, np.float32)
+        ctx.from_device(got, yp)
+        assert np.array_equal(bits(got), bits(oracle.fp8_gemv(w, rows, 2048, sc, rows // 128, 16, x2)))
+    # two tensors writing the same output stay in order: the second's values
+    # win, as with two launches
+    ctx.fp8_gemv_batch_async([(tk, 0, 512, xp, ya), (ta, 0, 512, xp, ya)])
+    ctx.synchronize()
+    got = np.empty(512, np.float32)
+    ctx.from_device(got, ya)
+    want_a0 = oracle.fp8_gemv(wa, 1024, 4096, wl.fp8_block_scales(60, 1024, 4096), 8, 32, x, 0, 512)
+    assert np.array_equal(bits(got), bits(want_a0))
+    for p in dev:
+        ctx.device_free(p)
+    for t in [ta, tk] + ts:
+        ctx.release(t)

@@ -165,6 +165,13 @@ struct wh_fp8_args {
     // 0 = one input for all rows (split-K path only: a power of two, at least
     // WH_FP8_SK_ROWS); x_group_shift = log2(x_group_rows), 32 for one input
     uint32_t x_group_rows, x_group_stride, x_group_shift;
+    // a second tensor on the same input in the same launch (split-K path,
+    // one input, no row groups): workgroups from blocks1 on run its rows
+    // [row_start2, row_end2) into y2; blocks1 = UINT32_MAX for one tensor
+    const uint8_t* w2;
+    const void* scales2;
+    float* y2;
+    uint32_t scale_cols2, row_group_shift2, row_start2, row_end2, blocks1;
 };
 
 template <bool kSpecial, bool kScaleU8>
@@ -287,7 +294,15 @@ __global__ void __launch_bounds__(256) k_fp8_gemv_sk(wh_fp8_args a) {
     constexpr uint32_t kR = WH_FP8_SK_ROWS / 4;  // rows per wave
     extern __shared__ __align__(16) float lds[];
     const uint32_t batch = blockIdx.y;
-    const uint32_t rb = blockIdx.x * WH_FP8_SK_ROWS;  // first row, relative to row_start
+    // the workgroup's tensor: the first, or the second from blocks1 on
+    const bool second = blockIdx.x >= a.blocks1;
+    const uint8_t* const aw = second ? a.w2 : a.w;
+    const void* const ascales = second ? a.scales2 : a.scales;
+    float* const ay = second ? a.y2 : a.y;
+    const uint32_t ascale_cols = second ? a.scale_cols2 : a.scale_cols;
+    const uint32_t arow_group_shift = second ? a.row_group_shift2 : a.row_group_shift;
+    const uint32_t arow_start = second ? a.row_start2 : a.row_start, arow_end = second ? a.row_end2 : a.row_end;
+    const uint32_t rb = (second ? blockIdx.x - a.blocks1 : blockIdx.x) * WH_FP8_SK_ROWS;  // relative to row start
     const float* x = a.x + (size_t)batch * a.x_stride +
                      (a.x_group_shift < 32 ? (size_t)(rb >> a.x_group_shift) * a.x_group_stride : 0);
     const uint32_t lane = threadIdx.x & 7, seg = (threadIdx.x >> 3) & 7;
@@ -303,10 +318,10 @@ __global__ void __launch_bounds__(256) k_fp8_gemv_sk(wh_fp8_args a) {
     uint32_t sbase[kR];
 #pragma unroll
     for (uint32_t j = 0; j < kR; ++j) {
-        const uint32_t r = a.row_start + rb + wv * kR + j;
-        const uint32_t rc = r < a.row_end ? r : a.row_start;  // rows past the end load row_start
-        wp[j] = (const uint4*)(a.w + (size_t)rc * cols) + lane;  // group g at wp[8 g]
-        sbase[j] = (rc >> a.row_group_shift) * a.scale_cols;
+        const uint32_t r = arow_start + rb + wv * kR + j;
+        const uint32_t rc = r < arow_end ? r : arow_start;  // rows past the end load row_start
+        wp[j] = (const uint4*)(aw + (size_t)rc * cols) + lane;  // group g at wp[8 g]
+        sbase[j] = (rc >> arow_group_shift) * ascale_cols;
     }
     // staging loads (x chunk, this lane's share of the rows' scales) go out
     // before the weight loads, so waiting for them never waits for weights
@@ -315,7 +330,7 @@ __global__ void __launch_bounds__(256) k_fp8_gemv_sk(wh_fp8_args a) {
     const uint32_t sg = seg * 8 + lane;  // scales g = sg, sg + 64, ...
     float sv[kR];
 #pragma unroll
-    for (uint32_t j = 0; j < kR; ++j) sv[j] = sg < G ? wh_fp8_scale<kSpecial, kScaleU8>(a.scales, sbase[j] + sg) : 0.0f;
+    for (uint32_t j = 0; j < kR; ++j) sv[j] = sg < G ? wh_fp8_scale<kSpecial, kScaleU8>(ascales, sbase[j] + sg) : 0.0f;
     auto stage_rest = [&]() {
         wh_stage_f32_fp8_store(st, xs);
         for (uint32_t q = threadIdx.x + 256; q < cols / 16; q += 256) {  // cols > 4096
@@ -327,7 +342,7 @@ __global__ void __launch_bounds__(256) k_fp8_gemv_sk(wh_fp8_args a) {
         for (uint32_t j = 0; j < kR; ++j) {
             float* srow = scl + (wv * kR + j) * G;
             if (sg < G) srow[sg] = sv[j];
-            for (uint32_t g = sg + 64; g < G; g += 64) srow[g] = wh_fp8_scale<kSpecial, kScaleU8>(a.scales, sbase[j] + g);
+            for (uint32_t g = sg + 64; g < G; g += 64) srow[g] = wh_fp8_scale<kSpecial, kScaleU8>(ascales, sbase[j] + g);
         }
     };
     if constexpr (kGps > 0) {
@@ -384,9 +399,9 @@ __global__ void __launch_bounds__(256) k_fp8_gemv_sk(wh_fp8_args a) {
         for (uint32_t g = 0; g < G; ++g) acc = __builtin_fmaf(gs[g], sc[g], acc);
     }
     const float sum = wh_hsum8(acc) + 0.0f;  // + tail (0 for col_group % 16 == 0)
-    const uint32_t row = a.row_start + rb + rl;
-    if (row < a.row_end && ln == 0) {
-        a.y[(size_t)batch * a.y_stride + (row - a.row_start)] = sum;
+    const uint32_t row = arow_start + rb + rl;
+    if (row < arow_end && ln == 0) {
+        ay[(size_t)batch * a.y_stride + (row - arow_start)] = sum;
         if (!(fabsf(sum) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
     }
 }

@@ -462,8 +462,11 @@ bool fp8_split_k(const Tensor& t) {
 // path only; see wh_fp8_args).
 int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x, float* y,
                size_t n_batch, size_t x_stride, size_t y_stride, size_t x_group_rows = 0,
-               size_t x_group_stride = 0) {
+               size_t x_group_stride = 0, const Tensor* t2 = nullptr, size_t r0_2 = 0, size_t r1_2 = 0,
+               float* y2 = nullptr) {
     wh_fp8_args a;
+    std::memset(&a, 0, sizeof a);
+    a.blocks1 = UINT32_MAX;
     a.w = t.w;
     a.scales = t.s;
     a.x = x;
@@ -483,8 +486,20 @@ int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x,
     if (x_group_rows && (!fp8_split_k(t) || !is_pow2(x_group_rows) || x_group_rows < WH_FP8_SK_ROWS))
         return WH_UNSUPPORTED;
     bool u8 = t.scale_fmt == WH_SCALE_UE8M0;
+    if (t2) {  // a second tensor on the same input: fp8_pair_ok
+        a.blocks1 = (uint32_t)((r1 - r0 + WH_FP8_SK_ROWS - 1) / WH_FP8_SK_ROWS);
+        a.w2 = t2->w;
+        a.scales2 = t2->s;
+        a.y2 = y2;
+        a.scale_cols2 = (uint32_t)t2->scale_cols;
+        a.row_group_shift2 = log2_of(t2->rows / t2->scale_rows);
+        a.row_start2 = (uint32_t)r0_2;
+        a.row_end2 = (uint32_t)r1_2;
+    }
     if (fp8_split_k(t)) {
-        dim3 grid((unsigned)((r1 - r0 + WH_FP8_SK_ROWS - 1) / WH_FP8_SK_ROWS), (unsigned)n_batch);
+        const size_t blocks = (r1 - r0 + WH_FP8_SK_ROWS - 1) / WH_FP8_SK_ROWS +
+                              (t2 ? (r1_2 - r0_2 + WH_FP8_SK_ROWS - 1) / WH_FP8_SK_ROWS : 0);
+        dim3 grid((unsigned)blocks, (unsigned)n_batch);
         const size_t lds = fp8_sk_lds(t.cols);
         // groups per segment known at compile time for the common widths
         const size_t gps = t.cols / 128 / 8;
@@ -2328,6 +2343,23 @@ int wh_set_fp8_mfma_min(wh_ctx* c, uint32_t min_inputs) {
     return WH_OK;
 }
 
+// Two projections of one input (wq_a and wkv of a decode layer) as one
+// launch: both split-K tensors of the same width, special-code set and
+// scale format, single row runs, one input, neither output overlapping that
+// input or the other output (the descriptors are ordered: where the order
+// could show, the pair stays two launches).
+bool fp8_pair_ok(const Tensor& t1, const wh_gemv_desc& d1, const Tensor& t2, const wh_gemv_desc& d2) {
+    if (d1.x_dev != d2.x_dev || !fp8_split_k(t1) || !fp8_split_k(t2) || t1.cols != t2.cols ||
+        t1.special != t2.special || t1.scale_fmt != t2.scale_fmt)
+        return false;
+    const uintptr_t x_lo = (uintptr_t)d1.x_dev, x_hi = (uintptr_t)(d1.x_dev + t1.cols);
+    const uintptr_t a_lo = (uintptr_t)d1.y_dev, a_hi = (uintptr_t)(d1.y_dev + (d1.row_end - d1.row_start));
+    const uintptr_t b_lo = (uintptr_t)d2.y_dev, b_hi = (uintptr_t)(d2.y_dev + (d2.row_end - d2.row_start));
+    if (a_lo < x_hi && x_lo < a_hi) return false;
+    if (b_lo < x_hi && x_lo < b_hi) return false;
+    return !(a_lo < b_hi && b_lo < a_hi);  // the second's output must not land on the first's
+}
+
 int wh_fp8_gemv_batch_async(wh_ctx* c, const wh_gemv_desc* descs, size_t n) {
     if (!c || (n && !descs)) return WH_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lk(c->mu);
@@ -2365,11 +2397,18 @@ int wh_fp8_gemv_batch_async(wh_ctx* c, const wh_gemv_desc* descs, size_t n) {
                 if (j - i > 1 && y_lo < x_hi && x_lo < y_hi) j = i + 1;
             }
         }
-        if (j - i > 1)
+        if (j - i > 1) {
             WH_TRY(launch_fp8(c, *t, d.row_start, descs[j - 1].row_end, d.x_dev, d.y_dev, 1, t->cols,
                               descs[j - 1].row_end - d.row_start, rows, (size_t)xs));
-        else
+        } else if (i + 1 < n && descs[i + 1].weight != d.weight &&
+                   fp8_pair_ok(*t, d, *find_tensor(c, descs[i + 1].weight), descs[i + 1])) {
+            const wh_gemv_desc& e = descs[i + 1];
+            WH_TRY(launch_fp8(c, *t, d.row_start, d.row_end, d.x_dev, d.y_dev, 1, t->cols, rows, 0, 0,
+                              find_tensor(c, e.weight), e.row_start, e.row_end, e.y_dev));
+            j = i + 2;
+        } else {
             WH_TRY(launch_fp8(c, *t, d.row_start, d.row_end, d.x_dev, d.y_dev, 1, t->cols, rows));
+        }
         i = j;
     }
     return WH_OK;
@@ -3216,7 +3255,14 @@ int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token
     wh_rowpost_args a = rowpost_args(hidden_dev, xq, 1, hidden, hidden, hidden);
     a.aq_len = (uint32_t)hidden;
     WH_TRY(rowpost_launch(c, a));
-    WH_TRY(launch_fp8(c, *wq_a, 0, q_lora, xq, ql, 1, hidden, q_lora));
+    // wq_a and wkv both read the act-quantized x: one launch when they can
+    // share it
+    const bool pair = fp8_split_k(*wq_a) && fp8_split_k(*wkv) && wq_a->special == wkv->special &&
+                      wq_a->scale_fmt == wkv->scale_fmt;
+    if (pair)
+        WH_TRY(launch_fp8(c, *wq_a, 0, q_lora, xq, ql, 1, hidden, q_lora, 0, 0, wkv, 0, head_dim, kvt));
+    else
+        WH_TRY(launch_fp8(c, *wq_a, 0, q_lora, xq, ql, 1, hidden, q_lora));
     a = rowpost_args(ql, ql, 1, q_lora, q_lora, q_lora);
     a.norm = 1;
     a.w = L->q_norm_bf16;
@@ -3232,7 +3278,7 @@ int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token
     WH_TRY(rowpost_launch(c, a));
     // kv path (E/compute.rs:4046-4075): wkv, kv norm, RoPE, act-quant of the
     // non-rope dims, into the cache row of this position
-    WH_TRY(launch_fp8(c, *wkv, 0, head_dim, xq, kvt, 1, hidden, head_dim));
+    if (!pair) WH_TRY(launch_fp8(c, *wkv, 0, head_dim, xq, kvt, 1, hidden, head_dim));
     a = rowpost_args(kvt, kv_row, 1, head_dim, head_dim, head_dim);
     a.norm = 1;
     a.w = L->kv_norm_bf16;
