@@ -422,7 +422,10 @@ int wh_routed_experts_async(wh_ctx* ctx, const wh_expert_route* routes, size_t n
  * is validated before the first launch.  A run of consecutive descriptors on
  * one tensor with equal, adjacent row groups (a power of two of at least 8
  * rows), evenly spaced inputs and back-to-back outputs goes out as one
- * launch; any other descriptor is a launch of its own.  Results are the
+ * launch; so do two consecutive descriptors of different tensors on the same
+ * input (wq_a and wkv) when the tensors share width, scale format and the
+ * special-code flag and neither output overlaps the input or the other
+ * output.  Any other descriptor is a launch of its own.  Results are the
  * same either way. */
 typedef struct {
     wh_tensor weight;
