@@ -41,6 +41,7 @@ struct wh_batch_args {
     uint32_t has_shared;           // the shared expert runs on every position
     wh_expert_ptrs shared;         // ... under the id n_table
     uint32_t mfma_min;             // experts with this many slots take MFMA items (0: never)
+    uint32_t mfma_external;        // the MFMA experts run in k_moe_batch_mx (moe_bmx.h), not here
     const void* x;                 // [npos][hidden], f32 or bf16
     uint32_t x_is_bf16;
     // assignments: i = p * topk + k for the routes, A + p for the shared
@@ -778,7 +779,8 @@ __global__ void __launch_bounds__(256, 3) k_moe_batch_gateup(wh_batch_args a) {
     extern __shared__ __align__(16) float lds[];
     __shared__ uint32_t item_s;
     const uint32_t n_mfma = a.meta[4], mt = a.inter >> 6, et = a.inter >> 4;
-    const uint32_t n_m = n_mfma * 2 * mt, n_items = n_m + (a.meta[0] - n_mfma) * et;
+    const uint32_t n_m = a.mfma_external ? 0u : n_mfma * 2 * mt, n_items = n_m + (a.meta[0] - n_mfma) * et;
+    if (n_items == 0) return;  // before the queue's atomic: every workgroup would take one
     wh_queue q{a.meta + 2, &item_s, 0};
     for (uint32_t item = q.first(); item < n_items; item = q.advance()) {
         q.prefetch();
@@ -837,7 +839,8 @@ __global__ void __launch_bounds__(256, 4) k_moe_batch_down(wh_batch_args a) {
     extern __shared__ __align__(16) float lds[];
     __shared__ uint32_t item_s;
     const uint32_t n_mfma = a.meta[4], mt = a.hidden >> 6, et = a.hidden >> 5;
-    const uint32_t n_m = n_mfma * mt, n_items = n_m + (a.meta[0] - n_mfma) * et;
+    const uint32_t n_m = a.mfma_external ? 0u : n_mfma * mt, n_items = n_m + (a.meta[0] - n_mfma) * et;
+    if (n_items == 0) return;  // before the queue's atomic: every workgroup would take one
     wh_queue q{a.meta + 3, &item_s, 0};
     for (uint32_t item = q.first(); item < n_items; item = q.advance()) {
         q.prefetch();

@@ -25,6 +25,7 @@
 #include "moe_batch.h"
 #include "moe_px.h"
 #include "fp8_mm.h"
+#include "moe_bmx.h"
 #include "probe.h"
 #include "quant_block.h"
 #include "router.h"
@@ -422,6 +423,9 @@ hipError_t kernel_setup_once(int device) {
         set((const void*)k_moe_batch_gateup<16>);
         set((const void*)k_moe_batch_down<0>);
         set((const void*)k_moe_batch_down<8>);
+        set((const void*)k_moe_batch_mx<4096, true>);
+        set((const void*)k_moe_batch_mx<2048, true>);
+        set((const void*)k_moe_batch_mx<2048, false>);
 #define WH_MM_SET(G_)                                    \
         set((const void*)k_fp8_mm<false, false, G_>);    \
         set((const void*)k_fp8_mm<false, true, G_>);     \
@@ -1038,7 +1042,7 @@ int layer_table(wh_ctx* c, uint32_t layer, LayerTable** out) {
 }
 
 // Workgroups of a persistent kernel that fit on the device at once.
-int persistent_grid(const void* kernel, size_t lds, unsigned* grid) {
+int persistent_grid(const void* kernel, size_t lds, unsigned* grid, int threads = 256) {
     static std::mutex mu;
     static std::map<std::pair<const void*, size_t>, unsigned> cache;
     std::lock_guard<std::mutex> lk(mu);
@@ -1050,7 +1054,7 @@ int persistent_grid(const void* kernel, size_t lds, unsigned* grid) {
     int dev = 0, cus = 0, per_cu = 0;
     WH_HIP(hipGetDevice(&dev));
     WH_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    WH_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, lds));
+    WH_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds));
     *grid = (unsigned)std::max(1, cus * std::max(1, per_cu));
     cache[{kernel, lds}] = *grid;
     return WH_OK;
@@ -1118,6 +1122,17 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
     unsigned grid_g = 0, grid_d = 0;
     WH_TRY(persistent_grid(kg, lds_g, &grid_g));
     WH_TRY(persistent_grid(kd, lds_d, &grid_d));
+    // With exact numerics off the MFMA experts run in k_moe_batch_mx (one
+    // 512-thread workgroup per CU) and the other kernels keep the exact ones.
+    const bool mx = !c->exact && c->moe_mfma_min && inter == 2048 && (hidden == 4096 || hidden == 2048) &&
+                    wh_bmx_lds(hidden) <= g_max_lds;
+    const void* kmg = hidden == 4096 ? (const void*)k_moe_batch_mx<4096, true> : (const void*)k_moe_batch_mx<2048, true>;
+    const void* kmd = (const void*)k_moe_batch_mx<2048, false>;
+    unsigned grid_mg = 0, grid_md = 0;
+    if (mx) {
+        WH_TRY(persistent_grid(kmg, wh_bmx_lds(hidden), &grid_mg, 512));
+        WH_TRY(persistent_grid(kmd, wh_bmx_lds(inter), &grid_md, 512));
+    }
     for (size_t p0 = 0; p0 < npos; p0 += chunk) {
         const size_t n = std::min(chunk, npos - p0), slots = n * per_pos;
         wh_batch_args a;
@@ -1159,6 +1174,7 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         a.hs8 = b.hs8;
         a.y = b.y;
         a.mfma_min = c->exact ? 0u : c->moe_mfma_min;  // exact numerics: every expert on the exact items
+        a.mfma_external = mx ? 1u : 0u;
         a.out = out + p0 * hidden;
         a.status = c->status;
         // the most items the queues can hold: used experts <= min(slots, ids),
@@ -1171,6 +1187,10 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         k_moe_batch_quant<<<(unsigned)((n * hidden / 16 + 255) / 256), 256, 0, c->stream>>>(
             a.x, a.x_is_bf16, (uint32_t)n, (uint32_t)hidden, a.xq, a.xq8, a.xs8, a.meta + 6);
         k_moe_batch_pack<<<1, 256, 0, c->stream>>>(a);
+        if (mx) {
+            if (hidden == 4096) k_moe_batch_mx<4096, true><<<grid_mg, 512, wh_bmx_lds(4096), c->stream>>>(a);
+            else k_moe_batch_mx<2048, true><<<grid_mg, 512, wh_bmx_lds(2048), c->stream>>>(a);
+        }
         if (hidden == 4096) k_moe_batch_gateup<16><<<gg, 256, lds_g, c->stream>>>(a);
         else k_moe_batch_gateup<0><<<gg, 256, lds_g, c->stream>>>(a);
         c->moe_last_slots = npos <= chunk ? slots : 0;
@@ -1181,6 +1201,7 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
             a.g, a.u, a.h, (uint32_t)(slots * inter));
         k_moe_batch_quant<<<(unsigned)((slots * inter / 16 + 255) / 256), 256, 0, c->stream>>>(
             a.h, 0u, (uint32_t)slots, (uint32_t)inter, a.hq, a.hq8, a.hs8, nullptr);
+        if (mx) k_moe_batch_mx<2048, false><<<grid_md, 512, wh_bmx_lds(2048), c->stream>>>(a);
         if (inter == 2048) k_moe_batch_down<8><<<gd, 256, lds_d, c->stream>>>(a);
         else k_moe_batch_down<0><<<gd, 256, lds_d, c->stream>>>(a);
         k_moe_batch_accumulate<<<dim3((unsigned)((hidden + 255) / 256), (unsigned)n), 256, 0, c->stream>>>(a);
