@@ -12,10 +12,14 @@
 //                        (counts, offsets, placement), the used experts in
 //                        ascending id, their work order, each position's
 //                        accumulation order
+//   k_moe_batch_mx       (exact numerics off) persistent MFMA kernel of the
+//                        MFMA experts' gate and up matvecs (moe_bmx.h)
 //   k_moe_batch_gateup   persistent: (expert, row tile) items from a queue,
-//                        gate and up matvecs of every slot
+//                        gate and up matvecs of every slot (after
+//                        k_moe_batch_mx: the exact experts only)
 //   k_moe_batch_swiglu   SwiGLU of every slot
 //   k_moe_batch_quant    act-quant of every slot's SwiGLU output
+//   k_moe_batch_mx       down of the MFMA experts
 //   k_moe_batch_down     persistent, as gate/up
 //   k_moe_batch_accumulate
 // Experts with at least `mfma_min` tokens take the MFMA items (block-scaled

@@ -84,6 +84,13 @@ __device__ __forceinline__ void wh_mx_raw_load_global(wh_mx_raw& r, const uint8_
     r.s = wh_ld8_global(srow + blk * 8);
 }
 
+// A value every lane of the wave holds alike, moved to scalar registers.
+__device__ __forceinline__ uint32_t wh_uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ const uint8_t* wh_uni(const uint8_t* p) {
+    const uint64_t v = (uint64_t)p;
+    return (const uint8_t*)(((uint64_t)wh_uni((uint32_t)(v >> 32)) << 32) | wh_uni((uint32_t)v));
+}
+
 // A staged virtual expert: its matrices (gate/up: w1, w3; down: w2 twice),
 // its first slot and its slot count (<= 16).
 struct wh_bmx_v {
@@ -182,9 +189,12 @@ __global__ void __launch_bounds__(512, 1) k_moe_batch_mx(wh_batch_args a) {
         // array indexed at run time would live in scratch memory)
         // (a copy of the struct itself goes through scratch memory)
         const uint32_t x1 = nv > 1 ? 1 : 0;
-        const uint8_t *w0a = vm[0].wa, *w0b = vm[0].wb, *s0a = vm[0].sa, *s0b = vm[0].sb;
-        const uint8_t *w1a = vm[x1].wa, *w1b = vm[x1].wb, *s1a = vm[x1].sa, *s1b = vm[x1].sb;
-        const uint32_t slot0_0 = vm[0].slot0, slot0_1 = vm[x1].slot0, cnt0 = vm[0].count, cnt1 = vm[x1].count;
+        const uint8_t *w0a = wh_uni(vm[0].wa), *w0b = wh_uni(vm[0].wb), *s0a = wh_uni(vm[0].sa),
+                      *s0b = wh_uni(vm[0].sb);
+        const uint8_t *w1a = wh_uni(vm[x1].wa), *w1b = wh_uni(vm[x1].wb), *s1a = wh_uni(vm[x1].sa),
+                      *s1b = wh_uni(vm[x1].sb);
+        const uint32_t slot0_0 = wh_uni(vm[0].slot0), slot0_1 = wh_uni(vm[x1].slot0), cnt0 = wh_uni(vm[0].count),
+                       cnt1 = wh_uni(vm[x1].count);
         // B staging loads (codes: kCols pieces per virtual expert, then the
         // E8M0 bytes: G pieces), issued before this wave's first weight loads
         constexpr uint32_t KB = (2 * WH_BMX_TOK * CPS + 511) / 512, KS = (2 * WH_BMX_TOK * G / 16 + 511) / 512;
@@ -203,7 +213,7 @@ __global__ void __launch_bounds__(512, 1) k_moe_batch_mx(wh_batch_args a) {
         // this wave's items of the phase and their blocks
         const uint32_t ps = i0 > vp * per_v ? i0 : vp * per_v;
         const uint32_t pe = i1 < (vp + nv) * per_v ? i1 : (vp + nv) * per_v;
-        const uint32_t it0 = ps + wave;
+        const uint32_t it0 = wh_uni(ps + wave);
         const uint32_t n_items = it0 < pe ? (pe - it0 + 7) / 8 : 0;
         const uint32_t J = n_items * NB;
         // block j of the wave: item it0 + 8 (j / NB) = virtual expert vp + q,
