@@ -36,6 +36,13 @@
 typedef int wh_v8i __attribute__((ext_vector_type(8)));
 typedef float wh_v4f __attribute__((ext_vector_type(4)));
 
+// A virtual expert of the MFMA kernels (moe_bmx.h): one MFMA expert's
+// slots slot0 .. slot0 + count - 1 (count <= 16) and its matrices.
+struct wh_bmx_vt {
+    const uint8_t *w1, *s1, *w3, *s3, *w2, *s2;
+    uint32_t slot0, count;
+};
+
 struct wh_batch_args {
     const wh_expert_ptrs* table;   // the layer's experts by id (null w1 = not resident)
     uint32_t n_table;              // valid ids are < n_table
@@ -59,7 +66,9 @@ struct wh_batch_args {
     uint32_t* meta;                // [0] used experts, [1] routes valid, [2]/[3] work queues
                                    // of gate/up and down, [4] experts on MFMA items, [6] an
                                    // input block held an inf or NaN (set by the quant of x,
-                                   // read and cleared by the pack)
+                                   // read and cleared by the pack), [7] virtual experts
+    wh_bmx_vt* vtab;               // [S] the MFMA experts' virtual experts, in work order
+    uint32_t* pos;                 // [S] position of each slot
     float* xq;                     // [npos][hidden] act-quantized inputs (column order)
     uint8_t* xq8;                  // [npos][hidden] their E4M3 codes, MFMA group order
     uint8_t* xs8;                  // [npos][hidden / 32] E8M0 scale bytes (x 1/8)
@@ -112,6 +121,7 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
     __shared__ uint32_t ids[WH_BATCH_MAX_ASSIGN];
     __shared__ uint32_t slot_of[WH_BATCH_MAX_ASSIGN];
     __shared__ uint32_t cnt[WH_BATCH_MAX_TABLE], off[WH_BATCH_MAX_TABLE], ucnt[WH_BATCH_MAX_TABLE];
+    __shared__ uint32_t uoffl[WH_BATCH_MAX_TABLE], uexpl[WH_BATCH_MAX_TABLE], uordl[WH_BATCH_MAX_TABLE];
     __shared__ uint32_t tot[4];
     __shared__ uint32_t bad, n_mfma, mfma_min;
     const uint32_t A = a.npos * a.topk, S = A + a.has_shared * a.npos, tid = threadIdx.x;
@@ -156,6 +166,7 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
     if (bad) {
         if (tid == 0) {
             for (int i = 0; i < 5; ++i) a.meta[i] = 0;
+            a.meta[7] = 0;
             atomicOr(a.status, WH_ST_NOT_RESIDENT);
         }
         return;
@@ -184,6 +195,8 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
             if (c4[j]) {
                 a.uexp[u] = e;
                 a.uoff[u] = o;
+                uexpl[u] = e;
+                uoffl[u] = o;
                 ucnt[u] = c4[j];
                 if (mfma_min && c4[j] >= mfma_min) atomicAdd(&n_mfma, 1u);
                 ++u;
@@ -199,6 +212,7 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
         const uint32_t e = ids[i];
         const uint32_t s = i >= A ? i : off[e] + atomicAdd(&cnt[e], 1u);
         a.sorted[s] = i;
+        a.pos[s] = wh_slot_pos(a, i);
         slot_of[i] = s;
     }
     // work order: most slots first, ties by ascending id (rank counting)
@@ -210,8 +224,38 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
             r += cw > cv || (cw == cv && w < v);
         }
         a.uorder[r] = v;
+        uordl[r] = v;
     }
     __syncthreads();
+    // the MFMA experts (the first n_mfma of the work order) as virtual
+    // experts of at most 16 slots; thread t takes work-order entries
+    // 4t .. 4t + 3
+    {
+        uint32_t ch[4], csum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t i = 4 * tid + j;
+            ch[j] = i < n_mfma ? (ucnt[uordl[i]] + 15) / 16 : 0u;
+            csum += ch[j];
+        }
+        uint32_t V;
+        uint32_t v = wh_wg_exclusive_scan(csum, tot, &V);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t i = 4 * tid + j;
+            if (i >= n_mfma) continue;
+            const uint32_t ui = uordl[i];
+            const wh_expert_ptrs ep = wh_batch_expert(a, uexpl[ui]);
+            for (uint32_t c = 0; c < ch[j]; ++c, ++v) {
+                wh_bmx_vt t;
+                t.w1 = ep.w1, t.s1 = ep.s1, t.w3 = ep.w3, t.s3 = ep.s3, t.w2 = ep.w2, t.s2 = ep.s2;
+                t.slot0 = uoffl[ui] + 16 * c;
+                t.count = ucnt[ui] - 16 * c < 16 ? ucnt[ui] - 16 * c : 16u;
+                a.vtab[v] = t;
+            }
+        }
+        if (tid == 0) a.meta[7] = V;
+    }
     // each position's route slots by ascending expert id, equal ids in route
     // order (E/server/generation.rs:2491-2506 pushes targets in that order)
     for (uint32_t p = tid; p < a.npos; p += 256) {

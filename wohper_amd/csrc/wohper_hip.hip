@@ -1065,7 +1065,8 @@ size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 // Device layout of one batch chunk inside c->batch.
 struct BatchBufs {
     float* wgt;
-    uint32_t *sorted, *uexp, *uoff, *uorder, *acc_order, *meta;
+    uint32_t *sorted, *uexp, *uoff, *uorder, *acc_order, *meta, *pos;
+    wh_bmx_vt* vtab;
     float *xq, *g, *u, *h, *hq, *y;
     uint8_t *xq8, *xs8, *hq8, *hs8;
 };
@@ -1083,7 +1084,8 @@ int batch_bufs(wh_ctx* c, size_t npos, size_t slots, size_t hidden, size_t inter
                  o_h = take(slots * inter * 4),
                  o_y = take(slots * hidden * 4),
                  o_hq = take(slots * inter * 4), o_xq8 = take(npos * hidden), o_xs8 = take(npos * hidden / 32),
-                 o_hq8 = take(slots * inter), o_hs8 = take(slots * inter / 32);
+                 o_hq8 = take(slots * inter), o_hs8 = take(slots * inter / 32),
+                 o_vt = take(slots * sizeof(wh_bmx_vt)), o_pos = take(slots * 4);
     WH_HIP(c->batch.ensure(off, true));  // zeroed when (re)allocated: meta's flag starts clear
     uint8_t* base = c->batch.as<uint8_t>();
     b->wgt = (float*)(base + o_w);
@@ -1103,6 +1105,8 @@ int batch_bufs(wh_ctx* c, size_t npos, size_t slots, size_t hidden, size_t inter
     b->xs8 = base + o_xs8;
     b->hq8 = base + o_hq8;
     b->hs8 = base + o_hs8;
+    b->vtab = (wh_bmx_vt*)(base + o_vt);
+    b->pos = (uint32_t*)(base + o_pos);
     return WH_OK;
 }
 
@@ -1163,6 +1167,8 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         a.uorder = b.uorder;
         a.acc_order = b.acc_order;
         a.meta = b.meta;
+        a.vtab = b.vtab;
+        a.pos = b.pos;
         a.xq = b.xq;
         a.xq8 = b.xq8;
         a.xs8 = b.xs8;
