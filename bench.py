@@ -632,6 +632,86 @@ def decode_stack_batch16(ctx, layers, n_layers: int, steps: int, seed: int, batc
             "tokens_per_s": round(batch / (step_us * 1e-6), 1)}
 
 
+TIMELINE_POINTS = {
+    "token_gateup": ["start", "x, tables staged", "x act-quantized", "tile 0 done", "tile 1 done", "tile 2 done",
+                     "tile 3 done", "end"],
+    "token_down": ["start", "h, tables staged", "h act-quantized", "unit 0 done", "unit 1 done", "unit 2 done",
+                   "unit 3 done", "end"],
+    "batch_gateup": ["start", "ring issued", "B staged", "wave's last item done", "workgroup end"],
+    "batch_down": ["start", "ring issued", "B staged", "wave's last item done", "workgroup end"],
+}
+
+
+def timeline(lib_path: str, seed: int = 2) -> dict:
+    """Per-wave timelines of the persistent expert kernels from the measuring
+    build (python -m wohper_amd.build --timeline PATH): the routed FP4 token
+    (MFMA numerics; k_moe_gateup_px, k_moe_down_px) and the batch-16 MoE with
+    the shared expert (k_moe_batch_mx gate/up and down).  Each kernel's lane 0
+    of every wave of the first 256 workgroups stamps s_memrealtime (100 MHz)
+    at fixed points; returned: per point the 0/10/50/90/100th percentiles in
+    us from the launch's earliest start stamp, of the last of 12 calls."""
+    import ctypes
+
+    import wohper_amd
+    from wohper_amd import workloads as wl
+
+    lib = wohper_amd.load_library(lib_path)
+    if not hasattr(lib, "wh_debug_timeline"):
+        raise SystemExit(f"{lib_path} is not a timeline build (python -m wohper_amd.build --timeline PATH)")
+    wohper_amd._lib = lib
+    lib.wh_debug_timeline.restype = ctypes.c_int
+    lib.wh_debug_timeline.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
+    ctx = wohper_amd.Context(0)
+    ctx.set_exact_numerics(False)
+    n_layers = 4
+    for layer in range(n_layers):
+        for e in range(wl.N_ROUTED + 1):
+            ctx.store_expert_synthetic(layer, e, wl.HIDDEN, wl.INTER, seed)
+    rng = np.random.default_rng(seed)
+    n_stamp = 512 * 16 * 8
+
+    def read(which, names):
+        buf = np.zeros(n_stamp, np.uint64)
+        assert lib.wh_debug_timeline(which, buf.ctypes.data, n_stamp) == 0
+        t = buf.reshape(512, 16, 8)[:256].astype(np.int64)
+        t0 = t[:, :, 0][t[:, :, 0] > 0].min()
+        out = {}
+        for k, name in enumerate(names):
+            v = t[:, :, k].ravel()
+            v = (v[v > 0] - t0) * 0.01
+            if v.size:
+                out[name] = [round(float(np.percentile(v, q)), 2) for q in (0, 10, 50, 90, 100)]
+        return out
+
+    res = {"percentiles": [0, 10, 50, 90, 100], "unit": "us from the launch's first start stamp"}
+    x = wl.bf16_bits(rng.standard_normal((1, wl.HIDDEN)).astype(np.float32))
+    x_dev, out_dev = ctx.device_alloc(x.nbytes), ctx.device_alloc(wl.HIDDEN * 4)
+    ctx.to_device(x_dev, x)
+    for i in range(12):
+        idx, w = wl.route_topk_sigmoid(rng.standard_normal(wl.N_ROUTED).astype(np.float32))
+        ctx.routed_experts_async([(i % n_layers, int(e), float(wt)) for e, wt in zip(idx, w)], x_dev, True, 1,
+                                 out_dev)
+        ctx.synchronize()
+    res["token_gateup"] = read(0, TIMELINE_POINTS["token_gateup"])
+    res["token_down"] = read(1, TIMELINE_POINTS["token_down"])
+    npos = 16
+    ids = np.stack([rng.choice(wl.N_ROUTED, wl.TOPK, replace=False) for _ in range(npos)]).astype(np.uint32)
+    sc = rng.uniform(0.1, 1.0, (npos, wl.TOPK)).astype(np.float32)
+    xb = wl.bf16_bits(rng.standard_normal((npos, wl.HIDDEN)).astype(np.float32))
+    xd, idd, scd, od = (ctx.device_alloc(xb.nbytes), ctx.device_alloc(ids.nbytes), ctx.device_alloc(sc.nbytes),
+                        ctx.device_alloc(npos * wl.HIDDEN * 4))
+    ctx.to_device(xd, xb)
+    ctx.to_device(idd, ids)
+    ctx.to_device(scd, sc)
+    for i in range(12):
+        ctx.moe_batch_async(i % n_layers, idd, scd, npos, wl.TOPK, xd, True, od, shared_key=(i % n_layers, wl.N_ROUTED))
+        ctx.synchronize()
+    res["batch_gateup"] = read(0, TIMELINE_POINTS["batch_gateup"])
+    res["batch_down"] = read(1, TIMELINE_POINTS["batch_down"])
+    ctx.close()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -653,6 +733,9 @@ def main():
     ap.add_argument("--batch-mfma-sweep", type=str, default="",
                     help="only time the ragged batch leg: exact items, then each MFMA threshold of this "
                          "comma-separated list (one JSON line each)")
+    ap.add_argument("--timeline", type=str, default="",
+                    help="only print the per-wave timelines of the expert kernels from this measuring build "
+                         "(python -m wohper_amd.build --timeline PATH)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 5 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -660,6 +743,10 @@ def main():
         print(f"bench.py measures one GPU only (every box here has one MI355X); --gpus {args.gpus} is not supported",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.timeline:
+        print(json.dumps(timeline(args.timeline)), flush=True)
+        return
 
     import wohper_amd
     from wohper_amd import workloads as wl

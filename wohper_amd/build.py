@@ -68,10 +68,15 @@ def build_libm_tables(verbose: bool = True) -> Path:
     return inc
 
 
-def build(verbose: bool = True) -> Path:
+def build(verbose: bool = True, timeline: Path | None = None) -> Path:
+    """Builds libwohper_hip.so in the package.  timeline: instead build the
+    per-wave timeline variant (-DWH_TIMELINE: the persistent expert kernels
+    stamp s_memrealtime at fixed points, read back with wh_debug_timeline)
+    to that path; it is a measuring build, not the product."""
     build_libm_tables(verbose)
-    cmd = [_hipcc(), *HIP_FLAGS, "-I", str(ROOT / "include"), "-I", str(CSRC), "-I", str(GEN),
-           "-o", str(LIB) + ".tmp", str(CSRC / "wohper_hip.hip")]
+    out = Path(timeline) if timeline else LIB
+    cmd = [_hipcc(), *HIP_FLAGS, *(["-DWH_TIMELINE"] if timeline else []), "-I", str(ROOT / "include"),
+           "-I", str(CSRC), "-I", str(GEN), "-o", str(out) + ".tmp", str(CSRC / "wohper_hip.hip")]
     if verbose:
         print("[wohper_amd] " + " ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -82,9 +87,14 @@ def build(verbose: bool = True) -> Path:
         raise RuntimeError("hipcc failed building libwohper_hip.so")
     if noise and verbose:
         sys.stderr.write("\n".join(noise) + "\n")
-    os.replace(str(LIB) + ".tmp", LIB)
-    return LIB
+    os.replace(str(out) + ".tmp", out)
+    return out
 
 
 if __name__ == "__main__":
-    build()
+    import argparse
+
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--timeline", type=Path, default=None,
+                    help="build the per-wave timeline variant to this path instead of the product library")
+    build(timeline=ap.parse_args().timeline)

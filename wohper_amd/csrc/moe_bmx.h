@@ -85,6 +85,9 @@ __global__ void __launch_bounds__(512, 1) k_moe_batch_mx(wh_batch_args a) {
     constexpr int D = WH_BMX_DEPTH;
     static_assert(NB == 8 || NB == 16, "2048 or 4096 columns");
     static_assert(D < (int)NB, "the ring spans at most two items");
+    // timeline points (builds with -DWH_TIMELINE): 0 start, 1 ring issued,
+    // 2 B staged, 3 the wave's last item done, 4 the workgroup's end
+    WH_TL(kGate ? 0 : 1, 0);
     const uint32_t V = a.meta[7];
     if (V == 0 || a.meta[1] == 0) return;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, L = tid & 63, g = L >> 4, nl = L & 15;
@@ -152,6 +155,7 @@ __global__ void __launch_bounds__(512, 1) k_moe_batch_mx(wh_batch_args a) {
             for (int d = 0; d < D; ++d) WH_BMX_ISSUE(ring[d], 0u);
         }
         __builtin_amdgcn_sched_barrier(0);
+        WH_TL(kGate ? 0 : 1, 1);
         // where each staged slot's codes come from
         if (tid < nv * WH_BMX_TOK) {
             const uint32_t q = tid / WH_BMX_TOK, n = tid % WH_BMX_TOK;
@@ -189,6 +193,7 @@ __global__ void __launch_bounds__(512, 1) k_moe_batch_mx(wh_batch_args a) {
                 *(uint4*)(lds + q * BUF + WH_BMX_TOK * TS + n * G + 16 * c) = sst[k];
         }
         __syncthreads();
+        WH_TL(kGate ? 0 : 1, 2);
         // consume side: block cur_blk of item cur_it
         uint32_t cur_it = wh_uni(ps + wave), cur_blk = 0;
         uint32_t dep = wh_opaque_zero(__uint_as_float(*(const uint32_t*)lds));
@@ -228,7 +233,9 @@ __global__ void __launch_bounds__(512, 1) k_moe_batch_mx(wh_batch_args a) {
         }
 #undef WH_BMX_ISSUE
 #undef WH_BMX_ITEM
+        WH_TL(kGate ? 0 : 1, 3);
         if (nf) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
         __syncthreads();  // the phase's buffers and counter are free
     }
+    WH_TL(kGate ? 0 : 1, 4);
 }
