@@ -120,8 +120,10 @@ __device__ __forceinline__ uint32_t wh_wg_exclusive_scan(uint32_t v, uint32_t* t
 __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
     __shared__ uint32_t ids[WH_BATCH_MAX_ASSIGN];
     __shared__ uint32_t slot_of[WH_BATCH_MAX_ASSIGN];
-    __shared__ uint32_t cnt[WH_BATCH_MAX_TABLE], off[WH_BATCH_MAX_TABLE], ucnt[WH_BATCH_MAX_TABLE];
+    __shared__ uint32_t cnt[WH_BATCH_MAX_TABLE], off[WH_BATCH_MAX_TABLE];
+    __shared__ __align__(16) uint32_t ucnt[WH_BATCH_MAX_TABLE];
     __shared__ uint32_t uoffl[WH_BATCH_MAX_TABLE], uexpl[WH_BATCH_MAX_TABLE], uordl[WH_BATCH_MAX_TABLE];
+    __shared__ uint32_t vst[WH_BATCH_MAX_TABLE];  // per work-order position: its virtual experts, then their start
     __shared__ uint32_t tot[4];
     __shared__ uint32_t bad, n_mfma, mfma_min;
     const uint32_t A = a.npos * a.topk, S = A + a.has_shared * a.npos, tid = threadIdx.x;
@@ -215,62 +217,95 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
         a.pos[s] = wh_slot_pos(a, i);
         slot_of[i] = s;
     }
-    // work order: most slots first, ties by ascending id (rank counting)
-    for (uint32_t v = tid; v < U; v += 256) {
+    // work order: most slots first, ties by ascending id (rank counting);
+    // thread t owns used experts t, t + 256, ... and requests their matrices
+    // first, so that the round trip overlaps the counting
+    constexpr int kOwn = WH_BATCH_MAX_TABLE / 256;
+    wh_expert_ptrs own[kOwn];
+    uint32_t own_r[kOwn];
+#pragma unroll
+    for (int k = 0; k < kOwn; ++k) {
+        const uint32_t v = tid + 256 * k;
+        if (v < U) own[k] = wh_batch_expert(a, uexpl[v]);
+    }
+#pragma unroll
+    for (int k = 0; k < kOwn; ++k) {
+        const uint32_t v = tid + 256 * k;
+        own_r[k] = 0;
+        if (v >= U) continue;
         const uint32_t cv = ucnt[v];
-        uint32_t r = 0;
-        for (uint32_t w = 0; w < U; ++w) {
+        uint32_t r = 0, w = 0;
+        for (; w + 4 <= U; w += 4) {
+            const uint4 c = *(const uint4*)&ucnt[w];
+            r += (c.x > cv || (c.x == cv && w < v)) + (c.y > cv || (c.y == cv && w + 1 < v)) +
+                 (c.z > cv || (c.z == cv && w + 2 < v)) + (c.w > cv || (c.w == cv && w + 3 < v));
+        }
+        for (; w < U; ++w) {
             const uint32_t cw = ucnt[w];
             r += cw > cv || (cw == cv && w < v);
         }
+        own_r[k] = r;
         a.uorder[r] = v;
         uordl[r] = v;
+        // the MFMA experts (the first n_mfma of the work order) become
+        // virtual experts of at most 16 slots
+        vst[r] = r < n_mfma ? (cv + 15) / 16 : 0u;
     }
     __syncthreads();
-    // the MFMA experts (the first n_mfma of the work order) as virtual
-    // experts of at most 16 slots; thread t takes work-order entries
-    // 4t .. 4t + 3
+    // their start in the list: a scan over the work order (positions
+    // 4t .. 4t + 3 per thread)
     {
         uint32_t ch[4], csum = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t i = 4 * tid + j;
-            ch[j] = i < n_mfma ? (ucnt[uordl[i]] + 15) / 16 : 0u;
+            ch[j] = i < U ? vst[i] : 0u;
             csum += ch[j];
         }
         uint32_t V;
-        uint32_t v = wh_wg_exclusive_scan(csum, tot, &V);
+        uint32_t v0 = wh_wg_exclusive_scan(csum, tot, &V);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t i = 4 * tid + j;
-            if (i >= n_mfma) continue;
-            const uint32_t ui = uordl[i];
-            const wh_expert_ptrs ep = wh_batch_expert(a, uexpl[ui]);
-            for (uint32_t c = 0; c < ch[j]; ++c, ++v) {
-                wh_bmx_vt t;
-                t.w1 = ep.w1, t.s1 = ep.s1, t.w3 = ep.w3, t.s3 = ep.s3, t.w2 = ep.w2, t.s2 = ep.s2;
-                t.slot0 = uoffl[ui] + 16 * c;
-                t.count = ucnt[ui] - 16 * c < 16 ? ucnt[ui] - 16 * c : 16u;
-                a.vtab[v] = t;
-            }
+            if (i < U) vst[i] = v0;
+            v0 += ch[j];
         }
         if (tid == 0) a.meta[7] = V;
     }
-    // each position's route slots by ascending expert id, equal ids in route
-    // order (E/server/generation.rs:2491-2506 pushes targets in that order)
-    for (uint32_t p = tid; p < a.npos; p += 256) {
-        uint32_t key[WH_BATCH_MAX_TOPK];
-        const uint32_t k0 = p * a.topk;
-        for (uint32_t k = 0; k < a.topk; ++k) {
-            const uint32_t kk = (ids[k0 + k] << 4) | k;
-            uint32_t j = k;
-            while (j > 0 && key[j - 1] > kk) {
-                key[j] = key[j - 1];
-                --j;
-            }
-            key[j] = kk;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kOwn; ++k) {
+        const uint32_t v = tid + 256 * k;
+        if (v >= U || own_r[k] >= n_mfma) continue;
+        const wh_expert_ptrs ep = own[k];
+        uint32_t vi = vst[own_r[k]];
+        for (uint32_t c = 0; 16 * c < ucnt[v]; ++c, ++vi) {
+            wh_bmx_vt t;
+            t.w1 = ep.w1, t.s1 = ep.s1, t.w3 = ep.w3, t.s3 = ep.s3, t.w2 = ep.w2, t.s2 = ep.s2;
+            t.slot0 = uoffl[v] + 16 * c;
+            t.count = ucnt[v] - 16 * c < 16 ? ucnt[v] - 16 * c : 16u;
+            a.vtab[vi] = t;
         }
-        for (uint32_t k = 0; k < a.topk; ++k) a.acc_order[k0 + k] = slot_of[k0 + (key[k] & 15u)];
+    }
+    // each position's route slots by ascending expert id, equal ids in route
+    // order (E/server/generation.rs:2491-2506 pushes targets in that order):
+    // key (id, route index) is distinct, and its rank among the position's
+    // keys is its place (compile-time indices only: the keys stay in
+    // registers)
+    for (uint32_t p = tid; p < a.npos; p += 256) {
+        const uint32_t k0 = p * a.topk;
+        uint32_t key[WH_BATCH_MAX_TOPK];
+#pragma unroll
+        for (uint32_t k = 0; k < WH_BATCH_MAX_TOPK; ++k) key[k] = k < a.topk ? (ids[k0 + k] << 4) | k : 0xffffffffu;
+#pragma unroll
+        for (uint32_t k = 0; k < WH_BATCH_MAX_TOPK; ++k) {
+            if (k < a.topk) {
+                uint32_t r = 0;
+#pragma unroll
+                for (uint32_t j = 0; j < WH_BATCH_MAX_TOPK; ++j) r += key[j] < key[k];
+                a.acc_order[k0 + r] = slot_of[k0 + k];
+            }
+        }
     }
     if (tid == 0) {
         a.meta[0] = U;
