@@ -152,9 +152,12 @@ def test_batch_generic_shapes(ctx, oracle):
     assert np.array_equal(bits(got), bits(want))
 
 
-def _mfma_case(ctx, oracle, layer, n_exp, hidden, inter, seed, npos, mfma_min):
+def _mfma_case(ctx, oracle, layer, n_exp, hidden, inter, seed, npos, mfma_min, routes=None):
+    """routes: (ids, scores, x) instead of the Zipf routing; returns the
+    worst matvec |diff| / tolerance and the count of virtual experts."""
     _store(ctx, layer, n_exp, hidden, inter, seed)
-    ids, sc, x = wl.zipf_batch_routes(seed=seed, n_tokens=npos, n_experts=n_exp, hidden=hidden)
+    ids, sc, x = routes if routes is not None else wl.zipf_batch_routes(seed=seed, n_tokens=npos, n_experts=n_exp,
+                                                                       hidden=hidden)
     experts = _host(ctx, layer, ids, seed, hidden, inter)
     topk, S = ids.shape[1], ids.size
     ctx.set_exact_numerics(False)
@@ -167,7 +170,7 @@ def _mfma_case(ctx, oracle, layer, n_exp, hidden, inter, seed, npos, mfma_min):
     srt, gate, up = rd(0, S, np.uint32), rd(1, (S, inter), np.float32), rd(2, (S, inter), np.float32)
     y, hq = rd(3, (S, hidden), np.float32), rd(8, (S, inter), np.float32)
     meta, uoff, uexp, uorder = rd(4, 8, np.uint32), rd(5, S + 1, np.uint32), rd(6, S, np.uint32), rd(7, S, np.uint32)
-    n_used, n_mfma = int(meta[0]), int(meta[4])
+    n_used, n_mfma, n_virtual = int(meta[0]), int(meta[4]), int(meta[7])
     assert 0 < n_mfma <= n_used, (n_used, n_mfma)
     if mfma_min > 1:
         assert n_mfma < n_used, (n_used, n_mfma)  # both paths run
@@ -197,18 +200,35 @@ def _mfma_case(ctx, oracle, layer, n_exp, hidden, inter, seed, npos, mfma_min):
     # the oracle's output is compared in norm only
     want = oracle.moe_batch(experts, ids, sc, x)
     assert np.linalg.norm(out - want) <= 1e-3 * np.linalg.norm(want)
-    return worst
+    return worst, n_virtual
 
 
 def test_batch_mfma_small_shapes(ctx, oracle):
-    worst = _mfma_case(ctx, oracle, 44, 12, 512, 256, 33, 48, 8)
+    worst, _ = _mfma_case(ctx, oracle, 44, 12, 512, 256, 33, 48, 8)
     print(f"worst MFMA matvec |diff| / tolerance: {worst:.3f}")
 
 
 @pytest.mark.parametrize("mfma_min", [16, DEFAULT_MFMA_MIN])
 def test_batch_mfma_real_shapes(ctx, oracle, mfma_min):
-    worst = _mfma_case(ctx, oracle, 45, 8, wl.HIDDEN, wl.INTER, 34, 24, mfma_min)
+    worst, _ = _mfma_case(ctx, oracle, 45, 8, wl.HIDDEN, wl.INTER, 34, 24, mfma_min)
     print(f"worst MFMA matvec |diff| / tolerance: {worst:.3f}")
+
+
+def test_batch_mfma_more_virtual_experts_than_workgroups(ctx, oracle):
+    """More than 256 virtual experts (about 300 experts on 300 positions,
+    uniform top-6): the persistent MFMA kernels' workgroups each cover more
+    than two virtual experts and stage them in phases of two; every matvec
+    within tolerance and every other stage bit-exact, as above."""
+    hidden = inter = 2048
+    n_exp, npos, seed = 300, 300, 36
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.choice(n_exp, 6, replace=False) for _ in range(npos)]).astype(np.uint32)
+    sc = rng.uniform(0.05, 1.0, (npos, 6)).astype(np.float32)
+    x = rng.standard_normal((npos, hidden)).astype(np.float32)
+    worst, n_virtual = _mfma_case(ctx, oracle, 47, n_exp, hidden, inter, seed, npos, DEFAULT_MFMA_MIN,
+                                  routes=(ids, sc, x))
+    assert n_virtual > 256, n_virtual
+    print(f"{n_virtual} virtual experts; worst MFMA matvec |diff| / tolerance: {worst:.3f}")
 
 
 def test_batch_exact_numerics_override_the_threshold(ctx, oracle):

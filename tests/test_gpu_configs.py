@@ -35,7 +35,7 @@ def bits(a):
 def test_ragged_batch_full_workload(ctx, oracle, mfma_min):
     """64 Zipf-routed tokens over 256 model-shape experts."""
     try:
-        worst = _mfma_case(ctx, oracle, 80, wl.N_ROUTED, wl.HIDDEN, wl.INTER, 4, 64, mfma_min)
+        worst, _ = _mfma_case(ctx, oracle, 80, wl.N_ROUTED, wl.HIDDEN, wl.INTER, 4, 64, mfma_min)
         print(f"ragged batch, MFMA threshold {mfma_min}: worst MFMA matvec |diff| / tolerance {worst:.3f}")
     finally:
         ctx.set_moe_mfma_min(1)
