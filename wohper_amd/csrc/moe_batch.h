@@ -17,8 +17,7 @@
 //   k_moe_batch_gateup   persistent: (expert, row tile) items from a queue,
 //                        gate and up matvecs of every slot (after
 //                        k_moe_batch_mx: the exact experts only)
-//   k_moe_batch_swiglu   SwiGLU of every slot
-//   k_moe_batch_quant    act-quant of every slot's SwiGLU output
+//   k_moe_batch_swiglu_quant  SwiGLU of every slot and its act-quant
 //   k_moe_batch_mx       down of the MFMA experts
 //   k_moe_batch_down     persistent, as gate/up
 //   k_moe_batch_accumulate
@@ -74,7 +73,6 @@ struct wh_batch_args {
     uint8_t* xs8;                  // [npos][hidden / 32] E8M0 scale bytes (x 1/8)
     float* g;                      // [S][inter] gate matvec (w1) by slot
     float* u;                      // [S][inter] up matvec (w3) by slot
-    float* h;                      // [S][inter] SwiGLU(g, u)
     float* hq;                     // [S][inter] act-quantized
     uint8_t* hq8;                  // [S][inter] codes
     uint8_t* hs8;                  // [S][inter / 32] scale bytes
@@ -317,6 +315,48 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
 }
 
 // ------------------------------------------------------------------ act-quant
+// amax over the 64 / kV lanes that hold one 64-block, kV values each (kV = 4
+// or 8; NaN skipped, as f32::max does): quad swaps, then the half-row mirror
+// (8 lanes) and, for kV = 4, the row mirror (16 lanes).
+template <int kV>
+__device__ __forceinline__ float wh_amax_block(float m) {
+    static_assert(kV == 4 || kV == 8, "64-block over 16 or 8 lanes");
+    m = fmaxf(m, wh_dpp_quad_swap1(m));
+    m = fmaxf(m, wh_dpp_quad_swap2(m));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x141, 0xf, 0xf, false)));  // row_half_mirror
+    if constexpr (kV == 4)
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x140, 0xf, 0xf, false)));  // row_mirror
+    return m;
+}
+
+// Act-quant (E/compute.rs:2504-2521, block 64) of kV consecutive values held
+// by one thread, the block's threads being 64 / kV consecutive lanes: q = the
+// E4M3 values before the scale 2^k.  The reference's semantics for
+// non-finite inputs, as wh_xq_quant16: NaN quantizes to -480, an infinite
+// amax gives an infinite scale; bad reports an inf or NaN among the kV.
+template <int kV>
+__device__ __forceinline__ void wh_aq_vals(const float (&v)[kV], const uint32_t* log2_thr, float (&q)[kV], int& k,
+                                           float& sc, bool& bad) {
+    float amax = 0.0f;
+    bad = false;
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+        const float m = fabsf(v[i]);
+        bad |= !(m <= 3.4028235e38f);
+        amax = fmaxf(amax, m);
+    }
+    amax = wh_amax_block<kV>(amax);
+    const bool inf_scale = !(amax <= 3.4028235e38f);
+    k = inf_scale ? 0 : wh_aq_scale_exp(amax, log2_thr);
+    const float inv = inf_scale ? 0.0f : wh_pow2f(-k);  // v / inf is v * 0
+    sc = inf_scale ? __uint_as_float(0x7f800000u) : wh_pow2f(k);
+#pragma unroll
+    for (int i = 0; i < kV; ++i) {
+        const float t = v[i] * inv;
+        q[i] = t != t ? -480.0f : wh_e4m3_round(wh_clamp448_finite(t));
+    }
+}
+
 // Act-quant (block 64) of rows of `n` values, 16 values per thread (a quad
 // of threads holds one 64-block; E/compute.rs:2504-2521).  Writes the values
 // in column order, their E4M3 codes in MFMA group order (per 32-col group,
@@ -378,15 +418,61 @@ __global__ void __launch_bounds__(256) k_moe_batch_quant(const void* __restrict_
     if (!h) s8[(size_t)r * (n / 32) + g] = (uint8_t)(be == 0xffu ? 0xffu : be - 3u);
 }
 
-// SwiGLU (E/deepseek_v4.rs:590-594) of the gate and up matvecs, one value
-// per thread: h = silu(min(g, 10)) * clamp(u, -10, 10).
-__global__ void __launch_bounds__(256) k_moe_batch_swiglu(const float* __restrict__ g, const float* __restrict__ u,
-                                                          float* __restrict__ h, uint32_t n) {
+// SwiGLU (E/deepseek_v4.rs:590-594) of the gate and up matvecs, h =
+// silu(min(g, 10)) * clamp(u, -10, 10), and the act-quant of h (block 64,
+// E/compute.rs:2504-2521) in one pass: 4 values per thread, a 64-block over
+// 16 lanes.  Writes what k_moe_batch_quant writes for h (the dequantized
+// values, the codes in MFMA group order, one E8M0 byte per 32-col group);
+// h itself is never stored.  n = slots * inter values (inter a multiple of
+// 64, so a block's 16 lanes are all in range or all out).  Grid: n / 1024
+// blocks of 256 threads, rounded up.
+__global__ void __launch_bounds__(256) k_moe_batch_swiglu_quant(const float* __restrict__ g,
+                                                                const float* __restrict__ u, uint32_t n,
+                                                                float* __restrict__ q32, uint8_t* __restrict__ q8,
+                                                                uint8_t* __restrict__ s8) {
     __shared__ uint64_t exp_tab[WH_EXP_TAB_LEN];
-    if (threadIdx.x < WH_EXP_TAB_LEN) exp_tab[threadIdx.x] = kExpTab[threadIdx.x];
-    __syncthreads();
+    __shared__ uint32_t thr[256];
+    wh_thr_stage ts;
+    wh_exp_stage es;
+    wh_thr_stage_load(ts);
+    wh_exp_stage_load(es);
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i < n) h[i] = wh_swiglu(g[i], u[i], exp_tab, kExpfExc, WH_EXPF_EXC_COUNT);
+    const bool on = 4 * i < n;
+    float4 gv = make_float4(0.0f, 0.0f, 0.0f, 0.0f), uv = gv;  // lanes past the end quantize zeros
+    if (on) {
+        gv = ((const float4*)g)[i];
+        uv = ((const float4*)u)[i];
+    }
+    wh_thr_stage_store(ts, thr);
+    wh_exp_stage_store(es, exp_tab);
+    __syncthreads();
+    const float v[4] = {wh_swiglu(gv.x, uv.x, exp_tab, kExpfExc, WH_EXPF_EXC_COUNT),
+                        wh_swiglu(gv.y, uv.y, exp_tab, kExpfExc, WH_EXPF_EXC_COUNT),
+                        wh_swiglu(gv.z, uv.z, exp_tab, kExpfExc, WH_EXPF_EXC_COUNT),
+                        wh_swiglu(gv.w, uv.w, exp_tab, kExpfExc, WH_EXPF_EXC_COUNT)};
+    float q[4], sc;
+    int k;
+    bool bad;
+    wh_aq_vals<4>(v, thr, q, k, sc, bad);
+    // this thread's codes, column 4j + e of its 32-col group in byte e
+    // (j = lane % 8)
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+    const uint32_t p = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+    // MFMA group order: byte 4c + m of the group holds column c + 8m, so
+    // dword d = j gathers byte d % 4 of the lanes d / 4 + 2m, m = 0..3
+    const uint32_t lane = threadIdx.x & 63u, j = lane & 7u;
+    const int src = (int)((lane & ~7u) + (j >> 2));
+    const uint32_t sh = 8u * (j & 3u);
+    uint32_t dw = 0;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) dw |= (((uint32_t)__shfl((int)p, src + 2 * m, 64) >> sh) & 0xffu) << (8 * m);
+    if (!on) return;
+    ((float4*)q32)[i] = make_float4(q[0] * sc, q[1] * sc, q[2] * sc, q[3] * sc);
+    ((uint32_t*)q8)[i] = dw;
+    // sc = 2^k: E8M0 byte 127 + k - 3 (0xFF for an infinite scale), as
+    // k_moe_batch_quant
+    const uint32_t be = (__float_as_uint(sc) >> 23) & 0xffu;
+    if (j == 0) s8[i >> 3] = (uint8_t)(be == 0xffu ? 0xffu : be - 3u);
 }
 
 // ------------------------------------------------------------ exact items

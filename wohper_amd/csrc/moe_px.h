@@ -118,48 +118,6 @@ __device__ __forceinline__ void wh_px_step(wh_v4f& acc, const wh_mx_raw& r, uint
     dep = wh_opaque_zero(acc[0]);
 }
 
-// amax over the 64 / kV lanes that hold one 64-block, kV values each (kV = 4
-// or 8; NaN skipped, as f32::max does): quad swaps, then the half-row mirror
-// (8 lanes) and, for kV = 4, the row mirror (16 lanes).
-template <int kV>
-__device__ __forceinline__ float wh_amax_block(float m) {
-    static_assert(kV == 4 || kV == 8, "64-block over 16 or 8 lanes");
-    m = fmaxf(m, wh_dpp_quad_swap1(m));
-    m = fmaxf(m, wh_dpp_quad_swap2(m));
-    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x141, 0xf, 0xf, false)));  // row_half_mirror
-    if constexpr (kV == 4)
-        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x140, 0xf, 0xf, false)));  // row_mirror
-    return m;
-}
-
-// Act-quant (E/compute.rs:2504-2521, block 64) of kV consecutive values held
-// by one thread, the block's threads being 64 / kV consecutive lanes: q = the
-// E4M3 values before the scale 2^k.  The reference's semantics for
-// non-finite inputs, as wh_xq_quant16: NaN quantizes to -480, an infinite
-// amax gives an infinite scale; bad reports an inf or NaN among the kV.
-template <int kV>
-__device__ __forceinline__ void wh_aq_vals(const float (&v)[kV], const uint32_t* log2_thr, float (&q)[kV], int& k,
-                                           float& sc, bool& bad) {
-    float amax = 0.0f;
-    bad = false;
-#pragma unroll
-    for (int i = 0; i < kV; ++i) {
-        const float m = fabsf(v[i]);
-        bad |= !(m <= 3.4028235e38f);
-        amax = fmaxf(amax, m);
-    }
-    amax = wh_amax_block<kV>(amax);
-    const bool inf_scale = !(amax <= 3.4028235e38f);
-    k = inf_scale ? 0 : wh_aq_scale_exp(amax, log2_thr);
-    const float inv = inf_scale ? 0.0f : wh_pow2f(-k);  // v / inf is v * 0
-    sc = inf_scale ? __uint_as_float(0x7f800000u) : wh_pow2f(k);
-#pragma unroll
-    for (int i = 0; i < kV; ++i) {
-        const float t = v[i] * inv;
-        q[i] = t != t ? -480.0f : wh_e4m3_round(wh_clamp448_finite(t));
-    }
-}
-
 // 8 consecutive input values of one thread, bf16 or f32.
 struct wh_in8 {
     uint4 r0, r1;

@@ -1067,7 +1067,7 @@ struct BatchBufs {
     float* wgt;
     uint32_t *sorted, *uexp, *uoff, *uorder, *acc_order, *meta, *pos;
     wh_bmx_vt* vtab;
-    float *xq, *g, *u, *h, *hq, *y;
+    float *xq, *g, *u, *hq, *y;
     uint8_t *xq8, *xs8, *hq8, *hs8;
 };
 int batch_bufs(wh_ctx* c, size_t npos, size_t slots, size_t hidden, size_t inter, BatchBufs* b) {
@@ -1081,7 +1081,6 @@ int batch_bufs(wh_ctx* c, size_t npos, size_t slots, size_t hidden, size_t inter
     const size_t o_me = take(16 * 4), o_w = take(slots * 4), o_so = take(slots * 4), o_ue = take(slots * 4),
                  o_uo = take((slots + 1) * 4), o_ur = take(slots * 4), o_ac = take(slots * 4),
                  o_xq = take(npos * hidden * 4), o_g = take(slots * inter * 4), o_u = take(slots * inter * 4),
-                 o_h = take(slots * inter * 4),
                  o_y = take(slots * hidden * 4),
                  o_hq = take(slots * inter * 4), o_xq8 = take(npos * hidden), o_xs8 = take(npos * hidden / 32),
                  o_hq8 = take(slots * inter), o_hs8 = take(slots * inter / 32),
@@ -1098,7 +1097,6 @@ int batch_bufs(wh_ctx* c, size_t npos, size_t slots, size_t hidden, size_t inter
     b->xq = (float*)(base + o_xq);
     b->g = (float*)(base + o_g);
     b->u = (float*)(base + o_u);
-    b->h = (float*)(base + o_h);
     b->y = (float*)(base + o_y);
     b->hq = (float*)(base + o_hq);
     b->xq8 = base + o_xq8;
@@ -1174,7 +1172,6 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         a.xs8 = b.xs8;
         a.g = b.g;
         a.u = b.u;
-        a.h = b.h;
         a.hq = b.hq;
         a.hq8 = b.hq8;
         a.hs8 = b.hs8;
@@ -1203,10 +1200,8 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         c->moe_last_npos = n;
         c->moe_last_hidden = hidden;
         c->moe_last_inter = inter;
-        k_moe_batch_swiglu<<<(unsigned)((slots * inter + 255) / 256), 256, 0, c->stream>>>(
-            a.g, a.u, a.h, (uint32_t)(slots * inter));
-        k_moe_batch_quant<<<(unsigned)((slots * inter / 16 + 255) / 256), 256, 0, c->stream>>>(
-            a.h, 0u, (uint32_t)slots, (uint32_t)inter, a.hq, a.hq8, a.hs8, nullptr);
+        k_moe_batch_swiglu_quant<<<(unsigned)((slots * inter / 4 + 255) / 256), 256, 0, c->stream>>>(
+            a.g, a.u, (uint32_t)(slots * inter), a.hq, a.hq8, a.hs8);
         if (mx) k_moe_batch_mx<2048, false><<<grid_md, 512, wh_bmx_lds(2048), c->stream>>>(a);
         if (inter == 2048) k_moe_batch_down<8><<<gd, 256, lds_d, c->stream>>>(a);
         else k_moe_batch_down<0><<<gd, 256, lds_d, c->stream>>>(a);
