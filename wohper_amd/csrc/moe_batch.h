@@ -7,11 +7,11 @@
 // shared expert out_p = shared(x_p) + acc_p (E/compute.rs:1838-1852).
 //
 // Launch sequence (one stream):
-//   k_moe_batch_quant    act-quant (block 64) of every position's input
-//   k_moe_batch_pack     one workgroup: weights, the per-expert token lists
+//   k_moe_batch_pack     workgroup 0: weights, the per-expert token lists
 //                        (counts, offsets, placement), the used experts in
 //                        ascending id, their work order, each position's
-//                        accumulation order
+//                        accumulation order; the others: act-quant (block
+//                        64) of every position's input
 //   k_moe_batch_mx       (exact numerics off) persistent MFMA kernel of the
 //                        MFMA experts' gate and up matvecs (moe_bmx.h)
 //   k_moe_batch_gateup   persistent: (expert, row tile) items from a queue,
@@ -64,8 +64,9 @@ struct wh_batch_args {
     uint32_t* acc_order;           // [A] per position: its route slots by ascending expert id
     uint32_t* meta;                // [0] used experts, [1] routes valid, [2]/[3] work queues
                                    // of gate/up and down, [4] experts on MFMA items, [6] an
-                                   // input block held an inf or NaN (set by the quant of x,
-                                   // read and cleared by the pack), [7] virtual experts
+                                   // input block held an inf or NaN (set by the act-quant
+                                   // of x; then no expert runs on MFMA items, and the
+                                   // accumulate clears it, [4] and [7]), [7] virtual experts
     wh_bmx_vt* vtab;               // [S] the MFMA experts' virtual experts, in work order
     uint32_t* pos;                 // [S] position of each slot
     float* xq;                     // [npos][hidden] act-quantized inputs (column order)
@@ -112,9 +113,73 @@ __device__ __forceinline__ uint32_t wh_wg_exclusive_scan(uint32_t v, uint32_t* t
     return before + incl - v;
 }
 
-// One workgroup of 256 threads; S <= 4096 slots, n_table < 1024.  An
-// expert's slots come in no particular order (each slot is computed on its
-// own); the accumulation order of a position is fixed by acc_order alone.
+// Act-quant (block 64) of rows of `n` values, 16 values per thread (a quad
+// of threads holds one 64-block; E/compute.rs:2504-2521): block `blk` of 256
+// threads of rows * n / 4096.  Writes the values in column order, their E4M3
+// codes in MFMA group order (per 32-col group, byte 4c + k holds column
+// c + 8k) and one E8M0 byte per group: the block scale divided by 8, which
+// takes the x8 of the FP4 integer LUT values.  Non-finite inputs follow the
+// reference (wh_xq_quant16); a block that held one sets *nonfinite, and the
+// gate/up and down kernels then run every expert on the exact items: -480 (a
+// NaN's code) and an infinite scale have no E4M3 / E8M0 encoding.  `thr` is
+// 256 words of LDS.
+__device__ __forceinline__ void wh_batch_quant_rows(const void* __restrict__ src, uint32_t src_bf16, uint32_t rows,
+                                                    uint32_t n, float* __restrict__ q32, uint8_t* __restrict__ q8,
+                                                    uint8_t* __restrict__ s8, uint32_t* nonfinite, uint32_t blk,
+                                                    uint32_t* thr) {
+    wh_thr_stage ts;
+    wh_thr_stage_load(ts);
+    wh_thr_stage_store(ts, thr);
+    __syncthreads();
+    const uint32_t per_row = n / 16;
+    const uint32_t i = blk * 256 + threadIdx.x;
+    const uint32_t r = i / per_row, t = i - r * per_row;
+    const bool on = r < rows;
+    const bool bf16 = src_bf16 != 0;
+    const size_t base = (size_t)(on ? r : 0) * n;
+    const void* row = bf16 ? (const void*)((const uint16_t*)src + base) : (const void*)((const float*)src + base);
+    wh_xq_stage st;
+    wh_xq_stage_load(st, row, bf16, on ? n : 0u, t);
+    float q[16], sc = 1.0f;
+    bool bad = false;
+    if (!wh_xq_quant16(st, bf16, thr, q, sc, &bad)) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) q[j] = 0.0f;  // rows past the end: the DPP partner below still reads
+    }
+    // codes: column c + 8k of the group sits at byte 4c + k; this thread
+    // holds k = 2h + (j >> 3) for c = j & 7 (h = which half of the group)
+    const uint32_t h = t & 1;
+    uint32_t pair[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+        pair[c] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[c], q[c + 8], 0, false) & 0xffffu;
+    uint32_t dw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t send = h ? pair[j] : pair[4 + j];
+        const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xb1, 0xf, 0xf, false);  // lane ^ 1
+        dw[j] = h ? (recv | (pair[4 + j] << 16)) : (pair[j] | (recv << 16));
+    }
+    if (!on) return;
+    if (bad) atomicOr(nonfinite, 1u);
+    float4* d32 = (float4*)(q32 + base + 16 * t);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        d32[j] = make_float4(q[4 * j] * sc, q[4 * j + 1] * sc, q[4 * j + 2] * sc, q[4 * j + 3] * sc);
+    const uint32_t g = t >> 1;  // 32-col group of the row
+    *(uint4*)(q8 + base + 32 * g + 16 * h) = make_uint4(dw[0], dw[1], dw[2], dw[3]);
+    // sc = 2^k: E8M0 byte 127 + k - 3 is its biased exponent - 3 (0xFF for an
+    // infinite scale, never read: such a batch runs no MFMA item)
+    const uint32_t be = (__float_as_uint(sc) >> 23) & 0xffu;
+    if (!h) s8[(size_t)r * (n / 32) + g] = (uint8_t)(be == 0xffu ? 0xffu : be - 3u);
+}
+
+// Workgroup 0 (256 threads; S <= 4096 slots, n_table < 1024) packs; the
+// others (npos * hidden / 4096 of them) act-quantize x.  An expert's slots
+// come in no particular order (each slot is computed on its own); the
+// accumulation order of a position is fixed by acc_order alone.  The split
+// into MFMA and exact experts does not wait for the act-quant: when an
+// input block held an inf or NaN, the consumers take every expert as exact.
 __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
     __shared__ uint32_t ids[WH_BATCH_MAX_ASSIGN];
     __shared__ uint32_t slot_of[WH_BATCH_MAX_ASSIGN];
@@ -124,15 +189,16 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
     __shared__ uint32_t vst[WH_BATCH_MAX_TABLE];  // per work-order position: its virtual experts, then their start
     __shared__ uint32_t tot[4];
     __shared__ uint32_t bad, n_mfma, mfma_min;
+    if (blockIdx.x != 0) {  // the other workgroups act-quantize x meanwhile
+        wh_batch_quant_rows(a.x, a.x_is_bf16, a.npos, a.hidden, a.xq, a.xq8, a.xs8, a.meta + 6, blockIdx.x - 1, ids);
+        return;
+    }
     const uint32_t A = a.npos * a.topk, S = A + a.has_shared * a.npos, tid = threadIdx.x;
     const uint32_t n_ids = a.n_table + a.has_shared;  // the shared expert is id n_table
     if (tid == 0) {
         bad = 0;
         n_mfma = 0;
-        // an input block with an inf or NaN (flagged by k_moe_batch_quant,
-        // which runs first) keeps every expert on the exact items
-        mfma_min = a.meta[6] ? 0u : a.mfma_min;
-        a.meta[6] = 0;
+        mfma_min = a.mfma_min;
     }
     for (uint32_t e = tid; e < n_ids; e += 256) cnt[e] = 0;
     // ids, checked against the table
@@ -357,71 +423,10 @@ __device__ __forceinline__ void wh_aq_vals(const float (&v)[kV], const uint32_t*
     }
 }
 
-// Act-quant (block 64) of rows of `n` values, 16 values per thread (a quad
-// of threads holds one 64-block; E/compute.rs:2504-2521).  Writes the values
-// in column order, their E4M3 codes in MFMA group order (per 32-col group,
-// byte 4c + k holds column c + 8k) and one E8M0 byte per group: the block
-// scale divided by 8, which takes the x8 of the FP4 integer LUT values.
-// Non-finite inputs follow the reference (wh_xq_quant16); a block that held
-// one sets *nonfinite (when given), and the pack then keeps every expert on
-// the exact items: -480 (a NaN's code) and an infinite scale have no E4M3 /
-// E8M0 encoding.  Grid: rows * n / 4096 blocks of 256 threads.
-__global__ void __launch_bounds__(256) k_moe_batch_quant(const void* __restrict__ src, uint32_t src_bf16,
-                                                         uint32_t rows, uint32_t n, float* __restrict__ q32,
-                                                         uint8_t* __restrict__ q8, uint8_t* __restrict__ s8,
-                                                         uint32_t* nonfinite) {
-    __shared__ uint32_t thr[256];
-    wh_thr_stage ts;
-    wh_thr_stage_load(ts);
-    wh_thr_stage_store(ts, thr);
-    __syncthreads();
-    const uint32_t per_row = n / 16;
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t r = i / per_row, t = i - r * per_row;
-    const bool on = r < rows;
-    const bool bf16 = src_bf16 != 0;
-    const size_t base = (size_t)(on ? r : 0) * n;
-    const void* row = bf16 ? (const void*)((const uint16_t*)src + base) : (const void*)((const float*)src + base);
-    wh_xq_stage st;
-    wh_xq_stage_load(st, row, bf16, on ? n : 0u, t);
-    float q[16], sc = 1.0f;
-    bool bad = false;
-    if (!wh_xq_quant16(st, bf16, thr, q, sc, &bad)) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) q[j] = 0.0f;  // rows past the end: the DPP partner below still reads
-    }
-    // codes: column c + 8k of the group sits at byte 4c + k; this thread
-    // holds k = 2h + (j >> 3) for c = j & 7 (h = which half of the group)
-    const uint32_t h = t & 1;
-    uint32_t pair[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c)
-        pair[c] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[c], q[c + 8], 0, false) & 0xffffu;
-    uint32_t dw[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t send = h ? pair[j] : pair[4 + j];
-        const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xb1, 0xf, 0xf, false);  // lane ^ 1
-        dw[j] = h ? (recv | (pair[4 + j] << 16)) : (pair[j] | (recv << 16));
-    }
-    if (!on) return;
-    if (bad && nonfinite) atomicOr(nonfinite, 1u);
-    float4* d32 = (float4*)(q32 + base + 16 * t);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        d32[j] = make_float4(q[4 * j] * sc, q[4 * j + 1] * sc, q[4 * j + 2] * sc, q[4 * j + 3] * sc);
-    const uint32_t g = t >> 1;  // 32-col group of the row
-    *(uint4*)(q8 + base + 32 * g + 16 * h) = make_uint4(dw[0], dw[1], dw[2], dw[3]);
-    // sc = 2^k: E8M0 byte 127 + k - 3 is its biased exponent - 3 (0xFF for an
-    // infinite scale, never read: such a batch runs no MFMA item)
-    const uint32_t be = (__float_as_uint(sc) >> 23) & 0xffu;
-    if (!h) s8[(size_t)r * (n / 32) + g] = (uint8_t)(be == 0xffu ? 0xffu : be - 3u);
-}
-
 // SwiGLU (E/deepseek_v4.rs:590-594) of the gate and up matvecs, h =
 // silu(min(g, 10)) * clamp(u, -10, 10), and the act-quant of h (block 64,
 // E/compute.rs:2504-2521) in one pass: 4 values per thread, a 64-block over
-// 16 lanes.  Writes what k_moe_batch_quant writes for h (the dequantized
+// 16 lanes.  Writes what wh_batch_quant_rows writes for x (the dequantized
 // values, the codes in MFMA group order, one E8M0 byte per 32-col group);
 // h itself is never stored.  n = slots * inter values (inter a multiple of
 // 64, so a block's 16 lanes are all in range or all out).  Grid: n / 1024
@@ -470,7 +475,7 @@ __global__ void __launch_bounds__(256) k_moe_batch_swiglu_quant(const float* __r
     ((float4*)q32)[i] = make_float4(q[0] * sc, q[1] * sc, q[2] * sc, q[3] * sc);
     ((uint32_t*)q8)[i] = dw;
     // sc = 2^k: E8M0 byte 127 + k - 3 (0xFF for an infinite scale), as
-    // k_moe_batch_quant
+    // wh_batch_quant_rows
     const uint32_t be = (__float_as_uint(sc) >> 23) & 0xffu;
     if (j == 0) s8[i >> 3] = (uint8_t)(be == 0xffu ? 0xffu : be - 3u);
 }
@@ -947,7 +952,7 @@ template <int kBlk>
 __global__ void __launch_bounds__(256, 3) k_moe_batch_gateup(wh_batch_args a) {
     extern __shared__ __align__(16) float lds[];
     __shared__ uint32_t item_s;
-    const uint32_t n_mfma = a.meta[4], mt = a.inter >> 6, et = a.inter >> 4;
+    const uint32_t n_mfma = a.meta[6] ? 0u : a.meta[4], mt = a.inter >> 6, et = a.inter >> 4;
     const uint32_t n_m = a.mfma_external ? 0u : n_mfma * 2 * mt, n_items = n_m + (a.meta[0] - n_mfma) * et;
     if (n_items == 0) return;  // before the queue's atomic: every workgroup would take one
     wh_queue q{a.meta + 2, &item_s, 0};
@@ -1007,7 +1012,7 @@ template <int kBlk>
 __global__ void __launch_bounds__(256, 4) k_moe_batch_down(wh_batch_args a) {
     extern __shared__ __align__(16) float lds[];
     __shared__ uint32_t item_s;
-    const uint32_t n_mfma = a.meta[4], mt = a.hidden >> 6, et = a.hidden >> 5;
+    const uint32_t n_mfma = a.meta[6] ? 0u : a.meta[4], mt = a.hidden >> 6, et = a.hidden >> 5;
     const uint32_t n_m = a.mfma_external ? 0u : n_mfma * mt, n_items = n_m + (a.meta[0] - n_mfma) * et;
     if (n_items == 0) return;  // before the queue's atomic: every workgroup would take one
     wh_queue q{a.meta + 3, &item_s, 0};
@@ -1055,8 +1060,15 @@ __global__ void __launch_bounds__(256, 4) k_moe_batch_down(wh_batch_args a) {
 // (E/compute.rs:1804-1807: `*slot += *value * weight`), then with the shared
 // expert out_p = shared + routed (E/compute.rs:1838-1848).  Grid
 // (hidden / 256, npos).  Nothing is written when a route was not resident.
+// The last kernel of a call: it clears the non-finite input flag (and with
+// it the counts of MFMA and virtual experts, none of which ran).
 __global__ void __launch_bounds__(256) k_moe_batch_accumulate(wh_batch_args a) {
     const uint32_t p = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
+    if (p == 0 && r == 0 && a.meta[6]) {
+        a.meta[4] = 0;
+        a.meta[6] = 0;
+        a.meta[7] = 0;
+    }
     if (r >= a.hidden || a.meta[1] == 0) return;
     float acc = 0.0f;
     for (uint32_t k = 0; k < a.topk; ++k) {

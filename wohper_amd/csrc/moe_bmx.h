@@ -88,7 +88,7 @@ __global__ void __launch_bounds__(512, 1) k_moe_batch_mx(wh_batch_args a) {
     // timeline points (builds with -DWH_TIMELINE): 0 start, 1 ring issued,
     // 2 B staged, 3 the wave's last item done, 4 the workgroup's end
     WH_TL(kGate ? 0 : 1, 0);
-    const uint32_t V = a.meta[7];
+    const uint32_t V = a.meta[6] ? 0u : a.meta[7];  // an inf or NaN input: every expert on the exact items
     if (V == 0 || a.meta[1] == 0) return;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, L = tid & 63, g = L >> 4, nl = L & 15;
     const uint32_t tiles = (kGate ? a.inter : a.hidden) >> 4;

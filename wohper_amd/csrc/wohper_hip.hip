@@ -1185,11 +1185,8 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         const size_t max_used = std::min(slots, (size_t)t.n + (shared ? 1 : 0));
         const unsigned gg = (unsigned)std::min<size_t>(grid_g, max_used * (inter / 16));
         const unsigned gd = (unsigned)std::min<size_t>(grid_d, max_used * (hidden / 32));
-        // the quant of x runs first: the pack keeps every expert off MFMA when
-        // an input block held an inf or NaN
-        k_moe_batch_quant<<<(unsigned)((n * hidden / 16 + 255) / 256), 256, 0, c->stream>>>(
-            a.x, a.x_is_bf16, (uint32_t)n, (uint32_t)hidden, a.xq, a.xq8, a.xs8, a.meta + 6);
-        k_moe_batch_pack<<<1, 256, 0, c->stream>>>(a);
+        // workgroup 0 packs, the others act-quantize x
+        k_moe_batch_pack<<<1 + (unsigned)((n * hidden / 16 + 255) / 256), 256, 0, c->stream>>>(a);
         if (mx) {
             if (hidden == 4096) k_moe_batch_mx<4096, true><<<grid_mg, 512, wh_bmx_lds(4096), c->stream>>>(a);
             else k_moe_batch_mx<2048, true><<<grid_mg, 512, wh_bmx_lds(2048), c->stream>>>(a);
