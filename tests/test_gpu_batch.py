@@ -270,3 +270,33 @@ def test_batch_nonfinite_inputs_follow_the_reference(ctx, oracle):
     assert e.value.name == "NonFiniteOutput"
     ctx.moe_batch(layer, ids, sc, x)
     assert int(ctx.debug_moe_batch_read(4, 8, np.uint32)[4]) > 0
+
+
+def test_batch_nonfinite_inputs_at_the_default_threshold(ctx, oracle):
+    """At threshold 1 every used expert is an MFMA expert and the exact-item
+    kernels are not launched; after a NaN input the MFMA kernel's gate/up runs
+    in fp32 from the act-quantized inputs (NaN -> -480 x the block scale, as
+    E/compute.rs:2504-2545): every matvec within tolerance of the oracle's on
+    the same input, SwiGLU + act-quant and the weighted sums bit-exact.  An inf
+    input still ends in NonFiniteOutput, and the next finite batch is
+    unaffected."""
+    layer, n_exp, hidden, inter, seed, npos = 48, 12, 2048, 2048, 36, 24
+    ids, sc, x = wl.zipf_batch_routes(seed=seed, n_tokens=npos, n_experts=n_exp, hidden=hidden)
+    xn = x.copy()
+    xn[3, [0, 70, 71]] = np.nan
+    xn[9, 64:128] = np.nan
+    worst, _ = _mfma_case(ctx, oracle, layer, n_exp, hidden, inter, seed, npos, DEFAULT_MFMA_MIN,
+                          routes=(ids, sc, xn))
+    print(f"worst fp32 matvec |diff| / tolerance: {worst:.3f}")
+    xi = x.copy()
+    xi[5, 200] = np.inf
+    ctx.set_exact_numerics(False)
+    ctx.set_moe_mfma_min(DEFAULT_MFMA_MIN)
+    try:
+        with pytest.raises(wohper_amd.DeepSeekV4KernelError) as e:
+            ctx.moe_batch(layer, ids, sc, xi)
+        assert e.value.name == "NonFiniteOutput"
+    finally:
+        ctx.set_exact_numerics(True)
+    worst, _ = _mfma_case(ctx, oracle, layer, n_exp, hidden, inter, seed, npos, DEFAULT_MFMA_MIN,
+                          routes=(ids, sc, x))

@@ -52,6 +52,9 @@ struct wh_batch_args {
     wh_expert_ptrs shared;         // ... under the id n_table
     uint32_t mfma_min;             // experts with this many slots take MFMA items (0: never)
     uint32_t mfma_external;        // the MFMA experts run in k_moe_batch_mx (moe_bmx.h), not here
+    uint32_t mx_fallback;          // every used expert is an MFMA expert and no exact-item kernel
+                                   // is launched: after an inf or NaN input k_moe_batch_mx's
+                                   // gate/up computes them in fp32
     const void* x;                 // [npos][hidden], f32 or bf16
     uint32_t x_is_bf16;
     // assignments: i = p * topk + k for the routes, A + p for the shared
@@ -65,8 +68,9 @@ struct wh_batch_args {
     uint32_t* meta;                // [0] used experts, [1] routes valid, [2]/[3] work queues
                                    // of gate/up and down, [4] experts on MFMA items, [6] an
                                    // input block held an inf or NaN (set by the act-quant
-                                   // of x; then no expert runs on MFMA items, and the
-                                   // accumulate clears it, [4] and [7]), [7] virtual experts
+                                   // of x; then no expert runs on MFMA items, or with
+                                   // mx_fallback the gate/up ones run in fp32; the
+                                   // accumulate clears it), [7] virtual experts
     wh_bmx_vt* vtab;               // [S] the MFMA experts' virtual experts, in work order
     uint32_t* pos;                 // [S] position of each slot
     float* xq;                     // [npos][hidden] act-quantized inputs (column order)
@@ -1061,13 +1065,16 @@ __global__ void __launch_bounds__(256, 4) k_moe_batch_down(wh_batch_args a) {
 // expert out_p = shared + routed (E/compute.rs:1838-1848).  Grid
 // (hidden / 256, npos).  Nothing is written when a route was not resident.
 // The last kernel of a call: it clears the non-finite input flag (and with
-// it the counts of MFMA and virtual experts, none of which ran).
+// it, unless k_moe_batch_mx fell back to fp32, the counts of MFMA and virtual
+// experts, none of which ran).
 __global__ void __launch_bounds__(256) k_moe_batch_accumulate(wh_batch_args a) {
     const uint32_t p = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
     if (p == 0 && r == 0 && a.meta[6]) {
-        a.meta[4] = 0;
+        if (!a.mx_fallback) {
+            a.meta[4] = 0;
+            a.meta[7] = 0;
+        }
         a.meta[6] = 0;
-        a.meta[7] = 0;
     }
     if (r >= a.hidden || a.meta[1] == 0) return;
     float acc = 0.0f;

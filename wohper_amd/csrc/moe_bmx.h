@@ -68,6 +68,37 @@ __device__ __forceinline__ void wh_mx_raw_load_global(wh_mx_raw& r, const uint8_
     r.s = wh_ld8_global(srow + blk * 8);
 }
 
+// Gate/up of the MFMA experts in fp32, for a batch with an inf or NaN input
+// (-480, a NaN's act-quantized value, has no E4M3 code and an infinite scale
+// no E8M0 byte) when no exact-item kernel follows: the workgroup's items
+// [i0, i1) from the dequantized inputs, one wave per item and every slot of
+// the item's virtual expert in turn (wh_px_rows_fp32).  The products are
+// exact in fp32; only the order of the sums differs from the reference's.
+template <int kCols>
+__device__ void wh_bmx_gate_fp32(const wh_batch_args& a, uint32_t i0, uint32_t i1, uint32_t per_v, uint32_t wave,
+                                 uint32_t L) {
+    constexpr uint32_t NB = kCols / 256, G = kCols / 32;
+#pragma unroll 1
+    for (uint32_t it = i0 + wave; it < i1; it += 8) {
+        const uint32_t v = it / per_v, rel = it - v * per_v, tile = rel >> 1, m = rel & 1;
+        const wh_bmx_vt* vt = a.vtab + v;
+        const uint32_t row = tile * 16 + (L & 15);
+        const uint8_t* wrow = (m ? vt->w3 : vt->w1) + (size_t)row * (kCols / 2);
+        const uint8_t* srow = (m ? vt->s3 : vt->s1) + (size_t)row * G;
+        const uint32_t slot0 = vt->slot0, count = vt->count;
+        float* dst = m ? a.u : a.g;
+#pragma unroll 1
+        for (uint32_t n = 0; n < count; ++n) {
+            const uint32_t s = slot0 + n;
+            const float r = wh_px_rows_fp32(wrow, srow, a.xq + (size_t)a.pos[s] * kCols, 0, NB, L);
+            if (L < 16) {
+                dst[(size_t)s * a.inter + tile * 16 + L] = r;
+                if (!(fabsf(r) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
+            }
+        }
+    }
+}
+
 // kGate: gate/up (kCols = hidden, B = x's codes by position, out g / u);
 // else down (kCols = inter, B = h's codes by slot, out y).  inter = 2048.
 // Grid: one workgroup of 512 threads per CU.
@@ -88,7 +119,12 @@ __global__ void __launch_bounds__(512, 1) k_moe_batch_mx(wh_batch_args a) {
     // timeline points (builds with -DWH_TIMELINE): 0 start, 1 ring issued,
     // 2 B staged, 3 the wave's last item done, 4 the workgroup's end
     WH_TL(kGate ? 0 : 1, 0);
-    const uint32_t V = a.meta[6] ? 0u : a.meta[7];  // an inf or NaN input: every expert on the exact items
+    // an inf or NaN input: every expert on the exact items, or with
+    // mx_fallback gate/up in fp32 here (h is then finite, or the batch has
+    // already failed with a non-finite g or u, so down stays on MFMA)
+    const bool nonfinite = a.meta[6] != 0;
+    if (nonfinite && !a.mx_fallback) return;
+    const uint32_t V = a.meta[7];
     if (V == 0 || a.meta[1] == 0) return;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, L = tid & 63, g = L >> 4, nl = L & 15;
     const uint32_t tiles = (kGate ? a.inter : a.hidden) >> 4;
@@ -96,6 +132,12 @@ __global__ void __launch_bounds__(512, 1) k_moe_batch_mx(wh_batch_args a) {
     const uint64_t W = (uint64_t)V * per_v;
     const uint32_t i0 = (uint32_t)(W * blockIdx.x / gridDim.x), i1 = (uint32_t)(W * (blockIdx.x + 1) / gridDim.x);
     if (i0 >= i1) return;
+    if constexpr (kGate) {
+        if (nonfinite) {
+            wh_bmx_gate_fp32<kCols>(a, i0, i1, per_v, wave, L);
+            return;
+        }
+    }
     const uint32_t lane_off = 64 * (g & 1) + 32 * (g >> 1);
     for (uint32_t vp = i0 / per_v, v_last = (i1 - 1) / per_v; vp <= v_last; vp += 2) {
         const uint32_t nv = v_last - vp + 1 < 2 ? v_last - vp + 1 : 2;

@@ -1178,6 +1178,11 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         a.y = b.y;
         a.mfma_min = c->exact ? 0u : c->moe_mfma_min;  // exact numerics: every expert on the exact items
         a.mfma_external = mx ? 1u : 0u;
+        // threshold 1: every used expert is an MFMA expert, so the exact-item
+        // kernels would only run after an inf or NaN input; k_moe_batch_mx
+        // covers that case and they are not launched
+        const bool fb = mx && a.mfma_min == 1;
+        a.mx_fallback = fb ? 1u : 0u;
         a.out = out + p0 * hidden;
         a.status = c->status;
         // the most items the queues can hold: used experts <= min(slots, ids),
@@ -1191,8 +1196,10 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
             if (hidden == 4096) k_moe_batch_mx<4096, true><<<grid_mg, 512, wh_bmx_lds(4096), c->stream>>>(a);
             else k_moe_batch_mx<2048, true><<<grid_mg, 512, wh_bmx_lds(2048), c->stream>>>(a);
         }
-        if (hidden == 4096) k_moe_batch_gateup<16><<<gg, 256, lds_g, c->stream>>>(a);
-        else k_moe_batch_gateup<0><<<gg, 256, lds_g, c->stream>>>(a);
+        if (!fb) {
+            if (hidden == 4096) k_moe_batch_gateup<16><<<gg, 256, lds_g, c->stream>>>(a);
+            else k_moe_batch_gateup<0><<<gg, 256, lds_g, c->stream>>>(a);
+        }
         c->moe_last_slots = npos <= chunk ? slots : 0;
         c->moe_last_npos = n;
         c->moe_last_hidden = hidden;
@@ -1200,8 +1207,10 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         k_moe_batch_swiglu_quant<<<(unsigned)((slots * inter / 4 + 255) / 256), 256, 0, c->stream>>>(
             a.g, a.u, (uint32_t)(slots * inter), a.hq, a.hq8, a.hs8);
         if (mx) k_moe_batch_mx<2048, false><<<grid_md, 512, wh_bmx_lds(2048), c->stream>>>(a);
-        if (inter == 2048) k_moe_batch_down<8><<<gd, 256, lds_d, c->stream>>>(a);
-        else k_moe_batch_down<0><<<gd, 256, lds_d, c->stream>>>(a);
+        if (!fb) {
+            if (inter == 2048) k_moe_batch_down<8><<<gd, 256, lds_d, c->stream>>>(a);
+            else k_moe_batch_down<0><<<gd, 256, lds_d, c->stream>>>(a);
+        }
         k_moe_batch_accumulate<<<dim3((unsigned)((hidden + 255) / 256), (unsigned)n), 256, 0, c->stream>>>(a);
         WH_HIP(hipGetLastError());
     }
