@@ -593,9 +593,9 @@ def decode_stack_batch16(ctx, layers, n_layers: int, steps: int, seed: int, batc
     def step(s_):
         for L in range(n_layers):
             hs = layers[L]
-            ctx.fp8_gemv_multi_async(hs["wq_a"], 0, 1024, dev["x"], batch, 4096, ydev["wq_a"], 1024)
+            ctx.fp8_gemv_multi_pair_async(hs["wq_a"], 0, 1024, ydev["wq_a"], 1024, hs["wkv"], 0, 512, ydev["wkv"], 512,
+                                          dev["x"], batch, 4096)
             ctx.fp8_gemv_multi_async(hs["wq_b"], 0, 32768, dev["qlat"], batch, 1024, ydev["wq_b"], 32768)
-            ctx.fp8_gemv_multi_async(hs["wkv"], 0, 512, dev["x"], batch, 4096, ydev["wkv"], 512)
             ctx.fp8_gemv_multi_groups_async(hs["wo_a"], 0, 8192, 1024, dev["oa"], 4096, batch, 8 * 4096,
                                             ydev["wo_a"], 8192)
             ctx.fp8_gemv_multi_async(hs["wo_b"], 0, 4096, dev["ob"], batch, 8192, ydev["wo_b"], 4096)

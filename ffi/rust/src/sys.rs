@@ -208,6 +208,10 @@ extern "C" {
     pub fn wh_fp8_gemv_multi_groups_async(ctx: *mut WhCtx, w: WhTensor, row_start: usize, row_end: usize,
                                           group_rows: usize, x_dev: *const f32, x_group_stride: usize,
                                           n: usize, x_stride: usize, y_dev: *mut f32, y_stride: usize) -> c_int;
+    pub fn wh_fp8_gemv_multi_pair_async(ctx: *mut WhCtx, w0: WhTensor, row_start0: usize, row_end0: usize,
+                                        y0_dev: *mut f32, y0_stride: usize, w1: WhTensor, row_start1: usize,
+                                        row_end1: usize, y1_dev: *mut f32, y1_stride: usize, x_dev: *const f32,
+                                        n: usize, x_stride: usize) -> c_int;
     pub fn wh_set_fp8_mfma_min(ctx: *mut WhCtx, min_inputs: u32) -> c_int;
     pub fn wh_fp8_gemv_async(ctx: *mut WhCtx, w: WhTensor, row_start: usize, row_end: usize,
                              x_dev: *const f32, y_dev: *mut f32) -> c_int;

@@ -449,6 +449,18 @@ int wh_fp8_gemv_batch_async(wh_ctx* ctx, const wh_gemv_desc* descs, size_t n);
 int wh_fp8_gemv_multi_async(wh_ctx* ctx, wh_tensor w, size_t row_start, size_t row_end, const float* x_dev, size_t n,
                             size_t x_stride, float* y_dev, size_t y_stride);
 
+/* Two wh_fp8_gemv_multi_async calls on the same n inputs, in order: rows
+ * [row_start0, row_end0) of w0 into y0_dev and rows [row_start1, row_end1) of
+ * w1 into y1_dev (wq_a and wkv of a batch of decode positions; the reference
+ * calls rows_multi once for each, E/compute.rs:4005-4013, 6384-6577).
+ * Results are those of the two calls; when both take the MFMA path with the
+ * same k split, the tensors share width, scale format, rows per scale row and
+ * the special-code flag, and neither output overlaps the inputs or the other
+ * output, they go out as one launch. */
+int wh_fp8_gemv_multi_pair_async(wh_ctx* ctx, wh_tensor w0, size_t row_start0, size_t row_end0, float* y0_dev,
+                                 size_t y0_stride, wh_tensor w1, size_t row_start1, size_t row_end1, float* y1_dev,
+                                 size_t y1_stride, const float* x_dev, size_t n, size_t x_stride);
+
 /* The reference's grouped batch projection, one rows_multi call per row group
  * with the group's own inputs (wo_a, E/compute.rs:4599-4622), as one call:
  * rows row_start + [g * group_rows, (g + 1) * group_rows) read input i of

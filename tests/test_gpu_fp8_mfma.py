@@ -181,3 +181,43 @@ def test_fp8_mfma_full_precision_inputs_exact(ctx, oracle):
         want = oracle.fp8_gemv(w, rows, cols, s, rows // 128, cols // 128, xs[i])
         assert np.array_equal(ys[i].view(np.uint32), want.view(np.uint32)), (i, int(np.count_nonzero(ys[i] != want)))
     ctx.release(t)
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_pair_equals_two_multi_calls(ctx, oracle, exact):
+    """wq_a (1024 x 4096) and wkv (512 x 4096) on the same 16 inputs through
+    wh_fp8_gemv_multi_pair_async (one launch on the MFMA path): bit-identical
+    to two wh_fp8_gemv_multi_async calls, and within tolerance of the oracle
+    (bit-exact with exact numerics, where the pair is two launches)."""
+    rng = np.random.default_rng(71)
+    n, cols = 16, 4096
+    shapes = [(1024, 3), (512, 4)]
+    ts, cases = [], []
+    for rows, seed in shapes:
+        w = rng.integers(0, 256, (rows, cols), dtype=np.uint8)
+        s = rng.uniform(0.5, 2.0, (rows // 128, cols // 128)).astype(np.float32)
+        ts.append(ctx.store_fp8(w, rows, cols, s, rows // 128, cols // 128, wohper_amd.SCALE_F32))
+        cases.append((w, rows, s))
+    xs = rng.standard_normal((n, cols)).astype(np.float32)
+    ctx.set_exact_numerics(exact)
+    xd = ctx.device_alloc(xs.nbytes)
+    y0, y1 = ctx.device_alloc(n * 1024 * 4), ctx.device_alloc(n * 512 * 4)
+    ctx.to_device(xd, xs)
+    ctx.fp8_gemv_multi_pair_async(ts[0], 0, 1024, y0, 1024, ts[1], 0, 512, y1, 512, xd, n, cols)
+    got = [np.empty((n, 1024), np.float32), np.empty((n, 512), np.float32)]
+    ctx.from_device(got[0], y0)
+    ctx.from_device(got[1], y1)
+    assert ctx.lib.wh_stream_status(ctx._h) == 0
+    for d in (xd, y0, y1):
+        ctx.device_free(d)
+    for (w, rows, s), t, g in zip(cases, ts, got):
+        sep = run_multi(ctx, t, xs, 0, rows, cols)
+        assert np.array_equal(g.view(np.uint32), sep.view(np.uint32)), rows
+        if exact:
+            for i in range(n):
+                want = oracle.fp8_gemv(w, rows, cols, s, s.shape[0], s.shape[1], xs[i], 0, rows)
+                assert np.array_equal(g[i].view(np.uint32), want.view(np.uint32)), (rows, i)
+        else:
+            check(oracle, w, rows, cols, s, xs, g)
+    for t in ts:
+        ctx.release(t)

@@ -81,7 +81,7 @@ EXPORTED = (
     "wh_probe_read_floor",
     "wh_store_fp8_synthetic", "wh_synth_fp8_host", "wh_routed_and_shared_experts", "wh_fp8_gemv_batch_async",
     "wh_routed_and_shared_experts_async", "wh_moe_batch", "wh_moe_batch_async", "wh_set_moe_mfma_min",
-    "wh_debug_moe_batch_read", "wh_fp8_gemv_multi_async", "wh_fp8_gemv_multi_groups_async", "wh_set_fp8_mfma_min",
+    "wh_debug_moe_batch_read", "wh_fp8_gemv_multi_async", "wh_fp8_gemv_multi_groups_async", "wh_fp8_gemv_multi_pair_async", "wh_set_fp8_mfma_min",
     "wh_set_exact_numerics", "wh_debug_moe_token_capture",
     "wh_debug_moe_token_read", "wh_fp8_shared_expert", "wh_fp8_shared_expert_async",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
@@ -222,6 +222,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_set_moe_mfma_min": (c.c_int, [vp, c.c_uint32]),
         "wh_fp8_gemv_multi_async": (c.c_int, [vp, c.c_uint64, sz, sz, vp, sz, sz, vp, sz]),
         "wh_fp8_gemv_multi_groups_async": (c.c_int, [vp, c.c_uint64, sz, sz, sz, vp, sz, sz, sz, vp, sz]),
+        "wh_fp8_gemv_multi_pair_async": (c.c_int, [vp, c.c_uint64, sz, sz, vp, sz, c.c_uint64, sz, sz, vp, sz, vp, sz,
+                                                    sz]),
         "wh_set_fp8_mfma_min": (c.c_int, [vp, c.c_uint32]),
         "wh_debug_moe_batch_read": (c.c_int, [vp, c.c_int, vp, sz]),
         "wh_set_exact_numerics": (c.c_int, [vp, c.c_int]),
@@ -608,6 +610,16 @@ class Context:
         _check(self.lib.wh_fp8_gemv_multi_groups_async(self._h, t, row_start, row_end, group_rows,
                                                        ctypes.c_void_p(x_ptr), x_group_stride, n, x_stride,
                                                        ctypes.c_void_p(y_ptr), y_stride), "fp8_gemv_multi_groups_async")
+
+    def fp8_gemv_multi_pair_async(self, t0: int, row_start0: int, row_end0: int, y0_ptr: int, y0_stride: int,
+                                  t1: int, row_start1: int, row_end1: int, y1_ptr: int, y1_stride: int, x_ptr: int,
+                                  n: int, x_stride: int):
+        """Two multi-input GEMVs on the same n inputs (wq_a and wkv), one
+        launch where the MFMA path allows it (strides in floats)."""
+        _check(self.lib.wh_fp8_gemv_multi_pair_async(self._h, t0, row_start0, row_end0, ctypes.c_void_p(y0_ptr),
+                                                     y0_stride, t1, row_start1, row_end1, ctypes.c_void_p(y1_ptr),
+                                                     y1_stride, ctypes.c_void_p(x_ptr), n, x_stride),
+               "fp8_gemv_multi_pair_async")
 
     def set_fp8_mfma_min(self, n: int):
         """Multi-input FP8 GEMVs with at least n inputs use MFMA when exact

@@ -63,6 +63,14 @@ struct wh_fp8mm_args {
     uint32_t xg_shift;    // log2(rows per input group); 31 = one group
     uint32_t xg_stride;
     uint32_t kc, splits, row_blocks;
+    // a second tensor on the same inputs (wq_a and wkv): the row blocks from
+    // rb_first on run its rows [row_start2, row_end2) into y2 (same width,
+    // scale format and rows per scale row); rb_first = row_blocks when there
+    // is none
+    const uint8_t* w2;
+    const void* scales2;
+    float* y2;
+    uint32_t row_start2, row_end2, y2_stride, rb_first;
 };
 
 // Two f32 to two bf16, each rounded to nearest even (v_cvt_pk_bf16_f32).
@@ -124,8 +132,16 @@ __global__ void __launch_bounds__(512, WH_FP8MM_WG_PER_CU) k_fp8_mm(wh_fp8mm_arg
     extern __shared__ __align__(16) uint16_t xmm[];  // [hi | mid | lo][G][m][q][t][8]
     const uint32_t rb = blockIdx.x, ks = blockIdx.y, tb = blockIdx.z;
     const uint32_t wave = threadIdx.x >> 6, L = threadIdx.x & 63, q = L >> 4;
-    const uint32_t r0 = a.row_start + rb * WH_FP8MM_ROWS;
-    const uint32_t grp = a.xg_shift < 31 ? (rb * WH_FP8MM_ROWS) >> a.xg_shift : 0;
+    // the row block's tensor
+    const bool t2 = rb >= a.rb_first;
+    const uint8_t* const W = t2 ? a.w2 : a.w;
+    const void* const SC = t2 ? a.scales2 : a.scales;
+    float* const Y = t2 ? a.y2 : a.y;
+    const uint32_t row_start = t2 ? a.row_start2 : a.row_start, row_end = t2 ? a.row_end2 : a.row_end;
+    const uint32_t y_stride = t2 ? a.y2_stride : a.y_stride;
+    const uint32_t rbl = t2 ? rb - a.rb_first : rb;  // row block within its tensor
+    const uint32_t r0 = row_start + rbl * WH_FP8MM_ROWS;
+    const uint32_t grp = a.xg_shift < 31 ? (rbl * WH_FP8MM_ROWS) >> a.xg_shift : 0;
     constexpr uint32_t G = kG;
     const uint32_t g0 = ks * G;
     const uint32_t P = G * 2048;  // bf16 of one plane
@@ -144,14 +160,14 @@ __global__ void __launch_bounds__(512, WH_FP8MM_WG_PER_CU) k_fp8_mm(wh_fp8mm_arg
     }
     // the lane's row (rows past the end load row_start's bytes; not stored)
     const uint32_t row = r0 + 16 * wave + (L & 15);
-    const uint32_t rc = row < a.row_end ? row : a.row_start;
-    const uint8_t* wrow = a.w + (size_t)rc * a.cols + (size_t)g0 * 128 + 32 * q;
-    const uint32_t trow = r0 + 16 * wave < a.row_end ? r0 + 16 * wave : a.row_end - 1;  // the tile's scale row
+    const uint32_t rc = row < row_end ? row : row_start;
+    const uint8_t* wrow = W + (size_t)rc * a.cols + (size_t)g0 * 128 + 32 * q;
+    const uint32_t trow = r0 + 16 * wave < row_end ? r0 + 16 * wave : row_end - 1;  // the tile's scale row
     const size_t srow = (size_t)(trow >> a.row_group_shift) * a.scale_cols + g0;
     // lane j < G holds the tile's scale of group j, loaded with the inputs so
     // that no wait in the weight loop covers a load issued after the ring's
     float sv = 0.0f;
-    if (L < G) sv = wh_fp8mm_scale<kScaleU8>(a.scales, srow + L);
+    if (L < G) sv = wh_fp8mm_scale<kScaleU8>(SC, srow + L);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();  // every wave's input loads go out before any weight load
     __builtin_amdgcn_sched_barrier(0);
@@ -219,8 +235,8 @@ __global__ void __launch_bounds__(512, WH_FP8MM_WG_PER_CU) k_fp8_mm(wh_fp8mm_arg
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t orow = r0 + 16 * wave + 4 * q + r;
-            if (orow < a.row_end && tg < a.n) {
-                a.y[(size_t)tg * a.y_stride + (orow - a.row_start)] = total[r];
+            if (orow < row_end && tg < a.n) {
+                Y[(size_t)tg * y_stride + (orow - row_start)] = total[r];
                 if (!(fabsf(total[r]) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
             }
         }
@@ -266,8 +282,8 @@ __global__ void __launch_bounds__(512, WH_FP8MM_WG_PER_CU) k_fp8_mm(wh_fp8mm_arg
     for (int k = 0; k < 4; ++k) {
         const uint32_t e = threadIdx.x + 512 * k;
         const uint32_t orow = r0 + (e >> 4), ttg = tb * WH_FP8MM_TOK + (e & 15);
-        if (orow < a.row_end && ttg < a.n) {
-            a.y[(size_t)ttg * a.y_stride + (orow - a.row_start)] = sum[k];
+        if (orow < row_end && ttg < a.n) {
+            Y[(size_t)ttg * y_stride + (orow - row_start)] = sum[k];
             if (!(fabsf(sum[k]) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
         }
     }

@@ -554,21 +554,42 @@ bool fp8_mm_ok(const Tensor& t, size_t r0, size_t r1, size_t group_rows) {
     return true;
 }
 
-// y_t = W x_t over rows [r0, r1) for n inputs; with group_rows, rows
-// r0 + [g group_rows, (g + 1) group_rows) read input group g at
-// x + g * xg_stride.  One launch over (row block, k split, token block).
-int launch_fp8_mm(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x, size_t n, size_t x_stride,
-                  float* y, size_t y_stride, size_t group_rows, size_t xg_stride) {
-    const size_t rows = r1 - r0, rb = (rows + WH_FP8MM_ROWS - 1) / WH_FP8MM_ROWS, G = t.cols / 128;
+// Groups per k split of a multi-input MFMA launch over `rows` rows and n
+// inputs: 8, 4 or 2 (what divides the width and fits LDS), the most that
+// still gives ~256 workgroups; 0 when none fits.
+size_t fp8_mm_groups(const Tensor& t, size_t rows, size_t n) {
+    const size_t rb = (rows + WH_FP8MM_ROWS - 1) / WH_FP8MM_ROWS, G = t.cols / 128;
     const size_t tbs = (n + WH_FP8MM_TOK - 1) / WH_FP8MM_TOK;
-    // groups per k split: 8, 4 or 2 (what divides the width and fits LDS),
-    // the most that still gives ~256 workgroups
     size_t kg = 0;
     for (size_t g = WH_FP8MM_MAX_GROUPS; g >= 2; g /= 2) {
         if (G % g || wh_fp8mm_lds(g * 128) > g_max_lds) continue;
         kg = g;
         if (rb * tbs * (G / g) >= 256) break;
     }
+    return kg;
+}
+
+// Rows [r0, r1) of a second tensor on the same inputs, for one launch.
+struct Fp8MmSecond {
+    const Tensor* t;
+    size_t r0, r1;
+    float* y;
+    size_t y_stride;
+};
+
+// y_t = W x_t over rows [r0, r1) for n inputs; with group_rows, rows
+// r0 + [g group_rows, (g + 1) group_rows) read input group g at
+// x + g * xg_stride.  One launch over (row block, k split, token block); with
+// `second`, its row blocks follow the first tensor's in the same launch
+// (the caller checks that both take the same k split).
+int launch_fp8_mm(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x, size_t n, size_t x_stride,
+                  float* y, size_t y_stride, size_t group_rows, size_t xg_stride,
+                  const Fp8MmSecond* second = nullptr) {
+    const size_t rows = r1 - r0, rb1 = (rows + WH_FP8MM_ROWS - 1) / WH_FP8MM_ROWS, G = t.cols / 128;
+    const size_t rb2 = second ? (second->r1 - second->r0 + WH_FP8MM_ROWS - 1) / WH_FP8MM_ROWS : 0;
+    const size_t rb = rb1 + rb2;
+    const size_t tbs = (n + WH_FP8MM_TOK - 1) / WH_FP8MM_TOK;
+    const size_t kg = fp8_mm_groups(t, rows, n);
     if (kg == 0) return WH_UNSUPPORTED;
     const size_t S = G / kg, kc = kg * 128;
     if (rb * S > 65535 || tbs > 65535) return WH_UNSUPPORTED;
@@ -598,6 +619,15 @@ int launch_fp8_mm(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float*
     a.kc = (uint32_t)kc;
     a.splits = (uint32_t)S;
     a.row_blocks = (uint32_t)rb;
+    a.rb_first = (uint32_t)rb1;
+    if (second) {
+        a.w2 = second->t->w;
+        a.scales2 = second->t->s;
+        a.y2 = second->y;
+        a.row_start2 = (uint32_t)second->r0;
+        a.row_end2 = (uint32_t)second->r1;
+        a.y2_stride = (uint32_t)second->y_stride;
+    }
     const dim3 grid((unsigned)rb, (unsigned)S, (unsigned)tbs);
     const size_t lds = wh_fp8mm_lds(kc);
     const bool u8 = t.scale_fmt == WH_SCALE_UE8M0;
@@ -2336,6 +2366,53 @@ int wh_fp8_gemv_multi_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row
     if (!c->exact && n >= c->fp8_mm_min && fp8_mm_ok(*t, row_start, row_end, 0))
         return launch_fp8_mm(c, *t, row_start, row_end, x_dev, n, x_stride, y_dev, y_stride, 0, 0);
     return launch_fp8(c, *t, row_start, row_end, x_dev, y_dev, n, x_stride, y_stride);
+}
+
+// Checks of wh_fp8_gemv_multi_async's arguments.
+static int fp8_multi_check(const Tensor* t, size_t row_start, size_t row_end, const float* x_dev, size_t n,
+                           size_t x_stride, float* y_dev, size_t y_stride) {
+    if (!t) return WH_NOT_RESIDENT;
+    if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
+    if (n == 0 || row_start >= row_end || row_end > t->rows) return WH_INVALID_SHAPE;  // E/compute.rs:6400-6430
+    if (x_stride < t->cols) return WH_INPUT_TOO_SMALL;
+    if (y_stride < row_end - row_start) return WH_OUTPUT_TOO_SMALL;
+    if (x_stride > UINT32_MAX || y_stride > UINT32_MAX || n > 65535) return WH_UNSUPPORTED;
+    WH_TRY(fp8_ptr_check(*t, x_dev, y_dev));
+    if (t->fast && (x_stride & 3)) return WH_INVALID_ARGUMENT;
+    return WH_OK;
+}
+
+int wh_fp8_gemv_multi_pair_async(wh_ctx* c, wh_tensor w0, size_t row_start0, size_t row_end0, float* y0_dev,
+                                 size_t y0_stride, wh_tensor w1, size_t row_start1, size_t row_end1, float* y1_dev,
+                                 size_t y1_stride, const float* x_dev, size_t n, size_t x_stride) {
+    if (!c || !x_dev || !y0_dev || !y1_dev) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    Tensor* t0 = find_tensor(c, w0);
+    Tensor* t1 = find_tensor(c, w1);
+    WH_TRY(fp8_multi_check(t0, row_start0, row_end0, x_dev, n, x_stride, y0_dev, y0_stride));
+    WH_TRY(fp8_multi_check(t1, row_start1, row_end1, x_dev, n, x_stride, y1_dev, y1_stride));
+    WH_HIP(hipSetDevice(c->device));
+    const bool mm0 = !c->exact && n >= c->fp8_mm_min && fp8_mm_ok(*t0, row_start0, row_end0, 0);
+    const bool mm1 = !c->exact && n >= c->fp8_mm_min && fp8_mm_ok(*t1, row_start1, row_end1, 0);
+    // one launch when both take the MFMA path with the same k split, the
+    // tensors agree in width, scale format, rows per scale row and special
+    // codes, and neither output overlaps the inputs or the other output
+    // (the two calls are ordered; where the order could show, they stay two)
+    if (mm0 && mm1 && t0->cols == t1->cols && t0->scale_fmt == t1->scale_fmt && t0->special == t1->special &&
+        t0->rows / t0->scale_rows == t1->rows / t1->scale_rows && t0->scale_cols == t1->scale_cols &&
+        fp8_mm_groups(*t0, row_end0 - row_start0, n) == fp8_mm_groups(*t1, row_end1 - row_start1, n)) {
+        const uintptr_t x_lo = (uintptr_t)x_dev, x_hi = (uintptr_t)(x_dev + (n - 1) * x_stride + t0->cols);
+        const uintptr_t a_lo = (uintptr_t)y0_dev, a_hi = (uintptr_t)(y0_dev + (n - 1) * y0_stride + (row_end0 - row_start0));
+        const uintptr_t b_lo = (uintptr_t)y1_dev, b_hi = (uintptr_t)(y1_dev + (n - 1) * y1_stride + (row_end1 - row_start1));
+        if (!(a_lo < x_hi && x_lo < a_hi) && !(b_lo < x_hi && x_lo < b_hi) && !(a_lo < b_hi && b_lo < a_hi)) {
+            const Fp8MmSecond sec{t1, row_start1, row_end1, y1_dev, y1_stride};
+            return launch_fp8_mm(c, *t0, row_start0, row_end0, x_dev, n, x_stride, y0_dev, y0_stride, 0, 0, &sec);
+        }
+    }
+    if (mm0) WH_TRY(launch_fp8_mm(c, *t0, row_start0, row_end0, x_dev, n, x_stride, y0_dev, y0_stride, 0, 0));
+    else WH_TRY(launch_fp8(c, *t0, row_start0, row_end0, x_dev, y0_dev, n, x_stride, y0_stride));
+    if (mm1) return launch_fp8_mm(c, *t1, row_start1, row_end1, x_dev, n, x_stride, y1_dev, y1_stride, 0, 0);
+    return launch_fp8(c, *t1, row_start1, row_end1, x_dev, y1_dev, n, x_stride, y1_stride);
 }
 
 int wh_fp8_gemv_multi_groups_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end, size_t group_rows,
