@@ -59,7 +59,7 @@ struct wh_batch_args {
     uint32_t x_is_bf16;
     // assignments: i = p * topk + k for the routes, A + p for the shared
     // expert (A = npos * topk); S = A + has_shared * npos slots
-    float* wgt;                    // [A] weight of route assignment i
+    float* wgt;                    // [A] per position: its route weights, in acc_order's order
     uint32_t* sorted;              // [S] assignments grouped by expert id: the slots
     uint32_t* uexp;                // [S] used expert ids, ascending
     uint32_t* uoff;                // [S + 1] their slot ranges
@@ -359,12 +359,18 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
     // order (E/server/generation.rs:2491-2506 pushes targets in that order):
     // key (id, route index) is distinct, and its rank among the position's
     // keys is its place (compile-time indices only: the keys stay in
-    // registers)
+    // registers).  The weights (written above by this same thread, in route
+    // order) are permuted into that order too, so the accumulate reads them
+    // beside the slots.
     for (uint32_t p = tid; p < a.npos; p += 256) {
         const uint32_t k0 = p * a.topk;
         uint32_t key[WH_BATCH_MAX_TOPK];
+        float wk[WH_BATCH_MAX_TOPK];
 #pragma unroll
-        for (uint32_t k = 0; k < WH_BATCH_MAX_TOPK; ++k) key[k] = k < a.topk ? (ids[k0 + k] << 4) | k : 0xffffffffu;
+        for (uint32_t k = 0; k < WH_BATCH_MAX_TOPK; ++k) {
+            key[k] = k < a.topk ? (ids[k0 + k] << 4) | k : 0xffffffffu;
+            wk[k] = k < a.topk ? a.wgt[k0 + k] : 0.0f;
+        }
 #pragma unroll
         for (uint32_t k = 0; k < WH_BATCH_MAX_TOPK; ++k) {
             if (k < a.topk) {
@@ -372,6 +378,7 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
 #pragma unroll
                 for (uint32_t j = 0; j < WH_BATCH_MAX_TOPK; ++j) r += key[j] < key[k];
                 a.acc_order[k0 + r] = slot_of[k0 + k];
+                a.wgt[k0 + r] = wk[k];
             }
         }
     }
@@ -1080,7 +1087,7 @@ __global__ void __launch_bounds__(256) k_moe_batch_accumulate(wh_batch_args a) {
     float acc = 0.0f;
     for (uint32_t k = 0; k < a.topk; ++k) {
         const uint32_t s = a.acc_order[p * a.topk + k];
-        const float v = a.y[(size_t)s * a.hidden + r] * a.wgt[a.sorted[s]];
+        const float v = a.y[(size_t)s * a.hidden + r] * a.wgt[p * a.topk + k];
         acc = acc + v;
     }
     if (a.has_shared) acc = a.y[(size_t)(a.npos * a.topk + p) * a.hidden + r] + acc;
