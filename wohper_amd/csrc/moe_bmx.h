@@ -25,7 +25,7 @@
 #include "moe_px.h"
 
 #ifndef WH_BMX_DEPTH
-#define WH_BMX_DEPTH 6  // weight blocks of a wave in flight
+#define WH_BMX_DEPTH 5  // weight blocks of a wave in flight
 #endif
 #define WH_BMX_TOK 16u                             // slots per virtual expert
 
