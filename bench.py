@@ -633,10 +633,15 @@ def decode_stack_batch16(ctx, layers, n_layers: int, steps: int, seed: int, batc
 
 
 TIMELINE_POINTS = {
-    "token_gateup": ["start", "x, tables staged", "x act-quantized", "tile 0 done", "tile 1 done", "tile 2 done",
-                     "tile 3 done", "end"],
-    "token_down": ["start", "h, tables staged", "h act-quantized", "unit 0 done", "unit 1 done", "unit 2 done",
-                   "unit 3 done", "end"],
+    "token_gateup": ["start", "DMAs issued", "x slice landed", "x slice act-quantized", "B operands loaded",
+                     "tile 0 done", "tile 1 done", "tile 2 done", "tile 3 done", None, "tiles summed", "end"],
+    "token_down": ["start", "DMAs issued", "h quarters landed", "h act-quantized, B operands loaded", None,
+                   "unit 0 done", "unit 1 done", "unit 2 done", "unit 3 done", None, "units summed", "end"],
+    "token_gateup_px": ["start", "tables staged", "x in registers", "x act-quantized", "ring issued",
+                        "barrier passed", "tile 0 done", "tile 1 done", "tile 2 done", "tile 3 done", "tiles summed",
+                        "end"],
+    "token_down_px": ["start", "tables staged", "h in registers", "h act-quantized", "ring issued", "barrier passed",
+                      "unit 0 done", "unit 1 done", "unit 2 done", "unit 3 done", "units summed", "end"],
     "batch_gateup": ["start", "ring issued", "B staged", "wave's last item done", "workgroup end"],
     "batch_down": ["start", "ring issued", "B staged", "wave's last item done", "workgroup end"],
 }
@@ -668,15 +673,18 @@ def timeline(lib_path: str, seed: int = 2) -> dict:
         for e in range(wl.N_ROUTED + 1):
             ctx.store_expert_synthetic(layer, e, wl.HIDDEN, wl.INTER, seed)
     rng = np.random.default_rng(seed)
-    n_stamp = 512 * 16 * 8
+    n_points = 16
+    n_stamp = 512 * 16 * n_points
 
     def read(which, names):
         buf = np.zeros(n_stamp, np.uint64)
         assert lib.wh_debug_timeline(which, buf.ctypes.data, n_stamp) == 0
-        t = buf.reshape(512, 16, 8)[:256].astype(np.int64)
+        t = buf.reshape(512, 16, n_points)[:256].astype(np.int64)
         t0 = t[:, :, 0][t[:, :, 0] > 0].min()
         out = {}
         for k, name in enumerate(names):
+            if name is None:
+                continue
             v = t[:, :, k].ravel()
             v = (v[v > 0] - t0) * 0.01
             if v.size:
@@ -687,13 +695,15 @@ def timeline(lib_path: str, seed: int = 2) -> dict:
     x = wl.bf16_bits(rng.standard_normal((1, wl.HIDDEN)).astype(np.float32))
     x_dev, out_dev = ctx.device_alloc(x.nbytes), ctx.device_alloc(wl.HIDDEN * 4)
     ctx.to_device(x_dev, x)
-    for i in range(12):
-        idx, w = wl.route_topk_sigmoid(rng.standard_normal(wl.N_ROUTED).astype(np.float32))
-        ctx.routed_experts_async([(i % n_layers, int(e), float(wt)) for e, wt in zip(idx, w)], x_dev, True, 1,
-                                 out_dev)
-        ctx.synchronize()
-    res["token_gateup"] = read(0, TIMELINE_POINTS["token_gateup"])
-    res["token_down"] = read(1, TIMELINE_POINTS["token_down"])
+    for version, tag in ((0, "_px"), (3, "")):
+        ctx.debug_token_kernels(version)
+        for i in range(12):
+            idx, w = wl.route_topk_sigmoid(rng.standard_normal(wl.N_ROUTED).astype(np.float32))
+            ctx.routed_experts_async([(i % n_layers, int(e), float(wt)) for e, wt in zip(idx, w)], x_dev, True, 1,
+                                     out_dev)
+            ctx.synchronize()
+        res["token_gateup" + tag] = read(0, TIMELINE_POINTS["token_gateup" + tag])
+        res["token_down" + tag] = read(1, TIMELINE_POINTS["token_down" + tag])
     npos = 16
     ids = np.stack([rng.choice(wl.N_ROUTED, wl.TOPK, replace=False) for _ in range(npos)]).astype(np.uint32)
     sc = rng.uniform(0.1, 1.0, (npos, wl.TOPK)).astype(np.float32)

@@ -227,6 +227,9 @@ extern "C" {
     pub fn wh_profile_routed(ctx: *mut WhCtx, routes: *const WhExpertRoute, n_routes: usize, n_sets: usize,
                              x_dev: *const c_void, x_is_bf16: c_int, out_dev: *mut f32, iters: usize,
                              us_per_launch: *mut f64) -> c_int;
+    pub fn wh_profile_token_pipeline(ctx: *mut WhCtx, routes: *const WhExpertRoute, n_routes: usize,
+                                     n_sets: usize, x_dev: *const c_void, x_is_bf16: c_int, x_stride: usize,
+                                     out_dev: *mut f32, iters: usize, mode: c_int, us_per_token: *mut f64) -> c_int;
     pub fn wh_rope_inv_freqs(rope_dim: usize, theta: f32, yarn: *const WhYarn, out_: *mut f32, out_len: usize) -> c_int;
     pub fn wh_deepseek_rope_for_layer(physical_layer: u32, theta: *mut f32, yarn: *mut WhYarn,
                                       has_yarn: *mut c_int) -> c_int;

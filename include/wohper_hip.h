@@ -365,6 +365,14 @@ int wh_set_exact_numerics(wh_ctx* ctx, int on);
  * outputs (f32 [T][n][inter]), 2 expert outputs (f32 [T][n][hidden]). */
 int wh_debug_moe_token_capture(wh_ctx* ctx, int on);
 int wh_debug_moe_token_read(wh_ctx* ctx, int which, void* out, size_t bytes);
+/* Measurement support, no counterpart in the reference: which kernels the
+ * MFMA numerics mode runs for a token at hidden 4096, inter 2048 and up to
+ * 8 experts.  mask bit 0: gate/up, bit 1: down streamed into LDS by direct
+ * loads; a clear bit: the register-ring kernel of that stage (also used for
+ * every other shape).  The default, 1, is the faster pair measured in the
+ * token pipeline.  All compute the same operands; only the fp32 summation
+ * order differs. */
+int wh_debug_token_kernels(wh_ctx* ctx, int mask);
 
 /* Batched routed experts for npos positions, expert-major, replacing the
  * batch-prefill MoE of the reference: per-position weights score / sum (or
@@ -523,6 +531,17 @@ int wh_probe_read_floor(wh_ctx* ctx, const void* buf_dev, size_t buf_bytes, size
 int wh_profile_routed(wh_ctx* ctx, const wh_expert_route* routes, size_t n_routes, size_t n_sets,
                       const void* x_dev, int x_is_bf16, float* out_dev, size_t iters,
                       double* us_per_launch);
+/* Measurement support, no counterpart in the reference: `iters` routed-expert
+ * tokens enqueued by one call, each token's gate/up then down, in the current
+ * numerics mode; token i takes route set i % n_sets (n_routes entries each),
+ * input row i % n_sets of x_dev (rows x_stride bytes apart, a multiple of 16)
+ * and output row i % n_sets of out_dev (hidden floats).  mode 0: a host loop
+ * of launches; 1: the same launches captured once into a HIP graph (kernel
+ * nodes only) and replayed.  *us_per_token: mean between HIP events on the
+ * context stream around the timed launches (the graph's second replay). */
+int wh_profile_token_pipeline(wh_ctx* ctx, const wh_expert_route* routes, size_t n_routes, size_t n_sets,
+                              const void* x_dev, int x_is_bf16, size_t x_stride, float* out_dev, size_t iters,
+                              int mode, double* us_per_token);
 
 /* Test support, no counterpart in the reference: evaluates the device libm
  * emulation on n values.  fn 0: silu(x) = x / (1 + expf(-x)) for x <= 10;
@@ -530,7 +549,9 @@ int wh_profile_routed(wh_ctx* ctx, const wh_expert_route* routes, size_t n_route
  * exp2f(ceilf(log2f(max(x, 1e-4) / 448))) for finite x >= 0; fn 3: a plain
  * device copy out = in (n a multiple of 4) that calibrates HBM byte counters;
  * fn 4: the router's sqrt_softplus(x); fn 5: log1pf(x) for x >= 0; fn 6:
- * expf(x) for any x. */
+ * expf(x) for any x; fn 7 / 8: the act-quant (block 64) of the LDS-streaming
+ * token kernels for bf16 / f32 inputs (n a multiple of 64, finite values;
+ * fn 7's inputs must be bf16 values), dequantized. */
 int wh_debug_eval(wh_ctx* ctx, int fn, const float* in, float* out, size_t n);
 
 /* ------------------------------------------------------------------

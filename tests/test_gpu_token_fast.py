@@ -59,8 +59,19 @@ def _oracle_forward(oracle, experts, weights, x, has_shared):
     return want.astype(np.float32)
 
 
-def test_fast_routed_six_experts(ctx, oracle):
-    """The headline token: 6 routed experts of the model's shapes."""
+@pytest.mark.parametrize("kernels", [1, 0, 2, 3])
+def test_fast_routed_six_experts(ctx, oracle, kernels):
+    """The headline token: 6 routed experts of the model's shapes, on each
+    pairing of the LDS-streaming and register-ring gate/up and down kernels
+    (mask bit 0: gate/up, bit 1: down; 1 is the default)."""
+    ctx.debug_token_kernels(kernels)
+    try:
+        _routed_six(ctx, oracle)
+    finally:
+        ctx.debug_token_kernels(1)
+
+
+def _routed_six(ctx, oracle):
     seed = 2
     idx, w, x = wl.moe_token_case(seed)
     routes = [(13, int(e), float(wt)) for e, wt in zip(idx, w)]

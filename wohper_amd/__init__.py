@@ -78,11 +78,11 @@ EXPORTED = (
     "wh_fp8_gemv", "wh_fp8_gemv_multi", "wh_fp4_matvec", "wh_fp4_expert_forward",
     "wh_act_quant_dequant", "wh_routed_experts", "wh_routed_experts_async", "wh_fp8_gemv_async",
     "wh_stream_status", "wh_debug_eval", "wh_timer_start", "wh_timer_stop", "wh_profile_routed",
-    "wh_probe_read_floor",
+    "wh_probe_read_floor", "wh_profile_token_pipeline",
     "wh_store_fp8_synthetic", "wh_synth_fp8_host", "wh_routed_and_shared_experts", "wh_fp8_gemv_batch_async",
     "wh_routed_and_shared_experts_async", "wh_moe_batch", "wh_moe_batch_async", "wh_set_moe_mfma_min",
     "wh_debug_moe_batch_read", "wh_fp8_gemv_multi_async", "wh_fp8_gemv_multi_groups_async", "wh_fp8_gemv_multi_pair_async", "wh_set_fp8_mfma_min",
-    "wh_set_exact_numerics", "wh_debug_moe_token_capture",
+    "wh_set_exact_numerics", "wh_debug_moe_token_capture", "wh_debug_token_kernels",
     "wh_debug_moe_token_read", "wh_fp8_shared_expert", "wh_fp8_shared_expert_async",
     "wh_device_alloc", "wh_device_free", "wh_memcpy", "wh_last_error",
     "wh_quant_block_header", "wh_quant_block_tensor", "wh_quant_block_fp4_expert", "wh_store_expert_block",
@@ -210,6 +210,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
                                                          c.c_uint32, vp, c.c_int, sz, vp]),
         "wh_routed_and_shared_experts_noalloc_async": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, c.c_uint32,
                                                                  c.c_uint32, vp, c.c_int, sz, vp]),
+        "wh_profile_token_pipeline": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, sz, vp, c.c_int, sz, vp, sz,
+                                                c.c_int, c.POINTER(c.c_double)]),
         "wh_profile_routed": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, sz, vp, c.c_int, vp, sz,
                                         c.POINTER(c.c_double)]),
         "wh_timer_stop": (c.c_int, [vp, c.POINTER(c.c_double)]),
@@ -230,6 +232,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_fp8_shared_expert": (c.c_int, [vp, c.c_uint64, c.c_uint64, c.c_uint64, f32p, sz, f32p, sz]),
         "wh_fp8_shared_expert_async": (c.c_int, [vp, c.c_uint64, c.c_uint64, c.c_uint64, vp, vp]),
         "wh_debug_moe_token_capture": (c.c_int, [vp, c.c_int]),
+        "wh_debug_token_kernels": (c.c_int, [vp, c.c_int]),
         "wh_debug_moe_token_read": (c.c_int, [vp, c.c_int, vp, sz]),
         "wh_quant_block_header": (c.c_int, [u8p, sz, c.POINTER(c.c_uint32), c.POINTER(c.c_uint32),
                                             c.POINTER(c.c_uint32)]),
@@ -515,6 +518,21 @@ class Context:
                                           ctypes.c_void_p(out_dev), iters, us), "profile_routed")
         return us[0], us[1]
 
+    def profile_token_pipeline(self, route_sets, x_dev: int, x_is_bf16: bool, x_stride: int, out_dev: int,
+                               iters: int, graph: bool) -> float:
+        """Mean microseconds per token of `iters` tokens (gate/up then down)
+        enqueued by one library call, token i on route set i % len(route_sets)
+        with input / output row i % len(route_sets); graph: replay of a HIP
+        graph captured from the same launches."""
+        n = len(route_sets[0])
+        flat = [r for rs in route_sets for r in rs]
+        arr = (WhExpertRoute * len(flat))(*[WhExpertRoute(int(l), int(e), float(w)) for l, e, w in flat])
+        us = ctypes.c_double()
+        _check(self.lib.wh_profile_token_pipeline(self._h, arr, n, len(route_sets), ctypes.c_void_p(x_dev),
+                                                  int(x_is_bf16), x_stride, ctypes.c_void_p(out_dev), iters,
+                                                  int(bool(graph)), ctypes.byref(us)), "profile_token_pipeline")
+        return us.value
+
     def probe_read_floor(self, buf_dev: int, buf_bytes: int, nbytes: int, reps: int):
         """Fastest plain streaming read of nbytes per launch (rotating windows
         of the device buffer): (us, grid, depth, empty-launch us)."""
@@ -698,6 +716,12 @@ class Context:
         summation order (bit-identical); False: split-K kernels, each matvec
         within 1e-5 * ||w_row|| * ||x|| of it."""
         _check(self.lib.wh_set_exact_numerics(self._h, int(bool(on))), "set_exact_numerics")
+
+    def debug_token_kernels(self, mask: int):
+        """MFMA token kernels at hidden 4096 / inter 2048: bit 0 gate/up, bit 1
+        down on the LDS-streaming kernels (default 1), else the register-ring
+        kernels."""
+        _check(self.lib.wh_debug_token_kernels(self._h, int(mask)), "debug_token_kernels")
 
     def debug_moe_token_capture(self, on: bool):
         _check(self.lib.wh_debug_moe_token_capture(self._h, int(bool(on))), "debug_moe_token_capture")

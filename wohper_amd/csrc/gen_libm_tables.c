@@ -157,6 +157,60 @@ static int check_sincos(void) {
     return bad != 0;
 }
 
+// wh_e4m3_code_scaled(h, k) against the code of wh_e4m3_round(h / 2^k) for
+// t = h / 2^k over every float in [0, 448] (both signs; every 11th float
+// for the other k), with h = t 2^k exactly representable.
+typedef struct {
+    uint32_t b0, b1;
+    long bad;
+} code_job;
+static uint32_t e4m3_code_of(float q) {  // q on the E4M3 grid, |q| <= 448
+    const uint32_t b = wh_float_to_bits(q), a = b & 0x7fffffffu;
+    const uint32_t mag = a >= 0x3c800000u ? (a >> 20) - 960u : (uint32_t)(wh_bits_to_float(a) * 512.0f);
+    return mag | ((b >> 31) << 7);
+}
+static void* code_verify(void* p) {
+    code_job* j = (code_job*)p;
+    static const int ks[5] = {-3, -23, -9, 0, 5};
+    for (uint32_t b = j->b0; b < j->b1; ++b) {
+        const float t = wh_bits_to_float(b);
+        for (int ki = 0; ki < 5; ++ki) {
+            if (ki > 0 && b % 11u) continue;
+            const int k = ks[ki];
+            const float h = t * wh_pow2f(k);
+            if (h * wh_pow2f(-k) != t) continue;  // t 2^k not exact (underflow)
+            for (int sg = 0; sg < 2; ++sg) {
+                const float hs = sg ? -h : h, ts = sg ? -t : t;
+                uint32_t want = e4m3_code_of(wh_e4m3_round(ts)), got = wh_e4m3_code_scaled(hs, k);
+                if ((want & 0x7f) == 0 && (got & 0x7f) == 0) want = got;  // zero: either sign
+                if (want != got && j->bad++ < 5)
+                    fprintf(stderr, "e4m3 code mismatch: h=%a k=%d got %02x want %02x\n", hs, k, got, want);
+            }
+        }
+    }
+    return NULL;
+}
+static int check_e4m3_code_scaled(void) {
+    enum { T = 8 };
+    code_job js[T];
+    pthread_t ts[T];
+    const uint32_t end = 0x43e00001u;  // +0 .. 448
+    for (int i = 0; i < T; ++i) {
+        js[i].b0 = (uint32_t)((uint64_t)end * i / T);
+        js[i].b1 = (uint32_t)((uint64_t)end * (i + 1) / T);
+        js[i].bad = 0;
+        pthread_create(&ts[i], NULL, code_verify, &js[i]);
+    }
+    long bad = 0;
+    for (int i = 0; i < T; ++i) {
+        pthread_join(ts[i], NULL);
+        bad += js[i].bad;
+    }
+    if (bad) fprintf(stderr, "e4m3 code: %ld mismatches\n", bad);
+    else fprintf(stderr, "e4m3 code: every scaled float matches wh_e4m3_round\n");
+    return bad != 0;
+}
+
 // Every float t in [-448, 448] against the brute-force nearest E4M3 value
 // (ties to the lower value, +0 for zero), walking the positive grid upward.
 static int check_e4m3_round(void) {
@@ -279,6 +333,13 @@ int main(int argc, char** argv) {
         fprintf(stderr, "log2f: %ld mismatches\n", bad);
         return 1;
     }
+    for (int e = -126; e <= 127; ++e) {
+        if (wh_log2f_thr(e) != thr[e + 126]) {
+            fprintf(stderr, "log2f: closed-form threshold of binade %d is %u, the table's %u\n", e, wh_log2f_thr(e),
+                    thr[e + 126]);
+            return 1;
+        }
+    }
     for (int k = -126; k <= 127; ++k) {
         if (wh_float_to_bits(exp2f((float)k)) != wh_float_to_bits(wh_pow2f(k))) {
             fprintf(stderr, "exp2f(%d) is not 2^%d\n", k, k);
@@ -287,6 +348,7 @@ int main(int argc, char** argv) {
     }
 
     if (check_e4m3_round()) return 1;
+    if (check_e4m3_code_scaled()) return 1;
     if (check_sincos()) return 1;
 
     // log1pf over [+0, +inf]

@@ -802,7 +802,7 @@ struct wh_moe_args {
     float* h;                      // [n_tokens][n_experts][inter] SwiGLU output
     float* y;                      // [n_tokens][n_experts][hidden] per-expert outputs
     float* out;                    // [n_tokens][hidden] routed sum
-    uint32_t* cnt_y;               // [n_tokens][hidden/32] arrivals per 32-row slice
+    uint32_t* cnt_y;               // [n_tokens][hidden/16] arrivals per 16- or 32-row slice
     uint32_t* status;
     float* gu;                     // null, or [n_tokens][n_experts][2][inter]: gate and up captured
 };
@@ -936,10 +936,12 @@ __device__ __forceinline__ float wh_dpp_row_shl8(float v) {  // lane i <- lane i
 // The first gate/up workgroup of a token clears the token's routed-sum
 // arrival counters, which the down launch after it counts with: whatever
 // the counters' memory held before, every call starts from zero.
+// The token's arrival counters: hidden / 16 of them (one per 16-row output
+// slice; the exact kernels' 32-row slices use the first half).
 __device__ __forceinline__ void wh_moe_clear_arrivals(const wh_moe_args& a, uint32_t tok) {
     if (blockIdx.x != 0) return;
-    uint32_t* cnt = a.cnt_y + (size_t)tok * (a.hidden >> 5);
-    for (uint32_t i = threadIdx.x; i < (a.hidden >> 5); i += blockDim.x)
+    uint32_t* cnt = a.cnt_y + (size_t)tok * (a.hidden >> 4);
+    for (uint32_t i = threadIdx.x; i < (a.hidden >> 4); i += blockDim.x)
         __hip_atomic_store(cnt + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -1068,7 +1070,7 @@ __device__ __forceinline__ void wh_h_stage_store(const wh_h_stage& st, float* xs
 __device__ __forceinline__ void wh_moe_routed_sum(const wh_moe_args& a, uint32_t tok, uint32_t rb, uint32_t* last) {
     wh_stores_done();
     __syncthreads();
-    uint32_t* cnt = a.cnt_y + (size_t)tok * (a.hidden >> 5) + rb;
+    uint32_t* cnt = a.cnt_y + (size_t)tok * (a.hidden >> 4) + rb;
     if (threadIdx.x == 0) *last = wh_arrive(cnt) == a.n_experts - 1;
     __syncthreads();
     if (!*last || threadIdx.x >= 32) return;

@@ -116,6 +116,22 @@ WH_HD int wh_ceil_log2f(float r, const uint32_t* thr) {
     return m > thr[e + 126] ? e + 1 : e;
 }
 
+// The same thresholds in closed form.  log2f(2^e (1 + m 2^-23)) is e plus
+// about 1.44 m 2^-23, and it rounds back to e while that is under half an
+// ulp of the result; the result's binade is that of |e| for e >= 0 and of
+// |e| - 1 for e < 0 (the result lies just above e), so the threshold
+// depends only on the bit length of e >= 0 ? e : -e - 1 (0..7):
+// {0, 0, 0, 1, 2, 5, 11, 22}.  The table generator checks this against the
+// table it derives from the host glibc, binade by binade, and fails the
+// build on any difference.
+WH_HD uint32_t wh_log2f_thr(int e) {
+    const uint32_t u = (uint32_t)(e ^ (e >> 31));  // e >= 0 ? e : -e - 1
+    uint32_t bl = 0;
+    while ((u >> bl) != 0u) ++bl;
+    return (uint32_t)((0x160B050201000000ull >> (8 * bl)) & 0xffu);
+}
+
+
 // glibc-exact log1pf(x) for x >= 0 (Rust's f32::ln_1p): the float form of
 // the published fdlibm log1p method (Sun Microsystems; s_log1pf.c as carried
 // by FreeBSD msun and glibc's sysdeps/ieee754/flt-32), evaluated in float
@@ -317,3 +333,41 @@ WH_HD float wh_e4m3_round(float t) {
     const uint32_t sub = wh_float_to_bits((float)n * 0.001953125f) | (n ? s : 0u);
     return wh_bits_to_float(a >= 0x3c800000u ? normal : sub);
 }
+
+// The E4M3 code of t = h / 2^k under the act-quant rounding (nearest, ties
+// toward -inf, E/compute.rs:2537-2545), from h's own bits, for |t| <= 448.
+// For |t| >= 2^-6 the grid keeps 3 mantissa bits and dividing by 2^k only
+// moves the exponent, so the rounded magnitude is ((|h| bits + 0x7ffff +
+// sign) >> 20) - (960 + 8 k): wh_e4m3_round's integer rounding, shifted.
+// Below 2^-6 the grid is n 2^-9 and wh_e4m3_round's second branch applies.
+// A zero result keeps the sign (0x80 for -0; the MFMA takes it as 0).  The
+// table generator compares it with wh_e4m3_round for every float h with
+// |h / 2^k| <= 448 at several k.
+WH_HD uint32_t wh_e4m3_code_scaled(float h, int k) {
+    const uint32_t b = wh_float_to_bits(h), a = b & 0x7fffffffu, sg = b >> 31;
+    uint32_t mag = ((a + 0x7ffffu + sg) >> 20) - (uint32_t)(960 + 8 * k);
+    if (a < ((uint32_t)(121 + k) << 23)) {
+        float at = wh_bits_to_float(a) * wh_pow2f(-k);  // |h / 2^k|, exact
+        at = at < 0.015625f ? at : 0.015625f;
+        mag = ((uint32_t)(at * 8589934592.0f) + 0x7fffffu + sg) >> 24;
+    }
+    return (mag < 0x7eu ? mag : 0x7eu) | (sg << 7);  // (the clamp only ever meets non-finite h)
+}
+
+#ifdef __HIPCC__
+// Device form: the bit length from the count of leading zeros.
+__device__ __forceinline__ uint32_t wh_log2f_thr_dev(int e) {
+    const uint32_t u = (uint32_t)(e ^ (e >> 31));
+    const uint32_t bl = 32u - (uint32_t)__clz((int)u);
+    return __builtin_amdgcn_perm(0x160B0502u, 0x01000000u, bl) & 0xffu;
+}
+// ceil(log2f(max(amax, 1e-4) / 448)): the act-quant scale exponent
+// (E/compute.rs:2511-2514) without the threshold table.
+__device__ __forceinline__ int wh_aq_scale_exp_fast(float amax) {
+    const float r = fmaxf(amax, 1.0e-4f) / 448.0f;
+    const uint32_t b = wh_float_to_bits(r);
+    const int e = (int)((b >> 23) & 0xff) - 127;
+    const uint32_t m = b & 0x7fffff;
+    return (m != 0u && m > wh_log2f_thr_dev(e)) ? e + 1 : e;
+}
+#endif

@@ -54,17 +54,23 @@
 
 // Optional per-wave timeline of the two kernels (build with -DWH_TIMELINE):
 // lane 0 of each wave stores the 100 MHz realtime counter at fixed points of
-// the kernel into wh_tl_buf[kernel][(workgroup * 16 + wave) * 8 + point],
+// the kernel into wh_tl_buf[kernel][(workgroup * 16 + wave) * 16 + point],
 // for the first 512 workgroups of token 0; wh_debug_timeline reads it back.
+// WH_TL_USE(v) makes the wave wait for a loaded value before the next stamp.
 #ifdef WH_TIMELINE
-__device__ uint64_t wh_tl_buf[2][512 * 16 * 8];
+#define WH_TL_POINTS 16
+__device__ uint64_t wh_tl_buf[2][512 * 16 * WH_TL_POINTS];
 #define WH_TL(kern, k)                                                                                    \
     do {                                                                                                  \
         if ((threadIdx.x & 63) == 0 && blockIdx.x < 512 && blockIdx.y == 0 && (threadIdx.x >> 6) < 16)     \
-            wh_tl_buf[kern][((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * 8 + (k)] =                    \
+            wh_tl_buf[kern][((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * WH_TL_POINTS + (k)] =         \
                 __builtin_amdgcn_s_memrealtime();                                                         \
     } while (0)
+#define WH_TL_USE(v) asm volatile("" ::"v"(v))
 #else
+#define WH_TL_USE(v) \
+    do {             \
+    } while (0)
 #define WH_TL(kern, k) \
     do {               \
     } while (0)
@@ -256,6 +262,9 @@ __global__ void __launch_bounds__(kCols / 8, 1) k_moe_gateup_px(wh_moe_args a) {
     wh_exp_stage_store(es, exp_tab);
     __syncthreads();
     WH_TL(0, 1);
+    WH_TL_USE(xin.r0.x);
+    WH_TL_USE(xin.r1.w);
+    WH_TL(0, 2);
     // act-quant of x (E/compute.rs:2504-2521): columns 8t .. 8t + 7
     float v[8], q[8], sc;
     int k;
@@ -264,9 +273,11 @@ __global__ void __launch_bounds__(kCols / 8, 1) k_moe_gateup_px(wh_moe_args a) {
     wh_aq_vals<8>(v, thr, q, k, sc, bad);
     wh_px_store_codes8(xc, xsb, threadIdx.x, q, k);
     __builtin_amdgcn_sched_barrier(0);
+    WH_TL(0, 3);
 #pragma unroll
     for (int j = kPro; j < kDepth; ++j) wh_mx_raw_load(ring[j], wrow[j / kB] + lane_off, srow[j / kB], j % kB);
     __builtin_amdgcn_sched_barrier(0);
+    WH_TL(0, 4);
     if (__syncthreads_or(bad)) {
         // -480 (a NaN's value) and an infinite scale have no E4M3 / E8M0
         // code: this token's rows run in fp32 from the dequantized x
@@ -279,7 +290,7 @@ __global__ void __launch_bounds__(kCols / 8, 1) k_moe_gateup_px(wh_moe_args a) {
             if (L < 16) red[(i * kWaves + wave) * 16 + L] = r;
         }
     } else {
-        WH_TL(0, 2);
+        WH_TL(0, 5);
         uint32_t dep = wh_opaque_zero(__uint_as_float(*(const uint32_t*)xsb));
         wh_v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -302,11 +313,12 @@ __global__ void __launch_bounds__(kCols / 8, 1) k_moe_gateup_px(wh_moe_args a) {
                     for (int r = 0; r < 4; ++r) red[(i * kWaves + wave) * 16 + 4 * g + r] = acc[r];
                 }
                 acc = wh_v4f{0.0f, 0.0f, 0.0f, 0.0f};
-                if (i < 4) WH_TL(0, 3 + i);
+                if (i < 4) WH_TL(0, 6 + i);
             }
         }
     }
     __syncthreads();
+    WH_TL(0, 10);
     // SwiGLU of the tiles' rows, thread t: tile t / 16, row t % 16
     if (threadIdx.x < nt * 16) {
         const uint32_t i = threadIdx.x >> 4, r = threadIdx.x & 15;
@@ -326,7 +338,7 @@ __global__ void __launch_bounds__(kCols / 8, 1) k_moe_gateup_px(wh_moe_args a) {
             a.gu[2 * he + a.inter + row] = uv;
         }
     }
-    WH_TL(0, 7);
+    WH_TL(0, 11);
 }
 
 // The ordered routed sum of one output row from the per-expert outputs yv
@@ -422,6 +434,15 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
     wh_thr_stage_store(ts, thr);
     __syncthreads();
     WH_TL(1, 1);
+#ifdef WH_TIMELINE
+    {
+        float hs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kU; ++i) hs += hv[i][0].x + hv[i][1].w;
+        WH_TL_USE(hs);
+    }
+#endif
+    WH_TL(1, 2);
     // act-quant of h (E/deepseek_v4.rs:595, block 64): h is finite whenever
     // gate/up was (a non-finite gate/up output is already reported); keep
     // the arithmetic in range regardless
@@ -442,11 +463,13 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
         if (c < n * 256) wh_px_store_codes8(hc + kCols * (c >> 8), hsb + kG * (c >> 8), c & 255, q, k);
     }
     __builtin_amdgcn_sched_barrier(0);
+    WH_TL(1, 3);
 #pragma unroll
     for (int j = kPro; j < kDepth; ++j) wh_mx_raw_load(ring[j], wl[j >> 1], sr[j >> 1], j & 1);
     __builtin_amdgcn_sched_barrier(0);
+    WH_TL(1, 4);
     __syncthreads();
-    WH_TL(1, 2);
+    WH_TL(1, 5);
     {
         uint32_t dep = wh_opaque_zero(__uint_as_float(*(const uint32_t*)hsb));
         wh_v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -469,11 +492,12 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
                     for (int r = 0; r < 4; ++r) red[(wave + 8 * kk) * 16 + 4 * g + r] = acc[r];
                 }
                 acc = wh_v4f{0.0f, 0.0f, 0.0f, 0.0f};
-                if (kk < 4) WH_TL(1, 3 + kk);
+                if (kk < 4) WH_TL(1, 6 + kk);
             }
         }
     }
     __syncthreads();
+    WH_TL(1, 10);
     // per-expert outputs (the 4 quarters of each expert), then the ordered
     // routed sum
     if (threadIdx.x < 16) {
@@ -495,5 +519,5 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
         if (!finite) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
         a.out[(size_t)tok * a.hidden + orow] = wh_route_combine(a, yv);
     }
-    WH_TL(1, 7);
+    WH_TL(1, 11);
 }

@@ -24,6 +24,7 @@
 #include "mla.h"
 #include "moe_batch.h"
 #include "moe_px.h"
+#include "moe_tok.h"
 #include "fp8_mm.h"
 #include "moe_bmx.h"
 #include "probe.h"
@@ -274,6 +275,7 @@ struct wh_ctx {
     uint32_t fp8_mm_min = 4;                // multi-input FP8 GEMVs with this many inputs use MFMA
     Scratch fp8mm_ws, fp8mm_cnt;            // their partial tiles and arrival counters
     bool exact = true;                      // routed experts in the reference's summation order
+    int token_kernels = 1;                  // MFMA token kernels: bit 0 gate/up, bit 1 down on k_*_tok (else k_*_px)
     bool capture_gu = false;                // routed experts keep gate/up in `gu` (test support)
     size_t tok_last_n = 0, tok_last_tokens = 0, tok_last_hidden = 0, tok_last_inter = 0;
     size_t moe_last_slots = 0, moe_last_npos = 0;  // sizes of the last single-chunk batch call
@@ -735,7 +737,7 @@ bool expert_fast(const ExpertView& v) {
 struct MoeBufs {
     float* h = nullptr;       // [T][n][inter] SwiGLU outputs
     float* y = nullptr;       // [T][n][hidden] per-expert outputs
-    uint32_t* cnt = nullptr;  // [T][hidden / 32] routed-sum arrivals (cleared by gate/up)
+    uint32_t* cnt = nullptr;  // [T][hidden / 16] routed-sum arrivals (cleared by gate/up)
     float* gu = nullptr;      // test capture of gate and up, or null
 };
 
@@ -770,7 +772,7 @@ MoeSizes moe_sizes(size_t n, size_t n_tokens, size_t hidden, size_t inter) {
     MoeSizes z;
     z.h = r(n_tokens * n * inter * sizeof(float));
     z.y = r(n_tokens * n * hidden * sizeof(float));
-    z.cnt = r(n_tokens * (hidden / 32) * sizeof(uint32_t));
+    z.cnt = r(n_tokens * (hidden / 16) * sizeof(uint32_t));
     return z;
 }
 
@@ -825,8 +827,25 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
     if (record)
         c->tok_last_n = n, c->tok_last_tokens = n_tokens, c->tok_last_hidden = hidden, c->tok_last_inter = inter;
     const bool sk = moe_mfma(c, hidden, inter);
+    // the LDS-DMA kernels (moe_tok.h): hidden 4096, inter 2048, up to 8 experts
+    const bool tk_shape = sk && hidden == 4096 && inter == 2048 && n <= 8;
+    const bool tk = tk_shape && (c->token_kernels & 1), tkd = tk_shape && (c->token_kernels & 2);
     if (stages & 1) {
-        if (sk) {
+        if (tk) {
+            const size_t tiles = n * inter / 16, cus = (size_t)device_cus();
+            const size_t per = std::min<size_t>(4, std::max<size_t>(1, (tiles * n_tokens + cus - 1) / cus));
+            dim3 ggrid((unsigned)((tiles + per - 1) / per), (unsigned)n_tokens);
+#define WH_GU_TOK(P)                                                                                        \
+    do {                                                                                                    \
+        if (x_bf16) k_moe_gateup_tok<P, WH_TOK_SLOTS, true><<<ggrid, 512, 0, c->stream>>>(a);               \
+        else k_moe_gateup_tok<P, WH_TOK_SLOTS, false><<<ggrid, 512, 0, c->stream>>>(a);                     \
+    } while (0)
+            if (per == 1) WH_GU_TOK(1);
+            else if (per == 2) WH_GU_TOK(2);
+            else if (per == 3) WH_GU_TOK(3);
+            else WH_GU_TOK(4);
+#undef WH_GU_TOK
+        } else if (sk) {
             // block-scaled FP8 MFMA over the act-quantized x: persistent
             // workgroups of `per` 16-row tiles, about one per CU
             const size_t tiles = n * inter / 16, cus = (size_t)device_cus();
@@ -852,7 +871,17 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
     }
     if (stages & 2) {
         dim3 dgrid((unsigned)(n * hidden / 32), (unsigned)n_tokens);
-        if (sk) {
+        if (tkd) {
+            // every expert of a 16-row output slice per workgroup, the
+            // weights and h streamed into LDS
+            dim3 pgrid((unsigned)(hidden / 16), (unsigned)n_tokens);
+            switch ((n + 1) / 2) {
+                case 1: k_moe_down_tok<1, WH_TOKD_SLOTS><<<pgrid, 512, 0, c->stream>>>(a); break;
+                case 2: k_moe_down_tok<2, WH_TOKD_SLOTS><<<pgrid, 512, 0, c->stream>>>(a); break;
+                case 3: k_moe_down_tok<3, WH_TOKD_SLOTS><<<pgrid, 512, 0, c->stream>>>(a); break;
+                default: k_moe_down_tok<4, WH_TOKD_SLOTS><<<pgrid, 512, 0, c->stream>>>(a); break;
+            }
+        } else if (sk) {
             // every expert of a 16-row output slice per workgroup: the routed
             // sum stays in the workgroup
             dim3 pgrid((unsigned)(hidden / 16), (unsigned)n_tokens);
@@ -2741,6 +2770,13 @@ int wh_set_exact_numerics(wh_ctx* c, int on) {
     return WH_OK;
 }
 
+int wh_debug_token_kernels(wh_ctx* c, int mask) {
+    if (!c || mask < 0 || mask > 3) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    c->token_kernels = mask;
+    return WH_OK;
+}
+
 int wh_debug_moe_token_capture(wh_ctx* c, int on) {
     if (!c) return WH_INVALID_ARGUMENT;
     std::lock_guard<std::mutex> lk(c->mu);
@@ -3084,20 +3120,86 @@ int wh_profile_routed(wh_ctx* c, const wh_expert_route* routes, size_t n_routes,
     return read_status(c);
 }
 
+int wh_profile_token_pipeline(wh_ctx* c, const wh_expert_route* routes, size_t n_routes, size_t n_sets,
+                              const void* x_dev, int x_bf16, size_t x_stride, float* out_dev, size_t iters, int mode,
+                              double* us_per_token) {
+    if (!c || !routes || !x_dev || !out_dev || !us_per_token || n_routes == 0 || n_sets == 0 || iters == 0 ||
+        n_routes > WH_MAX_EXPERTS || mode < 0 || mode > 1 || (x_stride & 15))
+        return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    std::vector<ExpertView> ev(n_sets * n_routes);
+    std::vector<float> wts(n_sets * n_routes);
+    for (size_t s = 0; s < n_sets; ++s) {
+        WH_TRY(routed_common(c, routes + s * n_routes, n_routes, &ev[s * n_routes], &wts[s * n_routes]));
+        const ExpertView* e = &ev[s * n_routes];
+        for (size_t i = 0; i < n_routes; ++i)
+            if (!expert_fast(e[i]) || e[i].w1->cols != e[0].w1->cols || e[i].w1->rows != e[0].w1->rows ||
+                e[i].w2->rows != e[0].w1->cols)
+                return WH_UNSUPPORTED;
+    }
+    const size_t hidden = ev[0].w1->cols;
+    MoeBufs bufs;
+    WH_TRY(moe_bufs_ctx(c, n_routes, 1, hidden, ev[0].w1->rows, &bufs));
+    auto enqueue = [&]() -> int {
+        for (size_t it = 0; it < iters; ++it) {
+            const size_t s = it % n_sets;
+            WH_TRY(moe_launch_fast(c, &ev[s * n_routes], &wts[s * n_routes], n_routes, false,
+                                   (const uint8_t*)x_dev + s * x_stride, x_bf16, 1, out_dev + s * hidden, 3, bufs,
+                                   true));
+        }
+        return WH_OK;
+    };
+    float ms = 0.0f;
+    if (mode == 0) {
+        WH_HIP(hipEventRecord(c->timer[0], c->stream));
+        WH_TRY(enqueue());
+        WH_HIP(hipEventRecord(c->timer[1], c->stream));
+        WH_HIP(hipEventSynchronize(c->timer[1]));
+        WH_HIP(hipEventElapsedTime(&ms, c->timer[0], c->timer[1]));
+    } else {
+        // the same launches captured once into a graph (kernel nodes only),
+        // replayed once untimed and once between the events
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        WH_HIP(hipStreamSynchronize(c->stream));
+        WH_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue();
+        const hipError_t ce = hipStreamEndCapture(c->stream, &graph);
+        if (rc != WH_OK || ce != hipSuccess) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return rc != WH_OK ? rc : hip_status(ce);
+        }
+        hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (e == hipSuccess) e = hipGraphLaunch(exec, c->stream);
+        if (e == hipSuccess) e = hipEventRecord(c->timer[0], c->stream);
+        if (e == hipSuccess) e = hipGraphLaunch(exec, c->stream);
+        if (e == hipSuccess) e = hipEventRecord(c->timer[1], c->stream);
+        if (e == hipSuccess) e = hipEventSynchronize(c->timer[1]);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, c->timer[0], c->timer[1]);
+        if (exec) (void)hipGraphExecDestroy(exec);
+        (void)hipGraphDestroy(graph);
+        WH_HIP(e);
+    }
+    *us_per_token = (double)ms * 1000.0 / (double)iters;
+    return read_status(c);
+}
+
 #ifdef WH_TIMELINE
 // Timeline of the last persistent token kernels (builds with -DWH_TIMELINE
-// only): which = 0 gate/up, 1 down; n <= 512 * 16 * 8 stamps.
+// only): which = 0 gate/up, 1 down; n <= 512 * 16 * WH_TL_POINTS stamps.
 int wh_debug_timeline(int which, uint64_t* out, size_t n) {
-    if (which < 0 || which > 1 || !out || n > 512 * 16 * 8) return WH_INVALID_ARGUMENT;
+    constexpr size_t kStamps = 512 * 16 * WH_TL_POINTS;
+    if (which < 0 || which > 1 || !out || n > kStamps) return WH_INVALID_ARGUMENT;
     WH_HIP(hipDeviceSynchronize());
-    WH_HIP(hipMemcpyFromSymbol(out, HIP_SYMBOL(wh_tl_buf), n * sizeof(uint64_t), (size_t)which * 512 * 16 * 8 * sizeof(uint64_t)));
+    WH_HIP(hipMemcpyFromSymbol(out, HIP_SYMBOL(wh_tl_buf), n * sizeof(uint64_t), (size_t)which * kStamps * sizeof(uint64_t)));
     return WH_OK;
 }
 #endif
 
 int wh_debug_eval(wh_ctx* c, int fn, const float* in, float* out, size_t n) {
-    if (!c || !in || !out || fn < 0 || fn > 6) return WH_INVALID_ARGUMENT;
-    if (fn == 3 && n % 4) return WH_INVALID_ARGUMENT;
+    if (!c || !in || !out || fn < 0 || fn > 8) return WH_INVALID_ARGUMENT;
+    if ((fn == 3 && n % 4) || (fn >= 7 && n % 64)) return WH_INVALID_ARGUMENT;
     if (n == 0) return WH_OK;
     std::lock_guard<std::mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
@@ -3107,6 +3209,12 @@ int wh_debug_eval(wh_ctx* c, int fn, const float* in, float* out, size_t n) {
     if (fn == 3)
         k_copy_f32x4<<<(unsigned)std::min<size_t>((n / 4 + 255) / 256, 8192), 256, 0, c->stream>>>(
             reinterpret_cast<const float4*>(c->x_in.p), reinterpret_cast<float4*>(c->y_out.p), (uint32_t)(n / 4));
+    else if (fn == 7)
+        k_debug_tok_quant<true><<<(unsigned)((n / 8 + 255) / 256), 256, 0, c->stream>>>(c->x_in.as<float>(),
+                                                                                    c->y_out.as<float>(), (uint32_t)n);
+    else if (fn == 8)
+        k_debug_tok_quant<false><<<(unsigned)((n / 8 + 255) / 256), 256, 0, c->stream>>>(c->x_in.as<float>(),
+                                                                                     c->y_out.as<float>(), (uint32_t)n);
     else if (fn >= 4)
         k_debug_eval_router<<<(unsigned)((n + 255) / 256), 256, 0, c->stream>>>(fn, c->x_in.as<float>(),
                                                                                c->y_out.as<float>(), (uint32_t)n);
