@@ -8,7 +8,10 @@ x ~ N(0,1) in bf16, SwiGLU then down then the ordered weighted sum.  A step
 is one token; each step routes a fresh token on one of `--layers` resident
 layers of 256 experts (round robin), so no step reuses weights that the
 previous ones left in the 256 MB Infinity Cache.  Inputs are resident in
-HBM before the timed region; value = algorithmic bytes / wall time.
+HBM before the timed region.  The K timed tokens are captured into one HIP
+graph and replayed by a single library call; value = algorithmic bytes per
+token / the device time per token between HIP events around that replay
+(the same tokens enqueued one Python call each are reported beside it).
 
 The headline runs the MFMA kernels (each matvec within
 1e-5 * ||w_row|| * ||x|| of the reference kernel); --exact runs the
@@ -45,7 +48,7 @@ TOKEN_BYTES = 6 * EXPERT_BYTES + 4096 * 2 + 4096 * 4   # + bf16 x + f32 y = 80,2
 GATEUP_BYTES = 6 * 2 * (4_194_304 + 262_144) + 4096 * 2 + 6 * 2048 * 4     # 53,534,720
 DOWN_BYTES = 6 * (4_194_304 + 262_144) + 6 * 2048 * 4 + 4096 * 4           # 26,804,224
 # The routed-expert kernels of each numerics mode (trace names).
-KERNELS = {False: ("k_moe_gateup_px<4096, 3>", "k_moe_down_px<3>"), True: ("k_moe_gateup<16, 4>", "k_moe_down<8, 4>")}
+KERNELS = {False: ("k_moe_gateup_tok<3, 4, true>", "k_moe_down_px<3>"), True: ("k_moe_gateup<16, 4>", "k_moe_down<8, 4>")}
 # HBM bytes per gate/up launch: rocprofv3 FETCH_SIZE and WRITE_SIZE KiB per
 # dispatch, scaled by what the same counters read for a 268,435,456-byte copy
 # (FETCH x2.00, WRITE x1.00); see profiles/.  None: not measured.
@@ -212,7 +215,10 @@ def read_floor(ctx, reps: int = 60):
 
 
 def fp8_dense(ctx, steps: int, warmup: int):
-    """4096x4096 FP8 GEMV (fp32 block scales) over 40 rotating copies (672 MB)."""
+    """4096x4096 FP8 GEMV (fp32 block scales) over 40 rotating copies (672
+    MB), in both numerics modes: the order-free kernel (exact numerics off,
+    within 1e-5 * ||w_row|| * ||x|| of the reference kernel) and the exact
+    kernel (the reference's summation order, bit-identical)."""
     import wohper_amd
     from wohper_amd import workloads as wl
 
@@ -225,30 +231,46 @@ def fp8_dense(ctx, steps: int, warmup: int):
     # one library call launches every timed GEMV, so the host's per-call
     # Python cost does not pace the device
     timed = ctx.gemv_descs([(handles[i % copies], 0, 4096, xd, yd) for i in range(steps)])
-    for i in range(warmup):
-        ctx.fp8_gemv_async(handles[i % copies], 0, 4096, xd, yd)
-    ctx.synchronize()
-    t0 = time.perf_counter()
-    ctx.timer_start()
-    ctx.fp8_gemv_batch_async(timed)
-    dev_us = ctx.timer_stop() / steps
-    ctx.synchronize()
-    el = time.perf_counter() - t0
-    us = el / steps * 1e6
-    gbs = FP8_BYTES / (us * 1e-6) / 1e9
+    res = {"workload": "fp8 e4m3 GEMV 4096x4096, fp32 128x128 block scales, bf16 x, batch 1",
+           "bytes": FP8_BYTES,
+           "note": "back-to-back launches from one wh_fp8_gemv_batch_async call over 40 rotating weight copies; "
+                   "wall clock and HIP events on the library stream"}
+    for exact, key in ((False, "order_free"), (True, "exact")):
+        ctx.set_exact_numerics(exact)
+        for i in range(warmup):
+            ctx.fp8_gemv_async(handles[i % copies], 0, 4096, xd, yd)
+        ctx.synchronize()
+        t0 = time.perf_counter()
+        ctx.timer_start()
+        ctx.fp8_gemv_batch_async(timed)
+        dev_us = ctx.timer_stop() / steps
+        ctx.synchronize()
+        us = (time.perf_counter() - t0) / steps * 1e6
+        gbs = FP8_BYTES / (us * 1e-6) / 1e9
+        res[key] = {"us_per_gemv": round(us, 3), "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                    "device_us_per_gemv": round(dev_us, 3), "device_GBps": round(FP8_BYTES / (dev_us * 1e-6) / 1e9, 1),
+                    "device_frac_of_hbm_peak": round(FP8_BYTES / (dev_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     ctx.device_free(xd)
     ctx.device_free(yd)
-    return {"workload": "fp8 e4m3 GEMV 4096x4096, fp32 128x128 block scales, bf16 x, batch 1",
-            "us_per_gemv": round(us, 3), "GBps": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "device_us_per_gemv": round(dev_us, 3), "device_GBps": round(FP8_BYTES / (dev_us * 1e-6) / 1e9, 1),
-            "note": "back-to-back launches from one wh_fp8_gemv_batch_async call over 40 rotating weight copies; "
-                    "wall clock and HIP events on the library stream"}
+    for h in handles:
+        ctx.release(h)
+    return res
 
 
 def fp8_decode_layer(ctx, steps: int):
     """Each FP8 projection of one decode layer on its own (wq_a, wq_b, wkv,
     wo_a as 8 row groups with their own inputs in one launch, wo_b; f32
-    128x128 block scales), back to back over 8 rotating weight copies."""
+    128x128 block scales), back to back over 8 rotating weight copies, in
+    both numerics modes."""
+    out = {}
+    for exact, key in ((False, "order_free"), (True, "exact")):
+        ctx.set_exact_numerics(exact)
+        out[key] = _fp8_decode_layer(ctx, steps)
+        out[key]["total_device_us"] = round(sum(v["device_us"] for v in out[key].values()), 2)
+    return out
+
+
+def _fp8_decode_layer(ctx, steps: int):
     from wohper_amd import workloads as wl
 
     res = {}
@@ -802,20 +824,27 @@ def main():
     for i in range(args.warmup):
         step(i)
     ctx.synchronize()
-    # the timed region: HIP events on the library stream (the stream every
-    # launch goes to) bracket exactly the timed steps, next to the host clock
+    # The timed region: the K timed tokens (token i on its own route list,
+    # input row and output row) captured once into a HIP graph of their
+    # gate/up and down launches and replayed by one library call, so no
+    # per-step Python call paces the device; HIP events on the library stream
+    # bracket exactly those K steps (the graph's second replay; the first is
+    # untimed).  The host clock around the same call is reported beside it.
     t0 = time.perf_counter()
+    launch_us = ctx.profile_token_pipeline(routes[args.warmup:total], x_dev + args.warmup * wl.HIDDEN * 2, True,
+                                           wl.HIDDEN * 2, out_dev + args.warmup * wl.HIDDEN * 4, args.steps, True)
+    call_s = time.perf_counter() - t0
+    ms_per_step = launch_us * 1e-3
+    value = TOKEN_BYTES / (launch_us * 1e-6) / 1e9
+    # the same steps enqueued one Python call per token (the entry point a
+    # caller uses per token), HIP events around them
     ctx.timer_start()
     for i in range(args.warmup, total):
         step(i)
-    dev_us = ctx.timer_stop()
+    py_us = ctx.timer_stop() / args.steps
     ctx.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed / args.steps * 1e3
-    value = args.steps * TOKEN_BYTES / elapsed / 1e9
-    launch_us = dev_us / args.steps  # k_moe_gateup + k_moe_down per step
-    log(f"routed FP4 MoE: {ms_per_step * 1e3:.2f} us/token wall, {value:.1f} GB/s; "
-        f"device {launch_us:.2f} us/token, {TOKEN_BYTES / (launch_us * 1e-6) / 1e9:.1f} GB/s")
+    log(f"routed FP4 MoE: {launch_us:.2f} us/token (graph of {args.steps} tokens), {value:.1f} GB/s; "
+        f"one Python call per token {py_us:.2f} us/token")
 
     # per-kernel launch durations: each stage launched back to back over the
     # timed steps' route lists, between HIP events on the library stream
@@ -830,7 +859,10 @@ def main():
              "MFMA (each matvec within 1e-5 * ||w_row|| * ||x|| of the reference kernel)",
              "kernels": {gu_name: {"us": round(gu_us, 3), "GBps": round(gu_gbs, 1), "bytes_per_launch": GATEUP_BYTES},
                          dn_name: {"us": round(dn_us, 3), "GBps": round(dn_gbs, 1), "bytes_per_launch": DOWN_BYTES},
-                         "token_device_us": round(launch_us, 3)}}
+                         "token_device_us": round(launch_us, 3)},
+             "timed_region": f"{args.steps} tokens replayed as one HIP graph (one library call, "
+                             f"{call_s * 1e3:.1f} ms host time for capture, untimed replay and timed replay)",
+             "token_us_one_python_call_per_token": round(py_us, 3)}
     # the other numerics mode's kernels on the same route lists
     ctx.set_exact_numerics(not args.exact)
     o_gu, o_dn = ctx.profile_routed(routes[args.warmup:args.warmup + min(args.steps, 64)], x_dev, True, out_dev,
@@ -842,8 +874,10 @@ def main():
     log(f"other numerics: {extra['other_numerics_kernels']}")
     if not args.no_fp8:
         extra["fp8_dense_gemv"] = fp8_dense(ctx, max(200, args.steps), 40)
+        ctx.set_exact_numerics(args.exact)
         log(f"fp8 dense: {extra['fp8_dense_gemv']}")
         extra["fp8_decode_layer"] = fp8_decode_layer(ctx, 200)
+        ctx.set_exact_numerics(args.exact)
         log(f"fp8 decode layer: {extra['fp8_decode_layer']}")
         extra["fp8_decode_layer_batch16"] = fp8_decode_layer_batch(ctx, 200)
         ctx.set_exact_numerics(args.exact)

@@ -355,7 +355,12 @@ int wh_fp8_shared_expert_async(wh_ctx* ctx, wh_tensor w1, wh_tensor w3, wh_tenso
  * matvec agrees with the reference kernel on the same input within
  * max|diff| <= 1e-5 * ||w_row||_2 * ||x||_2 (fp32 accumulation), while
  * act-quant, SwiGLU and the route-weighted sum stay bit-exact given the
- * matvec outputs.  No counterpart in the reference (it has one CPU kernel). */
+ * matvec outputs.  on = 0 also frees the order of the FP8 dequant GEMV
+ * (wh_fp8_gemv*, the shared expert, the multi-input GEMV below its MFMA
+ * threshold) on tensors of a multiple of 1024 columns whose codes avoid
+ * 0x7F / 0xFF, to the same bound; the router's FP8 gate keeps the reference
+ * order in both modes (its top-k selection must not move).  No counterpart
+ * in the reference (it has one CPU kernel). */
 int wh_set_exact_numerics(wh_ctx* ctx, int on);
 /* Test support, no counterpart in the reference: with capture on, the
  * routed-expert entry points also keep each expert's gate and up matvec
@@ -445,8 +450,8 @@ int wh_fp8_gemv_batch_async(wh_ctx* ctx, const wh_gemv_desc* descs, size_t n);
 
 /* Device-pointer variant of wh_fp8_gemv_multi (gemv_fp8_e4m3_ue8m0_rows_multi,
  * E/compute.rs:6384-6577): n f32 inputs at x_dev + i * x_stride, outputs at
- * y_dev + i * y_stride, each bit-identical to the single-input GEMV.  With
- * exact numerics off (wh_set_exact_numerics(ctx, 0)) and at least
+ * y_dev + i * y_stride, each bit-identical to the single-input GEMV in the
+ * same numerics mode.  With exact numerics off (wh_set_exact_numerics(ctx, 0)) and at least
  * wh_set_fp8_mfma_min inputs, tensors of a multiple of 256 columns in
  * 128-column scale groups, scale rows of a power of two >= 16 rows and
  * row_start % 16 == 0 run on bf16 MFMA instead: each weight byte is read once

@@ -141,16 +141,21 @@ def test_fp8_mfma_one_hot_exact(ctx, oracle, special):
 
 
 def test_fp8_mfma_threshold_keeps_exact_below(ctx, oracle):
-    """Below the MFMA threshold the multi-input GEMV stays bit-identical to
-    the reference kernel."""
+    """Below the MFMA threshold each input runs the single-input GEMV: the
+    order-free one (within tolerance) with exact numerics off, the reference
+    order (bit for bit) with them on."""
     rows, cols = 512, 2048
     case = wl.fp8_gemv_case(rows, cols, seed=2)
     t = ctx.store_fp8(case.w, rows, cols, case.scales, rows // 128, cols // 128, wohper_amd.SCALE_F32)
     xs = np.random.default_rng(8).standard_normal((3, cols)).astype(np.float32)
     ys = run_multi(ctx, t, xs, 0, rows, cols)
+    check(oracle, case.w, rows, cols, case.scales, xs, ys)
+    ctx.set_exact_numerics(True)
+    ys = run_multi(ctx, t, xs, 0, rows, cols)
     for i in range(3):
         want = oracle.fp8_gemv(case.w, rows, cols, case.scales, rows // 128, cols // 128, xs[i])
         assert np.array_equal(ys[i].view(np.uint32), want.view(np.uint32))
+    ctx.set_exact_numerics(False)
     ctx.set_fp8_mfma_min(2)
     try:
         ys = run_multi(ctx, t, xs, 0, rows, cols)

@@ -145,7 +145,19 @@ def test_router_ties_nan_and_uniform_fallback(ctx, oracle):
     assert np.all(got[1] == np.float32(1.5 / 4))
 
 
-def test_router_fp8_gate(ctx, oracle):
+@pytest.mark.parametrize("exact", [True, False])
+def test_router_fp8_gate(ctx, oracle, exact):
+    """An FP8 gate: ids and weights bit-exact in both numerics modes (the
+    gate GEMV keeps the reference's order even with exact numerics off: a
+    top-k has no tolerance)."""
+    ctx.set_exact_numerics(exact)
+    try:
+        _router_fp8_gate(ctx, oracle)
+    finally:
+        ctx.set_exact_numerics(True)
+
+
+def _router_fp8_gate(ctx, oracle):
     rows, cols = 256, 4096
     rng = np.random.default_rng(9)
     c = rng.integers(0, 254, (rows, cols))

@@ -26,6 +26,7 @@
 #include "moe_px.h"
 #include "moe_tok.h"
 #include "fp8_mm.h"
+#include "fp8_tol.h"
 #include "moe_bmx.h"
 #include "probe.h"
 #include "quant_block.h"
@@ -56,6 +57,7 @@ struct Tensor {
     int scale_fmt = WH_SCALE_UE8M0;
     bool fast = false;     // resident lane layout (else original row-major)
     bool special = false;  // FP8 codes 0x7F/0xFF present
+    bool zero_scale = false;  // FP4: some UE8M0 scale byte is 0 (the MFMA kernels would read it as 2^-127)
     size_t bytes = 0;
     size_t w_alloc = 0, s_alloc = 0;  // arena bytes behind w and s
 };
@@ -231,6 +233,7 @@ struct LayerTable {
     uint32_t n = 0;    // ids < n
     bool valid = false;
     bool fast = false;  // every resident expert has one fast shape
+    bool zero_scale = false;  // some resident expert has a UE8M0 scale byte 0
     size_t hidden = 0, inter = 0;
 };
 
@@ -466,10 +469,12 @@ bool fp8_split_k(const Tensor& t) {
 
 // x_group_rows / x_group_stride: row groups with their own input (split-K
 // path only; see wh_fp8_args).
+// order_free: with exact numerics off the order-free kernel may run (the
+// router's gate GEMV passes false: its top-k needs the reference's logits).
 int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x, float* y,
                size_t n_batch, size_t x_stride, size_t y_stride, size_t x_group_rows = 0,
                size_t x_group_stride = 0, const Tensor* t2 = nullptr, size_t r0_2 = 0, size_t r1_2 = 0,
-               float* y2 = nullptr) {
+               float* y2 = nullptr, bool order_free = true) {
     wh_fp8_args a;
     std::memset(&a, 0, sizeof a);
     a.blocks1 = UINT32_MAX;
@@ -501,6 +506,46 @@ int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x,
         a.row_group_shift2 = log2_of(t2->rows / t2->scale_rows);
         a.row_start2 = (uint32_t)r0_2;
         a.row_end2 = (uint32_t)r1_2;
+    }
+    // exact numerics off: the order-free kernel (fp8_tol.h) for lane-layout
+    // tensors without the reference's +-480 codes, widths of 1, 2, 4 or 8
+    // slices of 1024 columns
+    const size_t slices = t.cols / 1024;
+    const size_t tol_rows = (r1 - r0) + (t2 ? r1_2 - r0_2 : 0);
+    size_t kr = tol_rows >= 4096 ? 8 : (tol_rows >= 2048 ? 4 : 2);
+    if (slices == 1 && kr < 4) kr = 4;
+    const bool tol = order_free && !c->exact && t.fast && !t.special && t.cols % 1024 == 0 &&
+                     (slices == 1 || slices == 2 || slices == 4 || slices == 8) &&
+                     (!t2 || (t2->fast && !t2->special && t2->cols == t.cols)) &&
+                     (!x_group_rows || x_group_rows % kr == 0);  // a block stays inside one input's rows
+    if (tol) {
+        const size_t b1 = (r1 - r0 + kr - 1) / kr;
+        if (t2) a.blocks1 = (uint32_t)b1;
+        dim3 grid((unsigned)(b1 + (t2 ? (r1_2 - r0_2 + kr - 1) / kr : 0)), (unsigned)n_batch);
+#define WH_TOL(R, S)                                                                 \
+    do {                                                                             \
+        if (u8) k_fp8_gemv_tol<R, S, true><<<grid, 256, 0, c->stream>>>(a);          \
+        else k_fp8_gemv_tol<R, S, false><<<grid, 256, 0, c->stream>>>(a);            \
+    } while (0)
+#define WH_TOL_S(R)                          \
+    do {                                     \
+        if (slices == 2) WH_TOL(R, 2);       \
+        else if (slices == 4) WH_TOL(R, 4);  \
+        else WH_TOL(R, 8);                   \
+    } while (0)
+        if (kr == 8) {
+            if (slices == 1) WH_TOL(8, 1);
+            else WH_TOL_S(8);
+        } else if (kr == 4) {
+            if (slices == 1) WH_TOL(4, 1);
+            else WH_TOL_S(4);
+        } else {
+            WH_TOL_S(2);
+        }
+#undef WH_TOL_S
+#undef WH_TOL
+        WH_HIP(hipGetLastError());
+        return WH_OK;
     }
     if (fp8_split_k(t)) {
         const size_t blocks = (r1 - r0 + WH_FP8_SK_ROWS - 1) / WH_FP8_SK_ROWS +
@@ -728,6 +773,11 @@ int resolve_expert(wh_ctx* c, uint32_t layer, uint32_t expert, ExpertView* v) {
     return WH_OK;
 }
 
+// A UE8M0 scale byte 0 decodes to 0.0 (E/deepseek_v4.rs:166-172); the
+// block-scaled MFMA reads it as 2^-127, so experts that have one run on the
+// exact kernels.
+bool expert_zero_scale(const ExpertView& v) { return v.w1->zero_scale || v.w3->zero_scale || v.w2->zero_scale; }
+
 bool expert_fast(const ExpertView& v) {
     return v.w1->fast && v.w3->fast && v.w2->fast && v.w1->cols % 256 == 0 && v.w1->rows % 256 == 0 &&
            wh_moe_wg_lds(v.w1->cols) <= g_max_lds && wh_moe_wg_lds(v.w1->rows) <= g_max_lds;
@@ -826,7 +876,8 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
     a.gu = bufs.gu;
     if (record)
         c->tok_last_n = n, c->tok_last_tokens = n_tokens, c->tok_last_hidden = hidden, c->tok_last_inter = inter;
-    const bool sk = moe_mfma(c, hidden, inter);
+    bool sk = moe_mfma(c, hidden, inter);
+    for (size_t i = 0; i < n && sk; ++i) sk = !expert_zero_scale(ev[i]);
     // the LDS-DMA kernels (moe_tok.h): hidden 4096, inter 2048, up to 8 experts
     const bool tk_shape = sk && hidden == 4096 && inter == 2048 && n <= 8;
     const bool tk = tk_shape && (c->token_kernels & 1), tkd = tk_shape && (c->token_kernels & 2);
@@ -1065,6 +1116,7 @@ int layer_table(wh_ctx* c, uint32_t layer, LayerTable** out) {
     std::vector<wh_expert_ptrs> host(n);
     std::memset(host.data(), 0, n * sizeof(wh_expert_ptrs));
     bool fast = n > 0 && n < WH_BATCH_MAX_TABLE;  // one id stays free for the shared expert
+    bool zero_scale = false;
     size_t hidden = 0, inter = 0;
     for (auto it = lo; it != hi; ++it) {
         ExpertView v;
@@ -1074,6 +1126,7 @@ int layer_table(wh_ctx* c, uint32_t layer, LayerTable** out) {
             inter = v.w1->rows;
         }
         fast = fast && expert_fast(v) && v.w1->cols == hidden && v.w1->rows == inter && v.w2->rows == hidden;
+        zero_scale = zero_scale || expert_zero_scale(v);
         wh_expert_ptrs& p = host[it->first.second];
         p.w1 = v.w1->w;
         p.s1 = (const uint8_t*)v.w1->s;
@@ -1094,6 +1147,7 @@ int layer_table(wh_ctx* c, uint32_t layer, LayerTable** out) {
     if (n) WH_HIP(hipMemcpy(t.dev, host.data(), n * sizeof(wh_expert_ptrs), hipMemcpyHostToDevice));
     t.n = n;
     t.fast = fast;
+    t.zero_scale = zero_scale;
     t.hidden = hidden;
     t.inter = inter;
     t.valid = true;
@@ -1185,7 +1239,10 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
     WH_TRY(persistent_grid(kd, lds_d, &grid_d));
     // With exact numerics off the MFMA experts run in k_moe_batch_mx (one
     // 512-thread workgroup per CU) and the other kernels keep the exact ones.
-    const bool mx = !c->exact && c->moe_mfma_min && inter == 2048 && (hidden == 4096 || hidden == 2048) &&
+    // a UE8M0 scale byte 0 anywhere in the call's experts: every expert on
+    // the exact items (the MFMA would read the byte as 2^-127)
+    const bool zero_scale = t.zero_scale || (shared && expert_zero_scale(*shared));
+    const bool mx = !c->exact && !zero_scale && c->moe_mfma_min && inter == 2048 && (hidden == 4096 || hidden == 2048) &&
                     wh_bmx_lds(hidden) <= g_max_lds;
     const void* kmg = hidden == 4096 ? (const void*)k_moe_batch_mx<4096, true> : (const void*)k_moe_batch_mx<2048, true>;
     const void* kmd = (const void*)k_moe_batch_mx<2048, false>;
@@ -1235,7 +1292,7 @@ int moe_batch_fast(wh_ctx* c, const LayerTable& t, const uint32_t* ids, const fl
         a.hq8 = b.hq8;
         a.hs8 = b.hs8;
         a.y = b.y;
-        a.mfma_min = c->exact ? 0u : c->moe_mfma_min;  // exact numerics: every expert on the exact items
+        a.mfma_min = (c->exact || zero_scale) ? 0u : c->moe_mfma_min;  // exact numerics: every expert on the exact items
         a.mfma_external = mx ? 1u : 0u;
         // threshold 1: every used expert is an MFMA expert, so the exact-item
         // kernels would only run after an inf or NaN input; k_moe_batch_mx
@@ -1401,6 +1458,7 @@ int store_fp4_upload(wh_ctx* c, const uint8_t* packed, size_t packed_len, const 
     t.fast = (cols / scale_cols == 32) && cols % 256 == 0 && wh_fp4_wg_lds(cols) <= g_max_lds &&
              rows <= UINT32_MAX && cols <= UINT32_MAX;
     t.bytes = rows * row_bytes + rows * scale_cols;
+    t.zero_scale = std::memchr(scales, 0, rows * scale_cols) != nullptr;
     WH_TRY(alloc_tensor(c, t, rows * row_bytes, rows * scale_cols));
     if (t.fast) {
         const size_t piece = size_t(64) << 20;
@@ -1615,7 +1673,7 @@ int router_launch(wh_ctx* c, const Router& rt, wh_router_sel sa, const float* x,
     } else {
         Tensor* t = find_tensor(c, rt.fp8);
         if (!t) return WH_NOT_RESIDENT;
-        WH_TRY(launch_fp8(c, *t, 0, t->rows, x, logits, 1, 0, 0));
+        WH_TRY(launch_fp8(c, *t, 0, t->rows, x, logits, 1, 0, 0, 0, 0, nullptr, 0, 0, nullptr, false));
     }
     k_router_select<<<1, 256, 0, c->stream>>>(sa);
     WH_HIP(hipGetLastError());
@@ -1858,6 +1916,7 @@ int wh_store_expert_synthetic(wh_ctx* c, uint32_t layer, uint32_t expert, size_t
         t.scale_rows = t.rows;
         t.scale_cols = t.cols / 32;
         t.fast = true;
+        t.zero_scale = slo == 0;  // bytes uniform in [slo, shi]
         t.bytes = t.rows * t.cols / 2 + t.rows * t.scale_cols;
         const int st = alloc_tensor(c, t, t.rows * t.cols / 2, t.rows * t.scale_cols);
         if (st != WH_OK) {
