@@ -475,7 +475,8 @@ def fp8_decode_layer_batch(ctx, steps: int, batch: int = 16):
     return res
 
 
-def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps: int = 0, exact: bool = False):
+def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps: int = 0, exact: bool = False,
+                 graph: bool = True):
     """Full-depth synthetic stack at batch 1: per layer the FP8 projections
     of one decode layer (wq_a, wq_b, wkv, wo_a in 8 row groups, wo_b; f32
     128x128 block scales) and the MoE FFN (1 shared + top-6 of 256 routed
@@ -537,13 +538,31 @@ def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps:
     for s_ in range(warmup):
         step(s_)
     ctx.synchronize()
+    # host loop: two library calls per layer
     t1 = time.perf_counter()
     ctx.timer_start()
     for s_ in range(warmup, total):
         step(s_)
+    loop_us = ctx.timer_stop()
+    ctx.synchronize()
+    loop_wall = time.perf_counter() - t1
+    # the same steps captured as one HIP graph each (every step keeps its own
+    # routes), replayed once untimed, then timed back to back
+    graphs = [ctx.graph_capture(lambda s_=s_: step(s_)) for s_ in range(warmup, total)] if graph else []
+    for g in graphs:
+        ctx.graph_launch(g)
+    ctx.synchronize()
+    t1 = time.perf_counter()
+    ctx.timer_start()
+    for g in graphs:
+        ctx.graph_launch(g)
     dev_us = ctx.timer_stop()
     ctx.synchronize()
     wall = time.perf_counter() - t1
+    for g in graphs:
+        ctx.graph_release(g)
+    if not graph:
+        dev_us, wall = loop_us, loop_wall
     vec_bytes = (4096 + 1024 + 1024 + 32768 + 4096 + 512 + 8 * (4096 + 1024) + 8192 + 4096) * 4 + 4096 * 2 + 4096 * 4
     layer_bytes = wl.DECODE_LAYER_FP8_BYTES + 7 * wl.FP4_EXPERT_BYTES + vec_bytes
     step_us = dev_us / steps
@@ -551,8 +570,12 @@ def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps:
                        "wkv 512x4096, wo_a 8192x4096 in 8 groups, wo_b 4096x8192; f32 block scales) + MoE "
                        "(1 shared + top-6 of 256 routed FP4 experts) per layer",
            "resident_GB": round(dev_bytes / 1e9, 2), "bytes_per_layer": layer_bytes,
+           "timed_region": f"each step one HIP graph of its {n_layers} layers' launches (2 library calls per layer "
+                           "captured), graphs replayed back to back between HIP events" if graph else
+                           "host loop, 2 library calls per layer, between HIP events",
            "step_us": round(step_us, 1), "wall_step_us": round(wall / steps * 1e6, 1),
            "layer_us": round(step_us / n_layers, 2),
+           "host_loop": {"step_us": round(loop_us / steps, 1), "wall_step_us": round(loop_wall / steps * 1e6, 1)},
            "GBps": round(layer_bytes * n_layers / (step_us * 1e-6) / 1e9, 1)}
     res["frac_of_hbm_peak"] = round(res["GBps"] / HBM_PEAK_GBS, 4)
     for k in list(dev.values()) + [y, moe_x, moe_out]:
@@ -768,6 +791,9 @@ def main():
     ap.add_argument("--timeline", type=str, default="",
                     help="only print the per-wave timelines of the expert kernels from this measuring build "
                          "(python -m wohper_amd.build --timeline PATH)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time the headline and the stack as host loops of launches instead of HIP graph replays "
+                         "(for kernel-trace profiler runs, which do not follow graph launches here)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy 5 times (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -832,7 +858,8 @@ def main():
     # untimed).  The host clock around the same call is reported beside it.
     t0 = time.perf_counter()
     launch_us = ctx.profile_token_pipeline(routes[args.warmup:total], x_dev + args.warmup * wl.HIDDEN * 2, True,
-                                           wl.HIDDEN * 2, out_dev + args.warmup * wl.HIDDEN * 4, args.steps, True)
+                                           wl.HIDDEN * 2, out_dev + args.warmup * wl.HIDDEN * 4, args.steps,
+                                           not args.no_graph)
     call_s = time.perf_counter() - t0
     ms_per_step = launch_us * 1e-3
     value = TOKEN_BYTES / (launch_us * 1e-6) / 1e9
@@ -860,8 +887,10 @@ def main():
              "kernels": {gu_name: {"us": round(gu_us, 3), "GBps": round(gu_gbs, 1), "bytes_per_launch": GATEUP_BYTES},
                          dn_name: {"us": round(dn_us, 3), "GBps": round(dn_gbs, 1), "bytes_per_launch": DOWN_BYTES},
                          "token_device_us": round(launch_us, 3)},
-             "timed_region": f"{args.steps} tokens replayed as one HIP graph (one library call, "
-                             f"{call_s * 1e3:.1f} ms host time for capture, untimed replay and timed replay)",
+             "timed_region": (f"{args.steps} tokens replayed as one HIP graph (one library call, "
+                              f"{call_s * 1e3:.1f} ms host time for capture, untimed replay and timed replay)")
+                             if not args.no_graph else
+                             f"{args.steps} tokens enqueued by one library call as a host loop of launches",
              "token_us_one_python_call_per_token": round(py_us, 3)}
     # the other numerics mode's kernels on the same route lists
     ctx.set_exact_numerics(not args.exact)
@@ -902,7 +931,7 @@ def main():
         ctx.close()
         ctx = None
         extra["decode_stack"] = decode_stack(args.stack_layers, args.stack_steps, 3, seed, args.stack_batch_steps,
-                                             args.exact)
+                                             args.exact, not args.no_graph)
         log(f"decode stack: {extra['decode_stack']}")
 
     line = {

@@ -216,6 +216,10 @@ extern "C" {
     pub fn wh_fp8_gemv_async(ctx: *mut WhCtx, w: WhTensor, row_start: usize, row_end: usize,
                              x_dev: *const f32, y_dev: *mut f32) -> c_int;
     pub fn wh_stream_status(ctx: *mut WhCtx) -> c_int;
+    pub fn wh_graph_begin(ctx: *mut WhCtx) -> c_int;
+    pub fn wh_graph_end(ctx: *mut WhCtx, out_: *mut u64) -> c_int;
+    pub fn wh_graph_launch(ctx: *mut WhCtx, graph: u64) -> c_int;
+    pub fn wh_graph_release(ctx: *mut WhCtx, graph: u64) -> c_int;
     pub fn wh_device_alloc(ctx: *mut WhCtx, bytes: usize, out_: *mut *mut c_void) -> c_int;
     pub fn wh_device_free(ctx: *mut WhCtx, ptr: *mut c_void) -> c_int;
     pub fn wh_memcpy(ctx: *mut WhCtx, dst: *mut c_void, src: *const c_void, bytes: usize, kind: c_int) -> c_int;

@@ -497,6 +497,28 @@ int wh_fp8_gemv_async(wh_ctx* ctx, wh_tensor w, size_t row_start, size_t row_end
 /* Deferred status of *_async calls (same as wh_synchronize). */
 int wh_stream_status(wh_ctx* ctx);
 
+/* Captured launch sequences, no counterpart in the reference (its decode step
+ * runs on the CPU).  wh_graph_begin starts capturing the context stream: the
+ * *_async calls the same thread makes until wh_graph_end are recorded, not
+ * run, and wh_graph_end returns them as one HIP graph that wh_graph_launch
+ * enqueues on the context stream (any number of times; failures surface in
+ * wh_stream_status like those of the calls themselves).  A graph replays the
+ * device addresses and host arguments it captured: inputs and outputs at the
+ * same addresses, the same route lists, and the tensors and experts it reads
+ * resident and unchanged until wh_graph_release.  Run the captured calls
+ * once before capturing: a call that has to grow an internal buffer, or that
+ * synchronizes (every call without _async, stores, releases), fails during
+ * capture and wh_graph_end then returns an error (the context stays usable:
+ * captures run on a stream of their own, which wh_stream returns meanwhile).
+ * Buffers that grow after a capture are kept for the graphs until the last of
+ * them is released.  Only the capturing thread may use the context between
+ * begin and end. */
+typedef uint64_t wh_graph;
+int wh_graph_begin(wh_ctx* ctx);
+int wh_graph_end(wh_ctx* ctx, wh_graph* out);
+int wh_graph_launch(wh_ctx* ctx, wh_graph graph);
+int wh_graph_release(wh_ctx* ctx, wh_graph graph);
+
 /* Device buffers for the *_async entry points (the engine's resident
  * hidden-state buffers).  kind: 0 host->device, 1 device->host,
  * 2 device->device; wh_memcpy is ordered on the context stream and returns

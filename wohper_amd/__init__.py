@@ -91,6 +91,7 @@ EXPORTED = (
     "wh_rope_inv_freqs", "wh_deepseek_rope_for_layer", "wh_rms_norm_async", "wh_rope_async",
     "wh_act_quant_dequant_async", "wh_window_attention_async", "wh_mla_attention_decode_async",
     "wh_hc_split_sinkhorn_async", "wh_hc_pre_async", "wh_hc_post_async",
+    "wh_graph_begin", "wh_graph_end", "wh_graph_launch", "wh_graph_release",
 )
 
 ROUTER_RAW_LOGITS = 0
@@ -195,6 +196,10 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_routed_experts_async": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, vp, c.c_int, sz, vp]),
         "wh_fp8_gemv_async": (c.c_int, [vp, c.c_uint64, sz, sz, vp, vp]),
         "wh_stream_status": (c.c_int, [vp]),
+        "wh_graph_begin": (c.c_int, [vp]),
+        "wh_graph_end": (c.c_int, [vp, c.POINTER(c.c_uint64)]),
+        "wh_graph_launch": (c.c_int, [vp, c.c_uint64]),
+        "wh_graph_release": (c.c_int, [vp, c.c_uint64]),
         "wh_debug_eval": (c.c_int, [vp, c.c_int, f32p, f32p, sz]),
         "wh_device_alloc": (c.c_int, [vp, sz, c.POINTER(vp)]),
         "wh_device_free": (c.c_int, [vp, vp]),
@@ -318,6 +323,36 @@ class Context:
 
     def synchronize(self):
         _check(self.lib.wh_synchronize(self._h), "deferred kernel status")
+
+    # ------------------------------------------------------------- graphs
+    def graph_begin(self):
+        """Starts recording this thread's *_async calls into a HIP graph."""
+        _check(self.lib.wh_graph_begin(self._h), "graph_begin")
+
+    def graph_end(self) -> int:
+        """Ends the recording; returns the graph handle."""
+        out = ctypes.c_uint64()
+        _check(self.lib.wh_graph_end(self._h, ctypes.byref(out)), "graph_end")
+        return out.value
+
+    def graph_capture(self, fn) -> int:
+        """Records fn() into a graph; if fn raises, the capture is ended and
+        dropped before the exception propagates."""
+        self.graph_begin()
+        try:
+            fn()
+        except BaseException:
+            out = ctypes.c_uint64()
+            if self.lib.wh_graph_end(self._h, ctypes.byref(out)) == 0:
+                self.lib.wh_graph_release(self._h, out.value)
+            raise
+        return self.graph_end()
+
+    def graph_launch(self, graph: int):
+        _check(self.lib.wh_graph_launch(self._h, graph), "graph_launch")
+
+    def graph_release(self, graph: int):
+        _check(self.lib.wh_graph_release(self._h, graph), "graph_release")
 
     # ------------------------------------------------------------- store
     def store_fp8(self, weight, rows: int, cols: int, scales, scale_rows: int, scale_cols: int,

@@ -4,8 +4,8 @@
 // AVX2 kernel.  The exact kernel (k_fp8_gemv_sk) reproduces the reference's
 // per-lane FMA chain and hands every row's partial sums to one wave for the
 // ordered scale FMAs; this one reads like the HBM read-floor kernel instead:
-// small workgroups, every weight load of a thread issued before any
-// arithmetic, no LDS staging of x and no ordered hand-off.
+// every load of a thread issued before any arithmetic, no ordered hand-off,
+// cross-lane sums on the DPP / permlane-swap paths rather than through LDS.
 //
 // Resident layout (fp8_permute_row): in each 128-col group, 16-byte chunk l
 // holds the columns l + 16 j (bytes 0..7) and l + 8 + 16 j (bytes 8..15),
@@ -18,18 +18,74 @@
 #pragma once
 #include "kernels.h"
 
-// Grid (blocks of kR rows [+ the second tensor's blocks], n_batch), 256
-// threads.  Work items are (row, 1024-col slice) pairs, kS slices a row;
-// wave w runs pairs w, w + 4, ... of the block's kR * kS (a multiple of 4),
-// so a wave keeps one slice when kS <= 4 and two when kS = 8.
-template <int kR, int kS, bool kScaleU8>
-__global__ void __launch_bounds__(256) k_fp8_gemv_tol(wh_fp8_args a) {
-    static_assert((kR * kS) % 4 == 0 && (kS == 1 || kS == 2 || kS == 4 || kS == 8), "pairs per wave");
-    constexpr int kP = kR * kS / 4;           // pairs per wave
-    constexpr int kX = kS == 8 ? 2 : 1;        // x slices per wave
+template <int kCtrl>
+__device__ __forceinline__ float wh_dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
+// One halving step of a wave sum over lane bit kB (32, 16, 8, 4, 2, 1):
+// every lane holds kN partial sums v[0..kN); lanes with bit kB clear keep
+// sums [0, kN/2), the others [kN/2, kN), each adding the copy of a partner
+// lane with the same higher bits and the opposite bit kB.  kN = 1 adds the
+// partner's single value.  Partners: v_permlane32_swap (lanes L <-> L ^ 32),
+// v_permlane16_swap (L <-> L ^ 16), DPP row_ror:8 (L ^ 8), row_half_mirror
+// (L <-> L ^ 7 inside 8 lanes: bit 2 flips), quad_perm (L ^ 2, L ^ 1).
+template <int kB, int kN, int kCap>
+__device__ __forceinline__ void wh_wave_halve(float (&v)[kCap], uint32_t L) {
+    if constexpr (kB == 32 || kB == 16) {
+        // the swap exchanges the upper half of its first operand's pairs of
+        // lanes with the lower half of its second: lanes with bit kB clear
+        // then hold (own A, partner A), the others (partner B, own B)
+#pragma unroll
+        for (int p = 0; p < (kN > 1 ? kN / 2 : 1); ++p) {
+            const float A = v[p], B = kN > 1 ? v[p + kN / 2] : v[p];
+            const auto r = kB == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(A), __float_as_uint(B), false, false)
+                                    : __builtin_amdgcn_permlane16_swap(__float_as_uint(A), __float_as_uint(B), false, false);
+            v[p] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+    } else {
+        constexpr int kCtrl = kB == 8 ? 0x128 : kB == 4 ? 0x141 : kB == 2 ? 0x4E : 0xB1;
+        const bool up = (L & kB) != 0;
+#pragma unroll
+        for (int p = 0; p < (kN > 1 ? kN / 2 : 1); ++p) {
+            if constexpr (kN > 1) {
+                const float A = v[p], B = v[p + kN / 2];
+                v[p] = (up ? B : A) + wh_dpp_f<kCtrl>(up ? A : B);
+            } else {
+                v[p] = v[p] + wh_dpp_f<kCtrl>(v[p]);
+            }
+        }
+    }
+}
+
+// Sums kP values per lane over the wave: afterwards sum p sits in the lanes
+// L with L % (64 / kP) == 0, p = L / (64 / kP).
+template <int kP>
+__device__ __forceinline__ void wh_wave_sums(float (&v)[kP], uint32_t L) {
+    wh_wave_halve<32, (kP >= 2 ? kP : 1)>(v, L);
+    wh_wave_halve<16, (kP >= 4 ? kP / 2 : 1)>(v, L);
+    wh_wave_halve<8, (kP >= 8 ? kP / 4 : 1)>(v, L);
+    wh_wave_halve<4, (kP >= 16 ? kP / 8 : 1)>(v, L);
+    wh_wave_halve<2, (kP >= 32 ? kP / 16 : 1)>(v, L);
+    wh_wave_halve<1, (kP >= 64 ? kP / 32 : 1)>(v, L);
+}
+
+// Grid (blocks [+ the second tensor's blocks], n_batch), 64 kW threads.
+// Wave w takes the 1024-col slice w % kS of kP rows: rows row0 + w / kS +
+// (kW / kS) p, p < kP, so a block covers kR = kP kW / kS rows and every wave
+// reuses its 16 x values kP times.  kOneSR: every block's rows lie in one
+// scale row (the host checks rows per scale row % kR == 0 and row starts %
+// kR == 0), so a lane loads one scale for all its pairs.
+template <int kW, int kS, int kP, bool kScaleU8, bool kOneSR>
+__global__ void __launch_bounds__(64 * kW) k_fp8_gemv_tol(wh_fp8_args a) {
+    static_assert(kW % kS == 0 && (kS == 1 || kS == 2 || kS == 4 || kS == 8), "slices per block");
+    static_assert(kP == 1 || kP == 2 || kP == 4 || kP == 8 || kP == 16, "pairs per wave");
+    constexpr int kRw = kW / kS;  // waves per slice
+    constexpr int kR = kP * kRw;  // rows per block
     __shared__ float red[kR][kS];
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), L = threadIdx.x & 63;
     const uint32_t gi = L >> 3, l = L & 7;
+    const uint32_t sl = wave % kS, rw = wave / kS;
     // which tensor: blocks from blocks1 on run the second one
     const bool two = blockIdx.x >= a.blocks1;
     const uint8_t* w = two ? a.w2 : a.w;
@@ -41,38 +97,39 @@ __global__ void __launch_bounds__(256) k_fp8_gemv_tol(wh_fp8_args a) {
     const uint32_t blk = two ? blockIdx.x - a.blocks1 : blockIdx.x;
     const uint32_t row0 = r_lo + blk * kR;
     const uint32_t cols = a.cols;
+    const uint32_t col = sl * 1024 + gi * 128;
     // this block's input (row groups with their own input share one block)
     const uint32_t grp = a.x_group_shift < 32 ? (row0 - a.row_start) >> a.x_group_shift : 0u;
-    const float* x = a.x + (size_t)blockIdx.y * a.x_stride + (size_t)grp * a.x_group_stride;
+    const float* xs = a.x + (size_t)blockIdx.y * a.x_stride + (size_t)grp * a.x_group_stride + col + l;
+    // x first: the first pair's arithmetic waits for x and its own weights
+    // only
+    float xa[8], xb[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        xa[j] = xs[16 * j];
+        xb[j] = xs[16 * j + 8];
+    }
     // weight chunks of the wave's pairs (rows past r_hi repeat the last row;
     // their sums are not stored)
     uint4 wv[kP];
-    float s[kP];
 #pragma unroll
     for (int p = 0; p < kP; ++p) {
-        const uint32_t item = wave + 4 * p, r = item / kS, sl = item % kS;
-        uint32_t row = row0 + r;
+        uint32_t row = row0 + rw + kRw * p;
         row = row < r_hi ? row : r_hi - 1;
-        const uint32_t col = sl * 1024 + gi * 128;
         wv[p] = *(const uint4*)(w + (size_t)row * cols + col + 16 * l);
+    }
+    constexpr int kSc = kOneSR ? 1 : kP;
+    float s[kSc];
+#pragma unroll
+    for (int p = 0; p < kSc; ++p) {
+        uint32_t row = row0 + rw + kRw * p;
+        row = row < r_hi ? row : r_hi - 1;
         s[p] = wh_fp8_scale<false, kScaleU8>(sc, (row >> rg_shift) * scale_cols + (col >> 7));
     }
-    float xa[kX][8], xb[kX][8];
-#pragma unroll
-    for (int k = 0; k < kX; ++k) {
-        const uint32_t sl = (wave + 4 * k) % kS;
-        const float* xs = x + sl * 1024 + gi * 128 + l;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            xa[k][j] = xs[16 * j];
-            xb[k][j] = xs[16 * j + 8];
-        }
-    }
     __builtin_amdgcn_sched_barrier(0);  // every load above is issued before any arithmetic
-    float acc[kP];
+    float v[kP];
 #pragma unroll
     for (int p = 0; p < kP; ++p) {
-        const int k = kX == 2 ? (p & 1) : 0;  // pairs alternate between the two slices when kS = 8
         const uint32_t d[4] = {wv[p].x, wv[p].y, wv[p].z, wv[p].w};
         float g = 0.0f;
 #pragma unroll
@@ -83,59 +140,39 @@ __global__ void __launch_bounds__(256) k_fp8_gemv_tol(wh_fp8_args a) {
             const auto a1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[q], true);
             const auto b0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[2 + q], false);
             const auto b1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)d[2 + q], true);
-            g = __builtin_fmaf(a0[0], xa[k][4 * q], g);
-            g = __builtin_fmaf(a0[1], xa[k][4 * q + 1], g);
-            g = __builtin_fmaf(a1[0], xa[k][4 * q + 2], g);
-            g = __builtin_fmaf(a1[1], xa[k][4 * q + 3], g);
-            g = __builtin_fmaf(b0[0], xb[k][4 * q], g);
-            g = __builtin_fmaf(b0[1], xb[k][4 * q + 1], g);
-            g = __builtin_fmaf(b1[0], xb[k][4 * q + 2], g);
-            g = __builtin_fmaf(b1[1], xb[k][4 * q + 3], g);
+            g = __builtin_fmaf(a0[0], xa[4 * q], g);
+            g = __builtin_fmaf(a0[1], xa[4 * q + 1], g);
+            g = __builtin_fmaf(a1[0], xa[4 * q + 2], g);
+            g = __builtin_fmaf(a1[1], xa[4 * q + 3], g);
+            g = __builtin_fmaf(b0[0], xb[4 * q], g);
+            g = __builtin_fmaf(b0[1], xb[4 * q + 1], g);
+            g = __builtin_fmaf(b1[0], xb[4 * q + 2], g);
+            g = __builtin_fmaf(b1[1], xb[4 * q + 3], g);
         }
-        acc[p] = g * s[p];
+        v[p] = g * s[kOneSR ? 0 : p];
     }
-    // sum each pair over the wave's 64 lanes: halving exchanges while there
-    // are several sums per lane, then a tree on the last one
-    float v[kP];
+    wh_wave_sums<kP>(v, L);
+    const bool holder = (L & ((64 / kP) - 1)) == 0;
+    const uint32_t p = L / (64 / kP);
+    const uint32_t r = rw + kRw * p;  // the block row of sum p
+    if constexpr (kS == 1) {
+        const uint32_t row = row0 + r;
+        if (holder && row < r_hi) {
+            if (!(fabsf(v[0]) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
+            yb[(size_t)blockIdx.y * a.y_stride + (row - r_lo)] = v[0];
+        }
+    } else {
+        if (holder) red[r][sl] = v[0];
+        __syncthreads();
+        if (threadIdx.x < kR) {
+            const uint32_t rr = threadIdx.x, row = row0 + rr;
+            float y = red[rr][0];
 #pragma unroll
-    for (int p = 0; p < kP; ++p) v[p] = acc[p];
-    int n = kP, stride = 32;
-#pragma unroll
-    for (int step = 0; step < 6; ++step) {
-        if (n > 1) {
-            // lanes with bit `stride` clear keep the first half of the sums,
-            // the others the second half; each adds its partner's copy
-            const bool up = (L & stride) != 0;
-#pragma unroll
-            for (int p = 0; p < kP / 2; ++p) {
-                if (p < n / 2) {
-                    const float send = up ? v[p] : v[p + n / 2];
-                    const float keep = up ? v[p + n / 2] : v[p];
-                    v[p] = keep + __shfl_xor(send, stride, 64);
-                }
+            for (int k = 1; k < kS; ++k) y += red[rr][k];
+            if (row < r_hi) {
+                if (!(fabsf(y) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
+                yb[(size_t)blockIdx.y * a.y_stride + (row - r_lo)] = y;
             }
-            n /= 2;
-        } else {
-            v[0] += __shfl_xor(v[0], stride, 64);
-        }
-        stride >>= 1;
-    }
-    // after the halvings, sum p lives in the lanes whose bits (32, 16, ...)
-    // spell p, most significant first
-    if ((L & ((64 / kP) - 1)) == 0) {
-        const uint32_t p = L / (64 / kP);
-        const uint32_t item = wave + 4 * p;
-        red[item / kS][item % kS] = v[0];
-    }
-    __syncthreads();
-    if (threadIdx.x < kR) {
-        const uint32_t r = threadIdx.x, row = row0 + r;
-        float y = red[r][0];
-#pragma unroll
-        for (int sl = 1; sl < kS; ++sl) y += red[r][sl];
-        if (row < r_hi) {
-            if (!(fabsf(y) <= 3.4028235e38f)) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
-            yb[(size_t)blockIdx.y * a.y_stride + (row - r_lo)] = y;
         }
     }
 }

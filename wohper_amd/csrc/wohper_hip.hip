@@ -201,12 +201,29 @@ struct Arena {
 
 // Device scratch that grows on demand (allocation happens outside the
 // steady state: the first call at a given size allocates, later calls reuse).
+// While graphs captured from the context are alive, a buffer that has to
+// grow is retired (freed with the last graph) rather than freed: the graphs
+// keep its address.
+struct Retire {
+    size_t live = 0;             // captured graphs not yet released
+    std::vector<void*> retired;  // device buffers replaced meanwhile
+    void drop(void* q) {
+        if (!q) return;
+        if (live) retired.push_back(q);
+        else (void)hipFree(q);
+    }
+};
+
 struct Scratch {
     void* p = nullptr;
     size_t n = 0;
+    Retire* retire = nullptr;  // set for the context's buffers
     hipError_t ensure(size_t bytes, bool zero) {
         if (bytes <= n) return hipSuccess;
-        if (p) (void)hipFree(p);
+        if (p) {
+            if (retire) retire->drop(p);
+            else (void)hipFree(p);
+        }
         p = nullptr;
         n = 0;
         hipError_t e = hipMalloc(&p, bytes);
@@ -285,6 +302,18 @@ struct wh_ctx {
     size_t moe_last_hidden = 0, moe_last_inter = 0;
     std::mutex mu;
     hipEvent_t timer[2] = {nullptr, nullptr};  // wh_timer_start / wh_timer_stop
+    Retire retire;                                     // buffers kept for live graphs
+    std::map<uint64_t, hipGraphExec_t> graphs;         // wh_graph_end handles
+    uint64_t next_graph = 1;
+    // Between wh_graph_begin and wh_graph_end `stream` is cap_stream, a
+    // stream of its own in capture mode, so a call that breaks the capture
+    // leaves the context's stream (base_stream) untouched.
+    bool capturing = false;
+    hipStream_t base_stream = nullptr, cap_stream = nullptr;
+    std::vector<Scratch*> scratch() {
+        return {&x_in, &y_out, &h, &ybuf, &cnt_y, &tmp, &batch, &routes, &bout, &gu, &relayout, &rtr, &rtr_cnt,
+                &mla, &hcs, &fp8mm_ws, &fp8mm_cnt};
+    }
 };
 
 namespace {
@@ -509,43 +538,56 @@ int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x,
     }
     // exact numerics off: the order-free kernel (fp8_tol.h) for lane-layout
     // tensors without the reference's +-480 codes, widths of 1, 2, 4 or 8
-    // slices of 1024 columns
+    // slices of 1024 columns and a power of two rows per scale row
     const size_t slices = t.cols / 1024;
-    const size_t tol_rows = (r1 - r0) + (t2 ? r1_2 - r0_2 : 0);
-    size_t kr = tol_rows >= 4096 ? 8 : (tol_rows >= 2048 ? 4 : 2);
-    if (slices == 1 && kr < 4) kr = 4;
-    const bool tol = order_free && !c->exact && t.fast && !t.special && t.cols % 1024 == 0 &&
-                     (slices == 1 || slices == 2 || slices == 4 || slices == 8) &&
-                     (!t2 || (t2->fast && !t2->special && t2->cols == t.cols)) &&
-                     (!x_group_rows || x_group_rows % kr == 0);  // a block stays inside one input's rows
-    if (tol) {
-        const size_t b1 = (r1 - r0 + kr - 1) / kr;
-        if (t2) a.blocks1 = (uint32_t)b1;
-        dim3 grid((unsigned)(b1 + (t2 ? (r1_2 - r0_2 + kr - 1) / kr : 0)), (unsigned)n_batch);
-#define WH_TOL(R, S)                                                                 \
-    do {                                                                             \
-        if (u8) k_fp8_gemv_tol<R, S, true><<<grid, 256, 0, c->stream>>>(a);          \
-        else k_fp8_gemv_tol<R, S, false><<<grid, 256, 0, c->stream>>>(a);            \
+    const bool tol_shape = order_free && !c->exact && t.fast && !t.special && t.cols % 1024 == 0 &&
+                           (slices == 1 || slices == 2 || slices == 4 || slices == 8) &&
+                           is_pow2(t.rows / t.scale_rows) &&
+                           (!t2 || (t2->fast && !t2->special && t2->cols == t.cols));
+    if (tol_shape) {
+        // waves per workgroup: one per slice, at least 4; pairs (row,
+        // slice) per wave: as many as keep >= 512 workgroups, up to 8
+        const size_t kw = slices == 8 ? 8 : 4;
+        const size_t pairs = ((r1 - r0) + (t2 ? r1_2 - r0_2 : 0)) * slices;
+        size_t kp = pairs >= 8 * kw * 512 ? 8 : pairs >= 4 * kw * 512 ? 4 : 2;
+#ifdef WH_TOL_KP
+        kp = WH_TOL_KP;
+#endif
+        const size_t kr = kp * kw / slices;  // rows per workgroup
+        const size_t rg = t.rows / t.scale_rows;
+        // a workgroup stays inside one input's rows
+        if (!x_group_rows || x_group_rows % kr == 0) {
+            const bool one = rg % kr == 0 && r0 % kr == 0 &&
+                             (!t2 || ((t2->rows / t2->scale_rows) % kr == 0 && r0_2 % kr == 0));
+            const size_t b1 = (r1 - r0 + kr - 1) / kr;
+            if (t2) a.blocks1 = (uint32_t)b1;
+            dim3 grid((unsigned)(b1 + (t2 ? (r1_2 - r0_2 + kr - 1) / kr : 0)), (unsigned)n_batch);
+            const unsigned threads = (unsigned)(64 * kw);
+#define WH_TOL(W, S, P)                                                                      \
+    do {                                                                                     \
+        if (u8 && one) k_fp8_gemv_tol<W, S, P, true, true><<<grid, threads, 0, c->stream>>>(a);    \
+        else if (u8) k_fp8_gemv_tol<W, S, P, true, false><<<grid, threads, 0, c->stream>>>(a);     \
+        else if (one) k_fp8_gemv_tol<W, S, P, false, true><<<grid, threads, 0, c->stream>>>(a);    \
+        else k_fp8_gemv_tol<W, S, P, false, false><<<grid, threads, 0, c->stream>>>(a);            \
     } while (0)
-#define WH_TOL_S(R)                          \
-    do {                                     \
-        if (slices == 2) WH_TOL(R, 2);       \
-        else if (slices == 4) WH_TOL(R, 4);  \
-        else WH_TOL(R, 8);                   \
+#define WH_TOL_S(P)                            \
+    do {                                       \
+        if (slices == 1) WH_TOL(4, 1, P);      \
+        else if (slices == 2) WH_TOL(4, 2, P); \
+        else if (slices == 4) WH_TOL(4, 4, P); \
+        else WH_TOL(8, 8, P);                  \
     } while (0)
-        if (kr == 8) {
-            if (slices == 1) WH_TOL(8, 1);
+            if (kp == 2) WH_TOL_S(2);
+            else if (kp == 4) WH_TOL_S(4);
+#ifdef WH_TOL_KP
+            else if (kp == 16) WH_TOL_S(16);
+#endif
             else WH_TOL_S(8);
-        } else if (kr == 4) {
-            if (slices == 1) WH_TOL(4, 1);
-            else WH_TOL_S(4);
-        } else {
-            WH_TOL_S(2);
-        }
 #undef WH_TOL_S
 #undef WH_TOL
-        WH_HIP(hipGetLastError());
-        return WH_OK;
+            WH_HIP(hipGetLastError());
+            return WH_OK;
+        }
     }
     if (fp8_split_k(t)) {
         const size_t blocks = (r1 - r0 + WH_FP8_SK_ROWS - 1) / WH_FP8_SK_ROWS +
@@ -1138,7 +1180,7 @@ int layer_table(wh_ctx* c, uint32_t layer, LayerTable** out) {
     // kernels of earlier calls may still read the old table
     WH_HIP(hipStreamSynchronize(c->stream));
     if (n > t.cap) {
-        if (t.dev) (void)hipFree(t.dev);
+        c->retire.drop(t.dev);
         t.dev = nullptr;
         t.cap = 0;
         WH_HIP(hipMalloc((void**)&t.dev, n * sizeof(wh_expert_ptrs)));
@@ -1780,6 +1822,7 @@ int wh_init(int device, wh_ctx** out) {
     wh_ctx* c = new wh_ctx();
     c->device = device;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    c->base_stream = c->stream;
     if (e == hipSuccess) e = hipMalloc(&c->status, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMemset(c->status, 0, sizeof(uint32_t));
     if (e == hipSuccess) e = hipHostMalloc((void**)&c->status_host, sizeof(uint32_t), hipHostMallocDefault);
@@ -1789,6 +1832,7 @@ int wh_init(int device, wh_ctx** out) {
         delete c;
         return hip_status(e);
     }
+    for (Scratch* sp : c->scratch()) sp->retire = &c->retire;
     *out = c;
     return WH_OK;
 }
@@ -1797,10 +1841,18 @@ int wh_shutdown(wh_ctx* c) {
     if (!c) return WH_INVALID_ARGUMENT;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
+    if (c->capturing) {
+        hipGraph_t g = nullptr;
+        if (hipStreamEndCapture(c->cap_stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+        c->stream = c->base_stream;
+    }
+    if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
+    for (auto& kv : c->graphs) (void)hipGraphExecDestroy(kv.second);
+    (void)hipStreamSynchronize(c->stream);
     c->arena.release_all();
-    for (Scratch* s : {&c->x_in, &c->y_out, &c->h, &c->ybuf, &c->cnt_y, &c->tmp, &c->batch, &c->routes, &c->bout,
-                       &c->gu, &c->relayout, &c->rtr, &c->rtr_cnt, &c->mla, &c->hcs})
+    for (Scratch* s : c->scratch())
         if (s->p) (void)hipFree(s->p);
+    for (void* q : c->retire.retired) (void)hipFree(q);
     for (auto& kv : c->rope_tabs) (void)hipFree(kv.second);
     for (auto& kv : c->tables)
         if (kv.second.dev) (void)hipFree(kv.second.dev);
@@ -1823,6 +1875,77 @@ int wh_synchronize(wh_ctx* c) {
 }
 
 int wh_stream_status(wh_ctx* c) { return wh_synchronize(c); }
+
+int wh_graph_begin(wh_ctx* c) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (c->capturing) return WH_INVALID_ARGUMENT;
+    WH_HIP(hipSetDevice(c->device));
+    if (!c->cap_stream) WH_HIP(hipStreamCreateWithFlags(&c->cap_stream, hipStreamNonBlocking));
+    // thread-local: calls of this thread that would synchronize fail (and
+    // invalidate the capture) instead of running
+    WH_HIP(hipStreamBeginCapture(c->cap_stream, hipStreamCaptureModeThreadLocal));
+    c->stream = c->cap_stream;
+    c->capturing = true;
+    return WH_OK;
+}
+
+int wh_graph_end(wh_ctx* c, wh_graph* out) {
+    if (!c || !out) return WH_INVALID_ARGUMENT;
+    *out = 0;
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (!c->capturing) return WH_INVALID_ARGUMENT;
+    (void)hipSetDevice(c->device);
+    hipGraph_t g = nullptr;
+    const hipError_t ce = hipStreamEndCapture(c->cap_stream, &g);
+    c->stream = c->base_stream;
+    c->capturing = false;
+    if (ce != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        // a broken capture can leave its stream in capture mode: the next
+        // capture gets a fresh one
+        (void)hipStreamDestroy(c->cap_stream);
+        c->cap_stream = nullptr;
+        const int st = hip_status(ce);
+        (void)hipGetLastError();  // the thread's sticky error is this capture's, reported here
+        return st;
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    WH_HIP(e);
+    const wh_graph id = c->next_graph++;
+    c->graphs[id] = exec;
+    ++c->retire.live;
+    *out = id;
+    return WH_OK;
+}
+
+int wh_graph_launch(wh_ctx* c, wh_graph g) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    auto it = c->graphs.find(g);
+    if (it == c->graphs.end() || c->capturing) return WH_INVALID_ARGUMENT;
+    WH_HIP(hipSetDevice(c->device));
+    WH_HIP(hipGraphLaunch(it->second, c->stream));
+    return WH_OK;
+}
+
+int wh_graph_release(wh_ctx* c, wh_graph g) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    auto it = c->graphs.find(g);
+    if (it == c->graphs.end()) return WH_INVALID_ARGUMENT;
+    WH_HIP(hipSetDevice(c->device));
+    WH_HIP(hipStreamSynchronize(c->stream));  // replays still queued use the buffers
+    (void)hipGraphExecDestroy(it->second);
+    c->graphs.erase(it);
+    if (--c->retire.live == 0) {
+        for (void* q : c->retire.retired) (void)hipFree(q);
+        c->retire.retired.clear();
+    }
+    return WH_OK;
+}
 
 void* wh_stream(wh_ctx* c) { return c ? (void*)c->stream : nullptr; }
 
