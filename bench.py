@@ -689,6 +689,8 @@ TIMELINE_POINTS = {
                       "unit 0 done", "unit 1 done", "unit 2 done", "unit 3 done", "units summed", "end"],
     "batch_gateup": ["start", "ring issued", "B staged", "wave's last item done", "workgroup end"],
     "batch_down": ["start", "ring issued", "B staged", "wave's last item done", "workgroup end"],
+    "router": ["start", "x staged", "gate rows landed", "dot done", "scores published", "arrived",
+               "last: scores gathered", "last: selected", "last: keys", "last: rounds done", "last: weight sum"],
 }
 
 
@@ -763,6 +765,24 @@ def timeline(lib_path: str, seed: int = 2) -> dict:
         ctx.synchronize()
     res["batch_gateup"] = read(0, TIMELINE_POINTS["batch_gateup"])
     res["batch_down"] = read(1, TIMELINE_POINTS["batch_down"])
+    # the bf16 router (one wave per workgroup, 64 workgroups)
+    from wohper_amd import model_format as mf
+    rows, cols = 256, 4096
+    gate = ((rng.standard_normal((rows, cols)).astype(np.float32) * 0.02).view(np.uint32) >> 16).astype(np.uint16)
+    bias = (rng.standard_normal(rows) * 0.05).astype(np.float32)
+    for k in range(n_layers):
+        blk = mf.build_synthetic_quant_block([
+            mf.SyntheticTensor(f"layers.{k}.ffn.gate.weight", 9, (rows, cols), gate.tobytes(), 11, 2404),
+            mf.SyntheticTensor(f"layers.{k}.ffn.gate.bias", 9, (rows,), bias.tobytes(), 12, 2405)])
+        ctx.store_router(1000 + k, blk, cols)
+    rx, rout = ctx.device_alloc(cols * 4), ctx.device_alloc(256)
+    ctx.to_device(rx, rng.standard_normal(cols).astype(np.float32))
+    assert lib.wh_debug_timeline(0, None, 0) == 0  # clears the stamps
+    for i in range(12):
+        ctx.synchronize()
+        ctx.route_experts_async(1000 + i % n_layers, rx, cols, 6, 0, 0, rout, rout + 64, rout + 128, route_scale=1.5)
+    ctx.synchronize()
+    res["router"] = read(0, TIMELINE_POINTS["router"])
     ctx.close()
     return res
 

@@ -65,88 +65,115 @@ __device__ __forceinline__ float wh_bf16_hi(uint32_t v) { return __uint_as_float
 // rows, x staged in LDS (cols floats).  Thread L runs one AVX accumulator
 // chain: accumulator a = (L / 8) % 2, lane l = L % 8 of row
 // 4 * blockIdx.x + L / 16.  The resident layout gives the thread the eight
-// values of its chain in a 128-column block as 16 contiguous bytes; up to 32
-// blocks (4096 columns) are loaded at once, wider rows stream the rest
+// values of its chain in a 128-column block as 16 contiguous bytes; x is
+// staged so that the matching eight x values are contiguous too: column
+// 128 b + 32 j + 16 h + o (o = 8 a + l) at float (16 b + o) * 8 + 2 j + h.
+// 4096 columns: every weight block in flight at once and the x values of a
+// block read four blocks ahead of its FMAs; wider rows stream the weights
 // eight blocks ahead.  Returns the row's value in every thread of the row.
+__device__ __forceinline__ uint32_t wh_router_xs_index(uint32_t c) {
+    const uint32_t b = c >> 7, r = c & 127;
+    return ((b << 4) | (r & 15)) * 8 + 2 * (r >> 5) + ((r >> 4) & 1);
+}
+// late(): loads of the caller's, issued right after the weight loads (an
+// earlier load would be waited for before the first weight load issues).
+template <class Late>
 __device__ __forceinline__ float wh_router_gemv_rows(const uint16_t* __restrict__ w, const float* __restrict__ x,
-                                                     uint32_t rows, uint32_t cols, float* xs) {
-    constexpr int kAll = 32, kDepth = 8;
-    const uint32_t L = threadIdx.x, q = L & 15, off = 8 * (q >> 3) + (q & 7);  // column within a chunk
+                                                     uint32_t rows, uint32_t cols, float* xs, Late&& late) {
+    const uint32_t L = threadIdx.x, q = L & 15;  // q = 8 a + l: the chain's column within a 16-column chunk
     const uint32_t row = blockIdx.x * 4 + (L >> 4);
     const uint32_t r = row < rows ? row : rows - 1;  // spare lanes repeat the last row
     const uint4* wp = reinterpret_cast<const uint4*>(w + (size_t)r * cols) + q;
     const uint32_t nb = cols / 128;
-    // x first (16-byte loads, all in flight), then the weight ring
     const float4* x4 = reinterpret_cast<const float4*>(x);
-    constexpr int kX = 16;  // float4 per thread per pass: 4096 columns in one pass
-    auto stage_x = [&](uint32_t base, float4 (&xv)[kX]) {
-#pragma unroll
-        for (int k = 0; k < kX; ++k) {
-            const uint32_t i = base + 64 * k + L;
-            xv[k] = i < cols / 4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-    auto store_x = [&](uint32_t base, const float4 (&xv)[kX]) {
-#pragma unroll
-        for (int k = 0; k < kX; ++k) {
-            const uint32_t i = base + 64 * k + L;
-            if (i < cols / 4) reinterpret_cast<float4*>(xs)[i] = xv[k];
-        }
+    const float4* xq = reinterpret_cast<const float4*>(xs) + 2 * q;  // block b at xq[32 b], xq[32 b + 1]
+    // the four x values of float4 i go to four chains' slots, 8 floats apart
+    auto store_x4 = [&](uint32_t i, float4 v) {
+        const uint32_t k = wh_router_xs_index(4 * i);
+        xs[k] = v.x;
+        xs[k + 8] = v.y;
+        xs[k + 16] = v.z;
+        xs[k + 24] = v.w;
     };
     float acc = 0.0f;
-    auto fma8 = [&](const uint4 q4, uint32_t b) {
-        const uint32_t v[4] = {q4.x, q4.y, q4.z, q4.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t c = 128 * b + 32 * j + off;  // chunks 2j and 2j + 1
-            acc = __builtin_fmaf(wh_bf16_lo(v[j]), xs[c], acc);
-            acc = __builtin_fmaf(wh_bf16_hi(v[j]), xs[c + 16], acc);
-        }
+    auto fma8 = [&](const uint4 w4, const float4 x0, const float4 x1) {
+        acc = __builtin_fmaf(wh_bf16_lo(w4.x), x0.x, acc);
+        acc = __builtin_fmaf(wh_bf16_hi(w4.x), x0.y, acc);
+        acc = __builtin_fmaf(wh_bf16_lo(w4.y), x0.z, acc);
+        acc = __builtin_fmaf(wh_bf16_hi(w4.y), x0.w, acc);
+        acc = __builtin_fmaf(wh_bf16_lo(w4.z), x1.x, acc);
+        acc = __builtin_fmaf(wh_bf16_hi(w4.z), x1.y, acc);
+        acc = __builtin_fmaf(wh_bf16_lo(w4.w), x1.z, acc);
+        acc = __builtin_fmaf(wh_bf16_hi(w4.w), x1.w, acc);
     };
-    if (nb <= (uint32_t)kAll) {
-        // x, then every weight block, then wait for x only: the weights
-        // stream while x lands in LDS
+    if (nb == 32) {
+        // x (16-byte loads), then every weight block, then x into LDS: the
+        // weights stream while x lands
+        constexpr int kNb = 32, kX = 16, kPf = 4;
         float4 xv[kX];
-        stage_x(0, xv);
-        uint4 all[kAll];
 #pragma unroll
-        for (int d = 0; d < kAll; ++d) all[d] = d < (int)nb ? wp[16 * d] : make_uint4(0, 0, 0, 0);
-        store_x(0, xv);
+        for (int k = 0; k < kX; ++k) xv[k] = x4[64 * k + L];
+        uint4 all[kNb];
+#pragma unroll
+        for (int d = 0; d < kNb; ++d) all[d] = wp[16 * d];
+        late();
+        __builtin_amdgcn_sched_barrier(0);  // every load is issued before the first x store waits
+#pragma unroll
+        for (int k = 0; k < kX; ++k) store_x4(64 * k + L, xv[k]);
         __syncthreads();
+        WH_TL(0, 1);
+#ifdef WH_TIMELINE
+        WH_TL_USE(all[kNb - 1].x);
+        WH_TL(0, 2);
+#endif
+        float4 pf[kPf][2];
 #pragma unroll
-        for (int d = 0; d < kAll; ++d)
-            if (d < (int)nb) fma8(all[d], d);
-        goto reduce;
-    }
-    {
-    for (uint32_t base = 0; base < cols / 4; base += 64 * kX) {
-        float4 xv[kX];
-        stage_x(base, xv);
-        store_x(base, xv);
-    }
-    uint4 ring[kDepth];
+        for (int d = 0; d < kPf; ++d) {
+            pf[d][0] = xq[32 * d];
+            pf[d][1] = xq[32 * d + 1];
+        }
+        // the barriers keep each block's x reads kPf blocks ahead of its
+        // FMAs (the scheduler would sink them next to their use)
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) ring[d] = wp[16 * d];
-    __syncthreads();
-    for (uint32_t b0 = 0; b0 < nb; b0 += kDepth) {
+        for (int d = 0; d < kNb; ++d) {
+            const float4 x0 = pf[d % kPf][0], x1 = pf[d % kPf][1];
+            if (d + kPf < kNb) {
+                pf[d % kPf][0] = xq[32 * (d + kPf)];
+                pf[d % kPf][1] = xq[32 * (d + kPf) + 1];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            fma8(all[d], x0, x1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+        for (uint32_t i = L; i < cols / 4; i += 64) store_x4(i, x4[i]);
+        constexpr int kDepth = 8;
+        uint4 ring[kDepth];
 #pragma unroll
-        for (int d = 0; d < kDepth; ++d) {
-            const uint32_t b = b0 + d;
-            if (b < nb) {
-                const uint4 q4 = ring[d];
-                if (b + kDepth < nb) ring[d] = wp[16 * (b + kDepth)];
-                fma8(q4, b);
+        for (int d = 0; d < kDepth; ++d) ring[d] = (uint32_t)d < nb ? wp[16 * d] : make_uint4(0, 0, 0, 0);
+        late();
+        __syncthreads();
+        for (uint32_t b0 = 0; b0 < nb; b0 += kDepth) {
+#pragma unroll
+            for (int d = 0; d < kDepth; ++d) {
+                const uint32_t b = b0 + d;
+                if (b < nb) {
+                    const uint4 w4 = ring[d];
+                    if (b + kDepth < nb) ring[d] = wp[16 * (b + kDepth)];
+                    fma8(w4, xq[32 * b], xq[32 * b + 1]);
+                }
             }
         }
     }
-    }
-reduce:
-    // acc0 + acc1 of the lane, then hsum256's pairs (IEEE addition commutes,
-    // so both partners of each xor step hold the same sum)
-    float s = acc + __shfl_xor(acc, 8, 64);
-    s = s + __shfl_xor(s, 1, 64);
-    s = s + __shfl_xor(s, 2, 64);
-    s = s + __shfl_xor(s, 4, 64);
+    // acc0 + acc1 of the lane (DPP row_ror:8 = lane ^ 8), then hsum256's
+    // pairs (quad_perm lane ^ 1, lane ^ 2; then row_half_mirror pairs lane l
+    // with 7 - l, which after the first two steps holds the same sum as
+    // l ^ 4).  IEEE addition commutes, so both partners of a step hold the
+    // same sum.
+    float s = acc + wh_dpp_f<0x128>(acc);
+    s = s + wh_dpp_f<0xB1>(s);
+    s = s + wh_dpp_f<0x4E>(s);
+    s = s + wh_dpp_f<0x141>(s);
     return s + 0.0f;  // + the (empty) tail
 }
 
@@ -200,41 +227,52 @@ struct wh_router_sel {
     uint32_t* out_count;
 };
 
-// Wave-wide maximum of a 64-bit value, returned to every lane: DPP steps
-// (quad xor 1 and 2, half-row and row mirrors, the row broadcasts) leave the
-// maximum in lane 63.
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ uint64_t wh_dpp_max_u64(uint64_t v) {
-    const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp((int)lo, (int)lo, kCtrl, kRowMask, 0xf, false);
-    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp((int)hi, (int)hi, kCtrl, kRowMask, 0xf, false);
-    const uint64_t o = ((uint64_t)ohi << 32) | olo;
-    return o > v ? o : v;
-}
-__device__ __forceinline__ uint64_t wh_wave_max_u64(uint64_t v) {
-    v = wh_dpp_max_u64<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
-    v = wh_dpp_max_u64<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
-    v = wh_dpp_max_u64<0x141, 0xf>(v);  // row_half_mirror
-    v = wh_dpp_max_u64<0x140, 0xf>(v);  // row_mirror
-    v = wh_dpp_max_u64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
-    v = wh_dpp_max_u64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-    return ((uint64_t)hi << 32) | lo;
-}
-
 // f32::total_cmp order as a signed key.
 __device__ __forceinline__ int32_t wh_total_key(float f) {
     const int32_t k = (int32_t)__float_as_uint(f);
     return k ^ (int32_t)(((uint32_t)(k >> 31)) >> 1);
 }
 
+// Wave-wide maximum of a signed / minimum of an unsigned 32-bit value,
+// returned to every lane: DPP steps (quad xor 1 and 2, half-row and row
+// mirrors, then the row broadcasts into rows 1, 3 and 2, 3) leave the result
+// in lane 63.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ int32_t wh_dpp_i32(int32_t v) {
+    // full row mask: every lane is written, no copy of the old value needed
+    if constexpr (kRowMask == 0xf) return __builtin_amdgcn_mov_dpp(v, kCtrl, 0xf, 0xf, false);
+    else return __builtin_amdgcn_update_dpp(v, v, kCtrl, kRowMask, 0xf, false);
+}
+__device__ __forceinline__ int32_t wh_wave_max_i32(int32_t v) {
+    v = max(v, wh_dpp_i32<0xb1, 0xf>(v));
+    v = max(v, wh_dpp_i32<0x4e, 0xf>(v));
+    v = max(v, wh_dpp_i32<0x141, 0xf>(v));
+    v = max(v, wh_dpp_i32<0x140, 0xf>(v));
+    v = max(v, wh_dpp_i32<0x142, 0xa>(v));
+    v = max(v, wh_dpp_i32<0x143, 0xc>(v));
+    return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ uint32_t wh_wave_min_u32(uint32_t u) {
+    int32_t v = (int32_t)u;
+    v = (int32_t)min((uint32_t)v, (uint32_t)wh_dpp_i32<0xb1, 0xf>(v));
+    v = (int32_t)min((uint32_t)v, (uint32_t)wh_dpp_i32<0x4e, 0xf>(v));
+    v = (int32_t)min((uint32_t)v, (uint32_t)wh_dpp_i32<0x141, 0xf>(v));
+    v = (int32_t)min((uint32_t)v, (uint32_t)wh_dpp_i32<0x140, 0xf>(v));
+    v = (int32_t)min((uint32_t)v, (uint32_t)wh_dpp_i32<0x142, 0xa>(v));
+    v = (int32_t)min((uint32_t)v, (uint32_t)wh_dpp_i32<0x143, 0xc>(v));
+    return (uint32_t)__builtin_amdgcn_readlane(v, 63);
+}
+
 // Selection and weights by one wave (threads 0..63) from the scores in sc
-// (LDS, sqrt-softplus already applied).
+// (LDS, sqrt-softplus already applied).  Round t of the stable descending
+// sort takes the largest key, ties to the smallest candidate position: a
+// wave maximum of the lanes' best keys, then a wave minimum of the positions
+// holding it.  Lane i keeps the i-th selected id.
 template <uint32_t kSlots>
 __device__ __forceinline__ void wh_router_select_wave_n(const wh_router_sel& a, const float* sc, const float* sk,
                                                         uint32_t* sel, uint32_t& n_sel) {
     const uint32_t L = threadIdx.x & 63;
+    uint32_t my_sel = 0, n = 0;
     if (a.n_hash) {
         // hash layer (E/compute.rs:2190-2206): the row's ids that are
         // available and have a score, in table order
@@ -255,7 +293,10 @@ __device__ __forceinline__ void wh_router_select_wave_n(const wh_router_sel& a, 
         const uint64_t m = __ballot(ok);
         const uint32_t pos = (uint32_t)__popcll(m & ((1ull << L) - 1ull));
         if (ok && pos < a.active) sel[pos] = id;
-        if (L == 0) n_sel = min((uint32_t)__popcll(m), a.active);
+        n = min((uint32_t)__popcll(m), a.active);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+        if (L < n) my_sel = sel[L];
     } else {
         // the available experts by score (+ bias), descending, stable
         const uint32_t cnt = a.avail ? a.n_avail : a.rows;
@@ -271,43 +312,80 @@ __device__ __forceinline__ void wh_router_select_wave_n(const wh_router_sel& a, 
             else if (a.math && a.bias && live[s]) v = v + a.bias[id];
             key[s] = wh_total_key(v);
         }
-        uint32_t t = 0;
-        for (; t < a.active; ++t) {
-            // the lane's best: larger key, then smaller position; packed so
-            // that the unsigned maximum picks the winner (0: none)
-            uint64_t best = 0;
+        // the lane's live candidates in selection order (larger key first,
+        // then smaller position): an insertion sort of its slots
+        int32_t qk[kSlots];
+        uint32_t qp[kSlots];
+        uint32_t qn = 0;
 #pragma unroll
-            for (uint32_t s = 0; s < kSlots; ++s) {
-                const uint64_t p = live[s] ? (((uint64_t)((uint32_t)key[s] ^ 0x80000000u) << 32) |
-                                              (0xffffffffu - (L + 64 * s)))
-                                           : 0ull;
-                best = p > best ? p : best;
+        for (uint32_t s = 0; s < kSlots; ++s) {
+            // slots come in position order, so an equal key goes after
+            const int32_t k = key[s];
+            const uint32_t p = L + 64 * s;
+            bool placed = !live[s];
+#pragma unroll
+            for (int i = (int)kSlots - 1; i >= 0; --i) {
+                if (placed || (uint32_t)i > qn) continue;
+                const bool shift = i > 0 && k > qk[i - 1];
+                if (shift) {
+                    qk[i] = qk[i - 1];
+                    qp[i] = qp[i - 1];
+                } else {
+                    qk[i] = k;
+                    qp[i] = p;
+                    placed = true;
+                }
             }
-            const uint64_t win = wh_wave_max_u64(best);
-            if (win == 0) break;  // uniform
-            const uint32_t bp = 0xffffffffu - (uint32_t)win;
+            qn += live[s] ? 1u : 0u;
+        }
+#ifdef WH_TIMELINE
+        WH_TL_USE(qk[0]);
+        WH_TL(0, 8);
+#endif
+        for (; n < a.active; ++n) {
+            const bool has = qn > 0;
+            if (__ballot(has) == 0) break;  // uniform: no candidate left
+            const int32_t bk = has ? qk[0] : INT32_MIN;
+            const int32_t mk = wh_wave_max_i32(bk);
+            // one lane holding the maximum key: its head; several: the
+            // smallest of their heads
+            const uint64_t at = __ballot(has && bk == mk);
+            const uint32_t mp = __popcll(at) == 1
+                                    ? (uint32_t)__builtin_amdgcn_readlane((int)qp[0], (int)__ffsll((long long)at) - 1)
+                                    : wh_wave_min_u32(has && bk == mk ? qp[0] : 0xffffffffu);
+            if (has && qp[0] == mp) {  // the winner pops its head
 #pragma unroll
-            for (uint32_t s = 0; s < kSlots; ++s)
-                if (L + 64 * s == bp) live[s] = false;
-            if (L == 0) sel[t] = a.avail ? a.avail[bp] : bp;
+                for (uint32_t i = 0; i + 1 < kSlots; ++i) {
+                    qk[i] = qk[i + 1];
+                    qp[i] = qp[i + 1];
+                }
+                --qn;
+            }
+            if (L == n) my_sel = mp;
         }
-        if (L == 0) n_sel = t;
+        if (a.avail && L < n) my_sel = a.avail[my_sel];
+        WH_TL(0, 9);
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+    // finalize_route_weights (E/compute.rs:2254-2268): the sum in route
+    // order, then every lane its own weight
+    const float v = L < n ? sc[my_sel] : 0.0f;
+    float sum = 0.0f;
+#pragma unroll 1
+    for (uint32_t i = 0; i < n; ++i) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+    const bool norm = a.math != 0 && n > 0;
+    const bool ok = sum > 0.0f && sum <= 3.4028235e38f;
+    const float uniform = n ? a.route_scale / (float)n : 0.0f;
+#ifdef WH_TIMELINE
+    WH_TL_USE(sum);
+    WH_TL(0, 10);
+#endif
+    if (L < n) {
+        a.out_ids[L] = my_sel;
+        a.out_scores[L] = !norm ? v : (ok ? v / sum * a.route_scale : uniform);
+    }
     if (L == 0) {
-        const uint32_t n = n_sel;
-        float sum = 0.0f;
-        for (uint32_t i = 0; i < n; ++i) sum = sum + sc[sel[i]];
-        const bool norm = a.math != 0 && n > 0;
-        const bool ok = sum > 0.0f && sum <= 3.4028235e38f;
-        const float uniform = n ? a.route_scale / (float)n : 0.0f;
-        for (uint32_t i = 0; i < n; ++i) {
-            const float v = sc[sel[i]];
-            a.out_ids[i] = sel[i];
-            a.out_scores[i] = !norm ? v : (ok ? v / sum * a.route_scale : uniform);
-        }
         *a.out_count = n;
+        n_sel = n;
     }
 }
 
@@ -352,44 +430,59 @@ __global__ void __launch_bounds__(64) k_router_bf16(const uint16_t* __restrict__
     __shared__ uint64_t exp_tab[WH_EXP_TAB_LEN];
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 4);
     const bool writer = (threadIdx.x & 15) == 0 && row < a.rows;
-    const float bias = writer && a.math && a.bias ? a.bias[row] : 0.0f;  // loaded before the weights
-    const uint64_t tv = threadIdx.x < WH_EXP_TAB_LEN ? kExpTab[threadIdx.x] : 0ull;
-    if (threadIdx.x < WH_EXP_TAB_LEN) exp_tab[threadIdx.x] = tv;  // ordered before the GEMV's barrier
-    const float v = wh_router_gemv_rows(w, x, a.rows, cols, xs);
+    WH_TL(0, 0);
+    float bias = 0.0f;
+    uint64_t tv = 0;
+    const float v = wh_router_gemv_rows(w, x, a.rows, cols, xs, [&]() {
+        if (writer && a.math && a.bias) bias = a.bias[row];
+        if (threadIdx.x < WH_EXP_TAB_LEN) tv = kExpTab[threadIdx.x];
+    });
+    // the expf table goes to LDS once the GEMV is done
+    if (threadIdx.x < WH_EXP_TAB_LEN) exp_tab[threadIdx.x] = tv;
+    __syncthreads();
+    WH_TL(0, 3);
     if (writer) {
         const float score = a.math ? wh_sqrt_softplus(v, exp_tab) : v;
         float* pub = const_cast<float*>(a.logits);
         wh_store_coherent(pub + row, score);
         wh_store_coherent(pub + a.rows + row, a.math && a.bias ? score + bias : score);
     }
+    WH_TL(0, 4);
     wh_stores_done();
     uint32_t last = 0;
     if (threadIdx.x == 0) last = wh_arrive(counter) == gridDim.x - 1;
     last = __shfl(last, 0, 64);
+    WH_TL(0, 5);
     if (!last) return;
     // all published scores and keys are requested before the first LDS
     // store, so the wave waits for one round trip, not one per pass
-    constexpr uint32_t kPass = WH_ROUTER_MAX_ROWS / 64;
-    float rs[kPass], rk[kPass];
+    auto gather = [&](auto pass) {
+        constexpr uint32_t kPass = decltype(pass)::value;
+        float rs[kPass], rk[kPass];
 #pragma unroll
-    for (uint32_t k = 0; k < kPass; ++k) {
-        const uint32_t i = threadIdx.x + 64 * k;
-        if (i < a.rows) {
-            rs[k] = wh_load_coherent(a.logits + i);
-            rk[k] = wh_load_coherent(a.logits + a.rows + i);
+        for (uint32_t k = 0; k < kPass; ++k) {
+            const uint32_t i = threadIdx.x + 64 * k;
+            if (i < a.rows) {
+                rs[k] = wh_load_coherent(a.logits + i);
+                rk[k] = wh_load_coherent(a.logits + a.rows + i);
+            }
         }
-    }
 #pragma unroll
-    for (uint32_t k = 0; k < kPass; ++k) {
-        const uint32_t i = threadIdx.x + 64 * k;
-        if (i < a.rows) {
-            sc[i] = rs[k];
-            sk[i] = rk[k];
+        for (uint32_t k = 0; k < kPass; ++k) {
+            const uint32_t i = threadIdx.x + 64 * k;
+            if (i < a.rows) {
+                sc[i] = rs[k];
+                sk[i] = rk[k];
+            }
         }
-    }
+    };
+    if (a.rows <= 256) gather(std::integral_constant<uint32_t, 4>());
+    else gather(std::integral_constant<uint32_t, WH_ROUTER_MAX_ROWS / 64>());
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+    WH_TL(0, 6);
     wh_router_select_wave(a, sc, sk, sel, n_sel);
+    WH_TL(0, 7);
     if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

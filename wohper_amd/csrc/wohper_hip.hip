@@ -3372,8 +3372,15 @@ int wh_profile_token_pipeline(wh_ctx* c, const wh_expert_route* routes, size_t n
 // only): which = 0 gate/up, 1 down; n <= 512 * 16 * WH_TL_POINTS stamps.
 int wh_debug_timeline(int which, uint64_t* out, size_t n) {
     constexpr size_t kStamps = 512 * 16 * WH_TL_POINTS;
-    if (which < 0 || which > 1 || !out || n > kStamps) return WH_INVALID_ARGUMENT;
+    if (which < 0 || which > 1 || n > kStamps) return WH_INVALID_ARGUMENT;
     WH_HIP(hipDeviceSynchronize());
+    if (!out) {  // clears the kernel's stamps
+        void* p = nullptr;
+        WH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(wh_tl_buf)));
+        WH_HIP(hipMemset((uint64_t*)p + (size_t)which * kStamps, 0, kStamps * sizeof(uint64_t)));
+        WH_HIP(hipDeviceSynchronize());
+        return WH_OK;
+    }
     WH_HIP(hipMemcpyFromSymbol(out, HIP_SYMBOL(wh_tl_buf), n * sizeof(uint64_t), (size_t)which * kStamps * sizeof(uint64_t)));
     return WH_OK;
 }
