@@ -183,6 +183,10 @@ extern "C" {
     pub fn wh_routed_and_shared_experts_async(ctx: *mut WhCtx, routes: *const WhExpertRoute, n_routes: usize,
                                               shared_layer: u32, shared_expert: u32, x_dev: *const c_void,
                                               x_is_bf16: c_int, n_tokens: usize, out_dev: *mut f32) -> c_int;
+    pub fn wh_routed_and_shared_experts_dev_async(ctx: *mut WhCtx, layer_id: u32, ids_dev: *const u32,
+                                                  weights_dev: *const f32, count_dev: *const u32, n_slots: usize,
+                                                  shared_layer: u32, shared_expert: u32, x_dev: *const c_void,
+                                                  x_is_bf16: c_int, out_dev: *mut f32) -> c_int;
     pub fn wh_routed_and_shared_experts_noalloc_async(ctx: *mut WhCtx, routes: *const WhExpertRoute,
                                                       n_routes: usize, shared_layer: u32, shared_expert: u32,
                                                       x_dev: *const c_void, x_is_bf16: c_int,

@@ -311,6 +311,24 @@ int wh_routed_and_shared_experts_async(wh_ctx* ctx, const wh_expert_route* route
                                        uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
                                        int x_is_bf16, size_t n_tokens, float* out_dev);
 
+/* wh_routed_and_shared_experts_async for one token whose route list is in
+ * device memory, as wh_route_experts_async leaves it: count_dev[0] routes
+ * (at most n_slots are taken; n_slots >= 1 and at most 15 with a shared
+ * expert, 16 without)
+ * of layer_id, expert ids_dev[i] with weight weights_dev[i], in route order.
+ * The list is resolved against the layer's resident experts on the device,
+ * so a router on the device feeds the experts with no host round trip: the
+ * reference routes a decode token (route_experts_from_dense_block,
+ * E/compute.rs:2129-2268) and then runs compute_active_and_shared_experts
+ * (E/compute.rs:1872-1946) on those routes.  Every resident expert of the
+ * layer and the shared expert (WH_NO_SHARED_EXPERT: none) must share one
+ * shape the fast kernels take (else WH_UNSUPPORTED).  An id with no resident
+ * expert reports WH_NOT_RESIDENT through wh_stream_status. */
+int wh_routed_and_shared_experts_dev_async(wh_ctx* ctx, uint32_t layer_id, const uint32_t* ids_dev,
+                                           const float* weights_dev, const uint32_t* count_dev, size_t n_slots,
+                                           uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
+                                           int x_is_bf16, float* out_dev);
+
 /* Allocation-free variant of wh_routed_and_shared_experts_async, same
  * arguments and results.  No counterpart in the reference: it is for callers
  * that cannot allocate device memory (code under HIP graph capture, tight

@@ -92,6 +92,7 @@ EXPORTED = (
     "wh_act_quant_dequant_async", "wh_window_attention_async", "wh_mla_attention_decode_async",
     "wh_hc_split_sinkhorn_async", "wh_hc_pre_async", "wh_hc_post_async",
     "wh_graph_begin", "wh_graph_end", "wh_graph_launch", "wh_graph_release",
+    "wh_routed_and_shared_experts_dev_async",
 )
 
 ROUTER_RAW_LOGITS = 0
@@ -196,6 +197,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_routed_experts_async": (c.c_int, [vp, c.POINTER(WhExpertRoute), sz, vp, c.c_int, sz, vp]),
         "wh_fp8_gemv_async": (c.c_int, [vp, c.c_uint64, sz, sz, vp, vp]),
         "wh_stream_status": (c.c_int, [vp]),
+        "wh_routed_and_shared_experts_dev_async": (c.c_int, [vp, c.c_uint32, vp, vp, vp, sz, c.c_uint32, c.c_uint32,
+                                                            vp, c.c_int, vp]),
         "wh_graph_begin": (c.c_int, [vp]),
         "wh_graph_end": (c.c_int, [vp, c.POINTER(c.c_uint64)]),
         "wh_graph_launch": (c.c_int, [vp, c.c_uint64]),
@@ -620,6 +623,17 @@ class Context:
         _check(self.lib.wh_routed_and_shared_experts_async(self._h, arr, n, shared_key[0], shared_key[1],
                                                            ctypes.c_void_p(x_ptr), int(x_is_bf16), n_tokens,
                                                            ctypes.c_void_p(out_ptr)), "routed_and_shared_experts_async")
+
+    def routed_and_shared_experts_dev_async(self, layer_id: int, ids_ptr: int, weights_ptr: int, count_ptr: int,
+                                            n_slots: int, shared_key, x_ptr: int, x_is_bf16: bool, out_ptr: int):
+        """One token's experts from a route list in device memory (ids,
+        weights, count as route_experts_async writes them); shared_key None:
+        no shared expert."""
+        sl, se = shared_key if shared_key is not None else (0, NO_SHARED_EXPERT)
+        _check(self.lib.wh_routed_and_shared_experts_dev_async(
+            self._h, layer_id, ctypes.c_void_p(ids_ptr), ctypes.c_void_p(weights_ptr), ctypes.c_void_p(count_ptr),
+            n_slots, sl, se, ctypes.c_void_p(x_ptr), int(x_is_bf16), ctypes.c_void_p(out_ptr)),
+            "routed_and_shared_experts_dev_async")
 
     def routed_and_shared_experts_noalloc_async(self, routes, shared_key, x_ptr: int, x_is_bf16: bool,
                                                 n_tokens: int, out_ptr: int):

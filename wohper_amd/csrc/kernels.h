@@ -790,11 +790,22 @@ struct wh_expert_ptrs {
     const uint8_t* s2;
 };
 
+// A token's route list in device memory (the router's output resolved
+// against the layer's expert table by k_moe_resolve): slots [0, n_routed)
+// are the routes in route order; the slots after them up to the shared slot
+// hold copies of a resident expert, computed and never summed.
+struct wh_moe_dyn {
+    wh_expert_ptrs ex[WH_MAX_EXPERTS];
+    float route_w[WH_MAX_EXPERTS];
+    uint32_t n_routed;
+};
+
 struct wh_moe_args {
     wh_expert_ptrs ex[WH_MAX_EXPERTS];
     float route_w[WH_MAX_EXPERTS];
-    uint32_t n_experts;            // routed experts, plus the shared one when has_shared
+    uint32_t n_experts;            // expert slots: routed ones, plus the shared one (the last) when has_shared
     uint32_t has_shared;           // the last expert slot is the shared expert
+    const wh_moe_dyn* dyn;         // null: ex / route_w above; else the slots' experts and weights live there
     uint32_t hidden, inter;        // w1/w3: inter x hidden, w2: hidden x inter
     uint32_t n_tokens;             // tokens sharing the same expert list
     const void* x;                 // [n_tokens][hidden], f32 or bf16
@@ -806,6 +817,128 @@ struct wh_moe_args {
     uint32_t* status;
     float* gu;                     // null, or [n_tokens][n_experts][2][inter]: gate and up captured
 };
+
+// Slot e's expert, route weight i and the number of routed slots summed, from
+// the kernel arguments or the device route list.  The device list is read
+// through the constant address space: with a wave-uniform index these are
+// scalar loads, which leave the vector-memory counters of the kernels that
+// count their own loads untouched.
+typedef __attribute__((address_space(4))) const wh_moe_dyn wh_moe_dyn_k;
+__device__ __forceinline__ wh_expert_ptrs wh_moe_ex(const wh_moe_args& a, uint32_t e) {
+    if (a.dyn) {
+        wh_moe_dyn_k* d = (wh_moe_dyn_k*)a.dyn;
+        wh_expert_ptrs r;
+        r.w1 = d->ex[e].w1;
+        r.s1 = d->ex[e].s1;
+        r.w3 = d->ex[e].w3;
+        r.s3 = d->ex[e].s3;
+        r.w2 = d->ex[e].w2;
+        r.s2 = d->ex[e].s2;
+        return r;
+    }
+    return a.ex[e];
+}
+__device__ __forceinline__ float wh_moe_w(const wh_moe_args& a, uint32_t i) {
+    if (a.dyn) return ((wh_moe_dyn_k*)a.dyn)->route_w[i];
+    return a.route_w[i];
+}
+__device__ __forceinline__ uint32_t wh_moe_nr(const wh_moe_args& a) {
+    if (a.dyn) return ((wh_moe_dyn_k*)a.dyn)->n_routed;
+    return a.n_experts - a.has_shared;
+}
+
+// Resolves a token's route list in device memory (ids, route weights and
+// count as the router writes them) against a layer's expert table
+// (table_n entries, null where nothing is resident) into *out: slots
+// [0, n_routed) are the routes in order, n_routed = min(count, n_slots);
+// the later routed slots, and ids with no resident expert (reported as
+// NotResident), get a resident expert's pointers - the first resolved
+// route, else the shared expert, else the table's first resident entry -
+// computed and never summed; the shared expert goes to slot n_slots.  One
+// wave; the host checks that some expert is resident.
+__global__ void __launch_bounds__(64) k_moe_resolve(const uint32_t* __restrict__ ids, const float* __restrict__ w,
+                                                    const uint32_t* __restrict__ count,
+                                                    const wh_expert_ptrs* __restrict__ table, uint32_t table_n,
+                                                    wh_expert_ptrs shared, uint32_t has_shared, uint32_t n_slots,
+                                                    wh_moe_dyn* __restrict__ out, uint32_t* status) {
+    __shared__ wh_expert_ptrs got[64];
+    const uint32_t L = threadIdx.x;
+    const uint32_t cnt = min(*count, n_slots);
+    bool ok = false;
+    wh_expert_ptrs p = {};
+    if (L < cnt) {
+        const uint32_t id = ids[L];
+        if (id < table_n) {
+            p = table[id];
+            ok = p.w1 != nullptr;
+        }
+        if (!ok) atomicOr(status, WH_ST_NOT_RESIDENT);
+    }
+    got[L] = p;
+    const uint64_t okm = __ballot(ok);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+    wh_expert_ptrs fb = shared;
+    if (okm) {
+        fb = got[__ffsll((long long)okm) - 1];
+    } else if (!has_shared) {
+        for (uint32_t base = 0; base < table_n; base += 64) {
+            const uint32_t j = base + L;
+            const bool r = j < table_n && table[j].w1 != nullptr;
+            const uint64_t m = __ballot(r);
+            if (m) {
+                fb = table[base + __ffsll((long long)m) - 1];
+                break;
+            }
+        }
+    }
+    if (L < n_slots) {
+        out->ex[L] = ok ? p : fb;
+        out->route_w[L] = L < cnt ? w[L] : 0.0f;
+    }
+    if (L == n_slots && has_shared) out->ex[L] = shared;
+    if (L == 0) out->n_routed = cnt;
+}
+
+// The ordered routed sum of one output row from the per-slot outputs yv
+// (E/compute.rs:1929-2030): route-weighted in route order with the weight
+// rules of valid_route_weight_sum (E/compute.rs:2014-2030), then shared +
+// routed (E/compute.rs:1929-1941); the shared expert is the last slot.
+// yv is indexed with compile-time indices only (unrolled, guarded loops), so
+// it stays in registers.
+__device__ __forceinline__ float wh_route_combine(const wh_moe_args& a, const float (&yv)[WH_MAX_EXPERTS]) {
+    const uint32_t nr = wh_moe_nr(a);
+    float o = 0.0f;
+    if (nr == 1) {
+        o = yv[0];
+    } else if (nr > 1) {
+        float sum = 0.0f;
+        bool valid = true;
+        for (uint32_t i = 0; i < nr; ++i) {
+            const float w = wh_moe_w(a, i);
+            if (!(fabsf(w) <= 3.4028235e38f && w >= 0.0f)) valid = false;
+            sum = sum + w;
+        }
+        if (sum <= 1.1920929e-07f) valid = false;
+        const float uniform = 1.0f / (float)nr;
+#pragma unroll
+        for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i) {
+            if (i < nr) {
+                const float w = valid ? wh_moe_w(a, i) / sum : uniform;
+                const float p = yv[i] * w;
+                o = o + p;
+            }
+        }
+    }
+    if (a.has_shared) {
+        float sh = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i)
+            if (i + 1 == a.n_experts) sh = yv[i];
+        o = nr == 0 ? sh : sh + o;
+    }
+    return o;
+}
 
 // The per-binade log2f thresholds of the act-quant scale, staged in LDS: a
 // table lookup in global memory after the weight loads would make the wave
@@ -959,7 +1092,7 @@ __global__ void __launch_bounds__(256) k_moe_gateup(wh_moe_args a) {
     const uint32_t row = rb * 16 + (oct >> 1);
     const bool up = oct & 1;
     const uint32_t G = a.hidden >> 5;
-    const wh_expert_ptrs ep = a.ex[e];
+    const wh_expert_ptrs ep = wh_moe_ex(a, e);
     const uint8_t* wrow = (up ? ep.w3 : ep.w1) + (size_t)row * (a.hidden >> 1);
     const uint8_t* srow = (up ? ep.s3 : ep.s1) + (size_t)row * G;
     float* xs = lds;
@@ -1076,45 +1209,13 @@ __device__ __forceinline__ void wh_moe_routed_sum(const wh_moe_args& a, uint32_t
     if (!*last || threadIdx.x >= 32) return;
     const uint32_t r_out = rb * 32 + threadIdx.x;
     const size_t t0 = (size_t)tok * a.n_experts * a.hidden;
-    const uint32_t nr = a.n_experts - a.has_shared;  // routed experts
     // every expert's row is requested before any is used: one round trip
     // to the coherent level instead of one per expert
     float yv[WH_MAX_EXPERTS];
 #pragma unroll
     for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i)
         yv[i] = i < a.n_experts ? wh_load_coherent(a.y + t0 + (size_t)i * a.hidden + r_out) : 0.0f;
-    float o = 0.0f;
-    if (nr == 1) {
-        o = yv[0];
-    } else if (nr > 1) {
-        // valid_route_weight_sum (E/compute.rs:2014-2030)
-        float sum = 0.0f;
-        bool valid = true;
-        for (uint32_t i = 0; i < nr; ++i) {
-            float w = a.route_w[i];
-            if (!(fabsf(w) <= 3.4028235e38f && w >= 0.0f)) valid = false;
-            sum = sum + w;
-        }
-        if (sum <= 1.1920929e-07f) valid = false;
-        const float uniform = 1.0f / (float)nr;
-#pragma unroll
-        for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i) {
-            if (i < nr) {
-                float w = valid ? a.route_w[i] / sum : uniform;
-                float p = yv[i] * w;
-                o = o + p;
-            }
-        }
-    }
-    if (a.has_shared) {
-        // hidden = shared(x); hidden += routed (E/compute.rs:1929-1941)
-        float sh = 0.0f;
-#pragma unroll
-        for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i)
-            if (i == nr) sh = yv[i];
-        o = nr == 0 ? sh : sh + o;
-    }
-    a.out[(size_t)tok * a.hidden + r_out] = o;
+    a.out[(size_t)tok * a.hidden + r_out] = wh_route_combine(a, yv);
     if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -1132,7 +1233,7 @@ __global__ void __launch_bounds__(256) k_moe_down(wh_moe_args a) {
     const uint32_t lane = threadIdx.x & 7, oct = threadIdx.x >> 3;
     const uint32_t row = rb * 32 + oct;
     const uint32_t G = a.inter >> 5;
-    const wh_expert_ptrs ep = a.ex[e];
+    const wh_expert_ptrs ep = wh_moe_ex(a, e);
     const uint8_t* wrow = ep.w2 + (size_t)row * (a.inter >> 1);
     const uint8_t* srow = ep.s2 + (size_t)row * G;
     float* xs = lds;

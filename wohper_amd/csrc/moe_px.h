@@ -248,7 +248,7 @@ __global__ void __launch_bounds__(kCols / 8, 1) k_moe_gateup_px(wh_moe_args a) {
     for (int i = 0; i < kTiles; ++i) {
         const uint32_t t = tile0 + ((uint32_t)i < nt ? (uint32_t)i : nt - 1);
         const uint32_t e = t / per_e, row = (t - e * per_e) * 16 + (L & 15);
-        const wh_expert_ptrs ep = a.ex[e];
+        const wh_expert_ptrs ep = wh_moe_ex(a, e);
         wrow[i] = (m ? ep.w3 : ep.w1) + (size_t)row * (kCols / 2);
         srow[i] = (m ? ep.s3 : ep.s1) + (size_t)row * kG + 32 * s;
     }
@@ -341,44 +341,6 @@ __global__ void __launch_bounds__(kCols / 8, 1) k_moe_gateup_px(wh_moe_args a) {
     WH_TL(0, 11);
 }
 
-// The ordered routed sum of one output row from the per-expert outputs yv
-// (E/compute.rs:1929-2030): route-weighted in route order with the weight
-// rules of valid_route_weight_sum, then shared + routed.
-// yv is indexed with compile-time indices only (unrolled, guarded loops), so
-// it stays in registers.
-__device__ __forceinline__ float wh_route_combine(const wh_moe_args& a, const float (&yv)[WH_MAX_EXPERTS]) {
-    const uint32_t nr = a.n_experts - a.has_shared;
-    float o = 0.0f;
-    if (nr == 1) {
-        o = yv[0];
-    } else if (nr > 1) {
-        float sum = 0.0f;
-        bool valid = true;
-        for (uint32_t i = 0; i < nr; ++i) {
-            const float w = a.route_w[i];
-            if (!(fabsf(w) <= 3.4028235e38f && w >= 0.0f)) valid = false;
-            sum = sum + w;
-        }
-        if (sum <= 1.1920929e-07f) valid = false;
-        const float uniform = 1.0f / (float)nr;
-#pragma unroll
-        for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i) {
-            if (i < nr) {
-                const float w = valid ? a.route_w[i] / sum : uniform;
-                const float p = yv[i] * w;
-                o = o + p;
-            }
-        }
-    }
-    if (a.has_shared) {
-        float sh = 0.0f;
-#pragma unroll
-        for (uint32_t i = 0; i < WH_MAX_EXPERTS; ++i)
-            if (i == nr) sh = yv[i];
-        o = nr == 0 ? sh : sh + o;
-    }
-    return o;
-}
 
 // Down + routed sum, inter = 2048: grid (hidden / 16, n_tokens), 512
 // threads.  Unit u = (expert u / 4, column quarter u % 4 of 512 = blocks
@@ -423,8 +385,9 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
         uint32_t u = wave + 8 * k;
         u = u < n_units ? u : n_units - 1;
         const uint32_t e = u >> 2, qt = u & 3;
-        wl[k] = a.ex[e].w2 + (size_t)row * (kCols / 2) + 256 * qt + 64 * (g & 1) + 32 * (g >> 1);
-        sr[k] = a.ex[e].s2 + (size_t)row * kG + 16 * qt;
+        const wh_expert_ptrs ep = wh_moe_ex(a, e);
+        wl[k] = ep.w2 + (size_t)row * (kCols / 2) + 256 * qt + 64 * (g & 1) + 32 * (g >> 1);
+        sr[k] = ep.s2 + (size_t)row * kG + 16 * qt;
     }
     wh_issue_barrier();
     wh_mx_raw ring[kDepth];

@@ -241,7 +241,7 @@ __global__ void __launch_bounds__(512, 1) k_moe_gateup_tok(wh_moe_args a) {
     for (int i = 0; i < kTiles; ++i) {
         const uint32_t t = tile0 + ((uint32_t)i < nt ? (uint32_t)i : nt - 1);
         const uint32_t e = t / per_e, row = (t - e * per_e) * 16;
-        const wh_expert_ptrs ep = a.ex[e];
+        const wh_expert_ptrs ep = wh_moe_ex(a, e);
         wrow[i] = (m ? ep.w3 : ep.w1) + (size_t)row * (kCols / 2) + 512 * s;
         srow[i] = (m ? ep.s3 : ep.s1) + (size_t)row * kG + 32 * s;
     }
@@ -415,8 +415,9 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_tok(wh_moe_args a) {
         uint32_t u = wave + 8 * k;
         u = u < n_units ? u : n_units - 1;
         const uint32_t e = u >> 2, qt = u & 3;
-        wl[k] = a.ex[e].w2 + (size_t)row0 * (kIn / 2) + 256 * qt;
-        sl[k] = a.ex[e].s2 + (size_t)row0 * kGi + 16 * qt;
+        const wh_expert_ptrs ep = wh_moe_ex(a, e);
+        wl[k] = ep.w2 + (size_t)row0 * (kIn / 2) + 256 * qt;
+        sl[k] = ep.s2 + (size_t)row0 * kGi + 16 * qt;
         hl[k] = (const uint8_t*)(htok + (size_t)e * kIn + 512 * qt);
     }
     // DMAs per wave: the h quarters of its units (2 each), the units'

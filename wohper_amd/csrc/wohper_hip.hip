@@ -251,6 +251,7 @@ struct LayerTable {
     bool valid = false;
     bool fast = false;  // every resident expert has one fast shape
     bool zero_scale = false;  // some resident expert has a UE8M0 scale byte 0
+    uint32_t resident = 0;    // ids with a resident expert
     size_t hidden = 0, inter = 0;
 };
 
@@ -294,6 +295,7 @@ struct wh_ctx {
     uint32_t moe_mfma_min = 1;              // batch experts with this many tokens use MFMA (0: never)
     uint32_t fp8_mm_min = 4;                // multi-input FP8 GEMVs with this many inputs use MFMA
     Scratch fp8mm_ws, fp8mm_cnt;            // their partial tiles and arrival counters
+    Scratch moe_dyn;                        // a device route list resolved for the experts (wh_moe_dyn)
     bool exact = true;                      // routed experts in the reference's summation order
     int token_kernels = 1;                  // MFMA token kernels: bit 0 gate/up, bit 1 down on k_*_tok (else k_*_px)
     bool capture_gu = false;                // routed experts keep gate/up in `gu` (test support)
@@ -312,7 +314,7 @@ struct wh_ctx {
     hipStream_t base_stream = nullptr, cap_stream = nullptr;
     std::vector<Scratch*> scratch() {
         return {&x_in, &y_out, &h, &ybuf, &cnt_y, &tmp, &batch, &routes, &bout, &gu, &relayout, &rtr, &rtr_cnt,
-                &mla, &hcs, &fp8mm_ws, &fp8mm_cnt};
+                &mla, &hcs, &fp8mm_ws, &fp8mm_cnt, &moe_dyn};
     }
 };
 
@@ -887,14 +889,23 @@ int moe_bufs_ctx(wh_ctx* c, size_t n, size_t n_tokens, size_t hidden, size_t int
 // Launches the fast routed-expert kernels for n_tokens rows of x sharing one
 // route list.  stages: bit 0 = gate/up + SwiGLU, bit 1 = down + routed sum.
 // record: keep the call's sizes for the debug reads of the context buffers.
+// A route list in device memory (wh_moe_dyn) instead of ev / route_w: the
+// experts' shapes and whether any of them holds a UE8M0 scale byte 0.
+struct MoeDyn {
+    const wh_moe_dyn* p = nullptr;
+    size_t hidden = 0, inter = 0;
+    bool zero_scale = false;
+};
+
 int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_t n, bool has_shared,
                     const void* x_dev, int x_bf16, size_t n_tokens, float* out_dev, unsigned stages,
-                    const MoeBufs& bufs, bool record) {
-    const size_t hidden = ev[0].w1->cols, inter = ev[0].w1->rows;
+                    const MoeBufs& bufs, bool record, const MoeDyn* dyn = nullptr) {
+    const size_t hidden = dyn ? dyn->hidden : ev[0].w1->cols, inter = dyn ? dyn->inter : ev[0].w1->rows;
     if (((uintptr_t)x_dev & 15) || ((uintptr_t)out_dev & 3)) return WH_INVALID_ARGUMENT;
     wh_moe_args a;
     std::memset(&a, 0, sizeof a);
-    for (size_t i = 0; i < n; ++i) {
+    if (dyn) a.dyn = dyn->p;
+    for (size_t i = 0; i < n && !dyn; ++i) {
         a.ex[i].w1 = ev[i].w1->w;
         a.ex[i].s1 = (const uint8_t*)ev[i].w1->s;
         a.ex[i].w3 = ev[i].w3->w;
@@ -919,7 +930,8 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
     if (record)
         c->tok_last_n = n, c->tok_last_tokens = n_tokens, c->tok_last_hidden = hidden, c->tok_last_inter = inter;
     bool sk = moe_mfma(c, hidden, inter);
-    for (size_t i = 0; i < n && sk; ++i) sk = !expert_zero_scale(ev[i]);
+    if (dyn) sk = sk && !dyn->zero_scale;
+    for (size_t i = 0; i < n && sk && !dyn; ++i) sk = !expert_zero_scale(ev[i]);
     // the LDS-DMA kernels (moe_tok.h): hidden 4096, inter 2048, up to 8 experts
     const bool tk_shape = sk && hidden == 4096 && inter == 2048 && n <= 8;
     const bool tk = tk_shape && (c->token_kernels & 1), tkd = tk_shape && (c->token_kernels & 2);
@@ -1159,10 +1171,12 @@ int layer_table(wh_ctx* c, uint32_t layer, LayerTable** out) {
     std::memset(host.data(), 0, n * sizeof(wh_expert_ptrs));
     bool fast = n > 0 && n < WH_BATCH_MAX_TABLE;  // one id stays free for the shared expert
     bool zero_scale = false;
+    uint32_t resident = 0;
     size_t hidden = 0, inter = 0;
     for (auto it = lo; it != hi; ++it) {
         ExpertView v;
         if (resolve_expert(c, layer, it->first.second, &v) != WH_OK) continue;  // released tensors
+        ++resident;
         if (hidden == 0) {
             hidden = v.w1->cols;
             inter = v.w1->rows;
@@ -1190,6 +1204,7 @@ int layer_table(wh_ctx* c, uint32_t layer, LayerTable** out) {
     t.n = n;
     t.fast = fast;
     t.zero_scale = zero_scale;
+    t.resident = resident;
     t.hidden = hidden;
     t.inter = inter;
     t.valid = true;
@@ -2855,6 +2870,63 @@ int wh_routed_and_shared_experts_async(wh_ctx* c, const wh_expert_route* routes,
     float wts[WH_MAX_EXPERTS];
     WH_TRY(routed_shared_common(c, routes, n, shared_layer, shared_expert, ev, wts));
     return moe_forward(c, ev, wts, n + 1, true, x_dev, x_bf16, n_tokens, out_dev);
+}
+
+// The experts of one token whose route list is in device memory: resolved
+// on the device (k_moe_resolve), then the fast kernels with the list as
+// their wh_moe_dyn.
+int moe_dev_routes(wh_ctx* c, uint32_t layer_id, const uint32_t* ids_dev, const float* w_dev,
+                   const uint32_t* count_dev, size_t n_slots, uint32_t shared_layer, uint32_t shared_expert,
+                   const void* x_dev, int x_bf16, float* out_dev) {
+    LayerTable* t = nullptr;
+    WH_TRY(layer_table(c, layer_id, &t));
+    const bool has_shared = shared_expert != WH_NO_SHARED_EXPERT;
+    ExpertView sh;
+    if (has_shared) WH_TRY(resolve_expert(c, shared_layer, shared_expert, &sh));
+    if (t->resident == 0 && !has_shared) return WH_NOT_RESIDENT;
+    if (n_slots == 0 || n_slots + (has_shared ? 1 : 0) > WH_MAX_EXPERTS) return WH_INVALID_ARGUMENT;
+    // every resident expert (and the shared one) on one fast shape
+    size_t hidden = t->hidden, inter = t->inter;
+    bool fast = t->resident ? t->fast : true;
+    if (has_shared) {
+        if (!t->resident) hidden = sh.w1->cols, inter = sh.w1->rows;
+        fast = fast && expert_fast(sh) && sh.w1->cols == hidden && sh.w1->rows == inter && sh.w2->rows == hidden;
+    }
+    if (!fast) return WH_UNSUPPORTED;
+    WH_HIP(c->moe_dyn.ensure(sizeof(wh_moe_dyn), false));
+    wh_moe_dyn* dyn = c->moe_dyn.as<wh_moe_dyn>();
+    wh_expert_ptrs shp = {};
+    if (has_shared) {
+        shp.w1 = sh.w1->w;
+        shp.s1 = (const uint8_t*)sh.w1->s;
+        shp.w3 = sh.w3->w;
+        shp.s3 = (const uint8_t*)sh.w3->s;
+        shp.w2 = sh.w2->w;
+        shp.s2 = (const uint8_t*)sh.w2->s;
+    }
+    k_moe_resolve<<<1, 64, 0, c->stream>>>(ids_dev, w_dev, count_dev, t->dev, t->n, shp, has_shared ? 1u : 0u,
+                                          (uint32_t)n_slots, dyn, c->status);
+    WH_HIP(hipGetLastError());
+    const size_t n = n_slots + (has_shared ? 1 : 0);
+    MoeBufs bufs;
+    WH_TRY(moe_bufs_ctx(c, n, 1, hidden, inter, &bufs));
+    MoeDyn md;
+    md.p = dyn;
+    md.hidden = hidden;
+    md.inter = inter;
+    md.zero_scale = t->zero_scale || (has_shared && expert_zero_scale(sh));
+    return moe_launch_fast(c, nullptr, nullptr, n, has_shared, x_dev, x_bf16, 1, out_dev, 3u, bufs, true, &md);
+}
+
+int wh_routed_and_shared_experts_dev_async(wh_ctx* c, uint32_t layer_id, const uint32_t* ids_dev,
+                                           const float* weights_dev, const uint32_t* count_dev, size_t n_slots,
+                                           uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
+                                           int x_is_bf16, float* out_dev) {
+    if (!c || !ids_dev || !weights_dev || !count_dev || !x_dev || !out_dev) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    return moe_dev_routes(c, layer_id, ids_dev, weights_dev, count_dev, n_slots, shared_layer, shared_expert, x_dev,
+                          x_is_bf16, out_dev);
 }
 
 int wh_routed_and_shared_experts_noalloc_async(wh_ctx* c, const wh_expert_route* routes, size_t n,
