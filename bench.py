@@ -304,6 +304,116 @@ def _fp8_decode_layer(ctx, steps: int):
     return res
 
 
+def decode_layer(ctx, n_layers: int, steps: int, graph: bool = True) -> dict:
+    """The whole device decode layer (wh_deepseek_mhc_layer_async: hc_pre ->
+    norm -> MLA -> hc_post -> hc_pre -> norm -> router -> shared + routed
+    experts -> hc_post) at the model's shapes (hc 4, hidden 4096, 64 heads of
+    448 + 64, q_lora 1024, 8 output groups of 1024; bf16 router of 256
+    experts, top-6, route_scale 1.5, + the shared expert), on the n_layers
+    resident layers of the headline (their 256 routed experts), each with its
+    own MLA tensors, mHC parameters, norms and router.  A step runs every
+    layer once at position 127 (a full 128-row window); timed as one HIP
+    graph per step replayed back to back, and as a host loop, in both
+    numerics modes.  Nothing is read back between the layers: the router's
+    output feeds the experts on the device."""
+    import wohper_amd
+    from wohper_amd import model_format as mf
+    from wohper_amd import workloads as wl
+
+    hc, heads, nope, rope, q_lora, groups, o_lora = 4, 64, 448, 64, 1024, 8, 1024
+    head_dim, pos, cap = nope + rope, 127, 128
+    rng = np.random.default_rng(71)
+    keep, handles = [], []
+
+    def put(a):
+        a = np.ascontiguousarray(a)
+        p = ctx.device_alloc(max(a.nbytes, 4))
+        ctx.to_device(p, a)
+        keep.append(p)
+        return p
+
+    def bf16w(n):
+        return ((1.0 + 0.1 * rng.standard_normal(n).astype(np.float32)).view(np.uint32) >> 16).astype(np.uint16)
+
+    shapes = {"wq_a": (q_lora, wl.HIDDEN), "wq_b": (heads * head_dim, q_lora), "wkv": (head_dim, wl.HIDDEN),
+              "wo_a": (groups * o_lora, heads * head_dim // groups), "wo_b": (wl.HIDDEN, groups * o_lora)}
+    layers, kvs, hs = [], [], []
+    mix = (2 + hc) * hc
+    for L in range(n_layers):
+        ctx.store_expert_synthetic(L, wl.N_ROUTED, wl.HIDDEN, wl.INTER, 2)  # the layer's shared expert
+        t = {n: ctx.store_fp8_synthetic(r, c, 5, 100 * L + i, wl.fp8_block_scales(7 + 31 * L + i, r, c))
+             for i, (n, (r, c)) in enumerate(shapes.items())}
+        handles += list(t.values())
+        mla = wohper_amd.WhMlaLayer(L, heads, nope, rope, groups, o_lora, t["wq_a"], t["wq_b"], t["wkv"], t["wo_a"],
+                                    t["wo_b"], put(bf16w(q_lora)), put(bf16w(head_dim)),
+                                    put(rng.standard_normal(heads).astype(np.float32)))
+        gate = ((rng.standard_normal((wl.N_ROUTED, wl.HIDDEN)).astype(np.float32) * 0.02).view(np.uint32) >> 16)
+        bias = (rng.standard_normal(wl.N_ROUTED) * 0.05).astype(np.float32)
+        blk = mf.build_synthetic_quant_block([
+            mf.SyntheticTensor(f"layers.{L}.ffn.gate.weight", 9, (wl.N_ROUTED, wl.HIDDEN),
+                               gate.astype(np.uint16).tobytes(), 11, 2404),
+            mf.SyntheticTensor(f"layers.{L}.ffn.gate.bias", 9, (wl.N_ROUTED,), bias.tobytes(), 12, 2405)])
+        ctx.store_router(L, blk, wl.HIDDEN)
+        d = wohper_amd.WhMhcLayer()
+        d.hc, d.hidden, d.sinkhorn_iters, d.hc_eps = hc, wl.HIDDEN, 20, 1e-6
+        fns = [(rng.standard_normal((mix, hc * wl.HIDDEN)) / np.sqrt(hc * wl.HIDDEN)).astype(np.float32)
+               for _ in range(2)]
+        d.hc_attn_fn, d.hc_ffn_fn = put(fns[0]), put(fns[1])
+        d.hc_attn_scale, d.hc_ffn_scale = (put((0.5 + rng.random(3)).astype(np.float32)) for _ in range(2))
+        d.hc_attn_base, d.hc_ffn_base = (put((rng.standard_normal(mix) * 0.5).astype(np.float32)) for _ in range(2))
+        d.attn_norm_bf16, d.ffn_norm_bf16 = put(bf16w(wl.HIDDEN)), put(bf16w(wl.HIDDEN))
+        d.attn = mla
+        d.layer_id, d.active, d.available_dev, d.n_available = L, wl.TOPK, None, 0
+        d.route = wohper_amd.Context.route_options(wohper_amd.ROUTER_SQRT_SOFTPLUS, 1.5)
+        d.shared_layer, d.shared_expert = L, wl.N_ROUTED
+        layers.append(d)
+        kvs.append(put((rng.standard_normal((cap, head_dim)) * 0.3).astype(np.float32)))
+        hs.append(put((rng.standard_normal(hc * wl.HIDDEN) * 0.5).astype(np.float32)))
+
+    def step():
+        for L in range(n_layers):
+            ctx.deepseek_mhc_layer_async(layers[L], pos, hs[L], kvs[L], head_dim, cap)
+
+    mla_bytes = sum(r * c + (r // 128) * (c // 128) * 4 for r, c in shapes.values())
+    layer_bytes = (mla_bytes + wl.N_ROUTED * wl.HIDDEN * 2 + wl.N_ROUTED * 4 + (wl.TOPK + 1) * wl.FP4_EXPERT_BYTES +
+                   2 * mix * hc * wl.HIDDEN * 4 + cap * head_dim * 4)
+    res = {"workload": f"{n_layers} decode layers at batch 1, position {pos}: hc_pre, norm, MLA attention (FP8 "
+                       "projections, 128-row window), hc_post, hc_pre, norm, bf16 router 256x4096 top-6, shared + "
+                       "6 routed FP4 experts read from the router's device output, hc_post",
+           "bytes_per_layer": layer_bytes}
+    for exact in (False, True):
+        ctx.set_exact_numerics(exact)
+        step()
+        ctx.synchronize()
+        ctx.timer_start()
+        for _ in range(steps):
+            step()
+        loop_us = ctx.timer_stop() / steps / n_layers
+        ctx.synchronize()
+        r = {"host_loop_layer_us": round(loop_us, 2)}
+        if graph:
+            g = ctx.graph_capture(step)
+            ctx.graph_launch(g)
+            ctx.synchronize()
+            ctx.timer_start()
+            for _ in range(steps):
+                ctx.graph_launch(g)
+            us = ctx.timer_stop() / steps / n_layers
+            ctx.synchronize()
+            ctx.graph_release(g)
+            r["layer_us"] = round(us, 2)
+        else:
+            us = loop_us
+        r["GBps"] = round(layer_bytes / (us * 1e-6) / 1e9, 1)
+        r["frac_of_hbm_peak"] = round(layer_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        res["exact" if exact else "order_free"] = r
+    for p in keep:
+        ctx.device_free(p)
+    for t in handles:
+        ctx.release(t)
+    return res
+
+
 def router(ctx, steps: int):
     """The DeepSeek-V4 router of a layer (bf16 gate 256x4096, f32 bias,
     sqrt-softplus, top-6, route_scale 1.5) on device pointers, over 8
@@ -932,6 +1042,9 @@ def main():
         ctx.set_exact_numerics(args.exact)
         log(f"fp8 decode layer, batch 16: {extra['fp8_decode_layer_batch16']}")
     if not args.no_aux:
+        extra["decode_layer"] = decode_layer(ctx, args.layers, 20, not args.no_graph)
+        ctx.set_exact_numerics(args.exact)
+        log(f"decode layer: {extra['decode_layer']}")
         extra["read_floor"] = read_floor(ctx)
         log(f"read floor: {extra['read_floor']}")
         extra["router"] = router(ctx, 400)

@@ -115,6 +115,32 @@ pub struct WhMlaLayer {
     pub sink: *const f32,
 }
 
+/// One DeepSeek-V4 mHC decode layer on the device (wh_mhc_layer).
+#[repr(C)]
+#[derive(Clone, Copy, Debug)]
+pub struct WhMhcLayer {
+    pub hc: usize,
+    pub hidden: usize,
+    pub sinkhorn_iters: usize,
+    pub hc_eps: f32,
+    pub hc_attn_fn: *const f32,
+    pub hc_attn_scale: *const f32,
+    pub hc_attn_base: *const f32,
+    pub hc_ffn_fn: *const f32,
+    pub hc_ffn_scale: *const f32,
+    pub hc_ffn_base: *const f32,
+    pub attn_norm_bf16: *const u16,
+    pub ffn_norm_bf16: *const u16,
+    pub attn: WhMlaLayer,
+    pub layer_id: u32,
+    pub active: usize,
+    pub available_dev: *const u32,
+    pub n_available: usize,
+    pub route: WhRouteOptions,
+    pub shared_layer: u32,
+    pub shared_expert: u32,
+}
+
 pub const WH_SCALE_UE8M0: c_int = 0;
 pub const WH_SCALE_F32: c_int = 1;
 pub const WH_ROUTER_RAW_LOGITS: i32 = 0;
@@ -264,4 +290,7 @@ extern "C" {
     pub fn wh_hc_post_async(ctx: *mut WhCtx, y_dev: *const f32, residual_dev: *const f32,
                             post_dev: *const f32, comb_dev: *const f32, out_dev: *mut f32, hc: usize,
                             hidden: usize) -> c_int;
+    pub fn wh_deepseek_mhc_layer_async(ctx: *mut WhCtx, layer: *const WhMhcLayer, token_pos: usize,
+                                       hidden_dev: *mut f32, kv_cache_dev: *mut f32, kv_stride: usize,
+                                       kv_capacity: usize, comp_dev: *const f32, n_comp: usize) -> c_int;
 }

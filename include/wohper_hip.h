@@ -624,7 +624,10 @@ int wh_deepseek_rope_for_layer(uint32_t physical_layer, float* theta, wh_yarn* y
 /* rms_norm_in_place (E/compute.rs:7110-7122) of each of `rows` rows of n
  * values (weight_bf16_dev NULL), or apply_weighted_rms_norm
  * (E/compute.rs:3077-3107) with a bf16 weight of n values; eps 1e-6.
- * out_dev may equal x_dev.  n <= 4096. */
+ * out_dev may equal x_dev.  n <= 4096.  With exact numerics (the default)
+ * the sum of squares runs in the reference's order, bit-identical; with
+ * exact numerics off it is a fixed tree (the same value up to rounding,
+ * reproducible), as are the norms inside wh_mla_attention_decode_async. */
 int wh_rms_norm_async(wh_ctx* ctx, const float* x_dev, float* out_dev, size_t rows, size_t n,
                       const uint16_t* weight_bf16_dev);
 
@@ -715,6 +718,52 @@ int wh_hc_pre_async(wh_ctx* ctx, const float* fn_dev, const float* scale_dev, co
  * d].  Bit-identical to the reference. */
 int wh_hc_post_async(wh_ctx* ctx, const float* y_dev, const float* residual_dev, const float* post_dev,
                      const float* comb_dev, float* out_dev, size_t hc, size_t hidden);
+
+/* ------------------------------------------------------------------
+ * One DeepSeek-V4 decode layer on the device: compute_layer_deepseek_mhc
+ * (E/compute.rs:1448-1480) with the router between its two phases as the
+ * engine runs them (E/server/generation.rs:719-836).  On the hc copies of
+ * the hidden state at hidden_dev (hc * hidden floats, updated in place):
+ *   attention sub-block (phase 1, E/compute.rs:1552-1605): y = hc_pre(hc_attn,
+ *     hidden); y = rms_norm(y, attn_norm); y = MLA attention(y) (as
+ *     wh_mla_attention_decode_async, with the KV cache arguments below);
+ *     hidden' = hc_post(y, hidden);
+ *   ffn input (E/compute.rs:1607-1630): g = rms_norm(hc_pre(hc_ffn, hidden'),
+ *     ffn_norm);
+ *   router (route_experts_from_dense_block, E/compute.rs:2129-2268) of
+ *     layer_id on g, as wh_route_experts_async;
+ *   MoE (phase 2, E/compute.rs:1641-1700): z = shared(g) + routed experts of
+ *     layer_id on the router's list (wh_routed_and_shared_experts_dev_async);
+ *     hidden = hc_post(z, hidden').
+ * Every step is the kernel of its own entry point, so the layer is
+ * bit-identical to the reference under exact numerics; with exact numerics
+ * off the FP8 projections, the expert matvecs and hc_pre's sums take the
+ * order-free kernels (the router keeps the reference order).  Nothing is
+ * read back to the host: the whole layer can be captured (wh_graph_begin).
+ * hidden_dev 16-byte aligned; the norm weights are bf16 (NULL: plain RMS
+ * norm); available_dev / n_available as in wh_route_experts_async. */
+typedef struct {
+    size_t hc, hidden, sinkhorn_iters;
+    float hc_eps;
+    const float* hc_attn_fn;     /* device [(2 + hc) * hc][hc * hidden] */
+    const float* hc_attn_scale;  /* device [3] */
+    const float* hc_attn_base;   /* device [(2 + hc) * hc] */
+    const float* hc_ffn_fn;
+    const float* hc_ffn_scale;
+    const float* hc_ffn_base;
+    const uint16_t* attn_norm_bf16;  /* input_layernorm [hidden] or NULL */
+    const uint16_t* ffn_norm_bf16;   /* post_attention_layernorm [hidden] or NULL */
+    wh_mla_layer attn;
+    uint32_t layer_id;           /* router and routed experts */
+    size_t active;               /* experts per token */
+    const uint32_t* available_dev;
+    size_t n_available;
+    wh_route_options route;
+    uint32_t shared_layer, shared_expert;  /* WH_NO_SHARED_EXPERT: none */
+} wh_mhc_layer;
+int wh_deepseek_mhc_layer_async(wh_ctx* ctx, const wh_mhc_layer* layer, size_t token_pos, float* hidden_dev,
+                                float* kv_cache_dev, size_t kv_stride, size_t kv_capacity, const float* comp_dev,
+                                size_t n_comp);
 
 #ifdef __cplusplus
 }

@@ -483,3 +483,34 @@ def hc_post(y, residual, post, comb, hc: int, hidden: int):
     out = np.zeros(hc * hidden, np.float32)
     lib().or_hc_post(_pf(_f(y)), _pf(_f(residual)), _pf(_f(post)), _pf(_f(comb)), _pf(out), hc, hidden)
     return out
+
+
+# ------------------------------------------------------------ decode layer
+
+def mhc_decode_layer(hidden_hc, hc: int, hidden: int, hc_attn, hc_ffn, attn_norm, ffn_norm, mla: dict, gate_bits,
+                     bias, active: int, route_scale: float, moe, token_pos: int, kv_cache, comp=None,
+                     iters: int = 20, eps: float = 1e-6):
+    """compute_layer_deepseek_mhc (E/compute.rs:1448-1480) for one decode
+    position, with the router between its phases as the engine runs them
+    (E/server/generation.rs:719-836):
+      phase 1 (E/compute.rs:1552-1630): residual = hidden; y = hc_pre(hc_attn);
+      y = rms_norm(y, attn_norm); y = MLA(y); hidden = hc_post(y, residual);
+      g = rms_norm(hc_pre(hc_ffn, hidden), ffn_norm);
+      router (route_experts_from_dense_block, E/compute.rs:2129-2268) on g:
+      bf16 gate GEMV, sqrt-softplus, biased top-`active`;
+      phase 2 (E/compute.rs:1641-1700): z = moe(ids, weights, g) (shared +
+      routed experts); hidden = hc_post(z, hidden after phase 1).
+    hc_attn / hc_ffn: (fn, scale, base); mla: the keyword arguments of
+    mla_attention_decode besides x, token_pos, kv_cache and comp.  Returns
+    (new hidden, ids, weights); kv_cache is updated at token_pos."""
+    residual = _f(hidden_hc).copy()
+    y, _, post, comb, _ = hc_pre(*hc_attn, residual, hc, hidden, iters, eps)
+    y = rms_norm(y, attn_norm)
+    y = mla_attention_decode(y, token_pos=token_pos, kv_cache=kv_cache, comp=comp, **mla)
+    h = hc_post(y, residual, post, comb, hc, hidden)
+    g, _, post2, comb2, _ = hc_pre(*hc_ffn, h, hc, hidden, iters, eps)
+    g = rms_norm(g, ffn_norm)
+    ids, w = route_select(bf16_gemv(gate_bits, g), active, None, bias, ROUTER_SQRT_SOFTPLUS, route_scale)
+    z = moe(ids, w, g)
+    return hc_post(z, h, post2, comb2, hc, hidden), ids, w
+

@@ -77,6 +77,32 @@ def test_rms_norm_bit_exact(ctx, oracle, dev, rows, n, weighted):
     assert np.array_equal(bits(dev.get(xp, (rows, n))), bits(oracle.rms_norm(x)))
 
 
+@pytest.mark.parametrize("rows,n", [(1, 4096), (64, 512), (3, 7)])
+def test_rms_norm_tree_within_tolerance(ctx, oracle, dev, rows, n):
+    """Exact numerics off: the sum of squares in a fixed tree changes only
+    its rounding.  Both orders of n positive terms are within (n - 1) u of
+    the exact sum (u = 2^-24), the square root halves that, and the two
+    products after it add a rounding each: every value stays within
+    (0.5 (n + 16) + 4) u relative of the reference's, and runs reproduce each
+    other bit for bit."""
+    rng = np.random.default_rng(rows + n)
+    x = (rng.standard_normal((rows, n)) * np.exp2(rng.integers(-6, 6, (rows, 1)))).astype(np.float32)
+    w = _bf16_weights(rng, n)
+    xp, yp = dev.put(x), dev.empty(x.nbytes)
+    ctx.set_exact_numerics(False)
+    try:
+        ctx.rms_norm_async(xp, yp, rows, n, dev.put(w))
+        ctx.synchronize()
+        got = dev.get(yp, (rows, n))
+        ctx.rms_norm_async(xp, yp, rows, n, dev.put(w))
+        ctx.synchronize()
+        assert np.array_equal(bits(got), bits(dev.get(yp, (rows, n))))
+    finally:
+        ctx.set_exact_numerics(True)
+    want = oracle.rms_norm(x, w).astype(np.float64)
+    assert np.all(np.abs(got - want) <= (0.5 * (n + 16) + 4) * 2.0 ** -24 * np.abs(want) + 1e-30)
+
+
 @pytest.mark.parametrize("layer", [0, 2])
 def test_rope_bit_exact(ctx, oracle, dev, layer):
     theta, yarn = wohper_amd.deepseek_rope_for_layer(layer)

@@ -92,7 +92,7 @@ EXPORTED = (
     "wh_act_quant_dequant_async", "wh_window_attention_async", "wh_mla_attention_decode_async",
     "wh_hc_split_sinkhorn_async", "wh_hc_pre_async", "wh_hc_post_async",
     "wh_graph_begin", "wh_graph_end", "wh_graph_launch", "wh_graph_release",
-    "wh_routed_and_shared_experts_dev_async",
+    "wh_routed_and_shared_experts_dev_async", "wh_deepseek_mhc_layer_async",
 )
 
 ROUTER_RAW_LOGITS = 0
@@ -151,6 +151,16 @@ class WhRouteOptions(ctypes.Structure):
     _fields_ = [("math", ctypes.c_int32), ("route_scale", ctypes.c_float), ("hash_token_id", ctypes.c_int64)]
 
 
+class WhMhcLayer(ctypes.Structure):
+    _fields_ = [("hc", ctypes.c_size_t), ("hidden", ctypes.c_size_t), ("sinkhorn_iters", ctypes.c_size_t),
+                ("hc_eps", ctypes.c_float), ("hc_attn_fn", ctypes.c_void_p), ("hc_attn_scale", ctypes.c_void_p),
+                ("hc_attn_base", ctypes.c_void_p), ("hc_ffn_fn", ctypes.c_void_p), ("hc_ffn_scale", ctypes.c_void_p),
+                ("hc_ffn_base", ctypes.c_void_p), ("attn_norm_bf16", ctypes.c_void_p),
+                ("ffn_norm_bf16", ctypes.c_void_p), ("attn", WhMlaLayer), ("layer_id", ctypes.c_uint32),
+                ("active", ctypes.c_size_t), ("available_dev", ctypes.c_void_p), ("n_available", ctypes.c_size_t),
+                ("route", WhRouteOptions), ("shared_layer", ctypes.c_uint32), ("shared_expert", ctypes.c_uint32)]
+
+
 class WhExpertPackEntry(ctypes.Structure):
     _fields_ = [("layer_id", ctypes.c_uint32), ("expert_id", ctypes.c_uint32), ("offset", ctypes.c_uint64),
                 ("disk_bytes", ctypes.c_uint64), ("payload_bytes", ctypes.c_uint64)]
@@ -199,6 +209,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_stream_status": (c.c_int, [vp]),
         "wh_routed_and_shared_experts_dev_async": (c.c_int, [vp, c.c_uint32, vp, vp, vp, sz, c.c_uint32, c.c_uint32,
                                                             vp, c.c_int, vp]),
+        "wh_deepseek_mhc_layer_async": (c.c_int, [vp, c.POINTER(WhMhcLayer), sz, vp, vp, sz, sz, vp, sz]),
         "wh_graph_begin": (c.c_int, [vp]),
         "wh_graph_end": (c.c_int, [vp, c.POINTER(c.c_uint64)]),
         "wh_graph_launch": (c.c_int, [vp, c.c_uint64]),
@@ -743,6 +754,15 @@ class Context:
         _check(self.lib.wh_mla_attention_decode_async(self._h, ctypes.byref(layer), token_pos, hidden_ptr, kv_ptr,
                                                       kv_stride, kv_capacity, comp_ptr or None, n_comp),
                "mla_attention_decode_async")
+
+    def deepseek_mhc_layer_async(self, layer: "WhMhcLayer", token_pos: int, hidden_ptr: int, kv_ptr: int,
+                                 kv_stride: int, kv_capacity: int, comp_ptr: int = 0, n_comp: int = 0):
+        """One decode layer (hc_pre -> norm -> MLA -> hc_post -> hc_pre ->
+        norm -> router -> shared + routed experts -> hc_post) on the hc
+        copies of the hidden state at hidden_ptr, in place."""
+        _check(self.lib.wh_deepseek_mhc_layer_async(self._h, ctypes.byref(layer), token_pos, hidden_ptr, kv_ptr,
+                                                    kv_stride, kv_capacity, comp_ptr or None, n_comp),
+               "deepseek_mhc_layer_async")
 
     # ------------------------------------------------------------------ mHC
     def hc_split_sinkhorn_async(self, mixes_ptr: int, scale_ptr: int, base_ptr: int, hc: int, iters: int,

@@ -164,6 +164,53 @@ __global__ void __launch_bounds__(256) k_hc_finish(wh_hc_args a) {
         a.post[t] = 2.0f * wh_sigmoid(mixes[t + hc] * a.scale[1] + a.base[t + hc]);
     }
     const uint32_t n_ops = a.iters ? 2 * a.iters - 1 : 1;
+    if (hc == 4) {
+        // DeepSeek-V4's hc: comb[j][k] in lane 4j + k of each 16-lane row.
+        // A lane gathers its row with DPP quad broadcasts and its column
+        // with the three row rotations by 4, 8 and 12 lanes; which row each
+        // rotation brings is read off the rotated lane index, so the adds
+        // keep the reference's order with no assumption on the rotation's
+        // direction.
+        const uint32_t j = (t >> 2) & 3;
+        const uint32_t r1 = ((uint32_t)__builtin_amdgcn_mov_dpp((int)t, 0x124, 0xf, 0xf, false) >> 2) & 3;
+        const uint32_t r2 = ((uint32_t)__builtin_amdgcn_mov_dpp((int)t, 0x128, 0xf, 0xf, false) >> 2) & 3;
+        auto row_q = [](float x, auto q) {
+            constexpr int kQ = decltype(q)::value;
+            return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kQ * 0x55, 0xf, 0xf, false));
+        };
+        auto row_sum = [&](float x) {
+            float r = 0.0f;
+            r = r + row_q(x, std::integral_constant<int, 0>());
+            r = r + row_q(x, std::integral_constant<int, 1>());
+            r = r + row_q(x, std::integral_constant<int, 2>());
+            r = r + row_q(x, std::integral_constant<int, 3>());
+            return r;
+        };
+        auto col_sum = [&](float x) {
+            const float x1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x124, 0xf, 0xf, false));
+            const float x2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
+            const float x3 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x12C, 0xf, 0xf, false));
+            float r = 0.0f;
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) r = r + (j == q ? x : r1 == q ? x1 : r2 == q ? x2 : x3);
+            return r;
+        };
+        const bool on = t < 16;
+        float v = on ? mixes[8 + t] * a.scale[2] + a.base[8 + t] : 0.0f;
+        float mx = -__uint_as_float(0x7f800000u);
+        mx = fmaxf(mx, row_q(v, std::integral_constant<int, 0>()));
+        mx = fmaxf(mx, row_q(v, std::integral_constant<int, 1>()));
+        mx = fmaxf(mx, row_q(v, std::integral_constant<int, 2>()));
+        mx = fmaxf(mx, row_q(v, std::integral_constant<int, 3>()));
+        v = wh_expf_glibc(v - mx, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
+        v = v / row_sum(v) + eps;
+        for (uint32_t it = 0; it < n_ops; ++it) {
+            const float r = (it & 1) == 0 ? col_sum(v) : row_sum(v);
+            v = v / (r + eps);
+        }
+        if (on) a.comb[t] = v;
+        return;
+    }
     if (hh <= 64) {
         // comb[j][k] in lane j * hc + k; a lane gathers its row or column
         // with shuffles and sums it in order

@@ -55,34 +55,90 @@ struct wh_rowpost_args {
     const float* inv_freqs;     // [pairs]
     uint32_t pairs, rope_off, position, inverse;
     uint32_t aq_len;            // 0: no act-quant
+    uint32_t tree;              // norm: 1 = the sum of squares in a fixed tree (exact numerics off)
 };
 
-__global__ void __launch_bounds__(256) k_rowpost(wh_rowpost_args a) {
+// kT threads per row (256, or 1024 for a lone row); each thread's values
+// and norm weights are loaded up front.
+template <int kT>
+__global__ void __launch_bounds__(kT) k_rowpost(wh_rowpost_args a) {
+    constexpr int kPer = WH_ROWPOST_MAX / kT;  // values per thread at most
+    constexpr int kW = kT / 64;                // waves
     __shared__ __align__(16) float v[WH_ROWPOST_MAX];
     __shared__ float inv_s;
     const uint32_t t = threadIdx.x, n = a.n;
     const float* x = a.x + (size_t)blockIdx.x * a.ld_in;
-    for (uint32_t i = t; i < n; i += 256) v[i] = x[i];
+    float xv[kPer], wv[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t i = t + kT * k;
+        xv[k] = i < n ? x[i] : 0.0f;
+        wv[k] = a.norm && a.w && i < n ? wh_bf16_value(a.w[i]) : 1.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k)
+        if (t + kT * k < n) v[t + kT * k] = xv[k];
     __syncthreads();
     if (a.norm) {
-        if (t == 0) {
+        if (a.tree) {
+            // each thread its strided terms, then the wave butterfly, then
+            // the waves in order: the same value up to rounding
+            __shared__ float red[kW];
             float s = 0.0f;
-            for (uint32_t i = 0; i < n; ++i) s = s + v[i] * v[i];
-            const float ms = s / (float)n;
-            inv_s = 1.0f / sqrtf(ms + 1.0e-6f);
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) s = s + xv[k] * xv[k];  // zeros past n
+            for (int off = 32; off > 0; off >>= 1) s = s + __shfl_xor(s, off, 64);
+            if ((t & 63) == 0) red[t >> 6] = s;
+            __syncthreads();
+            if (t == 0) {
+                float r = red[0];
+#pragma unroll
+                for (int w = 1; w < kW; ++w) r = r + red[w];
+                inv_s = 1.0f / sqrtf(r / (float)n + 1.0e-6f);
+            }
+        } else {
+            // the reference's order: every product rounded on its own in
+            // parallel, then one lane adds them in sequence, 32 read ahead
+            __shared__ __align__(16) float sq[WH_ROWPOST_MAX];
+#pragma unroll
+            for (int k = 0; k < kPer; ++k)
+                if (t + kT * k < n) sq[t + kT * k] = xv[k] * xv[k];
+            __syncthreads();
+            if (t == 0) {
+                float s = 0.0f;
+                uint32_t i = 0;
+                for (; i + 32 <= n; i += 32) {
+                    float4 q[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) q[k] = *(const float4*)(sq + i + 4 * k);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        s = s + q[k].x;
+                        s = s + q[k].y;
+                        s = s + q[k].z;
+                        s = s + q[k].w;
+                    }
+                }
+                for (; i < n; ++i) s = s + sq[i];
+                inv_s = 1.0f / sqrtf(s / (float)n + 1.0e-6f);
+            }
         }
         __syncthreads();
         const float inv = inv_s;
-        for (uint32_t i = t; i < n; i += 256) {
-            float y = v[i] * inv;
-            if (a.w) y = y * wh_bf16_value(a.w[i]);
-            v[i] = y;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t i = t + kT * k;
+            if (i < n) {
+                float y = xv[k] * inv;
+                if (a.w) y = y * wv[k];
+                v[i] = y;
+            }
         }
         __syncthreads();
     }
     if (a.pairs) {
         const float pos = (float)a.position;
-        for (uint32_t p = t; p < a.pairs; p += 256) {
+        for (uint32_t p = t; p < a.pairs; p += kT) {
             const float ang = pos * a.inv_freqs[p];
             float sn = wh_sincosf_glibc(ang, 0);
             const float cs = wh_sincosf_glibc(ang, 1);
@@ -96,7 +152,7 @@ __global__ void __launch_bounds__(256) k_rowpost(wh_rowpost_args a) {
     }
     if (a.aq_len) {
         const uint32_t wave = t >> 6, lane = t & 63;
-        for (uint32_t b = wave; b * 64 < a.aq_len; b += 4) {
+        for (uint32_t b = wave; b * 64 < a.aq_len; b += kW) {
             const uint32_t i = b * 64 + lane;
             const bool valid = i < a.aq_len;
             const float q = wh_aq64_wave(valid ? v[i] : 0.0f, valid);
@@ -105,7 +161,7 @@ __global__ void __launch_bounds__(256) k_rowpost(wh_rowpost_args a) {
         __syncthreads();
     }
     float* out = a.out + (size_t)blockIdx.x * a.ld_out;
-    for (uint32_t i = t; i < n; i += 256) out[i] = v[i];
+    for (uint32_t i = t; i < n; i += kT) out[i] = v[i];
 }
 
 // --------------------------------------------------------- window softmax

@@ -296,13 +296,14 @@ struct wh_ctx {
     uint32_t fp8_mm_min = 4;                // multi-input FP8 GEMVs with this many inputs use MFMA
     Scratch fp8mm_ws, fp8mm_cnt;            // their partial tiles and arrival counters
     Scratch moe_dyn;                        // a device route list resolved for the experts (wh_moe_dyn)
+    Scratch layer;                          // the decode layer's state and activations between its steps
     bool exact = true;                      // routed experts in the reference's summation order
     int token_kernels = 1;                  // MFMA token kernels: bit 0 gate/up, bit 1 down on k_*_tok (else k_*_px)
     bool capture_gu = false;                // routed experts keep gate/up in `gu` (test support)
     size_t tok_last_n = 0, tok_last_tokens = 0, tok_last_hidden = 0, tok_last_inter = 0;
     size_t moe_last_slots = 0, moe_last_npos = 0;  // sizes of the last single-chunk batch call
     size_t moe_last_hidden = 0, moe_last_inter = 0;
-    std::mutex mu;
+    std::recursive_mutex mu;  // recursive: composite entry points call the others
     hipEvent_t timer[2] = {nullptr, nullptr};  // wh_timer_start / wh_timer_stop
     Retire retire;                                     // buffers kept for live graphs
     std::map<uint64_t, hipGraphExec_t> graphs;         // wh_graph_end handles
@@ -314,7 +315,7 @@ struct wh_ctx {
     hipStream_t base_stream = nullptr, cap_stream = nullptr;
     std::vector<Scratch*> scratch() {
         return {&x_in, &y_out, &h, &ybuf, &cnt_y, &tmp, &batch, &routes, &bout, &gu, &relayout, &rtr, &rtr_cnt,
-                &mla, &hcs, &fp8mm_ws, &fp8mm_cnt, &moe_dyn};
+                &mla, &hcs, &fp8mm_ws, &fp8mm_cnt, &moe_dyn, &layer};
     }
 };
 
@@ -1884,7 +1885,7 @@ int wh_shutdown(wh_ctx* c) {
 
 int wh_synchronize(wh_ctx* c) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     return read_status(c);
 }
@@ -1893,7 +1894,7 @@ int wh_stream_status(wh_ctx* c) { return wh_synchronize(c); }
 
 int wh_graph_begin(wh_ctx* c) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     if (c->capturing) return WH_INVALID_ARGUMENT;
     WH_HIP(hipSetDevice(c->device));
     if (!c->cap_stream) WH_HIP(hipStreamCreateWithFlags(&c->cap_stream, hipStreamNonBlocking));
@@ -1908,7 +1909,7 @@ int wh_graph_begin(wh_ctx* c) {
 int wh_graph_end(wh_ctx* c, wh_graph* out) {
     if (!c || !out) return WH_INVALID_ARGUMENT;
     *out = 0;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     if (!c->capturing) return WH_INVALID_ARGUMENT;
     (void)hipSetDevice(c->device);
     hipGraph_t g = nullptr;
@@ -1938,7 +1939,7 @@ int wh_graph_end(wh_ctx* c, wh_graph* out) {
 
 int wh_graph_launch(wh_ctx* c, wh_graph g) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     auto it = c->graphs.find(g);
     if (it == c->graphs.end() || c->capturing) return WH_INVALID_ARGUMENT;
     WH_HIP(hipSetDevice(c->device));
@@ -1948,7 +1949,7 @@ int wh_graph_launch(wh_ctx* c, wh_graph g) {
 
 int wh_graph_release(wh_ctx* c, wh_graph g) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     auto it = c->graphs.find(g);
     if (it == c->graphs.end()) return WH_INVALID_ARGUMENT;
     WH_HIP(hipSetDevice(c->device));
@@ -1976,7 +1977,7 @@ int wh_store_fp8(wh_ctx* c, const uint8_t* weight, size_t weight_len, size_t row
     if (weight_len < rows * cols) return WH_PACKED_WEIGHT_TOO_SMALL;
     size_t sbytes = scale_rows * scale_cols * (scale_format == WH_SCALE_F32 ? 4 : 1);
     if (scales_len < sbytes) return WH_SCALE_TOO_SMALL;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     Tensor t;
     t.kind = kFp8;
@@ -2007,7 +2008,7 @@ int wh_store_fp8(wh_ctx* c, const uint8_t* weight, size_t weight_len, size_t row
 int wh_store_fp4(wh_ctx* c, const uint8_t* packed, size_t packed_len, const uint8_t* scales,
                  size_t scales_len, size_t rows, size_t cols, size_t scale_cols, wh_tensor* out) {
     if (!c || !out || !packed || !scales) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     return store_fp4_upload(c, packed, packed_len, scales, scales_len, rows, cols, scale_cols, false, out);
 }
@@ -2015,7 +2016,7 @@ int wh_store_fp4(wh_ctx* c, const uint8_t* packed, size_t packed_len, const uint
 int wh_store_expert(wh_ctx* c, uint32_t layer, uint32_t expert, wh_tensor w1, wh_tensor w3,
                     wh_tensor w2) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     Tensor *t1 = find_tensor(c, w1), *t3 = find_tensor(c, w3), *t2 = find_tensor(c, w2);
     if (!t1 || !t3 || !t2) return WH_NOT_RESIDENT;
     if (t1->kind != kFp4 || t3->kind != kFp4 || t2->kind != kFp4) return WH_INVALID_QUANT_FORMAT;
@@ -2042,7 +2043,7 @@ int wh_store_expert_synthetic(wh_ctx* c, uint32_t layer, uint32_t expert, size_t
                               size_t inter, uint64_t seed, uint32_t slo, uint32_t shi) {
     if (!c || slo > shi || shi > 255) return WH_INVALID_ARGUMENT;
     if (hidden % 256 || inter % 256 || hidden == 0 || inter == 0) return WH_INVALID_SHAPE;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     wh_tensor ids[3];
     const size_t shapes[3][2] = {{inter, hidden}, {inter, hidden}, {hidden, inter}};
@@ -2137,7 +2138,7 @@ int wh_quant_block_fp4_expert(const uint8_t* block, size_t block_len, wh_fp4_vie
 
 int wh_store_expert_block(wh_ctx* c, uint32_t layer, uint32_t expert, const uint8_t* block, size_t block_len) {
     if (!c || (!block && block_len)) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     return store_block_locked(c, layer, expert, block, block_len, false, nullptr);
 }
@@ -2165,7 +2166,7 @@ int wh_store_expert_pack(wh_ctx* c, const char* pack_path, const wh_expert_pack_
             return WH_INVALID_ARGUMENT;
         }
     }
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     const int fd = open(pack_path, O_RDONLY | O_CLOEXEC);
     if (fd < 0) {
@@ -2241,7 +2242,7 @@ int wh_store_router(wh_ctx* c, uint32_t layer, const uint8_t* block, size_t bloc
         }
     }
     if (!have_gate) {  // Ok(None): the engine falls back to its own routing
-        std::lock_guard<std::mutex> lk(c->mu);
+        std::lock_guard<std::recursive_mutex> lk(c->mu);
         drop_router(c, layer);
         return WH_OK;
     }
@@ -2319,7 +2320,7 @@ int wh_store_router(wh_ctx* c, uint32_t layer, const uint8_t* block, size_t bloc
         rt.table.assign(r.data() + t.data_off, r.data() + t.data_off + t.data_len);
         break;
     }
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     if (fp8) {
         rt.gate = kGateFp8;
@@ -2363,7 +2364,7 @@ int wh_route_experts(wh_ctx* c, uint32_t layer, const float* hidden, size_t hidd
     if (!expert_ids || !scores) return WH_INVALID_ARGUMENT;
     if (out_cap < active) return WH_OUTPUT_TOO_SMALL;
     if (active > WH_ROUTER_MAX_ACTIVE || n_available > WH_ROUTER_MAX_ROWS) return WH_UNSUPPORTED;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     auto it = c->routers.find(layer);
     if (it == c->routers.end()) return WH_NOT_RESIDENT;
@@ -2401,7 +2402,7 @@ int wh_route_experts_async(wh_ctx* c, uint32_t layer, const float* x_dev, size_t
     if (!c || !opts || !x_dev || !ids_dev || !scores_dev || !count_dev) return WH_INVALID_ARGUMENT;
     if ((uintptr_t)x_dev & 15) return WH_INVALID_ARGUMENT;  // x is read in 16-byte pieces
     if (active > WH_ROUTER_MAX_ACTIVE || n_available > WH_ROUTER_MAX_ROWS) return WH_UNSUPPORTED;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     auto it = c->routers.find(layer);
     if (it == c->routers.end()) return WH_NOT_RESIDENT;
@@ -2433,7 +2434,7 @@ int wh_store_fp8_synthetic(wh_ctx* c, size_t rows, size_t cols, uint64_t seed, u
     if (rows == 0 || cols == 0 || scale_rows == 0 || scale_cols == 0 || rows % scale_rows || cols % scale_cols ||
         cols / scale_cols != 128)
         return WH_INVALID_SHAPE;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     Tensor t;
     t.kind = kFp8;
@@ -2456,7 +2457,7 @@ int wh_store_fp8_synthetic(wh_ctx* c, size_t rows, size_t cols, uint64_t seed, u
 
 int wh_store_release(wh_ctx* c, wh_tensor t) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     auto it = c->tensors.find(t);
     if (it == c->tensors.end()) return WH_NOT_RESIDENT;
     drop_tensor(c, t);
@@ -2466,7 +2467,7 @@ int wh_store_release(wh_ctx* c, wh_tensor t) {
 
 int wh_store_usage(wh_ctx* c, size_t* bytes, size_t* tensors, size_t* experts) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     if (bytes) *bytes = c->arena.live;
     if (tensors) *tensors = c->tensors.size();
     if (experts) *experts = c->experts.size();
@@ -2475,7 +2476,7 @@ int wh_store_usage(wh_ctx* c, size_t* bytes, size_t* tensors, size_t* experts) {
 
 int wh_tensor_dequant(wh_ctx* c, wh_tensor th, float* out, size_t out_len) {
     if (!c || !out) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     Tensor* t = find_tensor(c, th);
     if (!t) return WH_NOT_RESIDENT;
@@ -2505,7 +2506,7 @@ int wh_fp8_gemv_multi(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end,
                       const float* inputs, size_t n, size_t input_stride, float* outputs,
                       size_t output_stride, size_t* values_out) {
     if (!c || !inputs || !outputs) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     Tensor* t = find_tensor(c, w);
     if (!t) return WH_NOT_RESIDENT;
@@ -2540,7 +2541,7 @@ int wh_fp8_gemv(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end, const 
                 size_t input_len, float* output, size_t output_len, size_t* values_out) {
     if (!c || !input || !output) return WH_INVALID_ARGUMENT;
     {
-        std::lock_guard<std::mutex> lk(c->mu);
+        std::lock_guard<std::recursive_mutex> lk(c->mu);
         Tensor* t = find_tensor(c, w);
         if (!t) return WH_NOT_RESIDENT;
         if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
@@ -2564,7 +2565,7 @@ static int fp8_ptr_check(const Tensor& t, const float* x, const float* y) {
 int wh_fp8_gemv_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end,
                       const float* x_dev, float* y_dev) {
     if (!c || !x_dev || !y_dev) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     Tensor* t = find_tensor(c, w);
     if (!t) return WH_NOT_RESIDENT;
     if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
@@ -2577,7 +2578,7 @@ int wh_fp8_gemv_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end,
 int wh_fp8_gemv_multi_async(wh_ctx* c, wh_tensor w, size_t row_start, size_t row_end, const float* x_dev, size_t n,
                             size_t x_stride, float* y_dev, size_t y_stride) {
     if (!c || !x_dev || !y_dev) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     Tensor* t = find_tensor(c, w);
     if (!t) return WH_NOT_RESIDENT;
     if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
@@ -2612,7 +2613,7 @@ int wh_fp8_gemv_multi_pair_async(wh_ctx* c, wh_tensor w0, size_t row_start0, siz
                                  size_t y0_stride, wh_tensor w1, size_t row_start1, size_t row_end1, float* y1_dev,
                                  size_t y1_stride, const float* x_dev, size_t n, size_t x_stride) {
     if (!c || !x_dev || !y0_dev || !y1_dev) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     Tensor* t0 = find_tensor(c, w0);
     Tensor* t1 = find_tensor(c, w1);
     WH_TRY(fp8_multi_check(t0, row_start0, row_end0, x_dev, n, x_stride, y0_dev, y0_stride));
@@ -2645,7 +2646,7 @@ int wh_fp8_gemv_multi_groups_async(wh_ctx* c, wh_tensor w, size_t row_start, siz
                                    const float* x_dev, size_t x_group_stride, size_t n, size_t x_stride, float* y_dev,
                                    size_t y_stride) {
     if (!c || !x_dev || !y_dev || group_rows == 0) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     Tensor* t = find_tensor(c, w);
     if (!t) return WH_NOT_RESIDENT;
     if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
@@ -2669,7 +2670,7 @@ int wh_fp8_gemv_multi_groups_async(wh_ctx* c, wh_tensor w, size_t row_start, siz
 
 int wh_set_fp8_mfma_min(wh_ctx* c, uint32_t min_inputs) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     c->fp8_mm_min = min_inputs ? min_inputs : UINT32_MAX;
     return WH_OK;
 }
@@ -2693,7 +2694,7 @@ bool fp8_pair_ok(const Tensor& t1, const wh_gemv_desc& d1, const Tensor& t2, con
 
 int wh_fp8_gemv_batch_async(wh_ctx* c, const wh_gemv_desc* descs, size_t n) {
     if (!c || (n && !descs)) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     // validate everything before launching anything
     for (size_t i = 0; i < n; ++i) {
@@ -2748,7 +2749,7 @@ int wh_fp8_gemv_batch_async(wh_ctx* c, const wh_gemv_desc* descs, size_t n) {
 int wh_fp4_matvec(wh_ctx* c, wh_tensor w, const float* input, size_t input_len, float* output,
                   size_t output_len) {
     if (!c || !input || !output) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     Tensor* t = find_tensor(c, w);
     if (!t) return WH_NOT_RESIDENT;
@@ -2771,7 +2772,7 @@ int wh_act_quant_dequant(wh_ctx* c, float* values, size_t n, size_t block) {
     if (!c) return WH_INVALID_ARGUMENT;
     if (block == 0 || n == 0) return WH_OK;  // E/compute.rs:2505-2507
     if (!values) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     WH_HIP(c->x_in.ensure(n * sizeof(float), false));
     WH_HIP(hipMemcpyAsync(c->x_in.p, values, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
@@ -2798,7 +2799,7 @@ int wh_routed_experts(wh_ctx* c, const wh_expert_route* routes, size_t n, float*
     if (!c) return WH_INVALID_ARGUMENT;
     if (n == 0) return WH_OK;  // E/compute.rs:1956-1958
     if (!routes || !hidden) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     ExpertView ev[WH_MAX_EXPERTS];
     float wts[WH_MAX_EXPERTS];
@@ -2821,7 +2822,7 @@ int wh_routed_experts(wh_ctx* c, const wh_expert_route* routes, size_t n, float*
 int wh_routed_experts_async(wh_ctx* c, const wh_expert_route* routes, size_t n, const void* x_dev,
                             int x_bf16, size_t n_tokens, float* out_dev) {
     if (!c || !routes || !x_dev || !out_dev || n == 0 || n_tokens == 0) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     ExpertView ev[WH_MAX_EXPERTS];
     float wts[WH_MAX_EXPERTS];
@@ -2840,7 +2841,7 @@ static int routed_shared_common(wh_ctx* c, const wh_expert_route* routes, size_t
 int wh_routed_and_shared_experts(wh_ctx* c, const wh_expert_route* routes, size_t n, uint32_t shared_layer,
                                  uint32_t shared_expert, float* hidden, size_t hidden_len) {
     if (!c || !hidden || (n && !routes)) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     ExpertView ev[WH_MAX_EXPERTS];
     float wts[WH_MAX_EXPERTS];
@@ -2864,7 +2865,7 @@ int wh_routed_and_shared_experts_async(wh_ctx* c, const wh_expert_route* routes,
                                        uint32_t shared_expert, const void* x_dev, int x_bf16, size_t n_tokens,
                                        float* out_dev) {
     if (!c || !x_dev || !out_dev || n_tokens == 0 || (n && !routes)) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     ExpertView ev[WH_MAX_EXPERTS];
     float wts[WH_MAX_EXPERTS];
@@ -2923,7 +2924,7 @@ int wh_routed_and_shared_experts_dev_async(wh_ctx* c, uint32_t layer_id, const u
                                            uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
                                            int x_is_bf16, float* out_dev) {
     if (!c || !ids_dev || !weights_dev || !count_dev || !x_dev || !out_dev) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     return moe_dev_routes(c, layer_id, ids_dev, weights_dev, count_dev, n_slots, shared_layer, shared_expert, x_dev,
                           x_is_bf16, out_dev);
@@ -2933,7 +2934,7 @@ int wh_routed_and_shared_experts_noalloc_async(wh_ctx* c, const wh_expert_route*
                                                uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
                                                int x_bf16, size_t n_tokens, float* out_dev) {
     if (!c || !x_dev || !out_dev || n_tokens == 0 || (n && !routes)) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     ExpertView ev[WH_MAX_EXPERTS];
     float wts[WH_MAX_EXPERTS];
@@ -2991,7 +2992,7 @@ static int batch_setup(wh_ctx* c, uint32_t layer, size_t npos, size_t topk, uint
 
 int wh_debug_moe_batch_read(wh_ctx* c, int which, void* out, size_t bytes) {
     if (!c || !out) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     const size_t S = c->moe_last_slots, P = c->moe_last_npos, hidden = c->moe_last_hidden, inter = c->moe_last_inter;
     if (S == 0) return WH_INVALID_ARGUMENT;
@@ -3019,28 +3020,28 @@ int wh_debug_moe_batch_read(wh_ctx* c, int which, void* out, size_t bytes) {
 
 int wh_set_exact_numerics(wh_ctx* c, int on) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     c->exact = on != 0;
     return WH_OK;
 }
 
 int wh_debug_token_kernels(wh_ctx* c, int mask) {
     if (!c || mask < 0 || mask > 3) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     c->token_kernels = mask;
     return WH_OK;
 }
 
 int wh_debug_moe_token_capture(wh_ctx* c, int on) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     c->capture_gu = on != 0;
     return WH_OK;
 }
 
 int wh_debug_moe_token_read(wh_ctx* c, int which, void* out, size_t bytes) {
     if (!c || !out) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     const size_t T = c->tok_last_tokens, n = c->tok_last_n, hidden = c->tok_last_hidden, inter = c->tok_last_inter;
     if (T == 0) return WH_INVALID_ARGUMENT;
@@ -3063,7 +3064,7 @@ int wh_debug_moe_token_read(wh_ctx* c, int which, void* out, size_t bytes) {
 
 int wh_set_moe_mfma_min(wh_ctx* c, uint32_t min_tokens) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     c->moe_mfma_min = min_tokens;
     return WH_OK;
 }
@@ -3072,7 +3073,7 @@ int wh_moe_batch(wh_ctx* c, uint32_t layer_id, const uint32_t* route_ids, const 
                  size_t topk, uint32_t shared_layer, uint32_t shared_expert, const float* x, size_t x_len,
                  float* out, size_t out_len) {
     if (!c || !route_ids || !route_scores || !x || !out) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     LayerTable* t = nullptr;
     ExpertView sh;
@@ -3116,7 +3117,7 @@ int wh_moe_batch_async(wh_ctx* c, uint32_t layer_id, const uint32_t* route_ids_d
                        size_t npos, size_t topk, uint32_t shared_layer, uint32_t shared_expert, const void* x_dev,
                        int x_is_bf16, float* out_dev) {
     if (!c || !route_ids_dev || !route_scores_dev || !x_dev || !out_dev) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     LayerTable* t = nullptr;
     ExpertView sh;
@@ -3145,7 +3146,7 @@ int wh_fp4_expert_forward(wh_ctx* c, uint32_t layer, uint32_t expert, const floa
     if (!c || !input || !output) return WH_INVALID_ARGUMENT;
     ExpertView ev;
     {
-        std::lock_guard<std::mutex> lk(c->mu);
+        std::lock_guard<std::recursive_mutex> lk(c->mu);
         WH_TRY(resolve_expert(c, layer, expert, &ev));
     }
     // E/deepseek_v4.rs:567-580
@@ -3154,7 +3155,7 @@ int wh_fp4_expert_forward(wh_ctx* c, uint32_t layer, uint32_t expert, const floa
         return WH_INVALID_SHAPE;
     if (output_len < ev.w2->rows) return WH_OUTPUT_TOO_SMALL;
     if (scratch_len < ev.w1->rows * 2) return WH_SCRATCH_TOO_SMALL;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     const size_t hsz = ev.w1->cols, osz = ev.w2->rows;
     WH_HIP(c->x_in.ensure(hsz * sizeof(float), false));
@@ -3213,7 +3214,7 @@ int fp8_shared_check(wh_ctx* c, wh_tensor h1, wh_tensor h3, wh_tensor h2, const 
 int wh_fp8_shared_expert(wh_ctx* c, wh_tensor w1, wh_tensor w3, wh_tensor w2, const float* input, size_t input_len,
                          float* output, size_t output_len) {
     if (!c || !input || !output) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     const Tensor *t1, *t3, *t2;
     WH_TRY(fp8_shared_check(c, w1, w3, w2, &t1, &t3, &t2));
@@ -3235,7 +3236,7 @@ int wh_fp8_shared_expert(wh_ctx* c, wh_tensor w1, wh_tensor w3, wh_tensor w2, co
 int wh_fp8_shared_expert_async(wh_ctx* c, wh_tensor w1, wh_tensor w3, wh_tensor w2, const float* x_dev,
                                float* y_dev) {
     if (!c || !x_dev || !y_dev) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     const Tensor *t1, *t3, *t2;
     WH_TRY(fp8_shared_check(c, w1, w3, w2, &t1, &t3, &t2));
@@ -3263,7 +3264,7 @@ int wh_device_free(wh_ctx* c, void* p) {
 int wh_memcpy(wh_ctx* c, void* dst, const void* src, size_t bytes, int kind) {
     if (!c || (bytes && (!dst || !src)) || kind < 0 || kind > 2) return WH_INVALID_ARGUMENT;
     if (bytes == 0) return WH_OK;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     const hipMemcpyKind kinds[3] = {hipMemcpyHostToDevice, hipMemcpyDeviceToHost, hipMemcpyDeviceToDevice};
     WH_HIP(hipMemcpyAsync(dst, src, bytes, kinds[kind], c->stream));
@@ -3273,7 +3274,7 @@ int wh_memcpy(wh_ctx* c, void* dst, const void* src, size_t bytes, int kind) {
 
 int wh_timer_start(wh_ctx* c) {
     if (!c) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     WH_HIP(hipEventRecord(c->timer[0], c->stream));
     return WH_OK;
@@ -3281,7 +3282,7 @@ int wh_timer_start(wh_ctx* c) {
 
 int wh_timer_stop(wh_ctx* c, double* elapsed_us) {
     if (!c || !elapsed_us) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     WH_HIP(hipEventRecord(c->timer[1], c->stream));
     WH_HIP(hipEventSynchronize(c->timer[1]));
@@ -3298,7 +3299,7 @@ int wh_probe_read_floor(wh_ctx* c, const void* buf_dev, size_t buf_bytes, size_t
         return WH_INVALID_ARGUMENT;
     const size_t stride = (bytes + 4095) & ~(size_t)4095;  // window pitch
     if (buf_bytes < stride) return WH_INVALID_SHAPE;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     WH_HIP(c->y_out.ensure(8192 * sizeof(uint32_t), false));
     uint32_t* out = c->y_out.as<uint32_t>();
@@ -3344,7 +3345,7 @@ int wh_profile_routed(wh_ctx* c, const wh_expert_route* routes, size_t n_routes,
     if (!c || !routes || !x_dev || !out_dev || !us_per_launch || n_routes == 0 || n_sets == 0 || iters == 0 ||
         n_routes > WH_MAX_EXPERTS)
         return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     std::vector<ExpertView> ev(n_sets * n_routes);
     std::vector<float> wts(n_sets * n_routes);
@@ -3380,7 +3381,7 @@ int wh_profile_token_pipeline(wh_ctx* c, const wh_expert_route* routes, size_t n
     if (!c || !routes || !x_dev || !out_dev || !us_per_token || n_routes == 0 || n_sets == 0 || iters == 0 ||
         n_routes > WH_MAX_EXPERTS || mode < 0 || mode > 1 || (x_stride & 15))
         return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     std::vector<ExpertView> ev(n_sets * n_routes);
     std::vector<float> wts(n_sets * n_routes);
@@ -3462,7 +3463,7 @@ int wh_debug_eval(wh_ctx* c, int fn, const float* in, float* out, size_t n) {
     if (!c || !in || !out || fn < 0 || fn > 8) return WH_INVALID_ARGUMENT;
     if ((fn == 3 && n % 4) || (fn >= 7 && n % 64)) return WH_INVALID_ARGUMENT;
     if (n == 0) return WH_OK;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     WH_HIP(c->x_in.ensure(n * sizeof(float), false));
     WH_HIP(c->y_out.ensure(n * sizeof(float), false));
@@ -3542,9 +3543,14 @@ int rope_table(wh_ctx* c, size_t rope_dim, float theta, const wh_yarn* yarn, con
     return WH_OK;
 }
 
-int rowpost_launch(wh_ctx* c, const wh_rowpost_args& a) {
-    if (a.rows == 0) return WH_OK;
-    k_rowpost<<<a.rows, 256, 0, c->stream>>>(a);
+int rowpost_launch(wh_ctx* c, const wh_rowpost_args& args) {
+    if (args.rows == 0) return WH_OK;
+    wh_rowpost_args a = args;
+    a.tree = c->exact ? 0u : 1u;  // exact numerics off: the norms' sums of squares in a fixed tree
+    // a lone row gets 1024 threads (the act-quant's 64-value blocks and the
+    // norm's terms spread over 16 waves), many rows 256 each
+    if (a.rows < 16) k_rowpost<1024><<<a.rows, 1024, 0, c->stream>>>(a);
+    else k_rowpost<256><<<a.rows, 256, 0, c->stream>>>(a);
     WH_HIP(hipGetLastError());
     return WH_OK;
 }
@@ -3602,7 +3608,7 @@ int wh_rms_norm_async(wh_ctx* c, const float* x_dev, float* out_dev, size_t rows
     if (!c || !x_dev || !out_dev) return WH_INVALID_ARGUMENT;
     if (rows == 0 || n == 0) return WH_OK;  // E/compute.rs:7111-7113: an empty slice is left alone
     if (n > WH_ROWPOST_MAX || rows > 0x7fffffffu) return WH_UNSUPPORTED;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     wh_rowpost_args a = rowpost_args(x_dev, out_dev, rows, n, n, n);
     a.norm = 1;
@@ -3617,7 +3623,7 @@ int wh_rope_async(wh_ctx* c, float* values_dev, size_t rows, size_t row_stride, 
     if (!values_dev || !inv_freqs_dev) return WH_INVALID_ARGUMENT;
     if (offset + 2 * pairs > row_stride) return WH_INVALID_SHAPE;  // "RoPE input shorter than dim"
     if (row_stride > WH_ROWPOST_MAX || rows > 0x7fffffffu || position >= (1u << 24)) return WH_UNSUPPORTED;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     wh_rowpost_args a = rowpost_args(values_dev, values_dev, rows, row_stride, row_stride, row_stride);
     a.inv_freqs = inv_freqs_dev;
@@ -3633,7 +3639,7 @@ int wh_act_quant_dequant_async(wh_ctx* c, float* values_dev, size_t n, size_t bl
     if (block == 0 || n == 0) return WH_OK;  // E/compute.rs:2505-2507
     if (!values_dev) return WH_INVALID_ARGUMENT;
     if (n > 0xffffffffu || (n + block - 1) / block > 0x7fffffffu) return WH_UNSUPPORTED;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     k_act_quant_inplace<<<(unsigned)((n + block - 1) / block), 256, 0, c->stream>>>(values_dev, (uint32_t)n,
                                                                                      (uint32_t)block);
@@ -3653,7 +3659,7 @@ int wh_window_attention_async(wh_ctx* c, const float* q_dev, size_t heads, size_
     if (window_stride > 0xffffffffu) return WH_UNSUPPORTED;
     // the score kernel reads keys as float4
     if ((window_stride & 3) || ((uintptr_t)window_dev & 15) || ((uintptr_t)comp_dev & 15)) return WH_INVALID_ARGUMENT;
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     wh_attn_args a{};
     a.q = q_dev;
@@ -3689,7 +3695,7 @@ int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token
     const size_t context = token_pos + 1, window_start = context > 128 ? context - 128 : 0;
     const size_t n_win = context - window_start;
     WH_TRY(attn_check(heads, head_dim, nope, pairs, n_win + n_comp, token_pos));
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     const Tensor* wq_a = find_tensor(c, L->wq_a);
     const Tensor* wq_b = find_tensor(c, L->wq_b);
     const Tensor* wkv = find_tensor(c, L->wkv);
@@ -3821,7 +3827,7 @@ int wh_hc_split_sinkhorn_async(wh_ctx* c, const float* mixes_dev, const float* s
                                float* comb_dev) {
     if (!c || !mixes_dev || !scale_dev || !base_dev || !pre_dev || !post_dev || !comb_dev) return WH_INVALID_ARGUMENT;
     WH_TRY(hc_check(hc, 1));
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     wh_hc_args a = hc_args(hc, 1, sinkhorn_iters, eps);
     a.scale = scale_dev;
@@ -3841,7 +3847,7 @@ int wh_hc_pre_async(wh_ctx* c, const float* fn_dev, const float* scale_dev, cons
     if (!c || !fn_dev || !scale_dev || !base_dev || !x_dev || !y_dev || !post_dev || !comb_dev)
         return WH_INVALID_ARGUMENT;
     WH_TRY(hc_check(hc, hidden));
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     wh_hc_args a = hc_args(hc, hidden, sinkhorn_iters, eps);
     a.fn = fn_dev;
@@ -3871,11 +3877,59 @@ int wh_hc_post_async(wh_ctx* c, const float* y_dev, const float* residual_dev, c
                      const float* comb_dev, float* out_dev, size_t hc, size_t hidden) {
     if (!c || !y_dev || !residual_dev || !post_dev || !comb_dev || !out_dev) return WH_INVALID_ARGUMENT;
     WH_TRY(hc_check(hc, hidden));
-    std::lock_guard<std::mutex> lk(c->mu);
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     const size_t n = hc * hidden;
     k_hc_post<<<(unsigned)((n + 255) / 256), 256, 0, c->stream>>>(y_dev, residual_dev, post_dev, comb_dev, out_dev,
                                                                   (uint32_t)hc, (uint32_t)hidden);
     WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+
+// compute_layer_deepseek_mhc (E/compute.rs:1448-1480) with the router between
+// its phases (E/server/generation.rs:719-836), each step through the kernels
+// of its own entry point.  The state ping-pongs between hidden_dev and
+// scratch, so no copy of the residuals is made.
+int wh_deepseek_mhc_layer_async(wh_ctx* c, const wh_mhc_layer* L, size_t token_pos, float* hidden_dev,
+                                float* kv_cache_dev, size_t kv_stride, size_t kv_capacity, const float* comp_dev,
+                                size_t n_comp) {
+    if (!c || !L || !hidden_dev || ((uintptr_t)hidden_dev & 15)) return WH_INVALID_ARGUMENT;
+    const size_t hc = L->hc, hidden = L->hidden;
+    WH_TRY(hc_check(hc, hidden));
+    if (L->active == 0) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    // scratch: the state after the attention sub-block, y, g, z, the two
+    // hc_pre outputs (post, comb) and the route list, each 256-byte aligned
+    auto up = [](size_t n) { return (n + 63) & ~(size_t)63; };
+    const size_t o_state = 0, o_y = up(hc * hidden), o_g = o_y + up(hidden), o_z = o_g + up(hidden);
+    const size_t o_p1 = o_z + up(hidden), o_c1 = o_p1 + up(hc), o_p2 = o_c1 + up(hc * hc), o_c2 = o_p2 + up(hc);
+    const size_t o_ids = o_c2 + up(hc * hc), o_w = o_ids + up(WH_ROUTER_MAX_ACTIVE), o_n = o_w + up(WH_ROUTER_MAX_ACTIVE);
+    WH_HIP(c->layer.ensure((o_n + 64) * sizeof(float), false));
+    float* f = c->layer.as<float>();
+    float *state = f + o_state, *y = f + o_y, *g = f + o_g, *z = f + o_z;
+    float *post1 = f + o_p1, *comb1 = f + o_c1, *post2 = f + o_p2, *comb2 = f + o_c2;
+    uint32_t* ids = reinterpret_cast<uint32_t*>(f + o_ids);
+    float* w = f + o_w;
+    uint32_t* count = reinterpret_cast<uint32_t*>(f + o_n);
+    // attention sub-block (E/compute.rs:1552-1605)
+    WH_TRY(wh_hc_pre_async(c, L->hc_attn_fn, L->hc_attn_scale, L->hc_attn_base, hc, hidden, L->sinkhorn_iters,
+                           L->hc_eps, hidden_dev, y, post1, comb1));
+    WH_TRY(wh_rms_norm_async(c, y, g, 1, hidden, L->attn_norm_bf16));
+    WH_TRY(wh_mla_attention_decode_async(c, &L->attn, token_pos, g, kv_cache_dev, kv_stride, kv_capacity, comp_dev,
+                                         n_comp));
+    WH_TRY(wh_hc_post_async(c, g, hidden_dev, post1, comb1, state, hc, hidden));
+    // ffn hc_pre + norm: the gate input (E/compute.rs:1607-1630)
+    WH_TRY(wh_hc_pre_async(c, L->hc_ffn_fn, L->hc_ffn_scale, L->hc_ffn_base, hc, hidden, L->sinkhorn_iters,
+                           L->hc_eps, state, y, post2, comb2));
+    WH_TRY(wh_rms_norm_async(c, y, g, 1, hidden, L->ffn_norm_bf16));
+    // the router on the gate input, then the experts on its route list
+    // (E/compute.rs:1641-1700)
+    const size_t slots = L->active;
+    WH_TRY(wh_route_experts_async(c, L->layer_id, g, hidden, slots, L->available_dev, L->n_available, &L->route,
+                                  ids, w, count));
+    WH_TRY(moe_dev_routes(c, L->layer_id, ids, w, count, slots, L->shared_layer, L->shared_expert, g, 0, z));
+    WH_TRY(wh_hc_post_async(c, z, state, post2, comb2, hidden_dev, hc, hidden));
     return WH_OK;
 }
