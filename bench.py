@@ -186,9 +186,33 @@ def cpu_baseline(lib, seed: int, budget_s: float):
     extra["ragged_batch_64"] = {"threads": ref_threads, "us_per_step": round(per_fwd * ids.size * 1e6, 1),
                                 "sample": f"{sample_tokens} of 64 tokens ({sub.size} of {ids.size} token-expert "
                                           "forwards), scaled by forwards"}
+    # batch 16: the FP8 set through the oracle's rows_multi restatement
+    # (each row decoded once for the 16 inputs, as the reference's
+    # gemv_fp8_e4m3_ue8m0_rows_multi) and the MoE of 16 positions as the
+    # reference's batch path runs it (one expert forward per (position,
+    # expert) target, shared expert on every position), timed per forward
+    # above and scaled by the 16 x 7 targets
+    b16 = 16
+    xs16 = [rng.standard_normal((b16, groups, c)).astype(np.float32) for _, _, c, groups in wl.DECODE_LAYER_FP8]
+
+    def fp8_set16():
+        for (pc, r, c, groups, _), xg in zip(projs, xs16):
+            rows = r // groups
+            for g in range(groups):
+                oracle.fp8_gemv_rows_multi(pc.w, r, c, pc.scales, r // 128, c // 128, xg[:, g], g * rows,
+                                           (g + 1) * rows)
+
+    k, e = _timed(fp8_set16, short, 1)
+    fp8_16_us = e / k * 1e6
+    moe_16_us = per_fwd * b16 * (wl.TOPK + 1) * 1e6
+    layer16_us = fp8_16_us + moe_16_us
     extra["decode_stack_43_batch16"] = {
-        "note": "not measured: the reference's rows_multi decodes each FP8 row once for all inputs, which the "
-                "oracle's single-input restatement does not model, so single-input calls would overstate it"}
+        "threads": ref_threads, "us_per_step": round(43 * layer16_us, 1), "layer_us": round(layer16_us, 1),
+        "fp8_set_us": round(fp8_16_us, 1), "moe_us": round(moe_16_us, 1),
+        "tokens_per_s": round(b16 / (43 * layer16_us * 1e-6), 2),
+        "sample": "one layer's FP8 set at 16 inputs through the oracle's rows_multi restatement, timed; the MoE "
+                  "as 16 x (6 routed + shared) expert forwards at the per-forward time of the ragged sample; "
+                  "x 43 layers"}
     return headline, extra
 
 

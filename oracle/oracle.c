@@ -182,6 +182,35 @@ static int parallel_rows(float* output, size_t n, size_t min_rows, row_work_fn f
     return err;
 }
 
+/* parallel_rows over n rows of `group` floats each (the work function gets
+ * its rows' slice of the output) */
+static int parallel_rows_grouped(float* output, size_t n, size_t group, size_t min_rows, row_work_fn fn,
+                                 void* ctx) {
+    int threads = or_thread_count();
+    if (min_rows < 1) min_rows = 1;
+    if (threads <= 1 || n < min_rows * 2) return fn(ctx, 0, output, n);
+    size_t chunk = (n + (size_t)threads - 1) / (size_t)threads;
+    if (chunk < min_rows) chunk = min_rows;
+    size_t jobs = (n + chunk - 1) / chunk;
+    row_job* js = (row_job*)calloc(jobs, sizeof(row_job));
+    pthread_t* ts = (pthread_t*)calloc(jobs, sizeof(pthread_t));
+    size_t off = 0;
+    for (size_t j = 0; j < jobs; ++j) {
+        size_t take = n - off < chunk ? n - off : chunk;
+        js[j] = (row_job){fn, ctx, off, output + off * group, take, 0};
+        pthread_create(&ts[j], NULL, row_job_main, &js[j]);
+        off += take;
+    }
+    int err = OR_OK;
+    for (size_t j = 0; j < jobs; ++j) {
+        pthread_join(ts[j], NULL);
+        if (err == OR_OK && js[j].result != OR_OK) err = js[j].result;
+    }
+    free(js);
+    free(ts);
+    return err;
+}
+
 /* ------------------------------------------------------------ FP8 rows */
 
 /* E/compute.rs:5967-5973 */
@@ -286,6 +315,96 @@ int or_fp8_gemv(const uint8_t* weight, size_t rows, size_t cols, const float* sc
     fp8_gemv_ctx c = {weight, scales, rows, cols, scale_cols, rows / scale_rows,
                       cols / scale_cols, row_start, input, use_avx2};
     return parallel_rows(output, row_end - row_start, 32, fp8_gemv_work, &c);
+}
+
+/* E/compute.rs:6384-6577 (gemv_fp8_e4m3_ue8m0_rows_multi): every row's
+ * bytes decoded to f32 once (fp8_ue8m0_dot_row_avx2_store_dequant), then each
+ * input's dot on the decoded row in the single-input kernel's order
+ * (fp8_ue8m0_dot_dequant_row_avx2): the same groups, g0/g1 chains and
+ * acc = fma(g0 + g1, scale, acc) as or_fp8_dot_row_avx2 with plain loads
+ * in place of the gathers. */
+__attribute__((target("avx2,fma")))
+static float fp8_dot_dequant_row_avx2(const float* dequant, const float* scales, size_t groups, size_t col_group,
+                                      const float* input) {
+    __m256 acc = _mm256_setzero_ps();
+    float tail = 0.0f;
+    for (size_t g = 0; g < groups; ++g) {
+        float scale = scales[g];
+        const float* w = dequant + g * col_group;
+        const float* cols = input + g * col_group;
+        __m256 g0 = _mm256_setzero_ps();
+        __m256 g1 = _mm256_setzero_ps();
+        size_t chunks = col_group / 16;
+        for (size_t c = 0; c < chunks; ++c) {
+            size_t base = c * 16;
+            g0 = _mm256_fmadd_ps(_mm256_loadu_ps(w + base), _mm256_loadu_ps(cols + base), g0);
+            g1 = _mm256_fmadd_ps(_mm256_loadu_ps(w + base + 8), _mm256_loadu_ps(cols + base + 8), g1);
+        }
+        float rem = 0.0f;
+        for (size_t i = chunks * 16; i < col_group; ++i) rem += w[i] * cols[i];
+        acc = _mm256_fmadd_ps(_mm256_add_ps(g0, g1), _mm256_set1_ps(scale), acc);
+        tail += rem * scale;
+    }
+    return hsum256(acc) + tail;
+}
+
+typedef struct {
+    const uint8_t* weight;
+    const float* scales;
+    size_t cols, scale_cols, row_group, col_group, row_start;
+    const float* inputs;
+    size_t count, in_stride;
+} fp8_multi_ctx;
+
+/* rows of the flat [rows][count] result, one decoded row at a time */
+static int fp8_multi_work(void* p, size_t row_offset, float* chunk, size_t n) {
+    fp8_multi_ctx* c = (fp8_multi_ctx*)p;
+    float* dequant = (float*)malloc(c->cols * sizeof(float));
+    if (!dequant) return OR_INVALID_SHAPE;
+    int err = OR_OK;
+    for (size_t i = 0; i < n && err == OR_OK; ++i) {
+        size_t row = c->row_start + row_offset + i;
+        const uint8_t* bytes = c->weight + row * c->cols;
+        for (size_t k = 0; k < c->cols; ++k) dequant[k] = g_fp8_lut[bytes[k]];
+        const float* srow = c->scales + (row / c->row_group) * c->scale_cols;
+        for (size_t j = 0; j < c->count; ++j) {
+            float acc = fp8_dot_dequant_row_avx2(dequant, srow, c->scale_cols, c->col_group,
+                                                 c->inputs + j * c->in_stride);
+            if (!isfinite(acc)) {
+                err = OR_NON_FINITE_OUTPUT;
+                break;
+            }
+            chunk[i * c->count + j] = acc;
+        }
+    }
+    free(dequant);
+    return err;
+}
+
+/* outputs[j * out_stride + (row - row_start)] for input j at
+ * inputs + j * in_stride (scales decoded, as or_fp8_gemv). */
+int or_fp8_gemv_rows_multi(const uint8_t* weight, size_t rows, size_t cols, const float* scales,
+                           size_t scale_rows, size_t scale_cols, size_t row_start, size_t row_end,
+                           const float* inputs, size_t count, size_t in_stride, float* outputs,
+                           size_t out_stride) {
+    ensure_luts();
+    if (rows == 0 || cols == 0 || scale_rows == 0 || scale_cols == 0 || rows % scale_rows ||
+        cols % scale_cols || count == 0)
+        return OR_INVALID_SHAPE;
+    if (row_start >= row_end || row_end > rows) return OR_INVALID_SHAPE;
+    size_t n = row_end - row_start;
+    /* the flat [rows][count] array parallel_rows fills: count floats per
+     * row, so it is run over n * count "rows" of one float grouped by row */
+    float* flat = (float*)malloc(n * count * sizeof(float));
+    if (!flat) return OR_INVALID_SHAPE;
+    fp8_multi_ctx c = {weight, scales, cols, scale_cols, rows / scale_rows, cols / scale_cols, row_start,
+                       inputs, count, in_stride};
+    int err = parallel_rows_grouped(flat, n, count, 8, fp8_multi_work, &c);
+    if (err == OR_OK)
+        for (size_t j = 0; j < count; ++j)
+            for (size_t r = 0; r < n; ++r) outputs[j * out_stride + r] = flat[r * count + j];
+    free(flat);
+    return err;
 }
 
 /* ------------------------------------------------------------ FP4 rows */

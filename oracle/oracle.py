@@ -51,6 +51,7 @@ def lib():
             "or_fp8_dot_row_avx2": (c.c_float, [u8p, f32p, sz, sz, f32p]),
             "or_fp8_dot_row_scalar": (c.c_float, [u8p, f32p, sz, sz, f32p]),
             "or_fp8_gemv": (c.c_int, [u8p, sz, sz, f32p, sz, sz, sz, sz, f32p, f32p, c.c_int]),
+            "or_fp8_gemv_rows_multi": (c.c_int, [u8p, sz, sz, f32p, sz, sz, sz, sz, f32p, sz, sz, f32p, sz]),
             "or_fp4_dot_row_avx2": (c.c_float, [u8p, u8p, sz, sz, sz, f32p]),
             "or_fp4_matvec": (c.c_int, [u8p, sz, u8p, sz, sz, sz, sz, f32p, sz, f32p, sz, c.c_int]),
             "or_nearest_e4m3": (c.c_float, [c.c_float]),
@@ -140,6 +141,22 @@ def fp8_gemv(w, rows, cols, scales_f32, scale_rows, scale_cols, x, row_start=0, 
     y = np.zeros(row_end - row_start, np.float32)
     st = lib().or_fp8_gemv(_pu(w), rows, cols, _pf(s), scale_rows, scale_cols, row_start, row_end, _pf(x),
                            _pf(y), 1 if avx2 else 0)
+    if st:
+        raise OracleError(st)
+    return y
+
+
+def fp8_gemv_rows_multi(w, rows, cols, scales_f32, scale_rows, scale_cols, xs, row_start=0, row_end=None):
+    """gemv_fp8_e4m3_ue8m0_rows_multi (E/compute.rs:6384-6577): each row
+    decoded once, then every input of xs [n, cols] dotted in the single-input
+    order.  Returns [n, row_end - row_start]."""
+    w, s = _u(w), _f(scales_f32)
+    xs = np.ascontiguousarray(xs, np.float32)
+    n = xs.shape[0]
+    row_end = rows if row_end is None else row_end
+    y = np.zeros((n, row_end - row_start), np.float32)
+    st = lib().or_fp8_gemv_rows_multi(_pu(w), rows, cols, _pf(s), scale_rows, scale_cols, row_start, row_end,
+                                      _pf(xs), n, xs.shape[1], _pf(y), y.shape[1])
     if st:
         raise OracleError(st)
     return y

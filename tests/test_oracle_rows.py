@@ -96,6 +96,30 @@ def test_fp8_rows_is_a_slice_of_tensorwise(oracle):
     assert np.array_equal(full[200:330], part)
 
 
+@pytest.mark.parametrize("rows,cols,block,n", [(256, 1024, 128, 5), (96, 384, 48, 3), (128, 4096, 128, 16)])
+def test_fp8_rows_multi_is_the_single_input_kernel(oracle, rows, cols, block, n):
+    """rows_multi (decode each row once, then plain loads) against the
+    single-input kernel (gathers) input by input: the reference states the
+    two are bit-identical, and here they are two separate code paths.  The
+    results also stay within the float64 bound, every code included (+-480
+    and NaN-free), and a swapped input order is visible."""
+    rng = np.random.default_rng(rows + n)
+    w = rng.integers(0, 256, (rows, cols)).astype(np.uint8)
+    sr, sc = rows // block if rows % block == 0 else 1, cols // block
+    scales = np.exp2(rng.uniform(-10, -4, (sr, sc))).astype(np.float32)
+    xs = rng.standard_normal((n, cols)).astype(np.float32)
+    r0, r1 = 3, rows - 5
+    got = oracle.fp8_gemv_rows_multi(w, rows, cols, scales, sr, sc, xs, r0, r1)
+    fp8, _, _, _ = oracle.luts()
+    dense = fp8[w].astype(np.float64) * np.repeat(np.repeat(scales, rows // sr, 0), cols // sc, 1)
+    for i in range(n):
+        single = oracle.fp8_gemv(w, rows, cols, scales, sr, sc, xs[i], r0, r1)
+        assert np.array_equal(got[i].view(np.uint32), single.view(np.uint32)), i
+        ref = dense[r0:r1] @ xs[i].astype(np.float64)
+        assert np.all(np.abs(got[i] - ref) <= 1e-5 * np.linalg.norm(dense[r0:r1], axis=1) * np.linalg.norm(xs[i]))
+    assert not np.array_equal(got[0], oracle.fp8_gemv(w, rows, cols, scales, sr, sc, xs[1], r0, r1))
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 4096), (128, 2048)])
 def test_fp4_matvec_against_float64(oracle, rows, cols):
     rng = np.random.default_rng(rows)

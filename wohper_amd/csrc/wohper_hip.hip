@@ -27,6 +27,7 @@
 #include "moe_tok.h"
 #include "fp8_mm.h"
 #include "fp8_tol.h"
+#include "fp8_multi.h"
 #include "moe_bmx.h"
 #include "probe.h"
 #include "quant_block.h"
@@ -591,6 +592,41 @@ int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x,
             WH_HIP(hipGetLastError());
             return WH_OK;
         }
+    }
+    // several inputs in the reference's order: each weight byte decoded
+    // once for all of them (k_fp8_gemv_multi); the most inputs per
+    // workgroup (16, 8, 4, 2) that keep about 256 workgroups
+    const size_t mrows = (r1 - r0) + (t2 ? r1_2 - r0_2 : 0);
+    // (about 512 workgroups of 2 waves: one wave per SIMD); below 4096 rows
+    // the per-input kernel's wider grid is faster, and the weights are
+    // small enough to stay in cache across the inputs
+    size_t mk = 16;
+    while (mk > 4 && (mrows / WH_FP8_MULTI_ROWS) * ((n_batch + mk - 1) / mk) < 512) mk /= 2;
+    while (mk > 4 && mk / 2 >= n_batch) mk /= 2;  // no more slots than inputs
+    if (n_batch >= 2 && mrows >= 4096 && fp8_split_k(t) && t.cols % 512 == 0 &&
+        (!t2 || (fp8_split_k(*t2) && t2->cols == t.cols && t2->special == t.special)) &&
+        (!x_group_rows || (x_group_rows % WH_FP8_MULTI_ROWS == 0 && x_group_stride % 4 == 0)) && x_stride % 4 == 0) {
+        const size_t b1 = (r1 - r0 + WH_FP8_MULTI_ROWS - 1) / WH_FP8_MULTI_ROWS;
+        if (t2) a.blocks1 = (uint32_t)b1;
+        dim3 grid((unsigned)(b1 + (t2 ? (r1_2 - r0_2 + WH_FP8_MULTI_ROWS - 1) / WH_FP8_MULTI_ROWS : 0)),
+                  (unsigned)((n_batch + mk - 1) / mk));
+        const uint32_t n_in = (uint32_t)n_batch;
+#define WH_MULTI(N)                                                                               \
+    do {                                                                                          \
+        if (t.special) {                                                                          \
+            if (u8) k_fp8_gemv_multi<N, true, true><<<grid, 128, 0, c->stream>>>(a, n_in);        \
+            else k_fp8_gemv_multi<N, true, false><<<grid, 128, 0, c->stream>>>(a, n_in);          \
+        } else {                                                                                  \
+            if (u8) k_fp8_gemv_multi<N, false, true><<<grid, 128, 0, c->stream>>>(a, n_in);       \
+            else k_fp8_gemv_multi<N, false, false><<<grid, 128, 0, c->stream>>>(a, n_in);         \
+        }                                                                                         \
+    } while (0)
+        if (mk == 16) WH_MULTI(16);
+        else if (mk == 8) WH_MULTI(8);
+        else WH_MULTI(4);
+#undef WH_MULTI
+        WH_HIP(hipGetLastError());
+        return WH_OK;
     }
     if (fp8_split_k(t)) {
         const size_t blocks = (r1 - r0 + WH_FP8_SK_ROWS - 1) / WH_FP8_SK_ROWS +
@@ -2662,6 +2698,9 @@ int wh_fp8_gemv_multi_groups_async(wh_ctx* c, wh_tensor w, size_t row_start, siz
     if (!c->exact && n >= c->fp8_mm_min && fp8_mm_ok(*t, row_start, row_end, group_rows))
         return launch_fp8_mm(c, *t, row_start, row_end, x_dev, n, x_stride, y_dev, y_stride, group_rows,
                              x_group_stride);
+    // one launch over every group where the kernels take row groups
+    if (fp8_split_k(*t) && is_pow2(group_rows) && group_rows >= WH_FP8_SK_ROWS)
+        return launch_fp8(c, *t, row_start, row_end, x_dev, y_dev, n, x_stride, y_stride, group_rows, x_group_stride);
     for (size_t r = row_start, g = 0; r < row_end; r += group_rows, ++g)
         WH_TRY(launch_fp8(c, *t, r, r + group_rows, x_dev + g * x_group_stride, y_dev + (r - row_start), n, x_stride,
                           y_stride));
