@@ -892,11 +892,21 @@ __global__ void __launch_bounds__(64) k_moe_resolve(const uint32_t* __restrict__
             }
         }
     }
+    // field by field: a select of whole structs goes through scratch memory
+    auto put = [&](uint32_t slot, const wh_expert_ptrs& e) {
+        out->ex[slot].w1 = e.w1;
+        out->ex[slot].s1 = e.s1;
+        out->ex[slot].w3 = e.w3;
+        out->ex[slot].s3 = e.s3;
+        out->ex[slot].w2 = e.w2;
+        out->ex[slot].s2 = e.s2;
+    };
     if (L < n_slots) {
-        out->ex[L] = ok ? p : fb;
+        if (ok) put(L, p);
+        else put(L, fb);
         out->route_w[L] = L < cnt ? w[L] : 0.0f;
     }
-    if (L == n_slots && has_shared) out->ex[L] = shared;
+    if (L == n_slots && has_shared) put(L, shared);
     if (L == 0) out->n_routed = cnt;
 }
 

@@ -960,7 +960,7 @@ __device__ __forceinline__ void wh_mfma_store(const wh_batch_args& a, float* dst
 // exact ones, bound by VALU issue.
 // Three workgroups per CU: the register budget (168) is what the LDS allows.
 template <int kBlk>
-__global__ void __launch_bounds__(256, 3) k_moe_batch_gateup(wh_batch_args a) {
+__global__ void __launch_bounds__(256, 2) k_moe_batch_gateup(wh_batch_args a) {
     extern __shared__ __align__(16) float lds[];
     __shared__ uint32_t item_s;
     const uint32_t n_mfma = a.meta[6] ? 0u : a.meta[4], mt = a.inter >> 6, et = a.inter >> 4;
@@ -1020,7 +1020,7 @@ __global__ void __launch_bounds__(256, 3) k_moe_batch_gateup(wh_batch_args a) {
 // outputs of the slots.
 // Four workgroups per CU (128 registers).
 template <int kBlk>
-__global__ void __launch_bounds__(256, 4) k_moe_batch_down(wh_batch_args a) {
+__global__ void __launch_bounds__(256, 3) k_moe_batch_down(wh_batch_args a) {
     extern __shared__ __align__(16) float lds[];
     __shared__ uint32_t item_s;
     const uint32_t n_mfma = a.meta[6] ? 0u : a.meta[4], mt = a.hidden >> 6, et = a.hidden >> 5;
