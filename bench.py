@@ -819,7 +819,7 @@ TIMELINE_POINTS = {
     "token_gateup_px": ["start", "tables staged", "x in registers", "x act-quantized", "ring issued",
                         "barrier passed", "tile 0 done", "tile 1 done", "tile 2 done", "tile 3 done", "tiles summed",
                         "end"],
-    "token_down_px": ["start", "tables staged", "h in registers", "h act-quantized", "ring issued", "barrier passed",
+    "token_down_px": ["start", "prologue issued", "h in registers", "h act-quantized", "ring issued", "codes written",
                       "unit 0 done", "unit 1 done", "unit 2 done", "unit 3 done", "units summed", "end"],
     "batch_gateup": ["start", "ring issued", "B staged", "wave's last item done", "workgroup end"],
     "batch_down": ["start", "ring issued", "B staged", "wave's last item done", "workgroup end"],

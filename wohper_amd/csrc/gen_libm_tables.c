@@ -157,7 +157,7 @@ static int check_sincos(void) {
     return bad != 0;
 }
 
-// wh_e4m3_code_scaled(h, k) against the code of wh_e4m3_round(h / 2^k) for
+// wh_e4m3_code_scaled(h, k) and wh_e4m3_code_pow2(h, k) against the code of wh_e4m3_round(h / 2^k) for
 // t = h / 2^k over every float in [0, 448] (both signs; every 11th float
 // for the other k), with h = t 2^k exactly representable.
 typedef struct {
@@ -185,6 +185,10 @@ static void* code_verify(void* p) {
                 if ((want & 0x7f) == 0 && (got & 0x7f) == 0) want = got;  // zero: either sign
                 if (want != got && j->bad++ < 5)
                     fprintf(stderr, "e4m3 code mismatch: h=%a k=%d got %02x want %02x\n", hs, k, got, want);
+                const uint32_t got2 = wh_e4m3_code_pow2(hs, k);
+                if ((want & 0x7f) == 0 && (got2 & 0x7f) == 0) want = got2;
+                if (want != got2 && j->bad++ < 5)
+                    fprintf(stderr, "e4m3 pow2 code mismatch: h=%a k=%d got %02x want %02x\n", hs, k, got2, want);
             }
         }
     }

@@ -354,6 +354,23 @@ WH_HD uint32_t wh_e4m3_code_scaled(float h, int k) {
     return (mag < 0x7eu ? mag : 0x7eu) | (sg << 7);  // (the clamp only ever meets non-finite h)
 }
 
+// The same code as the token kernels form it, for finite v with
+// |v / 2^k| <= 448 (no clamp): the normal-range magnitude ((|v| bits +
+// 0x7ffff + sign) >> 20) - (960 + 8 k), folded into one add; below 2^-6 the
+// grid is n 2^-9 with n = (|v| 2^(33 - k) + 0x7fffff + sign) >> 24 (the
+// power-of-two scaling is exact, |v| 2^(33 - k) < 2^27 there).  The table
+// generator compares it with wh_e4m3_round for every float t = v / 2^k in
+// [-448, 448] at several k.
+WH_HD uint32_t wh_e4m3_code_pow2(float v, int k) {
+    const uint32_t b = wh_float_to_bits(v), a = b & 0x7fffffffu, sg = b >> 31;
+    const uint32_t K = 0x7ffffu - ((uint32_t)(960 + 8 * k) << 20), lim = (uint32_t)(121 + k) << 23;
+    const uint32_t nrm = (a + K + sg) >> 20;
+    float at = wh_bits_to_float(a) * wh_pow2f(33 - k);
+    at = at < 134217728.0f ? at : 134217728.0f;
+    const uint32_t sub = ((uint32_t)at + 0x7fffffu + sg) >> 24;
+    return (a < lim ? sub : nrm) | (sg << 7);
+}
+
 #ifdef __HIPCC__
 // Device form: the bit length from the count of leading zeros.
 __device__ __forceinline__ uint32_t wh_log2f_thr_dev(int e) {

@@ -51,6 +51,11 @@
 #ifndef WH_PX_PRO
 #define WH_PX_PRO 2
 #endif
+// The same for the down kernel, whose act-quant covers only the wave's own
+// units.
+#ifndef WH_PX_DN_PRO
+#define WH_PX_DN_PRO 2
+#endif
 
 // Optional per-wave timeline of the two kernels (build with -DWH_TIMELINE):
 // lane 0 of each wave stores the 100 MHz realtime counter at fixed points of
@@ -167,6 +172,74 @@ __device__ __forceinline__ void wh_px_store_codes8(uint8_t* rec, uint8_t* sb, ui
         grp[4 * j + 4] = (uint8_t)(two >> 8);
     }
     if ((c & 3) == 0) sb[c >> 2] = (uint8_t)(127 + k - 3);
+}
+
+// The amax of a 64-block held as 8 values by each of 8 consecutive lanes,
+// and its act-quant scale exponent k (E/compute.rs:2504-2521); bad: a
+// non-finite value in the thread's 8.
+__device__ __forceinline__ int wh_quant8_scale(const float (&v)[8], bool& bad) {
+    float amax = 0.0f;
+    bad = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float m = fabsf(v[i]);
+        bad |= !(m <= 3.4028235e38f);
+        amax = fmaxf(amax, m);
+    }
+    amax = wh_amax_block<8>(amax);
+    if (!(amax <= 3.4028235e38f)) amax = 1.0f;  // non-finite blocks take the fp32 path
+    return wh_aq_scale_exp_fast(amax);
+}
+
+// E4M3 codes of 8 finite f32 values under the block exponent k
+// (wh_e4m3_code_pow2 for |v / 2^k| <= 448): every value takes the
+// normal-range formula, and the whole of wh_e4m3_code_pow2 (the subnormal
+// grid below 2^(k - 6) and the select) runs only when some lane of the wave
+// holds a value under 2^(k - 6); where no value is that small the two agree.
+// A zero keeps its sign (0x80 for -0; the MFMA takes it as 0).
+__device__ __forceinline__ void wh_quant8_f32_codes(const float (&v)[8], int k, uint32_t (&c)[8]) {
+    const uint32_t K = 0x7ffffu - ((uint32_t)(960 + 8 * k) << 20), lim = (uint32_t)(121 + k) << 23;
+    float amin = fabsf(v[0]);
+#pragma unroll
+    for (int i = 1; i < 8; ++i) amin = fminf(amin, fabsf(v[i]));
+    if (__builtin_amdgcn_ballot_w64(__float_as_uint(amin) < lim) != 0) {  // wave-uniform
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i] = wh_e4m3_code_pow2(v[i], k);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t b = __float_as_uint(v[i]), sg = b >> 31;
+            c[i] = (((b & 0x7fffffffu) + K + sg) >> 20) | (sg << 7);
+        }
+    }
+}
+
+// Act-quant of 8 values held by one thread into the record layout: the
+// thread owns record dwords 2q and 2q + 1 of 32-col group G (q = t % 4,
+// G = t / 4), i.e. v[2k] = column 2q + 8k, v[2k + 1] = column 2q + 1 + 8k
+// (k = 0..3); the 64-block is the 8 lanes t & ~7 .. + 7.  Returns the two
+// code dwords and the block's scale exponent; bad: a non-finite value.
+template <bool kBf16>
+__device__ __forceinline__ void wh_tok_quant8(const float (&v)[8], uint32_t& d0, uint32_t& d1, int& k, bool& bad) {
+    k = wh_quant8_scale(v, bad);
+    if constexpr (kBf16) {
+        const float inv = wh_pow2f(-k);
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float s = v[i] * inv;
+            t[i] = __builtin_fmaf(-fabsf(s), 2.44140625e-4f, s);  // s - |s| 2^-12: ties toward -inf
+        }
+        d0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(t[0], t[2], 0, false);
+        d0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(t[4], t[6], (int)d0, true);
+        d1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(t[1], t[3], 0, false);
+        d1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(t[5], t[7], (int)d1, true);
+    } else {
+        uint32_t c[8];
+        wh_quant8_f32_codes(v, k, c);
+        d0 = c[0] | (c[2] << 8) | (c[4] << 16) | (c[6] << 24);
+        d1 = c[1] | (c[3] << 8) | (c[5] << 16) | (c[7] << 24);
+    }
 }
 
 // fp32 fallback of a gate/up wave for a token with a non-finite input: its
@@ -345,36 +418,34 @@ __global__ void __launch_bounds__(kCols / 8, 1) k_moe_gateup_px(wh_moe_args a) {
 // Down + routed sum, inter = 2048: grid (hidden / 16, n_tokens), 512
 // threads.  Unit u = (expert u / 4, column quarter u % 4 of 512 = blocks
 // 2 (u % 4), + 1) of the workgroup's 16 output rows; wave w runs units w,
-// w + 8, ... (kU = ceil(n_experts / 2) of them).  The act-quant of every
-// expert's h is the workgroup's own (8 values per thread and chunk).
+// w + 8, ... (kU = ceil(n_experts / 2) of them).  Wave w also act-quantizes
+// (E/deepseek_v4.rs:595, block 64) exactly the h values of its own units
+// (expert w / 4 + 2 i, quarter w % 4), so no wave waits for another before
+// its first MFMA.
 template <int kU>
 __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
     constexpr uint32_t kCols = 2048, kG = kCols / 32;
     constexpr int kJ = 2 * kU, kDepth = WH_PX_DN_DEPTH < kJ ? WH_PX_DN_DEPTH : kJ;
-    constexpr int kPro = WH_PX_PRO < kDepth ? WH_PX_PRO : kDepth;
+    constexpr int kPro = WH_PX_DN_PRO < kDepth ? WH_PX_DN_PRO : kDepth;
     __shared__ __align__(16) uint8_t hc[WH_MAX_EXPERTS * kCols];
     __shared__ __align__(16) uint8_t hsb[WH_MAX_EXPERTS * kG];
     __shared__ float red[WH_MAX_EXPERTS * 4 * 16];
-    __shared__ uint32_t thr[256];
     WH_TL(1, 0);
     const uint32_t tok = blockIdx.y, n = a.n_experts, n_units = 4 * n;
     const uint32_t wave = threadIdx.x >> 6, L = threadIdx.x & 63, g = L >> 4;
     const uint32_t row = blockIdx.x * 16 + (L & 15);
     const float* htok = a.h + (size_t)tok * n * kCols;
-    wh_thr_stage ts;
-    wh_thr_stage_load(ts);
-    // h of every expert: chunk c = 8 columns, expert c / 256 (kU chunks per
-    // thread cover n * 256)
+    // h of the wave's units: chunk i of thread t = columns 8 (c % 256) ..
+    // + 7 of expert c / 256, c = t + 512 i (expert w / 4 + 2 i, quarter
+    // w % 4 for wave w); chunks past the last expert load the last expert's
+    // and are not stored
     float4 hv[kU][2];
 #pragma unroll
     for (int i = 0; i < kU; ++i) {
-        const uint32_t c = threadIdx.x + 512 * i;
-        if (c < n * 256) {
-            hv[i][0] = ((const float4*)htok)[2 * c];
-            hv[i][1] = ((const float4*)htok)[2 * c + 1];
-        } else {
-            hv[i][0] = hv[i][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
+        const uint32_t c = threadIdx.x + 512 * i, e = c >> 8;
+        const float4* hp = (const float4*)(htok + (size_t)(e < n ? e : n - 1) * kCols + 8 * (c & 255));
+        hv[i][0] = hp[0];
+        hv[i][1] = hp[1];
     }
     // the wave's units (a unit past the end repeats unit n_units - 1; its
     // result is not stored)
@@ -394,8 +465,6 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
 #pragma unroll
     for (int j = 0; j < kPro; ++j) wh_mx_raw_load(ring[j], wl[j >> 1], sr[j >> 1], j & 1);
     __builtin_amdgcn_sched_barrier(0);
-    wh_thr_stage_store(ts, thr);
-    __syncthreads();
     WH_TL(1, 1);
 #ifdef WH_TIMELINE
     {
@@ -406,24 +475,24 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
     }
 #endif
     WH_TL(1, 2);
-    // act-quant of h (E/deepseek_v4.rs:595, block 64): h is finite whenever
-    // gate/up was (a non-finite gate/up output is already reported); keep
-    // the arithmetic in range regardless
+    // act-quant of h: h is finite whenever gate/up was (a non-finite gate/up
+    // output is already reported); the codes go to the record layout (column
+    // 8 (c % 4) + j of group c / 4 at byte 4 j + c % 4)
 #pragma unroll
     for (int i = 0; i < kU; ++i) {
-        const uint32_t c = threadIdx.x + 512 * i;
-        const float v[8] = {hv[i][0].x, hv[i][0].y, hv[i][0].z, hv[i][0].w, hv[i][1].x, hv[i][1].y, hv[i][1].z, hv[i][1].w};
-        float amax = 0.0f;
+        const uint32_t c = threadIdx.x + 512 * i, e = c >> 8, idx = c & 255;
+        const float v[8] = {hv[i][0].x, hv[i][0].y, hv[i][0].z, hv[i][0].w,
+                            hv[i][1].x, hv[i][1].y, hv[i][1].z, hv[i][1].w};
+        bool bad;
+        const int k = wh_quant8_scale(v, bad);
+        uint32_t cd[8];
+        wh_quant8_f32_codes(v, k, cd);
+        if (e < n) {
+            uint8_t* grp = hc + kCols * e + 32 * (idx >> 2) + (idx & 3);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
-        amax = wh_amax_block<8>(amax);
-        if (!(amax <= 3.4028235e38f)) amax = 1.0f;
-        const int k = wh_aq_scale_exp(amax, thr);
-        const float inv = wh_pow2f(-k);
-        float q[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) q[j] = wh_e4m3_round(wh_clamp448_finite(v[j] * inv));
-        if (c < n * 256) wh_px_store_codes8(hc + kCols * (c >> 8), hsb + kG * (c >> 8), c & 255, q, k);
+            for (int j = 0; j < 8; ++j) grp[4 * j] = (uint8_t)cd[j];
+            if ((idx & 3) == 0) hsb[kG * e + (idx >> 2)] = (uint8_t)(127 + k - 3);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     WH_TL(1, 3);
@@ -431,7 +500,10 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
     for (int j = kPro; j < kDepth; ++j) wh_mx_raw_load(ring[j], wl[j >> 1], sr[j >> 1], j & 1);
     __builtin_amdgcn_sched_barrier(0);
     WH_TL(1, 4);
-    __syncthreads();
+    // the wave reads back only codes it wrote itself: LDS operations of one
+    // wave complete in order, so no workgroup barrier is needed here (the
+    // clobber keeps the compiler from moving a read above the writes)
+    asm volatile("" ::: "memory");
     WH_TL(1, 5);
     {
         uint32_t dep = wh_opaque_zero(__uint_as_float(*(const uint32_t*)hsb));

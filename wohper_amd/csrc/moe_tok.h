@@ -144,61 +144,6 @@ __device__ __forceinline__ void wh_tok_step(wh_v4f& acc, const wh_mx_raw& r, con
     }
 }
 
-// Act-quant of 8 values held by one thread into the record layout: the
-// thread owns record dwords 2q and 2q + 1 of 32-col group G (q = t % 4,
-// G = t / 4), i.e. v[2k] = column 2q + 8k, v[2k + 1] = column 2q + 1 + 8k
-// (k = 0..3); the 64-block is the 8 lanes t & ~7 .. + 7.  Returns the two
-// code dwords and the block's scale exponent; bad: a non-finite value.
-template <bool kBf16>
-__device__ __forceinline__ void wh_tok_quant8(const float (&v)[8], uint32_t& d0, uint32_t& d1, int& k, bool& bad) {
-    float amax = 0.0f;
-    bad = false;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float m = fabsf(v[i]);
-        bad |= !(m <= 3.4028235e38f);
-        amax = fmaxf(amax, m);
-    }
-    amax = wh_amax_block<8>(amax);
-    if (!(amax <= 3.4028235e38f)) amax = 1.0f;  // non-finite blocks take the fp32 path
-    k = wh_aq_scale_exp_fast(amax);
-    if constexpr (kBf16) {
-        const float inv = wh_pow2f(-k);
-        float t[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float s = v[i] * inv;
-            t[i] = __builtin_fmaf(-fabsf(s), 2.44140625e-4f, s);  // s - |s| 2^-12: ties toward -inf
-        }
-        d0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(t[0], t[2], 0, false);
-        d0 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(t[4], t[6], (int)d0, true);
-        d1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(t[1], t[3], 0, false);
-        d1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(t[5], t[7], (int)d1, true);
-    } else {
-        // wh_e4m3_code_scaled's normal-range formula for all 8 values, the
-        // whole function only when the lane holds a value below 2^(k - 6)
-        // (|h / 2^k| < 2^-6, the E4M3 subnormal grid): one test per lane
-        // instead of one branch per value
-        float amin = fabsf(v[0]);
-#pragma unroll
-        for (int i = 1; i < 8; ++i) amin = fminf(amin, fabsf(v[i]));
-        uint32_t c[8];
-        if (__float_as_uint(amin) < ((uint32_t)(121 + k) << 23)) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) c[i] = wh_e4m3_code_scaled(v[i], k);
-        } else {
-            const uint32_t K = 0x7ffffu - ((uint32_t)(960 + 8 * k) << 20);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t b = __float_as_uint(v[i]), sg = b >> 31;
-                c[i] = (((b & 0x7fffffffu) + K + sg) >> 20) | (sg << 7);
-            }
-        }
-        d0 = c[0] | (c[2] << 8) | (c[4] << 16) | (c[6] << 24);
-        d1 = c[1] | (c[3] << 8) | (c[5] << 16) | (c[7] << 24);
-    }
-}
-
 // Gate/up + SwiGLU, hidden 4096, inter % 16 == 0: grid (ceil(n_experts *
 // inter / 16 / kTiles), n_tokens), 512 threads.  Wave w = (matrix m = w / 4,
 // 1024-col slice s = w % 4) of the workgroup's kTiles 16-row tiles: 4 blocks
