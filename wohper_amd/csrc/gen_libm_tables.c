@@ -157,6 +157,42 @@ static int check_sincos(void) {
     return bad != 0;
 }
 
+// wh_div448 against the float division for every float in [1e-4, FLT_MAX].
+typedef struct {
+    uint32_t b0, b1;
+    long bad;
+} div_job;
+static void* div_verify(void* p) {
+    div_job* j = (div_job*)p;
+    for (uint32_t b = j->b0; b < j->b1; ++b) {
+        const float a = wh_bits_to_float(b);
+        const volatile float want = a / 448.0f;
+        if (wh_float_to_bits(wh_div448(a)) != wh_float_to_bits(want) && j->bad++ < 5)
+            fprintf(stderr, "div448 mismatch: a=%a got %a want %a\n", a, wh_div448(a), (float)want);
+    }
+    return NULL;
+}
+static int check_div448(void) {
+    enum { T = 8 };
+    div_job js[T];
+    pthread_t ts[T];
+    const uint32_t lo = wh_float_to_bits(1.0e-4f), hi = 0x7f800000u;  // [1e-4, FLT_MAX]
+    for (int i = 0; i < T; ++i) {
+        js[i].b0 = lo + (uint32_t)((uint64_t)(hi - lo) * i / T);
+        js[i].b1 = lo + (uint32_t)((uint64_t)(hi - lo) * (i + 1) / T);
+        js[i].bad = 0;
+        pthread_create(&ts[i], NULL, div_verify, &js[i]);
+    }
+    long bad = 0;
+    for (int i = 0; i < T; ++i) {
+        pthread_join(ts[i], NULL);
+        bad += js[i].bad;
+    }
+    if (bad) fprintf(stderr, "div448: %ld mismatches\n", bad);
+    else fprintf(stderr, "div448: every float in [1e-4, FLT_MAX] matches the float division\n");
+    return bad != 0;
+}
+
 // wh_e4m3_code_scaled(h, k) and wh_e4m3_code_pow2(h, k) against the code of wh_e4m3_round(h / 2^k) for
 // t = h / 2^k over every float in [0, 448] (both signs; every 11th float
 // for the other k), with h = t 2^k exactly representable.
@@ -353,6 +389,7 @@ int main(int argc, char** argv) {
 
     if (check_e4m3_round()) return 1;
     if (check_e4m3_code_scaled()) return 1;
+    if (check_div448()) return 1;
     if (check_sincos()) return 1;
 
     // log1pf over [+0, +inf]

@@ -371,6 +371,16 @@ WH_HD uint32_t wh_e4m3_code_pow2(float v, int k) {
     return (a < lim ? sub : nrm) | (sg << 7);
 }
 
+// a / 448.0f, correctly rounded, for finite a >= 1e-4 (the act-quant's
+// amax / 448, E/compute.rs:2511-2514) without a float division: a / 7 is
+// never a midpoint between two floats (a 24-bit a would need 27 significant
+// bits), its distance to the nearest one is at least 2^-27.8 of its value,
+// and the double product a * (1 / 7) is within 2^-52 of it, so rounding
+// that product to float gives a / 7 correctly rounded; dividing by 64 is
+// exact above 1e-4 / 448.  The table generator compares it with the float
+// division for every float in [1e-4, FLT_MAX].
+WH_HD float wh_div448(float a) { return (float)((double)a * (1.0 / 7.0)) * 0.015625f; }
+
 #ifdef __HIPCC__
 // Device form: the bit length from the count of leading zeros.
 __device__ __forceinline__ uint32_t wh_log2f_thr_dev(int e) {
@@ -381,10 +391,10 @@ __device__ __forceinline__ uint32_t wh_log2f_thr_dev(int e) {
 // ceil(log2f(max(amax, 1e-4) / 448)): the act-quant scale exponent
 // (E/compute.rs:2511-2514) without the threshold table.
 __device__ __forceinline__ int wh_aq_scale_exp_fast(float amax) {
-    const float r = fmaxf(amax, 1.0e-4f) / 448.0f;
+    const float r = wh_div448(fmaxf(amax, 1.0e-4f));
     const uint32_t b = wh_float_to_bits(r);
     const int e = (int)((b >> 23) & 0xff) - 127;
     const uint32_t m = b & 0x7fffff;
-    return (m != 0u && m > wh_log2f_thr_dev(e)) ? e + 1 : e;
+    return m > wh_log2f_thr_dev(e) ? e + 1 : e;  // (m > threshold implies m != 0)
 }
 #endif

@@ -176,18 +176,19 @@ __device__ __forceinline__ void wh_px_store_codes8(uint8_t* rec, uint8_t* sb, ui
 
 // The amax of a 64-block held as 8 values by each of 8 consecutive lanes,
 // and its act-quant scale exponent k (E/compute.rs:2504-2521); bad: a
-// non-finite value in the thread's 8.
+// non-finite value in the thread's 8.  The maxima run on the magnitudes'
+// bit patterns (ordered as integers for non-negative floats), so the DPP
+// moves fold into the integer max; a block holding inf or NaN takes amax 1
+// (its values are reported as non-finite and not used).
 __device__ __forceinline__ int wh_quant8_scale(const float (&v)[8], bool& bad) {
-    float amax = 0.0f;
-    bad = false;
+    uint32_t m = 0u;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float m = fabsf(v[i]);
-        bad |= !(m <= 3.4028235e38f);
-        amax = fmaxf(amax, m);
-    }
-    amax = wh_amax_block<8>(amax);
-    if (!(amax <= 3.4028235e38f)) amax = 1.0f;  // non-finite blocks take the fp32 path
+    for (int i = 0; i < 8; ++i) m = max(m, __float_as_uint(v[i]) & 0x7fffffffu);
+    bad = m > 0x7f7fffffu;
+    m = max(m, (uint32_t)__builtin_amdgcn_mov_dpp((int)m, 0xb1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+    m = max(m, (uint32_t)__builtin_amdgcn_mov_dpp((int)m, 0x4e, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+    m = max(m, (uint32_t)__builtin_amdgcn_mov_dpp((int)m, 0x141, 0xf, 0xf, false));  // row_half_mirror
+    const float amax = m > 0x7f7fffffu ? 1.0f : __uint_as_float(m);
     return wh_aq_scale_exp_fast(amax);
 }
 
@@ -198,11 +199,13 @@ __device__ __forceinline__ int wh_quant8_scale(const float (&v)[8], bool& bad) {
 // holds a value under 2^(k - 6); where no value is that small the two agree.
 // A zero keeps its sign (0x80 for -0; the MFMA takes it as 0).
 __device__ __forceinline__ void wh_quant8_f32_codes(const float (&v)[8], int k, uint32_t (&c)[8]) {
-    const uint32_t K = 0x7ffffu - ((uint32_t)(960 + 8 * k) << 20), lim = (uint32_t)(121 + k) << 23;
-    float amin = fabsf(v[0]);
+    uint32_t K = 0x7ffffu - ((uint32_t)(960 + 8 * k) << 20);
+    asm volatile("" : "+v"(K));  // one constant per block: a + K + sign is then one add3
+    const uint32_t lim = (uint32_t)(121 + k) << 23;
+    uint32_t amin = 0xffffffffu;
 #pragma unroll
-    for (int i = 1; i < 8; ++i) amin = fminf(amin, fabsf(v[i]));
-    if (__builtin_amdgcn_ballot_w64(__float_as_uint(amin) < lim) != 0) {  // wave-uniform
+    for (int i = 0; i < 8; ++i) amin = min(amin, __float_as_uint(v[i]) & 0x7fffffffu);
+    if (__builtin_amdgcn_ballot_w64(amin < lim) != 0) {  // wave-uniform
 #pragma unroll
         for (int i = 0; i < 8; ++i) c[i] = wh_e4m3_code_pow2(v[i], k);
     } else {
@@ -432,7 +435,9 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
     __shared__ float red[WH_MAX_EXPERTS * 4 * 16];
     WH_TL(1, 0);
     const uint32_t tok = blockIdx.y, n = a.n_experts, n_units = 4 * n;
-    const uint32_t wave = threadIdx.x >> 6, L = threadIdx.x & 63, g = L >> 4;
+    // wave-uniform in SGPRs: the expert table reads are scalar loads, which
+    // do not queue behind the h loads
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), L = threadIdx.x & 63, g = L >> 4;
     const uint32_t row = blockIdx.x * 16 + (L & 15);
     const float* htok = a.h + (size_t)tok * n * kCols;
     // h of the wave's units: chunk i of thread t = columns 8 (c % 256) ..
@@ -475,11 +480,15 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
     }
 #endif
     WH_TL(1, 2);
-    // act-quant of h: h is finite whenever gate/up was (a non-finite gate/up
-    // output is already reported); the codes go to the record layout (column
-    // 8 (c % 4) + j of group c / 4 at byte 4 j + c % 4)
-#pragma unroll
-    for (int i = 0; i < kU; ++i) {
+    // act-quant of h, chunk i = unit i's 512 values (measured: quantizing
+    // each unit just before its MFMAs instead was slower): h is finite whenever
+    // gate/up was (a non-finite gate/up output is already reported); the
+    // codes go to the record layout (column 8 (c % 4) + j of group c / 4 at
+    // byte 4 j + c % 4).  The wave reads back only codes it wrote itself:
+    // LDS operations of one wave complete in order, so no workgroup barrier
+    // is needed (the clobber keeps the compiler from moving a read above the
+    // writes).
+    auto quant_chunk = [&](int i) {
         const uint32_t c = threadIdx.x + 512 * i, e = c >> 8, idx = c & 255;
         const float v[8] = {hv[i][0].x, hv[i][0].y, hv[i][0].z, hv[i][0].w,
                             hv[i][1].x, hv[i][1].y, hv[i][1].z, hv[i][1].w};
@@ -493,17 +502,16 @@ __global__ void __launch_bounds__(512, 1) k_moe_down_px(wh_moe_args a) {
             for (int j = 0; j < 8; ++j) grp[4 * j] = (uint8_t)cd[j];
             if ((idx & 3) == 0) hsb[kG * e + (idx >> 2)] = (uint8_t)(127 + k - 3);
         }
-    }
+        asm volatile("" ::: "memory");
+    };
+#pragma unroll
+    for (int i = 0; i < kU; ++i) quant_chunk(i);
     __builtin_amdgcn_sched_barrier(0);
     WH_TL(1, 3);
 #pragma unroll
     for (int j = kPro; j < kDepth; ++j) wh_mx_raw_load(ring[j], wl[j >> 1], sr[j >> 1], j & 1);
     __builtin_amdgcn_sched_barrier(0);
     WH_TL(1, 4);
-    // the wave reads back only codes it wrote itself: LDS operations of one
-    // wave complete in order, so no workgroup barrier is needed here (the
-    // clobber keeps the compiler from moving a read above the writes)
-    asm volatile("" ::: "memory");
     WH_TL(1, 5);
     {
         uint32_t dep = wh_opaque_zero(__uint_as_float(*(const uint32_t*)hsb));
