@@ -51,8 +51,10 @@ DOWN_BYTES = 6 * (4_194_304 + 262_144) + 6 * 2048 * 4 + 4096 * 4           # 26,
 KERNELS = {False: ("k_moe_gateup_tok<3, 4, true>", "k_moe_down_px<3>"), True: ("k_moe_gateup<16, 4>", "k_moe_down<8, 4>")}
 # HBM bytes per gate/up launch: rocprofv3 FETCH_SIZE and WRITE_SIZE KiB per
 # dispatch, scaled by what the same counters read for a 268,435,456-byte copy
-# (FETCH x2.00, WRITE x1.00); see profiles/.  None: not measured.
-GATEUP_TRAFFIC_BYTES = {False: round((26_245.0 * 2 + 48.0) * 1024), True: round((26_278.6 * 2 + 48.0) * 1024)}
+# (FETCH x2.00, WRITE x1.00); see profiles/ (moe_routed_fp4_token.md, the
+# FETCH_SIZE / WRITE_SIZE table of k_moe_gateup_tok<3, 4, true> and
+# k_moe_gateup<16, 4>).  None: not measured.
+GATEUP_TRAFFIC_BYTES = {False: round((26_259.7 * 2 + 48.0) * 1024), True: round((26_287.3 * 2 + 49.0) * 1024)}
 FP8_BYTES = 4096 * 4096 + 32 * 32 * 4 + 4096 * 4 + 4096 * 4
 
 
@@ -290,8 +292,47 @@ def fp8_decode_layer(ctx, steps: int):
     for exact, key in ((False, "order_free"), (True, "exact")):
         ctx.set_exact_numerics(exact)
         out[key] = _fp8_decode_layer(ctx, steps)
-        out[key]["total_device_us"] = round(sum(v["device_us"] for v in out[key].values()), 2)
+        out[key]["total_device_us_separate"] = round(sum(v["device_us"] for v in out[key].values()), 2)
+        out[key]["wq_a+wkv"] = _fp8_pair(ctx, steps)
+        # the layer as the decode step runs it: wq_a and wkv on their shared
+        # input in one launch
+        out[key]["total_device_us"] = round(sum(out[key][k]["device_us"] for k in ("wq_a+wkv", "wq_b", "wo_a",
+                                                                                    "wo_b")), 2)
     return out
+
+
+def _fp8_pair(ctx, steps: int) -> dict:
+    """wq_a (1024x4096) and wkv (512x4096) on one input, as the decode layer
+    runs them: one wh_fp8_gemv_batch_async pair per step (merged into one
+    launch), back to back over 8 rotating weight copies."""
+    copies = 8
+    rng = np.random.default_rng(8)
+    ha = [ctx.store_fp8_synthetic(1024, 4096, 3, 5000 + k, wl_scales(31 + k, 1024, 4096)) for k in range(copies)]
+    hk = [ctx.store_fp8_synthetic(512, 4096, 3, 6000 + k, wl_scales(41 + k, 512, 4096)) for k in range(copies)]
+    xd, yd = ctx.device_alloc(4096 * 4), ctx.device_alloc(1536 * 4)
+    ctx.to_device(xd, rng.standard_normal(4096).astype(np.float32))
+    per_copy = [[(ha[k], 0, 1024, xd, yd), (hk[k], 0, 512, xd, yd + 1024 * 4)] for k in range(copies)]
+    descs = [ctx.gemv_descs(d) for d in per_copy]
+    timed = ctx.gemv_descs([t for k in range(steps) for t in per_copy[k % copies]])
+    for k in range(10):
+        ctx.fp8_gemv_batch_async(descs[k % copies])
+    ctx.synchronize()
+    ctx.timer_start()
+    ctx.fp8_gemv_batch_async(timed)
+    us = ctx.timer_stop() / steps
+    nbytes = 1536 * 4096 + 12 * 32 * 4 + 4096 * 4 + 1536 * 4
+    for h in ha + hk:
+        ctx.release(h)
+    ctx.device_free(xd)
+    ctx.device_free(yd)
+    return {"shape": "1024x4096 + 512x4096, one input", "bytes": nbytes, "device_us": round(us, 2),
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+
+
+def wl_scales(seed: int, r: int, c: int):
+    from wohper_amd import workloads as wl
+
+    return wl.fp8_block_scales(seed, r, c)
 
 
 def _fp8_decode_layer(ctx, steps: int):
@@ -712,6 +753,8 @@ def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps:
            "host_loop": {"step_us": round(loop_us / steps, 1), "wall_step_us": round(loop_wall / steps * 1e6, 1)},
            "GBps": round(layer_bytes * n_layers / (step_us * 1e-6) / 1e9, 1)}
     res["frac_of_hbm_peak"] = round(res["GBps"] / HBM_PEAK_GBS, 4)
+    if graph:
+        res["with_gpu_router"] = stack_with_router(ctx, descs, moe_x, moe_out, n_layers, steps, seed)
     for k in list(dev.values()) + [y, moe_x, moe_out]:
         ctx.device_free(k)
     if batch_steps > 0:
@@ -725,6 +768,55 @@ def decode_stack(n_layers: int, steps: int, warmup: int, seed: int, batch_steps:
                                                                   "tokens_per_s")}}
     ctx.close()
     return res
+
+
+def stack_with_router(ctx, descs, moe_x, moe_out, n_layers: int, steps: int, seed: int) -> dict:
+    """The batch-1 stack with each layer's experts chosen on the device: per
+    layer the FP8 projections, the layer's bf16 router (256x4096 + bias,
+    sqrt-softplus, top-6, route_scale 1.5) on the MoE input, and the shared +
+    6 routed experts read from the router's device output (no host round
+    trip); each step one HIP graph, replayed back to back."""
+    from wohper_amd import model_format as mf
+    from wohper_amd import workloads as wl
+
+    rng = np.random.default_rng(seed + 17)
+    for L in range(n_layers):
+        gate = ((rng.standard_normal((wl.N_ROUTED, wl.HIDDEN)).astype(np.float32) * 0.02).view(np.uint32) >> 16)
+        bias = (rng.standard_normal(wl.N_ROUTED) * 0.05).astype(np.float32)
+        blk = mf.build_synthetic_quant_block([
+            mf.SyntheticTensor(f"layers.{L}.ffn.gate.weight", 9, (wl.N_ROUTED, wl.HIDDEN),
+                               gate.astype(np.uint16).tobytes(), 11, 2404),
+            mf.SyntheticTensor(f"layers.{L}.ffn.gate.bias", 9, (wl.N_ROUTED,), bias.tobytes(), 12, 2405)])
+        ctx.store_router(L, blk, wl.HIDDEN)
+    xb = np.empty(wl.HIDDEN, np.uint16)
+    ctx.from_device(xb, moe_x)
+    rx = ctx.device_alloc(wl.HIDDEN * 4)  # the router reads the same values as f32
+    ctx.to_device(rx, (xb.astype(np.uint32) << 16).view(np.float32))
+    rout = ctx.device_alloc(256)  # ids (64 B), weights (64 B), count
+
+    def step():
+        for L in range(n_layers):
+            ctx.fp8_gemv_batch_async(descs[L])
+            ctx.route_experts_async(L, rx, wl.HIDDEN, wl.TOPK, 0, 0, rout, rout + 64, rout + 128, route_scale=1.5)
+            ctx.routed_and_shared_experts_dev_async(L, rout, rout + 64, rout + 128, wl.TOPK, (L, wl.N_ROUTED), moe_x,
+                                                    True, moe_out)
+
+    step()
+    ctx.synchronize()
+    g = ctx.graph_capture(step)
+    ctx.graph_launch(g)
+    ctx.synchronize()
+    ctx.timer_start()
+    for _ in range(steps):
+        ctx.graph_launch(g)
+    us = ctx.timer_stop() / steps
+    ctx.synchronize()
+    ctx.graph_release(g)
+    ctx.device_free(rx)
+    ctx.device_free(rout)
+    return {"per_layer": "FP8 projections, bf16 router 256x4096 top-6 on the device, shared + 6 routed experts "
+                         "from the router's device output",
+            "step_us": round(us, 1), "layer_us": round(us / n_layers, 2)}
 
 
 def decode_stack_batch16(ctx, layers, n_layers: int, steps: int, seed: int, batch: int = 16):
@@ -911,9 +1003,12 @@ def timeline(lib_path: str, seed: int = 2) -> dict:
         ctx.store_router(1000 + k, blk, cols)
     rx, rout = ctx.device_alloc(cols * 4), ctx.device_alloc(256)
     ctx.to_device(rx, rng.standard_normal(cols).astype(np.float32))
-    assert lib.wh_debug_timeline(0, None, 0) == 0  # clears the stamps
     for i in range(12):
         ctx.synchronize()
+        if i == 11:
+            # clears the stamps: the "last:" points then hold only the last
+            # call's last workgroup (earlier calls' last workgroups differ)
+            assert lib.wh_debug_timeline(0, None, 0) == 0
         ctx.route_experts_async(1000 + i % n_layers, rx, cols, 6, 0, 0, rout, rout + 64, rout + 128, route_scale=1.5)
     ctx.synchronize()
     res["router"] = read(0, TIMELINE_POINTS["router"])
