@@ -1172,6 +1172,14 @@ def main():
         log(f"expert pack load: {extra['expert_pack_load']}")
     if args.batch_steps > 0:
         extra["ragged_batch"] = ragged_batch(ctx, args.layers, args.batch_steps, 3, args.exact)
+        if not args.exact:
+            # the configuration's own wording: MFMA only for experts of at
+            # least 16 tokens (the rest on the exact items)
+            t16 = ragged_batch(ctx, args.layers, args.batch_steps, 3, False, 16)
+            extra["ragged_batch"]["mfma_min_16"] = {k: t16[k] for k in ("numerics", "experts_on_mfma", "us_per_step",
+                                                                         "GBps", "frac_of_hbm_peak",
+                                                                         "device_us_per_step")}
+            ctx.set_moe_mfma_min(1)
         ctx.set_exact_numerics(args.exact)
         log(f"ragged batch: {extra['ragged_batch']}")
     cpu = None

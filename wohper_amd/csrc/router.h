@@ -225,6 +225,10 @@ struct wh_router_sel {
     uint32_t* out_ids;       // [active]
     float* out_scores;       // [active]
     uint32_t* out_count;
+    // k_router_bf16 only: every workgroup's 4 rows are published already in
+    // selection order (rows % 4 == 0, rows <= 256, no available list, no
+    // hash row); logits then holds [rows] u64 (score, key) and [rows] u32 ids
+    uint32_t sorted;
 };
 
 // f32::total_cmp order as a signed key.
@@ -389,6 +393,91 @@ __device__ __forceinline__ void wh_router_select_wave_n(const wh_router_sel& a, 
     }
 }
 
+// Selection and weights when every workgroup of k_router_bf16 published its
+// 4 candidates in selection order (key descending, then row ascending):
+// lane L takes workgroup L's list, already sorted, with the scores beside
+// the keys, so the last workgroup's wave loads one list per lane and goes
+// straight to the rounds of wh_router_select_wave_n (the same order: the
+// largest key, ties to the smallest row); the winner's lane hands its score
+// to the selected slot's lane.
+__device__ __forceinline__ void wh_router_select_sorted(const wh_router_sel& a) {
+    const uint32_t L = threadIdx.x & 63, n_lists = a.rows / 4;
+    const uint64_t* kv = (const uint64_t*)a.logits;
+    const uint64_t* idp = (const uint64_t*)(a.logits + 2 * a.rows);
+    int32_t qk[4];
+    float qs[4];
+    uint32_t qp[4], qn = 0;
+    if (L < n_lists) {
+        uint64_t d[4], e[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d[i] = __hip_atomic_load(kv + 4 * L + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) e[i] = __hip_atomic_load(idp + 2 * L + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            qs[i] = __uint_as_float((uint32_t)d[i]);
+            qk[i] = (int32_t)(uint32_t)(d[i] >> 32);
+            qp[i] = (uint32_t)(e[i >> 1] >> (32 * (i & 1)));
+        }
+        qn = 4;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qk[i] = INT32_MIN, qs[i] = 0.0f, qp[i] = 0xffffffffu;
+    }
+#ifdef WH_TIMELINE
+    WH_TL_USE(qk[0]);
+    WH_TL(0, 6);
+    WH_TL(0, 8);
+#endif
+    uint32_t my_sel = 0, n = 0;
+    float my_sc = 0.0f;
+    for (; n < a.active; ++n) {
+        const bool has = qn > 0;
+        if (__ballot(has) == 0) break;  // uniform: no candidate left
+        const int32_t bk = has ? qk[0] : INT32_MIN;
+        const int32_t mk = wh_wave_max_i32(bk);
+        const uint64_t at = __ballot(has && bk == mk);
+        const uint32_t mp = __popcll(at) == 1
+                                ? (uint32_t)__builtin_amdgcn_readlane((int)qp[0], (int)__ffsll((long long)at) - 1)
+                                : wh_wave_min_u32(has && bk == mk ? qp[0] : 0xffffffffu);
+        const bool win = has && bk == mk && qp[0] == mp;  // one lane: rows are distinct
+        const int wl = (int)__ffsll((long long)__ballot(win)) - 1;
+        const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qs[0]), wl));
+        if (win) {  // the winner pops its head
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                qk[i] = qk[i + 1];
+                qs[i] = qs[i + 1];
+                qp[i] = qp[i + 1];
+            }
+            --qn;
+        }
+        if (L == n) {
+            my_sel = mp;
+            my_sc = ws;
+        }
+    }
+    WH_TL(0, 9);
+    // finalize_route_weights (E/compute.rs:2254-2268): the sum in route
+    // order, then every lane its own weight
+    const float v = L < n ? my_sc : 0.0f;
+    float sum = 0.0f;
+#pragma unroll 1
+    for (uint32_t i = 0; i < n; ++i) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+    const bool norm = a.math != 0 && n > 0;
+    const bool ok = sum > 0.0f && sum <= 3.4028235e38f;
+    const float uniform = n ? a.route_scale / (float)n : 0.0f;
+#ifdef WH_TIMELINE
+    WH_TL_USE(sum);
+    WH_TL(0, 10);
+#endif
+    if (L < n) {
+        a.out_ids[L] = my_sel;
+        a.out_scores[L] = !norm ? v : (ok ? v / sum * a.route_scale : uniform);
+    }
+    if (L == 0) *a.out_count = n;
+}
+
 // kSlots candidates per lane: 4 up to 256 candidates, else 16.  sk: the
 // selection keys (score + bias) when precomputed, else null.
 __device__ __forceinline__ void wh_router_select_wave(const wh_router_sel& a, const float* sc, const float* sk,
@@ -441,7 +530,27 @@ __global__ void __launch_bounds__(64) k_router_bf16(const uint16_t* __restrict__
     if (threadIdx.x < WH_EXP_TAB_LEN) exp_tab[threadIdx.x] = tv;
     __syncthreads();
     WH_TL(0, 3);
-    if (writer) {
+    if (a.sorted) {
+        // the workgroup's 4 rows in selection order: writer j (lane 16 j)
+        // takes rank = the rows ahead of it (a larger key, or an equal key
+        // and a smaller row)
+        const float score = a.math ? wh_sqrt_softplus(v, exp_tab) : v;
+        const int32_t key = wh_total_key(a.math && a.bias ? score + bias : score);
+        const uint32_t j = threadIdx.x >> 4;
+        uint32_t rank = 0;
+#pragma unroll
+        for (uint32_t o = 0; o < 4; ++o) {
+            const int32_t ko = __shfl(key, (int)(16 * o), 64);
+            rank += (ko > key || (ko == key && o < j)) ? 1u : 0u;
+        }
+        if (writer) {
+            const uint32_t at = blockIdx.x * 4 + rank;
+            const uint64_t d = ((uint64_t)(uint32_t)key << 32) | __float_as_uint(score);
+            __hip_atomic_store((uint64_t*)a.logits + at, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store((uint32_t*)(a.logits + 2 * a.rows) + at, row, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    } else if (writer) {
         const float score = a.math ? wh_sqrt_softplus(v, exp_tab) : v;
         float* pub = const_cast<float*>(a.logits);
         wh_store_coherent(pub + row, score);
@@ -454,6 +563,12 @@ __global__ void __launch_bounds__(64) k_router_bf16(const uint16_t* __restrict__
     last = __shfl(last, 0, 64);
     WH_TL(0, 5);
     if (!last) return;
+    if (a.sorted) {
+        wh_router_select_sorted(a);
+        WH_TL(0, 7);
+        if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     // all published scores and keys are requested before the first LDS
     // store, so the wave waits for one round trip, not one per pass
     auto gather = [&](auto pass) {

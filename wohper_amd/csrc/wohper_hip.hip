@@ -1756,6 +1756,9 @@ int router_launch(wh_ctx* c, const Router& rt, wh_router_sel sa, const float* x,
     sa.out_scores = scores;
     sa.out_count = count;
     if (rt.gate == kGateBf16) {  // one launch: the last workgroup selects
+        // each workgroup's 4 candidates published in selection order where
+        // the candidates are exactly the rows (the scratch holds 3 words a row)
+        sa.sorted = (!avail && sa.n_hash == 0 && rows % 4 == 0 && rows <= 256) ? 1u : 0u;
         WH_HIP(c->rtr_cnt.ensure(sizeof(uint32_t), true));
         k_router_bf16<<<(rows + 3) / 4, 64, cols * sizeof(float), c->stream>>>(rt.bf16, x, cols, sa,
                                                                                c->rtr_cnt.as<uint32_t>());
@@ -2409,11 +2412,11 @@ int wh_route_experts(wh_ctx* c, uint32_t layer, const float* hidden, size_t hidd
     WH_TRY(router_prepare(rt, *opts, hidden_len, active, available ? n_available : rt.rows, &sa));
     // scratch: x [cols], logits [rows], available ids, then the outputs
     const size_t nav = available ? n_available : 0;
-    const size_t words = rt.cols + 2 * rt.rows + nav + 2 * WH_ROUTER_MAX_ACTIVE + 1;
+    const size_t words = rt.cols + 3 * rt.rows + nav + 2 * WH_ROUTER_MAX_ACTIVE + 1;
     WH_HIP(c->rtr.ensure(words * 4, false));
     float* x = c->rtr.as<float>();
-    float* logits = x + rt.cols;  // [2 * rows]: scores and selection keys
-    uint32_t* av = reinterpret_cast<uint32_t*>(logits + 2 * rt.rows);
+    float* logits = x + rt.cols;  // [3 * rows]: scores and selection keys, or (score, key) pairs and ids
+    uint32_t* av = reinterpret_cast<uint32_t*>(logits + 3 * rt.rows);
     uint32_t* ids = av + nav;
     float* sc = reinterpret_cast<float*>(ids + WH_ROUTER_MAX_ACTIVE);
     uint32_t* cnt = reinterpret_cast<uint32_t*>(sc + WH_ROUTER_MAX_ACTIVE);
@@ -2455,7 +2458,7 @@ int wh_route_experts_async(wh_ctx* c, uint32_t layer, const float* x_dev, size_t
         return WH_OK;
     }
     WH_TRY(router_prepare(rt, *opts, hidden_len, active, available_dev ? n_available : rt.rows, &sa));
-    WH_HIP(c->rtr.ensure((rt.cols + 2 * rt.rows + 2 * WH_ROUTER_MAX_ACTIVE + 1) * 4, false));
+    WH_HIP(c->rtr.ensure((rt.cols + 3 * rt.rows + 2 * WH_ROUTER_MAX_ACTIVE + 1) * 4, false));
     float* logits = c->rtr.as<float>() + rt.cols;
     return router_launch(c, rt, sa, x_dev, available_dev, logits, ids_dev, scores_dev, count_dev);
 }
