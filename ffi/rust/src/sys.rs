@@ -290,6 +290,10 @@ extern "C" {
     pub fn wh_hc_post_async(ctx: *mut WhCtx, y_dev: *const f32, residual_dev: *const f32,
                             post_dev: *const f32, comb_dev: *const f32, out_dev: *mut f32, hc: usize,
                             hidden: usize) -> c_int;
+    pub fn wh_mla_attention_decode_batch_async(ctx: *mut WhCtx, layer: *const WhMlaLayer, positions: *const usize,
+                                               npos: usize, hidden_dev: *mut f32, kv_cache_dev: *mut f32,
+                                               kv_stride: usize, kv_capacity: usize, comp_dev: *const *const f32,
+                                               n_comp: *const usize) -> c_int;
     pub fn wh_deepseek_mhc_layer_async(ctx: *mut WhCtx, layer: *const WhMhcLayer, token_pos: usize,
                                        hidden_dev: *mut f32, kv_cache_dev: *mut f32, kv_stride: usize,
                                        kv_capacity: usize, comp_dev: *const f32, n_comp: usize) -> c_int;

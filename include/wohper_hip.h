@@ -684,6 +684,20 @@ int wh_mla_attention_decode_async(wh_ctx* ctx, const wh_mla_layer* layer, size_t
                                   float* kv_cache_dev, size_t kv_stride, size_t kv_capacity, const float* comp_dev,
                                   size_t n_comp);
 
+/* The batched MLA attention of prefill and MTP verify
+ * (compute_deepseek_v4_mla_attention_batch, E/compute.rs:4307-4641) over
+ * npos positions in ascending order (hidden_dev [npos x hidden] in place,
+ * their KV cache rows written): the projections run over all positions at
+ * once (gemv_fp8_e4m3_ue8m0_rows_multi, each input bit-identical to the
+ * single-input kernels with exact numerics), the norms, RoPE and cache rows
+ * per position, then each position's window softmax over the cache rows up
+ * to its own and its n_comp[i] compressed rows at comp_dev[i] (host arrays
+ * of npos entries, or NULL for none).  With exact numerics the outputs
+ * equal npos calls of wh_mla_attention_decode_async in position order. */
+int wh_mla_attention_decode_batch_async(wh_ctx* ctx, const wh_mla_layer* layer, const size_t* positions, size_t npos,
+                                        float* hidden_dev, float* kv_cache_dev, size_t kv_stride, size_t kv_capacity,
+                                        const float* const* comp_dev, const size_t* n_comp);
+
 /* ------------------------------------------------------------------
  * mHC hyper-connections (E/compute.rs:4945-5092), device pointers, f32.
  * hc copies of the hidden state form a stream of hc * hidden floats;

@@ -90,6 +90,7 @@ EXPORTED = (
     "wh_routed_and_shared_experts_noalloc_async",
     "wh_rope_inv_freqs", "wh_deepseek_rope_for_layer", "wh_rms_norm_async", "wh_rope_async",
     "wh_act_quant_dequant_async", "wh_window_attention_async", "wh_mla_attention_decode_async",
+    "wh_mla_attention_decode_batch_async",
     "wh_hc_split_sinkhorn_async", "wh_hc_pre_async", "wh_hc_post_async",
     "wh_graph_begin", "wh_graph_end", "wh_graph_launch", "wh_graph_release",
     "wh_routed_and_shared_experts_dev_async", "wh_deepseek_mhc_layer_async",
@@ -270,6 +271,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_act_quant_dequant_async": (c.c_int, [vp, vp, sz, sz]),
         "wh_window_attention_async": (c.c_int, [vp, vp, sz, sz, sz, vp, sz, sz, vp, sz, vp, vp, sz, sz, vp, vp]),
         "wh_mla_attention_decode_async": (c.c_int, [vp, c.POINTER(WhMlaLayer), sz, vp, vp, sz, sz, vp, sz]),
+        "wh_mla_attention_decode_batch_async": (c.c_int, [vp, c.POINTER(WhMlaLayer), c.POINTER(sz), sz, vp, vp, sz,
+                                                          sz, c.POINTER(vp), c.POINTER(sz)]),
         "wh_hc_split_sinkhorn_async": (c.c_int, [vp, vp, vp, vp, sz, sz, c.c_float, vp, vp, vp]),
         "wh_hc_pre_async": (c.c_int, [vp, vp, vp, vp, sz, sz, sz, c.c_float, vp, vp, vp, vp]),
         "wh_hc_post_async": (c.c_int, [vp, vp, vp, vp, vp, vp, sz, sz]),
@@ -754,6 +757,22 @@ class Context:
         _check(self.lib.wh_mla_attention_decode_async(self._h, ctypes.byref(layer), token_pos, hidden_ptr, kv_ptr,
                                                       kv_stride, kv_capacity, comp_ptr or None, n_comp),
                "mla_attention_decode_async")
+
+    def mla_attention_decode_batch_async(self, layer: "WhMlaLayer", positions, hidden_ptr: int, kv_ptr: int,
+                                         kv_stride: int, kv_capacity: int, comps=None):
+        """compute_deepseek_v4_mla_attention_batch over ascending positions:
+        hidden_ptr holds len(positions) rows of hidden floats, overwritten
+        with the attention outputs.  comps: None, or one (device pointer,
+        row count) of compressed rows per position."""
+        n = len(positions)
+        pos = (ctypes.c_size_t * n)(*[int(p) for p in positions])
+        cp = cn = None
+        if comps is not None:
+            cp = (ctypes.c_void_p * n)(*[int(p) or None for p, _ in comps])
+            cn = (ctypes.c_size_t * n)(*[int(k) for _, k in comps])
+        _check(self.lib.wh_mla_attention_decode_batch_async(self._h, ctypes.byref(layer), pos, n, hidden_ptr, kv_ptr,
+                                                            kv_stride, kv_capacity, cp, cn),
+               "mla_attention_decode_batch_async")
 
     def deepseek_mhc_layer_async(self, layer: "WhMhcLayer", token_pos: int, hidden_ptr: int, kv_ptr: int,
                                  kv_stride: int, kv_capacity: int, comp_ptr: int = 0, n_comp: int = 0):

@@ -3844,6 +3844,142 @@ int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token
     return WH_OK;
 }
 
+// The batched MLA attention of prefill and MTP verify
+// (compute_deepseek_v4_mla_attention_batch, E/compute.rs:4307-4641): the
+// projections over all positions at once (rows_multi, bit-identical per
+// input to the single-input kernels in exact numerics), the per-position
+// norms, RoPE and KV cache rows, then every position's window softmax (a
+// position reads only cache rows at or before its own, so writing every
+// row first changes nothing), and the grouped output projections batched
+// again.
+int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const size_t* positions, size_t npos,
+                                        float* hidden_dev, float* kv_cache_dev, size_t kv_stride, size_t kv_capacity,
+                                        const float* const* comp_dev, const size_t* n_comp) {
+    if (!c || !L || !positions || !hidden_dev || !kv_cache_dev) return WH_INVALID_ARGUMENT;
+    if (npos == 0) return WH_INVALID_SHAPE;  // "MLA batch ys size"
+    for (size_t i = 0; i < npos; ++i) {
+        if (i && positions[i] <= positions[i - 1]) return WH_INVALID_ARGUMENT;  // ascending positions
+        if (n_comp && n_comp[i] && (!comp_dev || !comp_dev[i])) return WH_INVALID_ARGUMENT;
+    }
+    const size_t heads = L->heads, nope = L->nope_dim, rope = L->rope_dim, head_dim = nope + rope;
+    const size_t q_full = heads * head_dim, groups = L->o_groups, o_lora = L->o_lora_rank;
+    if (groups == 0 || o_lora == 0 || q_full == 0 || q_full % groups != 0) return WH_INVALID_SHAPE;
+    if (rope % 2) return WH_INVALID_SHAPE;
+    const size_t group_in = q_full / groups, o_mid = groups * o_lora, pairs = rope / 2;
+    if (kv_stride < head_dim || positions[npos - 1] >= kv_capacity) return WH_INVALID_SHAPE;
+    size_t max_keys = 0;
+    for (size_t i = 0; i < npos; ++i) {
+        const size_t ctx_i = positions[i] + 1, nw = ctx_i - (ctx_i > 128 ? ctx_i - 128 : 0);
+        const size_t nk = nw + (n_comp ? n_comp[i] : 0);
+        WH_TRY(attn_check(heads, head_dim, nope, pairs, nk, positions[i]));
+        max_keys = std::max(max_keys, nk);
+    }
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
+    const Tensor* wq_a = find_tensor(c, L->wq_a);
+    const Tensor* wq_b = find_tensor(c, L->wq_b);
+    const Tensor* wkv = find_tensor(c, L->wkv);
+    const Tensor* wo_a = find_tensor(c, L->wo_a);
+    const Tensor* wo_b = find_tensor(c, L->wo_b);
+    if (!wq_a || !wq_b || !wkv || !wo_a || !wo_b) return WH_NOT_RESIDENT;
+    for (const Tensor* t : {wq_a, wq_b, wkv, wo_a, wo_b})
+        if (t->kind != kFp8) return WH_INVALID_QUANT_FORMAT;
+    const size_t hidden = wq_a->cols, q_lora = wq_a->rows;
+    if (wkv->cols != hidden || wkv->rows != head_dim || wq_b->cols != q_lora || wq_b->rows != q_full ||
+        wo_a->cols != group_in || wo_a->rows != o_mid || wo_b->cols != o_mid || wo_b->rows != hidden)
+        return WH_INVALID_SHAPE;
+    if (hidden > WH_ROWPOST_MAX || q_lora > WH_ROWPOST_MAX || kv_stride > 0xffffffffu || npos > 65535)
+        return WH_UNSUPPORTED;
+    if (((uintptr_t)hidden_dev & 15) || ((uintptr_t)kv_cache_dev & 15) || (kv_stride & 3)) return WH_INVALID_ARGUMENT;
+    for (size_t i = 0; comp_dev && i < npos; ++i)
+        if ((uintptr_t)comp_dev[i] & 15) return WH_INVALID_ARGUMENT;
+    WH_HIP(hipSetDevice(c->device));
+    float theta;
+    wh_yarn yarn;
+    int has_yarn;
+    wh_deepseek_rope_for_layer(L->physical_layer, &theta, &yarn, &has_yarn);
+    const float* inv = nullptr;
+    WH_TRY(rope_table(c, rope, theta, has_yarn ? &yarn : nullptr, &inv));
+    // activations of every position, each array 256-byte aligned
+    auto up = [](size_t n) { return (n + 63) & ~(size_t)63; };
+    const size_t o_xq = 0, o_ql = o_xq + up(npos * hidden), o_q = o_ql + up(npos * q_lora),
+                 o_kv = o_q + up(npos * q_full), o_sc = o_kv + up(npos * head_dim), o_at = o_sc + up(heads * max_keys),
+                 o_om = o_at + up(npos * q_full), total = o_om + up(npos * o_mid);
+    WH_HIP(c->mla.ensure(total * sizeof(float), false));
+    float* base = c->mla.as<float>();
+    float *xq = base + o_xq, *ql = base + o_ql, *q = base + o_q, *kvt = base + o_kv, *sc = base + o_sc,
+          *at = base + o_at, *om = base + o_om;
+    // q and kv paths (E/compute.rs:4420-4490): act-quant of every x; wq_a
+    // and wkv over all positions; q norm + act-quant; wq_b over all positions
+    wh_rowpost_args a = rowpost_args(hidden_dev, xq, npos, hidden, hidden, hidden);
+    a.aq_len = (uint32_t)hidden;
+    WH_TRY(rowpost_launch(c, a));
+    WH_TRY(wh_fp8_gemv_multi_pair_async(c, L->wq_a, 0, q_lora, ql, q_lora, L->wkv, 0, head_dim, kvt, head_dim, xq, npos,
+                                        hidden));
+    a = rowpost_args(ql, ql, npos, q_lora, q_lora, q_lora);
+    a.norm = 1;
+    a.w = L->q_norm_bf16;
+    a.aq_len = (uint32_t)q_lora;
+    WH_TRY(rowpost_launch(c, a));
+    WH_TRY(wh_fp8_gemv_multi_async(c, L->wq_b, 0, q_full, ql, npos, q_lora, q, q_full));
+    // per position: per-head norm + RoPE of q; kv norm, RoPE, act-quant of
+    // the non-rope dims into the position's cache row
+    for (size_t i = 0; i < npos; ++i) {
+        a = rowpost_args(q + i * q_full, q + i * q_full, heads, head_dim, head_dim, head_dim);
+        a.norm = 1;
+        a.inv_freqs = inv;
+        a.pairs = (uint32_t)pairs;
+        a.rope_off = (uint32_t)nope;
+        a.position = (uint32_t)positions[i];
+        WH_TRY(rowpost_launch(c, a));
+        a = rowpost_args(kvt + i * head_dim, kv_cache_dev + positions[i] * kv_stride, 1, head_dim, head_dim, head_dim);
+        a.norm = 1;
+        a.w = L->kv_norm_bf16;
+        a.inv_freqs = inv;
+        a.pairs = (uint32_t)pairs;
+        a.rope_off = (uint32_t)nope;
+        a.position = (uint32_t)positions[i];
+        a.aq_len = (uint32_t)nope;
+        WH_TRY(rowpost_launch(c, a));
+    }
+    // every position's window softmax with sink (E/compute.rs:4497-4580)
+    for (size_t i = 0; i < npos; ++i) {
+        const size_t context = positions[i] + 1, window_start = context > 128 ? context - 128 : 0;
+        wh_attn_args w{};
+        w.q = q + i * q_full;
+        w.win = kv_cache_dev + window_start * kv_stride;
+        w.comp = comp_dev ? comp_dev[i] : nullptr;
+        w.sink = L->sink;
+        w.inv_freqs = inv;
+        w.scores = sc;
+        w.out = at + i * q_full;
+        w.heads = (uint32_t)heads;
+        w.head_dim = (uint32_t)head_dim;
+        w.nope_dim = (uint32_t)nope;
+        w.pairs = (uint32_t)pairs;
+        w.n_win = (uint32_t)(context - window_start);
+        w.n_comp = (uint32_t)(n_comp ? n_comp[i] : 0);
+        w.win_ld = (uint32_t)kv_stride;
+        w.token_pos = (uint32_t)positions[i];
+        w.scale = powf((float)head_dim, -0.5f);
+        WH_TRY(attn_launch(c, w));
+    }
+    // o path (E/compute.rs:4582-4631): act-quant per position, wo_a per
+    // output group over all positions, act-quant, wo_b over all positions
+    k_act_quant_inplace<<<(unsigned)((npos * q_full + 63) / 64), 256, 0, c->stream>>>(at, (uint32_t)(npos * q_full),
+                                                                                     64);
+    WH_TRY(wh_fp8_gemv_multi_groups_async(c, L->wo_a, 0, o_mid, o_lora, at, group_in, npos, q_full, om, o_mid));
+    if (o_mid % 64 == 0)  // (q_full is: head_dim % 64 == 0) the 64-blocks stay inside their position
+        k_act_quant_inplace<<<(unsigned)((npos * o_mid + 63) / 64), 256, 0, c->stream>>>(om, (uint32_t)(npos * o_mid),
+                                                                                        64);
+    else
+        for (size_t i = 0; i < npos; ++i)
+            k_act_quant_inplace<<<(unsigned)((o_mid + 63) / 64), 256, 0, c->stream>>>(om + i * o_mid, (uint32_t)o_mid,
+                                                                                     64);
+    WH_TRY(wh_fp8_gemv_multi_async(c, L->wo_b, 0, hidden, om, npos, o_mid, hidden_dev, hidden));
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
 // ------------------------------------------------------------------ mHC
 namespace {
 int hc_check(size_t hc, size_t hidden) {
