@@ -297,4 +297,8 @@ extern "C" {
     pub fn wh_deepseek_mhc_layer_async(ctx: *mut WhCtx, layer: *const WhMhcLayer, token_pos: usize,
                                        hidden_dev: *mut f32, kv_cache_dev: *mut f32, kv_stride: usize,
                                        kv_capacity: usize, comp_dev: *const f32, n_comp: usize) -> c_int;
+    pub fn wh_deepseek_mhc_layer_batch_async(ctx: *mut WhCtx, layer: *const WhMhcLayer, positions: *const usize,
+                                             npos: usize, hidden_dev: *mut f32, kv_cache_dev: *mut f32,
+                                             kv_stride: usize, kv_capacity: usize, comp_dev: *const *const f32,
+                                             n_comp: *const usize) -> c_int;
 }

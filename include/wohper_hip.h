@@ -779,6 +779,29 @@ int wh_deepseek_mhc_layer_async(wh_ctx* ctx, const wh_mhc_layer* layer, size_t t
                                 float* kv_cache_dev, size_t kv_stride, size_t kv_capacity, const float* comp_dev,
                                 size_t n_comp);
 
+/* The batched layer of prefill and MTP verify (E/server/generation.rs:
+ * 2437-2590), replacing compute_layer_deepseek_mhc_phase1_batch
+ * (E/compute.rs:4649-4750), the per-position router and
+ * finish_layer_deepseek_mhc_phase2_batch (E/compute.rs:1817-1870):
+ * hidden_dev holds npos states of hc * hidden floats at ascending positions.
+ *   phase 1: per position y = rms_norm(hc_pre(hc_attn, hidden), attn_norm);
+ *     the attention of all positions as wh_mla_attention_decode_batch_async;
+ *     per position hidden' = hc_post(y, hidden) and g = rms_norm(hc_pre(
+ *     hc_ffn, hidden'), ffn_norm);
+ *   the router per position on its g (wh_route_experts_async);
+ *   the MoE of the batch as wh_moe_batch_async: the union of the selected
+ *     experts in ascending id, each position's router weights divided by
+ *     their sum (the reference's batch path, E/server/generation.rs:
+ *     2487-2506, which renormalises the route_scale'd weights to 1), plus the
+ *     shared expert; hidden = hc_post(z, hidden').
+ * With exact numerics every position is bit-identical to the reference's
+ * batch path.  WH_UNSUPPORTED when an availability list has fewer than
+ * `active` entries (the batch MoE takes `active` routes per position).  At
+ * the model's expert shapes nothing is read back to the host. */
+int wh_deepseek_mhc_layer_batch_async(wh_ctx* ctx, const wh_mhc_layer* layer, const size_t* positions, size_t npos,
+                                      float* hidden_dev, float* kv_cache_dev, size_t kv_stride, size_t kv_capacity,
+                                      const float* const* comp_dev, const size_t* n_comp);
+
 #ifdef __cplusplus
 }
 #endif

@@ -531,3 +531,48 @@ def mhc_decode_layer(hidden_hc, hc: int, hidden: int, hc_attn, hc_ffn, attn_norm
     z = moe(ids, w, g)
     return hc_post(z, h, post2, comb2, hc, hidden), ids, w
 
+
+def mhc_decode_layer_batch(hiddens, positions, hc: int, hidden: int, hc_attn, hc_ffn, attn_norm, ffn_norm, mla: dict,
+                           gate_bits, bias, active: int, route_scale: float, experts, shared, kv_cache, comps=None,
+                           iters: int = 20, eps: float = 1e-6):
+    """The batched layer of prefill and MTP verify (E/server/generation.rs:
+    2437-2590) over ascending positions:
+      compute_layer_deepseek_mhc_phase1_batch (E/compute.rs:4649-4750): per
+      position y = rms_norm(hc_pre(hc_attn, hidden), attn_norm); the batched
+      attention (compute_deepseek_v4_mla_attention_batch, E/compute.rs:
+      4307-4641), which equals mla_attention_decode at each position in
+      order: its multi-input projections give each input the single-input
+      result (E/compute.rs:6447-6452), it writes every KV row before the
+      window loop and each window reads only rows at or before its own
+      position; then per position h = hc_post(y, hidden) and
+      g = rms_norm(hc_pre(hc_ffn, h), ffn_norm);
+      the router per position (E/server/generation.rs:2462-2480; DeepSeek-V4
+      weights are used as the router returns them, 3137-3150);
+      the union MoE with each position's weights divided by their sum
+      (moe_batch, E/server/generation.rs:2487-2569);
+      finish_layer_deepseek_mhc_phase2_batch (E/compute.rs:1817-1870):
+      z = shared(g) + routed sum; hidden = hc_post(z, h).
+    hiddens [npos, hc * hidden]; experts: id -> (w1, w3, w2) as moe_batch
+    takes them; shared: a triple or None; comps: None or one array of
+    compressed rows (or None) per position.  Returns (new hiddens, ids,
+    weights)."""
+    hs = _f(hiddens).reshape(len(positions), hc * hidden)
+    states, gs, posts, combs = [], [], [], []
+    for i, pos in enumerate(positions):
+        y, _, post, comb, _ = hc_pre(*hc_attn, hs[i], hc, hidden, iters, eps)
+        y = rms_norm(y, attn_norm)
+        y = mla_attention_decode(y, token_pos=pos, kv_cache=kv_cache, comp=comps[i] if comps else None, **mla)
+        h = hc_post(y, hs[i], post, comb, hc, hidden)
+        g, _, post2, comb2, _ = hc_pre(*hc_ffn, h, hc, hidden, iters, eps)
+        states.append(h)
+        gs.append(rms_norm(g, ffn_norm))
+        posts.append(post2)
+        combs.append(comb2)
+    routes = [route_select(bf16_gemv(gate_bits, g), active, None, bias, ROUTER_SQRT_SOFTPLUS, route_scale)
+              for g in gs]
+    ids = np.array([r[0] for r in routes], np.int64)
+    w = np.array([r[1] for r in routes], np.float32)
+    z = moe_batch(experts, ids, w, np.stack(gs), shared)
+    out = np.stack([hc_post(z[i], states[i], posts[i], combs[i], hc, hidden) for i in range(len(positions))])
+    return out, ids, w
+

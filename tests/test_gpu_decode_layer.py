@@ -75,6 +75,15 @@ def _setup(ctx, oracle, dev):
         return oracle.mhc_decode_layer(hidden, HC, wl.HIDDEN, attn_p, ffn_p, an, fnorm, mla, gate, bias, ACTIVE,
                                        SCALE, moe, pos, cache, None, ITERS, EPS)
 
+    class Experts:
+        def __getitem__(self, e):
+            return expert(int(e))
+
+    def want_batch(hiddens, positions, cache):
+        return oracle.mhc_decode_layer_batch(hiddens, positions, HC, wl.HIDDEN, attn_p, ffn_p, an, fnorm, mla, gate,
+                                             bias, ACTIVE, SCALE, Experts(), expert(N_EXP), cache, None, ITERS, EPS)
+
+    want.batch = want_batch
     return L, want, handles
 
 

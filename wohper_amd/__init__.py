@@ -93,7 +93,7 @@ EXPORTED = (
     "wh_mla_attention_decode_batch_async",
     "wh_hc_split_sinkhorn_async", "wh_hc_pre_async", "wh_hc_post_async",
     "wh_graph_begin", "wh_graph_end", "wh_graph_launch", "wh_graph_release",
-    "wh_routed_and_shared_experts_dev_async", "wh_deepseek_mhc_layer_async",
+    "wh_routed_and_shared_experts_dev_async", "wh_deepseek_mhc_layer_async", "wh_deepseek_mhc_layer_batch_async",
 )
 
 ROUTER_RAW_LOGITS = 0
@@ -211,6 +211,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "wh_routed_and_shared_experts_dev_async": (c.c_int, [vp, c.c_uint32, vp, vp, vp, sz, c.c_uint32, c.c_uint32,
                                                             vp, c.c_int, vp]),
         "wh_deepseek_mhc_layer_async": (c.c_int, [vp, c.POINTER(WhMhcLayer), sz, vp, vp, sz, sz, vp, sz]),
+        "wh_deepseek_mhc_layer_batch_async": (c.c_int, [vp, c.POINTER(WhMhcLayer), c.POINTER(sz), sz, vp, vp, sz, sz,
+                                                        c.POINTER(vp), c.POINTER(sz)]),
         "wh_graph_begin": (c.c_int, [vp]),
         "wh_graph_end": (c.c_int, [vp, c.POINTER(c.c_uint64)]),
         "wh_graph_launch": (c.c_int, [vp, c.c_uint64]),
@@ -782,6 +784,22 @@ class Context:
         _check(self.lib.wh_deepseek_mhc_layer_async(self._h, ctypes.byref(layer), token_pos, hidden_ptr, kv_ptr,
                                                     kv_stride, kv_capacity, comp_ptr or None, n_comp),
                "deepseek_mhc_layer_async")
+
+    def deepseek_mhc_layer_batch_async(self, layer: "WhMhcLayer", positions, hidden_ptr: int, kv_ptr: int,
+                                       kv_stride: int, kv_capacity: int, comps=None):
+        """The batched layer of prefill and verify over ascending positions:
+        hidden_ptr holds len(positions) states of hc * hidden floats, each
+        updated in place; the routed experts of all positions run as one
+        batch MoE.  comps as in mla_attention_decode_batch_async."""
+        n = len(positions)
+        pos = (ctypes.c_size_t * n)(*[int(p) for p in positions])
+        cp = cn = None
+        if comps is not None:
+            cp = (ctypes.c_void_p * n)(*[int(p) or None for p, _ in comps])
+            cn = (ctypes.c_size_t * n)(*[int(k) for _, k in comps])
+        _check(self.lib.wh_deepseek_mhc_layer_batch_async(self._h, ctypes.byref(layer), pos, n, hidden_ptr, kv_ptr,
+                                                          kv_stride, kv_capacity, cp, cn),
+               "deepseek_mhc_layer_batch_async")
 
     # ------------------------------------------------------------------ mHC
     def hc_split_sinkhorn_async(self, mixes_ptr: int, scale_ptr: int, base_ptr: int, hc: int, iters: int,

@@ -4111,3 +4111,63 @@ int wh_deepseek_mhc_layer_async(wh_ctx* c, const wh_mhc_layer* L, size_t token_p
     WH_TRY(wh_hc_post_async(c, z, state, post2, comb2, hidden_dev, hc, hidden));
     return WH_OK;
 }
+
+// The batched layer of prefill and MTP verify (E/server/generation.rs:
+// 2437-2590): compute_layer_deepseek_mhc_phase1_batch (E/compute.rs:4649-
+// 4750) over every position, the router per position, the union of the
+// selected experts with each position's weights divided by their sum
+// (E/server/generation.rs:2487-2506, the batch MoE), and
+// finish_layer_deepseek_mhc_phase2_batch (E/compute.rs:1817-1870): shared
+// expert + routed sum, hc_post.  hidden_dev holds npos states of hc * hidden.
+int wh_deepseek_mhc_layer_batch_async(wh_ctx* c, const wh_mhc_layer* L, const size_t* positions, size_t npos,
+                                      float* hidden_dev, float* kv_cache_dev, size_t kv_stride, size_t kv_capacity,
+                                      const float* const* comp_dev, const size_t* n_comp) {
+    if (!c || !L || !positions || !hidden_dev || ((uintptr_t)hidden_dev & 15)) return WH_INVALID_ARGUMENT;
+    if (npos == 0) return WH_INVALID_SHAPE;  // "mHC batch hidden state too small"
+    const size_t hc = L->hc, hidden = L->hidden;
+    WH_TRY(hc_check(hc, hidden));
+    if (L->active == 0) return WH_INVALID_ARGUMENT;
+    // the batch MoE takes a fixed number of routes per position: every
+    // position's router must find `active` candidates
+    if (L->available_dev && L->n_available < L->active) return WH_UNSUPPORTED;
+    if (npos > 65535 || hidden % 4) return WH_UNSUPPORTED;
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    const size_t hcd = hc * hidden, slots = L->active;
+    auto up = [](size_t n) { return (n + 63) & ~(size_t)63; };
+    const size_t o_state = 0, o_y = up(npos * hcd), o_g = o_y + up(npos * hidden), o_z = o_g + up(npos * hidden);
+    const size_t o_p1 = o_z + up(npos * hidden), o_c1 = o_p1 + up(npos * hc), o_p2 = o_c1 + up(npos * hc * hc),
+                 o_c2 = o_p2 + up(npos * hc), o_ids = o_c2 + up(npos * hc * hc), o_w = o_ids + up(npos * slots),
+                 o_n = o_w + up(npos * slots), total = o_n + up(npos);
+    WH_HIP(c->layer.ensure(total * sizeof(float), false));
+    float* f = c->layer.as<float>();
+    float *state = f + o_state, *y = f + o_y, *g = f + o_g, *z = f + o_z;
+    float *post1 = f + o_p1, *comb1 = f + o_c1, *post2 = f + o_p2, *comb2 = f + o_c2, *w = f + o_w;
+    uint32_t* ids = reinterpret_cast<uint32_t*>(f + o_ids);
+    uint32_t* count = reinterpret_cast<uint32_t*>(f + o_n);
+    // phase 1: hc_pre + attention norm per position, the batched attention,
+    // hc_post, ffn hc_pre + norm per position (E/compute.rs:4679-4750)
+    for (size_t i = 0; i < npos; ++i)
+        WH_TRY(wh_hc_pre_async(c, L->hc_attn_fn, L->hc_attn_scale, L->hc_attn_base, hc, hidden, L->sinkhorn_iters,
+                               L->hc_eps, hidden_dev + i * hcd, y + i * hidden, post1 + i * hc, comb1 + i * hc * hc));
+    WH_TRY(wh_rms_norm_async(c, y, g, npos, hidden, L->attn_norm_bf16));
+    WH_TRY(wh_mla_attention_decode_batch_async(c, &L->attn, positions, npos, g, kv_cache_dev, kv_stride, kv_capacity,
+                                               comp_dev, n_comp));
+    for (size_t i = 0; i < npos; ++i) {
+        WH_TRY(wh_hc_post_async(c, g + i * hidden, hidden_dev + i * hcd, post1 + i * hc, comb1 + i * hc * hc,
+                                state + i * hcd, hc, hidden));
+        WH_TRY(wh_hc_pre_async(c, L->hc_ffn_fn, L->hc_ffn_scale, L->hc_ffn_base, hc, hidden, L->sinkhorn_iters,
+                               L->hc_eps, state + i * hcd, y + i * hidden, post2 + i * hc, comb2 + i * hc * hc));
+    }
+    WH_TRY(wh_rms_norm_async(c, y, g, npos, hidden, L->ffn_norm_bf16));
+    // the router per position (E/server/generation.rs:2462-2480), then the
+    // experts of the whole batch on the device route lists
+    for (size_t i = 0; i < npos; ++i)
+        WH_TRY(wh_route_experts_async(c, L->layer_id, g + i * hidden, hidden, slots, L->available_dev,
+                                      L->n_available, &L->route, ids + i * slots, w + i * slots, count + i));
+    WH_TRY(wh_moe_batch_async(c, L->layer_id, ids, w, npos, slots, L->shared_layer, L->shared_expert, g, 0, z));
+    for (size_t i = 0; i < npos; ++i)
+        WH_TRY(wh_hc_post_async(c, z + i * hidden, state + i * hcd, post2 + i * hc, comb2 + i * hc * hc,
+                                hidden_dev + i * hcd, hc, hidden));
+    return WH_OK;
+}
