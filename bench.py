@@ -472,6 +472,31 @@ def decode_layer(ctx, n_layers: int, steps: int, graph: bool = True) -> dict:
         r["GBps"] = round(layer_bytes / (us * 1e-6) / 1e9, 1)
         r["frac_of_hbm_peak"] = round(layer_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
         res["exact" if exact else "order_free"] = r
+    # the batched layer of prefill and MTP verify: 16 positions (112..127,
+    # the last with a full window) per layer through
+    # wh_deepseek_mhc_layer_batch_async, the experts of the batch as one
+    # union MoE; host loop of library calls
+    bpos = list(range(cap - 16, cap))
+    hbs = [put((rng.standard_normal((len(bpos), hc * wl.HIDDEN)) * 0.5).astype(np.float32)) for _ in range(n_layers)]
+
+    def bstep():
+        for L in range(n_layers):
+            ctx.deepseek_mhc_layer_batch_async(layers[L], bpos, hbs[L], kvs[L], head_dim, cap)
+
+    bres = {"workload": f"{len(bpos)} positions ({bpos[0]}..{bpos[-1]}) per layer, the same layers"}
+    for exact in (False, True):
+        ctx.set_exact_numerics(exact)
+        bstep()
+        ctx.synchronize()
+        ctx.timer_start()
+        for _ in range(max(2, steps // 4)):
+            bstep()
+        us = ctx.timer_stop() / max(2, steps // 4) / n_layers
+        ctx.synchronize()
+        bres["exact" if exact else "order_free"] = {"layer_us": round(us, 1),
+                                                    "us_per_position": round(us / len(bpos), 2)}
+    res["batch16"] = bres
+    ctx.set_exact_numerics(False)
     for p in keep:
         ctx.device_free(p)
     for t in handles:

@@ -300,5 +300,5 @@ extern "C" {
     pub fn wh_deepseek_mhc_layer_batch_async(ctx: *mut WhCtx, layer: *const WhMhcLayer, positions: *const usize,
                                              npos: usize, hidden_dev: *mut f32, kv_cache_dev: *mut f32,
                                              kv_stride: usize, kv_capacity: usize, comp_dev: *const *const f32,
-                                             n_comp: *const usize) -> c_int;
+                                             n_comp: *const usize, token_ids: *const i64) -> c_int;
 }

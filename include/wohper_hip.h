@@ -794,13 +794,16 @@ int wh_deepseek_mhc_layer_async(wh_ctx* ctx, const wh_mhc_layer* layer, size_t t
  *     their sum (the reference's batch path, E/server/generation.rs:
  *     2487-2506, which renormalises the route_scale'd weights to 1), plus the
  *     shared expert; hidden = hc_post(z, hidden').
+ * token_ids: each position's token for a hash layer's row (the reference
+ * passes each item's token id, E/server/generation.rs:2462-2474), or NULL
+ * for layer->route.hash_token_id at every position.
  * With exact numerics every position is bit-identical to the reference's
  * batch path.  WH_UNSUPPORTED when an availability list has fewer than
  * `active` entries (the batch MoE takes `active` routes per position).  At
  * the model's expert shapes nothing is read back to the host. */
 int wh_deepseek_mhc_layer_batch_async(wh_ctx* ctx, const wh_mhc_layer* layer, const size_t* positions, size_t npos,
                                       float* hidden_dev, float* kv_cache_dev, size_t kv_stride, size_t kv_capacity,
-                                      const float* const* comp_dev, const size_t* n_comp);
+                                      const float* const* comp_dev, const size_t* n_comp, const int64_t* token_ids);
 
 #ifdef __cplusplus
 }

@@ -212,7 +212,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
                                                             vp, c.c_int, vp]),
         "wh_deepseek_mhc_layer_async": (c.c_int, [vp, c.POINTER(WhMhcLayer), sz, vp, vp, sz, sz, vp, sz]),
         "wh_deepseek_mhc_layer_batch_async": (c.c_int, [vp, c.POINTER(WhMhcLayer), c.POINTER(sz), sz, vp, vp, sz, sz,
-                                                        c.POINTER(vp), c.POINTER(sz)]),
+                                                        c.POINTER(vp), c.POINTER(sz), c.POINTER(c.c_int64)]),
         "wh_graph_begin": (c.c_int, [vp]),
         "wh_graph_end": (c.c_int, [vp, c.POINTER(c.c_uint64)]),
         "wh_graph_launch": (c.c_int, [vp, c.c_uint64]),
@@ -786,19 +786,23 @@ class Context:
                "deepseek_mhc_layer_async")
 
     def deepseek_mhc_layer_batch_async(self, layer: "WhMhcLayer", positions, hidden_ptr: int, kv_ptr: int,
-                                       kv_stride: int, kv_capacity: int, comps=None):
+                                       kv_stride: int, kv_capacity: int, comps=None, token_ids=None):
         """The batched layer of prefill and verify over ascending positions:
         hidden_ptr holds len(positions) states of hc * hidden floats, each
         updated in place; the routed experts of all positions run as one
-        batch MoE.  comps as in mla_attention_decode_batch_async."""
+        batch MoE.  comps as in mla_attention_decode_batch_async;
+        token_ids: each position's token for a hash layer, or None for the
+        layer's route options."""
         n = len(positions)
         pos = (ctypes.c_size_t * n)(*[int(p) for p in positions])
-        cp = cn = None
+        cp = cn = tk = None
         if comps is not None:
             cp = (ctypes.c_void_p * n)(*[int(p) or None for p, _ in comps])
             cn = (ctypes.c_size_t * n)(*[int(k) for _, k in comps])
+        if token_ids is not None:
+            tk = (ctypes.c_int64 * n)(*[int(t) for t in token_ids])
         _check(self.lib.wh_deepseek_mhc_layer_batch_async(self._h, ctypes.byref(layer), pos, n, hidden_ptr, kv_ptr,
-                                                          kv_stride, kv_capacity, cp, cn),
+                                                          kv_stride, kv_capacity, cp, cn, tk),
                "deepseek_mhc_layer_batch_async")
 
     # ------------------------------------------------------------------ mHC

@@ -37,7 +37,22 @@ struct wh_hc_args {
     float* comb;           // [hc * hc]
     uint32_t hc, hidden, hc_dim, mix_hc, iters, parts;
     float eps;
+    // several streams at once: stream z (blockIdx.z of the sums, blockIdx.x
+    // of k_hc_finish, blockIdx.y of k_hc_y) reads x + z * hc_dim and writes
+    // y + z * hidden, sums + z * sums_ld, pre / post + z * hc, comb + z * hc * hc
+    uint32_t sums_ld;
 };
+
+// The arguments of stream z of a batched launch.
+__device__ __forceinline__ wh_hc_args wh_hc_at(wh_hc_args a, uint32_t z) {
+    a.x += (size_t)z * a.hc_dim;
+    a.y += (size_t)z * a.hidden;
+    a.sums += (size_t)z * a.sums_ld;
+    a.pre += (size_t)z * a.hc;
+    a.post += (size_t)z * a.hc;
+    a.comb += (size_t)z * a.hc * a.hc;
+    return a;
+}
 
 // Sum over a wave in a fixed butterfly (every lane ends with the same bits).
 __device__ __forceinline__ float wh_hc_wave_sum(float v) {
@@ -52,7 +67,8 @@ __device__ __forceinline__ float wh_hc_wave_sum(float v) {
 // flight meanwhile, while thread 0 adds the previous chunk's products to
 // its running sum in order; two buffers alternate.
 #define WH_HC_CHUNK 768u  // 4 terms per producer thread
-__global__ void __launch_bounds__(256) k_hc_chains(wh_hc_args a) {
+__global__ void __launch_bounds__(256) k_hc_chains(wh_hc_args a0) {
+    const wh_hc_args a = wh_hc_at(a0, blockIdx.z);
     __shared__ __align__(16) float prod[2][WH_HC_CHUNK];
     const uint32_t t = threadIdx.x, c = blockIdx.x;
     const uint32_t n_chunks = (a.hc_dim + WH_HC_CHUNK - 1) / WH_HC_CHUNK;
@@ -103,7 +119,8 @@ __global__ void __launch_bounds__(256) k_hc_chains(wh_hc_args a) {
 // Partial sums (exact numerics off): grid (WH_HC_PARTS, mix_hc + 1), 256
 // threads; workgroup (p, c) sums slice p of chain c's products in a fixed
 // tree.
-__global__ void __launch_bounds__(256) k_hc_partials(wh_hc_args a) {
+__global__ void __launch_bounds__(256) k_hc_partials(wh_hc_args a0) {
+    const wh_hc_args a = wh_hc_at(a0, blockIdx.z);
     __shared__ float red[4];
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63, c = blockIdx.y;
     const uint32_t per = (a.hc_dim + a.parts - 1) / a.parts;
@@ -123,7 +140,8 @@ __device__ __forceinline__ float wh_sigmoid(float v) {
 
 // One workgroup of 256 threads: mixes = chain sums * inverse RMS (or the
 // given mixes), then hc_split_sinkhorn_scalar.
-__global__ void __launch_bounds__(256) k_hc_finish(wh_hc_args a) {
+__global__ void __launch_bounds__(256) k_hc_finish(wh_hc_args a0) {
+    const wh_hc_args a = wh_hc_at(a0, blockIdx.x);
     __shared__ float mixes[WH_HC_MAX_CHAINS];
     __shared__ float comb[WH_HC_MAX_CHAINS];
     __shared__ float rsum[16];
@@ -271,7 +289,8 @@ __global__ void __launch_bounds__(256) k_hc_finish(wh_hc_args a) {
 
 // y[d] = sum over i, in order, of pre[i] * x[i * hidden + d] (the end of
 // hc_pre_into), one output per thread.
-__global__ void __launch_bounds__(256) k_hc_y(wh_hc_args a) {
+__global__ void __launch_bounds__(256) k_hc_y(wh_hc_args a0) {
+    const wh_hc_args a = wh_hc_at(a0, blockIdx.y);
     const uint32_t d = blockIdx.x * 256 + threadIdx.x;
     if (d >= a.hidden) return;
     float acc = 0.0f;
@@ -280,10 +299,18 @@ __global__ void __launch_bounds__(256) k_hc_y(wh_hc_args a) {
 }
 
 // hc_post_into: out[k * hidden + d] = post[k] * y[d], then + comb[k][i] *
-// residual[i * hidden + d] for i in order.
+// residual[i * hidden + d] for i in order.  Stream z = blockIdx.y of a
+// batched launch: y + z * hidden, residual and out + z * hc * hidden,
+// post + z * hc, comb + z * hc * hc.
 __global__ void __launch_bounds__(256) k_hc_post(const float* __restrict__ y, const float* __restrict__ res,
                                                  const float* __restrict__ post, const float* __restrict__ comb,
                                                  float* __restrict__ out, uint32_t hc, uint32_t hidden) {
+    const size_t z = blockIdx.y, hcd = (size_t)hc * hidden;
+    y += z * hidden;
+    res += z * hcd;
+    out += z * hcd;
+    post += z * hc;
+    comb += z * hc * hc;
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (size_t)hc * hidden) return;
     const uint32_t k = (uint32_t)(idx / hidden), d = (uint32_t)(idx % hidden);

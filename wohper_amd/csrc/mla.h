@@ -17,6 +17,7 @@
 #define WH_ROWPOST_MAX 4096u     // values per row of k_rowpost
 #define WH_ATTN_MAX_KEYS 2048u   // window + compressed keys per head
 #define WH_ATTN_MAX_HEAD_DIM 1024u
+#define WH_POS_BATCH 32u         // positions per batched launch of k_rowpost / the attention
 
 __device__ __forceinline__ float wh_bf16_value(uint16_t raw) { return __uint_as_float((uint32_t)raw << 16); }
 
@@ -56,6 +57,12 @@ struct wh_rowpost_args {
     uint32_t pairs, rope_off, position, inverse;
     uint32_t aq_len;            // 0: no act-quant
     uint32_t tree;              // norm: 1 = the sum of squares in a fixed tree (exact numerics off)
+    // several positions in one launch: rows_per_pos > 0 puts row r at
+    // position bpos[r / rows_per_pos] (in place of `position`); out_at_pos
+    // sends row r to out + bpos[r] * ld_out (one row per position: a KV
+    // cache row)
+    uint32_t rows_per_pos, out_at_pos;
+    uint32_t bpos[WH_POS_BATCH];
 };
 
 // kT threads per row (256, or 1024 for a lone row); each thread's values
@@ -68,6 +75,12 @@ __global__ void __launch_bounds__(kT) k_rowpost(wh_rowpost_args a) {
     __shared__ float inv_s;
     const uint32_t t = threadIdx.x, n = a.n;
     const float* x = a.x + (size_t)blockIdx.x * a.ld_in;
+    uint32_t position = a.position;
+    size_t orow = blockIdx.x;
+    if (a.rows_per_pos) {
+        position = a.bpos[blockIdx.x / a.rows_per_pos];
+        if (a.out_at_pos) orow = position;
+    }
     float xv[kPer], wv[kPer];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -137,7 +150,7 @@ __global__ void __launch_bounds__(kT) k_rowpost(wh_rowpost_args a) {
         __syncthreads();
     }
     if (a.pairs) {
-        const float pos = (float)a.position;
+        const float pos = (float)position;
         for (uint32_t p = t; p < a.pairs; p += kT) {
             const float ang = pos * a.inv_freqs[p];
             float sn = wh_sincosf_glibc(ang, 0);
@@ -160,7 +173,7 @@ __global__ void __launch_bounds__(kT) k_rowpost(wh_rowpost_args a) {
         }
         __syncthreads();
     }
-    float* out = a.out + (size_t)blockIdx.x * a.ld_out;
+    float* out = a.out + orow * a.ld_out;
     for (uint32_t i = t; i < n; i += kT) out[i] = v[i];
 }
 
@@ -179,10 +192,45 @@ struct wh_attn_args {
     uint32_t heads, head_dim, nope_dim, pairs;
     uint32_t n_win, n_comp, win_ld, token_pos;
     float scale;           // head_dim^-0.5 (host powf, as the reference)
+    // a batch of positions (nb > 0): slot z = blockIdx.z takes q and out +
+    // z * q_ld, scores + z * scores_ld, token_pos = bpos[z], the window of
+    // the last wlen cache rows up to that position (win = the cache's row
+    // 0), compressed rows bcomp[z] (bncomp[z] of them)
+    uint32_t nb, q_ld, scores_ld, wlen;
+    uint32_t bpos[WH_POS_BATCH];
+    uint32_t bncomp[WH_POS_BATCH];
+    const float* bcomp[WH_POS_BATCH];
 };
 
-__device__ __forceinline__ const float* wh_attn_key(const wh_attn_args& a, uint32_t j) {
-    return j < a.n_win ? a.win + (size_t)j * a.win_ld : a.comp + (size_t)(j - a.n_win) * a.head_dim;
+// One position's keys, queries and outputs.
+struct wh_attn_pos {
+    const float* q;
+    const float* win;
+    const float* comp;
+    float* scores;
+    float* out;
+    uint32_t n_win, n_comp, token_pos;
+};
+
+__device__ __forceinline__ wh_attn_pos wh_attn_resolve(const wh_attn_args& a) {
+    wh_attn_pos v{a.q, a.win, a.comp, a.scores, a.out, a.n_win, a.n_comp, a.token_pos};
+    if (a.nb) {
+        const uint32_t z = blockIdx.z, p = a.bpos[z], context = p + 1;
+        const uint32_t ws = context > a.wlen ? context - a.wlen : 0u;
+        v.q = a.q + (size_t)z * a.q_ld;
+        v.out = a.out + (size_t)z * a.q_ld;
+        v.scores = a.scores + (size_t)z * a.scores_ld;
+        v.win = a.win + (size_t)ws * a.win_ld;
+        v.n_win = context - ws;
+        v.comp = a.bcomp[z];
+        v.n_comp = a.bncomp[z];
+        v.token_pos = p;
+    }
+    return v;
+}
+
+__device__ __forceinline__ const float* wh_attn_key(const wh_attn_args& a, const wh_attn_pos& v, uint32_t j) {
+    return j < v.n_win ? v.win + (size_t)j * a.win_ld : v.comp + (size_t)(j - v.n_win) * a.head_dim;
 }
 
 // scores[h][j] = (sum over d, in order, of q[h][d] * key_j[d]) * scale.
@@ -193,17 +241,19 @@ __device__ __forceinline__ const float* wh_attn_key(const wh_attn_args& a, uint3
 __global__ void __launch_bounds__(256) k_attn_scores(wh_attn_args a) {
     __shared__ float qs[4 * WH_ATTN_MAX_HEAD_DIM];
     __shared__ float tile[64 * 65];
+    const wh_attn_pos v = wh_attn_resolve(a);
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const uint32_t h0 = blockIdx.y * 4, j0 = blockIdx.x * 64;
-    const uint32_t nk = a.n_win + a.n_comp, hd = a.head_dim;
+    const uint32_t nk = v.n_win + v.n_comp, hd = a.head_dim;
+    if (j0 >= nk) return;  // a batched launch's grid covers its longest key list
     for (uint32_t i = t; i < 4 * hd; i += 256) {
         const uint32_t h = h0 + i / hd;
-        qs[i] = h < a.heads ? a.q[(size_t)h * hd + i % hd] : 0.0f;
+        qs[i] = h < a.heads ? v.q[(size_t)h * hd + i % hd] : 0.0f;
     }
     // staging: thread t copies 16 dims (t % 4) of key t / 4
     const uint32_t kk = t >> 2, part = t & 3;
     const bool kon = j0 + kk < nk;
-    const float* krow = kon ? wh_attn_key(a, j0 + kk) : nullptr;
+    const float* krow = kon ? wh_attn_key(a, v, j0 + kk) : nullptr;
     const float* qrow = qs + wave * hd;
     float s = 0.0f;
     for (uint32_t d0 = 0; d0 < hd; d0 += 64) {
@@ -225,7 +275,7 @@ __global__ void __launch_bounds__(256) k_attn_scores(wh_attn_args a) {
         for (uint32_t d = 0; d < 64; ++d) s = s + qrow[d0 + d] * kr[d];
     }
     const uint32_t h = h0 + wave, j = j0 + lane;
-    if (h < a.heads && j < nk) a.scores[(size_t)h * nk + j] = s * a.scale;
+    if (h < a.heads && j < nk) v.scores[(size_t)h * nk + j] = s * a.scale;
 }
 
 // The rest of the window loop for 4 heads x 64 dims per workgroup (grid
@@ -239,17 +289,18 @@ __global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
     __shared__ float wts[4 * WH_ATTN_MAX_KEYS];
     __shared__ float res[4 * 64];
     __shared__ float denom_s[4];
+    const wh_attn_pos v = wh_attn_resolve(a);
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const uint32_t h = blockIdx.y * 4 + wave, d = blockIdx.x * 64 + lane;
-    const uint32_t nk = a.n_win + a.n_comp;
+    const uint32_t nk = v.n_win + v.n_comp;
     const bool hon = h < a.heads;
     float* w = wts + wave * WH_ATTN_MAX_KEYS;
-    const float* sc = a.scores + (size_t)(hon ? h : 0) * nk;
+    const float* sc = v.scores + (size_t)(hon ? h : 0) * nk;
     float mx = -__uint_as_float(0x7f800000u);
     for (uint32_t j = lane; j < nk; j += 64) {
-        const float v = hon ? sc[j] : 0.0f;
-        w[j] = v;
-        mx = fmaxf(mx, v);
+        const float sv = hon ? sc[j] : 0.0f;
+        w[j] = sv;
+        mx = fmaxf(mx, sv);
     }
     mx = wh_wave_max(mx);
     for (uint32_t j = lane; j < nk; j += 64) w[j] = wh_expf_glibc(w[j] - mx, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
@@ -265,14 +316,14 @@ __global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
     if (hon) {
         uint32_t j = 0;
         for (; j + 4 <= nk; j += 4) {
-            const float k0 = wh_attn_key(a, j)[d], k1 = wh_attn_key(a, j + 1)[d];
-            const float k2 = wh_attn_key(a, j + 2)[d], k3 = wh_attn_key(a, j + 3)[d];
+            const float k0 = wh_attn_key(a, v, j)[d], k1 = wh_attn_key(a, v, j + 1)[d];
+            const float k2 = wh_attn_key(a, v, j + 2)[d], k3 = wh_attn_key(a, v, j + 3)[d];
             acc = acc + w[j] * k0;
             acc = acc + w[j + 1] * k1;
             acc = acc + w[j + 2] * k2;
             acc = acc + w[j + 3] * k3;
         }
-        for (; j < nk; ++j) acc = acc + w[j] * wh_attn_key(a, j)[d];
+        for (; j < nk; ++j) acc = acc + w[j] * wh_attn_key(a, v, j)[d];
     }
     __syncthreads();
     const float den = denom_s[wave];
@@ -282,7 +333,7 @@ __global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
     // inverse RoPE: the even lane of a pair in [nope_dim, head_dim) rotates it
     if (d >= a.nope_dim && ((d - a.nope_dim) & 1) == 0 && (d - a.nope_dim) / 2 < a.pairs) {
         const uint32_t p = (d - a.nope_dim) / 2;
-        const float ang = (float)a.token_pos * a.inv_freqs[p];
+        const float ang = (float)v.token_pos * a.inv_freqs[p];
         const float sn = -wh_sincosf_glibc(ang, 0);
         const float cs = wh_sincosf_glibc(ang, 1);
         const float e = res[wave * 64 + lane], o = res[wave * 64 + lane + 1];
@@ -290,5 +341,5 @@ __global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
         res[wave * 64 + lane + 1] = e * sn + o * cs;
     }
     __syncthreads();
-    if (hon) a.out[(size_t)h * a.head_dim + d] = res[wave * 64 + lane];
+    if (hon) v.out[(size_t)h * a.head_dim + d] = res[wave * 64 + lane];
 }

@@ -509,9 +509,21 @@ __global__ void __launch_bounds__(256) k_router_select(wh_router_sel a) {
 // floats of dynamic LDS.  Each workgroup computes four gate rows, their
 // scores and selection keys (score + bias) and publishes them (coherent
 // stores into a.logits [2 * rows]); the last workgroup to arrive selects.
-// *counter is 0 at launch and left at 0.
+// *counter is 0 at launch and left at 0.  grid.y > 1 routes several inputs
+// at once: input z = blockIdx.y reads x + z * x_ld, publishes into
+// a.logits + z * pub_ld, arrives on counter[z] and writes its ids and
+// weights at z * active and its count at z.
 __global__ void __launch_bounds__(64) k_router_bf16(const uint16_t* __restrict__ w, const float* __restrict__ x,
-                                                    uint32_t cols, wh_router_sel a, uint32_t* counter) {
+                                                    uint32_t cols, wh_router_sel a0, uint32_t* counter, uint32_t x_ld,
+                                                    uint32_t pub_ld) {
+    const uint32_t z = blockIdx.y;
+    wh_router_sel a = a0;
+    x += (size_t)z * x_ld;
+    counter += z;
+    a.logits += (size_t)z * pub_ld;
+    a.out_ids += (size_t)z * a0.active;
+    a.out_scores += (size_t)z * a0.active;
+    a.out_count += z;
     extern __shared__ float xs[];
     __shared__ float sc[WH_ROUTER_MAX_ROWS], sk[WH_ROUTER_MAX_ROWS];
     __shared__ uint32_t sel[WH_ROUTER_MAX_ACTIVE];

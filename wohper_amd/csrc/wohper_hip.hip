@@ -1761,7 +1761,7 @@ int router_launch(wh_ctx* c, const Router& rt, wh_router_sel sa, const float* x,
         sa.sorted = (!avail && sa.n_hash == 0 && rows % 4 == 0 && rows <= 256) ? 1u : 0u;
         WH_HIP(c->rtr_cnt.ensure(sizeof(uint32_t), true));
         k_router_bf16<<<(rows + 3) / 4, 64, cols * sizeof(float), c->stream>>>(rt.bf16, x, cols, sa,
-                                                                               c->rtr_cnt.as<uint32_t>());
+                                                                               c->rtr_cnt.as<uint32_t>(), 0, 0);
         WH_HIP(hipGetLastError());
         return WH_OK;
     }
@@ -1773,6 +1773,53 @@ int router_launch(wh_ctx* c, const Router& rt, wh_router_sel sa, const float* x,
         WH_TRY(launch_fp8(c, *t, 0, t->rows, x, logits, 1, 0, 0, 0, 0, nullptr, 0, 0, nullptr, false));
     }
     k_router_select<<<1, 256, 0, c->stream>>>(sa);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// The router of npos inputs (x: npos rows x_ld floats apart; ids and scores
+// npos x active, count npos), each as wh_route_experts_async routes it: one
+// launch for a bf16 gate of at most 256 rows (a multiple of 4) without an
+// available list or a hash row, else one call per input.  token_ids: each
+// input's hash token, or null for opts->hash_token_id.  The caller holds
+// c->mu.
+int route_batch(wh_ctx* c, uint32_t layer, const float* x, size_t x_ld, size_t hidden_len, size_t npos,
+                size_t active, const uint32_t* avail, size_t n_avail, const wh_route_options& opts,
+                const int64_t* token_ids, uint32_t* ids, float* scores, uint32_t* count) {
+    auto it = c->routers.find(layer);
+    if (it == c->routers.end()) return WH_NOT_RESIDENT;
+    const Router& rt = it->second;
+    bool hashed = false;
+    for (size_t i = 0; i < npos; ++i) hashed = hashed || (token_ids ? token_ids[i] : opts.hash_token_id) >= 0;
+    hashed = hashed && rt.has_table;
+    const bool one = rt.gate == kGateBf16 && !avail && !hashed && active > 0 && rt.rows % 4 == 0 &&
+                     rt.rows <= 256 && npos <= 65535 && x_ld <= 0xffffffffu && ((uintptr_t)x & 15) == 0 &&
+                     (x_ld & 3) == 0;
+    if (!one) {
+        for (size_t i = 0; i < npos; ++i) {
+            wh_route_options o = opts;
+            if (token_ids) o.hash_token_id = token_ids[i];
+            WH_TRY(wh_route_experts_async(c, layer, x + i * x_ld, hidden_len, active, avail, n_avail, &o,
+                                          ids + i * active, scores + i * active, count + i));
+        }
+        return WH_OK;
+    }
+    if (active > WH_ROUTER_MAX_ACTIVE) return WH_UNSUPPORTED;
+    wh_route_options o = opts;
+    o.hash_token_id = -1;
+    wh_router_sel sa;
+    WH_TRY(router_prepare(rt, o, hidden_len, active, rt.rows, &sa));
+    const size_t pub_ld = 3 * rt.rows;  // (key, score) u64 and the row id per row, a multiple of 2 words
+    WH_HIP(c->rtr.ensure((rt.cols + npos * pub_ld) * 4, false));
+    WH_HIP(c->rtr_cnt.ensure(npos * sizeof(uint32_t), true));
+    sa.logits = c->rtr.as<float>() + rt.cols;
+    sa.bias = sa.math ? rt.bias : nullptr;
+    sa.out_ids = ids;
+    sa.out_scores = scores;
+    sa.out_count = count;
+    sa.sorted = 1;
+    k_router_bf16<<<dim3((unsigned)(rt.rows / 4), (unsigned)npos), 64, rt.cols * sizeof(float), c->stream>>>(
+        rt.bf16, x, (uint32_t)rt.cols, sa, c->rtr_cnt.as<uint32_t>(), (uint32_t)x_ld, (uint32_t)pub_ld);
     WH_HIP(hipGetLastError());
     return WH_OK;
 }
@@ -3902,7 +3949,8 @@ int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const 
     // activations of every position, each array 256-byte aligned
     auto up = [](size_t n) { return (n + 63) & ~(size_t)63; };
     const size_t o_xq = 0, o_ql = o_xq + up(npos * hidden), o_q = o_ql + up(npos * q_lora),
-                 o_kv = o_q + up(npos * q_full), o_sc = o_kv + up(npos * head_dim), o_at = o_sc + up(heads * max_keys),
+                 o_kv = o_q + up(npos * q_full), o_sc = o_kv + up(npos * head_dim),
+                 o_at = o_sc + up(std::min<size_t>(npos, WH_POS_BATCH) * heads * max_keys),
                  o_om = o_at + up(npos * q_full), total = o_om + up(npos * o_mid);
     WH_HIP(c->mla.ensure(total * sizeof(float), false));
     float* base = c->mla.as<float>();
@@ -3922,46 +3970,60 @@ int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const 
     WH_TRY(rowpost_launch(c, a));
     WH_TRY(wh_fp8_gemv_multi_async(c, L->wq_b, 0, q_full, ql, npos, q_lora, q, q_full));
     // per position: per-head norm + RoPE of q; kv norm, RoPE, act-quant of
-    // the non-rope dims into the position's cache row
-    for (size_t i = 0; i < npos; ++i) {
-        a = rowpost_args(q + i * q_full, q + i * q_full, heads, head_dim, head_dim, head_dim);
+    // the non-rope dims into the position's cache row; up to WH_POS_BATCH
+    // positions per launch
+    for (size_t c0 = 0; c0 < npos; c0 += WH_POS_BATCH) {
+        const size_t nb = std::min<size_t>(WH_POS_BATCH, npos - c0);
+        a = rowpost_args(q + c0 * q_full, q + c0 * q_full, nb * heads, head_dim, head_dim, head_dim);
         a.norm = 1;
         a.inv_freqs = inv;
         a.pairs = (uint32_t)pairs;
         a.rope_off = (uint32_t)nope;
-        a.position = (uint32_t)positions[i];
+        a.rows_per_pos = (uint32_t)heads;
+        for (size_t i = 0; i < nb; ++i) a.bpos[i] = (uint32_t)positions[c0 + i];
         WH_TRY(rowpost_launch(c, a));
-        a = rowpost_args(kvt + i * head_dim, kv_cache_dev + positions[i] * kv_stride, 1, head_dim, head_dim, head_dim);
+        a = rowpost_args(kvt + c0 * head_dim, kv_cache_dev, nb, head_dim, head_dim, kv_stride);
         a.norm = 1;
         a.w = L->kv_norm_bf16;
         a.inv_freqs = inv;
         a.pairs = (uint32_t)pairs;
         a.rope_off = (uint32_t)nope;
-        a.position = (uint32_t)positions[i];
         a.aq_len = (uint32_t)nope;
+        a.rows_per_pos = 1;
+        a.out_at_pos = 1;
+        for (size_t i = 0; i < nb; ++i) a.bpos[i] = (uint32_t)positions[c0 + i];
         WH_TRY(rowpost_launch(c, a));
     }
-    // every position's window softmax with sink (E/compute.rs:4497-4580)
-    for (size_t i = 0; i < npos; ++i) {
-        const size_t context = positions[i] + 1, window_start = context > 128 ? context - 128 : 0;
+    // every position's window softmax with sink (E/compute.rs:4497-4580),
+    // after every cache row is written
+    for (size_t c0 = 0; c0 < npos; c0 += WH_POS_BATCH) {
+        const size_t nb = std::min<size_t>(WH_POS_BATCH, npos - c0);
         wh_attn_args w{};
-        w.q = q + i * q_full;
-        w.win = kv_cache_dev + window_start * kv_stride;
-        w.comp = comp_dev ? comp_dev[i] : nullptr;
+        w.q = q + c0 * q_full;
+        w.win = kv_cache_dev;
         w.sink = L->sink;
         w.inv_freqs = inv;
         w.scores = sc;
-        w.out = at + i * q_full;
+        w.out = at + c0 * q_full;
         w.heads = (uint32_t)heads;
         w.head_dim = (uint32_t)head_dim;
         w.nope_dim = (uint32_t)nope;
         w.pairs = (uint32_t)pairs;
-        w.n_win = (uint32_t)(context - window_start);
-        w.n_comp = (uint32_t)(n_comp ? n_comp[i] : 0);
         w.win_ld = (uint32_t)kv_stride;
-        w.token_pos = (uint32_t)positions[i];
         w.scale = powf((float)head_dim, -0.5f);
-        WH_TRY(attn_launch(c, w));
+        w.nb = (uint32_t)nb;
+        w.q_ld = (uint32_t)q_full;
+        w.scores_ld = (uint32_t)(heads * max_keys);
+        w.wlen = 128;
+        for (size_t i = 0; i < nb; ++i) {
+            w.bpos[i] = (uint32_t)positions[c0 + i];
+            w.bcomp[i] = comp_dev ? comp_dev[c0 + i] : nullptr;
+            w.bncomp[i] = (uint32_t)(n_comp ? n_comp[c0 + i] : 0);
+        }
+        const unsigned gy = (unsigned)((heads + 3) / 4);
+        k_attn_scores<<<dim3((unsigned)((max_keys + 63) / 64), gy, (unsigned)nb), 256, 0, c->stream>>>(w);
+        k_attn_combine<<<dim3((unsigned)(head_dim / 64), gy, (unsigned)nb), 256, 0, c->stream>>>(w);
+        WH_HIP(hipGetLastError());
     }
     // o path (E/compute.rs:4582-4631): act-quant per position, wo_a per
     // output group over all positions, act-quant, wo_b over all positions
@@ -4019,14 +4081,12 @@ int wh_hc_split_sinkhorn_async(wh_ctx* c, const float* mixes_dev, const float* s
     return WH_OK;
 }
 
-int wh_hc_pre_async(wh_ctx* c, const float* fn_dev, const float* scale_dev, const float* base_dev, size_t hc,
-                    size_t hidden, size_t sinkhorn_iters, float eps, const float* x_dev, float* y_dev,
-                    float* post_dev, float* comb_dev) {
-    if (!c || !fn_dev || !scale_dev || !base_dev || !x_dev || !y_dev || !post_dev || !comb_dev)
-        return WH_INVALID_ARGUMENT;
-    WH_TRY(hc_check(hc, hidden));
-    std::lock_guard<std::recursive_mutex> lk(c->mu);
-    WH_HIP(hipSetDevice(c->device));
+namespace {
+// hc_pre of npos streams (x_dev npos x hc * hidden, y_dev npos x hidden,
+// post_dev npos x hc, comb_dev npos x hc * hc) in one launch per stage.
+int hc_pre_launch(wh_ctx* c, const float* fn_dev, const float* scale_dev, const float* base_dev, size_t hc,
+                  size_t hidden, size_t sinkhorn_iters, float eps, const float* x_dev, float* y_dev, float* post_dev,
+                  float* comb_dev, size_t npos) {
     wh_hc_args a = hc_args(hc, hidden, sinkhorn_iters, eps);
     a.fn = fn_dev;
     a.scale = scale_dev;
@@ -4037,18 +4097,42 @@ int wh_hc_pre_async(wh_ctx* c, const float* fn_dev, const float* scale_dev, cons
     a.comb = comb_dev;
     a.parts = c->exact ? 1u : WH_HC_PARTS;
     const size_t n_sums = (size_t)WH_HC_PARTS * (a.mix_hc + 1);
-    WH_HIP(c->hcs.ensure((n_sums + 16) * sizeof(float), false));
+    a.sums_ld = (uint32_t)((n_sums + 63) & ~(size_t)63);
+    WH_HIP(c->hcs.ensure((npos * (a.sums_ld + hc) + 16) * sizeof(float), false));
     a.sums = c->hcs.as<float>();
-    a.pre = a.sums + n_sums;
+    a.pre = a.sums + npos * a.sums_ld;
+    const unsigned z = (unsigned)npos;
     if (c->exact) {
-        k_hc_chains<<<a.mix_hc + 1, 256, 0, c->stream>>>(a);
+        k_hc_chains<<<dim3(a.mix_hc + 1, 1, z), 256, 0, c->stream>>>(a);
     } else {
-        k_hc_partials<<<dim3(WH_HC_PARTS, a.mix_hc + 1), 256, 0, c->stream>>>(a);
+        k_hc_partials<<<dim3(WH_HC_PARTS, a.mix_hc + 1, z), 256, 0, c->stream>>>(a);
     }
-    k_hc_finish<<<1, 256, 0, c->stream>>>(a);
-    k_hc_y<<<(unsigned)((hidden + 255) / 256), 256, 0, c->stream>>>(a);
+    k_hc_finish<<<z, 256, 0, c->stream>>>(a);
+    k_hc_y<<<dim3((unsigned)((hidden + 255) / 256), z), 256, 0, c->stream>>>(a);
     WH_HIP(hipGetLastError());
     return WH_OK;
+}
+
+int hc_post_launch(wh_ctx* c, const float* y_dev, const float* residual_dev, const float* post_dev,
+                   const float* comb_dev, float* out_dev, size_t hc, size_t hidden, size_t npos) {
+    const size_t n = hc * hidden;
+    k_hc_post<<<dim3((unsigned)((n + 255) / 256), (unsigned)npos), 256, 0, c->stream>>>(
+        y_dev, residual_dev, post_dev, comb_dev, out_dev, (uint32_t)hc, (uint32_t)hidden);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+}  // namespace
+
+int wh_hc_pre_async(wh_ctx* c, const float* fn_dev, const float* scale_dev, const float* base_dev, size_t hc,
+                    size_t hidden, size_t sinkhorn_iters, float eps, const float* x_dev, float* y_dev,
+                    float* post_dev, float* comb_dev) {
+    if (!c || !fn_dev || !scale_dev || !base_dev || !x_dev || !y_dev || !post_dev || !comb_dev)
+        return WH_INVALID_ARGUMENT;
+    WH_TRY(hc_check(hc, hidden));
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
+    WH_HIP(hipSetDevice(c->device));
+    return hc_pre_launch(c, fn_dev, scale_dev, base_dev, hc, hidden, sinkhorn_iters, eps, x_dev, y_dev, post_dev,
+                         comb_dev, 1);
 }
 
 int wh_hc_post_async(wh_ctx* c, const float* y_dev, const float* residual_dev, const float* post_dev,
@@ -4057,11 +4141,7 @@ int wh_hc_post_async(wh_ctx* c, const float* y_dev, const float* residual_dev, c
     WH_TRY(hc_check(hc, hidden));
     std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
-    const size_t n = hc * hidden;
-    k_hc_post<<<(unsigned)((n + 255) / 256), 256, 0, c->stream>>>(y_dev, residual_dev, post_dev, comb_dev, out_dev,
-                                                                  (uint32_t)hc, (uint32_t)hidden);
-    WH_HIP(hipGetLastError());
-    return WH_OK;
+    return hc_post_launch(c, y_dev, residual_dev, post_dev, comb_dev, out_dev, hc, hidden, 1);
 }
 
 
@@ -4121,7 +4201,8 @@ int wh_deepseek_mhc_layer_async(wh_ctx* c, const wh_mhc_layer* L, size_t token_p
 // expert + routed sum, hc_post.  hidden_dev holds npos states of hc * hidden.
 int wh_deepseek_mhc_layer_batch_async(wh_ctx* c, const wh_mhc_layer* L, const size_t* positions, size_t npos,
                                       float* hidden_dev, float* kv_cache_dev, size_t kv_stride, size_t kv_capacity,
-                                      const float* const* comp_dev, const size_t* n_comp) {
+                                      const float* const* comp_dev, const size_t* n_comp,
+                                      const int64_t* token_ids) {
     if (!c || !L || !positions || !hidden_dev || ((uintptr_t)hidden_dev & 15)) return WH_INVALID_ARGUMENT;
     if (npos == 0) return WH_INVALID_SHAPE;  // "mHC batch hidden state too small"
     const size_t hc = L->hc, hidden = L->hidden;
@@ -4147,27 +4228,23 @@ int wh_deepseek_mhc_layer_batch_async(wh_ctx* c, const wh_mhc_layer* L, const si
     uint32_t* count = reinterpret_cast<uint32_t*>(f + o_n);
     // phase 1: hc_pre + attention norm per position, the batched attention,
     // hc_post, ffn hc_pre + norm per position (E/compute.rs:4679-4750)
-    for (size_t i = 0; i < npos; ++i)
-        WH_TRY(wh_hc_pre_async(c, L->hc_attn_fn, L->hc_attn_scale, L->hc_attn_base, hc, hidden, L->sinkhorn_iters,
-                               L->hc_eps, hidden_dev + i * hcd, y + i * hidden, post1 + i * hc, comb1 + i * hc * hc));
+    if (!L->hc_attn_fn || !L->hc_attn_scale || !L->hc_attn_base || !L->hc_ffn_fn || !L->hc_ffn_scale ||
+        !L->hc_ffn_base)
+        return WH_INVALID_ARGUMENT;
+    WH_TRY(hc_pre_launch(c, L->hc_attn_fn, L->hc_attn_scale, L->hc_attn_base, hc, hidden, L->sinkhorn_iters, L->hc_eps,
+                         hidden_dev, y, post1, comb1, npos));
     WH_TRY(wh_rms_norm_async(c, y, g, npos, hidden, L->attn_norm_bf16));
     WH_TRY(wh_mla_attention_decode_batch_async(c, &L->attn, positions, npos, g, kv_cache_dev, kv_stride, kv_capacity,
                                                comp_dev, n_comp));
-    for (size_t i = 0; i < npos; ++i) {
-        WH_TRY(wh_hc_post_async(c, g + i * hidden, hidden_dev + i * hcd, post1 + i * hc, comb1 + i * hc * hc,
-                                state + i * hcd, hc, hidden));
-        WH_TRY(wh_hc_pre_async(c, L->hc_ffn_fn, L->hc_ffn_scale, L->hc_ffn_base, hc, hidden, L->sinkhorn_iters,
-                               L->hc_eps, state + i * hcd, y + i * hidden, post2 + i * hc, comb2 + i * hc * hc));
-    }
+    WH_TRY(hc_post_launch(c, g, hidden_dev, post1, comb1, state, hc, hidden, npos));
+    WH_TRY(hc_pre_launch(c, L->hc_ffn_fn, L->hc_ffn_scale, L->hc_ffn_base, hc, hidden, L->sinkhorn_iters, L->hc_eps,
+                         state, y, post2, comb2, npos));
     WH_TRY(wh_rms_norm_async(c, y, g, npos, hidden, L->ffn_norm_bf16));
-    // the router per position (E/server/generation.rs:2462-2480), then the
-    // experts of the whole batch on the device route lists
-    for (size_t i = 0; i < npos; ++i)
-        WH_TRY(wh_route_experts_async(c, L->layer_id, g + i * hidden, hidden, slots, L->available_dev,
-                                      L->n_available, &L->route, ids + i * slots, w + i * slots, count + i));
+    // the router per position (E/server/generation.rs:2462-2480, each with
+    // its own token for a hash layer), then the experts of the whole batch
+    // on the device route lists
+    WH_TRY(route_batch(c, L->layer_id, g, hidden, hidden, npos, slots, L->available_dev, L->n_available, L->route,
+                       token_ids, ids, w, count));
     WH_TRY(wh_moe_batch_async(c, L->layer_id, ids, w, npos, slots, L->shared_layer, L->shared_expert, g, 0, z));
-    for (size_t i = 0; i < npos; ++i)
-        WH_TRY(wh_hc_post_async(c, z + i * hidden, state + i * hcd, post2 + i * hc, comb2 + i * hc * hc,
-                                hidden_dev + i * hcd, hc, hidden));
-    return WH_OK;
+    return hc_post_launch(c, z, state, post2, comb2, hidden_dev, hc, hidden, npos);
 }
