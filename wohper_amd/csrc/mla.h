@@ -197,6 +197,7 @@ struct wh_attn_args {
     // the last wlen cache rows up to that position (win = the cache's row
     // 0), compressed rows bcomp[z] (bncomp[z] of them)
     uint32_t nb, q_ld, scores_ld, wlen;
+    uint32_t wts_ld;       // k_attn_combine: floats per head of its dynamic LDS (>= every n_keys)
     uint32_t bpos[WH_POS_BATCH];
     uint32_t bncomp[WH_POS_BATCH];
     const float* bcomp[WH_POS_BATCH];
@@ -235,58 +236,81 @@ __device__ __forceinline__ const float* wh_attn_key(const wh_attn_args& a, const
 
 // scores[h][j] = (sum over d, in order, of q[h][d] * key_j[d]) * scale.
 // Grid (ceil(n_keys / 64), ceil(heads / 4)), 256 threads: wave w takes
-// head 4 * blockIdx.y + w, lane L key 64 * blockIdx.x + L; the 64 keys are
-// staged through LDS 64 dims at a time (row stride 65 floats: the lanes'
-// reads of one dim fall in distinct banks), the four heads' q rows once.
+// head 4 * blockIdx.y + w, lane L key 64 * blockIdx.x + L.  Every thread
+// requests its share of the 64 keys (16 dims of each 64-dim chunk, up to 8
+// chunks) at once, so the launch waits for one memory round trip, not one
+// per chunk; the chunks then go through LDS 64 dims at a time (row stride
+// 65 floats: the lanes' reads of one dim fall in distinct banks), the four
+// heads' q rows once.
+#define WH_ATTN_PREFETCH 8u  // 64-dim chunks of a key requested together
 __global__ void __launch_bounds__(256) k_attn_scores(wh_attn_args a) {
     __shared__ float qs[4 * WH_ATTN_MAX_HEAD_DIM];
     __shared__ float tile[64 * 65];
     const wh_attn_pos v = wh_attn_resolve(a);
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const uint32_t h0 = blockIdx.y * 4, j0 = blockIdx.x * 64;
-    const uint32_t nk = v.n_win + v.n_comp, hd = a.head_dim;
+    const uint32_t nk = v.n_win + v.n_comp, hd = a.head_dim, n_ch = hd / 64;
     if (j0 >= nk) return;  // a batched launch's grid covers its longest key list
+    // staging: thread t copies 16 dims (t % 4) of key t / 4 of each chunk
+    const uint32_t kk = t >> 2, part = t & 3;
+    const bool kon = j0 + kk < nk;
+    const float* krow = kon ? wh_attn_key(a, v, j0 + kk) : nullptr;
+    float4 kv[WH_ATTN_PREFETCH][4];
+    auto request = [&](uint32_t c0) {
+#pragma unroll
+        for (uint32_t c = 0; c < WH_ATTN_PREFETCH; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                kv[c][i] = kon && c0 + c < n_ch ? *(const float4*)(krow + 64 * (c0 + c) + part * 16 + 4 * i)
+                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    request(0);
     for (uint32_t i = t; i < 4 * hd; i += 256) {
         const uint32_t h = h0 + i / hd;
         qs[i] = h < a.heads ? v.q[(size_t)h * hd + i % hd] : 0.0f;
     }
-    // staging: thread t copies 16 dims (t % 4) of key t / 4
-    const uint32_t kk = t >> 2, part = t & 3;
-    const bool kon = j0 + kk < nk;
-    const float* krow = kon ? wh_attn_key(a, v, j0 + kk) : nullptr;
     const float* qrow = qs + wave * hd;
     float s = 0.0f;
-    for (uint32_t d0 = 0; d0 < hd; d0 += 64) {
-        float4 kv[4];
+    for (uint32_t c0 = 0; c0 < n_ch; c0 += WH_ATTN_PREFETCH) {
+        if (c0) request(c0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            kv[i] = kon ? *(const float4*)(krow + d0 + part * 16 + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-        __syncthreads();  // the previous chunk's reads are done
+        for (uint32_t c = 0; c < WH_ATTN_PREFETCH; ++c) {
+            if (c0 + c < n_ch) {  // uniform
+                __syncthreads();  // the previous chunk's reads are done (and q is staged)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float* d = tile + kk * 65 + part * 16 + 4 * i;
-            d[0] = kv[i].x;
-            d[1] = kv[i].y;
-            d[2] = kv[i].z;
-            d[3] = kv[i].w;
+                for (int i = 0; i < 4; ++i) {
+                    float* d = tile + kk * 65 + part * 16 + 4 * i;
+                    d[0] = kv[c][i].x;
+                    d[1] = kv[c][i].y;
+                    d[2] = kv[c][i].z;
+                    d[3] = kv[c][i].w;
+                }
+                __syncthreads();
+                const float* kr = tile + lane * 65;
+                const float* qc = qrow + 64 * (c0 + c);
+                for (uint32_t d = 0; d < 64; ++d) s = s + qc[d] * kr[d];
+            }
         }
-        __syncthreads();
-        const float* kr = tile + lane * 65;
-        for (uint32_t d = 0; d < 64; ++d) s = s + qrow[d0 + d] * kr[d];
     }
     const uint32_t h = h0 + wave, j = j0 + lane;
     if (h < a.heads && j < nk) v.scores[(size_t)h * nk + j] = s * a.scale;
 }
 
 // The rest of the window loop for 4 heads x 64 dims per workgroup (grid
-// (head_dim / 64, ceil(heads / 4)), 256 threads; wave w = head, lane = dim):
+// (head_dim / 64, ceil(heads / 4)), 256 threads, 4 * wts_ld floats of
+// dynamic LDS; wave w = head, lane = dim):
 //   max = the largest score (NaN scores never win, E/compute.rs:4125-4127);
 //   w_j = expf(score_j - max); denom = expf(sink - max) (if a sink) +
 //   (sequential sum of w_j); out_d = sequential sum of w_j * key_j[d] from 0;
 //   out_d /= denom when denom > 0; then the inverse RoPE of the output's
 //   rope dims at token_pos (E/compute.rs:4160-4197).
+// The keys' 64 dims of the workgroup go through LDS 128 keys at a time,
+// staged once for the four heads; the first 128 are requested before the
+// softmax pass.
+#define WH_ATTN_KCHUNK 128u
 __global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
-    __shared__ float wts[4 * WH_ATTN_MAX_KEYS];
+    extern __shared__ float wts[];  // [4][wts_ld]
+    __shared__ __align__(16) float tile[WH_ATTN_KCHUNK * 64];
     __shared__ float res[4 * 64];
     __shared__ float denom_s[4];
     const wh_attn_pos v = wh_attn_resolve(a);
@@ -294,7 +318,17 @@ __global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
     const uint32_t h = blockIdx.y * 4 + wave, d = blockIdx.x * 64 + lane;
     const uint32_t nk = v.n_win + v.n_comp;
     const bool hon = h < a.heads;
-    float* w = wts + wave * WH_ATTN_MAX_KEYS;
+    // staging: thread t copies dims 32 (t % 2) .. + 31 of key t / 2 of the chunk
+    const uint32_t kk = t >> 1, half = t & 1;
+    float4 kr[8];
+    auto request = [&](uint32_t c0) {
+        const bool on = c0 + kk < nk;
+        const float* src = on ? wh_attn_key(a, v, c0 + kk) + blockIdx.x * 64 + 32 * half : nullptr;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kr[i] = on ? *(const float4*)(src + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    request(0);
+    float* w = wts + wave * a.wts_ld;
     const float* sc = v.scores + (size_t)(hon ? h : 0) * nk;
     float mx = -__uint_as_float(0x7f800000u);
     for (uint32_t j = lane; j < nk; j += 64) {
@@ -313,17 +347,27 @@ __global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
         denom_s[wave] = den + ws;
     }
     float acc = 0.0f;
-    if (hon) {
-        uint32_t j = 0;
-        for (; j + 4 <= nk; j += 4) {
-            const float k0 = wh_attn_key(a, v, j)[d], k1 = wh_attn_key(a, v, j + 1)[d];
-            const float k2 = wh_attn_key(a, v, j + 2)[d], k3 = wh_attn_key(a, v, j + 3)[d];
-            acc = acc + w[j] * k0;
-            acc = acc + w[j + 1] * k1;
-            acc = acc + w[j + 2] * k2;
-            acc = acc + w[j + 3] * k3;
+    for (uint32_t c0 = 0; c0 < nk; c0 += WH_ATTN_KCHUNK) {
+        if (c0) {
+            __syncthreads();  // the previous chunk's reads are done
+            request(c0);
         }
-        for (; j < nk; ++j) acc = acc + w[j] * wh_attn_key(a, v, j)[d];
+        float* dst = tile + kk * 64 + 32 * half;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *(float4*)(dst + 4 * i) = kr[i];
+        __syncthreads();
+        const uint32_t m = min(WH_ATTN_KCHUNK, nk - c0);
+        if (hon) {
+            const float* wc = w + c0;
+            uint32_t j = 0;
+            for (; j + 4 <= m; j += 4) {
+                acc = acc + wc[j] * tile[j * 64 + lane];
+                acc = acc + wc[j + 1] * tile[(j + 1) * 64 + lane];
+                acc = acc + wc[j + 2] * tile[(j + 2) * 64 + lane];
+                acc = acc + wc[j + 3] * tile[(j + 3) * 64 + lane];
+            }
+            for (; j < m; ++j) acc = acc + wc[j] * tile[j * 64 + lane];
+        }
     }
     __syncthreads();
     const float den = denom_s[wave];

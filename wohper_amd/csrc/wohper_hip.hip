@@ -3655,10 +3655,12 @@ wh_rowpost_args rowpost_args(const float* x, float* out, size_t rows, size_t n, 
     return a;
 }
 
-int attn_launch(wh_ctx* c, const wh_attn_args& a) {
+int attn_launch(wh_ctx* c, const wh_attn_args& args) {
+    wh_attn_args a = args;
     const unsigned gy = (a.heads + 3) / 4, nk = a.n_win + a.n_comp;
+    a.wts_ld = nk;
     k_attn_scores<<<dim3((nk + 63) / 64, gy), 256, 0, c->stream>>>(a);
-    k_attn_combine<<<dim3(a.head_dim / 64, gy), 256, 0, c->stream>>>(a);
+    k_attn_combine<<<dim3(a.head_dim / 64, gy), 256, 4 * nk * sizeof(float), c->stream>>>(a);
     WH_HIP(hipGetLastError());
     return WH_OK;
 }
@@ -4015,6 +4017,7 @@ int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const 
         w.q_ld = (uint32_t)q_full;
         w.scores_ld = (uint32_t)(heads * max_keys);
         w.wlen = 128;
+        w.wts_ld = (uint32_t)max_keys;
         for (size_t i = 0; i < nb; ++i) {
             w.bpos[i] = (uint32_t)positions[c0 + i];
             w.bcomp[i] = comp_dev ? comp_dev[c0 + i] : nullptr;
@@ -4022,7 +4025,8 @@ int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const 
         }
         const unsigned gy = (unsigned)((heads + 3) / 4);
         k_attn_scores<<<dim3((unsigned)((max_keys + 63) / 64), gy, (unsigned)nb), 256, 0, c->stream>>>(w);
-        k_attn_combine<<<dim3((unsigned)(head_dim / 64), gy, (unsigned)nb), 256, 0, c->stream>>>(w);
+        k_attn_combine<<<dim3((unsigned)(head_dim / 64), gy, (unsigned)nb), 256, 4 * max_keys * sizeof(float),
+                         c->stream>>>(w);
         WH_HIP(hipGetLastError());
     }
     // o path (E/compute.rs:4582-4631): act-quant per position, wo_a per
