@@ -53,7 +53,7 @@ def _run(ctx, t, xs, r0, r1):
 @pytest.mark.parametrize("rows,cols,n,r0,r1,ue8m0", [
     (4096, 4096, 16, 0, 4096, False), (32768, 1024, 16, 0, 32768, True), (4096, 8192, 16, 0, 4096, False),
     (1024, 2048, 5, 100, 900, True), (512, 4096, 9, 3, 509, False), (1024, 1024, 2, 0, 1024, True),
-    (1024, 4096, 20, 64, 1024, False)])
+    (1024, 4096, 20, 64, 1024, False), (4096, 4096, 7, 0, 4096, True), (8192, 2048, 3, 128, 8064, False)])
 def test_multi_exact_matches_rows_multi(ctx, oracle, rows, cols, n, r0, r1, ue8m0):
     t, w, scales = _tensor(ctx, rows, cols, rows + cols + n, ue8m0)
     xs = np.random.default_rng(n).standard_normal((n, cols)).astype(np.float32)

@@ -12,7 +12,7 @@
 // workgroup holds 2 kN accumulators, one per row and input, and walks the
 // groups in order; each group's 16 weight bytes of the lane are decoded once
 // and dotted with the kN inputs' x values (one LDS read of a lane's x
-// serves both rows), which stream through LDS in chunks of 4 groups (the
+// serves both rows), which stream through LDS in chunks of groups (the
 // lane's 16 values of a group contiguous, as the single-input kernels stage
 // them), double-buffered, with the next chunk's weights and x loads in
 // flight during the current chunk's arithmetic.
@@ -21,15 +21,26 @@
 
 #define WH_FP8_MULTI_ROWS 32u  // rows per workgroup (128 threads, two rows each)
 
+// 128-column groups per staged chunk for kN inputs: 2 (a chunk of 16
+// inputs' x and the next chunk's loads leave room for two waves per SIMD),
+// more for fewer inputs so that every thread stages at least one 16-value
+// unit.  cols must be a multiple of 128 times this.
+#ifndef WH_FP8_MULTI_KC
+#define WH_FP8_MULTI_KC 2
+#endif
+__host__ __device__ constexpr int wh_fp8_multi_groups(int n) {
+    return WH_FP8_MULTI_KC * n >= 16 ? WH_FP8_MULTI_KC : 16 / n;
+}
+
 // Grid (row blocks [+ the second tensor's], ceil(n_in / kN)), 128 threads,
-// kN in {4, 8, 16}.  cols % 512 == 0; a workgroup's rows lie in one input's
+// kN in {2, 4, 8, 16}.  cols % (128 wh_fp8_multi_groups(kN)) == 0; a workgroup's rows lie in one input's
 // row group.  The host takes the largest kN that still gives a few hundred
 // workgroups (small matrices re-read their weights from cache once per
 // input block).
 template <int kN, bool kSpecial, bool kScaleU8>
 __global__ void __launch_bounds__(128) k_fp8_gemv_multi(wh_fp8_args a, uint32_t n_in) {
     constexpr int kT = 128;                          // threads
-    constexpr int kC = 4;                            // groups per chunk
+    constexpr int kC = wh_fp8_multi_groups(kN);
     constexpr int kChunk = kC * 128;                 // columns per chunk
     constexpr int kUnits = kN * kChunk / 16 / kT;    // 16-value staging units per thread per chunk
     static_assert(kUnits >= 1 && kN * kChunk % (16 * kT) == 0, "staging units");

@@ -595,15 +595,24 @@ int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x,
     }
     // several inputs in the reference's order: each weight byte decoded
     // once for all of them (k_fp8_gemv_multi); the most inputs per
-    // workgroup (16, 8, 4, 2) that keep about 256 workgroups
+    // workgroup (16, 8, 4, 2) that keep about 1024 workgroups (two waves
+    // per SIMD: every weight row is read once per block of inputs, and a
+    // fuller device outweighs the re-reads)
     const size_t mrows = (r1 - r0) + (t2 ? r1_2 - r0_2 : 0);
-    // (about 512 workgroups of 2 waves: one wave per SIMD); below 4096 rows
-    // the per-input kernel's wider grid is faster, and the weights are
-    // small enough to stay in cache across the inputs
     size_t mk = 16;
-    while (mk > 4 && (mrows / WH_FP8_MULTI_ROWS) * ((n_batch + mk - 1) / mk) < 512) mk /= 2;
-    while (mk > 4 && mk / 2 >= n_batch) mk /= 2;  // no more slots than inputs
-    if (n_batch >= 2 && mrows >= 4096 && fp8_split_k(t) && t.cols % 512 == 0 &&
+    while (mk > 2 && (mrows / WH_FP8_MULTI_ROWS) * ((n_batch + mk - 1) / mk) < 1024) mk /= 2;
+    while (mk > 2 && mk / 2 >= n_batch) mk /= 2;  // no more slots than inputs
+#ifdef WH_MULTI_MK
+    mk = WH_MULTI_MK;
+#endif
+#ifndef WH_MULTI_MINROWS
+#define WH_MULTI_MINROWS 4096
+#endif
+    // below WH_MULTI_MINROWS rows the per-input kernel's wider grid is
+    // faster, and the weights are small enough to stay in cache across the
+    // inputs
+    if (n_batch >= 2 && mrows >= WH_MULTI_MINROWS && fp8_split_k(t) &&
+        t.cols % (128 * (size_t)wh_fp8_multi_groups((int)mk)) == 0 &&
         (!t2 || (fp8_split_k(*t2) && t2->cols == t.cols && t2->special == t.special)) &&
         (!x_group_rows || (x_group_rows % WH_FP8_MULTI_ROWS == 0 && x_group_stride % 4 == 0)) && x_stride % 4 == 0) {
         const size_t b1 = (r1 - r0 + WH_FP8_MULTI_ROWS - 1) / WH_FP8_MULTI_ROWS;
@@ -623,7 +632,8 @@ int launch_fp8(wh_ctx* c, const Tensor& t, size_t r0, size_t r1, const float* x,
     } while (0)
         if (mk == 16) WH_MULTI(16);
         else if (mk == 8) WH_MULTI(8);
-        else WH_MULTI(4);
+        else if (mk == 4) WH_MULTI(4);
+        else WH_MULTI(2);
 #undef WH_MULTI
         WH_HIP(hipGetLastError());
         return WH_OK;
