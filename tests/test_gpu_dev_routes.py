@@ -78,11 +78,18 @@ def test_device_routes_equal_host_routes(ctx, oracle, layer, exact):
         ctx.device_free(p)
 
 
+@pytest.mark.parametrize("exact", [False, True])
 @pytest.mark.parametrize("count,shared", [(3, True), (1, True), (0, True), (4, False)])
-def test_device_routes_shorter_lists(ctx, layer, count, shared):
+def test_device_routes_shorter_lists(ctx, layer, count, shared, exact):
     """count below n_slots: only the first count routes are summed (the
-    other slots compute a copy of a resident expert that is never added)."""
-    ctx.set_exact_numerics(False)
+    other slots compute a copy of a resident expert that is never added).
+    Exact numerics: bit-identical to the host list of count routes.  MFMA
+    numerics: the 7-slot launch and the host list's shorter one may take
+    down kernels that round an expert's block sums in another order (one
+    256-column block per wave for an odd expert count, chained block pairs
+    for an even one), so they agree within 1e-5 of the largest output; a
+    padded slot added by mistake would move the output by a whole expert."""
+    ctx.set_exact_numerics(exact)
     rng = np.random.default_rng(count)
     x = rng.standard_normal(wl.HIDDEN).astype(np.float32)
     xd, ids, sc, cnt, out, out2 = _bufs(ctx, x)
@@ -99,7 +106,12 @@ def test_device_routes_shorter_lists(ctx, layer, count, shared):
     else:
         ctx.routed_experts_async(routes, xd, False, 1, out2)
     ctx.synchronize()
-    assert np.array_equal(bits(_read(ctx, out, wl.HIDDEN)), bits(_read(ctx, out2, wl.HIDDEN)))
+    got, want = _read(ctx, out, wl.HIDDEN), _read(ctx, out2, wl.HIDDEN)
+    if exact:
+        assert np.array_equal(bits(got), bits(want))
+    else:
+        assert float(np.abs(got - want).max()) <= 1e-5 * float(np.abs(want).max())
+    ctx.set_exact_numerics(False)
     for p in (xd, ids, sc, cnt, out, out2):
         ctx.device_free(p)
 

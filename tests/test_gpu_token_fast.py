@@ -85,7 +85,7 @@ def _routed_six(ctx, oracle):
     assert np.linalg.norm(got - want) <= 1e-3 * np.linalg.norm(want)
 
 
-@pytest.mark.parametrize("n_routed", [6, 1, 0])
+@pytest.mark.parametrize("n_routed", [6, 4, 2, 1, 0])
 def test_fast_shared_plus_routed(ctx, oracle, n_routed):
     seed = 4
     idx, w, x = wl.moe_token_case(seed)

@@ -418,6 +418,129 @@ __global__ void __launch_bounds__(kCols / 8, 1) k_moe_gateup_px(wh_moe_args a) {
 }
 
 
+// Down + routed sum for an odd number of experts kN, inter = 2048: grid
+// (hidden / 16, n_tokens), 512 threads.  The workgroup's 16 output rows
+// are 8 kN blocks of 256 columns; wave w takes the blocks of columns
+// [256 w, 256 w + 256) of every expert, kN blocks, so no wave runs a block
+// more than another (unit pairs of two blocks would leave four waves one
+// unit longer).  Wave w act-quantizes exactly those h values (two experts'
+// slices per 8-value chunk of its lanes), and the blocks' partial outputs
+// meet in LDS, summed per expert in block order (k_moe_down_px chains each
+// unit's two blocks in its MFMA accumulator instead: the same products, the
+// sums rounded in another order).
+template <int kN>
+__global__ void __launch_bounds__(512, 1) k_moe_down_pb(wh_moe_args a) {
+    constexpr uint32_t kCols = 2048, kG = kCols / 32;
+    constexpr int kJ = kN, kDepth = WH_PX_DN_DEPTH < kJ ? WH_PX_DN_DEPTH : kJ;
+    constexpr int kPro = WH_PX_DN_PRO < kDepth ? WH_PX_DN_PRO : kDepth;
+    constexpr int kCh = (kN + 1) / 2;  // 8-value chunks of h per lane
+    __shared__ __align__(16) uint8_t hc[kN * kCols];
+    __shared__ __align__(16) uint8_t hsb[kN * kG];
+    __shared__ float red[kN * 8 * 16];
+    WH_TL(1, 0);
+    const uint32_t tok = blockIdx.y;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), L = threadIdx.x & 63, g = L >> 4;
+    const uint32_t row = blockIdx.x * 16 + (L & 15);
+    const uint32_t qt = wave >> 1, b = wave & 1;
+    const float* htok = a.h + (size_t)tok * kN * kCols;
+    // chunk i of lane L: columns 256 w + 8 (L % 32) .. + 7 of expert
+    // 2 i + L / 32 (the last expert's when past the end; not stored)
+    float4 hv[kCh][2];
+#pragma unroll
+    for (int i = 0; i < kCh; ++i) {
+        const uint32_t e = 2 * i + (L >> 5);
+        const float4* hp = (const float4*)(htok + (size_t)(e < (uint32_t)kN ? e : kN - 1) * kCols + 256 * wave +
+                                           8 * (L & 31));
+        hv[i][0] = hp[0];
+        hv[i][1] = hp[1];
+    }
+    const uint8_t* wl[kJ];
+    const uint8_t* sr[kJ];
+#pragma unroll
+    for (int e = 0; e < kJ; ++e) {
+        const wh_expert_ptrs ep = wh_moe_ex(a, e);
+        wl[e] = ep.w2 + (size_t)row * (kCols / 2) + 256 * qt + 64 * (g & 1) + 32 * (g >> 1);
+        sr[e] = ep.s2 + (size_t)row * kG + 16 * qt;
+    }
+    wh_issue_barrier();
+    wh_mx_raw ring[kDepth];
+#pragma unroll
+    for (int j = 0; j < kPro; ++j) wh_mx_raw_load(ring[j], wl[j], sr[j], b);
+    __builtin_amdgcn_sched_barrier(0);
+    WH_TL(1, 1);
+    WH_TL(1, 2);
+    // act-quant of h (as k_moe_down_px): the wave reads back only codes it
+    // wrote itself, so no workgroup barrier is needed
+    auto quant_chunk = [&](int i) {
+        const uint32_t e = 2 * i + (L >> 5), idx = 32 * wave + (L & 31);
+        const float v[8] = {hv[i][0].x, hv[i][0].y, hv[i][0].z, hv[i][0].w,
+                            hv[i][1].x, hv[i][1].y, hv[i][1].z, hv[i][1].w};
+        bool bad;
+        const int k = wh_quant8_scale(v, bad);
+        uint32_t cd[8];
+        wh_quant8_f32_codes(v, k, cd);
+        if (e < (uint32_t)kN) {
+            uint8_t* grp = hc + kCols * e + 32 * (idx >> 2) + (idx & 3);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) grp[4 * j] = (uint8_t)cd[j];
+            if ((idx & 3) == 0) hsb[kG * e + (idx >> 2)] = (uint8_t)(127 + k - 3);
+        }
+        asm volatile("" ::: "memory");
+    };
+#pragma unroll
+    for (int i = 0; i < kCh; ++i) quant_chunk(i);
+    __builtin_amdgcn_sched_barrier(0);
+    WH_TL(1, 3);
+#pragma unroll
+    for (int j = kPro; j < kDepth; ++j) wh_mx_raw_load(ring[j], wl[j], sr[j], b);
+    __builtin_amdgcn_sched_barrier(0);
+    WH_TL(1, 4);
+    WH_TL(1, 5);
+    {
+        uint32_t dep = wh_opaque_zero(__uint_as_float(*(const uint32_t*)hsb));
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) {
+            wh_v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            wh_mx_bop bo;
+            wh_mx_bop_load(bo, hc + kCols * j + 256 * wave + dep, hsb + kG * j + 8 * wave + dep, g);
+            wh_px_step(acc, ring[j % kDepth], dep, bo, g);
+            if (j + kDepth < kJ) wh_mx_raw_load(ring[j % kDepth], wl[j + kDepth] + dep, sr[j + kDepth] + dep, b);
+            asm volatile("" : "+v"(acc));
+            if ((L & 15) == 0) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[(8 * j + wave) * 16 + 4 * g + r] = acc[r];
+            }
+            if (j < 4) WH_TL(1, 6 + j);
+        }
+    }
+    __syncthreads();
+    WH_TL(1, 10);
+    // per-expert outputs (the 8 blocks of each expert in order), then the
+    // ordered routed sum
+    if (threadIdx.x < 16) {
+        const uint32_t r = threadIdx.x, orow = blockIdx.x * 16 + r;
+        float yv[WH_MAX_EXPERTS];
+        bool finite = true;
+#pragma unroll
+        for (uint32_t e = 0; e < WH_MAX_EXPERTS; ++e) {
+            if (e < (uint32_t)kN) {
+                const float* p = red + 8 * e * 16 + r;
+                float y = p[0];
+#pragma unroll
+                for (int k = 1; k < 8; ++k) y = y + p[16 * k];
+                finite = finite && fabsf(y) <= 3.4028235e38f;
+                yv[e] = y;
+                a.y[((size_t)tok * kN + e) * a.hidden + orow] = y;
+            } else {
+                yv[e] = 0.0f;
+            }
+        }
+        if (!finite) atomicOr(a.status, WH_ST_NONFINITE_OUTPUT);
+        a.out[(size_t)tok * a.hidden + orow] = wh_route_combine(a, yv);
+    }
+    WH_TL(1, 11);
+}
+
 // Down + routed sum, inter = 2048: grid (hidden / 16, n_tokens), 512
 // threads.  Unit u = (expert u / 4, column quarter u % 4 of 512 = blocks
 // 2 (u % 4), + 1) of the workgroup's 16 output rows; wave w runs units w,

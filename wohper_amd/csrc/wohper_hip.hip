@@ -1037,6 +1037,15 @@ int moe_launch_fast(wh_ctx* c, const ExpertView* ev, const float* route_w, size_
             // every expert of a 16-row output slice per workgroup: the routed
             // sum stays in the workgroup
             dim3 pgrid((unsigned)(hidden / 16), (unsigned)n_tokens);
+#ifndef WH_NO_DOWN_PB
+            // an odd number of experts: one 256-column block per wave and
+            // expert, every wave the same count
+            if (n == 7) k_moe_down_pb<7><<<pgrid, 512, 0, c->stream>>>(a);
+            else if (n == 5) k_moe_down_pb<5><<<pgrid, 512, 0, c->stream>>>(a);
+            else if (n == 3) k_moe_down_pb<3><<<pgrid, 512, 0, c->stream>>>(a);
+            else if (n == 1) k_moe_down_pb<1><<<pgrid, 512, 0, c->stream>>>(a);
+            else
+#endif
             switch ((n + 1) / 2) {
                 case 1: k_moe_down_px<1><<<pgrid, 512, 0, c->stream>>>(a); break;
                 case 2: k_moe_down_px<2><<<pgrid, 512, 0, c->stream>>>(a); break;
