@@ -1051,6 +1051,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fp8", action="store_true")
     ap.add_argument("--no-aux", action="store_true", help="skip the router and experts-pack load legs")
+    ap.add_argument("--aux-legs", default="decode_layer,read_floor,router,expert_pack_load",
+                    help="which of the auxiliary legs to run (comma-separated)")
     ap.add_argument("--stack-layers", type=int, default=43, help="layers of the full-depth stack leg (0: skip)")
     ap.add_argument("--stack-steps", type=int, default=20)
     ap.add_argument("--batch-steps", type=int, default=20, help="steps of the ragged batch leg (0: skip)")
@@ -1185,14 +1187,18 @@ def main():
         extra["fp8_decode_layer_batch16"] = fp8_decode_layer_batch(ctx, 200)
         ctx.set_exact_numerics(args.exact)
         log(f"fp8 decode layer, batch 16: {extra['fp8_decode_layer_batch16']}")
-    if not args.no_aux:
+    aux = set(args.aux_legs.split(",")) if not args.no_aux else set()
+    if "decode_layer" in aux:
         extra["decode_layer"] = decode_layer(ctx, args.layers, 20, not args.no_graph)
         ctx.set_exact_numerics(args.exact)
         log(f"decode layer: {extra['decode_layer']}")
+    if "read_floor" in aux:
         extra["read_floor"] = read_floor(ctx)
         log(f"read floor: {extra['read_floor']}")
+    if "router" in aux:
         extra["router"] = router(ctx, 400)
         log(f"router: {extra['router']}")
+    if "expert_pack_load" in aux:
         extra["expert_pack_load"] = expert_pack_load(ctx)
         log(f"expert pack load: {extra['expert_pack_load']}")
     if args.batch_steps > 0:
