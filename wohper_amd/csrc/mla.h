@@ -234,6 +234,26 @@ __device__ __forceinline__ const float* wh_attn_key(const wh_attn_args& a, const
     return j < v.n_win ? v.win + (size_t)j * a.win_ld : v.comp + (size_t)(j - v.n_win) * a.head_dim;
 }
 
+// The q rows of heads h0 .. h0 + 3 into LDS (zeros past the last head):
+// every thread's float4 loads are issued before the first store (a load
+// inside a loop or under a branch would be waited for one at a time).
+__device__ __forceinline__ void wh_attn_stage_q(const wh_attn_args& a, const wh_attn_pos& v, uint32_t h0, float* qs) {
+    constexpr int kPer = 4 * WH_ATTN_MAX_HEAD_DIM / 4 / 256;  // float4 per thread at most
+    const uint32_t hd = a.head_dim, n4 = hd;                   // 4 * hd floats = hd float4
+    float4 qv[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t i4 = threadIdx.x + 256 * k, ic = i4 < n4 ? i4 : 0u, e = 4 * ic;
+        const uint32_t h = h0 + e / hd, hc = h < a.heads ? h : a.heads - 1;
+        qv[k] = *(const float4*)(v.q + (size_t)hc * hd + e % hd);
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t i4 = threadIdx.x + 256 * k, e = 4 * i4;
+        if (i4 < n4) *(float4*)(qs + e) = h0 + e / hd < a.heads ? qv[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
 // scores[h][j] = (sum over d, in order, of q[h][d] * key_j[d]) * scale.
 // Grid (ceil(n_keys / 64), ceil(heads / 4)), 256 threads: wave w takes
 // head 4 * blockIdx.y + w, lane L key 64 * blockIdx.x + L.  Every thread
@@ -244,7 +264,7 @@ __device__ __forceinline__ const float* wh_attn_key(const wh_attn_args& a, const
 // heads' q rows once.
 #define WH_ATTN_PREFETCH 8u  // 64-dim chunks of a key requested together
 __global__ void __launch_bounds__(256) k_attn_scores(wh_attn_args a) {
-    __shared__ float qs[4 * WH_ATTN_MAX_HEAD_DIM];
+    __shared__ __align__(16) float qs[4 * WH_ATTN_MAX_HEAD_DIM];
     __shared__ float tile[64 * 65];
     const wh_attn_pos v = wh_attn_resolve(a);
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
@@ -265,10 +285,7 @@ __global__ void __launch_bounds__(256) k_attn_scores(wh_attn_args a) {
                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
     };
     request(0);
-    for (uint32_t i = t; i < 4 * hd; i += 256) {
-        const uint32_t h = h0 + i / hd;
-        qs[i] = h < a.heads ? v.q[(size_t)h * hd + i % hd] : 0.0f;
-    }
+    wh_attn_stage_q(a, v, h0, qs);
     const float* qrow = qs + wave * hd;
     float s = 0.0f;
     for (uint32_t c0 = 0; c0 < n_ch; c0 += WH_ATTN_PREFETCH) {
