@@ -127,7 +127,20 @@ __global__ void __launch_bounds__(256) k_hc_partials(wh_hc_args a0) {
     const uint32_t i0 = blockIdx.x * per, i1 = min(i0 + per, a.hc_dim);
     const float* row = c < a.mix_hc ? a.fn + (size_t)c * a.hc_dim : a.x;
     float s = 0.0f;
-    for (uint32_t i = i0 + t; i < i1; i += 256) s = s + row[i] * a.x[i];
+    uint32_t i = i0 + t;
+    // four terms' loads at a time (a load in a loop is waited for before the
+    // next is issued)
+    for (; i + 3 * 256 < i1; i += 4 * 256) {
+        float rv[4], xv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            rv[k] = row[i + 256 * k];
+            xv[k] = a.x[i + 256 * k];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s = s + rv[k] * xv[k];
+    }
+    for (; i < i1; i += 256) s = s + row[i] * a.x[i];
     s = wh_hc_wave_sum(s);
     if (lane == 0) red[wave] = s;
     __syncthreads();
@@ -294,7 +307,19 @@ __global__ void __launch_bounds__(256) k_hc_y(wh_hc_args a0) {
     const uint32_t d = blockIdx.x * 256 + threadIdx.x;
     if (d >= a.hidden) return;
     float acc = 0.0f;
-    for (uint32_t i = 0; i < a.hc; ++i) acc = acc + a.pre[i] * a.x[(size_t)i * a.hidden + d];
+    if (a.hc == 4) {
+        // DeepSeek-V4's hc: the four copies' loads issued together
+        float xv[4], pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xv[i] = a.x[(size_t)i * a.hidden + d];
+            pv[i] = a.pre[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = acc + pv[i] * xv[i];
+    } else {
+        for (uint32_t i = 0; i < a.hc; ++i) acc = acc + a.pre[i] * a.x[(size_t)i * a.hidden + d];
+    }
     a.y[d] = acc;
 }
 
@@ -315,6 +340,18 @@ __global__ void __launch_bounds__(256) k_hc_post(const float* __restrict__ y, co
     if (idx >= (size_t)hc * hidden) return;
     const uint32_t k = (uint32_t)(idx / hidden), d = (uint32_t)(idx % hidden);
     float acc = post[k] * y[d];
-    for (uint32_t i = 0; i < hc; ++i) acc = acc + comb[k * hc + i] * res[(size_t)i * hidden + d];
+    if (hc == 4) {
+        // DeepSeek-V4's hc: the four copies' loads issued together
+        float rv[4], cv[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            rv[i] = res[(size_t)i * hidden + d];
+            cv[i] = comb[k * 4 + i];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) acc = acc + cv[i] * rv[i];
+    } else {
+        for (uint32_t i = 0; i < hc; ++i) acc = acc + comb[k * hc + i] * res[(size_t)i * hidden + d];
+    }
     out[idx] = acc;
 }

@@ -82,11 +82,23 @@ __global__ void __launch_bounds__(kT) k_rowpost(wh_rowpost_args a) {
         if (a.out_at_pos) orow = position;
     }
     float xv[kPer], wv[kPer];
+    // every load issued before any is used, from clamped indices (a load
+    // under a branch is waited for on its own; with no norm weights the
+    // row itself stands in as a valid address)
+    const bool use_w = a.norm && a.w;
+    const uint16_t* wp = use_w ? a.w : (const uint16_t*)x;
+    uint32_t wr[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t i = t + kT * k, ic = i < n ? i : 0u;
+        xv[k] = x[ic];
+        wr[k] = wp[ic];
+    }
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const uint32_t i = t + kT * k;
-        xv[k] = i < n ? x[i] : 0.0f;
-        wv[k] = a.norm && a.w && i < n ? wh_bf16_value(a.w[i]) : 1.0f;
+        if (i >= n) xv[k] = 0.0f;
+        wv[k] = use_w && i < n ? wh_bf16_value((uint16_t)wr[k]) : 1.0f;
     }
 #pragma unroll
     for (int k = 0; k < kPer; ++k)
@@ -348,10 +360,31 @@ __global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
     float* w = wts + wave * a.wts_ld;
     const float* sc = v.scores + (size_t)(hon ? h : 0) * nk;
     float mx = -__uint_as_float(0x7f800000u);
-    for (uint32_t j = lane; j < nk; j += 64) {
-        const float sv = hon ? sc[j] : 0.0f;
-        w[j] = sv;
-        mx = fmaxf(mx, sv);
+    uint32_t j = lane;
+    // four scores' loads at a time (sc is a valid row for every wave)
+    for (; j + 192 < nk; j += 256) {
+        float sv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sv[k] = sc[j + 64 * k];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float x = hon ? sv[k] : 0.0f;
+            w[j + 64 * k] = x;
+            mx = fmaxf(mx, x);
+        }
+    }
+    if (j + 64 < nk) {
+        const float s0 = sc[j], s1 = sc[j + 64];
+        const float x0 = hon ? s0 : 0.0f, x1 = hon ? s1 : 0.0f;
+        w[j] = x0;
+        w[j + 64] = x1;
+        mx = fmaxf(fmaxf(mx, x0), x1);
+        j += 128;
+    }
+    for (; j < nk; j += 64) {
+        const float x = hon ? sc[j] : 0.0f;
+        w[j] = x;
+        mx = fmaxf(mx, x);
     }
     mx = wh_wave_max(mx);
     for (uint32_t j = lane; j < nk; j += 64) w[j] = wh_expf_glibc(w[j] - mx, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
