@@ -160,6 +160,12 @@ __global__ void __launch_bounds__(256) k_hc_finish(wh_hc_args a0) {
     __shared__ float rsum[16];
     __shared__ float inv_s;
     const uint32_t t = threadIdx.x, hc = a.hc, hh = hc * hc;
+    // the parameters this thread uses, requested first (clamped indices:
+    // loads under branches would be waited for one at a time)
+    const uint32_t last = a.mix_hc - 1;
+    const float sc0 = a.scale[0], sc1 = a.scale[1], sc2 = a.scale[2];
+    const float bv0 = a.base[t < last ? t : last], bv1 = a.base[t + hc < last ? t + hc : last];
+    const float bv2 = a.base[2 * hc + t < last ? 2 * hc + t : last];
     if (a.mixes_in) {
         if (t < a.mix_hc) mixes[t] = a.mixes_in[t];
     } else {
@@ -169,8 +175,14 @@ __global__ void __launch_bounds__(256) k_hc_finish(wh_hc_args a0) {
             // the partial sums through LDS, then each chain's in the order
             // of the parts
             __shared__ float stage[WH_HC_PARTS * WH_HC_MAX_CHAINS];
-            const uint32_t n_ch = a.mix_hc + 1;
-            for (uint32_t i = t; i < a.parts * n_ch; i += 256) stage[i] = a.sums[i];
+            const uint32_t n_ch = a.mix_hc + 1, tot = a.parts * n_ch;
+            uint32_t i = t;
+            for (; i + 256 < tot; i += 512) {
+                const float s0 = a.sums[i], s1 = a.sums[i + 256];
+                stage[i] = s0;
+                stage[i + 256] = s1;
+            }
+            if (i < tot) stage[i] = a.sums[i];
             __syncthreads();
             if (t < n_ch) {
                 float s = 0.0f;
@@ -191,8 +203,8 @@ __global__ void __launch_bounds__(256) k_hc_finish(wh_hc_args a0) {
     const float eps = a.eps;
     if (t >= 64) return;
     if (t < hc) {
-        a.pre[t] = wh_sigmoid(mixes[t] * a.scale[0] + a.base[t]) + eps;
-        a.post[t] = 2.0f * wh_sigmoid(mixes[t + hc] * a.scale[1] + a.base[t + hc]);
+        a.pre[t] = wh_sigmoid(mixes[t] * sc0 + bv0) + eps;
+        a.post[t] = 2.0f * wh_sigmoid(mixes[t + hc] * sc1 + bv1);
     }
     const uint32_t n_ops = a.iters ? 2 * a.iters - 1 : 1;
     if (hc == 4) {
@@ -227,7 +239,7 @@ __global__ void __launch_bounds__(256) k_hc_finish(wh_hc_args a0) {
             return r;
         };
         const bool on = t < 16;
-        float v = on ? mixes[8 + t] * a.scale[2] + a.base[8 + t] : 0.0f;
+        float v = on ? mixes[8 + t] * sc2 + bv2 : 0.0f;  // 2 hc = 8
         float mx = -__uint_as_float(0x7f800000u);
         mx = fmaxf(mx, row_q(v, std::integral_constant<int, 0>()));
         mx = fmaxf(mx, row_q(v, std::integral_constant<int, 1>()));
@@ -247,7 +259,7 @@ __global__ void __launch_bounds__(256) k_hc_finish(wh_hc_args a0) {
         // with shuffles and sums it in order
         const uint32_t j = t / hc, k = t % hc;
         const bool on = t < hh;
-        float v = on ? mixes[2 * hc + t] * a.scale[2] + a.base[2 * hc + t] : 0.0f;
+        float v = on ? mixes[2 * hc + t] * sc2 + bv2 : 0.0f;
         float mx = -__uint_as_float(0x7f800000u);
         for (uint32_t q = 0; q < hc; ++q) mx = fmaxf(mx, __shfl(v, (int)(j * hc + q), 64));
         v = wh_expf_glibc(v - mx, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
