@@ -46,6 +46,48 @@ __host__ __device__ constexpr uint32_t wh_xs_floats(uint32_t cols) { return cols
 // workgroups are written and read with agent-scope relaxed atomics (coherent
 // at the device level), each writer waits for its stores to complete, and an
 // agent-scope atomic counter elects the last arriver.
+// acc + src[0] + src[1] + ... + src[len - 1], one add at a time in index
+// order (the reference's sequential f32 sums), from LDS.  Blocks of 256
+// values are straight-line code in which batches of 32 alternate between
+// two register sets, so the next batch's reads are in flight while the
+// current one is added (in straight-line code the compiler counts the reads
+// in flight exactly; across a loop's back edge it waits for all of them).
+// src 16-byte aligned.
+__device__ __forceinline__ float wh_ordered_sum_lds(const float* src, uint32_t len, float acc) {
+    float4 p[2][8];
+    auto rd = [&](float4 (&q)[8], const float* a) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = *(const float4*)(a + 4 * i);
+    };
+    auto add = [&](const float4 (&q)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            acc = acc + q[i].x;
+            acc = acc + q[i].y;
+            acc = acc + q[i].z;
+            acc = acc + q[i].w;
+        }
+    };
+    uint32_t e = 0;
+    for (; e + 256 <= len; e += 256) {
+        const float* b = src + e;
+        rd(p[0], b);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (k + 1 < 8) rd(p[(k + 1) & 1], b + 32 * (k + 1));
+            __builtin_amdgcn_sched_barrier(0);
+            add(p[k & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    for (; e + 32 <= len; e += 32) {
+        rd(p[0], src + e);
+        add(p[0]);
+    }
+    for (; e < len; ++e) acc = acc + src[e];
+    return acc;
+}
+
 __device__ __forceinline__ float wh_load_coherent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -95,21 +95,7 @@ __global__ void __launch_bounds__(256) k_hc_chains(wh_hc_args a0) {
         if (t == 0 && k > 0) {
             const float* src = prod[(k - 1) & 1];
             const uint32_t len = min(WH_HC_CHUNK, a.hc_dim - (k - 1) * WH_HC_CHUNK);
-            uint32_t e = 0;
-            // 32 products read ahead of their adds
-            for (; e + 32 <= len; e += 32) {
-                float4 p[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) p[i] = *(const float4*)(src + e + 4 * i);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    acc = acc + p[i].x;
-                    acc = acc + p[i].y;
-                    acc = acc + p[i].z;
-                    acc = acc + p[i].w;
-                }
-            }
-            for (; e < len; ++e) acc = acc + src[e];
+            acc = wh_ordered_sum_lds(src, len, acc);
         }
         __syncthreads();
     }

@@ -123,28 +123,14 @@ __global__ void __launch_bounds__(kT) k_rowpost(wh_rowpost_args a) {
             }
         } else {
             // the reference's order: every product rounded on its own in
-            // parallel, then one lane adds them in sequence, 32 read ahead
+            // parallel, then one lane adds them in sequence
             __shared__ __align__(16) float sq[WH_ROWPOST_MAX];
 #pragma unroll
             for (int k = 0; k < kPer; ++k)
                 if (t + kT * k < n) sq[t + kT * k] = xv[k] * xv[k];
             __syncthreads();
             if (t == 0) {
-                float s = 0.0f;
-                uint32_t i = 0;
-                for (; i + 32 <= n; i += 32) {
-                    float4 q[8];
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) q[k] = *(const float4*)(sq + i + 4 * k);
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        s = s + q[k].x;
-                        s = s + q[k].y;
-                        s = s + q[k].z;
-                        s = s + q[k].w;
-                    }
-                }
-                for (; i < n; ++i) s = s + sq[i];
+                const float s = wh_ordered_sum_lds(sq, n, 0.0f);
                 inv_s = 1.0f / sqrtf(s / (float)n + 1.0e-6f);
             }
         }
