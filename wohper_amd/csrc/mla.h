@@ -324,7 +324,7 @@ __global__ void __launch_bounds__(256) k_attn_scores(wh_attn_args a) {
 // softmax pass.
 #define WH_ATTN_KCHUNK 128u
 __global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
-    extern __shared__ float wts[];  // [4][wts_ld]
+    extern __shared__ __align__(16) float wts[];  // [4][wts_ld], wts_ld a multiple of 4
     __shared__ __align__(16) float tile[WH_ATTN_KCHUNK * 64];
     __shared__ float res[4 * 64];
     __shared__ float denom_s[4];
@@ -376,8 +376,7 @@ __global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
     for (uint32_t j = lane; j < nk; j += 64) w[j] = wh_expf_glibc(w[j] - mx, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
     __syncthreads();
     if (lane == 0) {
-        float ws = 0.0f;
-        for (uint32_t j = 0; j < nk; ++j) ws = ws + w[j];
+        const float ws = wh_ordered_sum_lds(w, nk, 0.0f);
         float den = 0.0f;
         if (a.sink && hon) den = den + wh_expf_glibc(a.sink[h] - mx, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
         denom_s[wave] = den + ws;
@@ -394,15 +393,45 @@ __global__ void __launch_bounds__(256) k_attn_combine(wh_attn_args a) {
         __syncthreads();
         const uint32_t m = min(WH_ATTN_KCHUNK, nk - c0);
         if (hon) {
+            // blocks of 16 keys: the weights (broadcast) and the lane's 16
+            // key values of the next block are read while the current block
+            // is added; a full chunk is straight-line code, in which the
+            // compiler counts the reads in flight exactly
             const float* wc = w + c0;
-            uint32_t j = 0;
-            for (; j + 4 <= m; j += 4) {
-                acc = acc + wc[j] * tile[j * 64 + lane];
-                acc = acc + wc[j + 1] * tile[(j + 1) * 64 + lane];
-                acc = acc + wc[j + 2] * tile[(j + 2) * 64 + lane];
-                acc = acc + wc[j + 3] * tile[(j + 3) * 64 + lane];
+            float4 wa[2][4];
+            float ta[2][16];
+            auto rdb = [&](int sl, uint32_t jb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wa[sl][i] = *(const float4*)(wc + 16 * jb + 4 * i);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) ta[sl][i] = tile[(16 * jb + i) * 64 + lane];
+            };
+            auto addb = [&](int sl) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc = acc + wa[sl][i].x * ta[sl][4 * i];
+                    acc = acc + wa[sl][i].y * ta[sl][4 * i + 1];
+                    acc = acc + wa[sl][i].z * ta[sl][4 * i + 2];
+                    acc = acc + wa[sl][i].w * ta[sl][4 * i + 3];
+                }
+            };
+            const uint32_t mb = m / 16;
+            if (mb == WH_ATTN_KCHUNK / 16) {
+                rdb(0, 0);
+#pragma unroll
+                for (int b = 0; b < (int)(WH_ATTN_KCHUNK / 16); ++b) {
+                    if (b + 1 < (int)(WH_ATTN_KCHUNK / 16)) rdb((b + 1) & 1, b + 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    addb(b & 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+                for (uint32_t b = 0; b < mb; ++b) {
+                    rdb(0, b);
+                    addb(0);
+                }
             }
-            for (; j < m; ++j) acc = acc + wc[j] * tile[j * 64 + lane];
+            for (uint32_t j = 16 * mb; j < m; ++j) acc = acc + wc[j] * tile[j * 64 + lane];
         }
     }
     __syncthreads();

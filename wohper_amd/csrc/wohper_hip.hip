@@ -3677,9 +3677,9 @@ wh_rowpost_args rowpost_args(const float* x, float* out, size_t rows, size_t n, 
 int attn_launch(wh_ctx* c, const wh_attn_args& args) {
     wh_attn_args a = args;
     const unsigned gy = (a.heads + 3) / 4, nk = a.n_win + a.n_comp;
-    a.wts_ld = nk;
+    a.wts_ld = (nk + 3) & ~3u;  // each head's weights 16-byte aligned
     k_attn_scores<<<dim3((nk + 63) / 64, gy), 256, 0, c->stream>>>(a);
-    k_attn_combine<<<dim3(a.head_dim / 64, gy), 256, 4 * nk * sizeof(float), c->stream>>>(a);
+    k_attn_combine<<<dim3(a.head_dim / 64, gy), 256, 4 * a.wts_ld * sizeof(float), c->stream>>>(a);
     WH_HIP(hipGetLastError());
     return WH_OK;
 }
@@ -4036,7 +4036,7 @@ int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const 
         w.q_ld = (uint32_t)q_full;
         w.scores_ld = (uint32_t)(heads * max_keys);
         w.wlen = 128;
-        w.wts_ld = (uint32_t)max_keys;
+        w.wts_ld = (uint32_t)((max_keys + 3) & ~(size_t)3);  // each head's weights 16-byte aligned
         for (size_t i = 0; i < nb; ++i) {
             w.bpos[i] = (uint32_t)positions[c0 + i];
             w.bcomp[i] = comp_dev ? comp_dev[c0 + i] : nullptr;
@@ -4044,7 +4044,7 @@ int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const 
         }
         const unsigned gy = (unsigned)((heads + 3) / 4);
         k_attn_scores<<<dim3((unsigned)((max_keys + 63) / 64), gy, (unsigned)nb), 256, 0, c->stream>>>(w);
-        k_attn_combine<<<dim3((unsigned)(head_dim / 64), gy, (unsigned)nb), 256, 4 * max_keys * sizeof(float),
+        k_attn_combine<<<dim3((unsigned)(head_dim / 64), gy, (unsigned)nb), 256, 4 * w.wts_ld * sizeof(float),
                          c->stream>>>(w);
         WH_HIP(hipGetLastError());
     }
