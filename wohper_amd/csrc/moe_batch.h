@@ -187,6 +187,7 @@ __device__ __forceinline__ void wh_batch_quant_rows(const void* __restrict__ src
 __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
     __shared__ uint32_t ids[WH_BATCH_MAX_ASSIGN];
     __shared__ uint32_t slot_of[WH_BATCH_MAX_ASSIGN];
+    __shared__ float wsh[WH_BATCH_MAX_ASSIGN];  // route weights in route order until they are permuted
     __shared__ uint32_t cnt[WH_BATCH_MAX_TABLE], off[WH_BATCH_MAX_TABLE];
     __shared__ __align__(16) uint32_t ucnt[WH_BATCH_MAX_TABLE];
     __shared__ uint32_t uoffl[WH_BATCH_MAX_TABLE], uexpl[WH_BATCH_MAX_TABLE], uordl[WH_BATCH_MAX_TABLE];
@@ -221,16 +222,26 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
     // is not finite and positive or a score is not finite
     // (E/server/generation.rs:2495-2503)
     for (uint32_t p = tid; p < a.npos; p += 256) {
+        // the position's scores requested together (unconditional loads from
+        // clamped indices: a load in the loop was waited for before the next)
         const float* sc = a.route_scores + (size_t)p * a.topk;
+        float sv[WH_BATCH_MAX_TOPK];
+#pragma unroll
+        for (uint32_t k = 0; k < WH_BATCH_MAX_TOPK; ++k) sv[k] = sc[k < a.topk ? k : 0u];
         float sum = 0.0f;
         bool finite = true;
-        for (uint32_t k = 0; k < a.topk; ++k) {
-            finite = finite && fabsf(sc[k]) <= 3.4028235e38f;
-            sum = sum + sc[k];
+#pragma unroll
+        for (uint32_t k = 0; k < WH_BATCH_MAX_TOPK; ++k) {
+            if (k < a.topk) {
+                finite = finite && fabsf(sv[k]) <= 3.4028235e38f;
+                sum = sum + sv[k];
+            }
         }
         finite = finite && fabsf(sum) <= 3.4028235e38f && sum > 0.0f;
         const float uniform = 1.0f / (float)a.topk;
-        for (uint32_t k = 0; k < a.topk; ++k) a.wgt[(size_t)p * a.topk + k] = finite ? sc[k] / sum : uniform;
+#pragma unroll
+        for (uint32_t k = 0; k < WH_BATCH_MAX_TOPK; ++k)
+            if (k < a.topk) wsh[p * a.topk + k] = finite ? sv[k] / sum : uniform;
     }
     __syncthreads();
     if (bad) {
@@ -359,9 +370,8 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
     // order (E/server/generation.rs:2491-2506 pushes targets in that order):
     // key (id, route index) is distinct, and its rank among the position's
     // keys is its place (compile-time indices only: the keys stay in
-    // registers).  The weights (written above by this same thread, in route
-    // order) are permuted into that order too, so the accumulate reads them
-    // beside the slots.
+    // registers).  The weights (in LDS, in route order) are permuted into
+    // that order too, so the accumulate reads them beside the slots.
     for (uint32_t p = tid; p < a.npos; p += 256) {
         const uint32_t k0 = p * a.topk;
         uint32_t key[WH_BATCH_MAX_TOPK];
@@ -369,7 +379,7 @@ __global__ void __launch_bounds__(256) k_moe_batch_pack(wh_batch_args a) {
 #pragma unroll
         for (uint32_t k = 0; k < WH_BATCH_MAX_TOPK; ++k) {
             key[k] = k < a.topk ? (ids[k0 + k] << 4) | k : 0xffffffffu;
-            wk[k] = k < a.topk ? a.wgt[k0 + k] : 0.0f;
+            wk[k] = k < a.topk ? wsh[k0 + k] : 0.0f;
         }
 #pragma unroll
         for (uint32_t k = 0; k < WH_BATCH_MAX_TOPK; ++k) {
