@@ -3791,10 +3791,16 @@ int wh_window_attention_async(wh_ctx* c, const float* q_dev, size_t heads, size_
     return attn_launch(c, a);
 }
 
-int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token_pos, float* hidden_dev,
-                                  float* kv_cache_dev, size_t kv_stride, size_t kv_capacity, const float* comp_dev,
-                                  size_t n_comp) {
-    if (!c || !L || !hidden_dev || !kv_cache_dev || (n_comp && !comp_dev)) return WH_INVALID_ARGUMENT;
+// The single-token attention with its input in in_dev and its output in
+// hidden_dev; in_norm: the RMS norm of the input (weights in_norm_w, or
+// none) runs in the same launch as the input's act-quant (the decode layer's
+// attention norm: the same values as a norm launch followed by the act-quant
+// launch).
+static int mla_decode_impl(wh_ctx* c, const wh_mla_layer* L, size_t token_pos, const float* in_dev, int in_norm,
+                           const uint16_t* in_norm_w, float* hidden_dev, float* kv_cache_dev, size_t kv_stride,
+                           size_t kv_capacity, const float* comp_dev, size_t n_comp) {
+    if (!c || !L || !in_dev || !hidden_dev || !kv_cache_dev || (n_comp && !comp_dev)) return WH_INVALID_ARGUMENT;
+    if ((uintptr_t)in_dev & 15) return WH_INVALID_ARGUMENT;
     const size_t heads = L->heads, nope = L->nope_dim, rope = L->rope_dim, head_dim = nope + rope;
     const size_t q_full = heads * head_dim, groups = L->o_groups, o_lora = L->o_lora_rank;
     // E/compute.rs:3932-3950
@@ -3842,7 +3848,9 @@ int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token
     float* kv_row = kv_cache_dev + token_pos * kv_stride;
     // q path (E/compute.rs:3998-4040): act-quant of x, wq_a, q norm + act-quant,
     // wq_b, per-head RMS norm + RoPE
-    wh_rowpost_args a = rowpost_args(hidden_dev, xq, 1, hidden, hidden, hidden);
+    wh_rowpost_args a = rowpost_args(in_dev, xq, 1, hidden, hidden, hidden);
+    a.norm = in_norm ? 1u : 0u;
+    a.w = in_norm_w;
     a.aq_len = (uint32_t)hidden;
     WH_TRY(rowpost_launch(c, a));
     // wq_a and wkv both read the act-quantized x: one launch when they can
@@ -3912,6 +3920,13 @@ int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token
     return WH_OK;
 }
 
+int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token_pos, float* hidden_dev,
+                                  float* kv_cache_dev, size_t kv_stride, size_t kv_capacity, const float* comp_dev,
+                                  size_t n_comp) {
+    return mla_decode_impl(c, L, token_pos, hidden_dev, 0, nullptr, hidden_dev, kv_cache_dev, kv_stride, kv_capacity,
+                           comp_dev, n_comp);
+}
+
 // The batched MLA attention of prefill and MTP verify
 // (compute_deepseek_v4_mla_attention_batch, E/compute.rs:4307-4641): the
 // projections over all positions at once (rows_multi, bit-identical per
@@ -3920,10 +3935,13 @@ int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token
 // position reads only cache rows at or before its own, so writing every
 // row first changes nothing), and the grouped output projections batched
 // again.
-int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const size_t* positions, size_t npos,
-                                        float* hidden_dev, float* kv_cache_dev, size_t kv_stride, size_t kv_capacity,
-                                        const float* const* comp_dev, const size_t* n_comp) {
-    if (!c || !L || !positions || !hidden_dev || !kv_cache_dev) return WH_INVALID_ARGUMENT;
+// in_dev / in_norm / in_norm_w as in mla_decode_impl, npos rows of hidden.
+static int mla_decode_batch_impl(wh_ctx* c, const wh_mla_layer* L, const size_t* positions, size_t npos,
+                                 const float* in_dev, int in_norm, const uint16_t* in_norm_w, float* hidden_dev,
+                                 float* kv_cache_dev, size_t kv_stride, size_t kv_capacity,
+                                 const float* const* comp_dev, const size_t* n_comp) {
+    if (!c || !L || !positions || !in_dev || !hidden_dev || !kv_cache_dev) return WH_INVALID_ARGUMENT;
+    if ((uintptr_t)in_dev & 15) return WH_INVALID_ARGUMENT;
     if (npos == 0) return WH_INVALID_SHAPE;  // "MLA batch ys size"
     for (size_t i = 0; i < npos; ++i) {
         if (i && positions[i] <= positions[i - 1]) return WH_INVALID_ARGUMENT;  // ascending positions
@@ -3979,7 +3997,9 @@ int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const 
           *at = base + o_at, *om = base + o_om;
     // q and kv paths (E/compute.rs:4420-4490): act-quant of every x; wq_a
     // and wkv over all positions; q norm + act-quant; wq_b over all positions
-    wh_rowpost_args a = rowpost_args(hidden_dev, xq, npos, hidden, hidden, hidden);
+    wh_rowpost_args a = rowpost_args(in_dev, xq, npos, hidden, hidden, hidden);
+    a.norm = in_norm ? 1u : 0u;
+    a.w = in_norm_w;
     a.aq_len = (uint32_t)hidden;
     WH_TRY(rowpost_launch(c, a));
     WH_TRY(wh_fp8_gemv_multi_pair_async(c, L->wq_a, 0, q_lora, ql, q_lora, L->wkv, 0, head_dim, kvt, head_dim, xq, npos,
@@ -4063,6 +4083,13 @@ int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const 
     WH_TRY(wh_fp8_gemv_multi_async(c, L->wo_b, 0, hidden, om, npos, o_mid, hidden_dev, hidden));
     WH_HIP(hipGetLastError());
     return WH_OK;
+}
+
+int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const size_t* positions, size_t npos,
+                                        float* hidden_dev, float* kv_cache_dev, size_t kv_stride, size_t kv_capacity,
+                                        const float* const* comp_dev, const size_t* n_comp) {
+    return mla_decode_batch_impl(c, L, positions, npos, hidden_dev, 0, nullptr, hidden_dev, kv_cache_dev, kv_stride,
+                                 kv_capacity, comp_dev, n_comp);
 }
 
 // ------------------------------------------------------------------ mHC
@@ -4197,9 +4224,10 @@ int wh_deepseek_mhc_layer_async(wh_ctx* c, const wh_mhc_layer* L, size_t token_p
     // attention sub-block (E/compute.rs:1552-1605)
     WH_TRY(wh_hc_pre_async(c, L->hc_attn_fn, L->hc_attn_scale, L->hc_attn_base, hc, hidden, L->sinkhorn_iters,
                            L->hc_eps, hidden_dev, y, post1, comb1));
-    WH_TRY(wh_rms_norm_async(c, y, g, 1, hidden, L->attn_norm_bf16));
-    WH_TRY(wh_mla_attention_decode_async(c, &L->attn, token_pos, g, kv_cache_dev, kv_stride, kv_capacity, comp_dev,
-                                         n_comp));
+    // the attention norm in the attention's first launch (with the
+    // act-quant of its input), the output in g
+    WH_TRY(mla_decode_impl(c, &L->attn, token_pos, y, 1, L->attn_norm_bf16, g, kv_cache_dev, kv_stride, kv_capacity,
+                           comp_dev, n_comp));
     WH_TRY(wh_hc_post_async(c, g, hidden_dev, post1, comb1, state, hc, hidden));
     // ffn hc_pre + norm: the gate input (E/compute.rs:1607-1630)
     WH_TRY(wh_hc_pre_async(c, L->hc_ffn_fn, L->hc_ffn_scale, L->hc_ffn_base, hc, hidden, L->sinkhorn_iters,
@@ -4256,9 +4284,8 @@ int wh_deepseek_mhc_layer_batch_async(wh_ctx* c, const wh_mhc_layer* L, const si
         return WH_INVALID_ARGUMENT;
     WH_TRY(hc_pre_launch(c, L->hc_attn_fn, L->hc_attn_scale, L->hc_attn_base, hc, hidden, L->sinkhorn_iters, L->hc_eps,
                          hidden_dev, y, post1, comb1, npos));
-    WH_TRY(wh_rms_norm_async(c, y, g, npos, hidden, L->attn_norm_bf16));
-    WH_TRY(wh_mla_attention_decode_batch_async(c, &L->attn, positions, npos, g, kv_cache_dev, kv_stride, kv_capacity,
-                                               comp_dev, n_comp));
+    WH_TRY(mla_decode_batch_impl(c, &L->attn, positions, npos, y, 1, L->attn_norm_bf16, g, kv_cache_dev, kv_stride,
+                                 kv_capacity, comp_dev, n_comp));
     WH_TRY(hc_post_launch(c, g, hidden_dev, post1, comb1, state, hc, hidden, npos));
     WH_TRY(hc_pre_launch(c, L->hc_ffn_fn, L->hc_ffn_scale, L->hc_ffn_base, hc, hidden, L->sinkhorn_iters, L->hc_eps,
                          state, y, post2, comb2, npos));
