@@ -63,6 +63,11 @@ struct wh_rowpost_args {
     // cache row)
     uint32_t rows_per_pos, out_at_pos;
     uint32_t bpos[WH_POS_BATCH];
+    // hc > 0: the row is the end of hc_pre_into (E/compute.rs:5044-5050),
+    // y[d] = sum over i in order of hc_pre[r * hc + i] * x[i * hc_stride + d]
+    // for the hc copies at x + r * ld_in, instead of x itself
+    const float* hc_pre;
+    uint32_t hc, hc_stride;
 };
 
 // kT threads per row (256, or 1024 for a lone row); each thread's values
@@ -88,11 +93,44 @@ __global__ void __launch_bounds__(kT) k_rowpost(wh_rowpost_args a) {
     const bool use_w = a.norm && a.w;
     const uint16_t* wp = use_w ? a.w : (const uint16_t*)x;
     uint32_t wr[kPer];
+    if (a.hc == 4) {
+        // the four copies' loads issued together, then the reference's sum
+        const float* pre = a.hc_pre + (size_t)blockIdx.x * 4;
+        const float p0 = pre[0], p1 = pre[1], p2 = pre[2], p3 = pre[3];
+        float cv[4][kPer];
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-        const uint32_t i = t + kT * k, ic = i < n ? i : 0u;
-        xv[k] = x[ic];
-        wr[k] = wp[ic];
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t i = t + kT * k, ic = i < n ? i : 0u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) cv[j][k] = x[(size_t)j * a.hc_stride + ic];
+            wr[k] = wp[ic];
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            float acc = 0.0f;
+            acc = acc + p0 * cv[0][k];
+            acc = acc + p1 * cv[1][k];
+            acc = acc + p2 * cv[2][k];
+            acc = acc + p3 * cv[3][k];
+            xv[k] = acc;
+        }
+    } else if (a.hc) {
+        const float* pre = a.hc_pre + (size_t)blockIdx.x * a.hc;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t i = t + kT * k, ic = i < n ? i : 0u;
+            float acc = 0.0f;
+            for (uint32_t j = 0; j < a.hc; ++j) acc = acc + pre[j] * x[(size_t)j * a.hc_stride + ic];
+            xv[k] = acc;
+            wr[k] = wp[ic];
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const uint32_t i = t + kT * k, ic = i < n ? i : 0u;
+            xv[k] = x[ic];
+            wr[k] = wp[ic];
+        }
     }
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {

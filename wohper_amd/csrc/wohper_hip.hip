@@ -3791,14 +3791,26 @@ int wh_window_attention_async(wh_ctx* c, const float* q_dev, size_t heads, size_
     return attn_launch(c, a);
 }
 
-// The single-token attention with its input in in_dev and its output in
-// hidden_dev; in_norm: the RMS norm of the input (weights in_norm_w, or
-// none) runs in the same launch as the input's act-quant (the decode layer's
-// attention norm: the same values as a norm launch followed by the act-quant
-// launch).
-static int mla_decode_impl(wh_ctx* c, const wh_mla_layer* L, size_t token_pos, const float* in_dev, int in_norm,
-                           const uint16_t* in_norm_w, float* hidden_dev, float* kv_cache_dev, size_t kv_stride,
-                           size_t kv_capacity, const float* comp_dev, size_t n_comp) {
+// The attention's input as its first launch reads it: x (rows ld floats
+// apart), optionally the end of hc_pre (y = sum of pre-weighted copies,
+// hc > 0) and the RMS norm (norm, weights w or none), then the act-quant.
+// The decode layers pass hc_pre's copies and the attention norm, so that
+// neither y nor the norm output takes a launch of its own (the same values).
+struct MlaIn {
+    const float* x;
+    size_t ld;
+    int norm;
+    const uint16_t* w;
+    const float* pre;
+    size_t hc, hc_stride;
+};
+
+// The single-token attention with its input in.x and its output in
+// hidden_dev.
+static int mla_decode_impl(wh_ctx* c, const wh_mla_layer* L, size_t token_pos, const MlaIn& in, float* hidden_dev,
+                           float* kv_cache_dev, size_t kv_stride, size_t kv_capacity, const float* comp_dev,
+                           size_t n_comp) {
+    const float* in_dev = in.x;
     if (!c || !L || !in_dev || !hidden_dev || !kv_cache_dev || (n_comp && !comp_dev)) return WH_INVALID_ARGUMENT;
     if ((uintptr_t)in_dev & 15) return WH_INVALID_ARGUMENT;
     const size_t heads = L->heads, nope = L->nope_dim, rope = L->rope_dim, head_dim = nope + rope;
@@ -3848,9 +3860,12 @@ static int mla_decode_impl(wh_ctx* c, const wh_mla_layer* L, size_t token_pos, c
     float* kv_row = kv_cache_dev + token_pos * kv_stride;
     // q path (E/compute.rs:3998-4040): act-quant of x, wq_a, q norm + act-quant,
     // wq_b, per-head RMS norm + RoPE
-    wh_rowpost_args a = rowpost_args(in_dev, xq, 1, hidden, hidden, hidden);
-    a.norm = in_norm ? 1u : 0u;
-    a.w = in_norm_w;
+    wh_rowpost_args a = rowpost_args(in_dev, xq, 1, hidden, in.ld ? in.ld : hidden, hidden);
+    a.norm = in.norm ? 1u : 0u;
+    a.w = in.w;
+    a.hc_pre = in.pre;
+    a.hc = (uint32_t)in.hc;
+    a.hc_stride = (uint32_t)in.hc_stride;
     a.aq_len = (uint32_t)hidden;
     WH_TRY(rowpost_launch(c, a));
     // wq_a and wkv both read the act-quantized x: one launch when they can
@@ -3923,8 +3938,9 @@ static int mla_decode_impl(wh_ctx* c, const wh_mla_layer* L, size_t token_pos, c
 int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token_pos, float* hidden_dev,
                                   float* kv_cache_dev, size_t kv_stride, size_t kv_capacity, const float* comp_dev,
                                   size_t n_comp) {
-    return mla_decode_impl(c, L, token_pos, hidden_dev, 0, nullptr, hidden_dev, kv_cache_dev, kv_stride, kv_capacity,
-                           comp_dev, n_comp);
+    MlaIn in{};
+    in.x = hidden_dev;
+    return mla_decode_impl(c, L, token_pos, in, hidden_dev, kv_cache_dev, kv_stride, kv_capacity, comp_dev, n_comp);
 }
 
 // The batched MLA attention of prefill and MTP verify
@@ -3935,11 +3951,11 @@ int wh_mla_attention_decode_async(wh_ctx* c, const wh_mla_layer* L, size_t token
 // position reads only cache rows at or before its own, so writing every
 // row first changes nothing), and the grouped output projections batched
 // again.
-// in_dev / in_norm / in_norm_w as in mla_decode_impl, npos rows of hidden.
+// in as in mla_decode_impl, npos rows.
 static int mla_decode_batch_impl(wh_ctx* c, const wh_mla_layer* L, const size_t* positions, size_t npos,
-                                 const float* in_dev, int in_norm, const uint16_t* in_norm_w, float* hidden_dev,
-                                 float* kv_cache_dev, size_t kv_stride, size_t kv_capacity,
-                                 const float* const* comp_dev, const size_t* n_comp) {
+                                 const MlaIn& in, float* hidden_dev, float* kv_cache_dev, size_t kv_stride,
+                                 size_t kv_capacity, const float* const* comp_dev, const size_t* n_comp) {
+    const float* in_dev = in.x;
     if (!c || !L || !positions || !in_dev || !hidden_dev || !kv_cache_dev) return WH_INVALID_ARGUMENT;
     if ((uintptr_t)in_dev & 15) return WH_INVALID_ARGUMENT;
     if (npos == 0) return WH_INVALID_SHAPE;  // "MLA batch ys size"
@@ -3997,9 +4013,12 @@ static int mla_decode_batch_impl(wh_ctx* c, const wh_mla_layer* L, const size_t*
           *at = base + o_at, *om = base + o_om;
     // q and kv paths (E/compute.rs:4420-4490): act-quant of every x; wq_a
     // and wkv over all positions; q norm + act-quant; wq_b over all positions
-    wh_rowpost_args a = rowpost_args(in_dev, xq, npos, hidden, hidden, hidden);
-    a.norm = in_norm ? 1u : 0u;
-    a.w = in_norm_w;
+    wh_rowpost_args a = rowpost_args(in_dev, xq, npos, hidden, in.ld ? in.ld : hidden, hidden);
+    a.norm = in.norm ? 1u : 0u;
+    a.w = in.w;
+    a.hc_pre = in.pre;
+    a.hc = (uint32_t)in.hc;
+    a.hc_stride = (uint32_t)in.hc_stride;
     a.aq_len = (uint32_t)hidden;
     WH_TRY(rowpost_launch(c, a));
     WH_TRY(wh_fp8_gemv_multi_pair_async(c, L->wq_a, 0, q_lora, ql, q_lora, L->wkv, 0, head_dim, kvt, head_dim, xq, npos,
@@ -4088,8 +4107,10 @@ static int mla_decode_batch_impl(wh_ctx* c, const wh_mla_layer* L, const size_t*
 int wh_mla_attention_decode_batch_async(wh_ctx* c, const wh_mla_layer* L, const size_t* positions, size_t npos,
                                         float* hidden_dev, float* kv_cache_dev, size_t kv_stride, size_t kv_capacity,
                                         const float* const* comp_dev, const size_t* n_comp) {
-    return mla_decode_batch_impl(c, L, positions, npos, hidden_dev, 0, nullptr, hidden_dev, kv_cache_dev, kv_stride,
-                                 kv_capacity, comp_dev, n_comp);
+    MlaIn in{};
+    in.x = hidden_dev;
+    return mla_decode_batch_impl(c, L, positions, npos, in, hidden_dev, kv_cache_dev, kv_stride, kv_capacity,
+                                 comp_dev, n_comp);
 }
 
 // ------------------------------------------------------------------ mHC
@@ -4134,9 +4155,11 @@ int wh_hc_split_sinkhorn_async(wh_ctx* c, const float* mixes_dev, const float* s
 namespace {
 // hc_pre of npos streams (x_dev npos x hc * hidden, y_dev npos x hidden,
 // post_dev npos x hc, comb_dev npos x hc * hc) in one launch per stage.
+// want_y false: y is left to the caller's next launch (a row kernel with
+// hc_pre set), and *pre_out gets the pre weights (npos x hc, in the scratch)
 int hc_pre_launch(wh_ctx* c, const float* fn_dev, const float* scale_dev, const float* base_dev, size_t hc,
                   size_t hidden, size_t sinkhorn_iters, float eps, const float* x_dev, float* y_dev, float* post_dev,
-                  float* comb_dev, size_t npos) {
+                  float* comb_dev, size_t npos, bool want_y = true, const float** pre_out = nullptr) {
     wh_hc_args a = hc_args(hc, hidden, sinkhorn_iters, eps);
     a.fn = fn_dev;
     a.scale = scale_dev;
@@ -4158,7 +4181,8 @@ int hc_pre_launch(wh_ctx* c, const float* fn_dev, const float* scale_dev, const 
         k_hc_partials<<<dim3(WH_HC_PARTS, a.mix_hc + 1, z), 256, 0, c->stream>>>(a);
     }
     k_hc_finish<<<z, 256, 0, c->stream>>>(a);
-    k_hc_y<<<dim3((unsigned)((hidden + 255) / 256), z), 256, 0, c->stream>>>(a);
+    if (want_y) k_hc_y<<<dim3((unsigned)((hidden + 255) / 256), z), 256, 0, c->stream>>>(a);
+    if (pre_out) *pre_out = a.pre;
     WH_HIP(hipGetLastError());
     return WH_OK;
 }
@@ -4222,17 +4246,37 @@ int wh_deepseek_mhc_layer_async(wh_ctx* c, const wh_mhc_layer* L, size_t token_p
     float* w = f + o_w;
     uint32_t* count = reinterpret_cast<uint32_t*>(f + o_n);
     // attention sub-block (E/compute.rs:1552-1605)
-    WH_TRY(wh_hc_pre_async(c, L->hc_attn_fn, L->hc_attn_scale, L->hc_attn_base, hc, hidden, L->sinkhorn_iters,
-                           L->hc_eps, hidden_dev, y, post1, comb1));
-    // the attention norm in the attention's first launch (with the
-    // act-quant of its input), the output in g
-    WH_TRY(mla_decode_impl(c, &L->attn, token_pos, y, 1, L->attn_norm_bf16, g, kv_cache_dev, kv_stride, kv_capacity,
-                           comp_dev, n_comp));
+    if (!L->hc_attn_fn || !L->hc_attn_scale || !L->hc_attn_base || !L->hc_ffn_fn || !L->hc_ffn_scale ||
+        !L->hc_ffn_base || hidden > WH_ROWPOST_MAX)
+        return hidden > WH_ROWPOST_MAX ? WH_UNSUPPORTED : WH_INVALID_ARGUMENT;
+    // hc_pre's y and the attention norm in the attention's first launch
+    // (with the act-quant of its input); the output in g
+    const float* pre = nullptr;
+    WH_TRY(hc_pre_launch(c, L->hc_attn_fn, L->hc_attn_scale, L->hc_attn_base, hc, hidden, L->sinkhorn_iters, L->hc_eps,
+                         hidden_dev, y, post1, comb1, 1, false, &pre));
+    MlaIn in{};
+    in.x = hidden_dev;
+    in.ld = hc * hidden;
+    in.norm = 1;
+    in.w = L->attn_norm_bf16;
+    in.pre = pre;
+    in.hc = hc;
+    in.hc_stride = hidden;
+    WH_TRY(mla_decode_impl(c, &L->attn, token_pos, in, g, kv_cache_dev, kv_stride, kv_capacity, comp_dev, n_comp));
     WH_TRY(wh_hc_post_async(c, g, hidden_dev, post1, comb1, state, hc, hidden));
-    // ffn hc_pre + norm: the gate input (E/compute.rs:1607-1630)
-    WH_TRY(wh_hc_pre_async(c, L->hc_ffn_fn, L->hc_ffn_scale, L->hc_ffn_base, hc, hidden, L->sinkhorn_iters,
-                           L->hc_eps, state, y, post2, comb2));
-    WH_TRY(wh_rms_norm_async(c, y, g, 1, hidden, L->ffn_norm_bf16));
+    // ffn hc_pre + norm: the gate input (E/compute.rs:1607-1630), y and the
+    // norm in one launch
+    WH_TRY(hc_pre_launch(c, L->hc_ffn_fn, L->hc_ffn_scale, L->hc_ffn_base, hc, hidden, L->sinkhorn_iters, L->hc_eps,
+                         state, y, post2, comb2, 1, false, &pre));
+    {
+        wh_rowpost_args a = rowpost_args(state, g, 1, hidden, hc * hidden, hidden);
+        a.norm = 1;
+        a.w = L->ffn_norm_bf16;
+        a.hc_pre = pre;
+        a.hc = (uint32_t)hc;
+        a.hc_stride = (uint32_t)hidden;
+        WH_TRY(rowpost_launch(c, a));
+    }
     // the router on the gate input, then the experts on its route list
     // (E/compute.rs:1641-1700)
     const size_t slots = L->active;
@@ -4282,14 +4326,33 @@ int wh_deepseek_mhc_layer_batch_async(wh_ctx* c, const wh_mhc_layer* L, const si
     if (!L->hc_attn_fn || !L->hc_attn_scale || !L->hc_attn_base || !L->hc_ffn_fn || !L->hc_ffn_scale ||
         !L->hc_ffn_base)
         return WH_INVALID_ARGUMENT;
+    if (hidden > WH_ROWPOST_MAX) return WH_UNSUPPORTED;
+    // hc_pre's y and each norm in the launch that follows (the same values)
+    const float* pre = nullptr;
     WH_TRY(hc_pre_launch(c, L->hc_attn_fn, L->hc_attn_scale, L->hc_attn_base, hc, hidden, L->sinkhorn_iters, L->hc_eps,
-                         hidden_dev, y, post1, comb1, npos));
-    WH_TRY(mla_decode_batch_impl(c, &L->attn, positions, npos, y, 1, L->attn_norm_bf16, g, kv_cache_dev, kv_stride,
-                                 kv_capacity, comp_dev, n_comp));
+                         hidden_dev, y, post1, comb1, npos, false, &pre));
+    MlaIn in{};
+    in.x = hidden_dev;
+    in.ld = hcd;
+    in.norm = 1;
+    in.w = L->attn_norm_bf16;
+    in.pre = pre;
+    in.hc = hc;
+    in.hc_stride = hidden;
+    WH_TRY(mla_decode_batch_impl(c, &L->attn, positions, npos, in, g, kv_cache_dev, kv_stride, kv_capacity, comp_dev,
+                                 n_comp));
     WH_TRY(hc_post_launch(c, g, hidden_dev, post1, comb1, state, hc, hidden, npos));
     WH_TRY(hc_pre_launch(c, L->hc_ffn_fn, L->hc_ffn_scale, L->hc_ffn_base, hc, hidden, L->sinkhorn_iters, L->hc_eps,
-                         state, y, post2, comb2, npos));
-    WH_TRY(wh_rms_norm_async(c, y, g, npos, hidden, L->ffn_norm_bf16));
+                         state, y, post2, comb2, npos, false, &pre));
+    {
+        wh_rowpost_args a = rowpost_args(state, g, npos, hidden, hcd, hidden);
+        a.norm = 1;
+        a.w = L->ffn_norm_bf16;
+        a.hc_pre = pre;
+        a.hc = (uint32_t)hc;
+        a.hc_stride = (uint32_t)hidden;
+        WH_TRY(rowpost_launch(c, a));
+    }
     // the router per position (E/server/generation.rs:2462-2480, each with
     // its own token for a hash layer), then the experts of the whole batch
     // on the device route lists
