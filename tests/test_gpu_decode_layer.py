@@ -139,3 +139,33 @@ def test_decode_layer_order_free_and_graph(ctx, oracle, dev):
         ctx.graph_release(g)
     for t in handles.values():
         ctx.release(t)
+
+
+def test_decode_layer_route_to_missing_expert(ctx, oracle, dev):
+    """A layer whose router selects experts that are not resident reports
+    NotResident through the stream, as the device route list does: the
+    router's last workgroup resolves the routes (one expert and the shared
+    one resident of 32 rows, so at least five of the six routes miss)."""
+    ctx.set_exact_numerics(False)
+    L, _, handles = _setup(ctx, oracle, dev)
+    other = LAYER + 1
+    rng = np.random.default_rng(SEED)
+    gate = ((rng.standard_normal((N_EXP, wl.HIDDEN)).astype(np.float32) * 0.02).view(np.uint32) >> 16)
+    blk = mf.build_synthetic_quant_block([
+        mf.SyntheticTensor(f"layers.{other}.ffn.gate.weight", 9, (N_EXP, wl.HIDDEN), gate.astype(np.uint16).tobytes(),
+                           11, 2404),
+        mf.SyntheticTensor(f"layers.{other}.ffn.gate.bias", 9, (N_EXP,), np.zeros(N_EXP, np.float32).tobytes(), 12,
+                           2405)])
+    ctx.store_router(other, blk, wl.HIDDEN)
+    for e in (0, N_EXP):
+        ctx.store_expert_synthetic(other, e, wl.HIDDEN, wl.INTER, SEED)
+    L.layer_id, L.shared_layer = other, other
+    cap, ld = 8, HEAD_DIM + 64
+    hp = dev.put((rng.standard_normal(HC * wl.HIDDEN) * 0.5).astype(np.float32))
+    kvp = dev.put(np.zeros((cap, ld), np.float32))
+    ctx.deepseek_mhc_layer_async(L, 0, hp, kvp, ld, cap)
+    with pytest.raises(wohper_amd.DeepSeekV4KernelError) as e:
+        ctx.synchronize()
+    assert e.value.name == "NotResident"
+    for t in handles.values():
+        ctx.release(t)

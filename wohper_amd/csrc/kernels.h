@@ -898,18 +898,20 @@ __device__ __forceinline__ uint32_t wh_moe_nr(const wh_moe_args& a) {
 // route, else the shared expert, else the table's first resident entry -
 // computed and never summed; the shared expert goes to slot n_slots.  One
 // wave; the host checks that some expert is resident.
-__global__ void __launch_bounds__(64) k_moe_resolve(const uint32_t* __restrict__ ids, const float* __restrict__ w,
-                                                    const uint32_t* __restrict__ count,
+// The resolve of one wave (k_moe_resolve, or the router's last arriver):
+// lane L < cnt holds route L's expert id and weight; slots [0, cnt) get
+// their experts, the slots after them up to n_slots a resident stand-in
+// (computed, never summed), slot n_slots the shared expert when there is
+// one.  got: 64 entries of workgroup memory.
+__device__ __forceinline__ void wh_moe_resolve_wave(uint32_t id, float wt, uint32_t cnt,
                                                     const wh_expert_ptrs* __restrict__ table, uint32_t table_n,
-                                                    wh_expert_ptrs shared, uint32_t has_shared, uint32_t n_slots,
-                                                    wh_moe_dyn* __restrict__ out, uint32_t* status) {
-    __shared__ wh_expert_ptrs got[64];
-    const uint32_t L = threadIdx.x;
-    const uint32_t cnt = min(*count, n_slots);
+                                                    const wh_expert_ptrs& shared, uint32_t has_shared,
+                                                    uint32_t n_slots, wh_moe_dyn* __restrict__ out, uint32_t* status,
+                                                    wh_expert_ptrs* got) {
+    const uint32_t L = threadIdx.x & 63;
     bool ok = false;
     wh_expert_ptrs p = {};
     if (L < cnt) {
-        const uint32_t id = ids[L];
         if (id < table_n) {
             p = table[id];
             ok = p.w1 != nullptr;
@@ -946,10 +948,23 @@ __global__ void __launch_bounds__(64) k_moe_resolve(const uint32_t* __restrict__
     if (L < n_slots) {
         if (ok) put(L, p);
         else put(L, fb);
-        out->route_w[L] = L < cnt ? w[L] : 0.0f;
+        out->route_w[L] = L < cnt ? wt : 0.0f;
     }
     if (L == n_slots && has_shared) put(L, shared);
     if (L == 0) out->n_routed = cnt;
+}
+
+__global__ void __launch_bounds__(64) k_moe_resolve(const uint32_t* __restrict__ ids, const float* __restrict__ w,
+                                                    const uint32_t* __restrict__ count,
+                                                    const wh_expert_ptrs* __restrict__ table, uint32_t table_n,
+                                                    wh_expert_ptrs shared, uint32_t has_shared, uint32_t n_slots,
+                                                    wh_moe_dyn* __restrict__ out, uint32_t* status) {
+    __shared__ wh_expert_ptrs got[64];
+    const uint32_t L = threadIdx.x;
+    const uint32_t cnt = min(*count, n_slots);
+    const uint32_t id = L < cnt ? ids[L] : 0u;
+    const float wt = L < cnt ? w[L] : 0.0f;
+    wh_moe_resolve_wave(id, wt, cnt, table, table_n, shared, has_shared, n_slots, out, status, got);
 }
 
 // The ordered routed sum of one output row from the per-slot outputs yv

@@ -229,6 +229,14 @@ struct wh_router_sel {
     // selection order (rows % 4 == 0, rows <= 256, no available list, no
     // hash row); logits then holds [rows] u64 (score, key) and [rows] u32 ids
     uint32_t sorted;
+    // with sorted: when rs_out is set, the last arriver also resolves the
+    // selected routes against a layer's expert table into rs_out (the work
+    // of k_moe_resolve, one launch fewer before the experts)
+    wh_moe_dyn* rs_out;
+    const wh_expert_ptrs* rs_table;
+    uint32_t rs_table_n, rs_slots, rs_has_shared;
+    uint32_t* rs_status;
+    wh_expert_ptrs rs_shared;
 };
 
 // f32::total_cmp order as a signed key.
@@ -471,11 +479,18 @@ __device__ __forceinline__ void wh_router_select_sorted(const wh_router_sel& a) 
     WH_TL_USE(sum);
     WH_TL(0, 10);
 #endif
+    const float wv = !norm ? v : (ok ? v / sum * a.route_scale : uniform);
     if (L < n) {
         a.out_ids[L] = my_sel;
-        a.out_scores[L] = !norm ? v : (ok ? v / sum * a.route_scale : uniform);
+        a.out_scores[L] = wv;
     }
     if (L == 0) *a.out_count = n;
+    if (a.rs_out) {
+        __shared__ wh_expert_ptrs got[64];
+        const uint32_t cnt = n < a.rs_slots ? n : a.rs_slots;
+        wh_moe_resolve_wave(L < cnt ? my_sel : 0u, L < cnt ? wv : 0.0f, cnt, a.rs_table, a.rs_table_n, a.rs_shared,
+                            a.rs_has_shared, a.rs_slots, a.rs_out, a.rs_status, got);
+    }
 }
 
 // kSlots candidates per lane: 4 up to 256 candidates, else 16.  sk: the

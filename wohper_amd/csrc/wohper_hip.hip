@@ -1763,10 +1763,21 @@ int router_prepare(const Router& rt, const wh_route_options& o, size_t hidden_le
     return WH_OK;
 }
 
+// What the experts of one token with a device route list need from the
+// host: the layer's expert table, the shared expert, the one fast shape.
+struct MoeDevPrep {
+    LayerTable* t = nullptr;
+    wh_expert_ptrs shp = {};
+    bool has_shared = false, zero_scale = false;
+    size_t n_slots = 0, hidden = 0, inter = 0;
+    wh_moe_dyn* dyn = nullptr;
+};
+
 // Gate GEMV then selection, on the context stream.  x: device f32 [cols];
 // avail: device ids or null; logits: device scratch [rows].
 int router_launch(wh_ctx* c, const Router& rt, wh_router_sel sa, const float* x, const uint32_t* avail,
-                  float* logits, uint32_t* ids, float* scores, uint32_t* count) {
+                  float* logits, uint32_t* ids, float* scores, uint32_t* count, const MoeDevPrep* rs = nullptr,
+                  bool* resolved = nullptr) {
     const unsigned rows = (unsigned)rt.rows, cols = (unsigned)rt.cols;
     sa.logits = logits;
     sa.bias = sa.math ? rt.bias : nullptr;
@@ -1778,6 +1789,16 @@ int router_launch(wh_ctx* c, const Router& rt, wh_router_sel sa, const float* x,
         // each workgroup's 4 candidates published in selection order where
         // the candidates are exactly the rows (the scratch holds 3 words a row)
         sa.sorted = (!avail && sa.n_hash == 0 && rows % 4 == 0 && rows <= 256) ? 1u : 0u;
+        if (sa.sorted && rs && rs->n_slots <= 64) {  // the last arriver also resolves the routes
+            sa.rs_out = rs->dyn;
+            sa.rs_table = rs->t->dev;
+            sa.rs_table_n = (uint32_t)rs->t->n;
+            sa.rs_slots = (uint32_t)rs->n_slots;
+            sa.rs_has_shared = rs->has_shared ? 1u : 0u;
+            sa.rs_status = c->status;
+            sa.rs_shared = rs->shp;
+            *resolved = true;
+        }
         WH_HIP(c->rtr_cnt.ensure(sizeof(uint32_t), true));
         k_router_bf16<<<(rows + 3) / 4, 64, cols * sizeof(float), c->stream>>>(rt.bf16, x, cols, sa,
                                                                                c->rtr_cnt.as<uint32_t>(), 0, 0);
@@ -2501,13 +2522,16 @@ int wh_route_experts(wh_ctx* c, uint32_t layer, const float* hidden, size_t hidd
     return read_status(c);
 }
 
-int wh_route_experts_async(wh_ctx* c, uint32_t layer, const float* x_dev, size_t hidden_len, size_t active,
-                           const uint32_t* available_dev, size_t n_available, const wh_route_options* opts,
-                           uint32_t* ids_dev, float* scores_dev, uint32_t* count_dev) {
+// wh_route_experts_async; with rs, the router's last workgroup also
+// resolves the selected routes into rs->dyn where the one-launch sorted
+// selection applies (*resolved then true).  The caller holds c->mu.
+int route_experts(wh_ctx* c, uint32_t layer, const float* x_dev, size_t hidden_len, size_t active,
+                  const uint32_t* available_dev, size_t n_available, const wh_route_options* opts,
+                  uint32_t* ids_dev, float* scores_dev, uint32_t* count_dev, const MoeDevPrep* rs, bool* resolved) {
+    if (resolved) *resolved = false;
     if (!c || !opts || !x_dev || !ids_dev || !scores_dev || !count_dev) return WH_INVALID_ARGUMENT;
     if ((uintptr_t)x_dev & 15) return WH_INVALID_ARGUMENT;  // x is read in 16-byte pieces
     if (active > WH_ROUTER_MAX_ACTIVE || n_available > WH_ROUTER_MAX_ROWS) return WH_UNSUPPORTED;
-    std::lock_guard<std::recursive_mutex> lk(c->mu);
     WH_HIP(hipSetDevice(c->device));
     auto it = c->routers.find(layer);
     if (it == c->routers.end()) return WH_NOT_RESIDENT;
@@ -2526,7 +2550,16 @@ int wh_route_experts_async(wh_ctx* c, uint32_t layer, const float* x_dev, size_t
     WH_TRY(router_prepare(rt, *opts, hidden_len, active, available_dev ? n_available : rt.rows, &sa));
     WH_HIP(c->rtr.ensure((rt.cols + 3 * rt.rows + 2 * WH_ROUTER_MAX_ACTIVE + 1) * 4, false));
     float* logits = c->rtr.as<float>() + rt.cols;
-    return router_launch(c, rt, sa, x_dev, available_dev, logits, ids_dev, scores_dev, count_dev);
+    return router_launch(c, rt, sa, x_dev, available_dev, logits, ids_dev, scores_dev, count_dev, rs, resolved);
+}
+
+int wh_route_experts_async(wh_ctx* c, uint32_t layer, const float* x_dev, size_t hidden_len, size_t active,
+                           const uint32_t* available_dev, size_t n_available, const wh_route_options* opts,
+                           uint32_t* ids_dev, float* scores_dev, uint32_t* count_dev) {
+    if (!c) return WH_INVALID_ARGUMENT;
+    std::lock_guard<std::recursive_mutex> lk(c->mu);
+    return route_experts(c, layer, x_dev, hidden_len, active, available_dev, n_available, opts, ids_dev, scores_dev,
+                         count_dev, nullptr, nullptr);
 }
 
 void wh_synth_fp8_host(uint64_t seed, uint64_t stream, uint8_t* weight, size_t n) {
@@ -2981,12 +3014,8 @@ int wh_routed_and_shared_experts_async(wh_ctx* c, const wh_expert_route* routes,
     return moe_forward(c, ev, wts, n + 1, true, x_dev, x_bf16, n_tokens, out_dev);
 }
 
-// The experts of one token whose route list is in device memory: resolved
-// on the device (k_moe_resolve), then the fast kernels with the list as
-// their wh_moe_dyn.
-int moe_dev_routes(wh_ctx* c, uint32_t layer_id, const uint32_t* ids_dev, const float* w_dev,
-                   const uint32_t* count_dev, size_t n_slots, uint32_t shared_layer, uint32_t shared_expert,
-                   const void* x_dev, int x_bf16, float* out_dev) {
+int moe_dev_prepare(wh_ctx* c, uint32_t layer_id, size_t n_slots, uint32_t shared_layer, uint32_t shared_expert,
+                    MoeDevPrep* m) {
     LayerTable* t = nullptr;
     WH_TRY(layer_table(c, layer_id, &t));
     const bool has_shared = shared_expert != WH_NO_SHARED_EXPERT;
@@ -3003,28 +3032,57 @@ int moe_dev_routes(wh_ctx* c, uint32_t layer_id, const uint32_t* ids_dev, const 
     }
     if (!fast) return WH_UNSUPPORTED;
     WH_HIP(c->moe_dyn.ensure(sizeof(wh_moe_dyn), false));
-    wh_moe_dyn* dyn = c->moe_dyn.as<wh_moe_dyn>();
-    wh_expert_ptrs shp = {};
+    m->t = t;
+    m->dyn = c->moe_dyn.as<wh_moe_dyn>();
+    m->shp = {};
     if (has_shared) {
-        shp.w1 = sh.w1->w;
-        shp.s1 = (const uint8_t*)sh.w1->s;
-        shp.w3 = sh.w3->w;
-        shp.s3 = (const uint8_t*)sh.w3->s;
-        shp.w2 = sh.w2->w;
-        shp.s2 = (const uint8_t*)sh.w2->s;
+        m->shp.w1 = sh.w1->w;
+        m->shp.s1 = (const uint8_t*)sh.w1->s;
+        m->shp.w3 = sh.w3->w;
+        m->shp.s3 = (const uint8_t*)sh.w3->s;
+        m->shp.w2 = sh.w2->w;
+        m->shp.s2 = (const uint8_t*)sh.w2->s;
     }
-    k_moe_resolve<<<1, 64, 0, c->stream>>>(ids_dev, w_dev, count_dev, t->dev, t->n, shp, has_shared ? 1u : 0u,
-                                          (uint32_t)n_slots, dyn, c->status);
+    m->has_shared = has_shared;
+    m->n_slots = n_slots;
+    m->hidden = hidden;
+    m->inter = inter;
+    m->zero_scale = t->zero_scale || (has_shared && expert_zero_scale(sh));
+    return WH_OK;
+}
+
+// The route-list resolve as its own launch (k_moe_resolve).
+int moe_dev_resolve(wh_ctx* c, const MoeDevPrep& m, const uint32_t* ids_dev, const float* w_dev,
+                    const uint32_t* count_dev) {
+    k_moe_resolve<<<1, 64, 0, c->stream>>>(ids_dev, w_dev, count_dev, m.t->dev, m.t->n, m.shp,
+                                          m.has_shared ? 1u : 0u, (uint32_t)m.n_slots, m.dyn, c->status);
     WH_HIP(hipGetLastError());
-    const size_t n = n_slots + (has_shared ? 1 : 0);
+    return WH_OK;
+}
+
+// The fast expert kernels on the resolved list (m.dyn).
+int moe_dev_experts(wh_ctx* c, const MoeDevPrep& m, const void* x_dev, int x_bf16, float* out_dev) {
+    const size_t n = m.n_slots + (m.has_shared ? 1 : 0);
     MoeBufs bufs;
-    WH_TRY(moe_bufs_ctx(c, n, 1, hidden, inter, &bufs));
+    WH_TRY(moe_bufs_ctx(c, n, 1, m.hidden, m.inter, &bufs));
     MoeDyn md;
-    md.p = dyn;
-    md.hidden = hidden;
-    md.inter = inter;
-    md.zero_scale = t->zero_scale || (has_shared && expert_zero_scale(sh));
-    return moe_launch_fast(c, nullptr, nullptr, n, has_shared, x_dev, x_bf16, 1, out_dev, 3u, bufs, true, &md);
+    md.p = m.dyn;
+    md.hidden = m.hidden;
+    md.inter = m.inter;
+    md.zero_scale = m.zero_scale;
+    return moe_launch_fast(c, nullptr, nullptr, n, m.has_shared, x_dev, x_bf16, 1, out_dev, 3u, bufs, true, &md);
+}
+
+// The experts of one token whose route list is in device memory: resolved
+// on the device (k_moe_resolve), then the fast kernels with the list as
+// their wh_moe_dyn.
+int moe_dev_routes(wh_ctx* c, uint32_t layer_id, const uint32_t* ids_dev, const float* w_dev,
+                   const uint32_t* count_dev, size_t n_slots, uint32_t shared_layer, uint32_t shared_expert,
+                   const void* x_dev, int x_bf16, float* out_dev) {
+    MoeDevPrep m;
+    WH_TRY(moe_dev_prepare(c, layer_id, n_slots, shared_layer, shared_expert, &m));
+    WH_TRY(moe_dev_resolve(c, m, ids_dev, w_dev, count_dev));
+    return moe_dev_experts(c, m, x_dev, x_bf16, out_dev);
 }
 
 int wh_routed_and_shared_experts_dev_async(wh_ctx* c, uint32_t layer_id, const uint32_t* ids_dev,
@@ -4278,11 +4336,15 @@ int wh_deepseek_mhc_layer_async(wh_ctx* c, const wh_mhc_layer* L, size_t token_p
         WH_TRY(rowpost_launch(c, a));
     }
     // the router on the gate input, then the experts on its route list
-    // (E/compute.rs:1641-1700)
-    const size_t slots = L->active;
-    WH_TRY(wh_route_experts_async(c, L->layer_id, g, hidden, slots, L->available_dev, L->n_available, &L->route,
-                                  ids, w, count));
-    WH_TRY(moe_dev_routes(c, L->layer_id, ids, w, count, slots, L->shared_layer, L->shared_expert, g, 0, z));
+    // (E/compute.rs:1641-1700); the route-list resolve in the router's last
+    // workgroup where its one-launch selection applies
+    MoeDevPrep mp;
+    WH_TRY(moe_dev_prepare(c, L->layer_id, L->active, L->shared_layer, L->shared_expert, &mp));
+    bool resolved = false;
+    WH_TRY(route_experts(c, L->layer_id, g, hidden, L->active, L->available_dev, L->n_available, &L->route, ids, w,
+                         count, &mp, &resolved));
+    if (!resolved) WH_TRY(moe_dev_resolve(c, mp, ids, w, count));
+    WH_TRY(moe_dev_experts(c, mp, g, 0, z));
     WH_TRY(wh_hc_post_async(c, z, state, post2, comb2, hidden_dev, hc, hidden));
     return WH_OK;
 }
