@@ -145,6 +145,29 @@ def test_router_ties_nan_and_uniform_fallback(ctx, oracle):
     assert np.all(got[1] == np.float32(1.5 / 4))
 
 
+def test_router_one_launch_selection_ties(ctx, oracle):
+    """256 rows, no available list: the one-launch selection, which finds
+    the selected set by a search for its smallest key and falls back to
+    one candidate per round when equal keys straddle that boundary.  Rows
+    5, 77 and 200 tie for first (ordered by row inside the set), 9 and 130
+    tie for sixth and seventh (the boundary at 6 active)."""
+    rows, cols = 256, 128
+    rng = np.random.default_rng(21)
+    x = wl.bf16_round(rng.standard_normal(cols).astype(np.float32))
+    gate = rng.standard_normal((rows, cols)).astype(np.float32) * 0.01
+    for r, a in ((200, 1.0), (5, 1.0), (77, 1.0), (33, 0.75), (150, 0.625), (130, 0.5), (9, 0.5)):
+        gate[r] = np.sign(x) * a
+    g = _bf16_bits(gate)
+    assert ctx.store_router(65, zcblk.build_block([_gate_t(g)]), cols)
+    logits = oracle.bf16_gemv(g, x)
+    order = np.argsort(-logits, kind="stable")
+    assert list(order[:7]) == [5, 77, 200, 33, 150, 9, 130] and logits[9] == logits[130] and logits[5] == logits[200]
+    for active in (1, 3, 5, 6, 7, 8, 64):
+        for math in (SP, RAW):
+            _same(ctx.route_experts(65, x, active, math=math, route_scale=1.5),
+                  _oracle_routes(oracle, logits, active, math=math))
+
+
 @pytest.mark.parametrize("exact", [True, False])
 def test_router_fp8_gate(ctx, oracle, exact):
     """An FP8 gate: ids and weights bit-exact in both numerics modes (the

@@ -229,7 +229,7 @@ struct wh_router_sel {
     // selection order (rows % 4 == 0, rows <= 256, no available list, no
     // hash row); logits then holds [rows] u64 (score, key) and [rows] u32 ids
     uint32_t sorted;
-    // with sorted: when rs_out is set, the last arriver also resolves the
+    // k_router_bf16<true> with sorted: the last arriver also resolves the
     // selected routes against a layer's expert table into rs_out (the work
     // of k_moe_resolve, one launch fewer before the experts)
     wh_moe_dyn* rs_out;
@@ -408,6 +408,7 @@ __device__ __forceinline__ void wh_router_select_wave_n(const wh_router_sel& a, 
 // straight to the rounds of wh_router_select_wave_n (the same order: the
 // largest key, ties to the smallest row); the winner's lane hands its score
 // to the selected slot's lane.
+template <bool kResolve>
 __device__ __forceinline__ void wh_router_select_sorted(const wh_router_sel& a) {
     const uint32_t L = threadIdx.x & 63, n_lists = a.rows / 4;
     const uint64_t* kv = (const uint64_t*)a.logits;
@@ -485,7 +486,7 @@ __device__ __forceinline__ void wh_router_select_sorted(const wh_router_sel& a) 
         a.out_scores[L] = wv;
     }
     if (L == 0) *a.out_count = n;
-    if (a.rs_out) {
+    if (kResolve) {
         __shared__ wh_expert_ptrs got[64];
         const uint32_t cnt = n < a.rs_slots ? n : a.rs_slots;
         wh_moe_resolve_wave(L < cnt ? my_sel : 0u, L < cnt ? wv : 0.0f, cnt, a.rs_table, a.rs_table_n, a.rs_shared,
@@ -528,6 +529,9 @@ __global__ void __launch_bounds__(256) k_router_select(wh_router_sel a) {
 // at once: input z = blockIdx.y reads x + z * x_ld, publishes into
 // a.logits + z * pub_ld, arrives on counter[z] and writes its ids and
 // weights at z * active and its count at z.
+// kResolve: with a.sorted, the route-list resolve in the last arriver
+// (a single input).
+template <bool kResolve>
 __global__ void __launch_bounds__(64) k_router_bf16(const uint16_t* __restrict__ w, const float* __restrict__ x,
                                                     uint32_t cols, wh_router_sel a0, uint32_t* counter, uint32_t x_ld,
                                                     uint32_t pub_ld) {
@@ -591,7 +595,7 @@ __global__ void __launch_bounds__(64) k_router_bf16(const uint16_t* __restrict__
     WH_TL(0, 5);
     if (!last) return;
     if (a.sorted) {
-        wh_router_select_sorted(a);
+        wh_router_select_sorted<kResolve>(a);
         WH_TL(0, 7);
         if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;

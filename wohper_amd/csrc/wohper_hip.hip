@@ -1800,8 +1800,9 @@ int router_launch(wh_ctx* c, const Router& rt, wh_router_sel sa, const float* x,
             *resolved = true;
         }
         WH_HIP(c->rtr_cnt.ensure(sizeof(uint32_t), true));
-        k_router_bf16<<<(rows + 3) / 4, 64, cols * sizeof(float), c->stream>>>(rt.bf16, x, cols, sa,
-                                                                               c->rtr_cnt.as<uint32_t>(), 0, 0);
+        auto kern = sa.rs_out ? k_router_bf16<true> : k_router_bf16<false>;
+        kern<<<(rows + 3) / 4, 64, cols * sizeof(float), c->stream>>>(rt.bf16, x, cols, sa, c->rtr_cnt.as<uint32_t>(),
+                                                                      0, 0);
         WH_HIP(hipGetLastError());
         return WH_OK;
     }
@@ -1858,7 +1859,7 @@ int route_batch(wh_ctx* c, uint32_t layer, const float* x, size_t x_ld, size_t h
     sa.out_scores = scores;
     sa.out_count = count;
     sa.sorted = 1;
-    k_router_bf16<<<dim3((unsigned)(rt.rows / 4), (unsigned)npos), 64, rt.cols * sizeof(float), c->stream>>>(
+    k_router_bf16<false><<<dim3((unsigned)(rt.rows / 4), (unsigned)npos), 64, rt.cols * sizeof(float), c->stream>>>(
         rt.bf16, x, (uint32_t)rt.cols, sa, c->rtr_cnt.as<uint32_t>(), (uint32_t)x_ld, (uint32_t)pub_ld);
     WH_HIP(hipGetLastError());
     return WH_OK;
