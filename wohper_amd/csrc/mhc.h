@@ -233,9 +233,13 @@ __global__ void __launch_bounds__(256) k_hc_finish(wh_hc_args a0) {
         mx = fmaxf(mx, row_q(v, std::integral_constant<int, 3>()));
         v = wh_expf_glibc(v - mx, kExpTab, kExpfExc, WH_EXPF_EXC_COUNT);
         v = v / row_sum(v) + eps;
-        for (uint32_t it = 0; it < n_ops; ++it) {
-            const float r = (it & 1) == 0 ? col_sum(v) : row_sum(v);
-            v = v / (r + eps);
+        // n_ops is odd: a column step, then (row, column) pairs; no branch
+        // on the step's parity inside the loop
+        v = v / (col_sum(v) + eps);
+#pragma unroll 2
+        for (uint32_t it = 1; it < n_ops; it += 2) {
+            v = v / (row_sum(v) + eps);
+            v = v / (col_sum(v) + eps);
         }
         if (on) a.comb[t] = v;
         return;
